@@ -1,0 +1,271 @@
+"""Throughput of the per-token Mamba-130M step on one MI355X through libredukt_gpu.so.
+
+Default workload: Mamba-130M with int8 weight-only quantisation (per-output-row f32
+scales on in_proj, x_proj, dt_proj, out_proj and the tied head; f32 activations and
+state), 32 lockstep streams with independent Zipf(1.1) token ids, every stream's state
+reset at the 4096-token boundary (placed inside the timed region).  A step is one token
+for each of the 32 streams.  Inputs (weights, token ids, slots) are resident in HBM
+before timing starts; logits stay on the device.
+
+Prints one JSON line.  `roofline` covers the dominant kernel (HIP events around its
+launches on the library's stream, in a probe pass after the timed region);
+`cpu_baseline` times the CPU oracle (a C restatement of the reference CPU path) on the
+host cores for a bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import tempfile
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from redukt_amd import ffi, hip, rbin, synth  # noqa: E402
+
+METRIC = "Mamba-130M tok/s at batch 1/32/128 (F32 & Q8); % of HBM roofline"
+HBM_PEAK_GBS = 8000.0
+RESET_PERIOD = 4096
+PROFILES = {"f32": 0, "q8": 1, "q8row": 2, "q8row-all": 6, "q8-all": 5}
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def weight_bytes(dims: rbin.MambaDims, profile: int) -> dict:
+    """HBM bytes of each projection as stored on the device (weights + scales)."""
+    d, di, dr, xr, V = dims.d_model, dims.d_inner, dims.dt_rank, dims.xr, dims.vocab
+    q = profile & 3
+    small_q = q and (profile & 4)
+
+    def mat(rows, cols, quant):
+        if not quant:
+            return rows * cols * 4
+        g = cols if q == 2 else (64 if cols % 64 == 0 else cols)
+        return rows * cols + rows * (cols // g) * 4
+
+    return {"in_proj": mat(2 * di, d, q), "x_proj": mat(xr, di, small_q), "dt_proj": mat(di, dr, small_q),
+            "out_proj": mat(d, di, q), "head": mat(V, d, q)}
+
+
+def algorithmic_bytes(dims: rbin.MambaDims, profile: int, n: int) -> dict:
+    """Bytes each kernel class must move per launch at n streams (compulsory traffic)."""
+    d, di, xr, V, dc = dims.d_model, dims.d_inner, dims.xr, dims.vocab, dims.d_conv
+    w = weight_bytes(dims, profile)
+    f = 4
+    return {
+        "embed": n * d * f * (2 if profile & 3 == 0 else 1) + (n * d // 64 * f if profile & 3 else 0),
+        "norm": 2 * n * d * f + d * f,
+        "in_proj": w["in_proj"] + n * d * f + n * 2 * di * f,
+        "conv": n * (2 * di * (dc - 1) * f + di * f + di * f) + di * (dc + 1) * f,
+        "x_proj": w["x_proj"] + n * di * f + n * xr * f,
+        "scan": n * (2 * di * 16 * f + 3 * di * f + xr * f) + w["dt_proj"] + di * 16 * f + 2 * di * f,
+        "out_proj": w["out_proj"] + n * di * f + 2 * n * d * f,
+        "head": w["head"] + n * d * f + n * V * f,
+        "softmax": 2 * n * V * f,
+    }
+
+
+def step_bytes(dims: rbin.MambaDims, profile: int, n: int) -> int:
+    """Whole-step compulsory HBM bytes: weights once, state read+write, embedding rows,
+    logits write (the B(N) of the workload description)."""
+    w = sum(weight_bytes(dims, profile).values())
+    L, d, di, dc = dims.n_layer, dims.d_model, dims.d_inner, dims.d_conv
+    # per layer: norm_w, conv_w, conv_b, dt_b, exp(A_log), D; then norm_f
+    small = L * (d + di * dc + di + di + 16 * di + di) * 4 + d * 4
+    state = 2 * L * di * ((dc - 1) + 16) * 4
+    return w + small + n * (state + dims.vocab * 4 + d * 4)
+
+
+def ensure_model(path: str) -> str:
+    dims = rbin.MAMBA_130M
+    expect = 44 + 4 * sum(int(np.prod(s)) for _, s in rbin.tensor_order(dims))
+    if not (os.path.isfile(path) and os.path.getsize(path) == expect):
+        log(f"writing synthetic Mamba-130M weights to {path}")
+        synth.write_synthetic_mamba(path, dims, seed=0)
+    return path
+
+
+def cpu_baseline(path: str, profile: int, n: int, tokens: np.ndarray, budget_s: float) -> dict:
+    from oracle import oracle as O   # the CPU restatement; test/baseline infrastructure only
+
+    threads = min(os.cpu_count() or 1, 16)
+    O.set_threads(threads)
+    m = O.MambaOracle(path, profile, cap=n)
+    slots = list(range(n))
+    m.forward(slots, [int(x) for x in tokens[0]])          # warm-up step
+    t0 = time.perf_counter()
+    m.forward(slots, [int(x) for x in tokens[1]])
+    one = time.perf_counter() - t0
+    steps = max(1, min(len(tokens) - 2, int(budget_s / max(one, 1e-6))))
+    t0 = time.perf_counter()
+    for t in range(steps):
+        m.forward(slots, [int(x) for x in tokens[2 + t]])
+    dt = time.perf_counter() - t0
+    m.close()
+    return {"value": round(n * steps / dt, 2), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"CPU oracle, same weights and profile, {n} lockstep streams x {steps} steps "
+                      f"({dt:.1f} s) after one warm-up step"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1024)
+    ap.add_argument("--warmup", type=int, default=32)
+    ap.add_argument("--streams", type=int, default=32)
+    ap.add_argument("--profile", default="q8row-all", choices=sorted(PROFILES))
+    ap.add_argument("--probe-steps", type=int, default=8)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--model", default=os.path.join(tempfile.gettempdir(), "redukt_bench", "mamba130m.rbin"))
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(f"bench.py measures one GPU: the backend serves all streams of a process on one device "
+              f"(--gpus {args.gpus} is not supported; shard streams over one process per GPU instead)",
+              file=sys.stderr)
+        return 2
+    if hip.device_count() < 1:
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 1
+
+    n, K, W = args.streams, args.steps, args.warmup
+    profile = PROFILES[args.profile]
+    dims = rbin.MAMBA_130M
+    path = ensure_model(args.model)
+    rng = np.random.default_rng(1234)
+    total = W + K + args.probe_steps + 1
+    tokens = synth.zipf_tokens(rng, dims.vocab, (total, n))
+
+    be = ffi.PluginBackend(path, 0, profile)
+    be.batch_init(n)
+    stream = be.stream()
+    d_tokens = hip.DeviceBuffer.from_array(tokens)
+    d_slots = hip.DeviceBuffer.from_array(np.arange(n, dtype=np.uint32))
+    d_out = hip.DeviceBuffer(n * dims.vocab * 4)
+    row = n * 4
+
+    # Every stream starts at forward number `since0`, so the 4096-token boundary (reset
+    # before forward 4097) falls on timed step K // 2.
+    reset_step = K // 2
+    since = RESET_PERIOD - W - reset_step
+
+    def step(t: int) -> None:
+        nonlocal since
+        if since >= RESET_PERIOD:                      # PluginState::tick for every stream
+            be.batch_reset(None)
+            since = 0
+        since += 1
+        be.forward_batch_device(n, d_slots.ptr, d_tokens.ptr + t * row, d_out.ptr)
+
+    log(f"warm-up {W} steps, n={n}, profile={args.profile}")
+    for t in range(W):
+        step(t)
+    assert be.device_status() == ffi.BackendResult.OK
+    e0, e1 = hip.Event(), hip.Event()
+    hip.stream_sync(stream)
+    wall0 = time.perf_counter()
+    e0.record(stream)
+    for t in range(W, W + K):
+        step(t)
+    e1.record(stream)
+    e1.synchronize()
+    wall = time.perf_counter() - wall0
+    ms = e0.elapsed_ms(e1)
+    assert be.device_status() == ffi.BackendResult.OK
+    tok_s = n * K / (ms / 1e3)
+    log(f"timed {K} steps: {ms:.2f} ms on the stream ({ms / K * 1e3:.1f} us/step), wall {wall * 1e3:.1f} ms")
+
+    # Probe pass: HIP events around each launch of every kernel class.
+    per_class = {}
+    P = args.probe_steps
+    for name, cls in ffi.KERNEL_CLASSES.items():
+        if name == "softmax":
+            continue
+        launches = dims.n_layer if name in ("in_proj", "conv", "x_proj", "scan", "out_proj") else (
+            dims.n_layer + 1 if name == "norm" else 1)
+        evs = [hip.Event() for _ in range(2 * launches * P)]
+        arr = (ctypes.c_void_p * len(evs))(*[e.h for e in evs])
+        be.probe_kernel(cls, arr)
+        t0 = W + K
+        for t in range(P):
+            step(t0 + t % (total - t0))
+        used = be.probe_used()
+        be.probe_kernel(0, None)
+        hip.stream_sync(stream)
+        assert used == len(evs), (name, used, len(evs))
+        durs = [evs[2 * i].elapsed_ms(evs[2 * i + 1]) for i in range(len(evs) // 2)]
+        per_class[name] = {"avg_us": 1e3 * float(np.mean(durs)), "launches_per_step": launches,
+                           "us_per_step": 1e3 * float(np.sum(durs)) / P}
+        for e in evs:
+            e.close()
+    alg = algorithmic_bytes(dims, profile, n)
+    dom = max(per_class, key=lambda k: per_class[k]["us_per_step"])
+    avg_s = per_class[dom]["avg_us"] / 1e6
+    achieved = alg[dom] / avg_s / 1e9
+    for k, v in per_class.items():
+        v["alg_bytes"] = alg[k]
+        v["GBps"] = round(alg[k] / (v["avg_us"] / 1e6) / 1e9, 1)
+        v["avg_us"] = round(v["avg_us"], 2)
+        v["us_per_step"] = round(v["us_per_step"], 2)
+    log("per kernel class: " + json.dumps(per_class))
+
+    # FFI end-to-end rate (host buffers, D2H of n rows of logits, synchronous).
+    out = np.empty((n, dims.vocab), np.float32)
+    slots = list(range(n))
+    f_steps = min(64, K)
+    be.forward_batch(slots, [int(x) for x in tokens[0]], out)
+    t0 = time.perf_counter()
+    for t in range(f_steps):
+        be.forward_batch(slots, [int(x) for x in tokens[t % total]], out)
+    ffi_tok_s = n * f_steps / (time.perf_counter() - t0)
+    be.close()
+    for b in (d_tokens, d_slots, d_out):
+        b.close()
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("timing the CPU oracle on the host cores")
+        cpu = cpu_baseline(path, profile, n, tokens, args.cpu_seconds)
+
+    sb = step_bytes(dims, profile, n)
+    result = {
+        "metric": METRIC,
+        "value": round(tok_s, 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(ms / K, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": f"mamba130m-{args.profile}-n{n}-zipf1.1", "layers": dims.n_layer,
+                   "d_model": dims.d_model, "vocab": dims.vocab, "streams": n, "weight_profile": args.profile,
+                   "reset_every": RESET_PERIOD, "reset_at_timed_step": reset_step, "parallelism": "none"},
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+        "step_bytes": sb,
+        "step_GBps": round(sb / (ms / K / 1e3) / 1e9, 1),
+        "step_hbm_frac": round(sb / (ms / K / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+        "ffi_tok_s": round(ffi_tok_s, 1),
+        "wall_ms": round(wall * 1e3, 2),
+        "kernels": per_class,
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

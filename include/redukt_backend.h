@@ -1,0 +1,149 @@
+/* redukt_backend.h — C ABI of libredukt_gpu.so, the MI355X (gfx950) backbone backend.
+ *
+ * The library is a drop-in replacement for redukt's GPU plugin.  The host loads it
+ * with dlopen from next to its executable (src/infrastructure/plugin_backend/loader.rs:116-153)
+ * and resolves the symbols below by name.  v1 and v2 are exactly the reference
+ * contract; v3 adds optional symbols the unchanged host never looks up.
+ *
+ * Contract summary (docs/api/PLUGIN-FFI-V2.md:7-108):
+ *   - process-global singleton, single-threaded, not reentrant;
+ *   - all calls synchronous: outputs are complete when a call returns;
+ *   - the caller owns every pointer argument for the duration of the call only;
+ *   - a stream's logits are bit-identical whether it runs through v1 or inside any
+ *     v2 batch, at any batch position and slot, and run after run.
+ */
+#ifndef REDUKT_BACKEND_H
+#define REDUKT_BACKEND_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Result codes — src/domain/backend_ffi.rs:27-41.  v1 entry points return the enum
+ * (int-sized), v2/v3 entry points return int32_t. */
+typedef enum {
+    BACKEND_OK = 0,
+    BACKEND_INIT_FAILED = 1,
+    BACKEND_FORWARD_FAILED = 2,
+    BACKEND_VERSION_MISMATCH = 3,
+    BACKEND_WEIGHTS_NOT_FOUND = 4,
+    BACKEND_INVALID_ARGUMENT = 5,
+} BackendResult;
+
+#define BACKEND_FFI_VERSION 1   /* BackendInfo.ffi_version, backend_ffi.rs:16 */
+#define BACKEND_ABI_VERSION 3   /* redukt_backend_abi_version(): v2 batch + v3 extensions */
+#define BACKEND_NAME_MAX 64
+#define BACKEND_MAX_STREAMS 4096u
+
+/* 76 bytes, backend_ffi.rs:63-72. */
+typedef struct {
+    uint32_t ffi_version;
+    uint32_t vocab_size;
+    uint32_t hidden_dim;
+    uint8_t name[BACKEND_NAME_MAX];
+} BackendInfo;
+
+/* ---------------- v1 (backend_ffi.rs:91-114) ---------------- */
+
+/* Replaces BackendInitFn (backend_ffi.rs:91-95).  weights_path: NUL-terminated path to
+ * a .rbin file, or a directory holding model.rbin.  device_id < 0 means 0.  Re-init
+ * frees everything first.  Bad or missing weights -> WEIGHTS_NOT_FOUND; device
+ * failure -> INIT_FAILED.  The weight profile (F32 / Q8) is taken from the
+ * REDUKT_GPU_PROFILE environment variable ("f32" default, "q8", "q8row", "q8row-all")
+ * or chosen explicitly with redukt_backend_init_ex. */
+BackendResult redukt_backend_init(const uint8_t* weights_path, int32_t device_id, BackendInfo* info_out);
+
+/* Replaces BackendForwardFn (backend_ffi.rs:102-106): one token on the private v1
+ * state; any error (vocab mismatch included) -> FORWARD_FAILED. */
+BackendResult redukt_backend_forward(uint32_t token, float* out_logits, uint32_t vocab_size);
+
+/* Replaces BackendResetFn (backend_ffi.rs:110): zero the v1 state. */
+void redukt_backend_reset_state(void);
+
+/* Replaces BackendFreeFn (backend_ffi.rs:114): release everything. */
+void redukt_backend_free(void);
+
+/* ---------------- v2 (backend_ffi.rs:136-177) ---------------- */
+
+/* Replaces BackendAbiVersionFn (backend_ffi.rs:137); returns BACKEND_ABI_VERSION. */
+uint32_t redukt_backend_abi_version(void);
+
+/* Replaces BackendBatchInitFn (backend_ffi.rs:142): free the old pool, allocate
+ * max_streams zeroed slots; 0 only frees.  INIT_FAILED without a model or on OOM,
+ * INVALID_ARGUMENT above BACKEND_MAX_STREAMS. */
+int32_t redukt_backend_batch_init(uint32_t max_streams);
+
+/* Replaces BackendBatchResetFn (backend_ffi.rs:146): zero the listed slots
+ * (slots == NULL: every slot).  INIT_FAILED without a pool, INVALID_ARGUMENT for a
+ * slot >= max_streams (nothing is reset then). */
+int32_t redukt_backend_batch_reset(const uint32_t* slots, uint32_t n_slots);
+
+/* Replaces BackendForwardBatchFn (backend_ffi.rs:156-162): advance each listed slot by
+ * one token and write row b of out_logits (n_streams * vocab_size f32, row-major).
+ * INIT_FAILED without a pool; INVALID_ARGUMENT (vocab mismatch, n > pool, slot >= pool,
+ * duplicate slot, token >= vocab, null pointer) launches nothing and changes no
+ * state.  n_streams == 0 is a no-op. */
+int32_t redukt_backend_forward_batch(uint32_t n_streams, const uint32_t* slots, const uint32_t* tokens,
+                                     float* out_logits, uint32_t vocab_size);
+
+/* ---------------- v3 extensions (optional; no counterpart in the reference ABI) ----
+ * The reference host resolves only the eight symbols above; these are looked up by
+ * hosts that know abi_version() >= 3, the way v2 was added (PLUGIN-FFI-V2.md:7-25). */
+
+/* Weight profiles (bit field): low two bits 0 = F32, 1 = Q8 with one scale per 64
+ * columns (the reference's Q8 profile, src/infrastructure/mamba/model.rs:56),
+ * 2 = Q8 with one scale per output row; bit 2 = also quantize x_proj and dt_proj.
+ * Quantization follows Q8wMatrix::quantize (src/domain/gemv.rs:256-273) at load. */
+#define BACKEND_PROFILE_F32 0u
+#define BACKEND_PROFILE_Q8_G64 1u
+#define BACKEND_PROFILE_Q8_ROW 2u
+#define BACKEND_PROFILE_Q8_SMALL 4u
+
+/* redukt_backend_init with an explicit weight profile (the model file stays F32). */
+int32_t redukt_backend_init_ex(const uint8_t* weights_path, int32_t device_id, uint32_t profile,
+                               BackendInfo* info_out);
+
+/* forward_batch that returns the probability vector softmax(logits) per stream
+ * instead of the logits, computed on the device in the order of softmax_into
+ * (src/domain/tensor.rs:1917-1933).  Same validation and state rules as forward_batch. */
+int32_t redukt_backend_forward_batch_probs(uint32_t n_streams, const uint32_t* slots, const uint32_t* tokens,
+                                           float* out_probs, uint32_t vocab_size);
+
+/* Stream-ordered step on device-resident inputs: d_slots, d_tokens and d_out are
+ * device pointers (n_streams u32, n_streams u32, n_streams*vocab_size f32).  Nothing is
+ * copied to or from the host and the call does not wait for the step to finish.
+ * Slots and tokens are checked on the device: an invalid or duplicate entry sets a
+ * sticky error that redukt_backend_device_status() reports and every index is clamped
+ * into range, so a bad entry can never address memory outside the pool.  flags bit 0:
+ * write probabilities instead of logits. */
+int32_t redukt_backend_forward_batch_device(uint32_t n_streams, const uint32_t* d_slots, const uint32_t* d_tokens,
+                                            float* d_out, uint32_t vocab_size, uint32_t flags);
+
+/* Wait for queued work; returns OK, or INVALID_ARGUMENT if a device-side check of
+ * forward_batch_device failed since the last call (the flag is then cleared). */
+int32_t redukt_backend_device_status(void);
+
+/* The hipStream_t every kernel of the library is launched on, as an opaque pointer,
+ * so a caller can time the step with events on that stream.  NULL before init. */
+void* redukt_backend_stream(void);
+
+/* Measurement hook.  While kernel_class != 0, every launch of that kernel class is
+ * bracketed by two hipEvent_t records taken in order from events[0..n_events) (caller
+ * owned, alive while probing); recording stops when they run out.  Classes: 1 embed,
+ * 2 norm, 3 in_proj, 4 conv, 5 x_proj, 6 scan, 7 out_proj, 8 head, 9 softmax.
+ * kernel_class 0 switches the probe off.  Returns OK or INVALID_ARGUMENT. */
+int32_t redukt_backend_probe_kernel(uint32_t kernel_class, void** events, uint32_t n_events);
+
+/* Number of events the current probe has recorded. */
+uint32_t redukt_backend_probe_used(void);
+
+/* Copy the recurrent state of one batch-pool slot and layer to host memory:
+ * conv (d_inner*(d_conv-1) f32), ssm (d_inner*d_state f32); either may be NULL. */
+int32_t redukt_backend_get_state(uint32_t slot, uint32_t layer, float* conv_out, float* ssm_out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,227 @@
+"""ctypes wrapper of the CPU oracle (liboracle.so built from this directory).
+
+TEST INFRASTRUCTURE ONLY: parity checker and the timed CPU baseline.  Imported only by
+tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from typing import Optional, Sequence
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+_u32p = ctypes.POINTER(ctypes.c_uint32)
+_f32p = ctypes.POINTER(ctypes.c_float)
+_i8p = ctypes.POINTER(ctypes.c_int8)
+_lib = None
+
+
+def build(force: bool = False) -> str:
+    args = ["make", "-C", HERE] + (["-B"] if force else [])
+    subprocess.run(args, check=True, stdout=subprocess.DEVNULL)
+    return LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.isfile(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        for name in ("orc_expf", "orc_lnf", "orc_lane_expf", "orc_sigmoidf", "orc_softplus"):
+            getattr(L, name).argtypes = [ctypes.c_float]
+            getattr(L, name).restype = ctypes.c_float
+        L.orc_softmax_into.argtypes = [_f32p, _f32p, ctypes.c_int]
+        L.orc_dot_f32.argtypes = [_f32p, _f32p, ctypes.c_int]
+        L.orc_dot_f32.restype = ctypes.c_float
+        L.orc_quantize.argtypes = [_f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int, _i8p, _f32p,
+                                   ctypes.POINTER(ctypes.c_int)]
+        L.orc_gemv_f32.argtypes = [_f32p, ctypes.c_int, ctypes.c_int, _f32p, _f32p]
+        L.orc_gemv_q8.argtypes = [_i8p, _f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int, _f32p, _f32p]
+        L.orc_rms_norm.argtypes = [_f32p, _f32p, ctypes.c_int, ctypes.c_float]
+        L.orc_layer_norm.argtypes = [_f32p, _f32p, _f32p, _f32p, ctypes.c_int, ctypes.c_float]
+        L.orc_ssm_d16.argtypes = [_f32p] * 8 + [ctypes.c_int]
+        L.orc_mamba_load.argtypes = [ctypes.c_char_p, ctypes.c_int, ctypes.POINTER(ctypes.c_int)]
+        L.orc_mamba_load.restype = ctypes.c_void_p
+        L.orc_mamba_free.argtypes = [ctypes.c_void_p]
+        L.orc_mamba_dims.argtypes = [ctypes.c_void_p, _u32p]
+        L.orc_mamba_pool_init.argtypes = [ctypes.c_void_p, ctypes.c_uint32]
+        L.orc_mamba_reset.argtypes = [ctypes.c_void_p, _u32p, ctypes.c_uint32]
+        L.orc_mamba_set_reset_every.argtypes = [ctypes.c_void_p, ctypes.c_uint64]
+        L.orc_mamba_forward.argtypes = [ctypes.c_void_p, ctypes.c_uint32, _u32p, _u32p, _f32p]
+        L.orc_mamba_get_state.argtypes = [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32, _f32p, _f32p]
+        L.orc_mamba_dequant.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_uint32, _f32p]
+        L.orc_set_threads.argtypes = [ctypes.c_int]
+        L.orc_get_threads.restype = ctypes.c_int
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray, ct=ctypes.c_float):
+    return a.ctypes.data_as(ctypes.POINTER(ct))
+
+
+def f32c(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+# ---- scalar / vector math ----
+def expf(x: float) -> float:
+    return lib().orc_expf(x)
+
+
+def lnf(x: float) -> float:
+    return lib().orc_lnf(x)
+
+
+def lane_expf(x: float) -> float:
+    return lib().orc_lane_expf(x)
+
+
+def softplus(x: float) -> float:
+    return lib().orc_softplus(x)
+
+
+def sigmoidf(x: float) -> float:
+    return lib().orc_sigmoidf(x)
+
+
+def softmax(logits) -> np.ndarray:
+    x = f32c(logits)
+    out = np.empty_like(x)
+    lib().orc_softmax_into(_p(x), _p(out), x.size)
+    return out
+
+
+def dot(w, v) -> float:
+    w, v = f32c(w), f32c(v)
+    return lib().orc_dot_f32(_p(w), _p(v), w.size)
+
+
+def quantize(w, group: int):
+    w = f32c(w)
+    rows, cols = w.shape
+    q = np.empty((rows, cols), np.int8)
+    g_eff = group if (group > 0 and group % 8 == 0 and cols % group == 0) else cols
+    sc = np.empty(rows * (cols // g_eff), np.float32)
+    g = ctypes.c_int(0)
+    lib().orc_quantize(_p(w), rows, cols, group, _p(q, ctypes.c_int8), _p(sc), ctypes.byref(g))
+    return q, sc.reshape(rows, -1), g.value
+
+
+def gemv_f32(w, v) -> np.ndarray:
+    w, v = f32c(w), f32c(v)
+    out = np.empty(w.shape[0], np.float32)
+    lib().orc_gemv_f32(_p(w), w.shape[0], w.shape[1], _p(v), _p(out))
+    return out
+
+
+def gemv_q8(q, scales, group: int, v) -> np.ndarray:
+    q = np.ascontiguousarray(q, dtype=np.int8)
+    sc, v = f32c(scales), f32c(v)
+    out = np.empty(q.shape[0], np.float32)
+    lib().orc_gemv_q8(_p(q, ctypes.c_int8), _p(sc), q.shape[0], q.shape[1], group, _p(v), _p(out))
+    return out
+
+
+def rms_norm(x, w, eps: float = 1e-5) -> np.ndarray:
+    x = f32c(x).copy()
+    w = f32c(w)
+    lib().orc_rms_norm(_p(x), _p(w), x.size, eps)
+    return x
+
+
+def layer_norm(x, w, b, eps: float = 1e-5) -> np.ndarray:
+    x, w, b = f32c(x), f32c(w), f32c(b)
+    out = np.empty_like(x)
+    lib().orc_layer_norm(_p(out), _p(x), _p(w), _p(b), x.size, eps)
+    return out
+
+
+def ssm_d16(ss, dt, conv_out, a_log, b, c, d_vec):
+    """One scan step; returns (y, new_state).  ss: [di,16]."""
+    ss = f32c(ss).copy()
+    dt, conv_out, a_log, b, c, d_vec = map(f32c, (dt, conv_out, a_log, b, c, d_vec))
+    y = np.empty(dt.size, np.float32)
+    lib().orc_ssm_d16(_p(y), _p(ss), _p(dt), _p(conv_out), _p(a_log), _p(b), _p(c), _p(d_vec), dt.size)
+    return y, ss
+
+
+def set_threads(n: int) -> None:
+    lib().orc_set_threads(n)
+
+
+def get_threads() -> int:
+    return lib().orc_get_threads()
+
+
+class MambaOracle:
+    """A Mamba model on the CPU oracle with a pool of `cap` stream slots."""
+
+    def __init__(self, rbin_path: str, profile: int = 0, cap: int = 1):
+        err = ctypes.c_int(0)
+        self.h = lib().orc_mamba_load(rbin_path.encode(), profile, ctypes.byref(err))
+        if not self.h:
+            raise RuntimeError(f"oracle load failed ({err.value}): {rbin_path}")
+        d = np.zeros(8, np.uint32)
+        lib().orc_mamba_dims(self.h, _p(d, ctypes.c_uint32))
+        self.vocab, self.d_model, self.d_inner, self.d_state, self.d_conv, self.dt_rank, self.n_layer, self.flags = \
+            (int(x) for x in d)
+        self.cap = 0
+        self.pool_init(cap)
+
+    def pool_init(self, cap: int) -> None:
+        if lib().orc_mamba_pool_init(self.h, cap) != 0:
+            raise MemoryError("oracle pool")
+        self.cap = cap
+
+    def set_reset_every(self, every: int) -> None:
+        lib().orc_mamba_set_reset_every(self.h, every)
+
+    def reset(self, slots: Optional[Sequence[int]] = None) -> None:
+        if slots is None:
+            lib().orc_mamba_reset(self.h, None, 0)
+        else:
+            s = np.ascontiguousarray(slots, dtype=np.uint32)
+            if lib().orc_mamba_reset(self.h, _p(s, ctypes.c_uint32), s.size) != 0:
+                raise ValueError("bad slot")
+
+    def forward(self, slots: Sequence[int], tokens: Sequence[int]) -> np.ndarray:
+        s = np.ascontiguousarray(slots, dtype=np.uint32)
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        out = np.empty((s.size, self.vocab), np.float32)
+        rc = lib().orc_mamba_forward(self.h, s.size, _p(s, ctypes.c_uint32), _p(t, ctypes.c_uint32), _p(out))
+        if rc != 0:
+            raise ValueError(f"oracle forward rc={rc}")
+        return out
+
+    def state(self, slot: int, layer: int):
+        conv = np.empty(self.d_inner * (self.d_conv - 1), np.float32)
+        ssm = np.empty(self.d_inner * self.d_state, np.float32)
+        if lib().orc_mamba_get_state(self.h, slot, layer, _p(conv), _p(ssm)) != 0:
+            raise ValueError("bad slot/layer")
+        return conv, ssm
+
+    def dequant(self, which: int, layer: int = 0) -> np.ndarray:
+        shapes = {0: (2 * self.d_inner, self.d_model), 1: (self.d_model, self.d_inner), 2: (self.vocab, self.d_model),
+                  3: (self.dt_rank + 2 * self.d_state, self.d_inner), 4: (self.d_inner, self.dt_rank)}
+        out = np.empty(shapes[which], np.float32)
+        if lib().orc_mamba_dequant(self.h, which, layer, _p(out)) != 0:
+            raise ValueError("bad matrix")
+        return out
+
+    def close(self) -> None:
+        if self.h:
+            lib().orc_mamba_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

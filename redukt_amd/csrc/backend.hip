@@ -1,0 +1,529 @@
+// backend.hip — host side of libredukt_gpu.so: the plugin C ABI of redukt
+// (src/domain/backend_ffi.rs, docs/api/PLUGIN-FFI-V2.md) over the gfx950 kernels.
+//
+// One process-global model, one non-blocking HIP stream at default priority, two
+// disjoint state pools (v1: one slot; v2: the batch pool).  Weights are read from a
+// .rbin file (F32) and, for the Q8 profiles, quantized here at load with the
+// reference recipe before upload.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/redukt_backend.h"
+#include "model.h"
+#include "portable_math.h"
+
+#pragma clang fp contract(off)
+
+namespace rdk {
+
+size_t DMat::bytes() const {
+    if (!w) return 0;
+    const size_t n = (size_t)rq * 4 * cols;
+    return group == 0 ? n * 4 : n + (size_t)rq * 4 * (cols / group) * 4;
+}
+
+namespace {
+
+constexpr uint32_t kRbinMagic = 0x55504752u;  // "RGPU"
+constexpr uint32_t kFlagNormBias = 1u << 0;
+constexpr uint32_t kFlagUntiedHead = 1u << 1;
+constexpr int kMaxCols = 2048;  // 8 column quads per lane in the projection kernel
+
+struct Model {
+    bool ready = false;
+    Dims dims;
+    uint32_t profile = 0;
+    std::vector<DLayer> layers;
+    DLayer* d_layers_host = nullptr;  // same as layers.data(); kernels take DLayer by value
+    DMat emb, head_own;
+    bool tied = true;
+    float* norm_f_w = nullptr;
+    float* norm_f_b = nullptr;
+    std::vector<void*> allocs;
+    hipStream_t stream = nullptr;
+    Pool v1, batch;
+    uint32_t* d_err = nullptr;
+    int device = 0;
+    Probe probe;
+};
+
+Model G;
+
+void log(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+void log(const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    fprintf(stderr, "[redukt-gpu-hip] ");
+    vfprintf(stderr, fmt, ap);
+    fprintf(stderr, "\n");
+    va_end(ap);
+}
+
+template <typename T>
+T* dev_upload(const T* host, size_t count) {
+    T* p = nullptr;
+    if (hipMalloc((void**)&p, sizeof(T) * (count ? count : 1)) != hipSuccess) return nullptr;
+    G.allocs.push_back(p);
+    if (count && hipMemcpy(p, host, sizeof(T) * count, hipMemcpyHostToDevice) != hipSuccess) return nullptr;
+    return p;
+}
+
+// Q8wMatrix::quantize (src/domain/gemv.rs:256-273): `group` columns per scale when it is
+// a multiple of 8 dividing cols, else one scale per row; scale = max|w|/127 (1 for an
+// all-zero group), q = clamp(round-half-away(w * (1/scale)), -127, 127).
+int quantize(const float* w, int rows, int cols, int group, std::vector<int8_t>& q, std::vector<float>& sc) {
+    if (!(group > 0 && group % 8 == 0 && cols % group == 0)) group = cols;
+    const size_t total = (size_t)rows * cols, ng = total / group;
+    q.resize(total);
+    sc.resize(ng);
+    for (size_t g = 0; g < ng; g++) {
+        const float* wg = w + g * group;
+        float amax = 0.0f;
+        for (int i = 0; i < group; i++) amax = std::fmax(amax, std::fabs(wg[i]));
+        const float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
+        const float inv = 1.0f / scale;
+        for (int i = 0; i < group; i++) {
+            float r = std::round(wg[i] * inv);
+            r = r < -127.0f ? -127.0f : (r > 127.0f ? 127.0f : r);
+            q[g * group + i] = std::isnan(r) ? 0 : (int8_t)r;
+        }
+        sc[g] = scale;
+    }
+    return group;
+}
+
+// Pack a row-major [rows][cols] matrix into 4x4 tiles (see DMat) and upload it, F32 or
+// quantized.  quant_group: 0 = F32, else the requested Q8 group (cols = per row).
+bool make_mat(DMat& m, const float* w, int rows, int cols, int quant_group) {
+    m.rows = rows;
+    m.cols = cols;
+    m.rq = (rows + 3) / 4;
+    const int kqn = cols / 4;
+    const size_t tiles = (size_t)m.rq * kqn;
+    if (quant_group == 0) {
+        std::vector<float> t(tiles * 16, 0.0f);
+        for (int r = 0; r < rows; r++)
+            for (int k = 0; k < cols; k++)
+                t[((size_t)(r / 4) * kqn + k / 4) * 16 + (r % 4) * 4 + (k % 4)] = w[(size_t)r * cols + k];
+        m.group = 0;
+        m.w = dev_upload(t.data(), t.size());
+        return m.w != nullptr;
+    }
+    std::vector<int8_t> q;
+    std::vector<float> sc;
+    m.group = quantize(w, rows, cols, quant_group, q, sc);
+    const int gpr = cols / m.group;
+    std::vector<int8_t> t(tiles * 16, 0);
+    for (int r = 0; r < rows; r++)
+        for (int k = 0; k < cols; k++)
+            t[((size_t)(r / 4) * kqn + k / 4) * 16 + (r % 4) * 4 + (k % 4)] = q[(size_t)r * cols + k];
+    std::vector<float> scp((size_t)m.rq * 4 * gpr, 0.0f);
+    std::memcpy(scp.data(), sc.data(), sizeof(float) * sc.size());
+    m.w = dev_upload(t.data(), t.size());
+    m.scales = dev_upload(scp.data(), scp.size());
+    return m.w && m.scales;
+}
+
+struct Reader {
+    FILE* f;
+    bool ok = true;
+    std::vector<float> read(size_t count) {
+        std::vector<float> v(count);
+        if (ok && fread(v.data(), sizeof(float), count, f) != count) ok = false;
+        return v;
+    }
+};
+
+// .rbin v1/v2 (scripts/convert-weights-gpu.py:43-53, 152-197; reader semantics of
+// plugins/redukt-gpu-cuda/mamba_cuda.cu:470-544).
+int load_weights(const std::string& path, uint32_t profile) {
+    FILE* f = fopen(path.c_str(), "rb");
+    if (!f) {
+        log("cannot open: %s", path.c_str());
+        return -1;
+    }
+    uint32_t h[11];
+    Reader rd{f};
+    bool hdr_ok = fread(h, 4, 11, f) == 11 && h[0] == kRbinMagic && (h[1] == 1 || h[1] == 2);
+    if (hdr_ok) {
+        hdr_ok = h[2] && h[3] && h[4] && h[5] && h[7] && h[8] && h[6] >= 2;
+        if (h[1] == 2) hdr_ok = hdr_ok && h[10] <= 1 && !(h[10] == 0 && h[2] != 256);
+        // Kernel limits: 16 SSM states per channel, column counts in whole quads and at
+        // most kMaxCols so a projection row's tiles fit in one lane's registers.
+        hdr_ok = hdr_ok && h[5] == 16 && h[3] % 4 == 0 && h[4] % 4 == 0 && h[3] <= (uint32_t)kMaxCols &&
+                 h[4] <= (uint32_t)kMaxCols;
+    }
+    if (!hdr_ok) {
+        log("bad/unsupported .rbin header in %s", path.c_str());
+        fclose(f);
+        return -1;
+    }
+    Dims& D = G.dims;
+    D.vocab = h[2]; D.d = h[3]; D.di = h[4]; D.ds = h[5]; D.dc = h[6]; D.dr = h[7]; D.nl = h[8]; D.flags = h[9];
+    D.tokenizer = h[1] == 1 ? (D.vocab == 256 ? 0u : 1u) : h[10];
+    const int quant = (profile & 3) == 0 ? 0 : ((profile & 3) == 1 ? 64 : (int)0x7fffffff);
+    auto qgroup = [&](int cols) { return quant == 0 ? 0 : (quant == 0x7fffffff ? cols : quant); };
+    const bool qsmall = quant != 0 && (profile & BACKEND_PROFILE_Q8_SMALL);
+    const bool nb = D.flags & kFlagNormBias, uh = D.flags & kFlagUntiedHead;
+    const size_t V = D.vocab, d = D.d, di = D.di, dc = D.dc, dr = D.dr, xr = D.xr();
+    log("rbin v%u: d=%u di=%u ds=%u dc=%u dr=%u nl=%u vs=%u flags=0x%02x tok=%u profile=%u", h[1], D.d, D.di, D.ds,
+        D.dc, D.dr, D.nl, D.vocab, D.flags, D.tokenizer, profile);
+    bool ok = true;
+    {
+        std::vector<float> e = rd.read(V * d);
+        ok = rd.ok && make_mat(G.emb, e.data(), (int)V, (int)d, qgroup((int)d));
+    }
+    G.layers.assign(D.nl, DLayer{});
+    for (uint32_t i = 0; ok && i < D.nl; i++) {
+        DLayer& L = G.layers[i];
+        std::vector<float> t = rd.read(d);
+        ok = rd.ok && (L.norm_w = dev_upload(t.data(), d));
+        if (ok && nb) { t = rd.read(d); ok = rd.ok && (L.norm_b = dev_upload(t.data(), d)); }
+        if (ok) { t = rd.read(2 * di * d); ok = rd.ok && make_mat(L.in_proj, t.data(), (int)(2 * di), (int)d, qgroup((int)d)); }
+        if (ok) { t = rd.read(di * dc); ok = rd.ok && (L.conv_w = dev_upload(t.data(), di * dc)); }
+        if (ok) { t = rd.read(di); ok = rd.ok && (L.conv_b = dev_upload(t.data(), di)); }
+        if (ok) {
+            t = rd.read(xr * di);
+            ok = rd.ok && make_mat(L.x_proj, t.data(), (int)xr, (int)di, qsmall ? qgroup((int)di) : 0);
+        }
+        if (ok) {
+            t = rd.read(di * dr);
+            ok = rd.ok;
+            if (ok && !qsmall) {
+                std::vector<float> tt(dr * di);
+                for (size_t j = 0; j < di; j++)
+                    for (size_t k = 0; k < dr; k++) tt[k * di + j] = t[j * dr + k];
+                ok = (L.dt_wt = dev_upload(tt.data(), tt.size())) != nullptr;
+            } else if (ok) {
+                std::vector<int8_t> q;
+                std::vector<float> sc;
+                L.dt_group = quantize(t.data(), (int)di, (int)dr, qgroup((int)dr), q, sc);
+                std::vector<int8_t> qt(dr * di);
+                for (size_t j = 0; j < di; j++)
+                    for (size_t k = 0; k < dr; k++) qt[k * di + j] = q[j * dr + k];
+                ok = (L.dt_qt = dev_upload(qt.data(), qt.size())) && (L.dt_scales = dev_upload(sc.data(), sc.size()));
+            }
+        }
+        if (ok) { t = rd.read(di); ok = rd.ok && (L.dt_b = dev_upload(t.data(), di)); }
+        if (ok) {
+            t = rd.read(di * 16);
+            for (float& v : t) v = lane_exp_f(v);  // exp(A_log) of every step, tensor.rs:1316
+            ok = rd.ok && (L.a_exp = dev_upload(t.data(), t.size()));
+        }
+        if (ok) { t = rd.read(di); ok = rd.ok && (L.d_vec = dev_upload(t.data(), di)); }
+        if (ok) { t = rd.read(d * di); ok = rd.ok && make_mat(L.out_proj, t.data(), (int)d, (int)di, qgroup((int)di)); }
+        if (ok && ((i + 1) % 8 == 0 || i + 1 == D.nl)) log("loaded layer %u/%u", i + 1, D.nl);
+    }
+    if (ok) { std::vector<float> t = rd.read(d); ok = rd.ok && (G.norm_f_w = dev_upload(t.data(), d)); }
+    if (ok && nb) { std::vector<float> t = rd.read(d); ok = rd.ok && (G.norm_f_b = dev_upload(t.data(), d)); }
+    G.tied = !uh;
+    if (ok && uh) {
+        std::vector<float> t = rd.read(V * d);
+        ok = rd.ok && make_mat(G.head_own, t.data(), (int)V, (int)d, qgroup((int)d));
+    }
+    fclose(f);
+    return ok ? 0 : -1;
+}
+
+void dev_free_all() {
+    for (void* p : G.allocs) (void)hipFree(p);
+    G.allocs.clear();
+}
+
+void pool_free(Pool& p) {
+    void* bufs[] = {p.conv, p.ssm, p.x, p.normed, p.xz, p.conv_out, p.zp, p.gated, p.out, p.d_slots, p.d_tokens};
+    for (void* b : bufs) (void)hipFree(b);
+    if (p.h_slots) (void)hipHostFree(p.h_slots);
+    if (p.h_tokens) (void)hipHostFree(p.h_tokens);
+    free(p.seen);
+    p = Pool{};
+}
+
+template <typename T>
+bool dev_zero(T*& p, size_t count) {
+    if (hipMalloc((void**)&p, sizeof(T) * (count ? count : 1)) != hipSuccess) {
+        p = nullptr;
+        return false;
+    }
+    return hipMemset(p, 0, sizeof(T) * (count ? count : 1)) == hipSuccess;
+}
+
+bool pool_alloc(Pool& p, uint32_t cap) {
+    const Dims& D = G.dims;
+    const size_t n = cap, d = D.d, di = D.di;
+    p = Pool{};
+    p.cap = cap;
+    bool ok = dev_zero(p.conv, (size_t)D.nl * n * di * (D.dc - 1)) && dev_zero(p.ssm, (size_t)D.nl * n * di * 16) &&
+              dev_zero(p.x, n * d) && dev_zero(p.normed, n * d) && dev_zero(p.xz, n * 2 * di) &&
+              dev_zero(p.conv_out, n * di) && dev_zero(p.zp, n * D.xr()) && dev_zero(p.gated, n * di) &&
+              dev_zero(p.out, n * D.vocab) && dev_zero(p.d_slots, n) && dev_zero(p.d_tokens, n);
+    ok = ok && hipHostMalloc((void**)&p.h_slots, sizeof(uint32_t) * n, hipHostMallocDefault) == hipSuccess;
+    ok = ok && hipHostMalloc((void**)&p.h_tokens, sizeof(uint32_t) * n, hipHostMallocDefault) == hipSuccess;
+    ok = ok && (p.seen = (uint8_t*)calloc(n, 1)) != nullptr;
+    return ok;
+}
+
+void free_model() {
+    if (G.stream) (void)hipStreamSynchronize(G.stream);
+    pool_free(G.v1);
+    pool_free(G.batch);
+    dev_free_all();
+    if (G.stream) (void)hipStreamDestroy(G.stream);
+    G = Model{};
+}
+
+StepArgs step_args(Pool& p, uint32_t n, const uint32_t* slots, const uint32_t* tokens, float* out, bool probs,
+                   bool check) {
+    StepArgs a;
+    a.dims = &G.dims;
+    a.layers = G.layers.data();
+    a.emb = &G.emb;
+    a.head = G.tied ? &G.emb : &G.head_own;
+    a.norm_f_w = G.norm_f_w;
+    a.norm_f_b = G.norm_f_b;
+    a.pool = &p;
+    a.n = n;
+    a.slots = slots;
+    a.tokens = tokens;
+    a.out = out;
+    a.probs = probs;
+    a.check = check;
+    a.err = G.d_err;
+    a.probe = &G.probe;
+    return a;
+}
+
+// pool_forward semantics (mamba_cuda.cu:604-635): validate on the host (nothing is
+// launched on INVALID_ARGUMENT), stage slots/tokens through pinned memory, enqueue the
+// step, copy the n rows back to the caller and wait.
+int pool_forward(Pool& p, uint32_t n, const uint32_t* slots, const uint32_t* tokens, float* out, bool probs) {
+    memset(p.seen, 0, p.cap);
+    for (uint32_t b = 0; b < n; b++) {
+        if (slots[b] >= p.cap || p.seen[slots[b]] || tokens[b] >= G.dims.vocab) return BACKEND_INVALID_ARGUMENT;
+        p.seen[slots[b]] = 1;
+    }
+    memcpy(p.h_slots, slots, sizeof(uint32_t) * n);
+    memcpy(p.h_tokens, tokens, sizeof(uint32_t) * n);
+    const size_t ib = sizeof(uint32_t) * n;
+    if (hipMemcpyAsync(p.d_slots, p.h_slots, ib, hipMemcpyHostToDevice, G.stream) != hipSuccess ||
+        hipMemcpyAsync(p.d_tokens, p.h_tokens, ib, hipMemcpyHostToDevice, G.stream) != hipSuccess)
+        return BACKEND_FORWARD_FAILED;
+    if (enqueue_step(step_args(p, n, p.d_slots, p.d_tokens, p.out, probs, false), G.stream) != hipSuccess)
+        return BACKEND_FORWARD_FAILED;
+    if (hipMemcpyAsync(out, p.out, sizeof(float) * n * G.dims.vocab, hipMemcpyDeviceToHost, G.stream) != hipSuccess)
+        return BACKEND_FORWARD_FAILED;
+    if (hipStreamSynchronize(G.stream) != hipSuccess) return BACKEND_FORWARD_FAILED;
+    return BACKEND_OK;
+}
+
+// pool_reset semantics (mamba_cuda.cu:637-658), validated before anything is queued.
+int pool_reset(Pool& p, uint32_t n, const uint32_t* slots) {
+    for (uint32_t b = 0; b < n; b++) {
+        const uint32_t s = slots ? slots[b] : b;
+        if (s >= p.cap) return BACKEND_INVALID_ARGUMENT;
+    }
+    if (n == 0) return BACKEND_OK;
+    // Every earlier call that used p.h_slots ended with a stream synchronize, so the
+    // staging buffer is free to overwrite.
+    for (uint32_t b = 0; b < n; b++) p.h_slots[b] = slots ? slots[b] : b;
+    if (hipMemcpyAsync(p.d_slots, p.h_slots, sizeof(uint32_t) * n, hipMemcpyHostToDevice, G.stream) != hipSuccess)
+        return BACKEND_FORWARD_FAILED;
+    if (enqueue_reset(G.dims, p, p.d_slots, n, G.stream) != hipSuccess) return BACKEND_FORWARD_FAILED;
+    if (hipStreamSynchronize(G.stream) != hipSuccess) return BACKEND_FORWARD_FAILED;
+    return BACKEND_OK;
+}
+
+std::string rbin_path(const uint8_t* weights_path) {
+    std::string p((const char*)weights_path);
+    if (p.size() < 5 || p.compare(p.size() - 5, 5, ".rbin") != 0) p += "/model.rbin";
+    return p;
+}
+
+uint32_t env_profile() {
+    const char* e = getenv("REDUKT_GPU_PROFILE");
+    if (!e || !*e || !strcmp(e, "f32")) return BACKEND_PROFILE_F32;
+    if (!strcmp(e, "q8")) return BACKEND_PROFILE_Q8_G64;
+    if (!strcmp(e, "q8row")) return BACKEND_PROFILE_Q8_ROW;
+    if (!strcmp(e, "q8row-all")) return BACKEND_PROFILE_Q8_ROW | BACKEND_PROFILE_Q8_SMALL;
+    if (!strcmp(e, "q8-all")) return BACKEND_PROFILE_Q8_G64 | BACKEND_PROFILE_Q8_SMALL;
+    return (uint32_t)strtoul(e, nullptr, 0) & 7u;
+}
+
+int init_common(const uint8_t* weights_path, int32_t device_id, uint32_t profile, BackendInfo* info_out) {
+    if (!weights_path || !info_out) return BACKEND_INIT_FAILED;
+    if (G.ready || G.stream) free_model();
+    if ((profile & 3) == 3) return BACKEND_INIT_FAILED;
+    const std::string path = rbin_path(weights_path);
+    log("init: weights=%s device=%d profile=%u", path.c_str(), device_id, profile);
+    G.device = device_id >= 0 ? device_id : 0;
+    if (hipSetDevice(G.device) != hipSuccess ||
+        hipStreamCreateWithFlags(&G.stream, hipStreamNonBlocking) != hipSuccess) {
+        free_model();
+        return BACKEND_INIT_FAILED;
+    }
+    G.profile = profile;
+    if (load_weights(path, profile) != 0) {
+        free_model();
+        return BACKEND_WEIGHTS_NOT_FOUND;
+    }
+    if (!dev_zero(G.d_err, 1) || !pool_alloc(G.v1, 1)) {
+        free_model();
+        return BACKEND_INIT_FAILED;
+    }
+    G.allocs.push_back(G.d_err);
+    G.ready = true;
+    memset(info_out, 0, sizeof(*info_out));
+    info_out->ffi_version = BACKEND_FFI_VERSION;
+    info_out->vocab_size = G.dims.vocab;
+    info_out->hidden_dim = G.dims.d;
+    static const char* names[] = {"hip-gfx950-mamba-f32", "hip-gfx950-mamba-q8", "hip-gfx950-mamba-q8row"};
+    const char* name = names[profile & 3];
+    memcpy(info_out->name, name, strlen(name));
+    size_t fr = 0, tot = 0;
+    (void)hipMemGetInfo(&fr, &tot);
+    log("ready: vocab=%u d_model=%u n_layer=%u abi=%d | GPU %.0f/%.0f MB used", G.dims.vocab, G.dims.d, G.dims.nl,
+        BACKEND_ABI_VERSION, (tot - fr) / 1048576.0, tot / 1048576.0);
+    return BACKEND_OK;
+}
+
+}  // namespace
+}  // namespace rdk
+
+using namespace rdk;
+
+extern "C" {
+
+BackendResult redukt_backend_init(const uint8_t* weights_path, int32_t device_id, BackendInfo* info_out) {
+    return (BackendResult)init_common(weights_path, device_id, env_profile(), info_out);
+}
+
+BackendResult redukt_backend_forward(uint32_t token, float* out_logits, uint32_t vocab_size) {
+    if (!G.ready || !out_logits || vocab_size != G.dims.vocab) return BACKEND_FORWARD_FAILED;
+    const uint32_t slot = 0;
+    return pool_forward(G.v1, 1, &slot, &token, out_logits, false) == BACKEND_OK ? BACKEND_OK
+                                                                                   : BACKEND_FORWARD_FAILED;
+}
+
+void redukt_backend_reset_state(void) {
+    if (!G.ready) return;
+    const uint32_t slot = 0;
+    if (pool_reset(G.v1, 1, &slot) != BACKEND_OK) log("reset_state failed");
+}
+
+void redukt_backend_free(void) {
+    free_model();
+    log("freed");
+}
+
+uint32_t redukt_backend_abi_version(void) { return BACKEND_ABI_VERSION; }
+
+int32_t redukt_backend_batch_init(uint32_t max_streams) {
+    if (!G.ready) return BACKEND_INIT_FAILED;
+    if (max_streams > BACKEND_MAX_STREAMS) return BACKEND_INVALID_ARGUMENT;
+    if (hipStreamSynchronize(G.stream) != hipSuccess) return BACKEND_INIT_FAILED;
+    pool_free(G.batch);
+    if (max_streams == 0) return BACKEND_OK;
+    if (!pool_alloc(G.batch, max_streams)) {
+        pool_free(G.batch);
+        return BACKEND_INIT_FAILED;
+    }
+    log("batch pool: %u streams", max_streams);
+    return BACKEND_OK;
+}
+
+int32_t redukt_backend_batch_reset(const uint32_t* slots, uint32_t n_slots) {
+    if (!G.ready || G.batch.cap == 0) return BACKEND_INIT_FAILED;
+    if (!slots) return pool_reset(G.batch, G.batch.cap, nullptr);
+    if (n_slots > G.batch.cap) return BACKEND_INVALID_ARGUMENT;
+    return pool_reset(G.batch, n_slots, slots);
+}
+
+static int32_t forward_batch_impl(uint32_t n, const uint32_t* slots, const uint32_t* tokens, float* out,
+                                  uint32_t vocab_size, bool probs) {
+    if (!G.ready || G.batch.cap == 0) return BACKEND_INIT_FAILED;
+    if (vocab_size != G.dims.vocab || n > G.batch.cap) return BACKEND_INVALID_ARGUMENT;
+    if (n == 0) return BACKEND_OK;
+    if (!slots || !tokens || !out) return BACKEND_INVALID_ARGUMENT;
+    return pool_forward(G.batch, n, slots, tokens, out, probs);
+}
+
+int32_t redukt_backend_forward_batch(uint32_t n_streams, const uint32_t* slots, const uint32_t* tokens,
+                                     float* out_logits, uint32_t vocab_size) {
+    return forward_batch_impl(n_streams, slots, tokens, out_logits, vocab_size, false);
+}
+
+int32_t redukt_backend_init_ex(const uint8_t* weights_path, int32_t device_id, uint32_t profile,
+                               BackendInfo* info_out) {
+    if (profile > 7u) return BACKEND_INVALID_ARGUMENT;
+    return init_common(weights_path, device_id, profile, info_out);
+}
+
+int32_t redukt_backend_forward_batch_probs(uint32_t n_streams, const uint32_t* slots, const uint32_t* tokens,
+                                           float* out_probs, uint32_t vocab_size) {
+    return forward_batch_impl(n_streams, slots, tokens, out_probs, vocab_size, true);
+}
+
+int32_t redukt_backend_forward_batch_device(uint32_t n_streams, const uint32_t* d_slots, const uint32_t* d_tokens,
+                                            float* d_out, uint32_t vocab_size, uint32_t flags) {
+    if (!G.ready || G.batch.cap == 0) return BACKEND_INIT_FAILED;
+    if (vocab_size != G.dims.vocab || n_streams > G.batch.cap) return BACKEND_INVALID_ARGUMENT;
+    if (n_streams == 0) return BACKEND_OK;
+    if (!d_slots || !d_tokens || !d_out) return BACKEND_INVALID_ARGUMENT;
+    StepArgs a = step_args(G.batch, n_streams, d_slots, d_tokens, d_out, (flags & 1u) != 0, true);
+    return enqueue_step(a, G.stream) == hipSuccess ? BACKEND_OK : BACKEND_FORWARD_FAILED;
+}
+
+int32_t redukt_backend_device_status(void) {
+    if (!G.ready) return BACKEND_INIT_FAILED;
+    uint32_t err = 0;
+    if (hipMemcpyAsync(&err, G.d_err, sizeof(err), hipMemcpyDeviceToHost, G.stream) != hipSuccess ||
+        hipStreamSynchronize(G.stream) != hipSuccess)
+        return BACKEND_FORWARD_FAILED;
+    if (err) {
+        const uint32_t zero = 0;
+        if (hipMemcpy(G.d_err, &zero, sizeof(zero), hipMemcpyHostToDevice) != hipSuccess) return BACKEND_FORWARD_FAILED;
+        return BACKEND_INVALID_ARGUMENT;
+    }
+    return BACKEND_OK;
+}
+
+void* redukt_backend_stream(void) { return (void*)G.stream; }
+
+int32_t redukt_backend_probe_kernel(uint32_t kernel_class, void** events, uint32_t n_events) {
+    if (!G.ready) return BACKEND_INIT_FAILED;
+    if (kernel_class >= KC_COUNT || (kernel_class != KC_NONE && (!events || n_events < 2)))
+        return BACKEND_INVALID_ARGUMENT;
+    G.probe = Probe{};
+    if (kernel_class != KC_NONE) {
+        G.probe.cls = kernel_class;
+        G.probe.ev = (hipEvent_t*)events;
+        G.probe.cap = n_events;
+    }
+    return BACKEND_OK;
+}
+
+uint32_t redukt_backend_probe_used(void) { return G.probe.used; }
+
+int32_t redukt_backend_get_state(uint32_t slot, uint32_t layer, float* conv_out, float* ssm_out) {
+    if (!G.ready || G.batch.cap == 0) return BACKEND_INIT_FAILED;
+    if (slot >= G.batch.cap || layer >= G.dims.nl) return BACKEND_INVALID_ARGUMENT;
+    if (hipStreamSynchronize(G.stream) != hipSuccess) return BACKEND_FORWARD_FAILED;
+    const size_t cl = (size_t)G.dims.di * (G.dims.dc - 1), sl = (size_t)G.dims.di * 16;
+    const Pool& p = G.batch;
+    if (conv_out && hipMemcpy(conv_out, p.conv + ((size_t)layer * p.cap + slot) * cl, cl * 4, hipMemcpyDeviceToHost) !=
+                        hipSuccess)
+        return BACKEND_FORWARD_FAILED;
+    if (ssm_out && hipMemcpy(ssm_out, p.ssm + ((size_t)layer * p.cap + slot) * sl, sl * 4, hipMemcpyDeviceToHost) !=
+                       hipSuccess)
+        return BACKEND_FORWARD_FAILED;
+    return BACKEND_OK;
+}
+
+}  // extern "C"
