@@ -56,19 +56,25 @@ def weight_bytes(dims: rbin.MambaDims, profile: int) -> dict:
 
 
 def algorithmic_bytes(dims: rbin.MambaDims, profile: int, n: int) -> dict:
-    """Bytes each kernel class must move per launch at n streams (compulsory traffic)."""
+    """Compulsory HBM bytes of one launch of each kernel class at n streams: weights once,
+    every activation and state element read or written once."""
     d, di, xr, V, dc = dims.d_model, dims.d_inner, dims.xr, dims.vocab, dims.d_conv
     w = weight_bytes(dims, profile)
     f = 4
+    nxb = di // 64
+    emb_row = d * f if profile & 3 == 0 else d + (4 if profile & 3 == 2 else d // 64 * f)
     return {
-        "embed": n * d * f * (2 if profile & 3 == 0 else 1) + (n * d // 64 * f if profile & 3 else 0),
-        "norm": 2 * n * d * f + d * f,
-        "in_proj": w["in_proj"] + n * d * f + n * 2 * di * f,
-        "conv": n * (2 * di * (dc - 1) * f + di * f + di * f) + di * (dc + 1) * f,
-        "x_proj": w["x_proj"] + n * di * f + n * xr * f,
-        "scan": n * (2 * di * 16 * f + 3 * di * f + xr * f) + w["dt_proj"] + di * 16 * f + 2 * di * f,
-        "out_proj": w["out_proj"] + n * di * f + 2 * n * d * f,
-        "head": w["head"] + n * d * f + n * V * f,
+        "embed": n * (emb_row + d * f),
+        # norm weights, in_proj, x_proj; x in; conv state in+out; conv w/b; u, z, x_proj partials out
+        "mix_in": d * f + w["in_proj"] + w["x_proj"] + n * d * f + n * 2 * di * (dc - 1) * f + di * (dc + 1) * f
+        + n * 2 * di * f + nxb * n * xr * f,
+        # partials in; dt_proj, dt_b, exp(A_log), D; u, z in; ssm state in+out; gated limbs out
+        "scan": nxb * n * xr * f + w["dt_proj"] + di * f + di * 16 * f + di * f + n * 2 * di * f
+        + n * 2 * di * 16 * f + n * di * 3 * 2,
+        # out_proj; gated limbs in; residual in+out
+        "mix_out": w["out_proj"] + n * di * 3 * 2 + 2 * n * d * f,
+        # final norm, head, x in, logits out
+        "head": d * f + w["head"] + n * d * f + n * V * f,
         "softmax": 2 * n * V * f,
     }
 
@@ -190,8 +196,7 @@ def main() -> int:
     for name, cls in ffi.KERNEL_CLASSES.items():
         if name == "softmax":
             continue
-        launches = dims.n_layer if name in ("in_proj", "conv", "x_proj", "scan", "out_proj") else (
-            dims.n_layer + 1 if name == "norm" else 1)
+        launches = dims.n_layer if name in ("mix_in", "scan", "mix_out") else 1
         evs = [hip.Event() for _ in range(2 * launches * P)]
         arr = (ctypes.c_void_p * len(evs))(*[e.h for e in evs])
         be.probe_kernel(cls, arr)

@@ -132,7 +132,9 @@ void* redukt_backend_stream(void);
 /* Measurement hook.  While kernel_class != 0, every launch of that kernel class is
  * bracketed by two hipEvent_t records taken in order from events[0..n_events) (caller
  * owned, alive while probing); recording stops when they run out.  Classes: 1 embed,
- * 2 norm, 3 in_proj, 4 conv, 5 x_proj, 6 scan, 7 out_proj, 8 head, 9 softmax.
+ * 2 mix_in (norm + in_proj + conv + x_proj partials), 3 scan (dt_proj + selective scan +
+ * gate), 4 mix_out (out_proj + residual), 5 head (final norm + LM head), 6 softmax.
+ * Probed steps are launched kernel by kernel instead of from the step's hipGraph.
  * kernel_class 0 switches the probe off.  Returns OK or INVALID_ARGUMENT. */
 int32_t redukt_backend_probe_kernel(uint32_t kernel_class, void** events, uint32_t n_events);
 

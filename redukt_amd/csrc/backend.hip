@@ -23,10 +23,11 @@
 
 namespace rdk {
 
-size_t DMat::bytes() const {
+size_t TMat::bytes() const {
     if (!w) return 0;
-    const size_t n = (size_t)rq * 4 * cols;
-    return group == 0 ? n * 4 : n + (size_t)rq * 4 * (cols / group) * 4;
+    const size_t n = (size_t)rt * kRowTile * ks * kKStep;
+    if (group == 0) return n * 4;
+    return n + (size_t)rt * kRowTile * (group == cols ? 1 : ks / 2) * 4;
 }
 
 namespace {
@@ -34,21 +35,21 @@ namespace {
 constexpr uint32_t kRbinMagic = 0x55504752u;  // "RGPU"
 constexpr uint32_t kFlagNormBias = 1u << 0;
 constexpr uint32_t kFlagUntiedHead = 1u << 1;
-constexpr int kMaxCols = 2048;  // 8 column quads per lane in the projection kernel
+constexpr int kMaxCols = 1024;  // d_model: activations of 32 streams staged in LDS, dt_rank in registers
 
 struct Model {
     bool ready = false;
     Dims dims;
     uint32_t profile = 0;
     std::vector<DLayer> layers;
-    DLayer* d_layers_host = nullptr;  // same as layers.data(); kernels take DLayer by value
-    DMat emb, head_own;
+    TMat emb, head_own;
     bool tied = true;
     float* norm_f_w = nullptr;
     float* norm_f_b = nullptr;
     std::vector<void*> allocs;
     hipStream_t stream = nullptr;
     Pool v1, batch;
+    StepRunner runner;
     uint32_t* d_err = nullptr;
     int device = 0;
     Probe probe;
@@ -99,19 +100,30 @@ int quantize(const float* w, int rows, int cols, int group, std::vector<int8_t>&
     return group;
 }
 
-// Pack a row-major [rows][cols] matrix into 4x4 tiles (see DMat) and upload it, F32 or
-// quantized.  quant_group: 0 = F32, else the requested Q8 group (cols = per row).
-bool make_mat(DMat& m, const float* w, int rows, int cols, int quant_group) {
+// Tile a row-major [rows][cols] matrix for the matrix-core kernels (see TMat) and upload
+// it, F32 or quantized.  quant_group: 0 = F32, else the requested Q8 group (cols = per
+// row).
+bool make_tmat(TMat& m, const float* w, int rows, int cols, int quant_group) {
     m.rows = rows;
     m.cols = cols;
-    m.rq = (rows + 3) / 4;
-    const int kqn = cols / 4;
-    const size_t tiles = (size_t)m.rq * kqn;
+    m.rt = (rows + kRowTile - 1) / kRowTile;
+    const int kp = (cols + kKAlign - 1) / kKAlign * kKAlign;
+    m.ks = kp / kKStep;
+    const size_t elems = (size_t)m.rt * kRowTile * kp;
+    auto f32_index = [&](int r, int k) {
+        const int t = r / kRowTile, st = k / kKStep;
+        const int lane = r % kRowTile + kRowTile * ((k % kKStep) / 8);
+        return (((size_t)t * m.ks + st) * 64 + lane) * 8 + k % 8;
+    };
+    auto q8_index = [&](int r, int k) {
+        const int t = r / kRowTile, st = k / kKStep;
+        const int lane = r % kRowTile + kRowTile * ((k % kKStep) / 8);
+        return ((((size_t)t * (m.ks / 2) + st / 2) * 64 + lane) * 2 + st % 2) * 8 + k % 8;
+    };
     if (quant_group == 0) {
-        std::vector<float> t(tiles * 16, 0.0f);
+        std::vector<float> t(elems, 0.0f);
         for (int r = 0; r < rows; r++)
-            for (int k = 0; k < cols; k++)
-                t[((size_t)(r / 4) * kqn + k / 4) * 16 + (r % 4) * 4 + (k % 4)] = w[(size_t)r * cols + k];
+            for (int k = 0; k < cols; k++) t[f32_index(r, k)] = w[(size_t)r * cols + k];
         m.group = 0;
         m.w = dev_upload(t.data(), t.size());
         return m.w != nullptr;
@@ -119,13 +131,14 @@ bool make_mat(DMat& m, const float* w, int rows, int cols, int quant_group) {
     std::vector<int8_t> q;
     std::vector<float> sc;
     m.group = quantize(w, rows, cols, quant_group, q, sc);
-    const int gpr = cols / m.group;
-    std::vector<int8_t> t(tiles * 16, 0);
+    std::vector<int8_t> t(elems, 0);
     for (int r = 0; r < rows; r++)
-        for (int k = 0; k < cols; k++)
-            t[((size_t)(r / 4) * kqn + k / 4) * 16 + (r % 4) * 4 + (k % 4)] = q[(size_t)r * cols + k];
-    std::vector<float> scp((size_t)m.rq * 4 * gpr, 0.0f);
-    std::memcpy(scp.data(), sc.data(), sizeof(float) * sc.size());
+        for (int k = 0; k < cols; k++) t[q8_index(r, k)] = q[(size_t)r * cols + k];
+    const int gpr = cols / m.group;               // scales per row as quantized
+    const int spr = m.group == cols ? 1 : m.ks / 2;  // scales per row as stored
+    std::vector<float> scp((size_t)m.rt * kRowTile * spr, 0.0f);
+    for (int r = 0; r < rows; r++)
+        for (int g = 0; g < gpr; g++) scp[(size_t)r * spr + g] = sc[(size_t)r * gpr + g];
     m.w = dev_upload(t.data(), t.size());
     m.scales = dev_upload(scp.data(), scp.size());
     return m.w && m.scales;
@@ -155,10 +168,11 @@ int load_weights(const std::string& path, uint32_t profile) {
     if (hdr_ok) {
         hdr_ok = h[2] && h[3] && h[4] && h[5] && h[7] && h[8] && h[6] >= 2;
         if (h[1] == 2) hdr_ok = hdr_ok && h[10] <= 1 && !(h[10] == 0 && h[2] != 256);
-        // Kernel limits: 16 SSM states per channel, column counts in whole quads and at
-        // most kMaxCols so a projection row's tiles fit in one lane's registers.
-        hdr_ok = hdr_ok && h[5] == 16 && h[3] % 4 == 0 && h[4] % 4 == 0 && h[3] <= (uint32_t)kMaxCols &&
-                 h[4] <= (uint32_t)kMaxCols;
+        // Kernel limits: 16 SSM states per channel; d_model in whole 32-column k-steps and
+        // at most kMaxCols; d_inner in whole 64-channel conv-branch blocks; x_proj rows
+        // (dt_rank <= 64) held in registers.
+        hdr_ok = hdr_ok && h[5] == 16 && h[3] % 32 == 0 && h[4] % 64 == 0 && h[3] <= (uint32_t)kMaxCols &&
+                 h[7] <= 64;
     }
     if (!hdr_ok) {
         log("bad/unsupported .rbin header in %s", path.c_str());
@@ -178,7 +192,7 @@ int load_weights(const std::string& path, uint32_t profile) {
     bool ok = true;
     {
         std::vector<float> e = rd.read(V * d);
-        ok = rd.ok && make_mat(G.emb, e.data(), (int)V, (int)d, qgroup((int)d));
+        ok = rd.ok && make_tmat(G.emb, e.data(), (int)V, (int)d, qgroup((int)d));
     }
     G.layers.assign(D.nl, DLayer{});
     for (uint32_t i = 0; ok && i < D.nl; i++) {
@@ -186,29 +200,37 @@ int load_weights(const std::string& path, uint32_t profile) {
         std::vector<float> t = rd.read(d);
         ok = rd.ok && (L.norm_w = dev_upload(t.data(), d));
         if (ok && nb) { t = rd.read(d); ok = rd.ok && (L.norm_b = dev_upload(t.data(), d)); }
-        if (ok) { t = rd.read(2 * di * d); ok = rd.ok && make_mat(L.in_proj, t.data(), (int)(2 * di), (int)d, qgroup((int)d)); }
+        if (ok) {
+            t = rd.read(2 * di * d);
+            ok = rd.ok && make_tmat(L.in_x, t.data(), (int)di, (int)d, qgroup((int)d)) &&
+                 make_tmat(L.in_z, t.data() + di * d, (int)di, (int)d, qgroup((int)d));
+        }
         if (ok) { t = rd.read(di * dc); ok = rd.ok && (L.conv_w = dev_upload(t.data(), di * dc)); }
         if (ok) { t = rd.read(di); ok = rd.ok && (L.conv_b = dev_upload(t.data(), di)); }
         if (ok) {
             t = rd.read(xr * di);
-            ok = rd.ok && make_mat(L.x_proj, t.data(), (int)xr, (int)di, qsmall ? qgroup((int)di) : 0);
+            ok = rd.ok && make_tmat(L.x_proj, t.data(), (int)xr, (int)di, qsmall ? qgroup((int)di) : 0);
         }
         if (ok) {
             t = rd.read(di * dr);
             ok = rd.ok;
+            L.dt_pad = (int)((dr + 15) / 16 * 16);
+            const size_t dp = (size_t)L.dt_pad;
             if (ok && !qsmall) {
-                std::vector<float> tt(dr * di);
+                std::vector<float> tp(di * dp, 0.0f);
                 for (size_t j = 0; j < di; j++)
-                    for (size_t k = 0; k < dr; k++) tt[k * di + j] = t[j * dr + k];
-                ok = (L.dt_wt = dev_upload(tt.data(), tt.size())) != nullptr;
+                    for (size_t k = 0; k < dr; k++) tp[j * dp + k] = t[j * dr + k];
+                ok = (L.dt_w = dev_upload(tp.data(), tp.size())) != nullptr;
             } else if (ok) {
                 std::vector<int8_t> q;
                 std::vector<float> sc;
-                L.dt_group = quantize(t.data(), (int)di, (int)dr, qgroup((int)dr), q, sc);
-                std::vector<int8_t> qt(dr * di);
+                // dt_rank <= 64: a 64-column group is the whole row or falls back to per-row.
+                const int grp = quantize(t.data(), (int)di, (int)dr, qgroup((int)dr), q, sc);
+                std::vector<int8_t> qp(di * dp, 0);
                 for (size_t j = 0; j < di; j++)
-                    for (size_t k = 0; k < dr; k++) qt[k * di + j] = q[j * dr + k];
-                ok = (L.dt_qt = dev_upload(qt.data(), qt.size())) && (L.dt_scales = dev_upload(sc.data(), sc.size()));
+                    for (size_t k = 0; k < dr; k++) qp[j * dp + k] = q[j * dr + k];
+                ok = grp == (int)dr && (L.dt_q = dev_upload(qp.data(), qp.size())) &&
+                     (L.dt_scales = dev_upload(sc.data(), sc.size()));
             }
         }
         if (ok) { t = rd.read(di); ok = rd.ok && (L.dt_b = dev_upload(t.data(), di)); }
@@ -218,7 +240,7 @@ int load_weights(const std::string& path, uint32_t profile) {
             ok = rd.ok && (L.a_exp = dev_upload(t.data(), t.size()));
         }
         if (ok) { t = rd.read(di); ok = rd.ok && (L.d_vec = dev_upload(t.data(), di)); }
-        if (ok) { t = rd.read(d * di); ok = rd.ok && make_mat(L.out_proj, t.data(), (int)d, (int)di, qgroup((int)di)); }
+        if (ok) { t = rd.read(d * di); ok = rd.ok && make_tmat(L.out_proj, t.data(), (int)d, (int)di, qgroup((int)di)); }
         if (ok && ((i + 1) % 8 == 0 || i + 1 == D.nl)) log("loaded layer %u/%u", i + 1, D.nl);
     }
     if (ok) { std::vector<float> t = rd.read(d); ok = rd.ok && (G.norm_f_w = dev_upload(t.data(), d)); }
@@ -226,7 +248,7 @@ int load_weights(const std::string& path, uint32_t profile) {
     G.tied = !uh;
     if (ok && uh) {
         std::vector<float> t = rd.read(V * d);
-        ok = rd.ok && make_mat(G.head_own, t.data(), (int)V, (int)d, qgroup((int)d));
+        ok = rd.ok && make_tmat(G.head_own, t.data(), (int)V, (int)d, qgroup((int)d));
     }
     fclose(f);
     return ok ? 0 : -1;
@@ -238,7 +260,7 @@ void dev_free_all() {
 }
 
 void pool_free(Pool& p) {
-    void* bufs[] = {p.conv, p.ssm, p.x, p.normed, p.xz, p.conv_out, p.zp, p.gated, p.out, p.d_slots, p.d_tokens};
+    void* bufs[] = {p.conv, p.ssm, p.x, p.u, p.z, p.xpart, p.glimb, p.out, p.slots, p.d_slots, p.d_tokens};
     for (void* b : bufs) (void)hipFree(b);
     if (p.h_slots) (void)hipHostFree(p.h_slots);
     if (p.h_tokens) (void)hipHostFree(p.h_tokens);
@@ -260,10 +282,12 @@ bool pool_alloc(Pool& p, uint32_t cap) {
     const size_t n = cap, d = D.d, di = D.di;
     p = Pool{};
     p.cap = cap;
+    p.gcap = (cap + 15) / 16;
     bool ok = dev_zero(p.conv, (size_t)D.nl * n * di * (D.dc - 1)) && dev_zero(p.ssm, (size_t)D.nl * n * di * 16) &&
-              dev_zero(p.x, n * d) && dev_zero(p.normed, n * d) && dev_zero(p.xz, n * 2 * di) &&
-              dev_zero(p.conv_out, n * di) && dev_zero(p.zp, n * D.xr()) && dev_zero(p.gated, n * di) &&
-              dev_zero(p.out, n * D.vocab) && dev_zero(p.d_slots, n) && dev_zero(p.d_tokens, n);
+              dev_zero(p.x, n * d) && dev_zero(p.u, n * di) && dev_zero(p.z, n * di) &&
+              dev_zero(p.xpart, xpart_floats(D, cap)) && dev_zero(p.glimb, glimb_elems(D, cap)) &&
+              dev_zero(p.out, n * D.vocab) && dev_zero(p.slots, n) && dev_zero(p.d_slots, n) &&
+              dev_zero(p.d_tokens, n);
     ok = ok && hipHostMalloc((void**)&p.h_slots, sizeof(uint32_t) * n, hipHostMallocDefault) == hipSuccess;
     ok = ok && hipHostMalloc((void**)&p.h_tokens, sizeof(uint32_t) * n, hipHostMallocDefault) == hipSuccess;
     ok = ok && (p.seen = (uint8_t*)calloc(n, 1)) != nullptr;
@@ -272,6 +296,7 @@ bool pool_alloc(Pool& p, uint32_t cap) {
 
 void free_model() {
     if (G.stream) (void)hipStreamSynchronize(G.stream);
+    G.runner.clear();
     pool_free(G.v1);
     pool_free(G.batch);
     dev_free_all();
@@ -279,25 +304,14 @@ void free_model() {
     G = Model{};
 }
 
-StepArgs step_args(Pool& p, uint32_t n, const uint32_t* slots, const uint32_t* tokens, float* out, bool probs,
-                   bool check) {
-    StepArgs a;
-    a.dims = &G.dims;
-    a.layers = G.layers.data();
-    a.emb = &G.emb;
-    a.head = G.tied ? &G.emb : &G.head_own;
-    a.norm_f_w = G.norm_f_w;
-    a.norm_f_b = G.norm_f_b;
-    a.pool = &p;
-    a.n = n;
-    a.slots = slots;
-    a.tokens = tokens;
-    a.out = out;
-    a.probs = probs;
-    a.check = check;
-    a.err = G.d_err;
-    a.probe = &G.probe;
-    return a;
+ModelView model_view() {
+    return ModelView{&G.dims, G.layers.data(), &G.emb, G.tied ? &G.emb : &G.head_own, G.norm_f_w, G.norm_f_b};
+}
+
+hipError_t run_step(Pool& p, uint32_t n, const uint32_t* slots, const uint32_t* tokens, float* out, bool probs,
+                    bool check) {
+    StepIO io{n, slots, tokens, out, probs, check, G.d_err};
+    return G.runner.run(model_view(), p, io, G.stream, &G.probe);
 }
 
 // pool_forward semantics (mamba_cuda.cu:604-635): validate on the host (nothing is
@@ -315,8 +329,7 @@ int pool_forward(Pool& p, uint32_t n, const uint32_t* slots, const uint32_t* tok
     if (hipMemcpyAsync(p.d_slots, p.h_slots, ib, hipMemcpyHostToDevice, G.stream) != hipSuccess ||
         hipMemcpyAsync(p.d_tokens, p.h_tokens, ib, hipMemcpyHostToDevice, G.stream) != hipSuccess)
         return BACKEND_FORWARD_FAILED;
-    if (enqueue_step(step_args(p, n, p.d_slots, p.d_tokens, p.out, probs, false), G.stream) != hipSuccess)
-        return BACKEND_FORWARD_FAILED;
+    if (run_step(p, n, p.d_slots, p.d_tokens, p.out, probs, false) != hipSuccess) return BACKEND_FORWARD_FAILED;
     if (hipMemcpyAsync(out, p.out, sizeof(float) * n * G.dims.vocab, hipMemcpyDeviceToHost, G.stream) != hipSuccess)
         return BACKEND_FORWARD_FAILED;
     if (hipStreamSynchronize(G.stream) != hipSuccess) return BACKEND_FORWARD_FAILED;
@@ -428,6 +441,7 @@ int32_t redukt_backend_batch_init(uint32_t max_streams) {
     if (!G.ready) return BACKEND_INIT_FAILED;
     if (max_streams > BACKEND_MAX_STREAMS) return BACKEND_INVALID_ARGUMENT;
     if (hipStreamSynchronize(G.stream) != hipSuccess) return BACKEND_INIT_FAILED;
+    G.runner.clear();
     pool_free(G.batch);
     if (max_streams == 0) return BACKEND_OK;
     if (!pool_alloc(G.batch, max_streams)) {
@@ -476,8 +490,9 @@ int32_t redukt_backend_forward_batch_device(uint32_t n_streams, const uint32_t* 
     if (vocab_size != G.dims.vocab || n_streams > G.batch.cap) return BACKEND_INVALID_ARGUMENT;
     if (n_streams == 0) return BACKEND_OK;
     if (!d_slots || !d_tokens || !d_out) return BACKEND_INVALID_ARGUMENT;
-    StepArgs a = step_args(G.batch, n_streams, d_slots, d_tokens, d_out, (flags & 1u) != 0, true);
-    return enqueue_step(a, G.stream) == hipSuccess ? BACKEND_OK : BACKEND_FORWARD_FAILED;
+    return run_step(G.batch, n_streams, d_slots, d_tokens, d_out, (flags & 1u) != 0, true) == hipSuccess
+               ? BACKEND_OK
+               : BACKEND_FORWARD_FAILED;
 }
 
 int32_t redukt_backend_device_status(void) {

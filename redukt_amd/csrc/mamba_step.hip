@@ -1,0 +1,1283 @@
+// mamba_step.hip — gfx950 kernels of one Mamba-1 token step for N lockstep streams.
+//
+// Per layer three kernels (all replayed from one hipGraph per step shape):
+//   k_mix_in : RMSNorm of the residual stream, in_proj on the matrix cores, then for the
+//              conv branch the causal conv1d step + SiLU and the split-K partial sums of
+//              x_proj over this workgroup's 64 channels; for the gate branch z.
+//   k_scan   : x_proj partials reduced in a fixed order, dt_proj + softplus, the d16
+//              selective scan with the D skip, the SiLU gate; writes the gated vector as
+//              bf16 limbs already tiled for the next matrix-core product.
+//   k_mix_out: out_proj on the matrix cores, four k-quarters summed in a fixed order,
+//              plus the residual.
+// and per step k_embed (+ device-side argument check), k_head (final norm + LM head) and
+// optionally k_softmax.
+//
+// Projections.  v_mfma_f32_16x16x32_bf16 multiplies bf16 operands exactly into f32
+// accumulators.  Every f32 activation is split into three bf16 limbs (hi + mid + lo
+// reproduces it to ~2^-24 relative); int8 weights are exact in bf16, so a Q8 product
+// takes three MFMAs per k-step; F32 weights are split the same way and take the six
+// limb products that reach 2^-24.  Activations are the B operand (16 streams per MFMA
+// column group), weights the A operand (16 rows per tile).
+//
+// Determinism and batch invariance: an output element's value depends only on its own
+// row and stream — MFMA columns are independent, every accumulation runs over k-steps
+// and limbs in a fixed order, cross-wave and split-K partials are summed in a fixed
+// order — never on n, the batch position or the slot; so one kernel family serves every
+// batch size.  No atomics take part in any arithmetic.
+//
+// The element-wise phases (conv + SiLU, dt_proj + softplus, scan, gate, softmax) are
+// per-thread code in the reference's own operation order and math
+// (src/infrastructure/mamba/model.rs:134-190, src/domain/tensor.rs:759-1325), so they
+// reproduce the CPU path's bits for identical inputs.  Contraction is off in this file.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstring>
+#include <memory>
+
+#include "model.h"
+#include "portable_math.h"
+
+#pragma clang fp contract(off)
+
+namespace rdk {
+
+size_t xpart_floats(const Dims& d, uint32_t cap) {
+    const size_t xr_pad = (d.xr() + kRowTile - 1) / kRowTile * kRowTile;
+    return (size_t)(d.di / 64) * cap * xr_pad;
+}
+
+size_t glimb_elems(const Dims& d, uint32_t cap) {
+    const size_t groups = (cap + 15) / 16;
+    return groups * (d.di / kKStep) * 3 * 64 * 8;
+}
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+constexpr int kBlock = 256;
+constexpr int kWaves = kBlock / kWave;
+constexpr int kChunk = 32;                 // streams per k_mix_in / k_head workgroup
+constexpr int kGroups = kChunk / kRowTile; // MFMA column groups per chunk
+constexpr int kLimbBytes = 64 * 8 * 2;     // one B fragment of one limb: 1 KB
+constexpr int kHeadTiles = 4;              // row tiles per wave in k_head
+constexpr int kRing = 4;                   // weight k-pairs in flight per wave (loop unrolled by it)
+constexpr int kTps = 8;                    // threads per stream while staging activations
+constexpr int kQuadBatch = 4;              // column quads a staging thread loads per iteration
+constexpr int kMaxDr = 64;                 // dt_rank limit (d_model <= 1024)
+constexpr int kMaxXr = kMaxDr + 32;        // x_proj rows
+constexpr int kOutWaves = 8;               // waves of k_mix_out
+constexpr int kOutPairs = 3;               // k-pairs per k_mix_out wave per pass
+
+__device__ __forceinline__ f32x4 mma(const bf16x8& a, const bf16x8& b, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+struct Limb3 {
+    __bf16 h, m, l;
+};
+
+// v = h + m + l: h = bf16(v), m = bf16(v - h), l = bf16(v - h - m); both differences are
+// exact in f32, so only the last rounding (below 2^-24 relative) is lost.
+__device__ __forceinline__ Limb3 split3(float v) {
+    Limb3 o;
+    o.h = (__bf16)v;
+    const float r = v - (float)o.h;
+    o.m = (__bf16)r;
+    o.l = (__bf16)(r - (float)o.m);
+    return o;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+
+__device__ __forceinline__ uint32_t clamp_slot(uint32_t s, uint32_t cap) { return s < cap ? s : cap - 1; }
+
+// ---------------------------------------------------------------- weight fragments
+
+// The A operand of one k-step: F32 weights as three limbs, Q8 weights as one exact one.
+struct AFrag {
+    bf16x8 h, m, l;
+};
+
+// Raw bytes of the fragments of k-steps [2p, 2p+2) of one lane: Q8 16 B, F32 64 B.
+struct RawPair {
+    int4 v[4];
+};
+
+template <bool Q8>
+__device__ __forceinline__ RawPair load_pair(const TMat& w, int t, int p, int lane) {
+    RawPair r;
+    if (Q8) {
+        r.v[0] = ((const int4*)w.w)[((size_t)t * (w.ks / 2) + p) * 64 + lane];
+    } else {
+        const int4* base = (const int4*)w.w;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const size_t f = (((size_t)t * w.ks + 2 * p + h) * 64 + lane) * 2;
+            r.v[2 * h] = base[f];
+            r.v[2 * h + 1] = base[f + 1];
+        }
+    }
+    return r;
+}
+
+template <bool Q8>
+__device__ __forceinline__ void decode_pair(const RawPair& r, AFrag& a0, AFrag& a1) {
+    if (Q8) {
+        const int w[4] = {r.v[0].x, r.v[0].y, r.v[0].z, r.v[0].w};
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            a0.h[j] = (__bf16)(float)(int8_t)(w[j / 4] >> (8 * (j % 4)));
+            a1.h[j] = (__bf16)(float)(int8_t)(w[2 + j / 4] >> (8 * (j % 4)));
+        }
+    } else {
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            AFrag& a = h ? a1 : a0;
+            const int4 lo = r.v[2 * h], hi = r.v[2 * h + 1];
+            const int w[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const Limb3 t = split3(bits_to_f((uint32_t)w[j]));
+                a.h[j] = t.h;
+                a.m[j] = t.m;
+                a.l[j] = t.l;
+            }
+        }
+    }
+}
+
+// acc += A * B for one k-step: Q8 three products (B limbs hi, mid, lo), F32 the six limb
+// products hi*hi, hi*mid, mid*hi, hi*lo, mid*mid, lo*hi — always in this order.
+template <bool Q8>
+__device__ __forceinline__ f32x4 mma_step(const AFrag& a, const bf16x8& bh, const bf16x8& bm, const bf16x8& bl,
+                                          f32x4 acc) {
+    if (Q8) {
+        acc = mma(a.h, bh, acc);
+        acc = mma(a.h, bm, acc);
+        acc = mma(a.h, bl, acc);
+    } else {
+        acc = mma(a.h, bh, acc);
+        acc = mma(a.h, bm, acc);
+        acc = mma(a.m, bh, acc);
+        acc = mma(a.h, bl, acc);
+        acc = mma(a.m, bm, acc);
+        acc = mma(a.l, bh, acc);
+    }
+    return acc;
+}
+
+__device__ __forceinline__ bf16x8 lds_frag(const __bf16* base) { return *(const bf16x8*)base; }
+
+// ---------------------------------------------------------------- activation staging
+
+// Norm of the chunk's streams and their bf16 limbs into LDS in B-fragment order:
+// lds[((g*ks + s)*3 + limb)*512 + lane*8 + j] = limb of normed(x[b0 + 16g + lane%16])
+// [32s + 8(lane/16) + j].  Streams >= n and columns >= d are zero.  RMSNorm
+// x*inv*w with inv = 1/sqrt(mean(x^2) + 1e-5) (tensor.rs:900-908) or LayerNorm
+// (tensor.rs:1390-1398).  Eight threads share a stream; each walks its column quads in
+// order (kQuadBatch loads in flight), then the eight partials meet in a fixed xor
+// butterfly (commutative pairings: every lane ends with the same bits).  The loops stay
+// rolled: these kernels run once per CU per step, so their code must stay small.
+__device__ __forceinline__ float4 quad_or_zero(const float4* p, int q, bool ok) {
+    return ok ? p[q] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+}
+
+__device__ void stage_normed(__bf16* lds, const float* __restrict__ x, const float* __restrict__ nw,
+                             const float* __restrict__ nb, int d, int ks, uint32_t b0, uint32_t n) {
+    const int bb = threadIdx.x / kTps, sub = threadIdx.x % kTps;
+    const uint32_t b = b0 + bb;
+    const bool live = b < n;
+    const int dq = d / 4;
+    const int qpt = ks * kKStep / 4 / kTps;  // quads per thread over the padded columns
+    const float4* xb = (const float4*)(x + (size_t)(live ? b : b0) * d);
+    float mean = 0.0f;
+    if (nb != nullptr) {
+        float s1 = 0.0f;
+#pragma unroll 1
+        for (int i0 = 0; i0 < qpt; i0 += kQuadBatch) {
+            float4 v[kQuadBatch];
+#pragma unroll
+            for (int u = 0; u < kQuadBatch; u++) {
+                const int q = sub + kTps * (i0 + u);
+                v[u] = quad_or_zero(xb, q, live && i0 + u < qpt && q < dq);
+            }
+#pragma unroll
+            for (int u = 0; u < kQuadBatch; u++) {
+                s1 += v[u].x;
+                s1 += v[u].y;
+                s1 += v[u].z;
+                s1 += v[u].w;
+            }
+        }
+#pragma unroll
+        for (int o = 1; o < kTps; o <<= 1) s1 += __shfl_xor(s1, o, kWave);
+        mean = s1 / (float)d;
+    }
+    float ss = 0.0f;
+#pragma unroll 1
+    for (int i0 = 0; i0 < qpt; i0 += kQuadBatch) {
+        float4 v[kQuadBatch];
+#pragma unroll
+        for (int u = 0; u < kQuadBatch; u++) {
+            const int q = sub + kTps * (i0 + u);
+            v[u] = quad_or_zero(xb, q, live && i0 + u < qpt && q < dq);
+        }
+#pragma unroll
+        for (int u = 0; u < kQuadBatch; u++) {
+            const int q = sub + kTps * (i0 + u);
+            if (nb == nullptr) {
+                ss += v[u].x * v[u].x;
+                ss += v[u].y * v[u].y;
+                ss += v[u].z * v[u].z;
+                ss += v[u].w * v[u].w;
+            } else if (q < dq) {
+                const float c[4] = {v[u].x - mean, v[u].y - mean, v[u].z - mean, v[u].w - mean};
+#pragma unroll
+                for (int e = 0; e < 4; e++) ss += c[e] * c[e];
+            }
+        }
+    }
+#pragma unroll
+    for (int o = 1; o < kTps; o <<= 1) ss += __shfl_xor(ss, o, kWave);
+    const float inv = 1.0f / sqrtf(ss / (float)d + 1e-5f);
+    const int g = bb / kRowTile;
+    typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+#pragma unroll 1
+    for (int i0 = 0; i0 < qpt; i0 += kQuadBatch) {
+        float4 v[kQuadBatch], w4[kQuadBatch], c4[kQuadBatch];
+#pragma unroll
+        for (int u = 0; u < kQuadBatch; u++) {
+            const int q = sub + kTps * (i0 + u);
+            const bool ok = live && i0 + u < qpt && q < dq;
+            v[u] = quad_or_zero(xb, q, ok);
+            w4[u] = quad_or_zero((const float4*)nw, q, ok);
+            c4[u] = quad_or_zero((const float4*)nb, q, ok && nb != nullptr);
+        }
+#pragma unroll
+        for (int u = 0; u < kQuadBatch; u++) {
+            const int q = sub + kTps * (i0 + u);
+            if (i0 + u >= qpt) continue;
+            const float xs[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+            const float ws[4] = {w4[u].x, w4[u].y, w4[u].z, w4[u].w};
+            const float cs[4] = {c4[u].x, c4[u].y, c4[u].z, c4[u].w};
+            bf16x4 h, m, l;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                float val = 0.0f;
+                if (live && q < dq) val = nb == nullptr ? xs[e] * inv * ws[e] : (xs[e] - mean) * inv * ws[e] + cs[e];
+                const Limb3 t3 = split3(val);
+                h[e] = t3.h;
+                m[e] = t3.m;
+                l[e] = t3.l;
+            }
+            const int k0 = 4 * q, st = k0 / kKStep, within = k0 % kKStep;
+            const int ln = (bb % kRowTile) + kRowTile * (within / 8);
+            __bf16* dst = lds + ((size_t)(g * ks + st) * 3) * 512 + ln * 8 + (within % 8);
+            *(bf16x4*)dst = h;
+            *(bf16x4*)(dst + 512) = m;
+            *(bf16x4*)(dst + 1024) = l;
+        }
+    }
+    __syncthreads();
+}
+
+// Row tiles a wave multiplies together, with a ring of their next kRing weight k-pairs
+// (requested ahead of the product, for instance while the activations stage).
+template <bool Q8, int T>
+struct Tiles {
+    int t[T];
+    bool ok[T];
+    RawPair ring[kRing][T];
+};
+
+template <bool Q8, int T>
+__device__ __forceinline__ void tiles_prefetch(const TMat& w, Tiles<Q8, T>& tl) {
+    const int lane = threadIdx.x % kWave;
+    const int np = w.ks / 2;
+#pragma unroll
+    for (int q = 0; q < kRing; q++)
+#pragma unroll
+        for (int i = 0; i < T; i++)
+            if (tl.ok[i] && q < np) tl.ring[q][i] = load_pair<Q8>(w, tl.t[i], q, lane);
+}
+
+// T row tiles times the staged activations of `ng` column groups over all k-steps.
+// Accumulators are kept per limb order so consecutive MFMAs are independent: Q8 order o
+// holds the products with activation limb o; F32 order 0 holds hi*hi, order 1 hi*mid and
+// mid*hi, order 2 hi*lo, mid*mid and lo*hi.  The row sum is (o0 + o1) + o2.  With Q8
+// group-64 scales each k-pair's partial (all limbs, fixed order) is scaled into order 0.
+// The weight ring is refilled kRing pairs ahead; the loop body covers one turn of the
+// ring and stays rolled.  Per-row scales are left to the caller.
+template <bool Q8, int T>
+__device__ __forceinline__ void tiles_gemm(const TMat& w, Tiles<Q8, T>& tl, const __bf16* lds, int ng,
+                                           f32x4 (&out)[T][kGroups]) {
+    const int lane = threadIdx.x % kWave;
+    const int np = w.ks / 2;
+    const bool grp = Q8 && w.group != w.cols;
+    const int gpr = w.ks / 2;
+    f32x4 acc[T][kGroups][3];
+#pragma unroll
+    for (int i = 0; i < T; i++)
+#pragma unroll
+        for (int g = 0; g < kGroups; g++)
+#pragma unroll
+            for (int o = 0; o < 3; o++) acc[i][g][o] = f32x4{0, 0, 0, 0};
+#pragma unroll 1
+    for (int p0 = 0; p0 < np; p0 += kRing) {
+#pragma unroll
+        for (int q = 0; q < kRing; q++) {
+            const int p = p0 + q;
+            if (p >= np) continue;
+            bf16x8 bf[kGroups][2][3];
+#pragma unroll
+            for (int g = 0; g < kGroups; g++) {
+                if (g >= ng) continue;
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const __bf16* f = lds + ((size_t)(g * w.ks + 2 * p + h) * 3) * 512 + lane * 8;
+#pragma unroll
+                    for (int m = 0; m < 3; m++) bf[g][h][m] = lds_frag(f + m * 512);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < T; i++) {
+                if (!tl.ok[i]) continue;
+                const RawPair cur = tl.ring[q][i];
+                if (p + kRing < np) tl.ring[q][i] = load_pair<Q8>(w, tl.t[i], p + kRing, lane);
+                AFrag a[2];
+                decode_pair<Q8>(cur, a[0], a[1]);
+                float sc[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+                if (grp) {
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        sc[e] = w.scales[(size_t)(tl.t[i] * kRowTile + (lane / 16) * 4 + e) * gpr + p];
+                }
+#pragma unroll
+                for (int g = 0; g < kGroups; g++) {
+                    if (g >= ng) continue;
+                    if (grp) {
+                        f32x4 tmp{0, 0, 0, 0};
+#pragma unroll
+                        for (int h = 0; h < 2; h++) tmp = mma_step<Q8>(a[h], bf[g][h][0], bf[g][h][1], bf[g][h][2], tmp);
+#pragma unroll
+                        for (int e = 0; e < 4; e++) acc[i][g][0][e] = __builtin_fmaf(tmp[e], sc[e], acc[i][g][0][e]);
+                    } else {
+#pragma unroll
+                        for (int h = 0; h < 2; h++) {
+                            if (Q8) {
+                                acc[i][g][0] = mma(a[h].h, bf[g][h][0], acc[i][g][0]);
+                                acc[i][g][1] = mma(a[h].h, bf[g][h][1], acc[i][g][1]);
+                                acc[i][g][2] = mma(a[h].h, bf[g][h][2], acc[i][g][2]);
+                            } else {
+                                acc[i][g][0] = mma(a[h].h, bf[g][h][0], acc[i][g][0]);
+                                acc[i][g][1] = mma(a[h].h, bf[g][h][1], acc[i][g][1]);
+                                acc[i][g][1] = mma(a[h].m, bf[g][h][0], acc[i][g][1]);
+                                acc[i][g][2] = mma(a[h].h, bf[g][h][2], acc[i][g][2]);
+                                acc[i][g][2] = mma(a[h].m, bf[g][h][1], acc[i][g][2]);
+                                acc[i][g][2] = mma(a[h].l, bf[g][h][0], acc[i][g][2]);
+                            }
+                        }
+                    }
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < T; i++)
+#pragma unroll
+        for (int g = 0; g < kGroups; g++) out[i][g] = (acc[i][g][0] + acc[i][g][1]) + acc[i][g][2];
+}
+
+__device__ __forceinline__ void apply_row_scales(const TMat& w, int t, f32x4 (&acc)[kGroups], int ng) {
+    if (w.group == 0 || w.group != w.cols) return;
+    const int lane = threadIdx.x % kWave;
+    float sc[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) sc[i] = w.scales[t * kRowTile + (lane / 16) * 4 + i];
+#pragma unroll
+    for (int g = 0; g < kGroups; g++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[g][i] = acc[g][i] * sc[i];
+}
+
+// ---------------------------------------------------------------- embedding
+
+struct EmbedArgs {
+    TMat emb;
+    float* x;                  // [n][d]
+    const uint32_t* tokens;    // caller's device pointers
+    const uint32_t* slots_in;
+    uint32_t* slots;           // validated copy used by the rest of the step
+    uint32_t n, cap;
+    int check;
+    uint32_t* err;
+};
+
+// x[b] = emb[token[b]] (Q8: q * scale), model.rs:93-101 / gemv.rs:285-295.  Block (0, b)
+// copies slot b into the step's slot list; with `check` it also validates the slot and
+// the token and looks for duplicate slots, recording failures in *err and clamping so
+// no index can leave its buffer.
+__global__ __launch_bounds__(kBlock) void k_embed(EmbedArgs a) {
+    const uint32_t b = blockIdx.y;
+    const int d = a.emb.cols;
+    uint32_t tok = a.tokens[b];
+    if (blockIdx.x == 0) {
+        const uint32_t s = a.slots_in[b];
+        if (a.check) {
+            bool dup = false;
+            for (uint32_t c = threadIdx.x; c < a.n; c += blockDim.x)
+                if (c != b && a.slots_in[c] == s) dup = true;
+            if (threadIdx.x == 0 && (tok >= (uint32_t)a.emb.rows || s >= a.cap)) atomicOr(a.err, 1u);
+            if (dup) atomicOr(a.err, 2u);
+        }
+        if (threadIdx.x == 0) a.slots[b] = clamp_slot(s, a.cap);
+    }
+    if (tok >= (uint32_t)a.emb.rows) tok = a.emb.rows - 1;
+    const int k = blockIdx.x * kBlock + threadIdx.x;
+    if (k >= d) return;
+    const int t = tok / kRowTile, s = k / kKStep;
+    const int ln = (tok % kRowTile) + kRowTile * ((k % kKStep) / 8), j = k % 8;
+    float v;
+    if (a.emb.group == 0) {
+        v = ((const float*)a.emb.w)[(((size_t)t * a.emb.ks + s) * 64 + ln) * 8 + j];
+    } else {
+        const int8_t q = ((const int8_t*)a.emb.w)[((((size_t)t * (a.emb.ks / 2) + s / 2) * 64 + ln) * 2 + s % 2) * 8 + j];
+        const float sc = a.emb.group == a.emb.cols ? a.emb.scales[tok]
+                                                   : a.emb.scales[(size_t)tok * (a.emb.ks / 2) + k / a.emb.group];
+        v = (float)q * sc;
+    }
+    a.x[(size_t)b * d + k] = v;
+}
+
+// ---------------------------------------------------------------- k_mix_in
+
+struct MixInArgs {
+    const float* x;            // [n][d] residual stream
+    const float* norm_w;
+    const float* norm_b;
+    TMat wx, wz, wxp;          // in_proj conv branch, gate branch; x_proj
+    int nxb;                   // conv-branch workgroups (64 channels each)
+    float* conv_st;            // this layer's conv state, [slot][di][dc-1]
+    const float* conv_w;
+    const float* conv_b;
+    const uint32_t* slots;
+    uint32_t cap, n;
+    float* u;                  // [n][di]
+    float* z;                  // [n][di]
+    float* xpart;              // [nxb][cap][xr_pad]
+    int di, dc, d, xr_pad;
+};
+
+template <bool Q8, bool Q8XP>
+__global__ __launch_bounds__(kBlock) void k_mix_in(MixInArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    __bf16* lds = (__bf16*)smem;
+    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    const uint32_t b0 = blockIdx.y * kChunk;
+    const int ng = (int)min((uint32_t)kGroups, (a.n - b0 + kRowTile - 1) / kRowTile);
+    const bool conv_branch = (int)blockIdx.x < a.nxb;
+    const TMat& w = conv_branch ? a.wx : a.wz;
+    const int t = (conv_branch ? blockIdx.x : blockIdx.x - a.nxb) * kWaves + wave;
+    const bool has_rows = t < w.rt;
+    Tiles<Q8, 1> tl;
+    tl.t[0] = t;
+    tl.ok[0] = has_rows;
+    tiles_prefetch<Q8, 1>(w, tl);  // weights in flight while the activations stage
+    stage_normed(lds, a.x, a.norm_w, a.norm_b, a.d, a.wx.ks, b0, a.n);
+
+    f32x4 acc[kGroups];
+    if (has_rows) {
+        f32x4 o[1][kGroups];
+        tiles_gemm<Q8, 1>(w, tl, lds, ng, o);
+#pragma unroll
+        for (int g = 0; g < kGroups; g++) acc[g] = o[0][g];
+        apply_row_scales(w, t, acc, ng);
+    }
+    const int j0 = t * kRowTile + (lane / 16) * 4;  // this lane's 4 consecutive channels
+    if (!conv_branch) {
+        if (has_rows && j0 < a.di) {
+#pragma unroll
+            for (int g = 0; g < kGroups; g++) {
+                const uint32_t b = b0 + g * kRowTile + lane % 16;
+                if (g >= ng) continue;
+                if (b < a.n) *(float4*)(a.z + (size_t)b * a.di + j0) = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
+            }
+        }
+        return;
+    }
+    // Conv branch: conv1d step + SiLU per (channel, stream), conv_silu_block order
+    // (model.rs:134-153) and silu_inplace's 256-channel body/tail rule (tensor.rs:1207-1211).
+    __syncthreads();  // every wave is done reading the staged activations
+    const int dc = a.dc;
+    // All conv operands of this lane's 4 channels x kGroups streams, requested at once.
+    float cwv[4][4], cbv[4];
+    if (dc == 4) {
+        const float4* cw4 = (const float4*)(a.conv_w + (size_t)j0 * 4);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float4 v = cw4[i];
+            cwv[i][0] = v.x; cwv[i][1] = v.y; cwv[i][2] = v.z; cwv[i][3] = v.w;
+        }
+        const float4 b4 = *(const float4*)(a.conv_b + j0);
+        cbv[0] = b4.x; cbv[1] = b4.y; cbv[2] = b4.z; cbv[3] = b4.w;
+    }
+    float4 stv[kGroups][3];
+    uint32_t slot_of[kGroups];
+#pragma unroll
+    for (int g = 0; g < kGroups; g++) {
+        const uint32_t b = b0 + g * kRowTile + lane % 16;
+        slot_of[g] = clamp_slot(a.slots[b < a.n ? b : b0], a.cap);
+        if (dc == 4 && g < ng && b < a.n) {
+            const float4* sp = (const float4*)(a.conv_st + ((size_t)slot_of[g] * a.di + j0) * 3);
+#pragma unroll
+            for (int k = 0; k < 3; k++) stv[g][k] = sp[k];
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < kGroups; g++) {
+        const uint32_t b = b0 + g * kRowTile + lane % 16;
+        float uv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (g < ng && has_rows && b < a.n && j0 < a.di) {
+            const uint32_t s = slot_of[g];
+            if (dc == 4) {
+                float st[12] = {stv[g][0].x, stv[g][0].y, stv[g][0].z, stv[g][0].w, stv[g][1].x, stv[g][1].y,
+                                stv[g][1].z, stv[g][1].w, stv[g][2].x, stv[g][2].y, stv[g][2].z, stv[g][2].w};
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float xv = acc[g][i];
+                    float val = 0.0f;
+                    val += st[3 * i] * cwv[i][0];
+                    val += st[3 * i + 1] * cwv[i][1];
+                    val += st[3 * i + 2] * cwv[i][2];
+                    val += xv * cwv[i][3];
+                    val += cbv[i];
+                    st[3 * i] = st[3 * i + 1];
+                    st[3 * i + 1] = st[3 * i + 2];
+                    st[3 * i + 2] = xv;
+                    uv[i] = val;
+                }
+                float4* sp = (float4*)(a.conv_st + ((size_t)s * a.di + j0) * 3);
+                sp[0] = make_float4(st[0], st[1], st[2], st[3]);
+                sp[1] = make_float4(st[4], st[5], st[6], st[7]);
+                sp[2] = make_float4(st[8], st[9], st[10], st[11]);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int j = j0 + i;
+                    float* st = a.conv_st + ((size_t)s * a.di + j) * (dc - 1);
+                    const float* cw = a.conv_w + (size_t)j * dc;
+                    const float xv = acc[g][i];
+                    float val = 0.0f;
+                    for (int k = 0; k < dc - 1; k++) val += st[k] * cw[k];
+                    val += xv * cw[dc - 1];
+                    val += a.conv_b[j];
+                    for (int k = 0; k + 2 < dc; k++) st[k] = st[k + 1];
+                    st[dc - 2] = xv;
+                    uv[i] = val;
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int j = j0 + i;
+                const int blk0 = j / 256 * 256;
+                const int len = min(256, a.di - blk0);
+                const bool body = (j - blk0) < len / 8 * 8;
+                const float val = uv[i];
+                const float sg = body ? lane_sigmoid_f(val) : 1.0f / (1.0f + exp_f(-val));
+                uv[i] = val * sg;
+            }
+            *(float4*)(a.u + (size_t)b * a.di + j0) = make_float4(uv[0], uv[1], uv[2], uv[3]);
+        }
+        // u as the B operand of x_proj over this block's 64 channels: two k-steps.
+        const int cl = wave * kRowTile + (lane / 16) * 4;  // local channel of uv[0]
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int c = cl + i, s = c / kKStep;
+            const int ln = (lane % 16) + kRowTile * ((c % kKStep) / 8);
+            const Limb3 t3 = split3(uv[i]);
+            __bf16* dst = lds + ((size_t)(g * 2 + s) * 3) * 512 + ln * 8 + (c % 8);
+            dst[0] = t3.h;
+            dst[512] = t3.m;
+            dst[1024] = t3.l;
+        }
+    }
+    __syncthreads();
+    // Split-K partial of x_proj: rows r of x_proj against this block's channels.
+    for (int tp = wave; tp < a.wxp.rt; tp += kWaves) {
+        const int p = blockIdx.x;  // k-pair index of x_proj = conv-branch block
+        RawPair raw = load_pair<Q8XP>(a.wxp, tp, p, lane);
+        AFrag a0, a1;
+        decode_pair<Q8XP>(raw, a0, a1);
+        float sc[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+        if (Q8XP) {
+            const bool grp = a.wxp.group != a.wxp.cols;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int r = tp * kRowTile + (lane / 16) * 4 + i;
+                sc[i] = grp ? a.wxp.scales[(size_t)r * (a.wxp.ks / 2) + p] : a.wxp.scales[r];
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < kGroups; g++) {
+            if (g >= ng) continue;
+            const __bf16* f0 = lds + ((size_t)(g * 2) * 3) * 512 + lane * 8;
+            const __bf16* f1 = f0 + 3 * 512;
+            f32x4 part{0, 0, 0, 0};
+            part = mma_step<Q8XP>(a0, lds_frag(f0), lds_frag(f0 + 512), lds_frag(f0 + 1024), part);
+            part = mma_step<Q8XP>(a1, lds_frag(f1), lds_frag(f1 + 512), lds_frag(f1 + 1024), part);
+            const uint32_t b = b0 + g * kRowTile + lane % 16;
+            if (b < a.n) {
+                float* dst = a.xpart + ((size_t)p * a.cap + b) * a.xr_pad + tp * kRowTile + (lane / 16) * 4;
+                *(float4*)dst = make_float4(part[0] * sc[0], part[1] * sc[1], part[2] * sc[2], part[3] * sc[3]);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------- k_scan
+
+struct ScanArgs {
+    const float* xpart;    // [nxb][cap][xr_pad]
+    int nxb, xr_pad, xr;
+    const float* u;        // [n][di]
+    const float* z;        // [n][di]
+    float* ssm;            // this layer's state, [slot][di][16]
+    const float* dt_w;     // F32 [di][dt_pad] or null
+    const int8_t* dt_q;    // Q8 [di][dt_pad] or null
+    const float* dt_scales;  // Q8: one per row
+    int dt_pad;
+    const float* dt_b;
+    const float* a_exp;    // [di][16]
+    const float* d_vec;
+    const uint32_t* slots;
+    uint32_t cap, n;
+    __bf16* glimb;         // [groups][di/32][3][64][8]
+    int di, dr;
+};
+
+// dot_avx2_order (tensor.rs:1680-1693) over one column of the transposed dt_proj.
+template <typename T>
+__device__ __forceinline__ float dot_ref_col(const T* __restrict__ wt, int stride, const float* v, int n) {
+    const int body = n / 8 * 8;
+    float l[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int c = 0; c < body; c += 8)
+#pragma unroll
+        for (int i = 0; i < 8; i++) l[i] += (float)wt[(size_t)(c + i) * stride] * v[c + i];
+    float s = ((l[0] + l[4]) + (l[2] + l[6])) + ((l[1] + l[5]) + (l[3] + l[7]));
+    for (int c = body; c < n; c++) s += (float)wt[(size_t)c * stride] * v[c];
+    return s;
+}
+
+// scan_block (model.rs:174-190) for one (stream, channel): x_proj row sums, dt_proj row in
+// the reference order, softplus(dt + b) (tensor.rs:859-861), the d16 recurrence with the
+// dt-sparse skip and the hsum_ssm tree (tensor.rs:1283-1325), y * (z * sigmoid(z))
+// (tensor.rs:1239-1243 on 64-channel blocks); the gated value leaves as bf16 limbs.
+// Every operand is requested before the first wait.
+__global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
+    __shared__ float zp[kMaxXr];
+    const int di = a.di, dr = a.dr;
+    const int j_raw = blockIdx.x * kBlock + threadIdx.x;
+    const bool live = j_raw < di;
+    const int j = live ? j_raw : di - 1;
+    const uint32_t b = blockIdx.y;
+    const uint32_t s = clamp_slot(a.slots[b], a.cap);
+    // Per-channel operands, requested first.
+    const float4* ap = (const float4*)(a.a_exp + (size_t)j * 16);
+    float4 av[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) av[i] = ap[i];
+    const float x = a.u[(size_t)b * di + j];
+    const float zz = a.z[(size_t)b * di + j];
+    const float dv = a.d_vec[j];
+    const float dtb = a.dt_b[j];
+    float4* stp = (float4*)(a.ssm + ((size_t)s * di + j) * 16);
+    float4 sv[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) sv[i] = stp[i];
+    float wdt[kMaxDr];
+    if (a.dt_w) {
+        const float4* wp = (const float4*)(a.dt_w + (size_t)j * a.dt_pad);
+#pragma unroll
+        for (int q = 0; q < kMaxDr / 4; q++) {
+            const float4 v = q * 4 < a.dt_pad ? wp[q] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            wdt[4 * q] = v.x; wdt[4 * q + 1] = v.y; wdt[4 * q + 2] = v.z; wdt[4 * q + 3] = v.w;
+        }
+    } else {
+        const int4* qp = (const int4*)(a.dt_q + (size_t)j * a.dt_pad);
+#pragma unroll
+        for (int q = 0; q < kMaxDr / 16; q++) {
+            const int4 v = q * 16 < a.dt_pad ? qp[q] : make_int4(0, 0, 0, 0);
+            const int wv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int e = 0; e < 16; e++) wdt[16 * q + e] = (float)(int8_t)(wv[e / 4] >> (8 * (e % 4)));
+        }
+    }
+    // x_proj partials of this stream (threads < xr), summed in block order.
+    const int r = threadIdx.x;
+    if (r < a.xr) {
+        float acc = 0.0f;
+        const float* pp = a.xpart + (size_t)b * a.xr_pad + r;
+        const size_t pstride = (size_t)a.cap * a.xr_pad;
+#pragma unroll 1
+        for (int p0 = 0; p0 < a.nxb; p0 += 4) {
+            float pv[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) pv[u] = p0 + u < a.nxb ? pp[(size_t)(p0 + u) * pstride] : 0.0f;
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+                if (p0 + u < a.nxb) acc += pv[u];
+        }
+        zp[r] = acc;
+    }
+    __syncthreads();
+    if (!live) return;
+    // dot_avx2_order (tensor.rs:1680-1693): eight lanes by column residue, fixed tree, tail.
+    // dt_rank <= 64 means a quantized dt_proj has one scale per row (a 64-column group
+    // spans the whole row or the group rule falls back to per-row), so the Q8 row is
+    // 0 + dot * scale (gemv.rs:490-502).  The row (padded to dt_pad columns) was loaded
+    // into wdt before the partial sums.
+    float dt;
+    {
+        const int body = dr / 8 * 8;
+        float l[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+        for (int c = 0; c < kMaxDr; c += 8) {
+            if (c < body) {
+#pragma unroll
+                for (int i = 0; i < 8; i++) l[i] += wdt[c + i] * zp[c + i];
+            }
+        }
+        float sdot = ((l[0] + l[4]) + (l[2] + l[6])) + ((l[1] + l[5]) + (l[3] + l[7]));
+#pragma unroll
+        for (int c = 0; c < kMaxDr; c++)
+            if (c >= body && c < dr) sdot += wdt[c] * zp[c];
+        dt = a.dt_w ? sdot : 0.0f + sdot * a.dt_scales[j];
+    }
+    dt = softplus_f(dt + dtb);
+    float st[16];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        st[4 * i] = sv[i].x; st[4 * i + 1] = sv[i].y; st[4 * i + 2] = sv[i].z; st[4 * i + 3] = sv[i].w;
+    }
+    const float* B = zp + dr;
+    const float* C = zp + dr + 16;
+    if (!(fabsf(dt) < 1e-6f)) {
+        const float dtx = dt * x;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float aa[4] = {av[i].x, av[i].y, av[i].z, av[i].w};
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const int k = 4 * i + c;
+                const float da = lane_exp_f(0.0f - dt * aa[c]);
+                st[k] = da * st[k] + dtx * B[k];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) stp[i] = make_float4(st[4 * i], st[4 * i + 1], st[4 * i + 2], st[4 * i + 3]);
+    }
+    float l[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) l[i] = st[i] * C[i] + st[i + 8] * C[i + 8];
+    const float y = ((l[0] + l[4]) + (l[1] + l[5])) + ((l[2] + l[6]) + (l[3] + l[7])) + dv * x;
+    const int blk0 = j / 64 * 64;
+    const int len = min(64, di - blk0);
+    const bool body = (j - blk0) < len / 8 * 8;
+    const float sg = body ? lane_sigmoid_f(zz) : 1.0f / (1.0f + exp_f(-zz));
+    const float gv = y * (zz * sg);
+    const Limb3 t3 = split3(gv);
+    const int g = b / kRowTile, sk = j / kKStep;
+    const int ln = (b % kRowTile) + kRowTile * ((j % kKStep) / 8);
+    __bf16* dst = a.glimb + ((((size_t)g * (di / kKStep) + sk) * 3) * 64 + ln) * 8 + (j % 8);
+    dst[0] = t3.h;
+    dst[512] = t3.m;
+    dst[1024] = t3.l;
+}
+
+// ---------------------------------------------------------------- k_mix_out
+
+struct MixOutArgs {
+    TMat w;                  // out_proj [d][di]
+    const __bf16* glimb;     // gated limbs, B fragments
+    float* x;                // [n][d] residual, updated in place
+    uint32_t n;
+    int d;
+};
+
+// out_proj + residual.  Eight waves share one 16-row tile, each summing an eighth of the
+// k-pairs (limb orders in separate accumulators, as in tiles_gemm) with kOutPairs pairs of
+// weight and activation fragments requested at once; the eighths are added in wave order,
+// then the per-row scale, then the residual: x += (((q0 + q1) + q2) + ... + q7).
+template <bool Q8>
+__global__ __launch_bounds__(kOutWaves * kWave) void k_mix_out(MixOutArgs a) {
+    __shared__ f32x4 part[kOutWaves - 1][kGroups][kWave];
+    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    const int t = blockIdx.x;
+    const uint32_t b0 = blockIdx.y * kChunk;
+    const int ng = (int)min((uint32_t)kGroups, (a.n - b0 + kRowTile - 1) / kRowTile);
+    const TMat& w = a.w;
+    const int np = w.ks / 2;
+    const int p_lo = wave * np / kOutWaves, p_hi = (wave + 1) * np / kOutWaves;
+    const bool grp = Q8 && w.group != w.cols;
+    const int gpr = w.ks / 2;
+    const uint32_t g0 = b0 / kRowTile;
+    f32x4 acc3[kGroups][3];
+#pragma unroll
+    for (int g = 0; g < kGroups; g++)
+#pragma unroll
+        for (int o = 0; o < 3; o++) acc3[g][o] = f32x4{0, 0, 0, 0};
+#pragma unroll 1
+    for (int pb = p_lo; pb < p_hi; pb += kOutPairs) {
+        RawPair raw[kOutPairs];
+        bf16x8 bfr[kOutPairs][kGroups][2][3];
+        float sc[kOutPairs][4];
+#pragma unroll
+        for (int q = 0; q < kOutPairs; q++) {
+            const int p = pb + q;
+            if (p >= p_hi) break;
+            raw[q] = load_pair<Q8>(w, t, p, lane);
+#pragma unroll
+            for (int g = 0; g < kGroups; g++) {
+                if (g >= ng) continue;
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const __bf16* f = a.glimb + (((size_t)(g0 + g) * w.ks + 2 * p + h) * 3) * 512 + lane * 8;
+                    bfr[q][g][h][0] = lds_frag(f);
+                    bfr[q][g][h][1] = lds_frag(f + 512);
+                    bfr[q][g][h][2] = lds_frag(f + 1024);
+                }
+            }
+            if (grp) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) sc[q][i] = w.scales[(size_t)(t * kRowTile + (lane / 16) * 4 + i) * gpr + p];
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < kOutPairs; q++) {
+            const int p = pb + q;
+            if (p >= p_hi) break;
+            AFrag a0, a1;
+            decode_pair<Q8>(raw[q], a0, a1);
+#pragma unroll
+            for (int g = 0; g < kGroups; g++) {
+                if (g >= ng) continue;
+                if (grp) {
+                    f32x4 pp{0, 0, 0, 0};
+                    pp = mma_step<Q8>(a0, bfr[q][g][0][0], bfr[q][g][0][1], bfr[q][g][0][2], pp);
+                    pp = mma_step<Q8>(a1, bfr[q][g][1][0], bfr[q][g][1][1], bfr[q][g][1][2], pp);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) acc3[g][0][i] = __builtin_fmaf(pp[i], sc[q][i], acc3[g][0][i]);
+                } else {
+#pragma unroll
+                    for (int h = 0; h < 2; h++) {
+                        const AFrag& af = h ? a1 : a0;
+                        const bf16x8* bb = bfr[q][g][h];
+                        if (Q8) {
+                            acc3[g][0] = mma(af.h, bb[0], acc3[g][0]);
+                            acc3[g][1] = mma(af.h, bb[1], acc3[g][1]);
+                            acc3[g][2] = mma(af.h, bb[2], acc3[g][2]);
+                        } else {
+                            acc3[g][0] = mma(af.h, bb[0], acc3[g][0]);
+                            acc3[g][1] = mma(af.h, bb[1], acc3[g][1]);
+                            acc3[g][1] = mma(af.m, bb[0], acc3[g][1]);
+                            acc3[g][2] = mma(af.h, bb[2], acc3[g][2]);
+                            acc3[g][2] = mma(af.m, bb[1], acc3[g][2]);
+                            acc3[g][2] = mma(af.l, bb[0], acc3[g][2]);
+                        }
+                    }
+                }
+            }
+        }
+    }
+    f32x4 acc[kGroups];
+#pragma unroll
+    for (int g = 0; g < kGroups; g++) acc[g] = (acc3[g][0] + acc3[g][1]) + acc3[g][2];
+    if (wave > 0) {
+#pragma unroll
+        for (int g = 0; g < kGroups; g++) part[wave - 1][g][lane] = acc[g];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    float rs[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+    if (Q8 && !grp) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) rs[i] = w.scales[t * kRowTile + (lane / 16) * 4 + i];
+    }
+    const int r0 = t * kRowTile + (lane / 16) * 4;
+#pragma unroll
+    for (int g = 0; g < kGroups; g++) {
+        if (g >= ng) continue;
+        f32x4 s = acc[g];
+        for (int q = 0; q < kOutWaves - 1; q++) s = s + part[q][g][lane];
+        const uint32_t b = b0 + g * kRowTile + lane % 16;
+        if (b < a.n && r0 < a.d) {
+            float4* xp = (float4*)(a.x + (size_t)b * a.d + r0);
+            const float4 xv = *xp;
+            *xp = make_float4(xv.x + s[0] * rs[0], xv.y + s[1] * rs[1], xv.z + s[2] * rs[2], xv.w + s[3] * rs[3]);
+        }
+    }
+}
+
+// ---------------------------------------------------------------- k_head
+
+struct HeadArgs {
+    const float* x;
+    const float* norm_w;
+    const float* norm_b;
+    TMat w;                  // head [vocab][d]
+    float* out;              // [n][vocab]
+    uint32_t n;
+    int d;
+};
+
+// Final norm (model.rs:745-752) and the LM head (model.rs:921-927, tied to the
+// embedding unless the file carries lm_head).  Each wave multiplies kHeadTiles row tiles
+// together, so every activation fragment read from LDS serves all of them.
+template <bool Q8>
+__global__ __launch_bounds__(kBlock) void k_head(HeadArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    __bf16* lds = (__bf16*)smem;
+    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    const uint32_t b0 = blockIdx.y * kChunk;
+    const int ng = (int)min((uint32_t)kGroups, (a.n - b0 + kRowTile - 1) / kRowTile);
+    const int V = a.w.rows;
+    const int t_first = (blockIdx.x * kWaves + wave) * kHeadTiles;
+    Tiles<Q8, kHeadTiles> tl;
+#pragma unroll
+    for (int i = 0; i < kHeadTiles; i++) {
+        tl.t[i] = t_first + i;
+        tl.ok[i] = t_first + i < a.w.rt;
+    }
+    tiles_prefetch<Q8, kHeadTiles>(a.w, tl);
+    stage_normed(lds, a.x, a.norm_w, a.norm_b, a.d, a.w.ks, b0, a.n);
+    f32x4 res[kHeadTiles][kGroups];
+    tiles_gemm<Q8, kHeadTiles>(a.w, tl, lds, ng, res);
+#pragma unroll
+    for (int tt = 0; tt < kHeadTiles; tt++) {
+        const int t = t_first + tt;
+        if (t >= a.w.rt) continue;
+        f32x4 acc[kGroups];
+#pragma unroll
+        for (int g = 0; g < kGroups; g++) acc[g] = res[tt][g];
+        apply_row_scales(a.w, t, acc, ng);
+        const int r0 = t * kRowTile + (lane / 16) * 4;
+#pragma unroll
+        for (int g = 0; g < kGroups; g++) {
+            const uint32_t b = b0 + g * kRowTile + lane % 16;
+            if (g >= ng || b >= a.n) continue;
+            float* o = a.out + (size_t)b * V + r0;
+            if (r0 + 3 < V && (V & 3) == 0) {
+                *(float4*)o = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
+            } else {
+                for (int i = 0; i < 4; i++)
+                    if (r0 + i < V) o[i] = acc[g][i];
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------- softmax
+
+struct SoftmaxArgs {
+    float* out;
+    int vocab;
+};
+
+// softmax_into (tensor.rs:1917-1933) per stream, in place: max, exp(l - max) with the
+// portable exp, the sum (fixed block tree instead of the sequential loop), division
+// by max(sum, FLT_EPSILON).
+__global__ __launch_bounds__(1024) void k_softmax(SoftmaxArgs a) {
+    __shared__ float sh[1024 / kWave];
+    float* row = a.out + (size_t)blockIdx.x * a.vocab;
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    float mx = -INFINITY;
+    for (int i = threadIdx.x; i < a.vocab; i += 1024) mx = fmaxf(mx, row[i]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
+    if (lane == 0) sh[wave] = mx;
+    __syncthreads();
+    mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 1024 / kWave; w++) mx = fmaxf(mx, sh[w]);
+    __syncthreads();
+    if (mx == -INFINITY) {
+        const float u = 1.0f / (float)a.vocab;
+        for (int i = threadIdx.x; i < a.vocab; i += 1024) row[i] = u;
+        return;
+    }
+    float s = 0.0f;
+    for (int i = threadIdx.x; i < a.vocab; i += 1024) {
+        const float e = exp_f(row[i] - mx);
+        row[i] = e;
+        s += e;
+    }
+    s = wave_sum(s);
+    if (lane == 0) sh[wave] = s;
+    __syncthreads();
+    float tsum = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 1024 / kWave; w++) tsum += sh[w];
+    const float denom = fmaxf(tsum, 1.1920929e-07f);
+    for (int i = threadIdx.x; i < a.vocab; i += 1024) row[i] = row[i] / denom;
+}
+
+// ---------------------------------------------------------------- reset
+
+struct ZeroArgs {
+    float* base;
+    const uint32_t* slots;
+    uint32_t cap;
+    size_t stride, layer_stride;
+    int nl;
+};
+
+__global__ __launch_bounds__(kBlock) void k_zero_slots(ZeroArgs a) {
+    const uint32_t s = a.slots[blockIdx.y];
+    if (s >= a.cap) return;
+    for (int l = 0; l < a.nl; l++) {
+        float* p = a.base + (size_t)l * a.layer_stride + (size_t)s * a.stride;
+        for (size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x; i < a.stride; i += (size_t)gridDim.x * kBlock)
+            p[i] = 0.0f;
+    }
+}
+
+// ---------------------------------------------------------------- step assembly
+
+}  // namespace
+
+struct Launch {
+    const void* fn;
+    dim3 grid, block;
+    uint32_t lds;
+    uint32_t cls;
+    std::unique_ptr<unsigned char[]> args;
+    void* argp;
+    template <typename A>
+    static Launch make(const void* fn, dim3 g, dim3 b, uint32_t lds, uint32_t cls, const A& a) {
+        Launch l;
+        l.fn = fn;
+        l.grid = g;
+        l.block = b;
+        l.lds = lds;
+        l.cls = cls;
+        l.args.reset(new unsigned char[sizeof(A)]);
+        memcpy(l.args.get(), &a, sizeof(A));
+        l.argp = l.args.get();
+        return l;
+    }
+};
+
+namespace {
+
+uint32_t stage_lds_bytes(int ks) { return (uint32_t)(kGroups * ks * 3 * kLimbBytes); }
+
+template <typename K>
+void allow_lds(K* fn, uint32_t bytes) {
+    static uint32_t set = 0;
+    if (bytes > set) {
+        (void)hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+        set = bytes;
+    }
+}
+
+const void* mix_in_fn(bool q8, bool q8xp, uint32_t lds) {
+    if (q8 && q8xp) { allow_lds(k_mix_in<true, true>, lds); return (const void*)k_mix_in<true, true>; }
+    if (q8) { allow_lds(k_mix_in<true, false>, lds); return (const void*)k_mix_in<true, false>; }
+    if (q8xp) { allow_lds(k_mix_in<false, true>, lds); return (const void*)k_mix_in<false, true>; }
+    allow_lds(k_mix_in<false, false>, lds);
+    return (const void*)k_mix_in<false, false>;
+}
+
+const void* head_fn(bool q8, uint32_t lds) {
+    if (q8) { allow_lds(k_head<true>, lds); return (const void*)k_head<true>; }
+    allow_lds(k_head<false>, lds);
+    return (const void*)k_head<false>;
+}
+
+// The launches of one step, in stream order; io_index / head_index / softmax_index name
+// the launches whose arguments carry caller pointers.
+void build_step(const ModelView& m, Pool& p, const StepIO& io, std::vector<Launch>& out, int& io_index,
+                int& head_index, int& softmax_index) {
+    const Dims& D = *m.dims;
+    const uint32_t n = io.n;
+    const int d = (int)D.d, di = (int)D.di;
+    const uint32_t chunks = (n + kChunk - 1) / kChunk;
+    const int xr_pad = m.layers[0].x_proj.rt * kRowTile;
+    const int nxb = di / 64;
+    out.clear();
+    EmbedArgs ea{*m.emb, p.x, io.tokens, io.slots, p.slots, n, p.cap, io.check ? 1 : 0, io.err};
+    io_index = (int)out.size();
+    out.push_back(Launch::make((const void*)k_embed, dim3((d + kBlock - 1) / kBlock, n), dim3(kBlock), 0, KC_EMBED, ea));
+    const size_t conv_layer = (size_t)p.cap * di * (D.dc - 1);
+    const size_t ssm_layer = (size_t)p.cap * di * 16;
+    const bool q8 = m.layers[0].in_x.group != 0;
+    const bool q8xp = m.layers[0].x_proj.group != 0;
+    const uint32_t lds_in = stage_lds_bytes(m.layers[0].in_x.ks);
+    const void* fin = mix_in_fn(q8, q8xp, lds_in);
+    for (uint32_t li = 0; li < D.nl; li++) {
+        const DLayer& L = m.layers[li];
+        MixInArgs ma{p.x, L.norm_w, L.norm_b, L.in_x, L.in_z, L.x_proj, nxb, p.conv + li * conv_layer,
+                     L.conv_w, L.conv_b, p.slots, p.cap, n, p.u, p.z, p.xpart, di, (int)D.dc, d, xr_pad};
+        const int zb = L.in_z.rt / kWaves;
+        out.push_back(Launch::make(fin, dim3(nxb + zb, chunks), dim3(kBlock), lds_in, KC_MIX_IN, ma));
+        ScanArgs sa{p.xpart, nxb, xr_pad, (int)D.xr(), p.u, p.z, p.ssm + li * ssm_layer, L.dt_w, L.dt_q,
+                    L.dt_scales, L.dt_pad, L.dt_b, L.a_exp, L.d_vec, p.slots, p.cap, n, p.glimb, di, (int)D.dr};
+        out.push_back(Launch::make((const void*)k_scan, dim3((di + kBlock - 1) / kBlock, n), dim3(kBlock), 0,
+                                   KC_SCAN, sa));
+        MixOutArgs oa{L.out_proj, p.glimb, p.x, n, d};
+        const void* fo = q8 ? (const void*)k_mix_out<true> : (const void*)k_mix_out<false>;
+        out.push_back(Launch::make(fo, dim3(L.out_proj.rt, chunks), dim3(kOutWaves * kWave), 0, KC_MIX_OUT, oa));
+    }
+    const TMat& H = *m.head;
+    HeadArgs ha{p.x, m.norm_f_w, m.norm_f_b, H, io.out, n, d};
+    const uint32_t lds_h = stage_lds_bytes(H.ks);
+    const int tiles_per_block = kWaves * kHeadTiles;
+    head_index = (int)out.size();
+    out.push_back(Launch::make(head_fn(H.group != 0, lds_h), dim3((H.rt + tiles_per_block - 1) / tiles_per_block, chunks),
+                               dim3(kBlock), lds_h, KC_HEAD, ha));
+    softmax_index = -1;
+    if (io.probs) {
+        softmax_index = (int)out.size();
+        out.push_back(Launch::make((const void*)k_softmax, dim3(n), dim3(1024), 0, KC_SOFTMAX,
+                                   SoftmaxArgs{io.out, (int)D.vocab}));
+    }
+}
+
+hipError_t launch_direct(const Launch& l, hipStream_t st) {
+    void* params[] = {l.argp};
+    return hipLaunchKernel(l.fn, l.grid, l.block, params, l.lds, st);
+}
+
+hipKernelNodeParams node_params(const Launch& l, void** params) {
+    hipKernelNodeParams kp{};
+    kp.func = (void*)l.fn;
+    kp.gridDim = l.grid;
+    kp.blockDim = l.block;
+    kp.sharedMemBytes = l.lds;
+    kp.kernelParams = params;
+    kp.extra = nullptr;
+    return kp;
+}
+
+}  // namespace
+
+#define RDK_TRY(expr)                    \
+    do {                                 \
+        hipError_t e_ = (expr);          \
+        if (e_ != hipSuccess) return e_; \
+    } while (0)
+
+StepRunner::~StepRunner() { clear(); }
+
+void StepRunner::destroy(Graph& g) {
+    if (g.exec) (void)hipGraphExecDestroy(g.exec);
+    if (g.g) (void)hipGraphDestroy(g.g);
+    delete g.launches;
+    g = Graph{};
+}
+
+void StepRunner::clear() {
+    for (Graph& g : graphs_) destroy(g);
+    graphs_.clear();
+}
+
+hipError_t StepRunner::run(const ModelView& m, Pool& p, const StepIO& io, hipStream_t st, Probe* probe) {
+    std::unique_ptr<std::vector<Launch>> owned(new std::vector<Launch>());
+    std::vector<Launch>& seq = *owned;
+    int io_i = -1, head_i = -1, sm_i = -1;
+    build_step(m, p, io, seq, io_i, head_i, sm_i);
+    if (probe && probe->cls != KC_NONE) {
+        for (const Launch& l : seq) {
+            const bool on = l.cls == probe->cls && probe->used + 2 <= probe->cap;
+            if (on) RDK_TRY(hipEventRecord(probe->ev[probe->used], st));
+            RDK_TRY(launch_direct(l, st));
+            if (on) {
+                RDK_TRY(hipEventRecord(probe->ev[probe->used + 1], st));
+                probe->used += 2;
+            }
+        }
+        return hipSuccess;
+    }
+    Graph* hit = nullptr;
+    for (Graph& g : graphs_)
+        if (g.n == io.n && g.probs == io.probs && g.check == io.check && g.pool == &p) hit = &g;
+    if (!hit) {
+        if (graphs_.size() >= 8) {
+            auto old = std::min_element(graphs_.begin(), graphs_.end(),
+                                        [](const Graph& a, const Graph& b) { return a.last_use < b.last_use; });
+            destroy(*old);
+            graphs_.erase(old);
+        }
+        Graph g;
+        g.n = io.n;
+        g.probs = io.probs;
+        g.check = io.check;
+        g.pool = &p;
+        RDK_TRY(hipGraphCreate(&g.g, 0));
+        hipGraphNode_t prev = nullptr;
+        for (size_t i = 0; i < seq.size(); i++) {
+            void* params[] = {seq[i].argp};
+            hipKernelNodeParams kp = node_params(seq[i], params);
+            hipGraphNode_t node;
+            hipError_t e = hipGraphAddKernelNode(&node, g.g, prev ? &prev : nullptr, prev ? 1 : 0, &kp);
+            if (e != hipSuccess) {
+                (void)hipGraphDestroy(g.g);
+                return e;
+            }
+            if ((int)i == io_i) g.io_node = node;
+            if ((int)i == head_i) g.head_node = node;
+            if ((int)i == sm_i) g.softmax_node = node;
+            prev = node;
+        }
+        hipError_t e = hipGraphInstantiate(&g.exec, g.g, nullptr, nullptr, 0);
+        if (e != hipSuccess) {
+            (void)hipGraphDestroy(g.g);
+            return e;
+        }
+        g.launches = owned.release();
+        graphs_.push_back(g);
+        hit = &graphs_.back();
+    } else {
+        // Same shape: only the caller pointers can differ.  The new arguments replace the
+        // stored ones, so the graph's parameter storage stays alive with it.
+        std::vector<Launch>& keep = *hit->launches;
+        keep[io_i] = std::move(seq[io_i]);
+        keep[head_i] = std::move(seq[head_i]);
+        if (sm_i >= 0) keep[sm_i] = std::move(seq[sm_i]);
+        const std::vector<Launch>& cur = keep;
+        void* p_io[] = {cur[io_i].argp};
+        hipKernelNodeParams k_io = node_params(cur[io_i], p_io);
+        RDK_TRY(hipGraphExecKernelNodeSetParams(hit->exec, hit->io_node, &k_io));
+        void* p_h[] = {cur[head_i].argp};
+        hipKernelNodeParams k_h = node_params(cur[head_i], p_h);
+        RDK_TRY(hipGraphExecKernelNodeSetParams(hit->exec, hit->head_node, &k_h));
+        if (sm_i >= 0) {
+            void* p_s[] = {cur[sm_i].argp};
+            hipKernelNodeParams k_s = node_params(cur[sm_i], p_s);
+            RDK_TRY(hipGraphExecKernelNodeSetParams(hit->exec, hit->softmax_node, &k_s));
+        }
+    }
+    hit->last_use = ++clock_;
+    return hipGraphLaunch(hit->exec, st);
+}
+
+hipError_t enqueue_reset(const Dims& D, Pool& P, const uint32_t* d_slots, uint32_t n, hipStream_t st) {
+    if (n == 0) return hipSuccess;
+    const size_t conv_stride = (size_t)D.di * (D.dc - 1), ssm_stride = (size_t)D.di * 16;
+    ZeroArgs zc{P.conv, d_slots, P.cap, conv_stride, (size_t)P.cap * conv_stride, (int)D.nl};
+    k_zero_slots<<<dim3((unsigned)((conv_stride + kBlock - 1) / kBlock), n), kBlock, 0, st>>>(zc);
+    RDK_TRY(hipGetLastError());
+    ZeroArgs zs{P.ssm, d_slots, P.cap, ssm_stride, (size_t)P.cap * ssm_stride, (int)D.nl};
+    k_zero_slots<<<dim3((unsigned)((ssm_stride + kBlock - 1) / kBlock), n), kBlock, 0, st>>>(zs);
+    return hipGetLastError();
+}
+
+}  // namespace rdk

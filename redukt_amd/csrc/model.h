@@ -1,41 +1,54 @@
 // model.h — device-side model and state-pool layout shared by the host code and the
-// kernel launchers of libredukt_gpu.so.
+// kernels of libredukt_gpu.so.
 #pragma once
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <vector>
+
 namespace rdk {
 
-// A projection matrix resident in HBM.  Rows are grouped in quads and columns in
-// quads; one 4x4 tile (4 rows x 4 consecutive columns) is contiguous: 64 bytes for
-// F32, 16 bytes for Q8.  Element (r, k) lives at tile (r/4)*(cols/4) + k/4, offset
-// (r%4)*4 + k%4.  A wavefront lane then streams whole tiles with one 16-byte (Q8) or
-// four 16-byte (F32) loads and applies each activation quad to four rows at once.
-// Rows are zero-padded to a multiple of 4.
-struct DMat {
-    int rows = 0, cols = 0, rq = 0;  // rq = row quads
-    int group = 0;                   // 0: F32; otherwise Q8 columns per scale
-    void* w = nullptr;               // tiles
-    float* scales = nullptr;         // Q8: [rq*4][cols/group]
-    size_t bytes() const;            // HBM bytes of weights + scales
+constexpr int kRowTile = 16;   // MFMA M and N
+constexpr int kKStep = 32;     // MFMA K of v_mfma_f32_16x16x32_bf16
+constexpr int kKAlign = 64;    // column padding: k-steps come in pairs
+
+// A projection matrix resident in HBM, pre-tiled for v_mfma_f32_16x16x32_bf16.
+// Rows are padded to whole 16-row tiles and columns to whole pairs of 32-column k-steps
+// (zeros).  For row tile t and k-step s, lane l of a wavefront owns the A fragment
+// W[16t + l%16][32s + 8(l/16) .. +8]:
+//   F32: [t][s][lane][8 f32]                 — 32 bytes per lane and k-step
+//   Q8 : [t][s/2][lane][s%2][8 int8]         — 16 bytes per lane and k-step pair
+// so every fragment load of a wavefront is one contiguous run (2 KB / 1 KB).
+// Q8 scales: group == cols: one per row, [rt*16]; otherwise (64 columns per scale)
+// [rt*16][ks/2].
+struct TMat {
+    int rows = 0, cols = 0;
+    int rt = 0, ks = 0;   // row tiles, k-steps (even)
+    int group = 0;        // 0: F32; Q8: columns per scale
+    void* w = nullptr;
+    float* scales = nullptr;
+    size_t bytes() const;  // HBM bytes of weights + scales as stored
 };
 
 struct DLayer {
     float* norm_w = nullptr;
-    float* norm_b = nullptr;         // LayerNorm bias (flags bit 0) or null
-    DMat in_proj, x_proj, out_proj;
-    float* conv_w = nullptr;         // [di][dc]
-    float* conv_b = nullptr;         // [di]
-    // dt_proj stored transposed, [dr][di], so lane j of a wave reads column j
-    // coalesced; F32 in dt_wt, or Q8 in dt_qt with dt_scales[di][dr/dt_group].
-    float* dt_wt = nullptr;
-    int8_t* dt_qt = nullptr;
+    float* norm_b = nullptr;   // LayerNorm bias (flags bit 0) or null
+    TMat in_x, in_z;           // in_proj rows [0, di) (conv branch) and [di, 2di) (gate)
+    TMat x_proj;               // [dr + 2*ds][di]
+    TMat out_proj;             // [d][di]
+    float* conv_w = nullptr;   // [di][dc]
+    float* conv_b = nullptr;   // [di]
+    // dt_proj row-major with rows padded to dt_pad (a multiple of 16) columns, so thread j
+    // loads its row with 16-byte vector loads.  F32 in dt_w, or Q8 in dt_q with one scale
+    // per row in dt_scales.
+    float* dt_w = nullptr;
+    int8_t* dt_q = nullptr;
     float* dt_scales = nullptr;
-    int dt_group = 0;
-    float* dt_b = nullptr;           // [di]
-    float* a_exp = nullptr;          // [di][16]: exp(A_log), constant per load
-    float* d_vec = nullptr;          // [di]
+    int dt_pad = 0;
+    float* dt_b = nullptr;     // [di]
+    float* a_exp = nullptr;    // [di][16]: exp(A_log), constant per load
+    float* d_vec = nullptr;    // [di]
 };
 
 struct Dims {
@@ -44,63 +57,98 @@ struct Dims {
 };
 
 // Recurrent state of `cap` slots plus the per-step scratch of `cap` batch rows.
-// State layout: conv [layer][slot][di][dc-1] and ssm [layer][slot][di][16], so a
-// layer's state for one slot is one contiguous run (18 KB + 96 KB at Mamba-130M).
+// State: conv [layer][slot][di][dc-1] and ssm [layer][slot][di][16] f32, so one slot's
+// state of one layer is one contiguous run (18 KB + 96 KB at Mamba-130M).
 struct Pool {
     uint32_t cap = 0;
+    uint32_t gcap = 0;           // stream groups of 16 covering cap
     float* conv = nullptr;
     float* ssm = nullptr;
-    float* x = nullptr;        // [cap][d] residual stream
-    float* normed = nullptr;   // [cap][d]
-    float* xz = nullptr;       // [cap][2*di]
-    float* conv_out = nullptr; // [cap][di]
-    float* zp = nullptr;       // [cap][xr]
-    float* gated = nullptr;    // [cap][di]
-    float* out = nullptr;      // [cap][vocab] logits or probabilities
-    uint32_t* d_slots = nullptr;
+    float* x = nullptr;          // [cap][d] residual stream
+    float* u = nullptr;          // [cap][di] conv + SiLU output
+    float* z = nullptr;          // [cap][di] gate branch
+    float* xpart = nullptr;      // [di/64][cap][xr_pad] split-K partials of x_proj
+    __bf16* glimb = nullptr;     // [gcap][di/32][3][64][8] gated, 3 bf16 limbs, B-fragment tiles
+    float* out = nullptr;        // [cap][vocab] logits or probabilities
+    uint32_t* slots = nullptr;   // [cap] slots of the current step (validated copy)
+    uint32_t* d_slots = nullptr; // [cap] H2D staging targets of the synchronous entry points
     uint32_t* d_tokens = nullptr;
-    uint32_t* h_slots = nullptr;   // pinned staging
+    uint32_t* h_slots = nullptr; // pinned staging
     uint32_t* h_tokens = nullptr;
-    uint8_t* seen = nullptr;       // host duplicate check, cap bytes
+    uint8_t* seen = nullptr;     // host duplicate check, cap bytes
 };
 
 // Kernel classes a caller can time with HIP events (see Probe).
 enum KernelClass : uint32_t {
-    KC_NONE = 0, KC_EMBED = 1, KC_NORM = 2, KC_IN_PROJ = 3, KC_CONV = 4, KC_X_PROJ = 5,
-    KC_SCAN = 6, KC_OUT_PROJ = 7, KC_HEAD = 8, KC_SOFTMAX = 9, KC_COUNT = 10
+    KC_NONE = 0, KC_EMBED = 1, KC_MIX_IN = 2, KC_SCAN = 3, KC_MIX_OUT = 4, KC_HEAD = 5, KC_SOFTMAX = 6,
+    KC_COUNT = 7
 };
 
 // Measurement hook: while cls != KC_NONE, every launch of that class is bracketed by
 // two events taken in order from ev[0..cap) (ev is caller-owned); `used` counts them.
+// Probed steps run as direct launches, not as the replayed graph.
 struct Probe {
     uint32_t cls = KC_NONE;
     hipEvent_t* ev = nullptr;
     uint32_t cap = 0, used = 0;
 };
 
-// Sticky device-side error word for forward_batch_device (bit 0: bad slot or token,
-// bit 1: duplicate slot).
-struct StepArgs {
+struct ModelView {
     const Dims* dims;
-    const DLayer* layers;
-    const DMat* emb;
-    const DMat* head;
+    const DLayer* layers;   // host array of nl layers
+    const TMat* emb;        // the embedding (tiled like a projection)
+    const TMat* head;       // emb when tied
     const float* norm_f_w;
     const float* norm_f_b;
-    Pool* pool;
-    uint32_t n;
-    const uint32_t* slots;   // device
-    const uint32_t* tokens;  // device
-    float* out;              // device [n][vocab]
-    bool probs;
-    bool check;              // run the device-side argument check
-    uint32_t* err;           // device error word
-    Probe* probe;            // may be null
 };
 
-// Enqueue one full step on `stream`.  Returns hipSuccess or the first launch error.
-hipError_t enqueue_step(const StepArgs& a, hipStream_t stream);
-// Zero the state of the n slots listed in d_slots (device).
+// One step's inputs.  slots/tokens/out are device pointers; `check` validates slots
+// and tokens on the device into *err (bit 0: out of range, bit 1: duplicate slot).
+struct StepIO {
+    uint32_t n;
+    const uint32_t* slots;
+    const uint32_t* tokens;
+    float* out;
+    bool probs;
+    bool check;
+    uint32_t* err;
+};
+
+// A linear sequence of kernel launches that is either issued directly on a stream or
+// recorded once as a hipGraph and replayed.
+struct Launch;
+
+class StepRunner {
+public:
+    ~StepRunner();
+    // Issue one step.  Builds (or reuses) the graph of this shape unless a probe is
+    // active, in which case the step is launched directly with events around the probed
+    // class.  Returns hipSuccess or the first error.
+    hipError_t run(const ModelView& m, Pool& p, const StepIO& io, hipStream_t st, Probe* probe);
+    void clear();
+
+private:
+    struct Graph {
+        uint32_t n = 0;
+        bool probs = false, check = false;
+        const Pool* pool = nullptr;
+        hipGraph_t g = nullptr;
+        hipGraphExec_t exec = nullptr;
+        hipGraphNode_t io_node = nullptr, head_node = nullptr, softmax_node = nullptr;
+        uint64_t last_use = 0;
+        std::vector<Launch>* launches = nullptr;  // argument storage, alive as long as the graph
+    };
+    void destroy(Graph& g);
+    std::vector<Graph> graphs_;
+    uint64_t clock_ = 0;
+};
+
+// Zero the state of the n slots listed in d_slots (device).  Uses no memset, so it is
+// safe under stream capture.
 hipError_t enqueue_reset(const Dims& dims, Pool& pool, const uint32_t* d_slots, uint32_t n, hipStream_t stream);
+
+// Scratch sizes of a pool of `cap` streams.
+size_t xpart_floats(const Dims& d, uint32_t cap);
+size_t glimb_elems(const Dims& d, uint32_t cap);
 
 }  // namespace rdk

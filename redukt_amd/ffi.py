@@ -42,8 +42,7 @@ V3_SYMBOLS = ("redukt_backend_init_ex", "redukt_backend_forward_batch_probs", "r
               "redukt_backend_probe_kernel", "redukt_backend_probe_used")
 
 # Kernel classes of redukt_backend_probe_kernel.
-KERNEL_CLASSES = {"embed": 1, "norm": 2, "in_proj": 3, "conv": 4, "x_proj": 5, "scan": 6, "out_proj": 7,
-                  "head": 8, "softmax": 9}
+KERNEL_CLASSES = {"embed": 1, "mix_in": 2, "scan": 3, "mix_out": 4, "head": 5, "softmax": 6}
 
 
 class BackendResult(enum.IntEnum):
