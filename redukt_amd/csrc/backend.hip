@@ -169,10 +169,10 @@ int load_weights(const std::string& path, uint32_t profile) {
         hdr_ok = h[2] && h[3] && h[4] && h[5] && h[7] && h[8] && h[6] >= 2;
         if (h[1] == 2) hdr_ok = hdr_ok && h[10] <= 1 && !(h[10] == 0 && h[2] != 256);
         // Kernel limits: 16 SSM states per channel; d_model in whole 32-column k-steps and
-        // at most kMaxCols; d_inner in whole 64-channel conv-branch blocks; x_proj rows
-        // (dt_rank <= 64) held in registers.
+        // at most kMaxCols; d_inner in whole 64-channel conv-branch blocks, at most 2048
+        // (32 x_proj partials per row); x_proj rows (dt_rank <= 64) held in registers.
         hdr_ok = hdr_ok && h[5] == 16 && h[3] % 32 == 0 && h[4] % 64 == 0 && h[3] <= (uint32_t)kMaxCols &&
-                 h[7] <= 64;
+                 h[4] <= 2048 && h[7] <= 64;
     }
     if (!hdr_ok) {
         log("bad/unsupported .rbin header in %s", path.c_str());
@@ -260,7 +260,7 @@ void dev_free_all() {
 }
 
 void pool_free(Pool& p) {
-    void* bufs[] = {p.conv, p.ssm, p.x, p.u, p.z, p.xpart, p.glimb, p.out, p.slots, p.d_slots, p.d_tokens};
+    void* bufs[] = {p.conv, p.ssm, p.x, p.u, p.z, p.xpart, p.glimb, p.xw, p.ssp, p.out, p.slots, p.d_slots, p.d_tokens};
     for (void* b : bufs) (void)hipFree(b);
     if (p.h_slots) (void)hipHostFree(p.h_slots);
     if (p.h_tokens) (void)hipHostFree(p.h_tokens);
@@ -286,6 +286,7 @@ bool pool_alloc(Pool& p, uint32_t cap) {
     bool ok = dev_zero(p.conv, (size_t)D.nl * n * di * (D.dc - 1)) && dev_zero(p.ssm, (size_t)D.nl * n * di * 16) &&
               dev_zero(p.x, n * d) && dev_zero(p.u, n * di) && dev_zero(p.z, n * di) &&
               dev_zero(p.xpart, xpart_floats(D, cap)) && dev_zero(p.glimb, glimb_elems(D, cap)) &&
+              dev_zero(p.xw, xw_elems(D, cap)) && dev_zero(p.ssp, ssp_floats(D, cap)) &&
               dev_zero(p.out, n * D.vocab) && dev_zero(p.slots, n) && dev_zero(p.d_slots, n) &&
               dev_zero(p.d_tokens, n);
     ok = ok && hipHostMalloc((void**)&p.h_slots, sizeof(uint32_t) * n, hipHostMallocDefault) == hipSuccess;

@@ -52,6 +52,14 @@ size_t glimb_elems(const Dims& d, uint32_t cap) {
     return groups * (d.di / kKStep) * 3 * 64 * 8;
 }
 
+size_t xw_elems(const Dims& d, uint32_t cap) {
+    const size_t groups = (cap + 15) / 16;
+    const size_t ks = (d.d + kKAlign - 1) / kKAlign * (kKAlign / kKStep);
+    return groups * ks * 3 * 64 * 8;
+}
+
+size_t ssp_floats(const Dims& d, uint32_t cap) { return (size_t)cap * (d.d / kRowTile); }
+
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -64,11 +72,16 @@ constexpr int kChunk = 32;                 // streams per k_mix_in / k_head work
 constexpr int kGroups = kChunk / kRowTile; // MFMA column groups per chunk
 constexpr int kLimbBytes = 64 * 8 * 2;     // one B fragment of one limb: 1 KB
 constexpr int kHeadTiles = 4;              // row tiles per wave in k_head
-constexpr int kRing = 4;                   // weight k-pairs in flight per wave (loop unrolled by it)
+// Weight k-pairs each wave keeps in flight (the product loop is unrolled by it): k_mix_in
+// holds its whole quarter of four Q8 row tiles of a d <= 1024 projection, k_head four
+// tiles' next eight pairs.
+constexpr int kInRingQ8 = 4, kInRingF32 = 1;
+constexpr int kHeadRingQ8 = 8, kHeadRingF32 = 2;
 constexpr int kTps = 8;                    // threads per stream while staging activations
 constexpr int kQuadBatch = 4;              // column quads a staging thread loads per iteration
 constexpr int kMaxDr = 64;                 // dt_rank limit (d_model <= 1024)
 constexpr int kMaxXr = kMaxDr + 32;        // x_proj rows
+constexpr int kMaxNxb = 32;                // d_inner / 64 (d_inner <= 2048)
 constexpr int kOutWaves = 8;               // waves of k_mix_out
 constexpr int kOutPairs = 3;               // k-pairs per k_mix_out wave per pass
 
@@ -289,38 +302,144 @@ __device__ void stage_normed(__bf16* lds, const float* __restrict__ x, const flo
     __syncthreads();
 }
 
-// Row tiles a wave multiplies together, with a ring of their next kRing weight k-pairs
+// Pre-staged activations (RMSNorm models).  The producer of the residual stream x
+// (k_embed, k_mix_out) also writes x * norm_w as bf16 limbs in B-fragment tiles (xw) and
+// partial sums of x^2 over each 16-column tile (ssp); a consumer copies its column groups'
+// tiles straight into LDS and applies the per-stream RMS scale
+// inv = 1 / sqrt(mean(x^2) + 1e-5) (tensor.rs:900-908) after the product:
+// sum_k W[r][k] * (x[k] * w[k]) * inv.
+//
+// Copy of groups [g0, g0 + ng): contiguous in xw and in LDS, 1 KB per wave instruction
+// (global_load_lds of 16 bytes per lane: lane i lands at LDS base + 16 i).  The caller
+// waits for vmcnt(0) and syncs before reading.
+typedef __attribute__((address_space(3))) unsigned char lds_u8;
+
+__device__ __forceinline__ void stage_copy(unsigned char* lds, const __bf16* __restrict__ xw, uint32_t g0, int ng,
+                                           int ks) {
+    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    const int blocks = ng * ks * 3;
+    const __bf16* src = xw + (size_t)g0 * ks * 3 * 512 + lane * 8;
+    lds_u8* dst = (lds_u8*)lds;
+#pragma unroll 4
+    for (int q = wave; q < blocks; q += kWaves)
+        __builtin_amdgcn_global_load_lds((const void*)(src + (size_t)q * 512), (void __attribute__((address_space(3)))*)(dst + q * kLimbBytes),
+                                         16, 0, 0);
+}
+
+// Copy of k-steps [s_lo, s_hi) of groups [g0, g0 + ng) by the calling wave alone, for a
+// product split over k across the waves: every wave waits for its own copies
+// (vmcnt(0)) and reads only what it copied, so no barrier is needed before the product.
+__device__ __forceinline__ void stage_copy_wave(unsigned char* lds, const __bf16* __restrict__ xw, uint32_t g0,
+                                                int ng, int ks, int s_lo, int s_hi) {
+    const int lane = threadIdx.x % kWave;
+    const int run = (s_hi - s_lo) * 3;
+#pragma unroll
+    for (int g = 0; g < kGroups; g++) {
+        if (g >= ng) continue;
+        const __bf16* src = xw + (((size_t)(g0 + g) * ks + s_lo) * 3) * 512 + lane * 8;
+        lds_u8* dst = (lds_u8*)lds + (size_t)((g * ks + s_lo) * 3) * kLimbBytes;
+#pragma unroll 4
+        for (int q = 0; q < run; q++)
+            __builtin_amdgcn_global_load_lds((const void*)(src + (size_t)q * 512),
+                                             (void __attribute__((address_space(3)))*)(dst + q * kLimbBytes), 16, 0, 0);
+    }
+}
+
+// RMS scale of the chunk's streams: eight threads per stream each take every eighth
+// 16-column partial (up to kSspPerThread of them, all requested at once), then a fixed
+// xor butterfly.  Split in a load half and a reduce half so the loads fly with the rest.
+constexpr int kSspPerThread = 8;  // d <= 1024: at most 64 tiles
+
+struct SspLoad {
+    float v[kSspPerThread];
+};
+
+__device__ __forceinline__ SspLoad ssp_load(const float* __restrict__ ssp, int tiles, uint32_t b0, uint32_t n) {
+    const int bb = threadIdx.x / kTps, sub = threadIdx.x % kTps;
+    const uint32_t b = b0 + bb;
+    SspLoad r;
+    const float* p = ssp + (size_t)(b < n ? b : b0) * tiles;
+#pragma unroll
+    for (int i = 0; i < kSspPerThread; i++) {
+        const int t = sub + kTps * i;
+        r.v[i] = t < tiles ? p[t] : 0.0f;
+    }
+    return r;
+}
+
+__device__ __forceinline__ void ssp_reduce(const SspLoad& r, float* invs, int tiles, int d) {
+    const int bb = threadIdx.x / kTps, sub = threadIdx.x % kTps;
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kSspPerThread; i++)
+        if (sub + kTps * i < tiles) ss += r.v[i];
+#pragma unroll
+    for (int o = 1; o < kTps; o <<= 1) ss += __shfl_xor(ss, o, kWave);
+    if (sub == 0) invs[bb] = 1.0f / sqrtf(ss / (float)d + 1e-5f);
+}
+
+// Producer side for one 16-column tile: lane l of the wave holds x[b][r0 + i], i < 4,
+// r0 = 16 t + 4 (l / 16), b = b0 + (l % 16) (the MFMA D layout).  Writes the three limbs of
+// x * w into column group b / 16 of xw and the tile's sum of x^2 for stream b into ssp
+// (sequential over the lane's four values, then xor 16, xor 32).  All lanes must call it;
+// `ok` masks the stores.
+__device__ __forceinline__ void produce_tile(__bf16* __restrict__ xw, float* __restrict__ ssp, int ks, int tiles,
+                                             int t, uint32_t b, bool ok, const float (&xv)[4], const float4& w4) {
+    const int lane = threadIdx.x % kWave;
+    typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+    const float wv[4] = {w4.x, w4.y, w4.z, w4.w};
+    bf16x4 h, m, l;
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const Limb3 t3 = split3(xv[i] * wv[i]);
+        h[i] = t3.h;
+        m[i] = t3.m;
+        l[i] = t3.l;
+        ss += xv[i] * xv[i];
+    }
+    ss += __shfl_xor(ss, 16, kWave);
+    ss += __shfl_xor(ss, 32, kWave);
+    if (!ok) return;
+    const int rr = (t % 2) * kRowTile + (lane / 16) * 4;  // row within k-step t / 2
+    const int ln = (int)(b % kRowTile) + kRowTile * (rr / 8);
+    __bf16* dst = xw + ((((size_t)(b / kRowTile) * ks + t / 2) * 3) * 64 + ln) * 8 + rr % 8;
+    *(bf16x4*)dst = h;
+    *(bf16x4*)(dst + 512) = m;
+    *(bf16x4*)(dst + 1024) = l;
+    if (lane < 16) ssp[(size_t)b * tiles + t] = ss;
+}
+
+// Row tiles a wave multiplies together, with a ring of their next R weight k-pairs
 // (requested ahead of the product, for instance while the activations stage).
-template <bool Q8, int T>
+template <bool Q8, int T, int R>
 struct Tiles {
     int t[T];
     bool ok[T];
-    RawPair ring[kRing][T];
+    RawPair ring[R][T];
 };
 
-template <bool Q8, int T>
-__device__ __forceinline__ void tiles_prefetch(const TMat& w, Tiles<Q8, T>& tl) {
+template <bool Q8, int T, int R>
+__device__ __forceinline__ void tiles_prefetch(const TMat& w, Tiles<Q8, T, R>& tl, int p_lo, int p_hi) {
     const int lane = threadIdx.x % kWave;
-    const int np = w.ks / 2;
 #pragma unroll
-    for (int q = 0; q < kRing; q++)
+    for (int q = 0; q < R; q++)
 #pragma unroll
         for (int i = 0; i < T; i++)
-            if (tl.ok[i] && q < np) tl.ring[q][i] = load_pair<Q8>(w, tl.t[i], q, lane);
+            if (tl.ok[i] && p_lo + q < p_hi) tl.ring[q][i] = load_pair<Q8>(w, tl.t[i], p_lo + q, lane);
 }
 
-// T row tiles times the staged activations of `ng` column groups over all k-steps.
-// Accumulators are kept per limb order so consecutive MFMAs are independent: Q8 order o
-// holds the products with activation limb o; F32 order 0 holds hi*hi, order 1 hi*mid and
-// mid*hi, order 2 hi*lo, mid*mid and lo*hi.  The row sum is (o0 + o1) + o2.  With Q8
-// group-64 scales each k-pair's partial (all limbs, fixed order) is scaled into order 0.
-// The weight ring is refilled kRing pairs ahead; the loop body covers one turn of the
-// ring and stays rolled.  Per-row scales are left to the caller.
-template <bool Q8, int T>
-__device__ __forceinline__ void tiles_gemm(const TMat& w, Tiles<Q8, T>& tl, const __bf16* lds, int ng,
-                                           f32x4 (&out)[T][kGroups]) {
+// T row tiles times the staged activations of `ng` column groups over k-pairs
+// [p_lo, p_hi).  Accumulators are kept per limb order so consecutive MFMAs are
+// independent: Q8 order o holds the products with activation limb o; F32 order 0 holds
+// hi*hi, order 1 hi*mid and mid*hi, order 2 hi*lo, mid*mid and lo*hi.  The sum is
+// (o0 + o1) + o2.  With Q8 group-64 scales each k-pair's partial (all limbs, fixed order)
+// is scaled into order 0.  The weight ring is refilled R pairs ahead; the loop body
+// covers one turn of the ring and stays rolled.  Per-row scales are left to the caller.
+template <bool Q8, int T, int R>
+__device__ __forceinline__ void tiles_gemm(const TMat& w, Tiles<Q8, T, R>& tl, const __bf16* lds, int ng, int p_lo,
+                                           int p_hi, f32x4 (&out)[T][kGroups]) {
     const int lane = threadIdx.x % kWave;
-    const int np = w.ks / 2;
     const bool grp = Q8 && w.group != w.cols;
     const int gpr = w.ks / 2;
     f32x4 acc[T][kGroups][3];
@@ -331,11 +450,11 @@ __device__ __forceinline__ void tiles_gemm(const TMat& w, Tiles<Q8, T>& tl, cons
 #pragma unroll
             for (int o = 0; o < 3; o++) acc[i][g][o] = f32x4{0, 0, 0, 0};
 #pragma unroll 1
-    for (int p0 = 0; p0 < np; p0 += kRing) {
+    for (int p0 = p_lo; p0 < p_hi; p0 += R) {
 #pragma unroll
-        for (int q = 0; q < kRing; q++) {
+        for (int q = 0; q < R; q++) {
             const int p = p0 + q;
-            if (p >= np) continue;
+            if (p >= p_hi) continue;
             bf16x8 bf[kGroups][2][3];
 #pragma unroll
             for (int g = 0; g < kGroups; g++) {
@@ -351,7 +470,7 @@ __device__ __forceinline__ void tiles_gemm(const TMat& w, Tiles<Q8, T>& tl, cons
             for (int i = 0; i < T; i++) {
                 if (!tl.ok[i]) continue;
                 const RawPair cur = tl.ring[q][i];
-                if (p + kRing < np) tl.ring[q][i] = load_pair<Q8>(w, tl.t[i], p + kRing, lane);
+                if (p + R < p_hi) tl.ring[q][i] = load_pair<Q8>(w, tl.t[i], p + R, lane);
                 AFrag a[2];
                 decode_pair<Q8>(cur, a[0], a[1]);
                 float sc[4] = {1.0f, 1.0f, 1.0f, 1.0f};
@@ -396,6 +515,83 @@ __device__ __forceinline__ void tiles_gemm(const TMat& w, Tiles<Q8, T>& tl, cons
         for (int g = 0; g < kGroups; g++) out[i][g] = (acc[i][g][0] + acc[i][g][1]) + acc[i][g][2];
 }
 
+// k_mix_in's product: the block's kWaves row tiles times both column groups over this
+// wave's k-pairs [p_lo, p_lo + cnt), cnt <= kQuarterMax.  The weights of the quarter are
+// requested up front into a ring of R pairs (Q8: the whole quarter; F32 refills R pairs
+// ahead).  One accumulator per (tile, group): per k-step the limb products go in the
+// order hi, mid, lo (F32: hi*hi, hi*mid, mid*hi, hi*lo, mid*mid, lo*hi) — eight
+// independent chains keep the matrix core busy.  Tiles past the matrix are clamped to its
+// last tile and column groups past n read whatever the LDS holds: both only feed output
+// elements that are never stored (MFMA output columns depend only on their own B column).
+constexpr int kQuarterMax = 4;  // k-pairs per wave: d <= 1024 is 16 pairs over 4 waves
+
+template <bool Q8, int R>
+struct Quarter {
+    RawPair ring[R][kWaves];
+};
+
+template <bool Q8, int R>
+__device__ __forceinline__ void quarter_prefetch(const TMat& w, Quarter<Q8, R>& qw, int tb, int p_lo, int cnt) {
+    const int lane = threadIdx.x % kWave;
+#pragma unroll
+    for (int q = 0; q < R; q++) {
+        if (q >= cnt) continue;
+#pragma unroll
+        for (int i = 0; i < kWaves; i++) qw.ring[q][i] = load_pair<Q8>(w, min(tb + i, w.rt - 1), p_lo + q, lane);
+    }
+}
+
+template <bool Q8, bool GRP, int R>
+__device__ __forceinline__ void quarter_gemm(const TMat& w, Quarter<Q8, R>& qw, int tb, const __bf16* lds, int p_lo,
+                                             int cnt, f32x4 (&out)[kWaves][kGroups]) {
+    const int lane = threadIdx.x % kWave;
+    const int gpr = w.ks / 2;
+#pragma unroll
+    for (int i = 0; i < kWaves; i++)
+#pragma unroll
+        for (int g = 0; g < kGroups; g++) out[i][g] = f32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int q = 0; q < kQuarterMax; q++) {
+        if (q >= cnt) continue;
+        const int p = p_lo + q;
+        bf16x8 bf[kGroups][2][3];
+#pragma unroll
+        for (int g = 0; g < kGroups; g++)
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const __bf16* f = lds + ((size_t)(g * w.ks + 2 * p + h) * 3) * 512 + lane * 8;
+#pragma unroll
+                for (int m = 0; m < 3; m++) bf[g][h][m] = lds_frag(f + m * 512);
+            }
+#pragma unroll
+        for (int i = 0; i < kWaves; i++) {
+            const RawPair cur = qw.ring[q % R][i];
+            if (R < kQuarterMax && q + R < cnt) qw.ring[q % R][i] = load_pair<Q8>(w, min(tb + i, w.rt - 1), p + R, lane);
+            AFrag a[2];
+            decode_pair<Q8>(cur, a[0], a[1]);
+            float sc[4];
+            if (GRP) {
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    sc[e] = w.scales[(size_t)(min(tb + i, w.rt - 1) * kRowTile + (lane / 16) * 4 + e) * gpr + p];
+            }
+#pragma unroll
+            for (int g = 0; g < kGroups; g++) {
+                if (GRP) {
+                    f32x4 tmp{0, 0, 0, 0};
+#pragma unroll
+                    for (int h = 0; h < 2; h++) tmp = mma_step<Q8>(a[h], bf[g][h][0], bf[g][h][1], bf[g][h][2], tmp);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) out[i][g][e] = __builtin_fmaf(tmp[e], sc[e], out[i][g][e]);
+                } else {
+#pragma unroll
+                    for (int h = 0; h < 2; h++) out[i][g] = mma_step<Q8>(a[h], bf[g][h][0], bf[g][h][1], bf[g][h][2], out[i][g]);
+                }
+            }
+        }
+    }
+}
+
 __device__ __forceinline__ void apply_row_scales(const TMat& w, int t, f32x4 (&acc)[kGroups], int ng) {
     if (w.group == 0 || w.group != w.cols) return;
     const int lane = threadIdx.x % kWave;
@@ -419,12 +615,18 @@ struct EmbedArgs {
     uint32_t n, cap;
     int check;
     uint32_t* err;
+    const float* nw0;          // layer 0 norm weight; with xw != null the pre-staged
+    __bf16* xw;                // activations of layer 0 are produced here
+    float* ssp;
+    int ks_x, tiles;
 };
 
 // x[b] = emb[token[b]] (Q8: q * scale), model.rs:93-101 / gemv.rs:285-295.  Block (0, b)
 // copies slot b into the step's slot list; with `check` it also validates the slot and
 // the token and looks for duplicate slots, recording failures in *err and clamping so
-// no index can leave its buffer.
+// no index can leave its buffer.  Thread q of block (x, b) owns columns 4q' .. 4q'+3,
+// q' = 256 x + q; with xw it also writes their x * w limbs and, four threads per
+// 16-column tile, the tile's sum of x^2 (sequential over the four, then xor 1, xor 2).
 __global__ __launch_bounds__(kBlock) void k_embed(EmbedArgs a) {
     const uint32_t b = blockIdx.y;
     const int d = a.emb.cols;
@@ -441,26 +643,55 @@ __global__ __launch_bounds__(kBlock) void k_embed(EmbedArgs a) {
         if (threadIdx.x == 0) a.slots[b] = clamp_slot(s, a.cap);
     }
     if (tok >= (uint32_t)a.emb.rows) tok = a.emb.rows - 1;
-    const int k = blockIdx.x * kBlock + threadIdx.x;
-    if (k >= d) return;
-    const int t = tok / kRowTile, s = k / kKStep;
-    const int ln = (tok % kRowTile) + kRowTile * ((k % kKStep) / 8), j = k % 8;
-    float v;
-    if (a.emb.group == 0) {
-        v = ((const float*)a.emb.w)[(((size_t)t * a.emb.ks + s) * 64 + ln) * 8 + j];
-    } else {
-        const int8_t q = ((const int8_t*)a.emb.w)[((((size_t)t * (a.emb.ks / 2) + s / 2) * 64 + ln) * 2 + s % 2) * 8 + j];
-        const float sc = a.emb.group == a.emb.cols ? a.emb.scales[tok]
-                                                   : a.emb.scales[(size_t)tok * (a.emb.ks / 2) + k / a.emb.group];
-        v = (float)q * sc;
+    const int k = 4 * (blockIdx.x * kBlock + threadIdx.x);
+    const bool live = k < d;
+    const int s = k / kKStep, j = k % 8;
+    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (live) {
+        const int t = tok / kRowTile;
+        const int ln = (tok % kRowTile) + kRowTile * ((k % kKStep) / 8);
+        if (a.emb.group == 0) {
+            const float4 f = *(const float4*)((const float*)a.emb.w + (((size_t)t * a.emb.ks + s) * 64 + ln) * 8 + j);
+            v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
+        } else {
+            const int8_t* q8 = (const int8_t*)a.emb.w;
+            const int packed = *(const int*)(q8 + ((((size_t)t * (a.emb.ks / 2) + s / 2) * 64 + ln) * 2 + s % 2) * 8 + j);
+            const float sc = a.emb.group == a.emb.cols ? a.emb.scales[tok]
+                                                       : a.emb.scales[(size_t)tok * (a.emb.ks / 2) + k / a.emb.group];
+#pragma unroll
+            for (int e = 0; e < 4; e++) v[e] = (float)(int8_t)(packed >> (8 * e)) * sc;
+        }
+        *(float4*)(a.x + (size_t)b * d + k) = make_float4(v[0], v[1], v[2], v[3]);
     }
-    a.x[(size_t)b * d + k] = v;
+    if (a.xw == nullptr) return;
+    const float4 w4 = live ? *(const float4*)(a.nw0 + k) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const float wv[4] = {w4.x, w4.y, w4.z, w4.w};
+    typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+    bf16x4 h, m, l;
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const Limb3 t3 = split3(v[e] * wv[e]);
+        h[e] = t3.h;
+        m[e] = t3.m;
+        l[e] = t3.l;
+        ss += v[e] * v[e];
+    }
+    ss += __shfl_xor(ss, 1, kWave);
+    ss += __shfl_xor(ss, 2, kWave);
+    if (!live) return;
+    const int ln = (int)(b % kRowTile) + kRowTile * ((k % kKStep) / 8);
+    __bf16* dst = a.xw + ((((size_t)(b / kRowTile) * a.ks_x + s) * 3) * 64 + ln) * 8 + j;
+    *(bf16x4*)dst = h;
+    *(bf16x4*)(dst + 512) = m;
+    *(bf16x4*)(dst + 1024) = l;
+    if (threadIdx.x % 4 == 0) a.ssp[(size_t)b * a.tiles + k / kRowTile] = ss;
 }
 
 // ---------------------------------------------------------------- k_mix_in
 
 struct MixInArgs {
-    const float* x;            // [n][d] residual stream
+    const float* x;            // [n][d] residual stream (LayerNorm path)
     const float* norm_w;
     const float* norm_b;
     TMat wx, wz, wxp;          // in_proj conv branch, gate branch; x_proj
@@ -474,34 +705,134 @@ struct MixInArgs {
     float* z;                  // [n][di]
     float* xpart;              // [nxb][cap][xr_pad]
     int di, dc, d, xr_pad;
+    const __bf16* xw;          // pre-staged activations (RMSNorm path)
+    const float* ssp;
+    int tiles;
 };
 
-template <bool Q8, bool Q8XP>
+// in_proj for 4 row tiles x 32 streams.  The product is split over k: wave w multiplies
+// all four tiles over k-pairs [w np / 4, (w + 1) np / 4); the quarters meet in LDS and
+// wave w adds tile w's in wave order, q0 + q1 + q2 + q3, then finishes tile w.  Every
+// operand is requested before the first wait: the weights of the wave's quarter, the
+// conv weights, this block's x_proj fragments and the activations (the wave's quarter of
+// the pre-staged tiles copied into LDS, or the residual stream normed here for
+// LayerNorm models); the conv state follows while the product runs.
+template <bool Q8, bool Q8XP, bool PRE, bool GRP>
 __global__ __launch_bounds__(kBlock) void k_mix_in(MixInArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ float invs[kChunk];
     __bf16* lds = (__bf16*)smem;
     const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
     const uint32_t b0 = blockIdx.y * kChunk;
     const int ng = (int)min((uint32_t)kGroups, (a.n - b0 + kRowTile - 1) / kRowTile);
     const bool conv_branch = (int)blockIdx.x < a.nxb;
     const TMat& w = conv_branch ? a.wx : a.wz;
-    const int t = (conv_branch ? blockIdx.x : blockIdx.x - a.nxb) * kWaves + wave;
+    const int tb = (conv_branch ? blockIdx.x : blockIdx.x - a.nxb) * kWaves;  // the block's first row tile
+    const int t = tb + wave;                                                   // the tile this wave finishes
     const bool has_rows = t < w.rt;
-    Tiles<Q8, 1> tl;
-    tl.t[0] = t;
-    tl.ok[0] = has_rows;
-    tiles_prefetch<Q8, 1>(w, tl);  // weights in flight while the activations stage
-    stage_normed(lds, a.x, a.norm_w, a.norm_b, a.d, a.wx.ks, b0, a.n);
-
-    f32x4 acc[kGroups];
-    if (has_rows) {
-        f32x4 o[1][kGroups];
-        tiles_gemm<Q8, 1>(w, tl, lds, ng, o);
-#pragma unroll
-        for (int g = 0; g < kGroups; g++) acc[g] = o[0][g];
-        apply_row_scales(w, t, acc, ng);
-    }
     const int j0 = t * kRowTile + (lane / 16) * 4;  // this lane's 4 consecutive channels
+    const int dc = a.dc;
+    const bool conv4 = conv_branch && dc == 4 && has_rows && j0 < a.di;
+    const int np = w.ks / 2;
+    const int p_lo = wave * np / kWaves, p_hi = (wave + 1) * np / kWaves;
+    uint32_t slot_of[kGroups];
+#pragma unroll
+    for (int g = 0; g < kGroups; g++) {
+        const uint32_t b = b0 + g * kRowTile + lane % 16;
+        slot_of[g] = conv_branch ? clamp_slot(a.slots[b < a.n ? b : b0], a.cap) : 0u;
+    }
+    SspLoad sl;
+    if constexpr (PRE) sl = ssp_load(a.ssp, a.tiles, b0, a.n);
+    constexpr int R = Q8 ? kInRingQ8 : kInRingF32;
+    Quarter<Q8, R> qw;
+    quarter_prefetch<Q8, R>(w, qw, tb, p_lo, p_hi - p_lo);
+    float cwv[4][4], cbv[4];
+    if (conv4) {
+        const float4* cw4 = (const float4*)(a.conv_w + (size_t)j0 * 4);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float4 v = cw4[i];
+            cwv[i][0] = v.x; cwv[i][1] = v.y; cwv[i][2] = v.z; cwv[i][3] = v.w;
+        }
+        const float4 b4 = *(const float4*)(a.conv_b + j0);
+        cbv[0] = b4.x; cbv[1] = b4.y; cbv[2] = b4.z; cbv[3] = b4.w;
+    }
+    // x_proj fragments of this block's k-pair: row tiles wave, wave + 4 (x_proj has at
+    // most kMaxXr / 16 = 6 row tiles).
+    RawPair xpw[2];
+    float xps[2][4];
+    if (conv_branch) {
+        const int p = blockIdx.x;
+        const bool grp = a.wxp.group != a.wxp.cols;
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const int tp = wave + kWaves * k;
+            if (tp >= a.wxp.rt) continue;
+            xpw[k] = load_pair<Q8XP>(a.wxp, tp, p, lane);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int r = tp * kRowTile + (lane / 16) * 4 + i;
+                xps[k][i] = !Q8XP ? 1.0f : grp ? a.wxp.scales[(size_t)r * (a.wxp.ks / 2) + p] : a.wxp.scales[r];
+            }
+        }
+    }
+    if constexpr (PRE) {
+        stage_copy_wave(smem, a.xw, b0 / kRowTile, ng, a.wx.ks, 2 * p_lo, 2 * p_hi);
+        ssp_reduce(sl, invs, a.tiles, a.d);
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's copies have landed
+    } else {
+        stage_normed(lds, a.x, a.norm_w, a.norm_b, a.d, a.wx.ks, b0, a.n);
+    }
+    float4 stv[kGroups][3];
+    if (conv4) {
+#pragma unroll
+        for (int g = 0; g < kGroups; g++) {
+            const uint32_t b = b0 + g * kRowTile + lane % 16;
+            if (g < ng && b < a.n) {
+                const float4* sp = (const float4*)(a.conv_st + ((size_t)slot_of[g] * a.di + j0) * 3);
+#pragma unroll
+                for (int k = 0; k < 3; k++) stv[g][k] = sp[k];
+            }
+        }
+    }
+
+    f32x4 q4[kWaves][kGroups];
+    quarter_gemm<Q8, GRP, R>(w, qw, tb, lds, p_lo, p_hi - p_lo, q4);
+    // Quarters through LDS (reusing the activation area): red[src wave][tile][g][lane].
+    __syncthreads();
+    f32x4* red = (f32x4*)smem;
+#pragma unroll
+    for (int i = 0; i < kWaves; i++) {
+        if (i == wave) continue;
+#pragma unroll
+        for (int g = 0; g < kGroups; g++) red[((wave * kWaves + i) * kGroups + g) * kWave + lane] = q4[i][g];
+    }
+    __syncthreads();
+    f32x4 acc[kGroups];
+#pragma unroll
+    for (int g = 0; g < kGroups; g++) {
+        f32x4 s{0, 0, 0, 0};
+#pragma unroll
+        for (int src = 0; src < kWaves; src++) {
+            f32x4 v;
+            if (src == wave) {
+#pragma unroll
+                for (int i = 0; i < kWaves; i++)
+                    if (i == wave) v = q4[i][g];
+            } else {
+                v = red[((src * kWaves + wave) * kGroups + g) * kWave + lane];
+            }
+            s = src == 0 ? v : s + v;
+        }
+        acc[g] = s;
+    }
+    if (has_rows) {
+        apply_row_scales(w, t, acc, ng);
+        if constexpr (PRE) {
+#pragma unroll
+            for (int g = 0; g < kGroups; g++) acc[g] = acc[g] * invs[g * kRowTile + lane % 16];
+        }
+    }
     if (!conv_branch) {
         if (has_rows && j0 < a.di) {
 #pragma unroll
@@ -515,32 +846,7 @@ __global__ __launch_bounds__(kBlock) void k_mix_in(MixInArgs a) {
     }
     // Conv branch: conv1d step + SiLU per (channel, stream), conv_silu_block order
     // (model.rs:134-153) and silu_inplace's 256-channel body/tail rule (tensor.rs:1207-1211).
-    __syncthreads();  // every wave is done reading the staged activations
-    const int dc = a.dc;
-    // All conv operands of this lane's 4 channels x kGroups streams, requested at once.
-    float cwv[4][4], cbv[4];
-    if (dc == 4) {
-        const float4* cw4 = (const float4*)(a.conv_w + (size_t)j0 * 4);
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float4 v = cw4[i];
-            cwv[i][0] = v.x; cwv[i][1] = v.y; cwv[i][2] = v.z; cwv[i][3] = v.w;
-        }
-        const float4 b4 = *(const float4*)(a.conv_b + j0);
-        cbv[0] = b4.x; cbv[1] = b4.y; cbv[2] = b4.z; cbv[3] = b4.w;
-    }
-    float4 stv[kGroups][3];
-    uint32_t slot_of[kGroups];
-#pragma unroll
-    for (int g = 0; g < kGroups; g++) {
-        const uint32_t b = b0 + g * kRowTile + lane % 16;
-        slot_of[g] = clamp_slot(a.slots[b < a.n ? b : b0], a.cap);
-        if (dc == 4 && g < ng && b < a.n) {
-            const float4* sp = (const float4*)(a.conv_st + ((size_t)slot_of[g] * a.di + j0) * 3);
-#pragma unroll
-            for (int k = 0; k < 3; k++) stv[g][k] = sp[k];
-        }
-    }
+    __syncthreads();  // every wave has read its quarters
 #pragma unroll
     for (int g = 0; g < kGroups; g++) {
         const uint32_t b = b0 + g * kRowTile + lane % 16;
@@ -610,21 +916,14 @@ __global__ __launch_bounds__(kBlock) void k_mix_in(MixInArgs a) {
         }
     }
     __syncthreads();
-    // Split-K partial of x_proj: rows r of x_proj against this block's channels.
-    for (int tp = wave; tp < a.wxp.rt; tp += kWaves) {
-        const int p = blockIdx.x;  // k-pair index of x_proj = conv-branch block
-        RawPair raw = load_pair<Q8XP>(a.wxp, tp, p, lane);
-        AFrag a0, a1;
-        decode_pair<Q8XP>(raw, a0, a1);
-        float sc[4] = {1.0f, 1.0f, 1.0f, 1.0f};
-        if (Q8XP) {
-            const bool grp = a.wxp.group != a.wxp.cols;
+    // Split-K partial of x_proj: rows of x_proj against this block's channels.
+    const int p = blockIdx.x;  // k-pair index of x_proj = conv-branch block
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int r = tp * kRowTile + (lane / 16) * 4 + i;
-                sc[i] = grp ? a.wxp.scales[(size_t)r * (a.wxp.ks / 2) + p] : a.wxp.scales[r];
-            }
-        }
+    for (int k = 0; k < 2; k++) {
+        const int tp = wave + kWaves * k;
+        if (tp >= a.wxp.rt) continue;
+        AFrag a0, a1;
+        decode_pair<Q8XP>(xpw[k], a0, a1);
 #pragma unroll
         for (int g = 0; g < kGroups; g++) {
             if (g >= ng) continue;
@@ -636,7 +935,8 @@ __global__ __launch_bounds__(kBlock) void k_mix_in(MixInArgs a) {
             const uint32_t b = b0 + g * kRowTile + lane % 16;
             if (b < a.n) {
                 float* dst = a.xpart + ((size_t)p * a.cap + b) * a.xr_pad + tp * kRowTile + (lane / 16) * 4;
-                *(float4*)dst = make_float4(part[0] * sc[0], part[1] * sc[1], part[2] * sc[2], part[3] * sc[3]);
+                *(float4*)dst = make_float4(part[0] * xps[k][0], part[1] * xps[k][1], part[2] * xps[k][2],
+                                            part[3] * xps[k][3]);
             }
         }
     }
@@ -723,18 +1023,15 @@ __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
     // x_proj partials of this stream (threads < xr), summed in block order.
     const int r = threadIdx.x;
     if (r < a.xr) {
-        float acc = 0.0f;
         const float* pp = a.xpart + (size_t)b * a.xr_pad + r;
         const size_t pstride = (size_t)a.cap * a.xr_pad;
-#pragma unroll 1
-        for (int p0 = 0; p0 < a.nxb; p0 += 4) {
-            float pv[4];
+        float pv[kMaxNxb];
 #pragma unroll
-            for (int u = 0; u < 4; u++) pv[u] = p0 + u < a.nxb ? pp[(size_t)(p0 + u) * pstride] : 0.0f;
+        for (int u = 0; u < kMaxNxb; u++) pv[u] = u < a.nxb ? pp[(size_t)u * pstride] : 0.0f;
+        float acc = 0.0f;
 #pragma unroll
-            for (int u = 0; u < 4; u++)
-                if (p0 + u < a.nxb) acc += pv[u];
-        }
+        for (int u = 0; u < kMaxNxb; u++)
+            if (u < a.nxb) acc += pv[u];
         zp[r] = acc;
     }
     __syncthreads();
@@ -810,12 +1107,17 @@ struct MixOutArgs {
     float* x;                // [n][d] residual, updated in place
     uint32_t n;
     int d;
+    const float* nw_next;    // next norm weight (next layer's, or the final norm's); with
+    __bf16* xw;              // xw != null the next consumer's pre-staged activations are
+    float* ssp;              // produced here
+    int ks_x, tiles;
 };
 
 // out_proj + residual.  Eight waves share one 16-row tile, each summing an eighth of the
 // k-pairs (limb orders in separate accumulators, as in tiles_gemm) with kOutPairs pairs of
 // weight and activation fragments requested at once; the eighths are added in wave order,
-// then the per-row scale, then the residual: x += (((q0 + q1) + q2) + ... + q7).
+// then the per-row scale, then the residual: x += (((q0 + q1) + q2) + ... + q7).  The new
+// residual rows then leave as the next projection's pre-staged activations.
 template <bool Q8>
 __global__ __launch_bounds__(kOutWaves * kWave) void k_mix_out(MixOutArgs a) {
     __shared__ f32x4 part[kOutWaves - 1][kGroups][kWave];
@@ -829,6 +1131,24 @@ __global__ __launch_bounds__(kOutWaves * kWave) void k_mix_out(MixOutArgs a) {
     const bool grp = Q8 && w.group != w.cols;
     const int gpr = w.ks / 2;
     const uint32_t g0 = b0 / kRowTile;
+    const int r0 = t * kRowTile + (lane / 16) * 4;
+    // Epilogue operands of wave 0, requested with the rest.
+    float4 xv[kGroups];
+    float rs[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+    float4 w4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (wave == 0) {
+#pragma unroll
+        for (int g = 0; g < kGroups; g++) {
+            const uint32_t b = b0 + g * kRowTile + lane % 16;
+            xv[g] = g < ng && b < a.n && r0 < a.d ? *(const float4*)(a.x + (size_t)b * a.d + r0)
+                                                  : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+        if (Q8 && !grp) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) rs[i] = w.scales[t * kRowTile + (lane / 16) * 4 + i];
+        }
+        if (a.xw != nullptr && r0 < a.d) w4 = *(const float4*)(a.nw_next + r0);
+    }
     f32x4 acc3[kGroups][3];
 #pragma unroll
     for (int g = 0; g < kGroups; g++)
@@ -906,23 +1226,17 @@ __global__ __launch_bounds__(kOutWaves * kWave) void k_mix_out(MixOutArgs a) {
     }
     __syncthreads();
     if (wave != 0) return;
-    float rs[4] = {1.0f, 1.0f, 1.0f, 1.0f};
-    if (Q8 && !grp) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) rs[i] = w.scales[t * kRowTile + (lane / 16) * 4 + i];
-    }
-    const int r0 = t * kRowTile + (lane / 16) * 4;
 #pragma unroll
     for (int g = 0; g < kGroups; g++) {
         if (g >= ng) continue;
         f32x4 s = acc[g];
         for (int q = 0; q < kOutWaves - 1; q++) s = s + part[q][g][lane];
         const uint32_t b = b0 + g * kRowTile + lane % 16;
-        if (b < a.n && r0 < a.d) {
-            float4* xp = (float4*)(a.x + (size_t)b * a.d + r0);
-            const float4 xv = *xp;
-            *xp = make_float4(xv.x + s[0] * rs[0], xv.y + s[1] * rs[1], xv.z + s[2] * rs[2], xv.w + s[3] * rs[3]);
-        }
+        const bool ok = b < a.n && r0 < a.d;
+        const float nx[4] = {xv[g].x + s[0] * rs[0], xv[g].y + s[1] * rs[1], xv[g].z + s[2] * rs[2],
+                             xv[g].w + s[3] * rs[3]};
+        if (ok) *(float4*)(a.x + (size_t)b * a.d + r0) = make_float4(nx[0], nx[1], nx[2], nx[3]);
+        if (a.xw != nullptr) produce_tile(a.xw, a.ssp, a.ks_x, a.tiles, t, b, ok, nx, w4);
     }
 }
 
@@ -936,30 +1250,45 @@ struct HeadArgs {
     float* out;              // [n][vocab]
     uint32_t n;
     int d;
+    const __bf16* xw;        // pre-staged activations (RMSNorm path)
+    const float* ssp;
+    int tiles;
 };
 
 // Final norm (model.rs:745-752) and the LM head (model.rs:921-927, tied to the
 // embedding unless the file carries lm_head).  Each wave multiplies kHeadTiles row tiles
 // together, so every activation fragment read from LDS serves all of them.
-template <bool Q8>
+template <bool Q8, bool PRE>
 __global__ __launch_bounds__(kBlock) void k_head(HeadArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ float invs[kChunk];
     __bf16* lds = (__bf16*)smem;
     const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
     const uint32_t b0 = blockIdx.y * kChunk;
     const int ng = (int)min((uint32_t)kGroups, (a.n - b0 + kRowTile - 1) / kRowTile);
     const int V = a.w.rows;
     const int t_first = (blockIdx.x * kWaves + wave) * kHeadTiles;
-    Tiles<Q8, kHeadTiles> tl;
+    SspLoad sl;
+    if constexpr (PRE) sl = ssp_load(a.ssp, a.tiles, b0, a.n);
+    constexpr int R = Q8 ? kHeadRingQ8 : kHeadRingF32;
+    Tiles<Q8, kHeadTiles, R> tl;
 #pragma unroll
     for (int i = 0; i < kHeadTiles; i++) {
         tl.t[i] = t_first + i;
         tl.ok[i] = t_first + i < a.w.rt;
     }
-    tiles_prefetch<Q8, kHeadTiles>(a.w, tl);
-    stage_normed(lds, a.x, a.norm_w, a.norm_b, a.d, a.w.ks, b0, a.n);
+    const int np = a.w.ks / 2;
+    tiles_prefetch<Q8, kHeadTiles, R>(a.w, tl, 0, np);
+    if constexpr (PRE) {
+        stage_copy(smem, a.xw, b0 / kRowTile, ng, a.w.ks);
+        ssp_reduce(sl, invs, a.tiles, a.d);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+    } else {
+        stage_normed(lds, a.x, a.norm_w, a.norm_b, a.d, a.w.ks, b0, a.n);
+    }
     f32x4 res[kHeadTiles][kGroups];
-    tiles_gemm<Q8, kHeadTiles>(a.w, tl, lds, ng, res);
+    tiles_gemm<Q8, kHeadTiles, R>(a.w, tl, lds, ng, 0, np, res);
 #pragma unroll
     for (int tt = 0; tt < kHeadTiles; tt++) {
         const int t = t_first + tt;
@@ -968,6 +1297,10 @@ __global__ __launch_bounds__(kBlock) void k_head(HeadArgs a) {
 #pragma unroll
         for (int g = 0; g < kGroups; g++) acc[g] = res[tt][g];
         apply_row_scales(a.w, t, acc, ng);
+        if constexpr (PRE) {
+#pragma unroll
+            for (int g = 0; g < kGroups; g++) acc[g] = acc[g] * invs[g * kRowTile + lane % 16];
+        }
         const int r0 = t * kRowTile + (lane / 16) * 4;
 #pragma unroll
         for (int g = 0; g < kGroups; g++) {
@@ -1079,6 +1412,13 @@ namespace {
 
 uint32_t stage_lds_bytes(int ks) { return (uint32_t)(kGroups * ks * 3 * kLimbBytes); }
 
+// k_mix_in reuses its activation area for the k-quarter partials and the x_proj operand.
+uint32_t mix_in_lds_bytes(int ks) {
+    const uint32_t quarters = kWaves * kWaves * kGroups * kWave * sizeof(f32x4);
+    const uint32_t xp_operand = kGroups * 2 * 3 * kLimbBytes;
+    return std::max(stage_lds_bytes(ks), std::max(quarters, xp_operand));
+}
+
 template <typename K>
 void allow_lds(K* fn, uint32_t bytes) {
     static uint32_t set = 0;
@@ -1088,19 +1428,37 @@ void allow_lds(K* fn, uint32_t bytes) {
     }
 }
 
-const void* mix_in_fn(bool q8, bool q8xp, uint32_t lds) {
-    if (q8 && q8xp) { allow_lds(k_mix_in<true, true>, lds); return (const void*)k_mix_in<true, true>; }
-    if (q8) { allow_lds(k_mix_in<true, false>, lds); return (const void*)k_mix_in<true, false>; }
-    if (q8xp) { allow_lds(k_mix_in<false, true>, lds); return (const void*)k_mix_in<false, true>; }
-    allow_lds(k_mix_in<false, false>, lds);
-    return (const void*)k_mix_in<false, false>;
+template <bool Q8, bool Q8XP, bool PRE, bool GRP>
+const void* mix_in_fn4(uint32_t lds) {
+    allow_lds(k_mix_in<Q8, Q8XP, PRE, GRP>, lds);
+    return (const void*)k_mix_in<Q8, Q8XP, PRE, GRP>;
 }
 
-const void* head_fn(bool q8, uint32_t lds) {
-    if (q8) { allow_lds(k_head<true>, lds); return (const void*)k_head<true>; }
-    allow_lds(k_head<false>, lds);
-    return (const void*)k_head<false>;
+template <bool Q8, bool Q8XP>
+const void* mix_in_fn2(bool pre, bool grp, uint32_t lds) {
+    if (pre) return grp ? mix_in_fn4<Q8, Q8XP, true, Q8>(lds) : mix_in_fn4<Q8, Q8XP, true, false>(lds);
+    return grp ? mix_in_fn4<Q8, Q8XP, false, Q8>(lds) : mix_in_fn4<Q8, Q8XP, false, false>(lds);
 }
+
+// grp: Q8 in_proj with 64-column scale groups.
+const void* mix_in_fn(bool q8, bool q8xp, bool pre, bool grp, uint32_t lds) {
+    if (q8 && q8xp) return mix_in_fn2<true, true>(pre, grp, lds);
+    if (q8) return mix_in_fn2<true, false>(pre, grp, lds);
+    if (q8xp) return mix_in_fn2<false, true>(pre, false, lds);
+    return mix_in_fn2<false, false>(pre, false, lds);
+}
+
+template <bool Q8>
+const void* head_fn2(bool pre, uint32_t lds) {
+    if (pre) {
+        allow_lds(k_head<Q8, true>, lds);
+        return (const void*)k_head<Q8, true>;
+    }
+    allow_lds(k_head<Q8, false>, lds);
+    return (const void*)k_head<Q8, false>;
+}
+
+const void* head_fn(bool q8, bool pre, uint32_t lds) { return q8 ? head_fn2<true>(pre, lds) : head_fn2<false>(pre, lds); }
 
 // The launches of one step, in stream order; io_index / head_index / softmax_index name
 // the launches whose arguments carry caller pointers.
@@ -1113,36 +1471,46 @@ void build_step(const ModelView& m, Pool& p, const StepIO& io, std::vector<Launc
     const int xr_pad = m.layers[0].x_proj.rt * kRowTile;
     const int nxb = di / 64;
     out.clear();
-    EmbedArgs ea{*m.emb, p.x, io.tokens, io.slots, p.slots, n, p.cap, io.check ? 1 : 0, io.err};
+    // RMSNorm models take the pre-staged activation path; LayerNorm models norm in the
+    // consumer.
+    const bool pre = m.layers[0].norm_b == nullptr && m.norm_f_b == nullptr;
+    const int ks_x = m.layers[0].in_x.ks, tiles = d / kRowTile;
+    EmbedArgs ea{*m.emb, p.x, io.tokens, io.slots, p.slots, n, p.cap, io.check ? 1 : 0, io.err,
+                 m.layers[0].norm_w, pre ? p.xw : nullptr, p.ssp, ks_x, tiles};
     io_index = (int)out.size();
-    out.push_back(Launch::make((const void*)k_embed, dim3((d + kBlock - 1) / kBlock, n), dim3(kBlock), 0, KC_EMBED, ea));
+    out.push_back(Launch::make((const void*)k_embed, dim3((d + 4 * kBlock - 1) / (4 * kBlock), n), dim3(kBlock), 0,
+                               KC_EMBED, ea));
     const size_t conv_layer = (size_t)p.cap * di * (D.dc - 1);
     const size_t ssm_layer = (size_t)p.cap * di * 16;
     const bool q8 = m.layers[0].in_x.group != 0;
     const bool q8xp = m.layers[0].x_proj.group != 0;
-    const uint32_t lds_in = stage_lds_bytes(m.layers[0].in_x.ks);
-    const void* fin = mix_in_fn(q8, q8xp, lds_in);
+    const uint32_t lds_in = mix_in_lds_bytes(ks_x);
+    const bool grp = q8 && m.layers[0].in_x.group != m.layers[0].in_x.cols;
+    const void* fin = mix_in_fn(q8, q8xp, pre, grp, lds_in);
     for (uint32_t li = 0; li < D.nl; li++) {
         const DLayer& L = m.layers[li];
         MixInArgs ma{p.x, L.norm_w, L.norm_b, L.in_x, L.in_z, L.x_proj, nxb, p.conv + li * conv_layer,
-                     L.conv_w, L.conv_b, p.slots, p.cap, n, p.u, p.z, p.xpart, di, (int)D.dc, d, xr_pad};
+                     L.conv_w, L.conv_b, p.slots, p.cap, n, p.u, p.z, p.xpart, di, (int)D.dc, d, xr_pad,
+                     p.xw, p.ssp, tiles};
         const int zb = L.in_z.rt / kWaves;
         out.push_back(Launch::make(fin, dim3(nxb + zb, chunks), dim3(kBlock), lds_in, KC_MIX_IN, ma));
         ScanArgs sa{p.xpart, nxb, xr_pad, (int)D.xr(), p.u, p.z, p.ssm + li * ssm_layer, L.dt_w, L.dt_q,
                     L.dt_scales, L.dt_pad, L.dt_b, L.a_exp, L.d_vec, p.slots, p.cap, n, p.glimb, di, (int)D.dr};
         out.push_back(Launch::make((const void*)k_scan, dim3((di + kBlock - 1) / kBlock, n), dim3(kBlock), 0,
                                    KC_SCAN, sa));
-        MixOutArgs oa{L.out_proj, p.glimb, p.x, n, d};
+        const float* nw_next = li + 1 < D.nl ? m.layers[li + 1].norm_w : m.norm_f_w;
+        MixOutArgs oa{L.out_proj, p.glimb, p.x, n, d, nw_next, pre ? p.xw : nullptr, p.ssp, ks_x, tiles};
         const void* fo = q8 ? (const void*)k_mix_out<true> : (const void*)k_mix_out<false>;
         out.push_back(Launch::make(fo, dim3(L.out_proj.rt, chunks), dim3(kOutWaves * kWave), 0, KC_MIX_OUT, oa));
     }
     const TMat& H = *m.head;
-    HeadArgs ha{p.x, m.norm_f_w, m.norm_f_b, H, io.out, n, d};
+    HeadArgs ha{p.x, m.norm_f_w, m.norm_f_b, H, io.out, n, d, p.xw, p.ssp, tiles};
     const uint32_t lds_h = stage_lds_bytes(H.ks);
     const int tiles_per_block = kWaves * kHeadTiles;
     head_index = (int)out.size();
-    out.push_back(Launch::make(head_fn(H.group != 0, lds_h), dim3((H.rt + tiles_per_block - 1) / tiles_per_block, chunks),
-                               dim3(kBlock), lds_h, KC_HEAD, ha));
+    out.push_back(Launch::make(head_fn(H.group != 0, pre, lds_h),
+                               dim3((H.rt + tiles_per_block - 1) / tiles_per_block, chunks), dim3(kBlock), lds_h,
+                               KC_HEAD, ha));
     softmax_index = -1;
     if (io.probs) {
         softmax_index = (int)out.size();

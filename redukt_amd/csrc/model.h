@@ -69,6 +69,12 @@ struct Pool {
     float* z = nullptr;          // [cap][di] gate branch
     float* xpart = nullptr;      // [di/64][cap][xr_pad] split-K partials of x_proj
     __bf16* glimb = nullptr;     // [gcap][di/32][3][64][8] gated, 3 bf16 limbs, B-fragment tiles
+    // Next projection's input, written by the producer of the residual stream (embedding,
+    // out_proj): x * norm_w as 3 bf16 limbs in B-fragment tiles, [gcap][ks_d][3][64][8]
+    // with ks_d = the k-steps of a d-column projection, plus per-16-column partial sums of
+    // x^2, [cap][d/16], from which the consumer forms the RMS scale of each stream.
+    __bf16* xw = nullptr;
+    float* ssp = nullptr;
     float* out = nullptr;        // [cap][vocab] logits or probabilities
     uint32_t* slots = nullptr;   // [cap] slots of the current step (validated copy)
     uint32_t* d_slots = nullptr; // [cap] H2D staging targets of the synchronous entry points
@@ -150,5 +156,7 @@ hipError_t enqueue_reset(const Dims& dims, Pool& pool, const uint32_t* d_slots, 
 // Scratch sizes of a pool of `cap` streams.
 size_t xpart_floats(const Dims& d, uint32_t cap);
 size_t glimb_elems(const Dims& d, uint32_t cap);
+size_t xw_elems(const Dims& d, uint32_t cap);
+size_t ssp_floats(const Dims& d, uint32_t cap);
 
 }  // namespace rdk
