@@ -68,8 +68,10 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kWave = 64;
 constexpr int kBlock = 256;
 constexpr int kWaves = kBlock / kWave;
-constexpr int kChunk = 32;                 // streams per k_mix_in / k_head workgroup
+constexpr int kChunk = 32;                 // streams per k_head / k_mix_out workgroup
 constexpr int kGroups = kChunk / kRowTile; // MFMA column groups per chunk
+constexpr int kInGroups = 1;               // column groups per k_mix_in workgroup
+constexpr int kInChunk = kInGroups * kRowTile;
 constexpr int kLimbBytes = 64 * 8 * 2;     // one B fragment of one limb: 1 KB
 constexpr int kHeadTiles = 4;              // row tiles per wave in k_head
 // Weight k-pairs each wave keeps in flight (the product loop is unrolled by it): k_mix_in
@@ -204,10 +206,10 @@ __device__ __forceinline__ float4 quad_or_zero(const float4* p, int q, bool ok) 
 }
 
 __device__ void stage_normed(__bf16* lds, const float* __restrict__ x, const float* __restrict__ nw,
-                             const float* __restrict__ nb, int d, int ks, uint32_t b0, uint32_t n) {
+                             const float* __restrict__ nb, int d, int ks, uint32_t b0, uint32_t n, int streams) {
     const int bb = threadIdx.x / kTps, sub = threadIdx.x % kTps;
     const uint32_t b = b0 + bb;
-    const bool live = b < n;
+    const bool live = b < n && bb < streams;
     const int dq = d / 4;
     const int qpt = ks * kKStep / 4 / kTps;  // quads per thread over the padded columns
     const float4* xb = (const float4*)(x + (size_t)(live ? b : b0) * d);
@@ -277,7 +279,7 @@ __device__ void stage_normed(__bf16* lds, const float* __restrict__ x, const flo
 #pragma unroll
         for (int u = 0; u < kQuadBatch; u++) {
             const int q = sub + kTps * (i0 + u);
-            if (i0 + u >= qpt) continue;
+            if (i0 + u >= qpt || bb >= streams) continue;
             const float xs[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
             const float ws[4] = {w4[u].x, w4[u].y, w4[u].z, w4[u].w};
             const float cs[4] = {c4[u].x, c4[u].y, c4[u].z, c4[u].w};
@@ -329,12 +331,13 @@ __device__ __forceinline__ void stage_copy(unsigned char* lds, const __bf16* __r
 // Copy of k-steps [s_lo, s_hi) of groups [g0, g0 + ng) by the calling wave alone, for a
 // product split over k across the waves: every wave waits for its own copies
 // (vmcnt(0)) and reads only what it copied, so no barrier is needed before the product.
+template <int G>
 __device__ __forceinline__ void stage_copy_wave(unsigned char* lds, const __bf16* __restrict__ xw, uint32_t g0,
                                                 int ng, int ks, int s_lo, int s_hi) {
     const int lane = threadIdx.x % kWave;
     const int run = (s_hi - s_lo) * 3;
 #pragma unroll
-    for (int g = 0; g < kGroups; g++) {
+    for (int g = 0; g < G; g++) {
         if (g >= ng) continue;
         const __bf16* src = xw + (((size_t)(g0 + g) * ks + s_lo) * 3) * 512 + lane * 8;
         lds_u8* dst = (lds_u8*)lds + (size_t)((g * ks + s_lo) * 3) * kLimbBytes;
@@ -354,20 +357,23 @@ struct SspLoad {
     float v[kSspPerThread];
 };
 
-__device__ __forceinline__ SspLoad ssp_load(const float* __restrict__ ssp, int tiles, uint32_t b0, uint32_t n) {
+// Streams [b0, b0 + streams) of the workgroup; threads past them idle.
+__device__ __forceinline__ SspLoad ssp_load(const float* __restrict__ ssp, int tiles, uint32_t b0, uint32_t n,
+                                            int streams) {
     const int bb = threadIdx.x / kTps, sub = threadIdx.x % kTps;
     const uint32_t b = b0 + bb;
+    const bool on = bb < streams && b < n;
     SspLoad r;
-    const float* p = ssp + (size_t)(b < n ? b : b0) * tiles;
+    const float* p = ssp + (size_t)(on ? b : 0) * tiles;
 #pragma unroll
     for (int i = 0; i < kSspPerThread; i++) {
         const int t = sub + kTps * i;
-        r.v[i] = t < tiles ? p[t] : 0.0f;
+        r.v[i] = on && t < tiles ? p[t] : 0.0f;
     }
     return r;
 }
 
-__device__ __forceinline__ void ssp_reduce(const SspLoad& r, float* invs, int tiles, int d) {
+__device__ __forceinline__ void ssp_reduce(const SspLoad& r, float* invs, int tiles, int d, int streams) {
     const int bb = threadIdx.x / kTps, sub = threadIdx.x % kTps;
     float ss = 0.0f;
 #pragma unroll
@@ -375,7 +381,7 @@ __device__ __forceinline__ void ssp_reduce(const SspLoad& r, float* invs, int ti
         if (sub + kTps * i < tiles) ss += r.v[i];
 #pragma unroll
     for (int o = 1; o < kTps; o <<= 1) ss += __shfl_xor(ss, o, kWave);
-    if (sub == 0) invs[bb] = 1.0f / sqrtf(ss / (float)d + 1e-5f);
+    if (sub == 0 && bb < streams) invs[bb] = 1.0f / sqrtf(ss / (float)d + 1e-5f);
 }
 
 // Producer side for one 16-column tile: lane l of the wave holds x[b][r0 + i], i < 4,
@@ -541,22 +547,22 @@ __device__ __forceinline__ void quarter_prefetch(const TMat& w, Quarter<Q8, R>& 
     }
 }
 
-template <bool Q8, bool GRP, int R>
+template <bool Q8, bool GRP, int R, int G>
 __device__ __forceinline__ void quarter_gemm(const TMat& w, Quarter<Q8, R>& qw, int tb, const __bf16* lds, int p_lo,
-                                             int cnt, f32x4 (&out)[kWaves][kGroups]) {
+                                             int cnt, f32x4 (&out)[kWaves][G]) {
     const int lane = threadIdx.x % kWave;
     const int gpr = w.ks / 2;
 #pragma unroll
     for (int i = 0; i < kWaves; i++)
 #pragma unroll
-        for (int g = 0; g < kGroups; g++) out[i][g] = f32x4{0, 0, 0, 0};
+        for (int g = 0; g < G; g++) out[i][g] = f32x4{0, 0, 0, 0};
 #pragma unroll
     for (int q = 0; q < kQuarterMax; q++) {
         if (q >= cnt) continue;
         const int p = p_lo + q;
-        bf16x8 bf[kGroups][2][3];
+        bf16x8 bf[G][2][3];
 #pragma unroll
-        for (int g = 0; g < kGroups; g++)
+        for (int g = 0; g < G; g++)
 #pragma unroll
             for (int h = 0; h < 2; h++) {
                 const __bf16* f = lds + ((size_t)(g * w.ks + 2 * p + h) * 3) * 512 + lane * 8;
@@ -576,7 +582,7 @@ __device__ __forceinline__ void quarter_gemm(const TMat& w, Quarter<Q8, R>& qw, 
                     sc[e] = w.scales[(size_t)(min(tb + i, w.rt - 1) * kRowTile + (lane / 16) * 4 + e) * gpr + p];
             }
 #pragma unroll
-            for (int g = 0; g < kGroups; g++) {
+            for (int g = 0; g < G; g++) {
                 if (GRP) {
                     f32x4 tmp{0, 0, 0, 0};
 #pragma unroll
@@ -710,42 +716,47 @@ struct MixInArgs {
     int tiles;
 };
 
-// in_proj for 4 row tiles x 32 streams.  The product is split over k: wave w multiplies
-// all four tiles over k-pairs [w np / 4, (w + 1) np / 4); the quarters meet in LDS and
-// wave w adds tile w's in wave order, q0 + q1 + q2 + q3, then finishes tile w.  Every
-// operand is requested before the first wait: the weights of the wave's quarter, the
-// conv weights, this block's x_proj fragments and the activations (the wave's quarter of
-// the pre-staged tiles copied into LDS, or the residual stream normed here for
-// LayerNorm models); the conv state follows while the product runs.
+// in_proj for 4 row tiles x kInChunk streams.  The product is split over k: wave w
+// multiplies all four tiles over k-pairs [w np / 4, (w + 1) np / 4); the quarters meet in
+// LDS and wave w adds tile w's in wave order, q0 + q1 + q2 + q3, then finishes tile w.
+// Every operand is requested before the first wait: the weights of the wave's quarter,
+// the row scales, conv weights and this block's x_proj fragments, and the activations
+// (the wave's quarter of the pre-staged tiles copied into LDS, or the residual stream
+// normed here for LayerNorm models); the conv state follows while the product runs.
 template <bool Q8, bool Q8XP, bool PRE, bool GRP>
 __global__ __launch_bounds__(kBlock) void k_mix_in(MixInArgs a) {
+    constexpr int G = kInGroups;
     extern __shared__ __align__(16) unsigned char smem[];
-    __shared__ float invs[kChunk];
+    __shared__ float invs[kInChunk];
     __bf16* lds = (__bf16*)smem;
     const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-    const uint32_t b0 = blockIdx.y * kChunk;
-    const int ng = (int)min((uint32_t)kGroups, (a.n - b0 + kRowTile - 1) / kRowTile);
+    const uint32_t b0 = blockIdx.y * kInChunk;
+    const int ng = (int)min((uint32_t)G, (a.n - b0 + kRowTile - 1) / kRowTile);
     const bool conv_branch = (int)blockIdx.x < a.nxb;
     const TMat& w = conv_branch ? a.wx : a.wz;
     const int tb = (conv_branch ? blockIdx.x : blockIdx.x - a.nxb) * kWaves;  // the block's first row tile
     const int t = tb + wave;                                                   // the tile this wave finishes
     const bool has_rows = t < w.rt;
+    const int tc = min(t, w.rt - 1);
     const int j0 = t * kRowTile + (lane / 16) * 4;  // this lane's 4 consecutive channels
     const int dc = a.dc;
     const bool conv4 = conv_branch && dc == 4 && has_rows && j0 < a.di;
     const int np = w.ks / 2;
     const int p_lo = wave * np / kWaves, p_hi = (wave + 1) * np / kWaves;
-    uint32_t slot_of[kGroups];
+    uint32_t slot_of[G];
 #pragma unroll
-    for (int g = 0; g < kGroups; g++) {
+    for (int g = 0; g < G; g++) {
         const uint32_t b = b0 + g * kRowTile + lane % 16;
         slot_of[g] = conv_branch ? clamp_slot(a.slots[b < a.n ? b : b0], a.cap) : 0u;
     }
     SspLoad sl;
-    if constexpr (PRE) sl = ssp_load(a.ssp, a.tiles, b0, a.n);
+    if constexpr (PRE) sl = ssp_load(a.ssp, a.tiles, b0, a.n, kInChunk);
     constexpr int R = Q8 ? kInRingQ8 : kInRingF32;
     Quarter<Q8, R> qw;
     quarter_prefetch<Q8, R>(w, qw, tb, p_lo, p_hi - p_lo);
+    // Per-row scale of the finished tile (Q8 without column groups).
+    float4 rsc = make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+    if (Q8 && !GRP) rsc = *(const float4*)(w.scales + tc * kRowTile + (lane / 16) * 4);
     float cwv[4][4], cbv[4];
     if (conv4) {
         const float4* cw4 = (const float4*)(a.conv_w + (size_t)j0 * 4);
@@ -758,35 +769,39 @@ __global__ __launch_bounds__(kBlock) void k_mix_in(MixInArgs a) {
         cbv[0] = b4.x; cbv[1] = b4.y; cbv[2] = b4.z; cbv[3] = b4.w;
     }
     // x_proj fragments of this block's k-pair: row tiles wave, wave + 4 (x_proj has at
-    // most kMaxXr / 16 = 6 row tiles).
+    // most kMaxXr / 16 = 6 row tiles), with their scales.
     RawPair xpw[2];
-    float xps[2][4];
+    float4 xps[2];
     if (conv_branch) {
         const int p = blockIdx.x;
         const bool grp = a.wxp.group != a.wxp.cols;
 #pragma unroll
         for (int k = 0; k < 2; k++) {
             const int tp = wave + kWaves * k;
+            xps[k] = make_float4(1.0f, 1.0f, 1.0f, 1.0f);
             if (tp >= a.wxp.rt) continue;
             xpw[k] = load_pair<Q8XP>(a.wxp, tp, p, lane);
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int r = tp * kRowTile + (lane / 16) * 4 + i;
-                xps[k][i] = !Q8XP ? 1.0f : grp ? a.wxp.scales[(size_t)r * (a.wxp.ks / 2) + p] : a.wxp.scales[r];
+            const int r = tp * kRowTile + (lane / 16) * 4;
+            if (Q8XP && !grp) {
+                xps[k] = *(const float4*)(a.wxp.scales + r);
+            } else if (Q8XP) {
+                const size_t gs = a.wxp.ks / 2;
+                xps[k] = make_float4(a.wxp.scales[r * gs + p], a.wxp.scales[(r + 1) * gs + p],
+                                     a.wxp.scales[(r + 2) * gs + p], a.wxp.scales[(r + 3) * gs + p]);
             }
         }
     }
     if constexpr (PRE) {
-        stage_copy_wave(smem, a.xw, b0 / kRowTile, ng, a.wx.ks, 2 * p_lo, 2 * p_hi);
-        ssp_reduce(sl, invs, a.tiles, a.d);
+        stage_copy_wave<G>(smem, a.xw, b0 / kRowTile, ng, a.wx.ks, 2 * p_lo, 2 * p_hi);
+        ssp_reduce(sl, invs, a.tiles, a.d, kInChunk);
         __builtin_amdgcn_s_waitcnt(0);  // this wave's copies have landed
     } else {
-        stage_normed(lds, a.x, a.norm_w, a.norm_b, a.d, a.wx.ks, b0, a.n);
+        stage_normed(lds, a.x, a.norm_w, a.norm_b, a.d, a.wx.ks, b0, a.n, kInChunk);
     }
-    float4 stv[kGroups][3];
+    float4 stv[G][3];
     if (conv4) {
 #pragma unroll
-        for (int g = 0; g < kGroups; g++) {
+        for (int g = 0; g < G; g++) {
             const uint32_t b = b0 + g * kRowTile + lane % 16;
             if (g < ng && b < a.n) {
                 const float4* sp = (const float4*)(a.conv_st + ((size_t)slot_of[g] * a.di + j0) * 3);
@@ -796,8 +811,8 @@ __global__ __launch_bounds__(kBlock) void k_mix_in(MixInArgs a) {
         }
     }
 
-    f32x4 q4[kWaves][kGroups];
-    quarter_gemm<Q8, GRP, R>(w, qw, tb, lds, p_lo, p_hi - p_lo, q4);
+    f32x4 q4[kWaves][G];
+    quarter_gemm<Q8, GRP, R, G>(w, qw, tb, lds, p_lo, p_hi - p_lo, q4);
     // Quarters through LDS (reusing the activation area): red[src wave][tile][g][lane].
     __syncthreads();
     f32x4* red = (f32x4*)smem;
@@ -805,12 +820,12 @@ __global__ __launch_bounds__(kBlock) void k_mix_in(MixInArgs a) {
     for (int i = 0; i < kWaves; i++) {
         if (i == wave) continue;
 #pragma unroll
-        for (int g = 0; g < kGroups; g++) red[((wave * kWaves + i) * kGroups + g) * kWave + lane] = q4[i][g];
+        for (int g = 0; g < G; g++) red[((wave * kWaves + i) * G + g) * kWave + lane] = q4[i][g];
     }
     __syncthreads();
-    f32x4 acc[kGroups];
+    f32x4 acc[G];
 #pragma unroll
-    for (int g = 0; g < kGroups; g++) {
+    for (int g = 0; g < G; g++) {
         f32x4 s{0, 0, 0, 0};
 #pragma unroll
         for (int src = 0; src < kWaves; src++) {
@@ -820,23 +835,23 @@ __global__ __launch_bounds__(kBlock) void k_mix_in(MixInArgs a) {
                 for (int i = 0; i < kWaves; i++)
                     if (i == wave) v = q4[i][g];
             } else {
-                v = red[((src * kWaves + wave) * kGroups + g) * kWave + lane];
+                v = red[((src * kWaves + wave) * G + g) * kWave + lane];
             }
             s = src == 0 ? v : s + v;
         }
-        acc[g] = s;
-    }
-    if (has_rows) {
-        apply_row_scales(w, t, acc, ng);
-        if constexpr (PRE) {
+        const float rs[4] = {rsc.x, rsc.y, rsc.z, rsc.w};
 #pragma unroll
-            for (int g = 0; g < kGroups; g++) acc[g] = acc[g] * invs[g * kRowTile + lane % 16];
+        for (int e = 0; e < 4; e++) {
+            float v = s[e];
+            if (Q8 && !GRP) v = v * rs[e];
+            if constexpr (PRE) v = v * invs[g * kRowTile + lane % 16];
+            acc[g][e] = v;
         }
     }
     if (!conv_branch) {
         if (has_rows && j0 < a.di) {
 #pragma unroll
-            for (int g = 0; g < kGroups; g++) {
+            for (int g = 0; g < G; g++) {
                 const uint32_t b = b0 + g * kRowTile + lane % 16;
                 if (g >= ng) continue;
                 if (b < a.n) *(float4*)(a.z + (size_t)b * a.di + j0) = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
@@ -848,7 +863,7 @@ __global__ __launch_bounds__(kBlock) void k_mix_in(MixInArgs a) {
     // (model.rs:134-153) and silu_inplace's 256-channel body/tail rule (tensor.rs:1207-1211).
     __syncthreads();  // every wave has read its quarters
 #pragma unroll
-    for (int g = 0; g < kGroups; g++) {
+    for (int g = 0; g < G; g++) {
         const uint32_t b = b0 + g * kRowTile + lane % 16;
         float uv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         if (g < ng && has_rows && b < a.n && j0 < a.di) {
@@ -924,8 +939,9 @@ __global__ __launch_bounds__(kBlock) void k_mix_in(MixInArgs a) {
         if (tp >= a.wxp.rt) continue;
         AFrag a0, a1;
         decode_pair<Q8XP>(xpw[k], a0, a1);
+        const float xs[4] = {xps[k].x, xps[k].y, xps[k].z, xps[k].w};
 #pragma unroll
-        for (int g = 0; g < kGroups; g++) {
+        for (int g = 0; g < G; g++) {
             if (g >= ng) continue;
             const __bf16* f0 = lds + ((size_t)(g * 2) * 3) * 512 + lane * 8;
             const __bf16* f1 = f0 + 3 * 512;
@@ -935,8 +951,7 @@ __global__ __launch_bounds__(kBlock) void k_mix_in(MixInArgs a) {
             const uint32_t b = b0 + g * kRowTile + lane % 16;
             if (b < a.n) {
                 float* dst = a.xpart + ((size_t)p * a.cap + b) * a.xr_pad + tp * kRowTile + (lane / 16) * 4;
-                *(float4*)dst = make_float4(part[0] * xps[k][0], part[1] * xps[k][1], part[2] * xps[k][2],
-                                            part[3] * xps[k][3]);
+                *(float4*)dst = make_float4(part[0] * xs[0], part[1] * xs[1], part[2] * xs[2], part[3] * xs[3]);
             }
         }
     }
@@ -1269,7 +1284,7 @@ __global__ __launch_bounds__(kBlock) void k_head(HeadArgs a) {
     const int V = a.w.rows;
     const int t_first = (blockIdx.x * kWaves + wave) * kHeadTiles;
     SspLoad sl;
-    if constexpr (PRE) sl = ssp_load(a.ssp, a.tiles, b0, a.n);
+    if constexpr (PRE) sl = ssp_load(a.ssp, a.tiles, b0, a.n, kChunk);
     constexpr int R = Q8 ? kHeadRingQ8 : kHeadRingF32;
     Tiles<Q8, kHeadTiles, R> tl;
 #pragma unroll
@@ -1281,11 +1296,11 @@ __global__ __launch_bounds__(kBlock) void k_head(HeadArgs a) {
     tiles_prefetch<Q8, kHeadTiles, R>(a.w, tl, 0, np);
     if constexpr (PRE) {
         stage_copy(smem, a.xw, b0 / kRowTile, ng, a.w.ks);
-        ssp_reduce(sl, invs, a.tiles, a.d);
+        ssp_reduce(sl, invs, a.tiles, a.d, kChunk);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
     } else {
-        stage_normed(lds, a.x, a.norm_w, a.norm_b, a.d, a.w.ks, b0, a.n);
+        stage_normed(lds, a.x, a.norm_w, a.norm_b, a.d, a.w.ks, b0, a.n, kChunk);
     }
     f32x4 res[kHeadTiles][kGroups];
     tiles_gemm<Q8, kHeadTiles, R>(a.w, tl, lds, ng, 0, np, res);
@@ -1412,11 +1427,13 @@ namespace {
 
 uint32_t stage_lds_bytes(int ks) { return (uint32_t)(kGroups * ks * 3 * kLimbBytes); }
 
-// k_mix_in reuses its activation area for the k-quarter partials and the x_proj operand.
+// k_mix_in stages kInGroups column groups and reuses that area for the k-quarter
+// partials and the x_proj operand.
 uint32_t mix_in_lds_bytes(int ks) {
-    const uint32_t quarters = kWaves * kWaves * kGroups * kWave * sizeof(f32x4);
-    const uint32_t xp_operand = kGroups * 2 * 3 * kLimbBytes;
-    return std::max(stage_lds_bytes(ks), std::max(quarters, xp_operand));
+    const uint32_t acts = kInGroups * ks * 3 * kLimbBytes;
+    const uint32_t quarters = kWaves * kWaves * kInGroups * kWave * sizeof(f32x4);
+    const uint32_t xp_operand = kInGroups * 2 * 3 * kLimbBytes;
+    return std::max(acts, std::max(quarters, xp_operand));
 }
 
 template <typename K>
@@ -1468,6 +1485,7 @@ void build_step(const ModelView& m, Pool& p, const StepIO& io, std::vector<Launc
     const uint32_t n = io.n;
     const int d = (int)D.d, di = (int)D.di;
     const uint32_t chunks = (n + kChunk - 1) / kChunk;
+    const uint32_t in_chunks = (n + kInChunk - 1) / kInChunk;
     const int xr_pad = m.layers[0].x_proj.rt * kRowTile;
     const int nxb = di / 64;
     out.clear();
@@ -1493,7 +1511,7 @@ void build_step(const ModelView& m, Pool& p, const StepIO& io, std::vector<Launc
                      L.conv_w, L.conv_b, p.slots, p.cap, n, p.u, p.z, p.xpart, di, (int)D.dc, d, xr_pad,
                      p.xw, p.ssp, tiles};
         const int zb = L.in_z.rt / kWaves;
-        out.push_back(Launch::make(fin, dim3(nxb + zb, chunks), dim3(kBlock), lds_in, KC_MIX_IN, ma));
+        out.push_back(Launch::make(fin, dim3(nxb + zb, in_chunks), dim3(kBlock), lds_in, KC_MIX_IN, ma));
         ScanArgs sa{p.xpart, nxb, xr_pad, (int)D.xr(), p.u, p.z, p.ssm + li * ssm_layer, L.dt_w, L.dt_q,
                     L.dt_scales, L.dt_pad, L.dt_b, L.a_exp, L.d_vec, p.slots, p.cap, n, p.glimb, di, (int)D.dr};
         out.push_back(Launch::make((const void*)k_scan, dim3((di + kBlock - 1) / kBlock, n), dim3(kBlock), 0,
