@@ -68,10 +68,12 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kWave = 64;
 constexpr int kBlock = 256;
 constexpr int kWaves = kBlock / kWave;
-constexpr int kChunk = 32;                 // streams per k_head / k_mix_out workgroup
+constexpr int kChunk = 32;                 // streams per k_head workgroup
 constexpr int kGroups = kChunk / kRowTile; // MFMA column groups per chunk
 constexpr int kInGroups = 1;               // column groups per k_mix_in workgroup
 constexpr int kInChunk = kInGroups * kRowTile;
+constexpr int kOutGroups = 1;              // column groups per k_mix_out workgroup
+constexpr int kOutChunk = kOutGroups * kRowTile;
 constexpr int kLimbBytes = 64 * 8 * 2;     // one B fragment of one limb: 1 KB
 constexpr int kHeadTiles = 4;              // row tiles per wave in k_head
 // Weight k-pairs each wave keeps in flight (the product loop is unrolled by it): k_mix_in
@@ -996,6 +998,7 @@ __device__ __forceinline__ float dot_ref_col(const T* __restrict__ wt, int strid
 // dt-sparse skip and the hsum_ssm tree (tensor.rs:1283-1325), y * (z * sigmoid(z))
 // (tensor.rs:1239-1243 on 64-channel blocks); the gated value leaves as bf16 limbs.
 // Every operand is requested before the first wait.
+template <bool Q8DT>
 __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
     __shared__ float zp[kMaxXr];
     const int di = a.di, dr = a.dr;
@@ -1003,8 +1006,12 @@ __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
     const bool live = j_raw < di;
     const int j = live ? j_raw : di - 1;
     const uint32_t b = blockIdx.y;
-    const uint32_t s = clamp_slot(a.slots[b], a.cap);
-    // Per-channel operands, requested first.
+    // Requested in this order, all before the first wait: the slot, the slot-independent
+    // per-channel operands, the x_proj partials, then the state once the slot is known
+    // (vector loads return in order, so waiting for the slot does not wait for the rest).
+    // Loads past a short row or partial list read its last element instead of branching;
+    // those values are never used.
+    const uint32_t slot_raw = a.slots[b];
     const float4* ap = (const float4*)(a.a_exp + (size_t)j * 16);
     float4 av[4];
 #pragma unroll
@@ -1013,36 +1020,31 @@ __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
     const float zz = a.z[(size_t)b * di + j];
     const float dv = a.d_vec[j];
     const float dtb = a.dt_b[j];
+    const float dts = Q8DT ? a.dt_scales[j] : 1.0f;
+    constexpr int kRowVecs = Q8DT ? kMaxDr / 16 : kMaxDr / 4;  // 16-byte vectors of a dt row
+    const int row_vecs = Q8DT ? a.dt_pad / 16 : a.dt_pad / 4;
+    int4 wraw[kRowVecs];
+    {
+        const int4* rp = Q8DT ? (const int4*)(a.dt_q + (size_t)j * a.dt_pad) : (const int4*)(a.dt_w + (size_t)j * a.dt_pad);
+#pragma unroll
+        for (int q = 0; q < kRowVecs; q++) wraw[q] = rp[min(q, row_vecs - 1)];
+    }
+    // x_proj partials of this stream (threads < xr), summed in block order.
+    const int r = threadIdx.x;
+    const bool part_lane = r < a.xr;
+    float pv[kMaxNxb];
+    {
+        const float* pp = a.xpart + (size_t)b * a.xr_pad + (part_lane ? r : 0);
+        const size_t pstride = (size_t)a.cap * a.xr_pad;
+#pragma unroll
+        for (int u = 0; u < kMaxNxb; u++) pv[u] = pp[(size_t)min(u, a.nxb - 1) * pstride];
+    }
+    const uint32_t s = clamp_slot(slot_raw, a.cap);
     float4* stp = (float4*)(a.ssm + ((size_t)s * di + j) * 16);
     float4 sv[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) sv[i] = stp[i];
-    float wdt[kMaxDr];
-    if (a.dt_w) {
-        const float4* wp = (const float4*)(a.dt_w + (size_t)j * a.dt_pad);
-#pragma unroll
-        for (int q = 0; q < kMaxDr / 4; q++) {
-            const float4 v = q * 4 < a.dt_pad ? wp[q] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            wdt[4 * q] = v.x; wdt[4 * q + 1] = v.y; wdt[4 * q + 2] = v.z; wdt[4 * q + 3] = v.w;
-        }
-    } else {
-        const int4* qp = (const int4*)(a.dt_q + (size_t)j * a.dt_pad);
-#pragma unroll
-        for (int q = 0; q < kMaxDr / 16; q++) {
-            const int4 v = q * 16 < a.dt_pad ? qp[q] : make_int4(0, 0, 0, 0);
-            const int wv[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-            for (int e = 0; e < 16; e++) wdt[16 * q + e] = (float)(int8_t)(wv[e / 4] >> (8 * (e % 4)));
-        }
-    }
-    // x_proj partials of this stream (threads < xr), summed in block order.
-    const int r = threadIdx.x;
-    if (r < a.xr) {
-        const float* pp = a.xpart + (size_t)b * a.xr_pad + r;
-        const size_t pstride = (size_t)a.cap * a.xr_pad;
-        float pv[kMaxNxb];
-#pragma unroll
-        for (int u = 0; u < kMaxNxb; u++) pv[u] = u < a.nxb ? pp[(size_t)u * pstride] : 0.0f;
+    if (part_lane) {
         float acc = 0.0f;
 #pragma unroll
         for (int u = 0; u < kMaxNxb; u++)
@@ -1051,6 +1053,18 @@ __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
     }
     __syncthreads();
     if (!live) return;
+    float wdt[kMaxDr];
+#pragma unroll
+    for (int q = 0; q < kRowVecs; q++) {
+        const int wv[4] = {wraw[q].x, wraw[q].y, wraw[q].z, wraw[q].w};
+        if (Q8DT) {
+#pragma unroll
+            for (int e = 0; e < 16; e++) wdt[16 * q + e] = (float)(int8_t)(wv[e / 4] >> (8 * (e % 4)));
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; e++) wdt[4 * q + e] = bits_to_f((uint32_t)wv[e]);
+        }
+    }
     // dot_avx2_order (tensor.rs:1680-1693): eight lanes by column residue, fixed tree, tail.
     // dt_rank <= 64 means a quantized dt_proj has one scale per row (a 64-column group
     // spans the whole row or the group rule falls back to per-row), so the Q8 row is
@@ -1071,7 +1085,7 @@ __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
 #pragma unroll
         for (int c = 0; c < kMaxDr; c++)
             if (c >= body && c < dr) sdot += wdt[c] * zp[c];
-        dt = a.dt_w ? sdot : 0.0f + sdot * a.dt_scales[j];
+        dt = Q8DT ? 0.0f + sdot * dts : sdot;
     }
     dt = softplus_f(dt + dtb);
     float st[16];
@@ -1135,11 +1149,12 @@ struct MixOutArgs {
 // residual rows then leave as the next projection's pre-staged activations.
 template <bool Q8>
 __global__ __launch_bounds__(kOutWaves * kWave) void k_mix_out(MixOutArgs a) {
-    __shared__ f32x4 part[kOutWaves - 1][kGroups][kWave];
+    constexpr int G = kOutGroups;
+    __shared__ f32x4 part[kOutWaves - 1][G][kWave];
     const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
     const int t = blockIdx.x;
-    const uint32_t b0 = blockIdx.y * kChunk;
-    const int ng = (int)min((uint32_t)kGroups, (a.n - b0 + kRowTile - 1) / kRowTile);
+    const uint32_t b0 = blockIdx.y * kOutChunk;
+    const int ng = (int)min((uint32_t)G, (a.n - b0 + kRowTile - 1) / kRowTile);
     const TMat& w = a.w;
     const int np = w.ks / 2;
     const int p_lo = wave * np / kOutWaves, p_hi = (wave + 1) * np / kOutWaves;
@@ -1148,12 +1163,12 @@ __global__ __launch_bounds__(kOutWaves * kWave) void k_mix_out(MixOutArgs a) {
     const uint32_t g0 = b0 / kRowTile;
     const int r0 = t * kRowTile + (lane / 16) * 4;
     // Epilogue operands of wave 0, requested with the rest.
-    float4 xv[kGroups];
+    float4 xv[G];
     float rs[4] = {1.0f, 1.0f, 1.0f, 1.0f};
     float4 w4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if (wave == 0) {
 #pragma unroll
-        for (int g = 0; g < kGroups; g++) {
+        for (int g = 0; g < G; g++) {
             const uint32_t b = b0 + g * kRowTile + lane % 16;
             xv[g] = g < ng && b < a.n && r0 < a.d ? *(const float4*)(a.x + (size_t)b * a.d + r0)
                                                   : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -1164,15 +1179,15 @@ __global__ __launch_bounds__(kOutWaves * kWave) void k_mix_out(MixOutArgs a) {
         }
         if (a.xw != nullptr && r0 < a.d) w4 = *(const float4*)(a.nw_next + r0);
     }
-    f32x4 acc3[kGroups][3];
+    f32x4 acc3[G][3];
 #pragma unroll
-    for (int g = 0; g < kGroups; g++)
+    for (int g = 0; g < G; g++)
 #pragma unroll
         for (int o = 0; o < 3; o++) acc3[g][o] = f32x4{0, 0, 0, 0};
 #pragma unroll 1
     for (int pb = p_lo; pb < p_hi; pb += kOutPairs) {
         RawPair raw[kOutPairs];
-        bf16x8 bfr[kOutPairs][kGroups][2][3];
+        bf16x8 bfr[kOutPairs][G][2][3];
         float sc[kOutPairs][4];
 #pragma unroll
         for (int q = 0; q < kOutPairs; q++) {
@@ -1180,7 +1195,7 @@ __global__ __launch_bounds__(kOutWaves * kWave) void k_mix_out(MixOutArgs a) {
             if (p >= p_hi) break;
             raw[q] = load_pair<Q8>(w, t, p, lane);
 #pragma unroll
-            for (int g = 0; g < kGroups; g++) {
+            for (int g = 0; g < G; g++) {
                 if (g >= ng) continue;
 #pragma unroll
                 for (int h = 0; h < 2; h++) {
@@ -1202,7 +1217,7 @@ __global__ __launch_bounds__(kOutWaves * kWave) void k_mix_out(MixOutArgs a) {
             AFrag a0, a1;
             decode_pair<Q8>(raw[q], a0, a1);
 #pragma unroll
-            for (int g = 0; g < kGroups; g++) {
+            for (int g = 0; g < G; g++) {
                 if (g >= ng) continue;
                 if (grp) {
                     f32x4 pp{0, 0, 0, 0};
@@ -1232,17 +1247,17 @@ __global__ __launch_bounds__(kOutWaves * kWave) void k_mix_out(MixOutArgs a) {
             }
         }
     }
-    f32x4 acc[kGroups];
+    f32x4 acc[G];
 #pragma unroll
-    for (int g = 0; g < kGroups; g++) acc[g] = (acc3[g][0] + acc3[g][1]) + acc3[g][2];
+    for (int g = 0; g < G; g++) acc[g] = (acc3[g][0] + acc3[g][1]) + acc3[g][2];
     if (wave > 0) {
 #pragma unroll
-        for (int g = 0; g < kGroups; g++) part[wave - 1][g][lane] = acc[g];
+        for (int g = 0; g < G; g++) part[wave - 1][g][lane] = acc[g];
     }
     __syncthreads();
     if (wave != 0) return;
 #pragma unroll
-    for (int g = 0; g < kGroups; g++) {
+    for (int g = 0; g < G; g++) {
         if (g >= ng) continue;
         f32x4 s = acc[g];
         for (int q = 0; q < kOutWaves - 1; q++) s = s + part[q][g][lane];
@@ -1327,6 +1342,136 @@ __global__ __launch_bounds__(kBlock) void k_head(HeadArgs a) {
             } else {
                 for (int i = 0; i < 4; i++)
                     if (r0 + i < V) o[i] = acc[g][i];
+            }
+        }
+    }
+}
+
+// Weights-stationary LM head for Q8 per-row weights and pre-staged activations.  Each of
+// the kHwWaves waves decodes its kHwTiles row tiles (all NP k-pairs) into bf16 registers
+// once and keeps them for the whole kernel, walking the workgroup's column groups: group
+// g's activation tiles are copied into one LDS buffer while group g - 1 is multiplied
+// from the other.  Per tile and group: one accumulator over k-steps in order, limbs hi,
+// mid, lo per k-step; then the row scale and the stream's RMS scale.
+constexpr int kHwWaves = 8;    // waves per workgroup
+constexpr int kHwTiles = 2;    // row tiles per wave
+constexpr int kHwGroups = 8;   // column groups (16 streams) per workgroup
+
+__device__ __forceinline__ void copy_group(unsigned char* buf, const __bf16* __restrict__ xw, uint32_t g, int ks) {
+    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    const int blocks = ks * 3;
+    const __bf16* src = xw + (size_t)g * blocks * 512 + lane * 8;
+    lds_u8* dst = (lds_u8*)buf;
+#pragma unroll 2
+    for (int q = wave; q < blocks; q += kHwWaves)
+        __builtin_amdgcn_global_load_lds((const void*)(src + (size_t)q * 512),
+                                         (void __attribute__((address_space(3)))*)(dst + q * kLimbBytes), 16, 0, 0);
+}
+
+template <int NP>
+__global__ __launch_bounds__(kHwWaves * kWave) void k_head_ws(HeadArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ float invs[kHwGroups * kRowTile];
+    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    const TMat& w = a.w;
+    const int np = w.ks / 2, ks = w.ks;
+    const int V = w.rows;
+    const uint32_t gb = blockIdx.y * kHwGroups;
+    const int ngr = (int)min((uint32_t)kHwGroups, (a.n + kRowTile - 1) / kRowTile - gb);
+    const int t0 = (blockIdx.x * kHwWaves + wave) * kHwTiles;
+    const size_t buf_bytes = (size_t)ks * 3 * kLimbBytes;
+    // Requested first: the RMS partials of every stream of the workgroup, the weights and
+    // row scales, the first group's activations.
+    float ssv[kSspPerThread];
+    const int sb = threadIdx.x / kTps, ssub = threadIdx.x % kTps;  // 64 streams per pass, two passes
+    float ssv2[kSspPerThread];
+    {
+        const uint32_t b1 = gb * kRowTile + sb, b2 = b1 + 64;
+#pragma unroll
+        for (int i = 0; i < kSspPerThread; i++) {
+            const int t = ssub + kTps * i;
+            ssv[i] = b1 < a.n && t < a.tiles ? a.ssp[(size_t)b1 * a.tiles + t] : 0.0f;
+            ssv2[i] = b2 < a.n && t < a.tiles ? a.ssp[(size_t)b2 * a.tiles + t] : 0.0f;
+        }
+    }
+    int4 wq[NP][kHwTiles];
+    float4 rsc[kHwTiles];
+#pragma unroll
+    for (int i = 0; i < kHwTiles; i++) {
+        const int t = min(t0 + i, w.rt - 1);
+#pragma unroll
+        for (int p = 0; p < NP; p++)
+            if (p < np) wq[p][i] = ((const int4*)w.w)[((size_t)t * np + p) * 64 + lane];
+        rsc[i] = *(const float4*)(w.scales + t * kRowTile + (lane / 16) * 4);
+    }
+    copy_group(smem, a.xw, gb, ks);
+    {
+        float s1 = 0.0f, s2 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kSspPerThread; i++)
+            if (ssub + kTps * i < a.tiles) {
+                s1 += ssv[i];
+                s2 += ssv2[i];
+            }
+#pragma unroll
+        for (int o = 1; o < kTps; o <<= 1) {
+            s1 += __shfl_xor(s1, o, kWave);
+            s2 += __shfl_xor(s2, o, kWave);
+        }
+        if (ssub == 0) {
+            invs[sb] = 1.0f / sqrtf(s1 / (float)a.d + 1e-5f);
+            invs[sb + 64] = 1.0f / sqrtf(s2 / (float)a.d + 1e-5f);
+        }
+    }
+    AFrag wd[NP][kHwTiles][2];
+#pragma unroll
+    for (int p = 0; p < NP; p++)
+#pragma unroll
+        for (int i = 0; i < kHwTiles; i++) {
+            RawPair raw;
+            raw.v[0] = p < np ? wq[p][i] : make_int4(0, 0, 0, 0);
+            decode_pair<true>(raw, wd[p][i][0], wd[p][i][1]);
+        }
+#pragma unroll 1
+    for (int gi = 0; gi < ngr; gi++) {
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's copies (and earlier stores) are done
+        __syncthreads();                // every wave's copies of group gi, and reads of gi - 1
+        if (gi + 1 < ngr) copy_group(smem + ((gi + 1) & 1) * buf_bytes, a.xw, gb + gi + 1, ks);
+        const __bf16* lds = (const __bf16*)(smem + (gi & 1) * buf_bytes);
+        f32x4 acc[kHwTiles];
+#pragma unroll
+        for (int i = 0; i < kHwTiles; i++) acc[i] = f32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int p = 0; p < NP; p++) {
+            if (p >= np) continue;
+            bf16x8 bf[2][3];
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const __bf16* f = lds + ((size_t)(2 * p + h) * 3) * 512 + lane * 8;
+#pragma unroll
+                for (int m = 0; m < 3; m++) bf[h][m] = lds_frag(f + m * 512);
+            }
+#pragma unroll
+            for (int i = 0; i < kHwTiles; i++) {
+                acc[i] = mma_step<true>(wd[p][i][0], bf[0][0], bf[0][1], bf[0][2], acc[i]);
+                acc[i] = mma_step<true>(wd[p][i][1], bf[1][0], bf[1][1], bf[1][2], acc[i]);
+            }
+        }
+        const uint32_t b = (gb + gi) * kRowTile + lane % 16;
+        const float inv = invs[gi * kRowTile + lane % 16];
+#pragma unroll
+        for (int i = 0; i < kHwTiles; i++) {
+            const int t = t0 + i;
+            const int r0 = t * kRowTile + (lane / 16) * 4;
+            if (t >= w.rt || b >= a.n) continue;
+            const float v[4] = {acc[i][0] * rsc[i].x * inv, acc[i][1] * rsc[i].y * inv, acc[i][2] * rsc[i].z * inv,
+                                acc[i][3] * rsc[i].w * inv};
+            float* o = a.out + (size_t)b * V + r0;
+            if (r0 + 3 < V && (V & 3) == 0) {
+                *(float4*)o = make_float4(v[0], v[1], v[2], v[3]);
+            } else {
+                for (int e = 0; e < 4; e++)
+                    if (r0 + e < V) o[e] = v[e];
             }
         }
     }
@@ -1477,6 +1622,16 @@ const void* head_fn2(bool pre, uint32_t lds) {
 
 const void* head_fn(bool q8, bool pre, uint32_t lds) { return q8 ? head_fn2<true>(pre, lds) : head_fn2<false>(pre, lds); }
 
+// Weights-stationary head for Q8 per-row weights with pre-staged activations and
+// d <= 768 (12 k-pairs held per tile); null where it does not apply.
+const void* head_ws_fn(int np, uint32_t lds) {
+    if (np <= 2) { allow_lds(k_head_ws<2>, lds); return (const void*)k_head_ws<2>; }
+    if (np <= 4) { allow_lds(k_head_ws<4>, lds); return (const void*)k_head_ws<4>; }
+    if (np <= 8) { allow_lds(k_head_ws<8>, lds); return (const void*)k_head_ws<8>; }
+    if (np <= 12) { allow_lds(k_head_ws<12>, lds); return (const void*)k_head_ws<12>; }
+    return nullptr;
+}
+
 // The launches of one step, in stream order; io_index / head_index / softmax_index name
 // the launches whose arguments carry caller pointers.
 void build_step(const ModelView& m, Pool& p, const StepIO& io, std::vector<Launch>& out, int& io_index,
@@ -1486,6 +1641,7 @@ void build_step(const ModelView& m, Pool& p, const StepIO& io, std::vector<Launc
     const int d = (int)D.d, di = (int)D.di;
     const uint32_t chunks = (n + kChunk - 1) / kChunk;
     const uint32_t in_chunks = (n + kInChunk - 1) / kInChunk;
+    const uint32_t out_chunks = (n + kOutChunk - 1) / kOutChunk;
     const int xr_pad = m.layers[0].x_proj.rt * kRowTile;
     const int nxb = di / 64;
     out.clear();
@@ -1514,21 +1670,31 @@ void build_step(const ModelView& m, Pool& p, const StepIO& io, std::vector<Launc
         out.push_back(Launch::make(fin, dim3(nxb + zb, in_chunks), dim3(kBlock), lds_in, KC_MIX_IN, ma));
         ScanArgs sa{p.xpart, nxb, xr_pad, (int)D.xr(), p.u, p.z, p.ssm + li * ssm_layer, L.dt_w, L.dt_q,
                     L.dt_scales, L.dt_pad, L.dt_b, L.a_exp, L.d_vec, p.slots, p.cap, n, p.glimb, di, (int)D.dr};
-        out.push_back(Launch::make((const void*)k_scan, dim3((di + kBlock - 1) / kBlock, n), dim3(kBlock), 0,
-                                   KC_SCAN, sa));
+        const void* fs = L.dt_q ? (const void*)k_scan<true> : (const void*)k_scan<false>;
+        out.push_back(Launch::make(fs, dim3((di + kBlock - 1) / kBlock, n), dim3(kBlock), 0, KC_SCAN, sa));
         const float* nw_next = li + 1 < D.nl ? m.layers[li + 1].norm_w : m.norm_f_w;
         MixOutArgs oa{L.out_proj, p.glimb, p.x, n, d, nw_next, pre ? p.xw : nullptr, p.ssp, ks_x, tiles};
         const void* fo = q8 ? (const void*)k_mix_out<true> : (const void*)k_mix_out<false>;
-        out.push_back(Launch::make(fo, dim3(L.out_proj.rt, chunks), dim3(kOutWaves * kWave), 0, KC_MIX_OUT, oa));
+        out.push_back(Launch::make(fo, dim3(L.out_proj.rt, out_chunks), dim3(kOutWaves * kWave), 0, KC_MIX_OUT, oa));
     }
     const TMat& H = *m.head;
     HeadArgs ha{p.x, m.norm_f_w, m.norm_f_b, H, io.out, n, d, p.xw, p.ssp, tiles};
-    const uint32_t lds_h = stage_lds_bytes(H.ks);
-    const int tiles_per_block = kWaves * kHeadTiles;
     head_index = (int)out.size();
-    out.push_back(Launch::make(head_fn(H.group != 0, pre, lds_h),
-                               dim3((H.rt + tiles_per_block - 1) / tiles_per_block, chunks), dim3(kBlock), lds_h,
-                               KC_HEAD, ha));
+    const bool ws = pre && H.group != 0 && H.group == H.cols && H.ks / 2 <= 12;
+    if (ws) {
+        const uint32_t lds_h = 2 * (uint32_t)H.ks * 3 * kLimbBytes;
+        const int tiles_per_block = kHwWaves * kHwTiles;
+        const uint32_t groups = (n + kRowTile - 1) / kRowTile;
+        out.push_back(Launch::make(head_ws_fn(H.ks / 2, lds_h),
+                                   dim3((H.rt + tiles_per_block - 1) / tiles_per_block, (groups + kHwGroups - 1) / kHwGroups),
+                                   dim3(kHwWaves * kWave), lds_h, KC_HEAD, ha));
+    } else {
+        const uint32_t lds_h = stage_lds_bytes(H.ks);
+        const int tiles_per_block = kWaves * kHeadTiles;
+        out.push_back(Launch::make(head_fn(H.group != 0, pre, lds_h),
+                                   dim3((H.rt + tiles_per_block - 1) / tiles_per_block, chunks), dim3(kBlock), lds_h,
+                                   KC_HEAD, ha));
+    }
     softmax_index = -1;
     if (io.probs) {
         softmax_index = (int)out.size();
