@@ -7,8 +7,9 @@ reset at the 4096-token boundary (placed inside the timed region).  A step is on
 for each of the 32 streams.  Inputs (weights, token ids, slots) are resident in HBM
 before timing starts; logits stay on the device.
 
-Prints one JSON line.  `roofline` covers the dominant kernel (HIP events around its
-launches on the library's stream, in a probe pass after the timed region);
+Prints one JSON line.  `roofline` covers the dominant kernel (HIP events on the
+library's stream around all of a step's launches of that kernel issued back to back, in
+a probe pass after the timed region);
 `cpu_baseline` times the CPU oracle (a C restatement of the reference CPU path) on the
 host cores for a bounded sample of the same workload.
 """
@@ -131,6 +132,9 @@ def main() -> int:
     ap.add_argument("--probe-steps", type=int, default=8)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration-mib", type=int, default=0,
+                    help="after the probe pass, copy this many MiB device to device on the library's "
+                         "stream (a copy of known size for scaling HBM byte counters)")
     ap.add_argument("--model", default=os.path.join(tempfile.gettempdir(), "redukt_bench", "mamba130m.rbin"))
     args = ap.parse_args()
 
@@ -190,28 +194,38 @@ def main() -> int:
     tok_s = n * K / (ms / 1e3)
     log(f"timed {K} steps: {ms:.2f} ms on the stream ({ms / K * 1e3:.1f} us/step), wall {wall * 1e3:.1f} ms")
 
-    # Probe pass: HIP events around each launch of every kernel class.
+    # Probe pass, after the timed region on the same stream and pool, two ways per kernel
+    # class: (1) class-only steps, all of a step's launches of the class back to back
+    # between one event pair (avg_us: per-launch time with the event cost spread over the
+    # launches; this is the roofline figure); (2) full steps with every launch of the class
+    # recording its own dispatch start and stop (dispatch_avg_us).
     per_class = {}
     P = args.probe_steps
-    for name, cls in ffi.KERNEL_CLASSES.items():
-        if name == "softmax":
-            continue
-        launches = dims.n_layer if name in ("mix_in", "scan", "mix_out") else 1
-        evs = [hip.Event() for _ in range(2 * launches * P)]
+    t0 = W + K
+
+    def probe(cls: int, n_events: int) -> list:
+        evs = [hip.Event() for _ in range(n_events)]
         arr = (ctypes.c_void_p * len(evs))(*[e.h for e in evs])
         be.probe_kernel(cls, arr)
-        t0 = W + K
         for t in range(P):
             step(t0 + t % (total - t0))
         used = be.probe_used()
         be.probe_kernel(0, None)
         hip.stream_sync(stream)
-        assert used == len(evs), (name, used, len(evs))
-        durs = [evs[2 * i].elapsed_ms(evs[2 * i + 1]) for i in range(len(evs) // 2)]
-        per_class[name] = {"avg_us": 1e3 * float(np.mean(durs)), "launches_per_step": launches,
-                           "us_per_step": 1e3 * float(np.sum(durs)) / P}
+        assert used == len(evs), (cls, used, len(evs))
+        durs = [1e3 * evs[2 * i].elapsed_ms(evs[2 * i + 1]) for i in range(len(evs) // 2)]
         for e in evs:
             e.close()
+        return durs
+
+    for name, cls in ffi.KERNEL_CLASSES.items():
+        if name == "softmax":
+            continue
+        launches = dims.n_layer if name in ("mix_in", "scan", "mix_out") else 1
+        only = probe(cls | ffi.PROBE_CLASS_ONLY, 2 * P)
+        each = probe(cls, 2 * launches * P)
+        per_class[name] = {"avg_us": float(np.mean(only)) / launches, "launches_per_step": launches,
+                           "us_per_step": float(np.mean(only)), "dispatch_avg_us": round(float(np.mean(each)), 2)}
     alg = algorithmic_bytes(dims, profile, n)
     dom = max(per_class, key=lambda k: per_class[k]["us_per_step"])
     avg_s = per_class[dom]["avg_us"] / 1e6
@@ -222,6 +236,15 @@ def main() -> int:
         v["avg_us"] = round(v["avg_us"], 2)
         v["us_per_step"] = round(v["us_per_step"], 2)
     log("per kernel class: " + json.dumps(per_class))
+
+    if args.copy_calibration_mib > 0:
+        nb = args.copy_calibration_mib << 20
+        src, dst = hip.DeviceBuffer(nb), hip.DeviceBuffer(nb)
+        hip.copy_d2d_async(dst.ptr, src.ptr, nb, stream)
+        hip.stream_sync(stream)
+        log(f"copy calibration: {nb} bytes device to device")
+        src.close()
+        dst.close()
 
     # FFI end-to-end rate (host buffers, D2H of n rows of logits, synchronous).
     out = np.empty((n, dims.vocab), np.float32)
@@ -241,6 +264,17 @@ def main() -> int:
         log("timing the CPU oracle on the host cores")
         cpu = cpu_baseline(path, profile, n, tokens, args.cpu_seconds)
 
+    # HBM bytes per launch of the dominant kernel from the committed counter passes
+    # (FETCH_SIZE / WRITE_SIZE scaled by a copy of known size), when they cover this workload.
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    workload = f"mamba130m-{args.profile}-n{n}-zipf1.1"
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            tj = json.load(f)
+        if tj.get("workload") == workload:
+            traffic = tj["bytes_per_launch"].get(dom)
+
     sb = step_bytes(dims, profile, n)
     result = {
         "metric": METRIC,
@@ -255,11 +289,11 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": f"mamba130m-{args.profile}-n{n}-zipf1.1", "layers": dims.n_layer,
+        "config": {"workload": workload, "layers": dims.n_layer,
                    "d_model": dims.d_model, "vocab": dims.vocab, "streams": n, "weight_profile": args.profile,
                    "reset_every": RESET_PERIOD, "reset_at_timed_step": reset_step, "parallelism": "none"},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic},
         "cpu_baseline": cpu,
         "step_bytes": sb,
         "step_GBps": round(sb / (ms / K / 1e3) / 1e9, 1),

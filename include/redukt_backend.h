@@ -129,13 +129,18 @@ int32_t redukt_backend_device_status(void);
  * so a caller can time the step with events on that stream.  NULL before init. */
 void* redukt_backend_stream(void);
 
-/* Measurement hook.  While kernel_class != 0, every launch of that kernel class is
- * bracketed by two hipEvent_t records taken in order from events[0..n_events) (caller
- * owned, alive while probing); recording stops when they run out.  Classes: 1 embed,
+/* Measurement hook.  While kernel_class != 0, every launch of that kernel class fills
+ * two hipEvent_t taken in order from events[0..n_events) (caller owned, alive while
+ * probing); recording stops when they run out.  Classes: 1 embed,
  * 2 mix_in (norm + in_proj + conv + x_proj partials), 3 scan (dt_proj + selective scan +
  * gate), 4 mix_out (out_proj + residual), 5 head (final norm + LM head), 6 softmax.
- * Probed steps are launched kernel by kernel instead of from the step's hipGraph.
- * kernel_class 0 switches the probe off.  Returns OK or INVALID_ARGUMENT. */
+ * Probed launches record their own dispatch start and stop (hipExtLaunchKernel), and
+ * probed steps are launched kernel by kernel instead of from the step's hipGraph.
+ * With REDUKT_PROBE_CLASS_ONLY or'ed into kernel_class, a probed step launches only the
+ * kernels of that class, back to back, between one pair of events: the other kernels
+ * of the step do not run (timing only; the recurrent state does not advance as in a
+ * real step).  kernel_class 0 switches the probe off.  Returns OK or INVALID_ARGUMENT. */
+#define REDUKT_PROBE_CLASS_ONLY 0x100u
 int32_t redukt_backend_probe_kernel(uint32_t kernel_class, void** events, uint32_t n_events);
 
 /* Number of events the current probe has recorded. */

@@ -514,11 +514,14 @@ void* redukt_backend_stream(void) { return (void*)G.stream; }
 
 int32_t redukt_backend_probe_kernel(uint32_t kernel_class, void** events, uint32_t n_events) {
     if (!G.ready) return BACKEND_INIT_FAILED;
+    const bool only = (kernel_class & REDUKT_PROBE_CLASS_ONLY) != 0;
+    kernel_class &= ~REDUKT_PROBE_CLASS_ONLY;
     if (kernel_class >= KC_COUNT || (kernel_class != KC_NONE && (!events || n_events < 2)))
         return BACKEND_INVALID_ARGUMENT;
     G.probe = Probe{};
     if (kernel_class != KC_NONE) {
         G.probe.cls = kernel_class;
+        G.probe.only = only;
         G.probe.ev = (hipEvent_t*)events;
         G.probe.cap = n_events;
     }

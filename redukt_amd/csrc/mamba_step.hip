@@ -29,9 +29,11 @@
 // per-thread code in the reference's own operation order and math
 // (src/infrastructure/mamba/model.rs:134-190, src/domain/tensor.rs:759-1325), so they
 // reproduce the CPU path's bits for identical inputs.  Contraction is off in this file.
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 
@@ -1727,6 +1729,16 @@ hipKernelNodeParams node_params(const Launch& l, void** params) {
         if (e_ != hipSuccess) return e_; \
     } while (0)
 
+// REDUKT_GPU_GRAPH=0 issues every step as direct launches instead of a replayed hipGraph
+// (for tools that do not follow graph launches).
+static bool use_graphs() {
+    static const bool on = [] {
+        const char* e = getenv("REDUKT_GPU_GRAPH");
+        return !(e && e[0] == '0');
+    }();
+    return on;
+}
+
 StepRunner::~StepRunner() { clear(); }
 
 void StepRunner::destroy(Graph& g) {
@@ -1741,26 +1753,87 @@ void StepRunner::clear() {
     graphs_.clear();
 }
 
+// Record one step as a graph by stream capture; the nodes whose arguments carry caller
+// pointers are looked up in capture order and checked against their kernels.
+hipError_t StepRunner::capture(const std::vector<Launch>& seq, int io_i, int head_i, int sm_i, hipStream_t st,
+                               Graph& g) {
+    RDK_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+    hipError_t err = hipSuccess;
+    for (const Launch& l : seq) {
+        err = launch_direct(l, st);
+        if (err != hipSuccess) break;
+    }
+    hipGraph_t graph = nullptr;
+    const hipError_t end = hipStreamEndCapture(st, &graph);
+    if (err == hipSuccess) err = end;
+    if (err != hipSuccess) {
+        if (graph) (void)hipGraphDestroy(graph);
+        return err;
+    }
+    g.g = graph;
+    size_t count = 0;
+    RDK_TRY(hipGraphGetNodes(graph, nullptr, &count));
+    std::vector<hipGraphNode_t> nodes(count);
+    RDK_TRY(hipGraphGetNodes(graph, nodes.data(), &count));
+    g.updatable = count == seq.size();
+    auto pick = [&](int i, hipGraphNode_t& out) {
+        out = nullptr;
+        if (i < 0 || !g.updatable) return;
+        hipKernelNodeParams kp{};
+        if (hipGraphKernelNodeGetParams(nodes[i], &kp) == hipSuccess && kp.func == seq[i].fn) {
+            out = nodes[i];
+        } else {
+            g.updatable = false;
+        }
+    };
+    pick(io_i, g.io_node);
+    pick(head_i, g.head_node);
+    pick(sm_i, g.softmax_node);
+    return hipGraphInstantiate(&g.exec, graph, nullptr, nullptr, 0);
+}
+
 hipError_t StepRunner::run(const ModelView& m, Pool& p, const StepIO& io, hipStream_t st, Probe* probe) {
     std::unique_ptr<std::vector<Launch>> owned(new std::vector<Launch>());
     std::vector<Launch>& seq = *owned;
     int io_i = -1, head_i = -1, sm_i = -1;
     build_step(m, p, io, seq, io_i, head_i, sm_i);
+    if (probe && probe->cls != KC_NONE && probe->only) {
+        const bool rec = probe->used + 2 <= probe->cap;
+        if (rec) RDK_TRY(hipEventRecord(probe->ev[probe->used], st));
+        for (const Launch& l : seq)
+            if (l.cls == probe->cls) RDK_TRY(launch_direct(l, st));
+        if (rec) {
+            RDK_TRY(hipEventRecord(probe->ev[probe->used + 1], st));
+            probe->used += 2;
+        }
+        return hipSuccess;
+    }
     if (probe && probe->cls != KC_NONE) {
+        // Probed launches carry their own dispatch start/stop timestamps.
         for (const Launch& l : seq) {
             const bool on = l.cls == probe->cls && probe->used + 2 <= probe->cap;
-            if (on) RDK_TRY(hipEventRecord(probe->ev[probe->used], st));
-            RDK_TRY(launch_direct(l, st));
             if (on) {
-                RDK_TRY(hipEventRecord(probe->ev[probe->used + 1], st));
+                void* params[] = {l.argp};
+                RDK_TRY(hipExtLaunchKernel(l.fn, l.grid, l.block, params, l.lds, st, probe->ev[probe->used],
+                                           probe->ev[probe->used + 1], 0));
                 probe->used += 2;
+            } else {
+                RDK_TRY(launch_direct(l, st));
             }
         }
         return hipSuccess;
     }
+    if (!use_graphs()) {
+        for (const Launch& l : seq) RDK_TRY(launch_direct(l, st));
+        return hipSuccess;
+    }
+    auto same_io = [&](const Graph& g) {
+        return g.tokens == io.tokens && g.slots == io.slots && g.out == io.out && g.err == io.err;
+    };
     Graph* hit = nullptr;
     for (Graph& g : graphs_)
-        if (g.n == io.n && g.probs == io.probs && g.check == io.check && g.pool == &p) hit = &g;
+        if (g.n == io.n && g.probs == io.probs && g.check == io.check && g.pool == &p && (g.updatable || same_io(g)))
+            hit = &g;
     if (!hit) {
         if (graphs_.size() >= 8) {
             auto old = std::min_element(graphs_.begin(), graphs_.end(),
@@ -1773,33 +1846,17 @@ hipError_t StepRunner::run(const ModelView& m, Pool& p, const StepIO& io, hipStr
         g.probs = io.probs;
         g.check = io.check;
         g.pool = &p;
-        RDK_TRY(hipGraphCreate(&g.g, 0));
-        hipGraphNode_t prev = nullptr;
-        for (size_t i = 0; i < seq.size(); i++) {
-            void* params[] = {seq[i].argp};
-            hipKernelNodeParams kp = node_params(seq[i], params);
-            hipGraphNode_t node;
-            hipError_t e = hipGraphAddKernelNode(&node, g.g, prev ? &prev : nullptr, prev ? 1 : 0, &kp);
-            if (e != hipSuccess) {
-                (void)hipGraphDestroy(g.g);
-                return e;
-            }
-            if ((int)i == io_i) g.io_node = node;
-            if ((int)i == head_i) g.head_node = node;
-            if ((int)i == sm_i) g.softmax_node = node;
-            prev = node;
-        }
-        hipError_t e = hipGraphInstantiate(&g.exec, g.g, nullptr, nullptr, 0);
+        const hipError_t e = capture(seq, io_i, head_i, sm_i, st, g);
         if (e != hipSuccess) {
-            (void)hipGraphDestroy(g.g);
+            destroy(g);
             return e;
         }
         g.launches = owned.release();
         graphs_.push_back(g);
         hit = &graphs_.back();
-    } else {
-        // Same shape: only the caller pointers can differ.  The new arguments replace the
-        // stored ones, so the graph's parameter storage stays alive with it.
+    } else if (!same_io(*hit)) {
+        // Same shape, other caller pointers: the new arguments replace the stored ones, so
+        // the graph's parameter storage stays alive with it.
         std::vector<Launch>& keep = *hit->launches;
         keep[io_i] = std::move(seq[io_i]);
         keep[head_i] = std::move(seq[head_i]);
@@ -1817,6 +1874,10 @@ hipError_t StepRunner::run(const ModelView& m, Pool& p, const StepIO& io, hipStr
             RDK_TRY(hipGraphExecKernelNodeSetParams(hit->exec, hit->softmax_node, &k_s));
         }
     }
+    hit->tokens = io.tokens;
+    hit->slots = io.slots;
+    hit->out = io.out;
+    hit->err = io.err;
     hit->last_use = ++clock_;
     return hipGraphLaunch(hit->exec, st);
 }

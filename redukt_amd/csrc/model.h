@@ -90,11 +90,13 @@ enum KernelClass : uint32_t {
     KC_COUNT = 7
 };
 
-// Measurement hook: while cls != KC_NONE, every launch of that class is bracketed by
-// two events taken in order from ev[0..cap) (ev is caller-owned); `used` counts them.
-// Probed steps run as direct launches, not as the replayed graph.
+// Measurement hook: while cls != KC_NONE, every launch of that class records its dispatch
+// start and stop into two events taken in order from ev[0..cap) (ev is caller-owned);
+// `used` counts them.  Probed steps run as direct launches, not as the replayed graph.
+// With `only`, a probed step launches just that class's kernels between one event pair.
 struct Probe {
     uint32_t cls = KC_NONE;
+    bool only = false;   // launch only this class, back to back, between one event pair
     hipEvent_t* ev = nullptr;
     uint32_t cap = 0, used = 0;
 };
@@ -138,12 +140,20 @@ private:
         uint32_t n = 0;
         bool probs = false, check = false;
         const Pool* pool = nullptr;
+        // Caller pointers the graph was last launched with; `updatable` when the nodes
+        // carrying them were found, so other pointers are set in place.
+        const uint32_t* tokens = nullptr;
+        const uint32_t* slots = nullptr;
+        const float* out = nullptr;
+        const uint32_t* err = nullptr;
+        bool updatable = false;
         hipGraph_t g = nullptr;
         hipGraphExec_t exec = nullptr;
         hipGraphNode_t io_node = nullptr, head_node = nullptr, softmax_node = nullptr;
         uint64_t last_use = 0;
         std::vector<Launch>* launches = nullptr;  // argument storage, alive as long as the graph
     };
+    hipError_t capture(const std::vector<Launch>& seq, int io_i, int head_i, int sm_i, hipStream_t st, Graph& g);
     void destroy(Graph& g);
     std::vector<Graph> graphs_;
     uint64_t clock_ = 0;

@@ -41,8 +41,10 @@ V3_SYMBOLS = ("redukt_backend_init_ex", "redukt_backend_forward_batch_probs", "r
               "redukt_backend_device_status", "redukt_backend_stream", "redukt_backend_get_state",
               "redukt_backend_probe_kernel", "redukt_backend_probe_used")
 
-# Kernel classes of redukt_backend_probe_kernel.
+# Kernel classes of redukt_backend_probe_kernel, and the flag that makes a probed step
+# launch only the kernels of that class (REDUKT_PROBE_CLASS_ONLY).
 KERNEL_CLASSES = {"embed": 1, "mix_in": 2, "scan": 3, "mix_out": 4, "head": 5, "softmax": 6}
+PROBE_CLASS_ONLY = 0x100
 
 
 class BackendResult(enum.IntEnum):

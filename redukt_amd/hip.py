@@ -38,6 +38,7 @@ def rt() -> ctypes.CDLL:
         h.hipFree.argtypes = [ctypes.c_void_p]
         h.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
         h.hipMemset.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t]
+        h.hipMemcpyAsync.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_void_p]
         h.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
         h.hipEventDestroy.argtypes = [ctypes.c_void_p]
         h.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
@@ -118,6 +119,12 @@ class Event:
         if self.h:
             rt().hipEventDestroy(self.h)
             self.h = None
+
+
+def copy_d2d_async(dst: int, src: int, nbytes: int, stream: int) -> None:
+    """Device-to-device copy on `stream` (hipMemcpyDeviceToDevice = 3)."""
+    check(rt().hipMemcpyAsync(ctypes.c_void_p(dst), ctypes.c_void_p(src), nbytes, 3, ctypes.c_void_p(stream)),
+          "hipMemcpyAsync")
 
 
 def stream_sync(stream: int) -> None:
