@@ -15,6 +15,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include "internal.h"
 #include "oracle.h"
 #include "pool.h"
 
@@ -98,7 +99,8 @@ float orc_lnf(float x) {
 /* tensor.rs:877-879: one lane of fast_exp_ps (a NaN lane is clamped to EXP_LO). */
 float orc_lane_expf(float x) { return orc_expf(isnan(x) ? -87.3365447505531f : x); }
 /* tensor.rs:883-885 */
-static inline float lane_sigmoidf(float x) { return 1.0f / (1.0f + orc_lane_expf(0.0f - x)); }
+float orc_lane_sigmoidf(float x) { return 1.0f / (1.0f + orc_lane_expf(0.0f - x)); }
+#define lane_sigmoidf orc_lane_sigmoidf
 /* tensor.rs:841-843 */
 float orc_sigmoidf(float x) { return 1.0f / (1.0f + orc_expf(-x)); }
 /* tensor.rs:853-855 */
@@ -245,13 +247,6 @@ void orc_ssm_d16(float* y, float* ss, const float* dt, const float* conv_out, co
  * ==================================================================== */
 
 typedef struct {
-    int rows, cols, group; /* group: 0 = F32 */
-    float* f;              /* F32 data (NULL for Q8) */
-    int8_t* q;
-    float* sc;
-} Mat;
-
-typedef struct {
     float *norm_w, *norm_b;
     Mat in_proj, x_proj, dt_proj, out_proj;
     float *conv_w, *conv_b, *dt_b, *a_log, *d_vec;
@@ -275,10 +270,10 @@ struct OrcMamba {
     float *x, *normed, *xz, *conv_out, *zp, *dt, *y, *gated, *res;
 };
 
-static void mat_free(Mat* m) { free(m->f); free(m->q); free(m->sc); memset(m, 0, sizeof(*m)); }
+void mat_free(Mat* m) { free(m->f); free(m->q); free(m->sc); memset(m, 0, sizeof(*m)); }
 
 /* MambaMatrix::new (model.rs:64-69) and, with profile bit 2, the same recipe on x/dt_proj. */
-static int mat_make(Mat* m, float* data, int rows, int cols, int quant, int group) {
+int mat_make(Mat* m, float* data, int rows, int cols, int quant, int group) {
     m->rows = rows; m->cols = cols;
     if (!quant) { m->f = data; m->group = 0; return 0; }
     int g = group > 0 ? group : cols;
@@ -292,7 +287,7 @@ static int mat_make(Mat* m, float* data, int rows, int cols, int quant, int grou
 }
 
 /* Row `row` into out: copy (F32) or q*scale per group (gemv.rs:285-295). */
-static void mat_row(const Mat* m, int row, float* out) {
+void mat_row(const Mat* m, int row, float* out) {
     if (!m->group) { memcpy(out, m->f + (size_t)row * m->cols, sizeof(float) * m->cols); return; }
     int gpr = m->cols / m->group;
     const int8_t* q = m->q + (size_t)row * m->cols;
@@ -301,7 +296,7 @@ static void mat_row(const Mat* m, int row, float* out) {
 }
 
 /* Rows [r0, r1) of out = M·v in the reference order (f32_rows / q8w_rows). */
-static void mat_rows(const Mat* m, int r0, int r1, const float* v, float* out) {
+void mat_rows(const Mat* m, int r0, int r1, const float* v, float* out) {
     if (!m->group) {
         for (int r = r0; r < r1; r++) out[r] = orc_dot_f32(m->f + (size_t)r * m->cols, v, m->cols);
     } else {
@@ -311,7 +306,7 @@ static void mat_rows(const Mat* m, int r0, int r1, const float* v, float* out) {
     }
 }
 
-static float* read_f32(FILE* f, size_t count) {
+float* read_f32(FILE* f, size_t count) {
     float* p = (float*)malloc(sizeof(float) * (count ? count : 1));
     if (!p) return NULL;
     if (fread(p, sizeof(float), count, f) != count) { free(p); return NULL; }

@@ -68,6 +68,37 @@ int       orc_mamba_get_state(const OrcMamba* m, uint32_t slot, uint32_t layer, 
  * 2 emb, 3 x_proj, 4 dt_proj; layer ignored for emb.  Writes rows*cols floats. */
 int       orc_mamba_dequant(const OrcMamba* m, int which, uint32_t layer, float* out);
 
+/* ---- RWKV-7 element-wise helpers (tensor.rs; 8-aligned body in lane form) ---- */
+void  orc_tanh_inplace(float* x, int n);
+void  orc_sigmoid_inplace(float* x, int n);
+void  orc_sigmoid_add_into(float* out, const float* base, const float* offset, int n);
+void  orc_decay_sigmoid_into(float* out, const float* base, const float* offset, int n);
+void  orc_sigmoid_mix_inplace(float* v, const float* v_first, const float* base, const float* offset, int n);
+void  orc_group_norm_into(float* out, const float* x, int groups, const float* w, const float* b, int n, float eps);
+void  orc_l2_normalize_per_head(float* x, int heads, int hs);
+void  orc_mat_vec_small(float* out, const float* a, const float* v, int n);
+/* One head's WKV-7 update and read-out; tmp holds 3n floats. */
+void  orc_wkv_head(float* S, int n, const float* r, const float* w, const float* kk, const float* a,
+                   const float* v, const float* kmod, float* out, float* tmp);
+float orc_lane_sigmoidf(float x);
+
+/* ---- RWKV-7 model (rwkv7/model.rs) ---- */
+typedef struct OrcRwkv OrcRwkv;
+/* NULL on a missing file, a bad header or a short/long body. */
+OrcRwkv*  orc_rwkv_load(const char* path, int profile);
+void      orc_rwkv_free(OrcRwkv* m);
+/* vocab, d_model, n_head, head_size, n_layer, d_ffn, lora w/a/v/g ranks, g1k */
+void      orc_rwkv_dims(const OrcRwkv* m, uint32_t out[11]);
+int       orc_rwkv_pool_init(OrcRwkv* m, uint32_t cap);
+int       orc_rwkv_reset(OrcRwkv* m, const uint32_t* slots, uint32_t n);
+void      orc_rwkv_set_reset_every(OrcRwkv* m, uint64_t every);
+int       orc_rwkv_forward(OrcRwkv* m, uint32_t n, const uint32_t* slots, const uint32_t* tokens,
+                           float* out_logits);
+/* A slot's state of one layer: token-shift inputs of the two mixers (d_model each) and
+ * the WKV matrices [n_head][head_size][head_size] (row i, column j as the reference). */
+int       orc_rwkv_get_state(const OrcRwkv* m, uint32_t slot, uint32_t layer, float* x_att, float* wkv,
+                             float* x_ffn);
+
 /* ---- thread pool used by both models ---- */
 void orc_set_threads(int n);
 int  orc_get_threads(void);

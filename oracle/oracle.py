@@ -13,7 +13,9 @@ from typing import Optional, Sequence
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "liboracle.so")
+# ORACLE_LIB names another build of the same sources (the tests use it to load a build
+# with a planted mistake in a child process).
+LIB_PATH = os.environ.get("ORACLE_LIB") or os.path.join(HERE, "liboracle.so")
 
 _u32p = ctypes.POINTER(ctypes.c_uint32)
 _f32p = ctypes.POINTER(ctypes.c_float)
@@ -56,6 +58,26 @@ def lib() -> ctypes.CDLL:
         L.orc_mamba_forward.argtypes = [ctypes.c_void_p, ctypes.c_uint32, _u32p, _u32p, _f32p]
         L.orc_mamba_get_state.argtypes = [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32, _f32p, _f32p]
         L.orc_mamba_dequant.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_uint32, _f32p]
+        L.orc_rwkv_load.argtypes = [ctypes.c_char_p, ctypes.c_int]
+        L.orc_rwkv_load.restype = ctypes.c_void_p
+        L.orc_rwkv_free.argtypes = [ctypes.c_void_p]
+        L.orc_rwkv_dims.argtypes = [ctypes.c_void_p, _u32p]
+        L.orc_rwkv_pool_init.argtypes = [ctypes.c_void_p, ctypes.c_uint32]
+        L.orc_rwkv_reset.argtypes = [ctypes.c_void_p, _u32p, ctypes.c_uint32]
+        L.orc_rwkv_set_reset_every.argtypes = [ctypes.c_void_p, ctypes.c_uint64]
+        L.orc_rwkv_forward.argtypes = [ctypes.c_void_p, ctypes.c_uint32, _u32p, _u32p, _f32p]
+        L.orc_rwkv_get_state.argtypes = [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32, _f32p, _f32p, _f32p]
+        for name in ("orc_tanh_inplace", "orc_sigmoid_inplace"):
+            getattr(L, name).argtypes = [_f32p, ctypes.c_int]
+        for name in ("orc_sigmoid_add_into", "orc_decay_sigmoid_into"):
+            getattr(L, name).argtypes = [_f32p, _f32p, _f32p, ctypes.c_int]
+        L.orc_sigmoid_mix_inplace.argtypes = [_f32p, _f32p, _f32p, _f32p, ctypes.c_int]
+        L.orc_group_norm_into.argtypes = [_f32p, _f32p, ctypes.c_int, _f32p, _f32p, ctypes.c_int, ctypes.c_float]
+        L.orc_l2_normalize_per_head.argtypes = [_f32p, ctypes.c_int, ctypes.c_int]
+        L.orc_mat_vec_small.argtypes = [_f32p, _f32p, _f32p, ctypes.c_int]
+        L.orc_wkv_head.argtypes = [_f32p, ctypes.c_int] + [_f32p] * 8
+        L.orc_lane_sigmoidf.argtypes = [ctypes.c_float]
+        L.orc_lane_sigmoidf.restype = ctypes.c_float
         L.orc_set_threads.argtypes = [ctypes.c_int]
         L.orc_get_threads.restype = ctypes.c_int
         _lib = L
@@ -225,3 +247,63 @@ class MambaOracle:
             self.close()
         except Exception:
             pass
+
+
+class RwkvOracle:
+    """An RWKV-7 model on the CPU oracle with a pool of `cap` stream slots."""
+
+    def __init__(self, path: str, profile: int = 0, cap: int = 1):
+        self.h = lib().orc_rwkv_load(path.encode(), profile)
+        if not self.h:
+            raise RuntimeError(f"oracle load failed: {path}")
+        d = np.zeros(11, np.uint32)
+        lib().orc_rwkv_dims(self.h, _p(d, ctypes.c_uint32))
+        (self.vocab, self.d_model, self.n_head, self.head_size, self.n_layer, self.d_ffn, self.lora_w, self.lora_a,
+         self.lora_v, self.lora_g, self.g1k) = (int(x) for x in d)
+        self.cap = 0
+        self.pool_init(cap)
+
+    def pool_init(self, cap: int) -> None:
+        if lib().orc_rwkv_pool_init(self.h, cap) != 0:
+            raise MemoryError("oracle pool")
+        self.cap = cap
+
+    def set_reset_every(self, every: int) -> None:
+        lib().orc_rwkv_set_reset_every(self.h, every)
+
+    def reset(self, slots: Optional[Sequence[int]] = None) -> None:
+        if slots is None:
+            lib().orc_rwkv_reset(self.h, None, 0)
+        else:
+            s = np.ascontiguousarray(slots, dtype=np.uint32)
+            if lib().orc_rwkv_reset(self.h, _p(s, ctypes.c_uint32), s.size) != 0:
+                raise ValueError("bad slot")
+
+    def forward(self, slots: Sequence[int], tokens: Sequence[int]) -> np.ndarray:
+        s = np.ascontiguousarray(slots, dtype=np.uint32)
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        out = np.empty((s.size, self.vocab), np.float32)
+        rc = lib().orc_rwkv_forward(self.h, s.size, _p(s, ctypes.c_uint32), _p(t, ctypes.c_uint32), _p(out))
+        if rc != 0:
+            raise ValueError(f"oracle forward rc={rc}")
+        return out
+
+    def state(self, slot: int, layer: int):
+        d, hs = self.d_model, self.head_size
+        xa, xf = np.empty(d, np.float32), np.empty(d, np.float32)
+        wkv = np.empty((self.n_head, hs, hs), np.float32)
+        if lib().orc_rwkv_get_state(self.h, slot, layer, _p(xa), _p(wkv), _p(xf)) != 0:
+            raise ValueError("bad slot/layer")
+        return xa, wkv, xf
+
+    def close(self) -> None:
+        if self.h:
+            lib().orc_rwkv_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
