@@ -133,7 +133,9 @@ void* redukt_backend_stream(void);
  * two hipEvent_t taken in order from events[0..n_events) (caller owned, alive while
  * probing); recording stops when they run out.  Classes: 1 embed,
  * 2 mix_in (norm + in_proj + conv + x_proj partials), 3 scan (dt_proj + selective scan +
- * gate), 4 mix_out (out_proj + residual), 5 head (final norm + LM head), 6 softmax.
+ * gate), 4 mix_out (out_proj + residual), 5 head (final norm + LM head), 6 softmax;
+ * RWKV-7: 7 shift (LayerNorm + token shift), 8 proj (matrix-core projections), 9 wkv (WKV-7
+ * with GroupNorm, bonus and gate), plus 1, 5, 6.
  * Probed launches record their own dispatch start and stop (hipExtLaunchKernel), and
  * probed steps are launched kernel by kernel instead of from the step's hipGraph.
  * With REDUKT_PROBE_CLASS_ONLY or'ed into kernel_class, a probed step launches only the
@@ -149,6 +151,13 @@ uint32_t redukt_backend_probe_used(void);
 /* Copy the recurrent state of one batch-pool slot and layer to host memory:
  * conv (d_inner*(d_conv-1) f32), ssm (d_inner*d_state f32); either may be NULL. */
 int32_t redukt_backend_get_state(uint32_t slot, uint32_t layer, float* conv_out, float* ssm_out);
+
+/* RWKV-7 models (weights in the RWKV-7 container: .rbin header with version 3, model 2).
+ * The state of one batch-pool slot and layer (Rwkv7State, src/infrastructure/rwkv7/
+ * model.rs:115-141): the two token-shift inputs (d_model f32 each) and the WKV-7 matrices
+ * [n_head][head_size][head_size] (row i, column j); any pointer may be NULL.
+ * INVALID_ARGUMENT for a Mamba model. */
+int32_t redukt_backend_get_rwkv_state(uint32_t slot, uint32_t layer, float* x_att, float* wkv, float* x_ffn);
 
 #ifdef __cplusplus
 }

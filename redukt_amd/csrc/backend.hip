@@ -37,9 +37,17 @@ constexpr uint32_t kFlagNormBias = 1u << 0;
 constexpr uint32_t kFlagUntiedHead = 1u << 1;
 constexpr int kMaxCols = 1024;  // d_model: activations of 32 streams staged in LDS, dt_rank in registers
 
+enum ModelKind : uint32_t { kKindNone = 0, kKindMamba = 1, kKindRwkv = 2 };
+
 struct Model {
     bool ready = false;
-    Dims dims;
+    uint32_t kind = kKindNone;
+    Dims dims;                  // Mamba dims; for RWKV-7 only vocab, d and nl are set
+    RDims rdims;                // RWKV-7
+    std::vector<RLayer> rlayers;
+    TMat r_emb, r_head;
+    float* ln_out_w = nullptr;
+    float* ln_out_b = nullptr;
     uint32_t profile = 0;
     std::vector<DLayer> layers;
     TMat emb, head_own;
@@ -254,13 +262,109 @@ int load_weights(const std::string& path, uint32_t profile) {
     return ok ? 0 : -1;
 }
 
+// RWKV-7 container (redukt_amd/rwkv.py): 16-word header (magic, version 3, model 2,
+// vocab, d_model, n_head, head_size, n_layer, d_ffn, four LoRA ranks, flags, tokenizer,
+// 0), then the f32 tensors in that module's order.  Quantized profiles apply the Q8
+// recipe to receptance, key, value, output, FFN key/value and the head; the embedding
+// and the LoRAs stay F32 (src/infrastructure/rwkv7/model.rs:997-1059).
+int load_rwkv(const std::string& path, uint32_t profile) {
+    FILE* f = fopen(path.c_str(), "rb");
+    if (!f) {
+        log("cannot open: %s", path.c_str());
+        return -1;
+    }
+    uint32_t h[16];
+    Reader rd{f};
+    bool hdr_ok = fread(h, 4, 16, f) == 16 && h[0] == kRbinMagic && h[1] == 3 && h[2] == 2;
+    // Kernel limits: 64-wide heads; d_model in whole 64-column k-pairs, at most 1024.
+    hdr_ok = hdr_ok && h[3] && h[4] == h[5] * h[6] && h[6] == 64 && h[4] % 64 == 0 && h[4] <= 1024 && h[7] &&
+             h[8] && h[8] % 16 == 0 && h[9] && h[10] && h[11] && h[12] && h[9] <= 512 && h[10] <= 512 &&
+             h[11] <= 512 && h[12] <= 512 && h[14] <= 1;
+    if (!hdr_ok) {
+        log("bad/unsupported RWKV-7 header in %s", path.c_str());
+        fclose(f);
+        return -1;
+    }
+    RDims& R = G.rdims;
+    R.vocab = h[3]; R.d = h[4]; R.h = h[5]; R.n = h[6]; R.nl = h[7]; R.f = h[8];
+    R.lora[kLoraW] = h[9]; R.lora[kLoraA] = h[10]; R.lora[kLoraV] = h[11]; R.lora[kLoraG] = h[12];
+    R.g1k = h[13] & 1u;
+    G.dims = Dims{};
+    G.dims.vocab = R.vocab;
+    G.dims.d = R.d;
+    G.dims.nl = R.nl;
+    G.dims.tokenizer = h[14];
+    const int quant = (profile & 3) == 0 ? 0 : ((profile & 3) == 1 ? 64 : (int)0x7fffffff);
+    auto qgroup = [&](int cols) { return quant == 0 ? 0 : (quant == 0x7fffffff ? cols : quant); };
+    const size_t V = R.vocab, d = R.d, ff = R.f;
+    log("rwkv7: d=%u heads=%u x %u layers=%u d_ffn=%u lora=%u/%u/%u/%u vocab=%u g1k=%u profile=%u", R.d, R.h, R.n,
+        R.nl, R.f, R.lora[kLoraW], R.lora[kLoraA], R.lora[kLoraV], R.lora[kLoraG], R.vocab, R.g1k, profile);
+    bool ok = true;
+    auto vec = [&](float*& dst) {
+        std::vector<float> t = rd.read(d);
+        ok = ok && rd.ok && (dst = dev_upload(t.data(), d)) != nullptr;
+    };
+    auto mat = [&](TMat& m, size_t rows, size_t cols, int group) {
+        std::vector<float> t = rd.read(rows * cols);
+        ok = ok && rd.ok && make_tmat(m, t.data(), (int)rows, (int)cols, group);
+    };
+    mat(G.r_emb, V, d, 0);
+    G.rlayers.assign(R.nl, RLayer{});
+    for (uint32_t i = 0; ok && i < R.nl; i++) {
+        RLayer& L = G.rlayers[i];
+        vec(L.ln1_w); vec(L.ln1_b); vec(L.ln2_w); vec(L.ln2_b);
+        for (int k = 0; k < 6; k++) vec(L.mix[k]);
+        vec(L.w0);
+        mat(L.l1[kLoraW], R.lora[kLoraW], d, 0);
+        mat(L.l2[kLoraW], d, R.lora[kLoraW], 0);
+        vec(L.a0);
+        mat(L.l1[kLoraA], R.lora[kLoraA], d, 0);
+        mat(L.l2[kLoraA], d, R.lora[kLoraA], 0);
+        vec(L.v0);
+        mat(L.l1[kLoraV], R.lora[kLoraV], d, 0);
+        mat(L.l2[kLoraV], d, R.lora[kLoraV], 0);
+        mat(L.l1[kLoraG], R.lora[kLoraG], d, 0);
+        mat(L.l2[kLoraG], d, R.lora[kLoraG], 0);
+        vec(L.k_k); vec(L.k_a); vec(L.r_k);
+        mat(L.r, d, d, qgroup((int)d));
+        mat(L.k, d, d, qgroup((int)d));
+        mat(L.v, d, d, qgroup((int)d));
+        mat(L.o, d, d, qgroup((int)d));
+        vec(L.ln_x_w); vec(L.ln_x_b); vec(L.ffn_x_k);
+        mat(L.fk, ff, d, qgroup((int)d));
+        mat(L.fv, d, ff, qgroup((int)ff));
+        if (ok && ((i + 1) % 4 == 0 || i + 1 == R.nl)) log("loaded layer %u/%u", i + 1, R.nl);
+    }
+    vec(G.ln_out_w);
+    vec(G.ln_out_b);
+    mat(G.r_head, V, d, qgroup((int)d));
+    if (ok) {
+        char extra;
+        ok = fread(&extra, 1, 1, f) == 0;
+    }
+    fclose(f);
+    return ok ? 0 : -1;
+}
+
+// Model kind from the first header words: "RGPU" version 3 model 2 is RWKV-7, anything
+// else goes to the .rbin (Mamba) reader.
+uint32_t file_kind(const std::string& path) {
+    FILE* f = fopen(path.c_str(), "rb");
+    if (!f) return kKindMamba;
+    uint32_t h[3] = {0, 0, 0};
+    const bool got = fread(h, 4, 3, f) == 3;
+    fclose(f);
+    return got && h[0] == kRbinMagic && h[1] == 3 && h[2] == 2 ? kKindRwkv : kKindMamba;
+}
+
 void dev_free_all() {
     for (void* p : G.allocs) (void)hipFree(p);
     G.allocs.clear();
 }
 
 void pool_free(Pool& p) {
-    void* bufs[] = {p.conv, p.ssm, p.x, p.u, p.z, p.xpart, p.glimb, p.xw, p.ssp, p.out, p.slots, p.d_slots, p.d_tokens};
+    void* bufs[] = {p.conv, p.ssm, p.x, p.u, p.z, p.xpart, p.glimb, p.xw, p.ssp, p.out, p.slots, p.d_slots, p.d_tokens,
+                    p.x_att, p.x_ffn, p.wkv, p.vfirst, p.rkv, p.lorad, p.mixl, p.loral, p.gatedl, p.ffnl, p.actl, p.headl};
     for (void* b : bufs) (void)hipFree(b);
     if (p.h_slots) (void)hipHostFree(p.h_slots);
     if (p.h_tokens) (void)hipHostFree(p.h_tokens);
@@ -277,7 +381,27 @@ bool dev_zero(T*& p, size_t count) {
     return hipMemset(p, 0, sizeof(T) * (count ? count : 1)) == hipSuccess;
 }
 
+bool pool_alloc_rwkv(Pool& p, uint32_t cap) {
+    const RDims& R = G.rdims;
+    const size_t n = cap, d = R.d;
+    const RwkvSizes z = rwkv_sizes(R, cap);
+    p = Pool{};
+    p.cap = cap;
+    p.gcap = (cap + 15) / 16;
+    bool ok = dev_zero(p.x, n * d) && dev_zero(p.x_att, z.state_d) && dev_zero(p.x_ffn, z.state_d) &&
+              dev_zero(p.wkv, z.wkv) && dev_zero(p.vfirst, n * d) && dev_zero(p.rkv, n * 3 * d) &&
+              dev_zero(p.lorad, n * 4 * d) && dev_zero(p.mixl, 6 * z.mixl) && dev_zero(p.loral, z.loral) &&
+              dev_zero(p.gatedl, z.gatedl) && dev_zero(p.ffnl, z.mixl) && dev_zero(p.actl, z.actl) &&
+              dev_zero(p.headl, z.mixl) && dev_zero(p.out, n * R.vocab) && dev_zero(p.slots, n) &&
+              dev_zero(p.d_slots, n) && dev_zero(p.d_tokens, n);
+    ok = ok && hipHostMalloc((void**)&p.h_slots, sizeof(uint32_t) * n, hipHostMallocDefault) == hipSuccess;
+    ok = ok && hipHostMalloc((void**)&p.h_tokens, sizeof(uint32_t) * n, hipHostMallocDefault) == hipSuccess;
+    ok = ok && (p.seen = (uint8_t*)calloc(n, 1)) != nullptr;
+    return ok;
+}
+
 bool pool_alloc(Pool& p, uint32_t cap) {
+    if (G.kind == kKindRwkv) return pool_alloc_rwkv(p, cap);
     const Dims& D = G.dims;
     const size_t n = cap, d = D.d, di = D.di;
     p = Pool{};
@@ -312,7 +436,12 @@ ModelView model_view() {
 hipError_t run_step(Pool& p, uint32_t n, const uint32_t* slots, const uint32_t* tokens, float* out, bool probs,
                     bool check) {
     StepIO io{n, slots, tokens, out, probs, check, G.d_err};
-    return G.runner.run(model_view(), p, io, G.stream, &G.probe);
+    if (G.kind == kKindRwkv) {
+        const RwkvStep src(RwkvView{&G.rdims, G.rlayers.data(), &G.r_emb, &G.r_head, G.ln_out_w, G.ln_out_b});
+        return G.runner.run(src, p, io, G.stream, &G.probe);
+    }
+    const MambaStep src(model_view());
+    return G.runner.run(src, p, io, G.stream, &G.probe);
 }
 
 // pool_forward semantics (mamba_cuda.cu:604-635): validate on the host (nothing is
@@ -349,7 +478,9 @@ int pool_reset(Pool& p, uint32_t n, const uint32_t* slots) {
     for (uint32_t b = 0; b < n; b++) p.h_slots[b] = slots ? slots[b] : b;
     if (hipMemcpyAsync(p.d_slots, p.h_slots, sizeof(uint32_t) * n, hipMemcpyHostToDevice, G.stream) != hipSuccess)
         return BACKEND_FORWARD_FAILED;
-    if (enqueue_reset(G.dims, p, p.d_slots, n, G.stream) != hipSuccess) return BACKEND_FORWARD_FAILED;
+    const hipError_t e = G.kind == kKindRwkv ? enqueue_reset_rwkv(G.rdims, p, p.d_slots, n, G.stream)
+                                             : enqueue_reset(G.dims, p, p.d_slots, n, G.stream);
+    if (e != hipSuccess) return BACKEND_FORWARD_FAILED;
     if (hipStreamSynchronize(G.stream) != hipSuccess) return BACKEND_FORWARD_FAILED;
     return BACKEND_OK;
 }
@@ -383,7 +514,8 @@ int init_common(const uint8_t* weights_path, int32_t device_id, uint32_t profile
         return BACKEND_INIT_FAILED;
     }
     G.profile = profile;
-    if (load_weights(path, profile) != 0) {
+    G.kind = file_kind(path);
+    if ((G.kind == kKindRwkv ? load_rwkv(path, profile) : load_weights(path, profile)) != 0) {
         free_model();
         return BACKEND_WEIGHTS_NOT_FOUND;
     }
@@ -397,8 +529,9 @@ int init_common(const uint8_t* weights_path, int32_t device_id, uint32_t profile
     info_out->ffi_version = BACKEND_FFI_VERSION;
     info_out->vocab_size = G.dims.vocab;
     info_out->hidden_dim = G.dims.d;
-    static const char* names[] = {"hip-gfx950-mamba-f32", "hip-gfx950-mamba-q8", "hip-gfx950-mamba-q8row"};
-    const char* name = names[profile & 3];
+    static const char* names[2][3] = {{"hip-gfx950-mamba-f32", "hip-gfx950-mamba-q8", "hip-gfx950-mamba-q8row"},
+                                       {"hip-gfx950-rwkv7-f32", "hip-gfx950-rwkv7-q8", "hip-gfx950-rwkv7-q8row"}};
+    const char* name = names[G.kind == kKindRwkv ? 1 : 0][profile & 3];
     memcpy(info_out->name, name, strlen(name));
     size_t fr = 0, tot = 0;
     (void)hipMemGetInfo(&fr, &tot);
@@ -530,8 +663,24 @@ int32_t redukt_backend_probe_kernel(uint32_t kernel_class, void** events, uint32
 
 uint32_t redukt_backend_probe_used(void) { return G.probe.used; }
 
+int32_t redukt_backend_get_rwkv_state(uint32_t slot, uint32_t layer, float* x_att, float* wkv, float* x_ffn) {
+    if (!G.ready || G.batch.cap == 0) return BACKEND_INIT_FAILED;
+    if (G.kind != kKindRwkv || slot >= G.batch.cap || layer >= G.rdims.nl) return BACKEND_INVALID_ARGUMENT;
+    if (hipStreamSynchronize(G.stream) != hipSuccess) return BACKEND_FORWARD_FAILED;
+    const RDims& R = G.rdims;
+    const size_t d = R.d, wl = (size_t)R.h * R.n * R.n, row = (size_t)slot * R.nl + layer;
+    const Pool& p = G.batch;
+    if (x_att && hipMemcpy(x_att, p.x_att + row * d, d * 4, hipMemcpyDeviceToHost) != hipSuccess)
+        return BACKEND_FORWARD_FAILED;
+    if (wkv && hipMemcpy(wkv, p.wkv + row * wl, wl * 4, hipMemcpyDeviceToHost) != hipSuccess) return BACKEND_FORWARD_FAILED;
+    if (x_ffn && hipMemcpy(x_ffn, p.x_ffn + row * d, d * 4, hipMemcpyDeviceToHost) != hipSuccess)
+        return BACKEND_FORWARD_FAILED;
+    return BACKEND_OK;
+}
+
 int32_t redukt_backend_get_state(uint32_t slot, uint32_t layer, float* conv_out, float* ssm_out) {
     if (!G.ready || G.batch.cap == 0) return BACKEND_INIT_FAILED;
+    if (G.kind != kKindMamba) return BACKEND_INVALID_ARGUMENT;
     if (slot >= G.batch.cap || layer >= G.dims.nl) return BACKEND_INVALID_ARGUMENT;
     if (hipStreamSynchronize(G.stream) != hipSuccess) return BACKEND_FORWARD_FAILED;
     const size_t cl = (size_t)G.dims.di * (G.dims.dc - 1), sl = (size_t)G.dims.di * 16;

@@ -37,8 +37,10 @@
 #include <cstring>
 #include <memory>
 
+#include "mfma_common.h"
 #include "model.h"
 #include "portable_math.h"
+#include "step.h"
 
 #pragma clang fp contract(off)
 
@@ -64,10 +66,6 @@ size_t ssp_floats(const Dims& d, uint32_t cap) { return (size_t)cap * (d.d / kRo
 
 namespace {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-constexpr int kWave = 64;
 constexpr int kBlock = 256;
 constexpr int kWaves = kBlock / kWave;
 constexpr int kChunk = 32;                 // streams per k_head workgroup
@@ -76,7 +74,6 @@ constexpr int kInGroups = 1;               // column groups per k_mix_in workgro
 constexpr int kInChunk = kInGroups * kRowTile;
 constexpr int kOutGroups = 1;              // column groups per k_mix_out workgroup
 constexpr int kOutChunk = kOutGroups * kRowTile;
-constexpr int kLimbBytes = 64 * 8 * 2;     // one B fragment of one limb: 1 KB
 constexpr int kHeadTiles = 4;              // row tiles per wave in k_head
 // Weight k-pairs each wave keeps in flight (the product loop is unrolled by it): k_mix_in
 // holds its whole quarter of four Q8 row tiles of a d <= 1024 projection, k_head four
@@ -90,110 +87,6 @@ constexpr int kMaxXr = kMaxDr + 32;        // x_proj rows
 constexpr int kMaxNxb = 32;                // d_inner / 64 (d_inner <= 2048)
 constexpr int kOutWaves = 8;               // waves of k_mix_out
 constexpr int kOutPairs = 3;               // k-pairs per k_mix_out wave per pass
-
-__device__ __forceinline__ f32x4 mma(const bf16x8& a, const bf16x8& b, const f32x4& c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
-
-struct Limb3 {
-    __bf16 h, m, l;
-};
-
-// v = h + m + l: h = bf16(v), m = bf16(v - h), l = bf16(v - h - m); both differences are
-// exact in f32, so only the last rounding (below 2^-24 relative) is lost.
-__device__ __forceinline__ Limb3 split3(float v) {
-    Limb3 o;
-    o.h = (__bf16)v;
-    const float r = v - (float)o.h;
-    o.m = (__bf16)r;
-    o.l = (__bf16)(r - (float)o.m);
-    return o;
-}
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-    return v;
-}
-
-__device__ __forceinline__ uint32_t clamp_slot(uint32_t s, uint32_t cap) { return s < cap ? s : cap - 1; }
-
-// ---------------------------------------------------------------- weight fragments
-
-// The A operand of one k-step: F32 weights as three limbs, Q8 weights as one exact one.
-struct AFrag {
-    bf16x8 h, m, l;
-};
-
-// Raw bytes of the fragments of k-steps [2p, 2p+2) of one lane: Q8 16 B, F32 64 B.
-struct RawPair {
-    int4 v[4];
-};
-
-template <bool Q8>
-__device__ __forceinline__ RawPair load_pair(const TMat& w, int t, int p, int lane) {
-    RawPair r;
-    if (Q8) {
-        r.v[0] = ((const int4*)w.w)[((size_t)t * (w.ks / 2) + p) * 64 + lane];
-    } else {
-        const int4* base = (const int4*)w.w;
-#pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const size_t f = (((size_t)t * w.ks + 2 * p + h) * 64 + lane) * 2;
-            r.v[2 * h] = base[f];
-            r.v[2 * h + 1] = base[f + 1];
-        }
-    }
-    return r;
-}
-
-template <bool Q8>
-__device__ __forceinline__ void decode_pair(const RawPair& r, AFrag& a0, AFrag& a1) {
-    if (Q8) {
-        const int w[4] = {r.v[0].x, r.v[0].y, r.v[0].z, r.v[0].w};
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            a0.h[j] = (__bf16)(float)(int8_t)(w[j / 4] >> (8 * (j % 4)));
-            a1.h[j] = (__bf16)(float)(int8_t)(w[2 + j / 4] >> (8 * (j % 4)));
-        }
-    } else {
-#pragma unroll
-        for (int h = 0; h < 2; h++) {
-            AFrag& a = h ? a1 : a0;
-            const int4 lo = r.v[2 * h], hi = r.v[2 * h + 1];
-            const int w[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const Limb3 t = split3(bits_to_f((uint32_t)w[j]));
-                a.h[j] = t.h;
-                a.m[j] = t.m;
-                a.l[j] = t.l;
-            }
-        }
-    }
-}
-
-// acc += A * B for one k-step: Q8 three products (B limbs hi, mid, lo), F32 the six limb
-// products hi*hi, hi*mid, mid*hi, hi*lo, mid*mid, lo*hi — always in this order.
-template <bool Q8>
-__device__ __forceinline__ f32x4 mma_step(const AFrag& a, const bf16x8& bh, const bf16x8& bm, const bf16x8& bl,
-                                          f32x4 acc) {
-    if (Q8) {
-        acc = mma(a.h, bh, acc);
-        acc = mma(a.h, bm, acc);
-        acc = mma(a.h, bl, acc);
-    } else {
-        acc = mma(a.h, bh, acc);
-        acc = mma(a.h, bm, acc);
-        acc = mma(a.m, bh, acc);
-        acc = mma(a.h, bl, acc);
-        acc = mma(a.m, bm, acc);
-        acc = mma(a.l, bh, acc);
-    }
-    return acc;
-}
-
-__device__ __forceinline__ bf16x8 lds_frag(const __bf16* base) { return *(const bf16x8*)base; }
 
 // ---------------------------------------------------------------- activation staging
 
@@ -318,7 +211,6 @@ __device__ void stage_normed(__bf16* lds, const float* __restrict__ x, const flo
 // Copy of groups [g0, g0 + ng): contiguous in xw and in LDS, 1 KB per wave instruction
 // (global_load_lds of 16 bytes per lane: lane i lands at LDS base + 16 i).  The caller
 // waits for vmcnt(0) and syncs before reading.
-typedef __attribute__((address_space(3))) unsigned char lds_u8;
 
 __device__ __forceinline__ void stage_copy(unsigned char* lds, const __bf16* __restrict__ xw, uint32_t g0, int ng,
                                            int ks) {
@@ -396,27 +288,18 @@ __device__ __forceinline__ void ssp_reduce(const SspLoad& r, float* invs, int ti
 __device__ __forceinline__ void produce_tile(__bf16* __restrict__ xw, float* __restrict__ ssp, int ks, int tiles,
                                              int t, uint32_t b, bool ok, const float (&xv)[4], const float4& w4) {
     const int lane = threadIdx.x % kWave;
-    typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
     const float wv[4] = {w4.x, w4.y, w4.z, w4.w};
-    bf16x4 h, m, l;
+    float v[4];
     float ss = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const Limb3 t3 = split3(xv[i] * wv[i]);
-        h[i] = t3.h;
-        m[i] = t3.m;
-        l[i] = t3.l;
+        v[i] = xv[i] * wv[i];
         ss += xv[i] * xv[i];
     }
     ss += __shfl_xor(ss, 16, kWave);
     ss += __shfl_xor(ss, 32, kWave);
     if (!ok) return;
-    const int rr = (t % 2) * kRowTile + (lane / 16) * 4;  // row within k-step t / 2
-    const int ln = (int)(b % kRowTile) + kRowTile * (rr / 8);
-    __bf16* dst = xw + ((((size_t)(b / kRowTile) * ks + t / 2) * 3) * 64 + ln) * 8 + rr % 8;
-    *(bf16x4*)dst = h;
-    *(bf16x4*)(dst + 512) = m;
-    *(bf16x4*)(dst + 1024) = l;
+    write_limbs4(xw, ks, t, b, v);
     if (lane < 16) ssp[(size_t)b * tiles + t] = ss;
 }
 
@@ -1387,13 +1270,14 @@ __global__ __launch_bounds__(kHwWaves * kWave) void k_head_ws(HeadArgs a) {
     float ssv[kSspPerThread];
     const int sb = threadIdx.x / kTps, ssub = threadIdx.x % kTps;  // 64 streams per pass, two passes
     float ssv2[kSspPerThread];
+    const bool rms = a.ssp != nullptr;  // else the activations arrive normed (scale 1)
     {
         const uint32_t b1 = gb * kRowTile + sb, b2 = b1 + 64;
 #pragma unroll
         for (int i = 0; i < kSspPerThread; i++) {
             const int t = ssub + kTps * i;
-            ssv[i] = b1 < a.n && t < a.tiles ? a.ssp[(size_t)b1 * a.tiles + t] : 0.0f;
-            ssv2[i] = b2 < a.n && t < a.tiles ? a.ssp[(size_t)b2 * a.tiles + t] : 0.0f;
+            ssv[i] = rms && b1 < a.n && t < a.tiles ? a.ssp[(size_t)b1 * a.tiles + t] : 0.0f;
+            ssv2[i] = rms && b2 < a.n && t < a.tiles ? a.ssp[(size_t)b2 * a.tiles + t] : 0.0f;
         }
     }
     int4 wq[NP][kHwTiles];
@@ -1421,8 +1305,8 @@ __global__ __launch_bounds__(kHwWaves * kWave) void k_head_ws(HeadArgs a) {
             s2 += __shfl_xor(s2, o, kWave);
         }
         if (ssub == 0) {
-            invs[sb] = 1.0f / sqrtf(s1 / (float)a.d + 1e-5f);
-            invs[sb + 64] = 1.0f / sqrtf(s2 / (float)a.d + 1e-5f);
+            invs[sb] = rms ? 1.0f / sqrtf(s1 / (float)a.d + 1e-5f) : 1.0f;
+            invs[sb + 64] = rms ? 1.0f / sqrtf(s2 / (float)a.d + 1e-5f) : 1.0f;
         }
     }
     AFrag wd[NP][kHwTiles][2];
@@ -1548,27 +1432,6 @@ __global__ __launch_bounds__(kBlock) void k_zero_slots(ZeroArgs a) {
 
 }  // namespace
 
-struct Launch {
-    const void* fn;
-    dim3 grid, block;
-    uint32_t lds;
-    uint32_t cls;
-    std::unique_ptr<unsigned char[]> args;
-    void* argp;
-    template <typename A>
-    static Launch make(const void* fn, dim3 g, dim3 b, uint32_t lds, uint32_t cls, const A& a) {
-        Launch l;
-        l.fn = fn;
-        l.grid = g;
-        l.block = b;
-        l.lds = lds;
-        l.cls = cls;
-        l.args.reset(new unsigned char[sizeof(A)]);
-        memcpy(l.args.get(), &a, sizeof(A));
-        l.argp = l.args.get();
-        return l;
-    }
-};
 
 namespace {
 
@@ -1581,15 +1444,6 @@ uint32_t mix_in_lds_bytes(int ks) {
     const uint32_t quarters = kWaves * kWaves * kInGroups * kWave * sizeof(f32x4);
     const uint32_t xp_operand = kInGroups * 2 * 3 * kLimbBytes;
     return std::max(acts, std::max(quarters, xp_operand));
-}
-
-template <typename K>
-void allow_lds(K* fn, uint32_t bytes) {
-    static uint32_t set = 0;
-    if (bytes > set) {
-        (void)hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
-        set = bytes;
-    }
 }
 
 template <bool Q8, bool Q8XP, bool PRE, bool GRP>
@@ -1634,6 +1488,41 @@ const void* head_ws_fn(int np, uint32_t lds) {
     return nullptr;
 }
 
+}  // namespace
+
+Launch embed_launch(const TMat& emb, Pool& p, const StepIO& io, const float* nw0, __bf16* xw, float* ssp, int ks_x,
+                    int tiles) {
+    const int d = emb.cols;
+    EmbedArgs ea{emb, p.x, io.tokens, io.slots, p.slots, io.n, p.cap, io.check ? 1 : 0, io.err, nw0, xw, ssp, ks_x, tiles};
+    return Launch::make((const void*)k_embed, dim3((d + 4 * kBlock - 1) / (4 * kBlock), io.n), dim3(kBlock), 0, KC_EMBED,
+                        ea);
+}
+
+Launch head_launch(const TMat& H, Pool& p, const StepIO& io, const float* x, const float* nw, const float* nb,
+                   const __bf16* xw, const float* ssp, int d, int tiles, bool ws) {
+    const uint32_t n = io.n;
+    HeadArgs ha{x, nw, nb, H, io.out, n, d, xw, ssp, tiles};
+    if (ws) {
+        const uint32_t lds_h = 2 * (uint32_t)H.ks * 3 * kLimbBytes;
+        const int tiles_per_block = kHwWaves * kHwTiles;
+        const uint32_t groups = (n + kRowTile - 1) / kRowTile;
+        return Launch::make(head_ws_fn(H.ks / 2, lds_h),
+                            dim3((H.rt + tiles_per_block - 1) / tiles_per_block, (groups + kHwGroups - 1) / kHwGroups),
+                            dim3(kHwWaves * kWave), lds_h, KC_HEAD, ha);
+    }
+    const uint32_t lds_h = stage_lds_bytes(H.ks);
+    const int tiles_per_block = kWaves * kHeadTiles;
+    return Launch::make(head_fn(H.group != 0, xw != nullptr, lds_h),
+                        dim3((H.rt + tiles_per_block - 1) / tiles_per_block, (n + kChunk - 1) / kChunk), dim3(kBlock),
+                        lds_h, KC_HEAD, ha);
+}
+
+Launch softmax_launch(float* out, int vocab, uint32_t n) {
+    return Launch::make((const void*)k_softmax, dim3(n), dim3(1024), 0, KC_SOFTMAX, SoftmaxArgs{out, vocab});
+}
+
+namespace {
+
 // The launches of one step, in stream order; io_index / head_index / softmax_index name
 // the launches whose arguments carry caller pointers.
 void build_step(const ModelView& m, Pool& p, const StepIO& io, std::vector<Launch>& out, int& io_index,
@@ -1651,11 +1540,8 @@ void build_step(const ModelView& m, Pool& p, const StepIO& io, std::vector<Launc
     // consumer.
     const bool pre = m.layers[0].norm_b == nullptr && m.norm_f_b == nullptr;
     const int ks_x = m.layers[0].in_x.ks, tiles = d / kRowTile;
-    EmbedArgs ea{*m.emb, p.x, io.tokens, io.slots, p.slots, n, p.cap, io.check ? 1 : 0, io.err,
-                 m.layers[0].norm_w, pre ? p.xw : nullptr, p.ssp, ks_x, tiles};
     io_index = (int)out.size();
-    out.push_back(Launch::make((const void*)k_embed, dim3((d + 4 * kBlock - 1) / (4 * kBlock), n), dim3(kBlock), 0,
-                               KC_EMBED, ea));
+    out.push_back(embed_launch(*m.emb, p, io, m.layers[0].norm_w, pre ? p.xw : nullptr, p.ssp, ks_x, tiles));
     const size_t conv_layer = (size_t)p.cap * di * (D.dc - 1);
     const size_t ssm_layer = (size_t)p.cap * di * 16;
     const bool q8 = m.layers[0].in_x.group != 0;
@@ -1680,28 +1566,13 @@ void build_step(const ModelView& m, Pool& p, const StepIO& io, std::vector<Launc
         out.push_back(Launch::make(fo, dim3(L.out_proj.rt, out_chunks), dim3(kOutWaves * kWave), 0, KC_MIX_OUT, oa));
     }
     const TMat& H = *m.head;
-    HeadArgs ha{p.x, m.norm_f_w, m.norm_f_b, H, io.out, n, d, p.xw, p.ssp, tiles};
     head_index = (int)out.size();
     const bool ws = pre && H.group != 0 && H.group == H.cols && H.ks / 2 <= 12;
-    if (ws) {
-        const uint32_t lds_h = 2 * (uint32_t)H.ks * 3 * kLimbBytes;
-        const int tiles_per_block = kHwWaves * kHwTiles;
-        const uint32_t groups = (n + kRowTile - 1) / kRowTile;
-        out.push_back(Launch::make(head_ws_fn(H.ks / 2, lds_h),
-                                   dim3((H.rt + tiles_per_block - 1) / tiles_per_block, (groups + kHwGroups - 1) / kHwGroups),
-                                   dim3(kHwWaves * kWave), lds_h, KC_HEAD, ha));
-    } else {
-        const uint32_t lds_h = stage_lds_bytes(H.ks);
-        const int tiles_per_block = kWaves * kHeadTiles;
-        out.push_back(Launch::make(head_fn(H.group != 0, pre, lds_h),
-                                   dim3((H.rt + tiles_per_block - 1) / tiles_per_block, chunks), dim3(kBlock), lds_h,
-                                   KC_HEAD, ha));
-    }
+    out.push_back(head_launch(H, p, io, p.x, m.norm_f_w, m.norm_f_b, pre ? p.xw : nullptr, p.ssp, d, tiles, ws));
     softmax_index = -1;
     if (io.probs) {
         softmax_index = (int)out.size();
-        out.push_back(Launch::make((const void*)k_softmax, dim3(n), dim3(1024), 0, KC_SOFTMAX,
-                                   SoftmaxArgs{io.out, (int)D.vocab}));
+        out.push_back(softmax_launch(io.out, (int)D.vocab, n));
     }
 }
 
@@ -1792,11 +1663,15 @@ hipError_t StepRunner::capture(const std::vector<Launch>& seq, int io_i, int hea
     return hipGraphInstantiate(&g.exec, graph, nullptr, nullptr, 0);
 }
 
-hipError_t StepRunner::run(const ModelView& m, Pool& p, const StepIO& io, hipStream_t st, Probe* probe) {
+void MambaStep::build(Pool& p, const StepIO& io, std::vector<Launch>& out, int& io_i, int& head_i, int& sm_i) const {
+    build_step(m, p, io, out, io_i, head_i, sm_i);
+}
+
+hipError_t StepRunner::run(const StepSource& src, Pool& p, const StepIO& io, hipStream_t st, Probe* probe) {
     std::unique_ptr<std::vector<Launch>> owned(new std::vector<Launch>());
     std::vector<Launch>& seq = *owned;
     int io_i = -1, head_i = -1, sm_i = -1;
-    build_step(m, p, io, seq, io_i, head_i, sm_i);
+    src.build(p, io, seq, io_i, head_i, sm_i);
     if (probe && probe->cls != KC_NONE && probe->only) {
         const bool rec = probe->used + 2 <= probe->cap;
         if (rec) RDK_TRY(hipEventRecord(probe->ev[probe->used], st));
@@ -1880,6 +1755,21 @@ hipError_t StepRunner::run(const ModelView& m, Pool& p, const StepIO& io, hipStr
     hit->err = io.err;
     hit->last_use = ++clock_;
     return hipGraphLaunch(hit->exec, st);
+}
+
+// Rwkv7State::reset (rwkv7/model.rs:135-140) for the listed slots: both token-shift
+// inputs and the WKV matrices of every layer (each slot's block is contiguous).
+hipError_t enqueue_reset_rwkv(const RDims& D, Pool& P, const uint32_t* d_slots, uint32_t n, hipStream_t st) {
+    if (n == 0) return hipSuccess;
+    const size_t sd = (size_t)D.nl * D.d, sw = (size_t)D.nl * D.h * D.n * D.n;
+    float* bases[3] = {P.x_att, P.x_ffn, P.wkv};
+    const size_t strides[3] = {sd, sd, sw};
+    for (int i = 0; i < 3; i++) {
+        ZeroArgs z{bases[i], d_slots, P.cap, strides[i], 0, 1};
+        k_zero_slots<<<dim3((unsigned)std::min<size_t>((strides[i] + kBlock - 1) / kBlock, 4096), n), kBlock, 0, st>>>(z);
+        RDK_TRY(hipGetLastError());
+    }
+    return hipSuccess;
 }
 
 hipError_t enqueue_reset(const Dims& D, Pool& P, const uint32_t* d_slots, uint32_t n, hipStream_t st) {

@@ -75,6 +75,19 @@ struct Pool {
     // x^2, [cap][d/16], from which the consumer forms the RMS scale of each stream.
     __bf16* xw = nullptr;
     float* ssp = nullptr;
+    // RWKV-7 (allocated for RWKV-7 models only)
+    float* x_att = nullptr;      // [slot][layer][d] time-mix token-shift input (ln1 output)
+    float* x_ffn = nullptr;      // [slot][layer][d] channel-mix token-shift input (ln2 output)
+    float* wkv = nullptr;        // [slot][layer][head][i][j] WKV-7 state, row i, column j
+    float* vfirst = nullptr;     // [cap][d] layer-0 value of the current token, per batch position
+    float* rkv = nullptr;        // [cap][3d] receptance, key, value
+    float* lorad = nullptr;      // [cap][4d] second LoRA stages: decay, a, g, v
+    __bf16* mixl = nullptr;      // 6 x [gcap][ks_d][3][64][8]: x_r, x_w, x_k, x_v, x_a, x_g inputs
+    __bf16* loral = nullptr;     // 4 x [gcap][ks_lora][3][64][8]: tanh(w1·x), a1·x, sigmoid(g1·x), v1·x
+    __bf16* gatedl = nullptr;    // [gcap][ks_d][3][64][8] gated WKV output
+    __bf16* ffnl = nullptr;      // [gcap][ks_d][3][64][8] channel-mix input
+    __bf16* actl = nullptr;      // [gcap][ks_ffn][3][64][8] squared-ReLU activations
+    __bf16* headl = nullptr;     // [gcap][ks_d][3][64][8] final LayerNorm output
     float* out = nullptr;        // [cap][vocab] logits or probabilities
     uint32_t* slots = nullptr;   // [cap] slots of the current step (validated copy)
     uint32_t* d_slots = nullptr; // [cap] H2D staging targets of the synchronous entry points
@@ -87,7 +100,9 @@ struct Pool {
 // Kernel classes a caller can time with HIP events (see Probe).
 enum KernelClass : uint32_t {
     KC_NONE = 0, KC_EMBED = 1, KC_MIX_IN = 2, KC_SCAN = 3, KC_MIX_OUT = 4, KC_HEAD = 5, KC_SOFTMAX = 6,
-    KC_COUNT = 7
+    // RWKV-7: LayerNorm + token shift, matrix-core projections, WKV-7 (with GroupNorm, bonus, gate)
+    KC_SHIFT = 7, KC_PROJ = 8, KC_WKV = 9,
+    KC_COUNT = 10
 };
 
 // Measurement hook: while cls != KC_NONE, every launch of that class records its dispatch
@@ -100,6 +115,42 @@ struct Probe {
     hipEvent_t* ev = nullptr;
     uint32_t cap = 0, used = 0;
 };
+
+// RWKV-7 (src/infrastructure/rwkv7/model.rs:14-141).
+struct RDims {
+    uint32_t vocab = 0, d = 0, h = 0, n = 0, nl = 0, f = 0;
+    uint32_t lora[4] = {0, 0, 0, 0};   // ranks of the decay (w), a, g and v LoRAs
+    uint32_t g1k = 0;
+};
+
+enum { kLoraW = 0, kLoraA = 1, kLoraG = 2, kLoraV = 3 };
+
+struct RLayer {
+    float *ln1_w = nullptr, *ln1_b = nullptr, *ln2_w = nullptr, *ln2_b = nullptr;
+    float* mix[6] = {};               // x_r, x_w, x_k, x_v, x_a, x_g
+    float *w0 = nullptr, *a0 = nullptr, *v0 = nullptr, *k_k = nullptr, *k_a = nullptr, *r_k = nullptr;
+    float *ln_x_w = nullptr, *ln_x_b = nullptr, *ffn_x_k = nullptr;
+    TMat r, k, v, o;                  // [d][d]
+    TMat l1[4];                       // first LoRA stages [rank][d] (F32): w1, a1, g1, v1
+    TMat l2[4];                       // second LoRA stages [d][rank] (F32): w2, a2, g2, v2
+    TMat fk, fv;                      // [d_ffn][d], [d][d_ffn]
+};
+
+struct RwkvView {
+    const RDims* dims;
+    const RLayer* layers;
+    const TMat* emb;       // [vocab][d] F32, already through ln0
+    const TMat* head;      // [vocab][d]
+    const float* ln_out_w;
+    const float* ln_out_b;
+};
+
+// Scratch and state sizes of an RWKV-7 pool of `cap` streams (elements).
+struct RwkvSizes {
+    size_t state_d, wkv, mixl, loral, lora_off[4], gatedl, actl;
+    int ks_d, ks_f, ks_lora[4];
+};
+RwkvSizes rwkv_sizes(const RDims& d, uint32_t cap);
 
 struct ModelView {
     const Dims* dims;
@@ -126,13 +177,33 @@ struct StepIO {
 // recorded once as a hipGraph and replayed.
 struct Launch;
 
+// Builds the launch list of one step of a model; io_i / head_i / sm_i name the launches
+// whose arguments carry the caller's pointers (embedding, head, softmax; -1 if absent).
+struct StepSource {
+    virtual ~StepSource() = default;
+    virtual void build(Pool& p, const StepIO& io, std::vector<Launch>& out, int& io_i, int& head_i,
+                       int& sm_i) const = 0;
+};
+
+struct MambaStep final : StepSource {
+    ModelView m;
+    explicit MambaStep(const ModelView& v) : m(v) {}
+    void build(Pool& p, const StepIO& io, std::vector<Launch>& out, int& io_i, int& head_i, int& sm_i) const override;
+};
+
+struct RwkvStep final : StepSource {
+    RwkvView m;
+    explicit RwkvStep(const RwkvView& v) : m(v) {}
+    void build(Pool& p, const StepIO& io, std::vector<Launch>& out, int& io_i, int& head_i, int& sm_i) const override;
+};
+
 class StepRunner {
 public:
     ~StepRunner();
     // Issue one step.  Builds (or reuses) the graph of this shape unless a probe is
     // active, in which case the step is launched directly with events around the probed
     // class.  Returns hipSuccess or the first error.
-    hipError_t run(const ModelView& m, Pool& p, const StepIO& io, hipStream_t st, Probe* probe);
+    hipError_t run(const StepSource& src, Pool& p, const StepIO& io, hipStream_t st, Probe* probe);
     void clear();
 
 private:
@@ -162,6 +233,7 @@ private:
 // Zero the state of the n slots listed in d_slots (device).  Uses no memset, so it is
 // safe under stream capture.
 hipError_t enqueue_reset(const Dims& dims, Pool& pool, const uint32_t* d_slots, uint32_t n, hipStream_t stream);
+hipError_t enqueue_reset_rwkv(const RDims& dims, Pool& pool, const uint32_t* d_slots, uint32_t n, hipStream_t stream);
 
 // Scratch sizes of a pool of `cap` streams.
 size_t xpart_floats(const Dims& d, uint32_t cap);

@@ -1,0 +1,62 @@
+// step.h — a step as a list of kernel launches (issued directly or recorded as a graph).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cstring>
+#include <memory>
+
+namespace rdk {
+
+struct Launch {
+    const void* fn;
+    dim3 grid, block;
+    uint32_t lds;
+    uint32_t cls;
+    std::unique_ptr<unsigned char[]> args;
+    void* argp;
+    template <typename A>
+    static Launch make(const void* fn, dim3 g, dim3 b, uint32_t lds, uint32_t cls, const A& a) {
+        Launch l;
+        l.fn = fn;
+        l.grid = g;
+        l.block = b;
+        l.lds = lds;
+        l.cls = cls;
+        l.args.reset(new unsigned char[sizeof(A)]);
+        memcpy(l.args.get(), &a, sizeof(A));
+        l.argp = l.args.get();
+        return l;
+    }
+};
+
+struct TMat;
+struct Pool;
+struct StepIO;
+
+// Launches shared by the step builders of both models (kernels in mamba_step.hip).
+// embed: x = emb[token] with the device argument check; with xw, the pre-staged
+// activations of the first RMSNorm consumer.  head: ws selects the weights-stationary
+// head (Q8 per-row, activations pre-staged in xw; ssp null = already normed); otherwise
+// the streamed head norms x itself (LayerNorm when nb is given, RMSNorm otherwise, or
+// pre-staged xw/ssp).
+Launch embed_launch(const TMat& emb, Pool& p, const StepIO& io, const float* nw0, __bf16* xw, float* ssp, int ks_x,
+                    int tiles);
+Launch head_launch(const TMat& H, Pool& p, const StepIO& io, const float* x, const float* nw, const float* nb,
+                   const __bf16* xw, const float* ssp, int d, int tiles, bool ws);
+Launch softmax_launch(float* out, int vocab, uint32_t n);
+
+namespace {
+
+template <typename K>
+void allow_lds(K* fn, uint32_t bytes) {
+    static uint32_t set = 0;
+    if (bytes > set) {
+        (void)hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+        set = bytes;
+    }
+}
+
+}  // namespace
+}  // namespace rdk

@@ -39,11 +39,12 @@ V2_SYMBOLS = ("redukt_backend_abi_version", "redukt_backend_batch_init", "redukt
               "redukt_backend_forward_batch")
 V3_SYMBOLS = ("redukt_backend_init_ex", "redukt_backend_forward_batch_probs", "redukt_backend_forward_batch_device",
               "redukt_backend_device_status", "redukt_backend_stream", "redukt_backend_get_state",
-              "redukt_backend_probe_kernel", "redukt_backend_probe_used")
+              "redukt_backend_probe_kernel", "redukt_backend_probe_used", "redukt_backend_get_rwkv_state")
 
 # Kernel classes of redukt_backend_probe_kernel, and the flag that makes a probed step
 # launch only the kernels of that class (REDUKT_PROBE_CLASS_ONLY).
 KERNEL_CLASSES = {"embed": 1, "mix_in": 2, "scan": 3, "mix_out": 4, "head": 5, "softmax": 6}
+RWKV_KERNEL_CLASSES = {"embed": 1, "shift": 7, "proj": 8, "wkv": 9, "head": 5, "softmax": 6}
 PROBE_CLASS_ONLY = 0x100
 
 
@@ -144,6 +145,8 @@ class PluginLibrary:
             L.redukt_backend_stream.restype = ctypes.c_void_p
             L.redukt_backend_get_state.argtypes = [ctypes.c_uint32, ctypes.c_uint32, _f32p, _f32p]
             L.redukt_backend_get_state.restype = ctypes.c_int32
+            L.redukt_backend_get_rwkv_state.argtypes = [ctypes.c_uint32, ctypes.c_uint32, _f32p, _f32p, _f32p]
+            L.redukt_backend_get_rwkv_state.restype = ctypes.c_int32
             L.redukt_backend_probe_kernel.argtypes = [ctypes.c_uint32, ctypes.c_void_p, ctypes.c_uint32]
             L.redukt_backend_probe_kernel.restype = ctypes.c_int32
             L.redukt_backend_probe_used.argtypes = []
@@ -331,6 +334,15 @@ class PluginBackend:
 
     def stream(self) -> int:
         return int(self.lib.lib.redukt_backend_stream() or 0)
+
+    def get_rwkv_state(self, slot: int, layer: int, d_model: int, n_head: int, head_size: int = 64):
+        xa, xf = np.empty(d_model, np.float32), np.empty(d_model, np.float32)
+        wkv = np.empty((n_head, head_size, head_size), np.float32)
+        res = BackendResult.from_code(self.lib.lib.redukt_backend_get_rwkv_state(
+            slot, layer, _ptr(xa, ctypes.c_float), _ptr(wkv, ctypes.c_float), _ptr(xf, ctypes.c_float)))
+        if res != BackendResult.OK:
+            raise BackendError(res, "get_rwkv_state")
+        return xa, wkv, xf
 
     def get_state(self, slot: int, layer: int, d_inner: int, d_conv: int, d_state: int = 16):
         conv = np.empty(d_inner * (d_conv - 1), np.float32)

@@ -165,7 +165,7 @@ def test_wkv_head_against_matrix_form():
 
 @pytest.fixture(scope="module")
 def small_model(tmp_path_factory):
-    p = str(tmp_path_factory.mktemp("rwkv") / "small.rwkv")
+    p = str(tmp_path_factory.mktemp("rwkv") / "small.rbin")
     rwkv.write_synthetic(p, SMALL, seed=1)
     return p
 
@@ -309,7 +309,7 @@ def test_container_round_trip_and_header(small_model, tmp_path):
     bad = bytearray(head)
     bad[8] = 1                                   # model word != RWKV-7
     assert rwkv.parse_header(bytes(bad)) is None
-    short = tmp_path / "short.rwkv"
+    short = tmp_path / "short.rbin"
     short.write_bytes(open(small_model, "rb").read()[:-4])
     with pytest.raises(RuntimeError):
         O.RwkvOracle(str(short), 0)
