@@ -28,7 +28,7 @@ import numpy as np
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-from redukt_amd import ffi, hip, rbin, synth  # noqa: E402
+from redukt_amd import ffi, hip, rbin, rwkv, synth  # noqa: E402
 
 METRIC = "Mamba-130M tok/s at batch 1/32/128 (F32 & Q8); % of HBM roofline"
 HBM_PEAK_GBS = 8000.0
@@ -91,6 +91,59 @@ def step_bytes(dims: rbin.MambaDims, profile: int, n: int) -> int:
     return w + small + n * (state + dims.vocab * 4 + d * 4)
 
 
+def launches_per_step(dims, name: str, mamba: bool, profile: int) -> int:
+    L = dims.n_layer
+    if mamba:
+        return L if name in ("mix_in", "scan", "mix_out") else 1
+    ws = (profile & 3) == 2 and dims.d_model <= 768       # the weights-stationary head needs ln_out staged
+    return {"shift": 2 * L + (1 if ws else 0), "proj": 5 * L, "wkv": L}.get(name, 1)
+
+
+def rwkv_weight_bytes(dims, profile: int) -> dict:
+    d, f, V = dims.d_model, dims.d_ffn, dims.vocab
+    q = profile & 3
+
+    def mat(rows, cols):
+        if not q:
+            return rows * cols * 4
+        g = cols if q == 2 else (64 if cols % 64 == 0 else cols)
+        return rows * cols + rows * (cols // g) * 4
+
+    ranks = dims.lora_w + dims.lora_a + dims.lora_v + dims.lora_g
+    per_layer = 4 * mat(d, d) + mat(f, d) + mat(d, f) + 2 * d * ranks * 4
+    return {"proj": dims.n_layer * per_layer, "head": mat(V, d), "emb_row": d * 4}
+
+
+def rwkv_algorithmic_bytes(dims, profile: int, n: int) -> dict:
+    """Compulsory HBM bytes per launch of each RWKV-7 kernel class at n streams (the step's
+    bytes of that class over its launches): weights once, activations and state read or
+    written once at f32."""
+    d, f, V, L, H = dims.d_model, dims.d_ffn, dims.vocab, dims.n_layer, dims.n_head
+    w = rwkv_weight_bytes(dims, profile)
+    R = dims.lora_w + dims.lora_a + dims.lora_v + dims.lora_g
+    ws = (profile & 3) == 2 and d <= 768
+    proj = w["proj"] + n * L * 4 * (7 * d + 3 * d + 2 * R + 4 * d + 3 * d + d + f + f + 2 * d)
+    wkv = L * (n * (2 * H * 64 * 64 * 4 + 8 * d * 4 + 2 * d * 4) + 9 * d * 4)
+    shift = n * d * 4 * (L * (1 + 2 + 6) + L * (1 + 2 + 1) + (2 if ws else 0))
+    return {"embed": n * (w["emb_row"] + d * 4), "proj": proj // (5 * L), "wkv": wkv // L,
+            "shift": shift // (2 * L + (1 if ws else 0)), "head": w["head"] + n * d * 4 + n * V * 4,
+            "softmax": 2 * n * V * 4}
+
+
+def rwkv_step_bytes(dims, profile: int, n: int) -> int:
+    d, V, L, H = dims.d_model, dims.vocab, dims.n_layer, dims.n_head
+    w = rwkv_weight_bytes(dims, profile)
+    state = L * (2 * d + H * 64 * 64) * 4 * 2
+    return w["proj"] + w["head"] + L * 16 * d * 4 + n * (state + V * 4 + d * 4)
+
+
+def ensure_rwkv(path: str) -> str:
+    if not (os.path.isfile(path) and os.path.getsize(path) == rwkv.file_bytes(rwkv.RWKV7_0_1B)):
+        log(f"writing synthetic RWKV-7 0.1B weights to {path}")
+        rwkv.write_synthetic(path, rwkv.RWKV7_0_1B, seed=0)
+    return path
+
+
 def ensure_model(path: str) -> str:
     dims = rbin.MAMBA_130M
     expect = 44 + 4 * sum(int(np.prod(s)) for _, s in rbin.tensor_order(dims))
@@ -100,12 +153,12 @@ def ensure_model(path: str) -> str:
     return path
 
 
-def cpu_baseline(path: str, profile: int, n: int, tokens: np.ndarray, budget_s: float) -> dict:
+def cpu_baseline(path: str, profile: int, n: int, tokens: np.ndarray, budget_s: float, mamba: bool = True) -> dict:
     from oracle import oracle as O   # the CPU restatement; test/baseline infrastructure only
 
     threads = min(os.cpu_count() or 1, 16)
     O.set_threads(threads)
-    m = O.MambaOracle(path, profile, cap=n)
+    m = O.MambaOracle(path, profile, cap=n) if mamba else O.RwkvOracle(path, profile, cap=n)
     slots = list(range(n))
     m.forward(slots, [int(x) for x in tokens[0]])          # warm-up step
     t0 = time.perf_counter()
@@ -127,7 +180,9 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1024)
     ap.add_argument("--warmup", type=int, default=32)
-    ap.add_argument("--streams", type=int, default=32)
+    ap.add_argument("--streams", type=int, default=None, help="default 32 (Mamba), 64 (RWKV-7)")
+    ap.add_argument("--arch", default="mamba130m", choices=["mamba130m", "rwkv7-0.1b"],
+                    help="rwkv7-0.1b: RWKV-7 0.1B, uniform byte-level tokens (not the headline metric)")
     ap.add_argument("--profile", default="q8row-all", choices=sorted(PROFILES))
     ap.add_argument("--probe-steps", type=int, default=8)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
@@ -135,7 +190,7 @@ def main() -> int:
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="after the probe pass, copy this many MiB device to device on the library's "
                          "stream (a copy of known size for scaling HBM byte counters)")
-    ap.add_argument("--model", default=os.path.join(tempfile.gettempdir(), "redukt_bench", "mamba130m.rbin"))
+    ap.add_argument("--model", default=None, help="weight file (written with synthetic weights if absent)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -147,20 +202,29 @@ def main() -> int:
         print("bench.py: no GPU visible", file=sys.stderr)
         return 1
 
-    n, K, W = args.streams, args.steps, args.warmup
+    mamba = args.arch == "mamba130m"
+    n = args.streams or (32 if mamba else 64)
+    K, W = args.steps, args.warmup
     profile = PROFILES[args.profile]
-    dims = rbin.MAMBA_130M
-    path = ensure_model(args.model)
     rng = np.random.default_rng(1234)
     total = W + K + args.probe_steps + 1
-    tokens = synth.zipf_tokens(rng, dims.vocab, (total, n))
+    if mamba:
+        dims = rbin.MAMBA_130M
+        path = ensure_model(args.model or os.path.join(tempfile.gettempdir(), "redukt_bench", "mamba130m.rbin"))
+        tokens = synth.zipf_tokens(rng, dims.vocab, (total, n))
+        vocab, workload = dims.vocab, f"mamba130m-{args.profile}-n{n}-zipf1.1"
+    else:
+        dims = rwkv.RWKV7_0_1B
+        path = ensure_rwkv(args.model or os.path.join(tempfile.gettempdir(), "redukt_bench", "rwkv7_0_1b.rbin"))
+        tokens = rng.integers(0, 256, size=(total, n), dtype=np.uint32)   # byte-level ids
+        vocab, workload = dims.vocab, f"rwkv7-0.1b-{args.profile}-n{n}-bytes"
 
     be = ffi.PluginBackend(path, 0, profile)
     be.batch_init(n)
     stream = be.stream()
     d_tokens = hip.DeviceBuffer.from_array(tokens)
     d_slots = hip.DeviceBuffer.from_array(np.arange(n, dtype=np.uint32))
-    d_out = hip.DeviceBuffer(n * dims.vocab * 4)
+    d_out = hip.DeviceBuffer(n * vocab * 4)
     row = n * 4
 
     # Every stream starts at forward number `since0`, so the 4096-token boundary (reset
@@ -218,15 +282,16 @@ def main() -> int:
             e.close()
         return durs
 
-    for name, cls in ffi.KERNEL_CLASSES.items():
+    classes = ffi.KERNEL_CLASSES if mamba else ffi.RWKV_KERNEL_CLASSES
+    for name, cls in classes.items():
         if name == "softmax":
             continue
-        launches = dims.n_layer if name in ("mix_in", "scan", "mix_out") else 1
+        launches = launches_per_step(dims, name, mamba, profile)
         only = probe(cls | ffi.PROBE_CLASS_ONLY, 2 * P)
         each = probe(cls, 2 * launches * P)
         per_class[name] = {"avg_us": float(np.mean(only)) / launches, "launches_per_step": launches,
                            "us_per_step": float(np.mean(only)), "dispatch_avg_us": round(float(np.mean(each)), 2)}
-    alg = algorithmic_bytes(dims, profile, n)
+    alg = algorithmic_bytes(dims, profile, n) if mamba else rwkv_algorithmic_bytes(dims, profile, n)
     dom = max(per_class, key=lambda k: per_class[k]["us_per_step"])
     avg_s = per_class[dom]["avg_us"] / 1e6
     achieved = alg[dom] / avg_s / 1e9
@@ -247,7 +312,7 @@ def main() -> int:
         dst.close()
 
     # FFI end-to-end rate (host buffers, D2H of n rows of logits, synchronous).
-    out = np.empty((n, dims.vocab), np.float32)
+    out = np.empty((n, vocab), np.float32)
     slots = list(range(n))
     f_steps = min(64, K)
     be.forward_batch(slots, [int(x) for x in tokens[0]], out)
@@ -262,22 +327,21 @@ def main() -> int:
     cpu = None
     if not args.no_cpu_baseline:
         log("timing the CPU oracle on the host cores")
-        cpu = cpu_baseline(path, profile, n, tokens, args.cpu_seconds)
+        cpu = cpu_baseline(path, profile, n, tokens, args.cpu_seconds, mamba)
 
     # HBM bytes per launch of the dominant kernel from the committed counter passes
     # (FETCH_SIZE / WRITE_SIZE scaled by a copy of known size), when they cover this workload.
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "hbm_traffic.json")
-    workload = f"mamba130m-{args.profile}-n{n}-zipf1.1"
     if os.path.exists(tpath):
         with open(tpath) as f:
             tj = json.load(f)
         if tj.get("workload") == workload:
             traffic = tj["bytes_per_launch"].get(dom)
 
-    sb = step_bytes(dims, profile, n)
+    sb = step_bytes(dims, profile, n) if mamba else rwkv_step_bytes(dims, profile, n)
     result = {
-        "metric": METRIC,
+        "metric": METRIC if mamba else "RWKV-7 0.1B tok/s (lockstep streams, byte-level tokens)",
         "value": round(tok_s, 1),
         "unit": "tok/s",
         "n_gpus": 1,
@@ -290,7 +354,7 @@ def main() -> int:
         "dtype": "f32",
         "data": "synthetic",
         "config": {"workload": workload, "layers": dims.n_layer,
-                   "d_model": dims.d_model, "vocab": dims.vocab, "streams": n, "weight_profile": args.profile,
+                   "d_model": dims.d_model, "vocab": vocab, "streams": n, "weight_profile": args.profile,
                    "reset_every": RESET_PERIOD, "reset_at_timed_step": reset_step, "parallelism": "none"},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic},
