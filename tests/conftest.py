@@ -1,6 +1,8 @@
 import os
 import sys
 
+import pytest
+
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
@@ -8,3 +10,14 @@ if ROOT not in sys.path:
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU; calls the HIP library through the C ABI")
+
+
+@pytest.fixture(scope="session")
+def full_model(tmp_path_factory):
+    """Mamba-130M (d 768, 24 layers, vocab 50280) with synthetic seed-0 weights, shared by
+    every GPU module of the session."""
+    from redukt_amd import rbin, synth
+
+    p = str(tmp_path_factory.mktemp("mamba130m") / "model.rbin")
+    synth.write_synthetic_mamba(p, rbin.MAMBA_130M, seed=0)
+    return p

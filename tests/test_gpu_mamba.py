@@ -54,13 +54,6 @@ def models(tmp_path_factory):
     return out
 
 
-@pytest.fixture(scope="session")
-def full_model(tmp_path_factory):
-    p = str(tmp_path_factory.mktemp("mamba130m") / "model.rbin")
-    synth.write_synthetic_mamba(p, rbin.MAMBA_130M, seed=0)
-    return p
-
-
 def run_lockstep(backend, oracle, n, steps, tok_fn, cap=None):
     backend.batch_init(cap or n)
     outs = []
