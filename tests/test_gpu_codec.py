@@ -8,8 +8,6 @@ lockstep driver of libredukt_host.so).
 * The CDFs coded from the GPU's logits are the oracle's CDFs of those same logits, bit
   for bit (src/application/codec.rs:785-798).
 """
-import dataclasses
-
 import numpy as np
 import pytest
 
