@@ -249,8 +249,8 @@ int32_t redukt_lockstep::run_lockstep(const Job& job, redukt_lockstep_stats& sta
         if (!resets.empty() && api.batch_reset(resets.data(), uint32_t(resets.size())) != BACKEND_OK)
             return REDUKT_LOCKSTEP_FORWARD;
         if (!fwd_slots.empty() &&
-            api.forward_batch(uint32_t(fwd_slots.size()), fwd_slots.data(), fwd_tokens.data(), logits.data(),
-                              uint32_t(size_t(fwd_slots.size()) * vocab)) != BACKEND_OK)
+            api.forward_batch(uint32_t(fwd_slots.size()), fwd_slots.data(), fwd_tokens.data(), logits.data(), vocab) !=
+                BACKEND_OK)
             return REDUKT_LOCKSTEP_FORWARD;
         stats.forward_secs += since(tb);
         ++stats.steps;

@@ -94,11 +94,16 @@ int32_t redukt_backend_batch_reset(const uint32_t* slots, uint32_t n) {
     return 0;
 }
 
+/* vocab_size is the vocabulary (out holds n * vocab_size floats), as in the v2 ABI
+ * (src/domain/backend_ffi.rs:148-162); slots must be distinct. */
 int32_t redukt_backend_forward_batch(uint32_t n, const uint32_t* slots, const uint32_t* toks, float* out,
-                                     uint32_t out_len) {
-    if ((uint64_t)n * g_vocab != out_len) return 5;
-    for (uint32_t i = 0; i < n; ++i)
+                                     uint32_t vocab_size) {
+    if (vocab_size != g_vocab || n > g_cap) return 5;
+    for (uint32_t i = 0; i < n; ++i) {
         if (slots[i] >= g_cap || toks[i] >= g_vocab) return 5;
+        for (uint32_t j = 0; j < i; ++j)
+            if (slots[j] == slots[i]) return 5;
+    }
     for (uint32_t i = 0; i < n; ++i) {
         g_slot[slots[i]] = step(g_slot[slots[i]], toks[i]);
         logits_of(g_slot[slots[i]], out + (size_t)i * g_vocab);
