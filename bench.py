@@ -184,6 +184,8 @@ def main() -> int:
     ap.add_argument("--arch", default="mamba130m", choices=["mamba130m", "rwkv7-0.1b"],
                     help="rwkv7-0.1b: RWKV-7 0.1B, uniform byte-level tokens (not the headline metric)")
     ap.add_argument("--profile", default="q8row-all", choices=sorted(PROFILES))
+    ap.add_argument("--exact-scan", action="store_true",
+                    help="Mamba scan decay factors by the reference's portable exp (profile bit 3)")
     ap.add_argument("--probe-steps", type=int, default=8)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -205,14 +207,15 @@ def main() -> int:
     mamba = args.arch == "mamba130m"
     n = args.streams or (32 if mamba else 64)
     K, W = args.steps, args.warmup
-    profile = PROFILES[args.profile]
+    profile = PROFILES[args.profile] | (ffi.PROFILE_EXACT_SCAN if args.exact_scan else 0)
     rng = np.random.default_rng(1234)
     total = W + K + args.probe_steps + 1
     if mamba:
         dims = rbin.MAMBA_130M
         path = ensure_model(args.model or os.path.join(tempfile.gettempdir(), "redukt_bench", "mamba130m.rbin"))
         tokens = synth.zipf_tokens(rng, dims.vocab, (total, n))
-        vocab, workload = dims.vocab, f"mamba130m-{args.profile}-n{n}-zipf1.1"
+        exact = "-exactscan" if args.exact_scan else ""
+        vocab, workload = dims.vocab, f"mamba130m-{args.profile}{exact}-n{n}-zipf1.1"
     else:
         dims = rwkv.RWKV7_0_1B
         path = ensure_rwkv(args.model or os.path.join(tempfile.gettempdir(), "redukt_bench", "rwkv7_0_1b.rbin"))

@@ -100,6 +100,10 @@ int32_t redukt_backend_forward_batch(uint32_t n_streams, const uint32_t* slots, 
 #define BACKEND_PROFILE_Q8_G64 1u
 #define BACKEND_PROFILE_Q8_ROW 2u
 #define BACKEND_PROFILE_Q8_SMALL 4u
+/* Profile bit 3: the Mamba scan's decay factors exp(-dt*A) by the reference's portable
+ * exp (bit-identical element-wise scan) instead of the hardware exp2 (about 1e-7
+ * relative; the default).  REDUKT_GPU_EXACT_SCAN=1 sets it for redukt_backend_init. */
+#define BACKEND_PROFILE_EXACT_SCAN 8u
 
 /* redukt_backend_init with an explicit weight profile (the model file stays F32). */
 int32_t redukt_backend_init_ex(const uint8_t* weights_path, int32_t device_id, uint32_t profile,

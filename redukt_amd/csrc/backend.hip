@@ -430,7 +430,8 @@ void free_model() {
 }
 
 ModelView model_view() {
-    return ModelView{&G.dims, G.layers.data(), &G.emb, G.tied ? &G.emb : &G.head_own, G.norm_f_w, G.norm_f_b};
+    return ModelView{&G.dims, G.layers.data(), &G.emb, G.tied ? &G.emb : &G.head_own, G.norm_f_w, G.norm_f_b,
+                     (G.profile & BACKEND_PROFILE_EXACT_SCAN) != 0};
 }
 
 hipError_t run_step(Pool& p, uint32_t n, const uint32_t* slots, const uint32_t* tokens, float* out, bool probs,
@@ -491,14 +492,19 @@ std::string rbin_path(const uint8_t* weights_path) {
     return p;
 }
 
-uint32_t env_profile() {
+uint32_t env_weight_profile() {
     const char* e = getenv("REDUKT_GPU_PROFILE");
     if (!e || !*e || !strcmp(e, "f32")) return BACKEND_PROFILE_F32;
     if (!strcmp(e, "q8")) return BACKEND_PROFILE_Q8_G64;
     if (!strcmp(e, "q8row")) return BACKEND_PROFILE_Q8_ROW;
     if (!strcmp(e, "q8row-all")) return BACKEND_PROFILE_Q8_ROW | BACKEND_PROFILE_Q8_SMALL;
     if (!strcmp(e, "q8-all")) return BACKEND_PROFILE_Q8_G64 | BACKEND_PROFILE_Q8_SMALL;
-    return (uint32_t)strtoul(e, nullptr, 0) & 7u;
+    return (uint32_t)strtoul(e, nullptr, 0) & 15u;
+}
+
+uint32_t env_profile() {
+    const char* x = getenv("REDUKT_GPU_EXACT_SCAN");
+    return env_weight_profile() | (x && *x && strcmp(x, "0") ? BACKEND_PROFILE_EXACT_SCAN : 0u);
 }
 
 int init_common(const uint8_t* weights_path, int32_t device_id, uint32_t profile, BackendInfo* info_out) {
@@ -609,7 +615,7 @@ int32_t redukt_backend_forward_batch(uint32_t n_streams, const uint32_t* slots, 
 
 int32_t redukt_backend_init_ex(const uint8_t* weights_path, int32_t device_id, uint32_t profile,
                                BackendInfo* info_out) {
-    if (profile > 7u) return BACKEND_INVALID_ARGUMENT;
+    if (profile > 15u) return BACKEND_INVALID_ARGUMENT;
     return init_common(weights_path, device_id, profile, info_out);
 }
 

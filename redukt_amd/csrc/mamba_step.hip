@@ -865,28 +865,27 @@ struct ScanArgs {
     int di, dr;
 };
 
-// dot_avx2_order (tensor.rs:1680-1693) over one column of the transposed dt_proj.
-template <typename T>
-__device__ __forceinline__ float dot_ref_col(const T* __restrict__ wt, int stride, const float* v, int n) {
-    const int body = n / 8 * 8;
-    float l[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int c = 0; c < body; c += 8)
-#pragma unroll
-        for (int i = 0; i < 8; i++) l[i] += (float)wt[(size_t)(c + i) * stride] * v[c + i];
-    float s = ((l[0] + l[4]) + (l[2] + l[6])) + ((l[1] + l[5]) + (l[3] + l[7]));
-    for (int c = body; c < n; c++) s += (float)wt[(size_t)c * stride] * v[c];
-    return s;
-}
-
 // scan_block (model.rs:174-190) for one (stream, channel): x_proj row sums, dt_proj row in
 // the reference order, softplus(dt + b) (tensor.rs:859-861), the d16 recurrence with the
 // dt-sparse skip and the hsum_ssm tree (tensor.rs:1283-1325), y * (z * sigmoid(z))
 // (tensor.rs:1239-1243 on 64-channel blocks); the gated value leaves as bf16 limbs.
 // Every operand is requested before the first wait.
-template <bool Q8DT>
+//
+// FAST takes the 16 decay factors exp(-dt * A[n]) from the hardware exp2 (v_exp_f32, on
+// x * log2 e; about 1e-7 relative) instead of the reference's portable exp, which is
+// about 30 VALU operations each and most of this kernel's instruction stream.  Every
+// other element-wise operation keeps the reference's arithmetic.  DR and NXB fix dt_rank
+// and the number of 64-channel x_proj blocks at compile time (0: taken from the
+// arguments, bounded by kMaxDr / kMaxNxb), which removes the guards of the unrolled loops.
+__device__ __forceinline__ float hw_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
+
+template <bool Q8DT, bool FAST, int DR, int NXB>
 __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
+    static_assert(DR >= 0 && DR <= kMaxDr && NXB >= 0 && NXB <= kMaxNxb, "scan shape");
     __shared__ float zp[kMaxXr];
-    const int di = a.di, dr = a.dr;
+    constexpr int kDr = DR ? DR : kMaxDr;
+    constexpr int kNxb = NXB ? NXB : kMaxNxb;
+    const int di = a.di, dr = DR ? DR : a.dr, nxb = NXB ? NXB : a.nxb;
     const int j_raw = blockIdx.x * kBlock + threadIdx.x;
     const bool live = j_raw < di;
     const int j = live ? j_raw : di - 1;
@@ -906,23 +905,23 @@ __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
     const float dv = a.d_vec[j];
     const float dtb = a.dt_b[j];
     const float dts = Q8DT ? a.dt_scales[j] : 1.0f;
-    constexpr int kRowVecs = Q8DT ? kMaxDr / 16 : kMaxDr / 4;  // 16-byte vectors of a dt row
-    const int row_vecs = Q8DT ? a.dt_pad / 16 : a.dt_pad / 4;
+    constexpr int kRowVecs = Q8DT ? (kDr + 15) / 16 : (kDr + 3) / 4;  // 16-byte vectors of a dt row
+    const int row_vecs = DR ? kRowVecs : (Q8DT ? a.dt_pad / 16 : a.dt_pad / 4);
     int4 wraw[kRowVecs];
     {
         const int4* rp = Q8DT ? (const int4*)(a.dt_q + (size_t)j * a.dt_pad) : (const int4*)(a.dt_w + (size_t)j * a.dt_pad);
 #pragma unroll
-        for (int q = 0; q < kRowVecs; q++) wraw[q] = rp[min(q, row_vecs - 1)];
+        for (int q = 0; q < kRowVecs; q++) wraw[q] = rp[DR ? q : min(q, row_vecs - 1)];
     }
     // x_proj partials of this stream (threads < xr), summed in block order.
     const int r = threadIdx.x;
     const bool part_lane = r < a.xr;
-    float pv[kMaxNxb];
+    float pv[kNxb];
     {
         const float* pp = a.xpart + (size_t)b * a.xr_pad + (part_lane ? r : 0);
         const size_t pstride = (size_t)a.cap * a.xr_pad;
 #pragma unroll
-        for (int u = 0; u < kMaxNxb; u++) pv[u] = pp[(size_t)min(u, a.nxb - 1) * pstride];
+        for (int u = 0; u < kNxb; u++) pv[u] = pp[(size_t)(NXB ? u : min(u, nxb - 1)) * pstride];
     }
     const uint32_t s = clamp_slot(slot_raw, a.cap);
     float4* stp = (float4*)(a.ssm + ((size_t)s * di + j) * 16);
@@ -932,13 +931,13 @@ __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
     if (part_lane) {
         float acc = 0.0f;
 #pragma unroll
-        for (int u = 0; u < kMaxNxb; u++)
-            if (u < a.nxb) acc += pv[u];
+        for (int u = 0; u < kNxb; u++)
+            if (NXB || u < nxb) acc += pv[u];
         zp[r] = acc;
     }
     __syncthreads();
     if (!live) return;
-    float wdt[kMaxDr];
+    float wdt[kRowVecs * (Q8DT ? 16 : 4)];
 #pragma unroll
     for (int q = 0; q < kRowVecs; q++) {
         const int wv[4] = {wraw[q].x, wraw[q].y, wraw[q].z, wraw[q].w};
@@ -960,15 +959,15 @@ __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
         const int body = dr / 8 * 8;
         float l[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-        for (int c = 0; c < kMaxDr; c += 8) {
-            if (c < body) {
+        for (int c = 0; c + 8 <= kDr; c += 8) {
+            if (DR || c < body) {
 #pragma unroll
                 for (int i = 0; i < 8; i++) l[i] += wdt[c + i] * zp[c + i];
             }
         }
         float sdot = ((l[0] + l[4]) + (l[2] + l[6])) + ((l[1] + l[5]) + (l[3] + l[7]));
 #pragma unroll
-        for (int c = 0; c < kMaxDr; c++)
+        for (int c = DR / 8 * 8; c < kDr; c++)
             if (c >= body && c < dr) sdot += wdt[c] * zp[c];
         dt = Q8DT ? 0.0f + sdot * dts : sdot;
     }
@@ -988,7 +987,8 @@ __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
 #pragma unroll
             for (int c = 0; c < 4; c++) {
                 const int k = 4 * i + c;
-                const float da = lane_exp_f(0.0f - dt * aa[c]);
+                const float e = 0.0f - dt * aa[c];
+                const float da = FAST ? hw_exp(e) : lane_exp_f(e);
                 st[k] = da * st[k] + dtx * B[k];
             }
         }
@@ -999,10 +999,12 @@ __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
 #pragma unroll
     for (int i = 0; i < 8; i++) l[i] = st[i] * C[i] + st[i + 8] * C[i + 8];
     const float y = ((l[0] + l[4]) + (l[1] + l[5])) + ((l[2] + l[6]) + (l[3] + l[7])) + dv * x;
+    // Gate: the 8-aligned body of each 64-channel block takes the lane form
+    // 1 / (1 + lane_exp(0 - z)), the tail 1 / (1 + exp(-z)); one exp_f serves both.
     const int blk0 = j / 64 * 64;
     const int len = min(64, di - blk0);
     const bool body = (j - blk0) < len / 8 * 8;
-    const float sg = body ? lane_sigmoid_f(zz) : 1.0f / (1.0f + exp_f(-zz));
+    const float sg = 1.0f / (1.0f + exp_f(body ? lane_exp_arg(0.0f - zz) : -zz));
     const float gv = y * (zz * sg);
     const Limb3 t3 = split3(gv);
     const int g = b / kRowTile, sk = j / kKStep;
@@ -1011,6 +1013,18 @@ __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
     dst[0] = t3.h;
     dst[512] = t3.m;
     dst[1024] = t3.l;
+}
+
+// The scan instance for a layer shape: Mamba-130M's (dt_rank 48, 24 x_proj blocks) is
+// specialised, every other shape takes the generic kernel.
+const void* scan_fn(bool q8dt, bool fast, int dr, int nxb) {
+    const bool m130 = dr == 48 && nxb == 24;
+    if (q8dt) {
+        if (m130) return fast ? (const void*)k_scan<true, true, 48, 24> : (const void*)k_scan<true, false, 48, 24>;
+        return fast ? (const void*)k_scan<true, true, 0, 0> : (const void*)k_scan<true, false, 0, 0>;
+    }
+    if (m130) return fast ? (const void*)k_scan<false, true, 48, 24> : (const void*)k_scan<false, false, 48, 24>;
+    return fast ? (const void*)k_scan<false, true, 0, 0> : (const void*)k_scan<false, false, 0, 0>;
 }
 
 // ---------------------------------------------------------------- k_mix_out
@@ -1558,7 +1572,7 @@ void build_step(const ModelView& m, Pool& p, const StepIO& io, std::vector<Launc
         out.push_back(Launch::make(fin, dim3(nxb + zb, in_chunks), dim3(kBlock), lds_in, KC_MIX_IN, ma));
         ScanArgs sa{p.xpart, nxb, xr_pad, (int)D.xr(), p.u, p.z, p.ssm + li * ssm_layer, L.dt_w, L.dt_q,
                     L.dt_scales, L.dt_pad, L.dt_b, L.a_exp, L.d_vec, p.slots, p.cap, n, p.glimb, di, (int)D.dr};
-        const void* fs = L.dt_q ? (const void*)k_scan<true> : (const void*)k_scan<false>;
+        const void* fs = scan_fn(L.dt_q != nullptr, !m.exact_scan, (int)D.dr, nxb);
         out.push_back(Launch::make(fs, dim3((di + kBlock - 1) / kBlock, n), dim3(kBlock), 0, KC_SCAN, sa));
         const float* nw_next = li + 1 < D.nl ? m.layers[li + 1].norm_w : m.norm_f_w;
         MixOutArgs oa{L.out_proj, p.glimb, p.x, n, d, nw_next, pre ? p.xw : nullptr, p.ssp, ks_x, tiles};

@@ -159,6 +159,7 @@ struct ModelView {
     const TMat* head;       // emb when tied
     const float* norm_f_w;
     const float* norm_f_b;
+    bool exact_scan;        // scan decay factors by the portable exp (else the hardware exp2)
 };
 
 // One step's inputs.  slots/tokens/out are device pointers; `check` validates slots

@@ -58,8 +58,10 @@ RDK_HD float exp_f(float x) {
 }
 
 // exp as one SIMD lane of the reference computes it: NaN becomes the lower clamp
-// (tensor.rs:877-879).
-RDK_HD float lane_exp_f(float x) { return exp_f(x != x ? -87.3365447505531f : x); }
+// (tensor.rs:877-879).  lane_exp_arg is that argument rule alone, for callers that pick
+// between the lane and the scalar form before one exp_f.
+RDK_HD float lane_exp_arg(float x) { return x != x ? -87.3365447505531f : x; }
+RDK_HD float lane_exp_f(float x) { return exp_f(lane_exp_arg(x)); }
 
 // 1 / (1 + exp(0 - x)) (tensor.rs:883-885).
 RDK_HD float lane_sigmoid_f(float x) { return 1.0f / (1.0f + lane_exp_f(0.0f - x)); }

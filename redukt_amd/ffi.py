@@ -33,6 +33,7 @@ PROFILE_F32 = 0
 PROFILE_Q8_G64 = 1
 PROFILE_Q8_ROW = 2
 PROFILE_Q8_SMALL = 4
+PROFILE_EXACT_SCAN = 8  # Mamba scan decay by the portable exp instead of the hardware exp2
 
 V1_SYMBOLS = ("redukt_backend_init", "redukt_backend_forward", "redukt_backend_reset_state", "redukt_backend_free")
 V2_SYMBOLS = ("redukt_backend_abi_version", "redukt_backend_batch_init", "redukt_backend_batch_reset",

@@ -66,8 +66,10 @@ def run_lockstep(backend, oracle, n, steps, tok_fn, cap=None):
     return outs
 
 
+# profile 8 / 14: the scan's decay factors by the portable exp (exact element-wise scan)
 @pytest.mark.parametrize("name,profile", [("reftest", 0), ("reftest", 1), ("reftest", 2), ("reftest", 6),
-                                          ("base", 0), ("base", 1), ("base", 6), ("flags", 0), ("flags", 6)])
+                                          ("reftest", 8), ("base", 0), ("base", 1), ("base", 6), ("base", 14),
+                                          ("flags", 0), ("flags", 6)])
 def test_small_model_parity(models, name, profile):
     with ffi.PluginBackend(models[name], profile=profile) as be:
         orc = O.MambaOracle(models[name], profile, cap=9)
@@ -243,7 +245,7 @@ def test_device_resident_entry_point(models):
                 b.close()
 
 
-@pytest.mark.parametrize("profile", [0, 1, 6])
+@pytest.mark.parametrize("profile", [0, 1, 6, 14])
 def test_mamba130m_parity(full_model, profile):
     with ffi.PluginBackend(full_model, profile=profile) as be:
         orc = O.MambaOracle(full_model, profile, cap=4)
