@@ -163,6 +163,14 @@ int32_t redukt_backend_get_state(uint32_t slot, uint32_t layer, float* conv_out,
  * INVALID_ARGUMENT for a Mamba model. */
 int32_t redukt_backend_get_rwkv_state(uint32_t slot, uint32_t layer, float* x_att, float* wkv, float* x_ffn);
 
+/* Test hook, no counterpart in the reference: evaluates one of the portable element-wise
+ * functions on the device for n host inputs (y[i] = f(x[i])), so that tests can compare
+ * its bits with the CPU path's.  fn: 0 exp (tensor.rs:765-794), 1 lane exp (NaN -> lower
+ * clamp, :877-879), 2 ln (:799-837), 3 softplus (:859-861), 4 lane sigmoid (:883-885),
+ * 5 sigmoid 1 / (1 + exp(-x)).  Needs no model; allocates and synchronizes. */
+#define REDUKT_MATH_FN_COUNT 6u
+int32_t redukt_backend_eval_math(uint32_t fn, const float* x, float* y, uint32_t n);
+
 #ifdef __cplusplus
 }
 #endif

@@ -551,6 +551,25 @@ int init_common(const uint8_t* weights_path, int32_t device_id, uint32_t profile
 
 using namespace rdk;
 
+namespace {
+// The portable element-wise functions on the device (redukt_backend_eval_math).
+__global__ void k_eval_math(uint32_t fn, const float* __restrict__ x, float* __restrict__ y, uint32_t n) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float v = x[i];
+    float r;
+    switch (fn) {
+        case 0: r = exp_f(v); break;
+        case 1: r = lane_exp_f(v); break;
+        case 2: r = ln_f(v); break;
+        case 3: r = softplus_f(v); break;
+        case 4: r = lane_sigmoid_f(v); break;
+        default: r = 1.0f / (1.0f + exp_f(-v)); break;
+    }
+    y[i] = r;
+}
+}  // namespace
+
 extern "C" {
 
 BackendResult redukt_backend_init(const uint8_t* weights_path, int32_t device_id, BackendInfo* info_out) {
@@ -698,6 +717,22 @@ int32_t redukt_backend_get_state(uint32_t slot, uint32_t layer, float* conv_out,
                        hipSuccess)
         return BACKEND_FORWARD_FAILED;
     return BACKEND_OK;
+}
+
+int32_t redukt_backend_eval_math(uint32_t fn, const float* x, float* y, uint32_t n) {
+    if (fn >= REDUKT_MATH_FN_COUNT || (n && (!x || !y))) return BACKEND_INVALID_ARGUMENT;
+    if (n == 0) return BACKEND_OK;
+    float* d = nullptr;
+    const size_t bytes = sizeof(float) * n;
+    if (hipMalloc(&d, 2 * bytes) != hipSuccess) return BACKEND_FORWARD_FAILED;
+    hipError_t e = hipMemcpy(d, x, bytes, hipMemcpyHostToDevice);
+    if (e == hipSuccess) {
+        hipLaunchKernelGGL(k_eval_math, dim3((n + 255) / 256), dim3(256), 0, 0, fn, d, d + n, n);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) e = hipMemcpy(y, d + n, bytes, hipMemcpyDeviceToHost);
+    (void)hipFree(d);
+    return e == hipSuccess ? BACKEND_OK : BACKEND_FORWARD_FAILED;
 }
 
 }  // extern "C"

@@ -72,8 +72,10 @@ constexpr int kChunk = 32;                 // streams per k_head workgroup
 constexpr int kGroups = kChunk / kRowTile; // MFMA column groups per chunk
 constexpr int kInGroups = 1;               // column groups per k_mix_in workgroup
 constexpr int kInChunk = kInGroups * kRowTile;
-constexpr int kOutGroups = 1;              // column groups per k_mix_out workgroup
-constexpr int kOutChunk = kOutGroups * kRowTile;
+// Column groups (16 streams each) per k_mix_out workgroup: 1 up to kOutWideFrom streams,
+// 2 from there, so that a large batch fits the chip in one round of workgroups (one
+// 8-wave workgroup per CU).  A stream's arithmetic does not depend on the choice.
+constexpr int kOutWideFrom = 80;
 constexpr int kHeadTiles = 4;              // row tiles per wave in k_head
 // Weight k-pairs each wave keeps in flight (the product loop is unrolled by it): k_mix_in
 // holds its whole quarter of four Q8 row tiles of a d <= 1024 projection, k_head four
@@ -87,6 +89,11 @@ constexpr int kMaxXr = kMaxDr + 32;        // x_proj rows
 constexpr int kMaxNxb = 32;                // d_inner / 64 (d_inner <= 2048)
 constexpr int kOutWaves = 8;               // waves of k_mix_out
 constexpr int kOutPairs = 3;               // k-pairs per k_mix_out wave per pass
+// s_waitcnt immediates that wait on vector memory only (expcnt and lgkmcnt at their
+// "no wait" maxima): vmcnt <= 0, and vmcnt <= 3 * kInGroups (k_mix_in's conv state).
+constexpr int kVmcnt0 = 0xF70;
+constexpr int kVmcnt3G = 0xF70 | (3 * kInGroups);
+static_assert(3 * kInGroups <= 15, "vmcnt field");
 
 // ---------------------------------------------------------------- activation staging
 
@@ -253,7 +260,9 @@ struct SspLoad {
     float v[kSspPerThread];
 };
 
-// Streams [b0, b0 + streams) of the workgroup; threads past them idle.
+// Streams [b0, b0 + streams) of the workgroup; threads past them load a valid row that
+// is never used.  The loads are unconditional (clamped rows and tiles) so that they are
+// issued in straight-line code with the caller's other loads; ssp_reduce masks them.
 __device__ __forceinline__ SspLoad ssp_load(const float* __restrict__ ssp, int tiles, uint32_t b0, uint32_t n,
                                             int streams) {
     const int bb = threadIdx.x / kTps, sub = threadIdx.x % kTps;
@@ -262,10 +271,7 @@ __device__ __forceinline__ SspLoad ssp_load(const float* __restrict__ ssp, int t
     SspLoad r;
     const float* p = ssp + (size_t)(on ? b : 0) * tiles;
 #pragma unroll
-    for (int i = 0; i < kSspPerThread; i++) {
-        const int t = sub + kTps * i;
-        r.v[i] = on && t < tiles ? p[t] : 0.0f;
-    }
+    for (int i = 0; i < kSspPerThread; i++) r.v[i] = p[min(sub + kTps * i, tiles - 1)];
     return r;
 }
 
@@ -423,15 +429,16 @@ struct Quarter {
     RawPair ring[R][kWaves];
 };
 
+// Every ring slot is filled, slots past the quarter with its last pair (loads in
+// straight-line code, so none of them waits for another; the extra copies are unused).
 template <bool Q8, int R>
 __device__ __forceinline__ void quarter_prefetch(const TMat& w, Quarter<Q8, R>& qw, int tb, int p_lo, int cnt) {
     const int lane = threadIdx.x % kWave;
 #pragma unroll
-    for (int q = 0; q < R; q++) {
-        if (q >= cnt) continue;
+    for (int q = 0; q < R; q++)
 #pragma unroll
-        for (int i = 0; i < kWaves; i++) qw.ring[q][i] = load_pair<Q8>(w, min(tb + i, w.rt - 1), p_lo + q, lane);
-    }
+        for (int i = 0; i < kWaves; i++)
+            qw.ring[q][i] = load_pair<Q8>(w, min(tb + i, w.rt - 1), p_lo + min(q, cnt - 1), lane);
 }
 
 template <bool Q8, bool GRP, int R, int G>
@@ -630,12 +637,11 @@ __global__ __launch_bounds__(kBlock) void k_mix_in(MixInArgs a) {
     const bool conv4 = conv_branch && dc == 4 && has_rows && j0 < a.di;
     const int np = w.ks / 2;
     const int p_lo = wave * np / kWaves, p_hi = (wave + 1) * np / kWaves;
-    uint32_t slot_of[G];
+    // Slots first and used last: every load below is issued before the first wait, and
+    // only the conv state, which needs the slot, follows the slot's arrival.
+    uint32_t slot_raw[G];
 #pragma unroll
-    for (int g = 0; g < G; g++) {
-        const uint32_t b = b0 + g * kRowTile + lane % 16;
-        slot_of[g] = conv_branch ? clamp_slot(a.slots[b < a.n ? b : b0], a.cap) : 0u;
-    }
+    for (int g = 0; g < G; g++) slot_raw[g] = a.slots[min(b0 + g * kRowTile + lane % 16, a.n - 1)];
     SspLoad sl;
     if constexpr (PRE) sl = ssp_load(a.ssp, a.tiles, b0, a.n, kInChunk);
     constexpr int R = Q8 ? kInRingQ8 : kInRingF32;
@@ -657,45 +663,54 @@ __global__ __launch_bounds__(kBlock) void k_mix_in(MixInArgs a) {
     }
     // x_proj fragments of this block's k-pair: row tiles wave, wave + 4 (x_proj has at
     // most kMaxXr / 16 = 6 row tiles), with their scales.
+    // Loaded by every block from clamped, in-bounds tiles (a gate-branch block or a tile
+    // past x_proj's rows reads tile 0 / the last tile and never uses it); the scale index
+    // is r * gs + p for column groups and r for one scale per row, without a branch.
     RawPair xpw[2];
     float4 xps[2];
-    if (conv_branch) {
-        const int p = blockIdx.x;
+    {
+        const int p = min((int)blockIdx.x, a.nxb - 1);
         const bool grp = a.wxp.group != a.wxp.cols;
+        const size_t gs = grp ? (size_t)(a.wxp.ks / 2) : 1, po = grp ? (size_t)p : 0;
 #pragma unroll
         for (int k = 0; k < 2; k++) {
-            const int tp = wave + kWaves * k;
-            xps[k] = make_float4(1.0f, 1.0f, 1.0f, 1.0f);
-            if (tp >= a.wxp.rt) continue;
+            const int tp = min(wave + kWaves * k, a.wxp.rt - 1);
             xpw[k] = load_pair<Q8XP>(a.wxp, tp, p, lane);
-            const int r = tp * kRowTile + (lane / 16) * 4;
-            if (Q8XP && !grp) {
-                xps[k] = *(const float4*)(a.wxp.scales + r);
-            } else if (Q8XP) {
-                const size_t gs = a.wxp.ks / 2;
-                xps[k] = make_float4(a.wxp.scales[r * gs + p], a.wxp.scales[(r + 1) * gs + p],
-                                     a.wxp.scales[(r + 2) * gs + p], a.wxp.scales[(r + 3) * gs + p]);
-            }
+            const size_t r = (size_t)tp * kRowTile + (lane / 16) * 4;
+            xps[k] = Q8XP ? make_float4(a.wxp.scales[r * gs + po], a.wxp.scales[(r + 1) * gs + po],
+                                        a.wxp.scales[(r + 2) * gs + po], a.wxp.scales[(r + 3) * gs + po])
+                          : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
         }
     }
-    if constexpr (PRE) {
-        stage_copy_wave<G>(smem, a.xw, b0 / kRowTile, ng, a.wx.ks, 2 * p_lo, 2 * p_hi);
-        ssp_reduce(sl, invs, a.tiles, a.d, kInChunk);
-        __builtin_amdgcn_s_waitcnt(0);  // this wave's copies have landed
-    } else {
-        stage_normed(lds, a.x, a.norm_w, a.norm_b, a.d, a.wx.ks, b0, a.n, kInChunk);
-    }
+    if constexpr (PRE) stage_copy_wave<G>(smem, a.xw, b0 / kRowTile, ng, a.wx.ks, 2 * p_lo, 2 * p_hi);
+    uint32_t slot_of[G];
+#pragma unroll
+    for (int g = 0; g < G; g++) slot_of[g] = conv_branch ? clamp_slot(slot_raw[g], a.cap) : 0u;
+    // Conv state (dc = 4): three loads per group, issued unconditionally from in-bounds
+    // addresses (clamped slot; a conv-branch wave's channels are all < di) so that the
+    // wait below can leave exactly those in flight.
+    const bool conv_ld = conv_branch && dc == 4;
     float4 stv[G][3];
-    if (conv4) {
+    __builtin_amdgcn_sched_barrier(0);  // the copies stay ahead of the conv state loads
+    if (conv_ld) {
 #pragma unroll
         for (int g = 0; g < G; g++) {
-            const uint32_t b = b0 + g * kRowTile + lane % 16;
-            if (g < ng && b < a.n) {
-                const float4* sp = (const float4*)(a.conv_st + ((size_t)slot_of[g] * a.di + j0) * 3);
+            const float4* sp = (const float4*)(a.conv_st + ((size_t)slot_of[g] * a.di + min(j0, a.di - 4)) * 3);
 #pragma unroll
-                for (int k = 0; k < 3; k++) stv[g][k] = sp[k];
-            }
+            for (int k = 0; k < 3; k++) stv[g][k] = sp[k];
         }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (PRE) {
+        ssp_reduce(sl, invs, a.tiles, a.d, kInChunk);
+        // This wave's activation copies have landed; the conv state may still fly
+        // (vector loads complete in order).
+        if (conv_ld)
+            __builtin_amdgcn_s_waitcnt(kVmcnt3G);
+        else
+            __builtin_amdgcn_s_waitcnt(kVmcnt0);
+    } else {
+        stage_normed(lds, a.x, a.norm_w, a.norm_b, a.d, a.wx.ks, b0, a.n, kInChunk);
     }
 
     f32x4 q4[kWaves][G];
@@ -913,27 +928,29 @@ __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
 #pragma unroll
         for (int q = 0; q < kRowVecs; q++) wraw[q] = rp[DR ? q : min(q, row_vecs - 1)];
     }
-    // x_proj partials of this stream (threads < xr), summed in block order.
+    // x_proj partials of this stream, summed in block order.  Every thread loads and sums
+    // (threads past xr re-read row 0), only threads < xr store: the loads stay in
+    // straight-line code.  The partial array is < 4 GiB, so offsets are 32-bit.
     const int r = threadIdx.x;
     const bool part_lane = r < a.xr;
     float pv[kNxb];
     {
-        const float* pp = a.xpart + (size_t)b * a.xr_pad + (part_lane ? r : 0);
-        const size_t pstride = (size_t)a.cap * a.xr_pad;
+        const uint32_t o0 = b * (uint32_t)a.xr_pad + (uint32_t)(part_lane ? r : 0);
+        const uint32_t pstride = (uint32_t)a.cap * (uint32_t)a.xr_pad;
 #pragma unroll
-        for (int u = 0; u < kNxb; u++) pv[u] = pp[(size_t)(NXB ? u : min(u, nxb - 1)) * pstride];
+        for (int u = 0; u < kNxb; u++) pv[u] = a.xpart[o0 + (uint32_t)(NXB ? u : min(u, nxb - 1)) * pstride];
     }
     const uint32_t s = clamp_slot(slot_raw, a.cap);
     float4* stp = (float4*)(a.ssm + ((size_t)s * di + j) * 16);
     float4 sv[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) sv[i] = stp[i];
-    if (part_lane) {
+    {
         float acc = 0.0f;
 #pragma unroll
         for (int u = 0; u < kNxb; u++)
             if (NXB || u < nxb) acc += pv[u];
-        zp[r] = acc;
+        if (part_lane) zp[r] = acc;
     }
     __syncthreads();
     if (!live) return;
@@ -1046,13 +1063,12 @@ struct MixOutArgs {
 // weight and activation fragments requested at once; the eighths are added in wave order,
 // then the per-row scale, then the residual: x += (((q0 + q1) + q2) + ... + q7).  The new
 // residual rows then leave as the next projection's pre-staged activations.
-template <bool Q8>
+template <bool Q8, int G>
 __global__ __launch_bounds__(kOutWaves * kWave) void k_mix_out(MixOutArgs a) {
-    constexpr int G = kOutGroups;
     __shared__ f32x4 part[kOutWaves - 1][G][kWave];
     const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
     const int t = blockIdx.x;
-    const uint32_t b0 = blockIdx.y * kOutChunk;
+    const uint32_t b0 = blockIdx.y * G * kRowTile;
     const int ng = (int)min((uint32_t)G, (a.n - b0 + kRowTile - 1) / kRowTile);
     const TMat& w = a.w;
     const int np = w.ks / 2;
@@ -1546,7 +1562,8 @@ void build_step(const ModelView& m, Pool& p, const StepIO& io, std::vector<Launc
     const int d = (int)D.d, di = (int)D.di;
     const uint32_t chunks = (n + kChunk - 1) / kChunk;
     const uint32_t in_chunks = (n + kInChunk - 1) / kInChunk;
-    const uint32_t out_chunks = (n + kOutChunk - 1) / kOutChunk;
+    const int out_g = n >= (uint32_t)kOutWideFrom ? 2 : 1;
+    const uint32_t out_chunks = (n + out_g * kRowTile - 1) / (out_g * kRowTile);
     const int xr_pad = m.layers[0].x_proj.rt * kRowTile;
     const int nxb = di / 64;
     out.clear();
@@ -1576,7 +1593,8 @@ void build_step(const ModelView& m, Pool& p, const StepIO& io, std::vector<Launc
         out.push_back(Launch::make(fs, dim3((di + kBlock - 1) / kBlock, n), dim3(kBlock), 0, KC_SCAN, sa));
         const float* nw_next = li + 1 < D.nl ? m.layers[li + 1].norm_w : m.norm_f_w;
         MixOutArgs oa{L.out_proj, p.glimb, p.x, n, d, nw_next, pre ? p.xw : nullptr, p.ssp, ks_x, tiles};
-        const void* fo = q8 ? (const void*)k_mix_out<true> : (const void*)k_mix_out<false>;
+        const void* fo = q8 ? (out_g == 2 ? (const void*)k_mix_out<true, 2> : (const void*)k_mix_out<true, 1>)
+                            : (out_g == 2 ? (const void*)k_mix_out<false, 2> : (const void*)k_mix_out<false, 1>);
         out.push_back(Launch::make(fo, dim3(L.out_proj.rt, out_chunks), dim3(kOutWaves * kWave), 0, KC_MIX_OUT, oa));
     }
     const TMat& H = *m.head;

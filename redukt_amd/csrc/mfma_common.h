@@ -2,6 +2,9 @@
 // v_mfma_f32_16x16x32_bf16, the three-limb bf16 split of f32 activations, and the
 // fragment loads of pre-tiled weights (layouts in model.h, TMat).
 #pragma once
+// No a*b+c in this file may be fused: the element-wise arithmetic follows the
+// reference operation by operation (a header is compiled before its includer's pragmas).
+#pragma clang fp contract(off)
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>

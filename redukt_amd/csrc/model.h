@@ -1,6 +1,9 @@
 // model.h — device-side model and state-pool layout shared by the host code and the
 // kernels of libredukt_gpu.so.
 #pragma once
+// No a*b+c in this file may be fused: the element-wise arithmetic follows the
+// reference operation by operation (a header is compiled before its includer's pragmas).
+#pragma clang fp contract(off)
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>

@@ -5,9 +5,10 @@
 // that every platform produces the same bits.  Running the same algorithms on the GPU
 // makes the element-wise phases (conv SiLU, softplus, selective scan, gate, softmax)
 // bit-identical to the CPU path for identical inputs.  The constants are the published
-// Cephes and musl coefficients the reference uses.  Every caller must compile this with
-// floating-point contraction off, or a*b+c would fuse and change the last bit.
+// Cephes and musl coefficients the reference uses.  Floating-point contraction is off
+// from here to the end of the including file: a fused a*b+c changes the last bit.
 #pragma once
+#pragma clang fp contract(off)
 
 #include <stdint.h>
 #include <string.h>

@@ -1,5 +1,8 @@
 // step.h — a step as a list of kernel launches (issued directly or recorded as a graph).
 #pragma once
+// No a*b+c in this file may be fused: the element-wise arithmetic follows the
+// reference operation by operation (a header is compiled before its includer's pragmas).
+#pragma clang fp contract(off)
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>

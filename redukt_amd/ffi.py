@@ -40,7 +40,10 @@ V2_SYMBOLS = ("redukt_backend_abi_version", "redukt_backend_batch_init", "redukt
               "redukt_backend_forward_batch")
 V3_SYMBOLS = ("redukt_backend_init_ex", "redukt_backend_forward_batch_probs", "redukt_backend_forward_batch_device",
               "redukt_backend_device_status", "redukt_backend_stream", "redukt_backend_get_state",
-              "redukt_backend_probe_kernel", "redukt_backend_probe_used", "redukt_backend_get_rwkv_state")
+              "redukt_backend_probe_kernel", "redukt_backend_probe_used", "redukt_backend_get_rwkv_state",
+              "redukt_backend_eval_math")
+# redukt_backend_eval_math function codes: the portable element-wise functions
+MATH_FNS = {"exp": 0, "lane_exp": 1, "ln": 2, "softplus": 3, "lane_sigmoid": 4, "sigmoid": 5}
 
 # Kernel classes of redukt_backend_probe_kernel, and the flag that makes a probed step
 # launch only the kernels of that class (REDUKT_PROBE_CLASS_ONLY).
@@ -152,6 +155,18 @@ class PluginLibrary:
             L.redukt_backend_probe_kernel.restype = ctypes.c_int32
             L.redukt_backend_probe_used.argtypes = []
             L.redukt_backend_probe_used.restype = ctypes.c_uint32
+            L.redukt_backend_eval_math.argtypes = [ctypes.c_uint32, _f32p, _f32p, ctypes.c_uint32]
+            L.redukt_backend_eval_math.restype = ctypes.c_int32
+
+    def eval_math(self, fn: str, x: np.ndarray) -> np.ndarray:
+        """One portable element-wise function evaluated on the device (test hook)."""
+        xi = np.ascontiguousarray(x, np.float32)
+        y = np.empty_like(xi)
+        res = BackendResult.from_code(self.lib.redukt_backend_eval_math(MATH_FNS[fn], _ptr(xi, ctypes.c_float),
+                                                                         _ptr(y, ctypes.c_float), xi.size))
+        if res != BackendResult.OK:
+            raise BackendError(res, f"eval_math({fn})")
+        return y
 
     def _resolve_v2(self) -> Optional[int]:
         """loader.rs:196-216: all four symbols and abi >= 2, else v1 only."""
