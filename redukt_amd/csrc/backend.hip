@@ -244,8 +244,11 @@ int load_weights(const std::string& path, uint32_t profile) {
         if (ok) { t = rd.read(di); ok = rd.ok && (L.dt_b = dev_upload(t.data(), di)); }
         if (ok) {
             t = rd.read(di * 16);
-            for (float& v : t) v = lane_exp_f(v);  // exp(A_log) of every step, tensor.rs:1316
-            ok = rd.ok && (L.a_exp = dev_upload(t.data(), t.size()));
+            // exp(A_log) of every step (tensor.rs:1316), stored state-major [16][di]
+            std::vector<float> ta(di * 16);
+            for (size_t j = 0; j < di; j++)
+                for (size_t n = 0; n < 16; n++) ta[n * di + j] = lane_exp_f(t[j * 16 + n]);
+            ok = rd.ok && (L.a_exp = dev_upload(ta.data(), ta.size()));
         }
         if (ok) { t = rd.read(di); ok = rd.ok && (L.d_vec = dev_upload(t.data(), di)); }
         if (ok) { t = rd.read(d * di); ok = rd.ok && make_tmat(L.out_proj, t.data(), (int)d, (int)di, qgroup((int)di)); }
@@ -713,9 +716,16 @@ int32_t redukt_backend_get_state(uint32_t slot, uint32_t layer, float* conv_out,
     if (conv_out && hipMemcpy(conv_out, p.conv + ((size_t)layer * p.cap + slot) * cl, cl * 4, hipMemcpyDeviceToHost) !=
                         hipSuccess)
         return BACKEND_FORWARD_FAILED;
-    if (ssm_out && hipMemcpy(ssm_out, p.ssm + ((size_t)layer * p.cap + slot) * sl, sl * 4, hipMemcpyDeviceToHost) !=
-                       hipSuccess)
-        return BACKEND_FORWARD_FAILED;
+    if (ssm_out) {
+        // the pool holds [16][di] per slot; the caller gets [di][16]
+        std::vector<float> sm(sl);
+        if (hipMemcpy(sm.data(), p.ssm + ((size_t)layer * p.cap + slot) * sl, sl * 4, hipMemcpyDeviceToHost) !=
+            hipSuccess)
+            return BACKEND_FORWARD_FAILED;
+        const size_t di = G.dims.di;
+        for (size_t j = 0; j < di; j++)
+            for (size_t n = 0; n < 16; n++) ssm_out[j * 16 + n] = sm[n * di + j];
+    }
     return BACKEND_OK;
 }
 

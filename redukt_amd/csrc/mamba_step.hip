@@ -866,13 +866,13 @@ struct ScanArgs {
     int nxb, xr_pad, xr;
     const float* u;        // [n][di]
     const float* z;        // [n][di]
-    float* ssm;            // this layer's state, [slot][di][16]
+    float* ssm;            // this layer's state, [slot][16][di] (state-major)
     const float* dt_w;     // F32 [di][dt_pad] or null
     const int8_t* dt_q;    // Q8 [di][dt_pad] or null
     const float* dt_scales;  // Q8: one per row
     int dt_pad;
     const float* dt_b;
-    const float* a_exp;    // [di][16]
+    const float* a_exp;    // [16][di]
     const float* d_vec;
     const uint32_t* slots;
     uint32_t cap, n;
@@ -911,10 +911,11 @@ __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
     // Loads past a short row or partial list read its last element instead of branching;
     // those values are never used.
     const uint32_t slot_raw = a.slots[b];
-    const float4* ap = (const float4*)(a.a_exp + (size_t)j * 16);
-    float4 av[4];
+    // State-major operands ([16][di]): for each n the wave's 64 channels are one
+    // contiguous 256-byte run, so every load and store below is fully coalesced.
+    float av[16];
 #pragma unroll
-    for (int i = 0; i < 4; i++) av[i] = ap[i];
+    for (int n = 0; n < 16; n++) av[n] = a.a_exp[(size_t)n * di + j];
     const float x = a.u[(size_t)b * di + j];
     const float zz = a.z[(size_t)b * di + j];
     const float dv = a.d_vec[j];
@@ -941,10 +942,10 @@ __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
         for (int u = 0; u < kNxb; u++) pv[u] = a.xpart[o0 + (uint32_t)(NXB ? u : min(u, nxb - 1)) * pstride];
     }
     const uint32_t s = clamp_slot(slot_raw, a.cap);
-    float4* stp = (float4*)(a.ssm + ((size_t)s * di + j) * 16);
-    float4 sv[4];
+    float* stp = a.ssm + (size_t)s * 16 * di + j;
+    float st[16];
 #pragma unroll
-    for (int i = 0; i < 4; i++) sv[i] = stp[i];
+    for (int n = 0; n < 16; n++) st[n] = stp[(size_t)n * di];
     {
         float acc = 0.0f;
 #pragma unroll
@@ -989,28 +990,18 @@ __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
         dt = Q8DT ? 0.0f + sdot * dts : sdot;
     }
     dt = softplus_f(dt + dtb);
-    float st[16];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        st[4 * i] = sv[i].x; st[4 * i + 1] = sv[i].y; st[4 * i + 2] = sv[i].z; st[4 * i + 3] = sv[i].w;
-    }
     const float* B = zp + dr;
     const float* C = zp + dr + 16;
     if (!(fabsf(dt) < 1e-6f)) {
         const float dtx = dt * x;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float aa[4] = {av[i].x, av[i].y, av[i].z, av[i].w};
-#pragma unroll
-            for (int c = 0; c < 4; c++) {
-                const int k = 4 * i + c;
-                const float e = 0.0f - dt * aa[c];
-                const float da = FAST ? hw_exp(e) : lane_exp_f(e);
-                st[k] = da * st[k] + dtx * B[k];
-            }
+        for (int k = 0; k < 16; k++) {
+            const float e = 0.0f - dt * av[k];
+            const float da = FAST ? hw_exp(e) : lane_exp_f(e);
+            st[k] = da * st[k] + dtx * B[k];
         }
 #pragma unroll
-        for (int i = 0; i < 4; i++) stp[i] = make_float4(st[4 * i], st[4 * i + 1], st[4 * i + 2], st[4 * i + 3]);
+        for (int n = 0; n < 16; n++) stp[(size_t)n * di] = st[n];
     }
     float l[8];
 #pragma unroll

@@ -50,7 +50,7 @@ struct DLayer {
     float* dt_scales = nullptr;
     int dt_pad = 0;
     float* dt_b = nullptr;     // [di]
-    float* a_exp = nullptr;    // [di][16]: exp(A_log), constant per load
+    float* a_exp = nullptr;    // [16][di] (state-major): exp(A_log), constant per load
     float* d_vec = nullptr;    // [di]
 };
 
@@ -60,8 +60,9 @@ struct Dims {
 };
 
 // Recurrent state of `cap` slots plus the per-step scratch of `cap` batch rows.
-// State: conv [layer][slot][di][dc-1] and ssm [layer][slot][di][16] f32, so one slot's
-// state of one layer is one contiguous run (18 KB + 96 KB at Mamba-130M).
+// State: conv [layer][slot][di][dc-1] and ssm [layer][slot][16][di] f32 (state-major, so
+// the scan's loads of one state index over 64 channels are contiguous); one slot's state
+// of one layer is one contiguous run either way (18 KB + 96 KB at Mamba-130M).
 struct Pool {
     uint32_t cap = 0;
     uint32_t gcap = 0;           // stream groups of 16 covering cap
