@@ -224,10 +224,12 @@ int load_weights(const std::string& path, uint32_t profile) {
             ok = rd.ok;
             L.dt_pad = (int)((dr + 15) / 16 * 16);
             const size_t dp = (size_t)L.dt_pad;
+            // Rows are stored in 16-byte chunks, chunk-major: chunk c of channel j at
+            // [c][j], so the scan's 64 lanes read one contiguous kilobyte per chunk.
             if (ok && !qsmall) {
                 std::vector<float> tp(di * dp, 0.0f);
                 for (size_t j = 0; j < di; j++)
-                    for (size_t k = 0; k < dr; k++) tp[j * dp + k] = t[j * dr + k];
+                    for (size_t k = 0; k < dr; k++) tp[((k / 4) * di + j) * 4 + k % 4] = t[j * dr + k];
                 ok = (L.dt_w = dev_upload(tp.data(), tp.size())) != nullptr;
             } else if (ok) {
                 std::vector<int8_t> q;
@@ -236,7 +238,7 @@ int load_weights(const std::string& path, uint32_t profile) {
                 const int grp = quantize(t.data(), (int)di, (int)dr, qgroup((int)dr), q, sc);
                 std::vector<int8_t> qp(di * dp, 0);
                 for (size_t j = 0; j < di; j++)
-                    for (size_t k = 0; k < dr; k++) qp[j * dp + k] = q[j * dr + k];
+                    for (size_t k = 0; k < dr; k++) qp[((k / 16) * di + j) * 16 + k % 16] = q[j * dr + k];
                 ok = grp == (int)dr && (L.dt_q = dev_upload(qp.data(), qp.size())) &&
                      (L.dt_scales = dev_upload(sc.data(), sc.size()));
             }

@@ -867,8 +867,8 @@ struct ScanArgs {
     const float* u;        // [n][di]
     const float* z;        // [n][di]
     float* ssm;            // this layer's state, [slot][16][di] (state-major)
-    const float* dt_w;     // F32 [di][dt_pad] or null
-    const int8_t* dt_q;    // Q8 [di][dt_pad] or null
+    const float* dt_w;     // F32 [dt_pad/4][di][4] (16-byte chunks, chunk-major) or null
+    const int8_t* dt_q;    // Q8 [dt_pad/16][di][16] or null
     const float* dt_scales;  // Q8: one per row
     int dt_pad;
     const float* dt_b;
@@ -925,9 +925,9 @@ __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
     const int row_vecs = DR ? kRowVecs : (Q8DT ? a.dt_pad / 16 : a.dt_pad / 4);
     int4 wraw[kRowVecs];
     {
-        const int4* rp = Q8DT ? (const int4*)(a.dt_q + (size_t)j * a.dt_pad) : (const int4*)(a.dt_w + (size_t)j * a.dt_pad);
+        const int4* rp = Q8DT ? (const int4*)a.dt_q + j : (const int4*)a.dt_w + j;
 #pragma unroll
-        for (int q = 0; q < kRowVecs; q++) wraw[q] = rp[DR ? q : min(q, row_vecs - 1)];
+        for (int q = 0; q < kRowVecs; q++) wraw[q] = rp[(size_t)(DR ? q : min(q, row_vecs - 1)) * di];
     }
     // x_proj partials of this stream, summed in block order.  Every thread loads and sums
     // (threads past xr re-read row 0), only threads < xr store: the loads stay in
