@@ -892,6 +892,25 @@ struct ScanArgs {
 // other element-wise operation keeps the reference's arithmetic.  DR and NXB fix dt_rank
 // and the number of 64-channel x_proj blocks at compile time (0: taken from the
 // arguments, bounded by kMaxDr / kMaxNxb), which removes the guards of the unrolled loops.
+// Raw buffer access: a descriptor with a uniform base and an exact byte size (gfx9 word 3:
+// 32-bit data format, untyped), a per-lane 32-bit byte offset and a uniform byte offset.
+// Offsets past the size read 0 and drop stores, so every descriptor covers its array.
+typedef __amdgpu_buffer_rsrc_t BufRsrc;
+constexpr int kBufWord3 = 0x00020000;
+__device__ __forceinline__ BufRsrc buf_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kBufWord3);
+}
+__device__ __forceinline__ float buf_ld_f32(BufRsrc r, uint32_t voff, uint32_t soff) {
+    return bits_to_f(__builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0));
+}
+__device__ __forceinline__ int4 buf_ld_i4(BufRsrc r, uint32_t voff, uint32_t soff) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
+    return make_int4((int)v[0], (int)v[1], (int)v[2], (int)v[3]);
+}
+__device__ __forceinline__ void buf_st_f32(float v, BufRsrc r, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_buffer_store_b32(f_to_bits(v), r, (int)voff, (int)soff, 0);
+}
+
 __device__ __forceinline__ float hw_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
 
 template <bool Q8DT, bool FAST, int DR, int NXB>
@@ -904,6 +923,12 @@ __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
     const int j_raw = blockIdx.x * kBlock + threadIdx.x;
     const bool live = j_raw < di;
     const int j = live ? j_raw : di - 1;
+    // Buffer addressing: one descriptor per array (uniform base and exact byte size), the
+    // lane's 32-bit channel offset and a uniform row offset, so no load or store needs
+    // per-lane 64-bit address arithmetic.
+    const uint32_t ju = (uint32_t)j, diu = (uint32_t)di;
+    const uint32_t j4 = ju * 4u, j16 = ju * 16u;
+    const uint32_t row4 = diu * 4u;  // bytes of one [di] row
     const uint32_t b = blockIdx.y;
     // Requested in this order, all before the first wait: the slot, the slot-independent
     // per-channel operands, the x_proj partials, then the state once the slot is known
@@ -914,20 +939,24 @@ __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
     // State-major operands ([16][di]): for each n the wave's 64 channels are one
     // contiguous 256-byte run, so every load and store below is fully coalesced.
     float av[16];
+    {
+        const BufRsrc ra = buf_rsrc(a.a_exp, 16u * row4);
 #pragma unroll
-    for (int n = 0; n < 16; n++) av[n] = a.a_exp[(size_t)n * di + j];
-    const float x = a.u[(size_t)b * di + j];
-    const float zz = a.z[(size_t)b * di + j];
-    const float dv = a.d_vec[j];
-    const float dtb = a.dt_b[j];
-    const float dts = Q8DT ? a.dt_scales[j] : 1.0f;
+        for (int n = 0; n < 16; n++) av[n] = buf_ld_f32(ra, j4, (uint32_t)n * row4);
+    }
+    const float x = buf_ld_f32(buf_rsrc(a.u + (size_t)b * diu, row4), j4, 0);
+    const float zz = buf_ld_f32(buf_rsrc(a.z + (size_t)b * diu, row4), j4, 0);
+    const float dv = buf_ld_f32(buf_rsrc(a.d_vec, row4), j4, 0);
+    const float dtb = buf_ld_f32(buf_rsrc(a.dt_b, row4), j4, 0);
+    const float dts = Q8DT ? buf_ld_f32(buf_rsrc(a.dt_scales, row4), j4, 0) : 1.0f;
     constexpr int kRowVecs = Q8DT ? (kDr + 15) / 16 : (kDr + 3) / 4;  // 16-byte vectors of a dt row
     const int row_vecs = DR ? kRowVecs : (Q8DT ? a.dt_pad / 16 : a.dt_pad / 4);
     int4 wraw[kRowVecs];
     {
-        const int4* rp = Q8DT ? (const int4*)a.dt_q + j : (const int4*)a.dt_w + j;
+        const void* rp = Q8DT ? (const void*)a.dt_q : (const void*)a.dt_w;
+        const BufRsrc rd = buf_rsrc(rp, (uint32_t)row_vecs * 16u * diu);
 #pragma unroll
-        for (int q = 0; q < kRowVecs; q++) wraw[q] = rp[(size_t)(DR ? q : min(q, row_vecs - 1)) * di];
+        for (int q = 0; q < kRowVecs; q++) wraw[q] = buf_ld_i4(rd, j16, (uint32_t)(DR ? q : min(q, row_vecs - 1)) * 16u * diu);
     }
     // x_proj partials of this stream, summed in block order.  Every thread loads and sums
     // (threads past xr re-read row 0), only threads < xr store: the loads stay in
@@ -936,16 +965,17 @@ __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
     const bool part_lane = r < a.xr;
     float pv[kNxb];
     {
-        const uint32_t o0 = b * (uint32_t)a.xr_pad + (uint32_t)(part_lane ? r : 0);
-        const uint32_t pstride = (uint32_t)a.cap * (uint32_t)a.xr_pad;
+        const uint32_t o0 = (b * (uint32_t)a.xr_pad + (uint32_t)(part_lane ? r : 0)) * 4u;
+        const uint32_t pstride = (uint32_t)a.cap * (uint32_t)a.xr_pad * 4u;
+        const BufRsrc rp = buf_rsrc(a.xpart, (uint32_t)nxb * pstride);
 #pragma unroll
-        for (int u = 0; u < kNxb; u++) pv[u] = a.xpart[o0 + (uint32_t)(NXB ? u : min(u, nxb - 1)) * pstride];
+        for (int u = 0; u < kNxb; u++) pv[u] = buf_ld_f32(rp, o0, (uint32_t)(NXB ? u : min(u, nxb - 1)) * pstride);
     }
     const uint32_t s = clamp_slot(slot_raw, a.cap);
-    float* stp = a.ssm + (size_t)s * 16 * di + j;
+    const BufRsrc rs = buf_rsrc(a.ssm + (size_t)s * 16 * diu, 16u * row4);
     float st[16];
 #pragma unroll
-    for (int n = 0; n < 16; n++) st[n] = stp[(size_t)n * di];
+    for (int n = 0; n < 16; n++) st[n] = buf_ld_f32(rs, j4, (uint32_t)n * row4);
     {
         float acc = 0.0f;
 #pragma unroll
@@ -1001,7 +1031,7 @@ __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
             st[k] = da * st[k] + dtx * B[k];
         }
 #pragma unroll
-        for (int n = 0; n < 16; n++) stp[(size_t)n * di] = st[n];
+        for (int n = 0; n < 16; n++) buf_st_f32(st[n], rs, j4, (uint32_t)n * row4);
     }
     float l[8];
 #pragma unroll
