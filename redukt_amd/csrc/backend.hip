@@ -386,6 +386,8 @@ bool dev_zero(T*& p, size_t count) {
     return hipMemset(p, 0, sizeof(T) * (count ? count : 1)) == hipSuccess;
 }
 
+size_t slot_words(uint32_t cap) { return ((size_t)cap + kSlotWordAlign - 1) / kSlotWordAlign * kSlotWordAlign; }
+
 bool pool_alloc_rwkv(Pool& p, uint32_t cap) {
     const RDims& R = G.rdims;
     const size_t n = cap, d = R.d;
@@ -397,7 +399,7 @@ bool pool_alloc_rwkv(Pool& p, uint32_t cap) {
               dev_zero(p.wkv, z.wkv) && dev_zero(p.vfirst, n * d) && dev_zero(p.rkv, n * 3 * d) &&
               dev_zero(p.lorad, n * 4 * d) && dev_zero(p.mixl, 6 * z.mixl) && dev_zero(p.loral, z.loral) &&
               dev_zero(p.gatedl, z.gatedl) && dev_zero(p.ffnl, z.mixl) && dev_zero(p.actl, z.actl) &&
-              dev_zero(p.headl, z.mixl) && dev_zero(p.out, n * R.vocab) && dev_zero(p.slots, n) &&
+              dev_zero(p.headl, z.mixl) && dev_zero(p.out, n * R.vocab) && dev_zero(p.slots, slot_words(cap)) &&
               dev_zero(p.d_slots, n) && dev_zero(p.d_tokens, n);
     ok = ok && hipHostMalloc((void**)&p.h_slots, sizeof(uint32_t) * n, hipHostMallocDefault) == hipSuccess;
     ok = ok && hipHostMalloc((void**)&p.h_tokens, sizeof(uint32_t) * n, hipHostMallocDefault) == hipSuccess;
@@ -416,7 +418,7 @@ bool pool_alloc(Pool& p, uint32_t cap) {
               dev_zero(p.x, n * d) && dev_zero(p.u, n * di) && dev_zero(p.z, n * di) &&
               dev_zero(p.xpart, xpart_floats(D, cap)) && dev_zero(p.glimb, glimb_elems(D, cap)) &&
               dev_zero(p.xw, xw_elems(D, cap)) && dev_zero(p.ssp, ssp_floats(D, cap)) &&
-              dev_zero(p.out, n * D.vocab) && dev_zero(p.slots, n) && dev_zero(p.d_slots, n) &&
+              dev_zero(p.out, n * D.vocab) && dev_zero(p.slots, slot_words(cap)) && dev_zero(p.d_slots, n) &&
               dev_zero(p.d_tokens, n);
     ok = ok && hipHostMalloc((void**)&p.h_slots, sizeof(uint32_t) * n, hipHostMallocDefault) == hipSuccess;
     ok = ok && hipHostMalloc((void**)&p.h_tokens, sizeof(uint32_t) * n, hipHostMallocDefault) == hipSuccess;

@@ -89,11 +89,10 @@ constexpr int kMaxXr = kMaxDr + 32;        // x_proj rows
 constexpr int kMaxNxb = 32;                // d_inner / 64 (d_inner <= 2048)
 constexpr int kOutWaves = 8;               // waves of k_mix_out
 constexpr int kOutPairs = 3;               // k-pairs per k_mix_out wave per pass
-// s_waitcnt immediates that wait on vector memory only (expcnt and lgkmcnt at their
-// "no wait" maxima): vmcnt <= 0, and vmcnt <= 3 * kInGroups (k_mix_in's conv state).
+// s_waitcnt immediate that waits on vector memory only (expcnt and lgkmcnt at their
+// "no wait" maxima): vmcnt <= 0.
 constexpr int kVmcnt0 = 0xF70;
-constexpr int kVmcnt3G = 0xF70 | (3 * kInGroups);
-static_assert(3 * kInGroups <= 15, "vmcnt field");
+static_assert(kSlotWordAlign % kInChunk == 0, "k_mix_in reads its chunk's slot words whole");
 
 // ---------------------------------------------------------------- activation staging
 
@@ -221,7 +220,7 @@ __device__ void stage_normed(__bf16* lds, const float* __restrict__ x, const flo
 
 __device__ __forceinline__ void stage_copy(unsigned char* lds, const __bf16* __restrict__ xw, uint32_t g0, int ng,
                                            int ks) {
-    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave, wave = wave_index();
     const int blocks = ng * ks * 3;
     const __bf16* src = xw + (size_t)g0 * ks * 3 * 512 + lane * 8;
     lds_u8* dst = (lds_u8*)lds;
@@ -234,20 +233,31 @@ __device__ __forceinline__ void stage_copy(unsigned char* lds, const __bf16* __r
 // Copy of k-steps [s_lo, s_hi) of groups [g0, g0 + ng) by the calling wave alone, for a
 // product split over k across the waves: every wave waits for its own copies
 // (vmcnt(0)) and reads only what it copied, so no barrier is needed before the product.
-template <int G>
+// RUN > 0 fixes the copies per group (3 (s_hi - s_lo)) at compile time: the copy is then
+// straight-line code, through which the compiler counts outstanding loads exactly.
+template <int G, int RUN>
 __device__ __forceinline__ void stage_copy_wave(unsigned char* lds, const __bf16* __restrict__ xw, uint32_t g0,
                                                 int ng, int ks, int s_lo, int s_hi) {
     const int lane = threadIdx.x % kWave;
-    const int run = (s_hi - s_lo) * 3;
+    const int run = RUN > 0 ? RUN : (s_hi - s_lo) * 3;
 #pragma unroll
     for (int g = 0; g < G; g++) {
-        if (g >= ng) continue;
+        if (G > 1 && g >= ng) continue;  // the first group always holds a stream
         const __bf16* src = xw + (((size_t)(g0 + g) * ks + s_lo) * 3) * 512 + lane * 8;
         lds_u8* dst = (lds_u8*)lds + (size_t)((g * ks + s_lo) * 3) * kLimbBytes;
+        if constexpr (RUN > 0) {
+#pragma unroll
+            for (int q = 0; q < RUN; q++)
+                __builtin_amdgcn_global_load_lds((const void*)(src + (size_t)q * 512),
+                                                 (void __attribute__((address_space(3)))*)(dst + q * kLimbBytes), 16, 0,
+                                                 0);
+        } else {
 #pragma unroll 4
-        for (int q = 0; q < run; q++)
-            __builtin_amdgcn_global_load_lds((const void*)(src + (size_t)q * 512),
-                                             (void __attribute__((address_space(3)))*)(dst + q * kLimbBytes), 16, 0, 0);
+            for (int q = 0; q < run; q++)
+                __builtin_amdgcn_global_load_lds((const void*)(src + (size_t)q * 512),
+                                                 (void __attribute__((address_space(3)))*)(dst + q * kLimbBytes), 16, 0,
+                                                 0);
+        }
     }
 }
 
@@ -418,8 +428,8 @@ __device__ __forceinline__ void tiles_gemm(const TMat& w, Tiles<Q8, T, R>& tl, c
 // wave's k-pairs [p_lo, p_lo + cnt), cnt <= kQuarterMax.  The weights of the quarter are
 // requested up front into a ring of R pairs (Q8: the whole quarter; F32 refills R pairs
 // ahead).  One accumulator per (tile, group): per k-step the limb products go in the
-// order hi, mid, lo (F32: hi*hi, hi*mid, mid*hi, hi*lo, mid*mid, lo*hi) — eight
-// independent chains keep the matrix core busy.  Tiles past the matrix are clamped to its
+// order hi, mid, lo (F32: hi*hi, hi*mid, mid*hi, hi*lo, mid*mid, lo*hi), issued across
+// the tiles so that no MFMA waits for its predecessor.  Tiles past the matrix are clamped to its
 // last tile and column groups past n read whatever the LDS holds: both only feed output
 // elements that are never stored (MFMA output columns depend only on their own B column).
 constexpr int kQuarterMax = 4;  // k-pairs per wave: d <= 1024 is 16 pairs over 4 waves
@@ -463,32 +473,46 @@ __device__ __forceinline__ void quarter_gemm(const TMat& w, Quarter<Q8, R>& qw, 
 #pragma unroll
                 for (int m = 0; m < 3; m++) bf[g][h][m] = lds_frag(f + m * 512);
             }
+        AFrag a[kWaves][2];
+        float sc[kWaves][4];
 #pragma unroll
         for (int i = 0; i < kWaves; i++) {
             const RawPair cur = qw.ring[q % R][i];
             if (R < kQuarterMax && q + R < cnt) qw.ring[q % R][i] = load_pair<Q8>(w, min(tb + i, w.rt - 1), p + R, lane);
-            AFrag a[2];
-            decode_pair<Q8>(cur, a[0], a[1]);
-            float sc[4];
+            decode_pair<Q8>(cur, a[i][0], a[i][1]);
             if (GRP) {
 #pragma unroll
                 for (int e = 0; e < 4; e++)
-                    sc[e] = w.scales[(size_t)(min(tb + i, w.rt - 1) * kRowTile + (lane / 16) * 4 + e) * gpr + p];
+                    sc[i][e] = w.scales[(size_t)(min(tb + i, w.rt - 1) * kRowTile + (lane / 16) * 4 + e) * gpr + p];
             }
+        }
+        // Product by product across the tiles: consecutive MFMAs feed different
+        // accumulators, and each accumulator still takes mma_step's order, k-step by k-step.
+        f32x4 tmp[kWaves][G];
+#pragma unroll
+        for (int i = 0; i < kWaves; i++)
+#pragma unroll
+            for (int g = 0; g < G; g++) tmp[i][g] = GRP ? f32x4{0, 0, 0, 0} : out[i][g];
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int j = 0; j < kProds<Q8>; j++)
+#pragma unroll
+                for (int g = 0; g < G; g++)
+#pragma unroll
+                    for (int i = 0; i < kWaves; i++)
+                        tmp[i][g] = mma_prod<Q8>(j, a[i][h], bf[g][h][0], bf[g][h][1], bf[g][h][2], tmp[i][g]);
+#pragma unroll
+        for (int i = 0; i < kWaves; i++)
 #pragma unroll
             for (int g = 0; g < G; g++) {
                 if (GRP) {
-                    f32x4 tmp{0, 0, 0, 0};
 #pragma unroll
-                    for (int h = 0; h < 2; h++) tmp = mma_step<Q8>(a[h], bf[g][h][0], bf[g][h][1], bf[g][h][2], tmp);
-#pragma unroll
-                    for (int e = 0; e < 4; e++) out[i][g][e] = __builtin_fmaf(tmp[e], sc[e], out[i][g][e]);
+                    for (int e = 0; e < 4; e++) out[i][g][e] = __builtin_fmaf(tmp[i][g][e], sc[i][e], out[i][g][e]);
                 } else {
-#pragma unroll
-                    for (int h = 0; h < 2; h++) out[i][g] = mma_step<Q8>(a[h], bf[g][h][0], bf[g][h][1], bf[g][h][2], out[i][g]);
+                    out[i][g] = tmp[i][g];
                 }
             }
-        }
     }
 }
 
@@ -617,13 +641,13 @@ struct MixInArgs {
 // the row scales, conv weights and this block's x_proj fragments, and the activations
 // (the wave's quarter of the pre-staged tiles copied into LDS, or the residual stream
 // normed here for LayerNorm models); the conv state follows while the product runs.
-template <bool Q8, bool Q8XP, bool PRE, bool GRP>
+template <bool Q8, bool Q8XP, bool PRE, bool GRP, int QP>
 __global__ __launch_bounds__(kBlock) void k_mix_in(MixInArgs a) {
     constexpr int G = kInGroups;
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ float invs[kInChunk];
     __bf16* lds = (__bf16*)smem;
-    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave, wave = wave_index();
     const uint32_t b0 = blockIdx.y * kInChunk;
     const int ng = (int)min((uint32_t)G, (a.n - b0 + kRowTile - 1) / kRowTile);
     const bool conv_branch = (int)blockIdx.x < a.nxb;
@@ -634,14 +658,36 @@ __global__ __launch_bounds__(kBlock) void k_mix_in(MixInArgs a) {
     const int tc = min(t, w.rt - 1);
     const int j0 = t * kRowTile + (lane / 16) * 4;  // this lane's 4 consecutive channels
     const int dc = a.dc;
-    const bool conv4 = conv_branch && dc == 4 && has_rows && j0 < a.di;
+    // QP > 0: every wave takes exactly QP k-pairs (w.ks = 2 kWaves QP, checked on the host).
     const int np = w.ks / 2;
-    const int p_lo = wave * np / kWaves, p_hi = (wave + 1) * np / kWaves;
-    // Slots first and used last: every load below is issued before the first wait, and
-    // only the conv state, which needs the slot, follows the slot's arrival.
+    const int p_lo = QP > 0 ? wave * QP : wave * np / kWaves, p_hi = QP > 0 ? p_lo + QP : (wave + 1) * np / kWaves;
+    // Slots by scalar loads, first: they do not count on the vector memory counter, so
+    // waiting for them before the conv state loads leaves every vector load in flight.
+    // The slot list is allocated in whole kSlotWordAlign blocks; a word past n feeds only
+    // a stream that is never stored (and is clamped below like any other).
     uint32_t slot_raw[G];
 #pragma unroll
-    for (int g = 0; g < G; g++) slot_raw[g] = a.slots[min(b0 + g * kRowTile + lane % 16, a.n - 1)];
+    for (int g = 0; g < G; g++) {
+        // Constant address space: the list is read-only for this kernel, and uniform loads
+        // from that space always go through the scalar unit.
+        const __attribute__((address_space(4))) uint32_t* sp =
+            (const __attribute__((address_space(4))) uint32_t*)(a.slots + b0 + g * kRowTile);
+        uint32_t sv[kRowTile];
+#pragma unroll
+        for (int q = 0; q < kRowTile; q += 4) {
+            sv[q] = sp[q];
+            sv[q + 1] = sp[q + 1];
+            sv[q + 2] = sp[q + 2];
+            sv[q + 3] = sp[q + 3];
+            // Pinned to scalar registers: otherwise the per-lane select below is folded
+            // back into a per-lane vector load of the selected word.
+            asm volatile("" : "+s"(sv[q]), "+s"(sv[q + 1]), "+s"(sv[q + 2]), "+s"(sv[q + 3]));
+        }
+        uint32_t mine = sv[0];
+#pragma unroll
+        for (int i = 1; i < kRowTile; i++) mine = lane % 16 == i ? sv[i] : mine;
+        slot_raw[g] = mine;
+    }
     SspLoad sl;
     if constexpr (PRE) sl = ssp_load(a.ssp, a.tiles, b0, a.n, kInChunk);
     constexpr int R = Q8 ? kInRingQ8 : kInRingF32;
@@ -650,15 +696,18 @@ __global__ __launch_bounds__(kBlock) void k_mix_in(MixInArgs a) {
     // Per-row scale of the finished tile (Q8 without column groups).
     float4 rsc = make_float4(1.0f, 1.0f, 1.0f, 1.0f);
     if (Q8 && !GRP) rsc = *(const float4*)(w.scales + tc * kRowTile + (lane / 16) * 4);
+    // Conv weights and bias of the lane's channels (used when dc = 4), loaded by every lane
+    // from indices clamped into the arrays: no branch in the load prologue.
     float cwv[4][4], cbv[4];
-    if (conv4) {
-        const float4* cw4 = (const float4*)(a.conv_w + (size_t)j0 * 4);
+    {
+        const int jc = min(j0, a.di - 4);
+        const float4* cw4 = (const float4*)(a.conv_w + min(jc * 4, a.di * dc - 16));
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const float4 v = cw4[i];
             cwv[i][0] = v.x; cwv[i][1] = v.y; cwv[i][2] = v.z; cwv[i][3] = v.w;
         }
-        const float4 b4 = *(const float4*)(a.conv_b + j0);
+        const float4 b4 = *(const float4*)(a.conv_b + jc);
         cbv[0] = b4.x; cbv[1] = b4.y; cbv[2] = b4.z; cbv[3] = b4.w;
     }
     // x_proj fragments of this block's k-pair: row tiles wave, wave + 4 (x_proj has at
@@ -682,39 +731,34 @@ __global__ __launch_bounds__(kBlock) void k_mix_in(MixInArgs a) {
                           : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
         }
     }
-    if constexpr (PRE) stage_copy_wave<G>(smem, a.xw, b0 / kRowTile, ng, a.wx.ks, 2 * p_lo, 2 * p_hi);
     uint32_t slot_of[G];
 #pragma unroll
     for (int g = 0; g < G; g++) slot_of[g] = conv_branch ? clamp_slot(slot_raw[g], a.cap) : 0u;
-    // Conv state (dc = 4): three loads per group, issued unconditionally from in-bounds
-    // addresses (clamped slot; a conv-branch wave's channels are all < di) so that the
-    // wait below can leave exactly those in flight.
-    const bool conv_ld = conv_branch && dc == 4;
+    // Conv state (used when dc = 4 on the conv branch): three loads per group, issued by
+    // every wave, without a branch, from addresses clamped into the state buffer, ahead of
+    // the activation copies: one wait for everything follows the copies.
+    const size_t conv_floats = (size_t)a.cap * a.di * (dc - 1);
     float4 stv[G][3];
-    __builtin_amdgcn_sched_barrier(0);  // the copies stay ahead of the conv state loads
-    if (conv_ld) {
 #pragma unroll
-        for (int g = 0; g < G; g++) {
-            const float4* sp = (const float4*)(a.conv_st + ((size_t)slot_of[g] * a.di + min(j0, a.di - 4)) * 3);
+    for (int g = 0; g < G; g++) {
+        const size_t off = min(((size_t)slot_of[g] * a.di + min(j0, a.di - 4)) * 3, conv_floats - 12);
+        const float4* sp = (const float4*)(a.conv_st + off);
 #pragma unroll
-            for (int k = 0; k < 3; k++) stv[g][k] = sp[k];
-        }
+        for (int k = 0; k < 3; k++) stv[g][k] = sp[k];
     }
-    __builtin_amdgcn_sched_barrier(0);
     if constexpr (PRE) {
-        ssp_reduce(sl, invs, a.tiles, a.d, kInChunk);
-        // This wave's activation copies have landed; the conv state may still fly
-        // (vector loads complete in order).
-        if (conv_ld)
-            __builtin_amdgcn_s_waitcnt(kVmcnt3G);
-        else
-            __builtin_amdgcn_s_waitcnt(kVmcnt0);
+        stage_copy_wave<G, 6 * QP>(smem, a.xw, b0 / kRowTile, ng, a.wx.ks, 2 * p_lo, 2 * p_hi);
+        __builtin_amdgcn_s_waitcnt(kVmcnt0);  // this wave's loads and activation copies
+        __builtin_amdgcn_sched_barrier(0);
     } else {
         stage_normed(lds, a.x, a.norm_w, a.norm_b, a.d, a.wx.ks, b0, a.n, kInChunk);
     }
 
     f32x4 q4[kWaves][G];
     quarter_gemm<Q8, GRP, R, G>(w, qw, tb, lds, p_lo, p_hi - p_lo, q4);
+    // The RMS scales are first needed after the barrier below.  Reduced here, after the
+    // product: their LDS store would otherwise wait for every LDS copy in flight.
+    if constexpr (PRE) ssp_reduce(sl, invs, a.tiles, a.d, kInChunk);
     // Quarters through LDS (reusing the activation area): red[src wave][tile][g][lane].
     __syncthreads();
     f32x4* red = (f32x4*)smem;
@@ -1087,7 +1131,7 @@ struct MixOutArgs {
 template <bool Q8, int G>
 __global__ __launch_bounds__(kOutWaves * kWave) void k_mix_out(MixOutArgs a) {
     __shared__ f32x4 part[kOutWaves - 1][G][kWave];
-    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave, wave = wave_index();
     const int t = blockIdx.x;
     const uint32_t b0 = blockIdx.y * G * kRowTile;
     const int ng = (int)min((uint32_t)G, (a.n - b0 + kRowTile - 1) / kRowTile);
@@ -1229,7 +1273,7 @@ __global__ __launch_bounds__(kBlock) void k_head(HeadArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ float invs[kChunk];
     __bf16* lds = (__bf16*)smem;
-    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave, wave = wave_index();
     const uint32_t b0 = blockIdx.y * kChunk;
     const int ng = (int)min((uint32_t)kGroups, (a.n - b0 + kRowTile - 1) / kRowTile);
     const int V = a.w.rows;
@@ -1294,7 +1338,7 @@ constexpr int kHwTiles = 2;    // row tiles per wave
 constexpr int kHwGroups = 8;   // column groups (16 streams) per workgroup
 
 __device__ __forceinline__ void copy_group(unsigned char* buf, const __bf16* __restrict__ xw, uint32_t g, int ks) {
-    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave, wave = wave_index();
     const int blocks = ks * 3;
     const __bf16* src = xw + (size_t)g * blocks * 512 + lane * 8;
     lds_u8* dst = (lds_u8*)buf;
@@ -1308,7 +1352,7 @@ template <int NP>
 __global__ __launch_bounds__(kHwWaves * kWave) void k_head_ws(HeadArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ float invs[kHwGroups * kRowTile];
-    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave, wave = wave_index();
     const TMat& w = a.w;
     const int np = w.ks / 2, ks = w.ks;
     const int V = w.rows;
@@ -1388,11 +1432,14 @@ __global__ __launch_bounds__(kHwWaves * kWave) void k_head_ws(HeadArgs a) {
 #pragma unroll
                 for (int m = 0; m < 3; m++) bf[h][m] = lds_frag(f + m * 512);
             }
+            // mma_step's order per tile, the tiles' products interleaved.
 #pragma unroll
-            for (int i = 0; i < kHwTiles; i++) {
-                acc[i] = mma_step<true>(wd[p][i][0], bf[0][0], bf[0][1], bf[0][2], acc[i]);
-                acc[i] = mma_step<true>(wd[p][i][1], bf[1][0], bf[1][1], bf[1][2], acc[i]);
-            }
+            for (int h = 0; h < 2; h++)
+#pragma unroll
+                for (int j = 0; j < kProds<true>; j++)
+#pragma unroll
+                    for (int i = 0; i < kHwTiles; i++)
+                        acc[i] = mma_prod<true>(j, wd[p][i][h], bf[h][0], bf[h][1], bf[h][2], acc[i]);
         }
         const uint32_t b = (gb + gi) * kRowTile + lane % 16;
         const float inv = invs[gi * kRowTile + lane % 16];
@@ -1497,24 +1544,34 @@ uint32_t mix_in_lds_bytes(int ks) {
     return std::max(acts, std::max(quarters, xp_operand));
 }
 
-template <bool Q8, bool Q8XP, bool PRE, bool GRP>
-const void* mix_in_fn4(uint32_t lds) {
-    allow_lds(k_mix_in<Q8, Q8XP, PRE, GRP>, lds);
-    return (const void*)k_mix_in<Q8, Q8XP, PRE, GRP>;
+template <bool Q8, bool Q8XP, bool PRE, bool GRP, int QP>
+const void* mix_in_fn5(uint32_t lds) {
+    allow_lds(k_mix_in<Q8, Q8XP, PRE, GRP, QP>, lds);
+    return (const void*)k_mix_in<Q8, Q8XP, PRE, GRP, QP>;
 }
 
+// Three k-pairs per wave (d = 768, Mamba-130M) is compiled as a fixed shape.
+constexpr int kInFixedPairs = 3;
+
+template <bool Q8, bool Q8XP, bool PRE, bool GRP>
+const void* mix_in_fn4(uint32_t lds, bool fixed) {
+    return fixed ? mix_in_fn5<Q8, Q8XP, PRE, GRP, kInFixedPairs>(lds) : mix_in_fn5<Q8, Q8XP, PRE, GRP, 0>(lds);
+}
+
+// The fixed shape pays off with pre-staged activations (the copy is unrolled); the
+// LayerNorm path keeps the general one.
 template <bool Q8, bool Q8XP>
-const void* mix_in_fn2(bool pre, bool grp, uint32_t lds) {
-    if (pre) return grp ? mix_in_fn4<Q8, Q8XP, true, Q8>(lds) : mix_in_fn4<Q8, Q8XP, true, false>(lds);
-    return grp ? mix_in_fn4<Q8, Q8XP, false, Q8>(lds) : mix_in_fn4<Q8, Q8XP, false, false>(lds);
+const void* mix_in_fn2(bool pre, bool grp, bool fixed, uint32_t lds) {
+    if (pre) return grp ? mix_in_fn4<Q8, Q8XP, true, Q8>(lds, fixed) : mix_in_fn4<Q8, Q8XP, true, false>(lds, fixed);
+    return grp ? mix_in_fn5<Q8, Q8XP, false, Q8, 0>(lds) : mix_in_fn5<Q8, Q8XP, false, false, 0>(lds);
 }
 
 // grp: Q8 in_proj with 64-column scale groups.
-const void* mix_in_fn(bool q8, bool q8xp, bool pre, bool grp, uint32_t lds) {
-    if (q8 && q8xp) return mix_in_fn2<true, true>(pre, grp, lds);
-    if (q8) return mix_in_fn2<true, false>(pre, grp, lds);
-    if (q8xp) return mix_in_fn2<false, true>(pre, false, lds);
-    return mix_in_fn2<false, false>(pre, false, lds);
+const void* mix_in_fn(bool q8, bool q8xp, bool pre, bool grp, bool fixed, uint32_t lds) {
+    if (q8 && q8xp) return mix_in_fn2<true, true>(pre, grp, fixed, lds);
+    if (q8) return mix_in_fn2<true, false>(pre, grp, fixed, lds);
+    if (q8xp) return mix_in_fn2<false, true>(pre, false, fixed, lds);
+    return mix_in_fn2<false, false>(pre, false, fixed, lds);
 }
 
 template <bool Q8>
@@ -1581,7 +1638,6 @@ void build_step(const ModelView& m, Pool& p, const StepIO& io, std::vector<Launc
     const Dims& D = *m.dims;
     const uint32_t n = io.n;
     const int d = (int)D.d, di = (int)D.di;
-    const uint32_t chunks = (n + kChunk - 1) / kChunk;
     const uint32_t in_chunks = (n + kInChunk - 1) / kInChunk;
     const int out_g = n >= (uint32_t)kOutWideFrom ? 2 : 1;
     const uint32_t out_chunks = (n + out_g * kRowTile - 1) / (out_g * kRowTile);
@@ -1600,7 +1656,8 @@ void build_step(const ModelView& m, Pool& p, const StepIO& io, std::vector<Launc
     const bool q8xp = m.layers[0].x_proj.group != 0;
     const uint32_t lds_in = mix_in_lds_bytes(ks_x);
     const bool grp = q8 && m.layers[0].in_x.group != m.layers[0].in_x.cols;
-    const void* fin = mix_in_fn(q8, q8xp, pre, grp, lds_in);
+    const bool fixed = ks_x == 2 * kWaves * kInFixedPairs && m.layers[0].in_z.ks == ks_x;
+    const void* fin = mix_in_fn(q8, q8xp, pre, grp, fixed, lds_in);
     for (uint32_t li = 0; li < D.nl; li++) {
         const DLayer& L = m.layers[li];
         MixInArgs ma{p.x, L.norm_w, L.norm_b, L.in_x, L.in_z, L.x_proj, nxb, p.conv + li * conv_layer,

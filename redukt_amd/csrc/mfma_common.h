@@ -47,6 +47,10 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// The wave's index within its workgroup as a wave-uniform (scalar) value: indices derived
+// from it stay in scalar registers instead of being recomputed per lane.
+__device__ __forceinline__ int wave_index() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave)); }
+
 __device__ __forceinline__ uint32_t clamp_slot(uint32_t s, uint32_t cap) { return s < cap ? s : cap - 1; }
 
 // ---------------------------------------------------------------- weight fragments
@@ -122,6 +126,26 @@ __device__ __forceinline__ f32x4 mma_step(const AFrag& a, const bf16x8& bh, cons
         acc = mma(a.l, bh, acc);
     }
     return acc;
+}
+
+// Product j (j < kProds<Q8>) of mma_step's sequence alone, so that a caller can interleave
+// the products of several independent accumulators (a dependent MFMA waits for the whole
+// latency of the previous one) while each accumulator still sees mma_step's order.
+template <bool Q8>
+constexpr int kProds = Q8 ? 3 : 6;
+
+template <bool Q8>
+__device__ __forceinline__ f32x4 mma_prod(int j, const AFrag& a, const bf16x8& bh, const bf16x8& bm, const bf16x8& bl,
+                                          const f32x4& acc) {
+    if (Q8) return mma(a.h, j == 0 ? bh : j == 1 ? bm : bl, acc);
+    switch (j) {
+        case 0: return mma(a.h, bh, acc);
+        case 1: return mma(a.h, bm, acc);
+        case 2: return mma(a.m, bh, acc);
+        case 3: return mma(a.h, bl, acc);
+        case 4: return mma(a.m, bm, acc);
+        default: return mma(a.l, bh, acc);
+    }
 }
 
 __device__ __forceinline__ bf16x8 lds_frag(const __bf16* base) { return *(const bf16x8*)base; }

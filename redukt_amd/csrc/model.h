@@ -60,6 +60,11 @@ struct Dims {
 };
 
 // Recurrent state of `cap` slots plus the per-step scratch of `cap` batch rows.
+// The step's validated slot list (Pool::slots) is allocated in whole blocks of this many
+// words: a kernel may read the slot words of its whole stream chunk with scalar loads, past
+// the last stream of a ragged chunk too (those words only feed streams never stored).
+constexpr uint32_t kSlotWordAlign = 64;
+
 // State: conv [layer][slot][di][dc-1] and ssm [layer][slot][16][di] f32 (state-major, so
 // the scan's loads of one state index over 64 channels are contiguous); one slot's state
 // of one layer is one contiguous run either way (18 KB + 96 KB at Mamba-130M).
