@@ -89,9 +89,6 @@ constexpr int kMaxXr = kMaxDr + 32;        // x_proj rows
 constexpr int kMaxNxb = 32;                // d_inner / 64 (d_inner <= 2048)
 constexpr int kOutWaves = 8;               // waves of k_mix_out
 constexpr int kOutPairs = 3;               // k-pairs per k_mix_out wave per pass
-// s_waitcnt immediate that waits on vector memory only (expcnt and lgkmcnt at their
-// "no wait" maxima): vmcnt <= 0.
-constexpr int kVmcnt0 = 0xF70;
 static_assert(kSlotWordAlign % kInChunk == 0, "k_mix_in reads its chunk's slot words whole");
 
 // ---------------------------------------------------------------- activation staging
@@ -228,37 +225,6 @@ __device__ __forceinline__ void stage_copy(unsigned char* lds, const __bf16* __r
     for (int q = wave; q < blocks; q += kWaves)
         __builtin_amdgcn_global_load_lds((const void*)(src + (size_t)q * 512), (void __attribute__((address_space(3)))*)(dst + q * kLimbBytes),
                                          16, 0, 0);
-}
-
-// Copy of k-steps [s_lo, s_hi) of groups [g0, g0 + ng) by the calling wave alone, for a
-// product split over k across the waves: every wave waits for its own copies
-// (vmcnt(0)) and reads only what it copied, so no barrier is needed before the product.
-// RUN > 0 fixes the copies per group (3 (s_hi - s_lo)) at compile time: the copy is then
-// straight-line code, through which the compiler counts outstanding loads exactly.
-template <int G, int RUN>
-__device__ __forceinline__ void stage_copy_wave(unsigned char* lds, const __bf16* __restrict__ xw, uint32_t g0,
-                                                int ng, int ks, int s_lo, int s_hi) {
-    const int lane = threadIdx.x % kWave;
-    const int run = RUN > 0 ? RUN : (s_hi - s_lo) * 3;
-#pragma unroll
-    for (int g = 0; g < G; g++) {
-        if (G > 1 && g >= ng) continue;  // the first group always holds a stream
-        const __bf16* src = xw + (((size_t)(g0 + g) * ks + s_lo) * 3) * 512 + lane * 8;
-        lds_u8* dst = (lds_u8*)lds + (size_t)((g * ks + s_lo) * 3) * kLimbBytes;
-        if constexpr (RUN > 0) {
-#pragma unroll
-            for (int q = 0; q < RUN; q++)
-                __builtin_amdgcn_global_load_lds((const void*)(src + (size_t)q * 512),
-                                                 (void __attribute__((address_space(3)))*)(dst + q * kLimbBytes), 16, 0,
-                                                 0);
-        } else {
-#pragma unroll 4
-            for (int q = 0; q < run; q++)
-                __builtin_amdgcn_global_load_lds((const void*)(src + (size_t)q * 512),
-                                                 (void __attribute__((address_space(3)))*)(dst + q * kLimbBytes), 16, 0,
-                                                 0);
-        }
-    }
 }
 
 // RMS scale of the chunk's streams: eight threads per stream each take every eighth
@@ -434,13 +400,66 @@ __device__ __forceinline__ void tiles_gemm(const TMat& w, Tiles<Q8, T, R>& tl, c
 // elements that are never stored (MFMA output columns depend only on their own B column).
 constexpr int kQuarterMax = 4;  // k-pairs per wave: d <= 1024 is 16 pairs over 4 waves
 
+// Slot q of a quarter of cnt pairs loads pair p_lo + quarter_slot(q, cnt): slots past the
+// quarter repeat its last pair, and a wave with no pairs (fewer k-pairs than waves) loads
+// pair p_lo, which is always a pair of the matrix (p_lo = floor(wave np / kWaves) < np).
+// Such loads are never used.
+__device__ __forceinline__ int quarter_slot(int q, int cnt) { return max(min(q, cnt - 1), 0); }
+
 template <bool Q8, int R>
 struct Quarter {
     RawPair ring[R][kWaves];
 };
 
-// Every ring slot is filled, slots past the quarter with its last pair (loads in
-// straight-line code, so none of them waits for another; the extra copies are unused).
+// The activation (B) fragments of a wave's quarter, [k-pair][group][k-step of the pair]
+// [limb].  No other wave reads them, so with pre-staged activations they are loaded from
+// the tiles in global memory straight into registers.  CNT > 0 is the quarter's exact
+// k-pair count; otherwise every slot is loaded as quarter_slot says.
+template <int G>
+struct BQuarter {
+    bf16x8 f[kQuarterMax][G][2][3];
+};
+
+template <int G, int CNT>
+__device__ __forceinline__ void bquarter_load(BQuarter<G>& bq, const __bf16* __restrict__ xw, uint32_t g0, int ng,
+                                              int ks, int p_lo, int cnt) {
+    const int lane = threadIdx.x % kWave;
+    constexpr int Q = CNT > 0 ? CNT : kQuarterMax;
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        const int gg = G > 1 ? min(g, ng - 1) : g;
+        const __bf16* base = xw + ((size_t)(g0 + gg) * ks + 2 * p_lo) * 3 * 512 + lane * 8;
+#pragma unroll
+        for (int q = 0; q < Q; q++) {
+            const int qq = CNT > 0 ? q : quarter_slot(q, cnt);
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+#pragma unroll
+                for (int m = 0; m < 3; m++) bq.f[q][g][h][m] = lds_frag(base + ((2 * qq + h) * 3 + m) * 512);
+        }
+    }
+}
+
+// The same fragments from activations staged in LDS (the LayerNorm path, normed in place).
+template <int G>
+__device__ __forceinline__ void bquarter_lds(BQuarter<G>& bq, const __bf16* lds, int ks, int p_lo, int cnt) {
+    const int lane = threadIdx.x % kWave;
+#pragma unroll
+    for (int q = 0; q < kQuarterMax; q++) {
+        const int qq = quarter_slot(q, cnt);
+#pragma unroll
+        for (int g = 0; g < G; g++)
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const __bf16* f = lds + ((size_t)(g * ks + 2 * (p_lo + qq) + h) * 3) * 512 + lane * 8;
+#pragma unroll
+                for (int m = 0; m < 3; m++) bq.f[q][g][h][m] = lds_frag(f + m * 512);
+            }
+    }
+}
+
+// Every ring slot is filled (loads in straight-line code, so none of them waits for
+// another; the extra copies are unused).
 template <bool Q8, int R>
 __device__ __forceinline__ void quarter_prefetch(const TMat& w, Quarter<Q8, R>& qw, int tb, int p_lo, int cnt) {
     const int lane = threadIdx.x % kWave;
@@ -448,12 +467,12 @@ __device__ __forceinline__ void quarter_prefetch(const TMat& w, Quarter<Q8, R>& 
     for (int q = 0; q < R; q++)
 #pragma unroll
         for (int i = 0; i < kWaves; i++)
-            qw.ring[q][i] = load_pair<Q8>(w, min(tb + i, w.rt - 1), p_lo + min(q, cnt - 1), lane);
+            qw.ring[q][i] = load_pair<Q8>(w, min(tb + i, w.rt - 1), p_lo + quarter_slot(q, cnt), lane);
 }
 
 template <bool Q8, bool GRP, int R, int G>
-__device__ __forceinline__ void quarter_gemm(const TMat& w, Quarter<Q8, R>& qw, int tb, const __bf16* lds, int p_lo,
-                                             int cnt, f32x4 (&out)[kWaves][G]) {
+__device__ __forceinline__ void quarter_gemm(const TMat& w, Quarter<Q8, R>& qw, int tb, const BQuarter<G>& bq,
+                                             int p_lo, int cnt, f32x4 (&out)[kWaves][G]) {
     const int lane = threadIdx.x % kWave;
     const int gpr = w.ks / 2;
 #pragma unroll
@@ -464,15 +483,7 @@ __device__ __forceinline__ void quarter_gemm(const TMat& w, Quarter<Q8, R>& qw, 
     for (int q = 0; q < kQuarterMax; q++) {
         if (q >= cnt) continue;
         const int p = p_lo + q;
-        bf16x8 bf[G][2][3];
-#pragma unroll
-        for (int g = 0; g < G; g++)
-#pragma unroll
-            for (int h = 0; h < 2; h++) {
-                const __bf16* f = lds + ((size_t)(g * w.ks + 2 * p + h) * 3) * 512 + lane * 8;
-#pragma unroll
-                for (int m = 0; m < 3; m++) bf[g][h][m] = lds_frag(f + m * 512);
-            }
+        const bf16x8 (&bf)[G][2][3] = bq.f[q];
         AFrag a[kWaves][2];
         float sc[kWaves][4];
 #pragma unroll
@@ -689,10 +700,16 @@ __global__ __launch_bounds__(kBlock) void k_mix_in(MixInArgs a) {
         slot_raw[g] = mine;
     }
     SspLoad sl;
-    if constexpr (PRE) sl = ssp_load(a.ssp, a.tiles, b0, a.n, kInChunk);
+    // Vector loads in the order of first use (they complete in order): the quarter's
+    // weights and activations, then what the epilogue reads.
     constexpr int R = Q8 ? kInRingQ8 : kInRingF32;
     Quarter<Q8, R> qw;
     quarter_prefetch<Q8, R>(w, qw, tb, p_lo, p_hi - p_lo);
+    BQuarter<G> bq;
+    if constexpr (PRE) {
+        bquarter_load<G, QP>(bq, a.xw, b0 / kRowTile, ng, a.wx.ks, p_lo, p_hi - p_lo);
+        sl = ssp_load(a.ssp, a.tiles, b0, a.n, kInChunk);
+    }
     // Per-row scale of the finished tile (Q8 without column groups).
     float4 rsc = make_float4(1.0f, 1.0f, 1.0f, 1.0f);
     if (Q8 && !GRP) rsc = *(const float4*)(w.scales + tc * kRowTile + (lane / 16) * 4);
@@ -735,8 +752,7 @@ __global__ __launch_bounds__(kBlock) void k_mix_in(MixInArgs a) {
 #pragma unroll
     for (int g = 0; g < G; g++) slot_of[g] = conv_branch ? clamp_slot(slot_raw[g], a.cap) : 0u;
     // Conv state (used when dc = 4 on the conv branch): three loads per group, issued by
-    // every wave, without a branch, from addresses clamped into the state buffer, ahead of
-    // the activation copies: one wait for everything follows the copies.
+    // every wave, without a branch, from addresses clamped into the state buffer.
     const size_t conv_floats = (size_t)a.cap * a.di * (dc - 1);
     float4 stv[G][3];
 #pragma unroll
@@ -746,21 +762,18 @@ __global__ __launch_bounds__(kBlock) void k_mix_in(MixInArgs a) {
 #pragma unroll
         for (int k = 0; k < 3; k++) stv[g][k] = sp[k];
     }
-    if constexpr (PRE) {
-        stage_copy_wave<G, 6 * QP>(smem, a.xw, b0 / kRowTile, ng, a.wx.ks, 2 * p_lo, 2 * p_hi);
-        __builtin_amdgcn_s_waitcnt(kVmcnt0);  // this wave's loads and activation copies
-        __builtin_amdgcn_sched_barrier(0);
-    } else {
+    if constexpr (!PRE) {
         stage_normed(lds, a.x, a.norm_w, a.norm_b, a.d, a.wx.ks, b0, a.n, kInChunk);
+        bquarter_lds<G>(bq, lds, a.wx.ks, p_lo, p_hi - p_lo);
     }
 
     f32x4 q4[kWaves][G];
-    quarter_gemm<Q8, GRP, R, G>(w, qw, tb, lds, p_lo, p_hi - p_lo, q4);
-    // The RMS scales are first needed after the barrier below.  Reduced here, after the
-    // product: their LDS store would otherwise wait for every LDS copy in flight.
+    quarter_gemm<Q8, GRP, R, G>(w, qw, tb, bq, p_lo, p_hi - p_lo, q4);
+    // The RMS scales are first needed after the barrier below.
     if constexpr (PRE) ssp_reduce(sl, invs, a.tiles, a.d, kInChunk);
-    // Quarters through LDS (reusing the activation area): red[src wave][tile][g][lane].
-    __syncthreads();
+    // Quarters through LDS: red[src wave][tile][g][lane] (on the LayerNorm path over the
+    // staged activations, once every wave has read them).
+    if constexpr (!PRE) __syncthreads();
     f32x4* red = (f32x4*)smem;
 #pragma unroll
     for (int i = 0; i < kWaves; i++) {
@@ -1535,10 +1548,10 @@ namespace {
 
 uint32_t stage_lds_bytes(int ks) { return (uint32_t)(kGroups * ks * 3 * kLimbBytes); }
 
-// k_mix_in stages kInGroups column groups and reuses that area for the k-quarter
-// partials and the x_proj operand.
-uint32_t mix_in_lds_bytes(int ks) {
-    const uint32_t acts = kInGroups * ks * 3 * kLimbBytes;
+// k_mix_in: the k-quarter partials and the x_proj operand, and on the LayerNorm path the
+// staged activations of kInGroups column groups (the same area, reused).
+uint32_t mix_in_lds_bytes(int ks, bool pre) {
+    const uint32_t acts = pre ? 0u : kInGroups * ks * 3 * kLimbBytes;
     const uint32_t quarters = kWaves * kWaves * kInGroups * kWave * sizeof(f32x4);
     const uint32_t xp_operand = kInGroups * 2 * 3 * kLimbBytes;
     return std::max(acts, std::max(quarters, xp_operand));
@@ -1654,7 +1667,7 @@ void build_step(const ModelView& m, Pool& p, const StepIO& io, std::vector<Launc
     const size_t ssm_layer = (size_t)p.cap * di * 16;
     const bool q8 = m.layers[0].in_x.group != 0;
     const bool q8xp = m.layers[0].x_proj.group != 0;
-    const uint32_t lds_in = mix_in_lds_bytes(ks_x);
+    const uint32_t lds_in = mix_in_lds_bytes(ks_x, pre);
     const bool grp = q8 && m.layers[0].in_x.group != m.layers[0].in_x.cols;
     const bool fixed = ks_x == 2 * kWaves * kInFixedPairs && m.layers[0].in_z.ks == ks_x;
     const void* fin = mix_in_fn(q8, q8xp, pre, grp, fixed, lds_in);
