@@ -55,6 +55,8 @@ struct Model {
     float* norm_f_w = nullptr;
     float* norm_f_b = nullptr;
     std::vector<void*> allocs;
+    unsigned char* arena = nullptr;   // current weight chunk and its fill
+    size_t arena_used = 0;
     hipStream_t stream = nullptr;
     Pool v1, batch;
     StepRunner runner;
@@ -75,11 +77,37 @@ void log(const char* fmt, ...) {
     va_end(ap);
 }
 
+// Weights go into 64 MB chunks in load order, 256-byte aligned, so that one layer's arrays
+// sit together in a few large pages rather than in one small allocation each (fewer
+// address-translation misses when a kernel first touches them).  An array larger than a
+// quarter chunk gets its own allocation.  Every chunk ends in kArenaTail unused bytes, the
+// slack a separate allocation would have had past its last array.
+constexpr size_t kArenaChunk = (size_t)64 << 20;
+constexpr size_t kArenaTail = (size_t)64 << 10;
+
+void* arena_alloc(size_t bytes) {
+    bytes = (bytes + 255) & ~(size_t)255;
+    void* p = nullptr;
+    if (bytes > kArenaChunk / 4) {
+        if (hipMalloc(&p, bytes) != hipSuccess) return nullptr;
+        G.allocs.push_back(p);
+        return p;
+    }
+    if (G.arena == nullptr || G.arena_used + bytes > kArenaChunk) {
+        if (hipMalloc(&p, kArenaChunk + kArenaTail) != hipSuccess) return nullptr;
+        G.allocs.push_back(p);
+        G.arena = (unsigned char*)p;
+        G.arena_used = 0;
+    }
+    p = G.arena + G.arena_used;
+    G.arena_used += bytes;
+    return p;
+}
+
 template <typename T>
 T* dev_upload(const T* host, size_t count) {
-    T* p = nullptr;
-    if (hipMalloc((void**)&p, sizeof(T) * (count ? count : 1)) != hipSuccess) return nullptr;
-    G.allocs.push_back(p);
+    T* p = (T*)arena_alloc(sizeof(T) * (count ? count : 1));
+    if (p == nullptr) return nullptr;
     if (count && hipMemcpy(p, host, sizeof(T) * count, hipMemcpyHostToDevice) != hipSuccess) return nullptr;
     return p;
 }
@@ -365,6 +393,8 @@ uint32_t file_kind(const std::string& path) {
 void dev_free_all() {
     for (void* p : G.allocs) (void)hipFree(p);
     G.allocs.clear();
+    G.arena = nullptr;
+    G.arena_used = 0;
 }
 
 void pool_free(Pool& p) {
