@@ -398,22 +398,41 @@ void dev_free_all() {
 }
 
 void pool_free(Pool& p) {
-    void* bufs[] = {p.conv, p.ssm, p.x, p.u, p.z, p.xpart, p.glimb, p.xw, p.ssp, p.out, p.slots, p.d_slots, p.d_tokens,
-                    p.x_att, p.x_ffn, p.wkv, p.vfirst, p.rkv, p.lorad, p.mixl, p.loral, p.gatedl, p.ffnl, p.actl, p.headl};
-    for (void* b : bufs) (void)hipFree(b);
+    if (p.block) (void)hipFree(p.block);
     if (p.h_slots) (void)hipHostFree(p.h_slots);
     if (p.h_tokens) (void)hipHostFree(p.h_tokens);
     free(p.seen);
     p = Pool{};
 }
 
-template <typename T>
-bool dev_zero(T*& p, size_t count) {
-    if (hipMalloc((void**)&p, sizeof(T) * (count ? count : 1)) != hipSuccess) {
-        p = nullptr;
+// A pool's device arrays are carved from one zeroed allocation (256-byte aligned, in the
+// order given: the per-step scratch first, the recurrent state last), so a step touches
+// few, large pages.  The layout function runs twice: to size the block, then to carve it.
+struct Carve {
+    unsigned char* base = nullptr;
+    size_t off = 0;
+    template <typename T>
+    void take(T*& p, size_t count) {
+        off = (off + 255) & ~(size_t)255;
+        p = base ? (T*)(base + off) : nullptr;
+        off += sizeof(T) * (count ? count : 1);
+    }
+};
+
+template <typename F>
+bool pool_carve(Pool& p, F&& layout) {
+    Carve c;
+    layout(c);
+    const size_t bytes = c.off + kArenaTail;
+    if (hipMalloc(&p.block, bytes) != hipSuccess) {
+        p.block = nullptr;
         return false;
     }
-    return hipMemset(p, 0, sizeof(T) * (count ? count : 1)) == hipSuccess;
+    if (hipMemset(p.block, 0, bytes) != hipSuccess) return false;
+    c.base = (unsigned char*)p.block;
+    c.off = 0;
+    layout(c);
+    return true;
 }
 
 size_t slot_words(uint32_t cap) { return ((size_t)cap + kSlotWordAlign - 1) / kSlotWordAlign * kSlotWordAlign; }
@@ -425,12 +444,25 @@ bool pool_alloc_rwkv(Pool& p, uint32_t cap) {
     p = Pool{};
     p.cap = cap;
     p.gcap = (cap + 15) / 16;
-    bool ok = dev_zero(p.x, n * d) && dev_zero(p.x_att, z.state_d) && dev_zero(p.x_ffn, z.state_d) &&
-              dev_zero(p.wkv, z.wkv) && dev_zero(p.vfirst, n * d) && dev_zero(p.rkv, n * 3 * d) &&
-              dev_zero(p.lorad, n * 4 * d) && dev_zero(p.mixl, 6 * z.mixl) && dev_zero(p.loral, z.loral) &&
-              dev_zero(p.gatedl, z.gatedl) && dev_zero(p.ffnl, z.mixl) && dev_zero(p.actl, z.actl) &&
-              dev_zero(p.headl, z.mixl) && dev_zero(p.out, n * R.vocab) && dev_zero(p.slots, slot_words(cap)) &&
-              dev_zero(p.d_slots, n) && dev_zero(p.d_tokens, n);
+    bool ok = pool_carve(p, [&](Carve& c) {
+        c.take(p.slots, slot_words(cap));
+        c.take(p.d_slots, n);
+        c.take(p.d_tokens, n);
+        c.take(p.x, n * d);
+        c.take(p.vfirst, n * d);
+        c.take(p.rkv, n * 3 * d);
+        c.take(p.lorad, n * 4 * d);
+        c.take(p.mixl, 6 * z.mixl);
+        c.take(p.loral, z.loral);
+        c.take(p.gatedl, z.gatedl);
+        c.take(p.ffnl, z.mixl);
+        c.take(p.actl, z.actl);
+        c.take(p.headl, z.mixl);
+        c.take(p.out, n * R.vocab);
+        c.take(p.x_att, z.state_d);
+        c.take(p.x_ffn, z.state_d);
+        c.take(p.wkv, z.wkv);
+    });
     ok = ok && hipHostMalloc((void**)&p.h_slots, sizeof(uint32_t) * n, hipHostMallocDefault) == hipSuccess;
     ok = ok && hipHostMalloc((void**)&p.h_tokens, sizeof(uint32_t) * n, hipHostMallocDefault) == hipSuccess;
     ok = ok && (p.seen = (uint8_t*)calloc(n, 1)) != nullptr;
@@ -444,12 +476,21 @@ bool pool_alloc(Pool& p, uint32_t cap) {
     p = Pool{};
     p.cap = cap;
     p.gcap = (cap + 15) / 16;
-    bool ok = dev_zero(p.conv, (size_t)D.nl * n * di * (D.dc - 1)) && dev_zero(p.ssm, (size_t)D.nl * n * di * 16) &&
-              dev_zero(p.x, n * d) && dev_zero(p.u, n * di) && dev_zero(p.z, n * di) &&
-              dev_zero(p.xpart, xpart_floats(D, cap)) && dev_zero(p.glimb, glimb_elems(D, cap)) &&
-              dev_zero(p.xw, xw_elems(D, cap)) && dev_zero(p.ssp, ssp_floats(D, cap)) &&
-              dev_zero(p.out, n * D.vocab) && dev_zero(p.slots, slot_words(cap)) && dev_zero(p.d_slots, n) &&
-              dev_zero(p.d_tokens, n);
+    bool ok = pool_carve(p, [&](Carve& c) {
+        c.take(p.slots, slot_words(cap));
+        c.take(p.d_slots, n);
+        c.take(p.d_tokens, n);
+        c.take(p.x, n * d);
+        c.take(p.xw, xw_elems(D, cap));
+        c.take(p.ssp, ssp_floats(D, cap));
+        c.take(p.u, n * di);
+        c.take(p.z, n * di);
+        c.take(p.xpart, xpart_floats(D, cap));
+        c.take(p.glimb, glimb_elems(D, cap));
+        c.take(p.out, n * D.vocab);
+        c.take(p.conv, (size_t)D.nl * n * di * (D.dc - 1));
+        c.take(p.ssm, (size_t)D.nl * n * di * 16);
+    });
     ok = ok && hipHostMalloc((void**)&p.h_slots, sizeof(uint32_t) * n, hipHostMallocDefault) == hipSuccess;
     ok = ok && hipHostMalloc((void**)&p.h_tokens, sizeof(uint32_t) * n, hipHostMallocDefault) == hipSuccess;
     ok = ok && (p.seen = (uint8_t*)calloc(n, 1)) != nullptr;
@@ -562,11 +603,16 @@ int init_common(const uint8_t* weights_path, int32_t device_id, uint32_t profile
         free_model();
         return BACKEND_WEIGHTS_NOT_FOUND;
     }
-    if (!dev_zero(G.d_err, 1) || !pool_alloc(G.v1, 1)) {
+    if (hipMalloc((void**)&G.d_err, sizeof(uint32_t)) != hipSuccess) {
+        G.d_err = nullptr;
         free_model();
         return BACKEND_INIT_FAILED;
     }
     G.allocs.push_back(G.d_err);
+    if (hipMemset(G.d_err, 0, sizeof(uint32_t)) != hipSuccess || !pool_alloc(G.v1, 1)) {
+        free_model();
+        return BACKEND_INIT_FAILED;
+    }
     G.ready = true;
     memset(info_out, 0, sizeof(*info_out));
     info_out->ffi_version = BACKEND_FFI_VERSION;

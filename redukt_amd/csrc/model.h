@@ -71,6 +71,7 @@ constexpr uint32_t kSlotWordAlign = 64;
 struct Pool {
     uint32_t cap = 0;
     uint32_t gcap = 0;           // stream groups of 16 covering cap
+    void* block = nullptr;       // the one device allocation all device arrays below are carved from
     float* conv = nullptr;
     float* ssm = nullptr;
     float* x = nullptr;          // [cap][d] residual stream
