@@ -754,13 +754,14 @@ __global__ __launch_bounds__(kBlock) void k_mix_in(MixInArgs a) {
     // Conv state (used when dc = 4 on the conv branch): three loads per group, issued by
     // every wave, without a branch, from addresses clamped into the state buffer.
     const size_t conv_floats = (size_t)a.cap * a.di * (dc - 1);
-    float4 stv[G][3];
+    // Streamed (non-temporal): the state is read and written once per step.
+    f32x4 stv[G][3];
 #pragma unroll
     for (int g = 0; g < G; g++) {
         const size_t off = min(((size_t)slot_of[g] * a.di + min(j0, a.di - 4)) * 3, conv_floats - 12);
-        const float4* sp = (const float4*)(a.conv_st + off);
+        const f32x4* sp = (const f32x4*)(a.conv_st + off);
 #pragma unroll
-        for (int k = 0; k < 3; k++) stv[g][k] = sp[k];
+        for (int k = 0; k < 3; k++) stv[g][k] = __builtin_nontemporal_load(sp + k);
     }
     if constexpr (!PRE) {
         stage_normed(lds, a.x, a.norm_w, a.norm_b, a.d, a.wx.ks, b0, a.n, kInChunk);
@@ -844,10 +845,10 @@ __global__ __launch_bounds__(kBlock) void k_mix_in(MixInArgs a) {
                     st[3 * i + 2] = xv;
                     uv[i] = val;
                 }
-                float4* sp = (float4*)(a.conv_st + ((size_t)s * a.di + j0) * 3);
-                sp[0] = make_float4(st[0], st[1], st[2], st[3]);
-                sp[1] = make_float4(st[4], st[5], st[6], st[7]);
-                sp[2] = make_float4(st[8], st[9], st[10], st[11]);
+                f32x4* sp = (f32x4*)(a.conv_st + ((size_t)s * a.di + j0) * 3);
+                __builtin_nontemporal_store(f32x4{st[0], st[1], st[2], st[3]}, sp);
+                __builtin_nontemporal_store(f32x4{st[4], st[5], st[6], st[7]}, sp + 1);
+                __builtin_nontemporal_store(f32x4{st[8], st[9], st[10], st[11]}, sp + 2);
             } else {
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
@@ -957,15 +958,20 @@ constexpr int kBufWord3 = 0x00020000;
 __device__ __forceinline__ BufRsrc buf_rsrc(const void* base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kBufWord3);
 }
+// Cache policy of a buffer access (gfx9 "aux" bits): kStream = nt, for data read or
+// written once per step (the recurrent state), so it does not displace reused lines.
+constexpr int kCached = 0, kStream = 2;
+template <int POLICY = kCached>
 __device__ __forceinline__ float buf_ld_f32(BufRsrc r, uint32_t voff, uint32_t soff) {
-    return bits_to_f(__builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0));
+    return bits_to_f(__builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, POLICY));
 }
 __device__ __forceinline__ int4 buf_ld_i4(BufRsrc r, uint32_t voff, uint32_t soff) {
     const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
     return make_int4((int)v[0], (int)v[1], (int)v[2], (int)v[3]);
 }
+template <int POLICY = kCached>
 __device__ __forceinline__ void buf_st_f32(float v, BufRsrc r, uint32_t voff, uint32_t soff) {
-    __builtin_amdgcn_raw_buffer_store_b32(f_to_bits(v), r, (int)voff, (int)soff, 0);
+    __builtin_amdgcn_raw_buffer_store_b32(f_to_bits(v), r, (int)voff, (int)soff, POLICY);
 }
 
 __device__ __forceinline__ float hw_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
@@ -1032,7 +1038,7 @@ __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
     const BufRsrc rs = buf_rsrc(a.ssm + (size_t)s * 16 * diu, 16u * row4);
     float st[16];
 #pragma unroll
-    for (int n = 0; n < 16; n++) st[n] = buf_ld_f32(rs, j4, (uint32_t)n * row4);
+    for (int n = 0; n < 16; n++) st[n] = buf_ld_f32<kStream>(rs, j4, (uint32_t)n * row4);
     {
         float acc = 0.0f;
 #pragma unroll
@@ -1088,7 +1094,7 @@ __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
             st[k] = da * st[k] + dtx * B[k];
         }
 #pragma unroll
-        for (int n = 0; n < 16; n++) buf_st_f32(st[n], rs, j4, (uint32_t)n * row4);
+        for (int n = 0; n < 16; n++) buf_st_f32<kStream>(st[n], rs, j4, (uint32_t)n * row4);
     }
     float l[8];
 #pragma unroll
