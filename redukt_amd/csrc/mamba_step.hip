@@ -1336,11 +1336,12 @@ __global__ __launch_bounds__(kBlock) void k_head(HeadArgs a) {
             const uint32_t b = b0 + g * kRowTile + lane % 16;
             if (g >= ng || b >= a.n) continue;
             float* o = a.out + (size_t)b * V + r0;
+            // Logits are written once and read later (host copy, softmax): streamed.
             if (r0 + 3 < V && (V & 3) == 0) {
-                *(float4*)o = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
+                __builtin_nontemporal_store(f32x4{acc[g][0], acc[g][1], acc[g][2], acc[g][3]}, (f32x4*)o);
             } else {
                 for (int i = 0; i < 4; i++)
-                    if (r0 + i < V) o[i] = acc[g][i];
+                    if (r0 + i < V) __builtin_nontemporal_store(acc[g][i], o + i);
             }
         }
     }
@@ -1470,11 +1471,12 @@ __global__ __launch_bounds__(kHwWaves * kWave) void k_head_ws(HeadArgs a) {
             const float v[4] = {acc[i][0] * rsc[i].x * inv, acc[i][1] * rsc[i].y * inv, acc[i][2] * rsc[i].z * inv,
                                 acc[i][3] * rsc[i].w * inv};
             float* o = a.out + (size_t)b * V + r0;
+            // Logits are written once and read later (host copy, softmax): streamed.
             if (r0 + 3 < V && (V & 3) == 0) {
-                *(float4*)o = make_float4(v[0], v[1], v[2], v[3]);
+                __builtin_nontemporal_store(f32x4{v[0], v[1], v[2], v[3]}, (f32x4*)o);
             } else {
                 for (int e = 0; e < 4; e++)
-                    if (r0 + e < V) o[e] = v[e];
+                    if (r0 + e < V) __builtin_nontemporal_store(v[e], o + e);
             }
         }
     }
