@@ -46,9 +46,13 @@
 
 namespace rdk {
 
+// Channels per x_proj split-K block at most: the channels of one k_mix_in conv-branch
+// workgroup of two row tiles, one k-step of x_proj (four row tiles make 64-channel blocks).
+constexpr int kXpBlock = 32;
+
 size_t xpart_floats(const Dims& d, uint32_t cap) {
     const size_t xr_pad = (d.xr() + kRowTile - 1) / kRowTile * kRowTile;
-    return (size_t)(d.di / 64) * cap * xr_pad;
+    return (size_t)(d.di / kXpBlock) * cap * xr_pad;
 }
 
 size_t glimb_elems(const Dims& d, uint32_t cap) {
@@ -71,6 +75,8 @@ constexpr int kWaves = kBlock / kWave;
 constexpr int kChunk = 32;                 // streams per k_head workgroup
 constexpr int kGroups = kChunk / kRowTile; // MFMA column groups per chunk
 constexpr int kInGroups = 1;               // column groups per k_mix_in workgroup
+// Row tiles per k_mix_in workgroup: 2 up to kInWideFrom streams, 4 from there.
+constexpr int kInWideFrom = 64;
 constexpr int kInChunk = kInGroups * kRowTile;
 // Column groups (16 streams each) per k_mix_out workgroup: 1 up to kOutWideFrom streams,
 // 2 from there, so that a large batch fits the chip in one round of workgroups (one
@@ -86,7 +92,7 @@ constexpr int kTps = 8;                    // threads per stream while staging a
 constexpr int kQuadBatch = 4;              // column quads a staging thread loads per iteration
 constexpr int kMaxDr = 64;                 // dt_rank limit (d_model <= 1024)
 constexpr int kMaxXr = kMaxDr + 32;        // x_proj rows
-constexpr int kMaxNxb = 32;                // d_inner / 64 (d_inner <= 2048)
+constexpr int kMaxNxb = 64;                // x_proj split-K blocks, d_inner / 32 (d_inner <= 2048)
 constexpr int kOutWaves = 8;               // waves of k_mix_out
 constexpr int kOutPairs = 3;               // k-pairs per k_mix_out wave per pass
 static_assert(kSlotWordAlign % kInChunk == 0, "k_mix_in reads its chunk's slot words whole");
@@ -390,7 +396,7 @@ __device__ __forceinline__ void tiles_gemm(const TMat& w, Tiles<Q8, T, R>& tl, c
         for (int g = 0; g < kGroups; g++) out[i][g] = (acc[i][g][0] + acc[i][g][1]) + acc[i][g][2];
 }
 
-// k_mix_in's product: the block's kWaves row tiles times both column groups over this
+// k_mix_in's product: the block's T row tiles times its column groups over this
 // wave's k-pairs [p_lo, p_lo + cnt), cnt <= kQuarterMax.  The weights of the quarter are
 // requested up front into a ring of R pairs (Q8: the whole quarter; F32 refills R pairs
 // ahead).  One accumulator per (tile, group): per k-step the limb products go in the
@@ -406,9 +412,9 @@ constexpr int kQuarterMax = 4;  // k-pairs per wave: d <= 1024 is 16 pairs over 
 // Such loads are never used.
 __device__ __forceinline__ int quarter_slot(int q, int cnt) { return max(min(q, cnt - 1), 0); }
 
-template <bool Q8, int R>
+template <bool Q8, int R, int T>
 struct Quarter {
-    RawPair ring[R][kWaves];
+    RawPair ring[R][T];
 };
 
 // The activation (B) fragments of a wave's quarter, [k-pair][group][k-step of the pair]
@@ -460,23 +466,23 @@ __device__ __forceinline__ void bquarter_lds(BQuarter<G>& bq, const __bf16* lds,
 
 // Every ring slot is filled (loads in straight-line code, so none of them waits for
 // another; the extra copies are unused).
-template <bool Q8, int R>
-__device__ __forceinline__ void quarter_prefetch(const TMat& w, Quarter<Q8, R>& qw, int tb, int p_lo, int cnt) {
+template <bool Q8, int R, int T>
+__device__ __forceinline__ void quarter_prefetch(const TMat& w, Quarter<Q8, R, T>& qw, int tb, int p_lo, int cnt) {
     const int lane = threadIdx.x % kWave;
 #pragma unroll
     for (int q = 0; q < R; q++)
 #pragma unroll
-        for (int i = 0; i < kWaves; i++)
+        for (int i = 0; i < T; i++)
             qw.ring[q][i] = load_pair<Q8>(w, min(tb + i, w.rt - 1), p_lo + quarter_slot(q, cnt), lane);
 }
 
-template <bool Q8, bool GRP, int R, int G>
-__device__ __forceinline__ void quarter_gemm(const TMat& w, Quarter<Q8, R>& qw, int tb, const BQuarter<G>& bq,
-                                             int p_lo, int cnt, f32x4 (&out)[kWaves][G]) {
+template <bool Q8, bool GRP, int R, int T, int G>
+__device__ __forceinline__ void quarter_gemm(const TMat& w, Quarter<Q8, R, T>& qw, int tb, const BQuarter<G>& bq,
+                                             int p_lo, int cnt, f32x4 (&out)[T][G]) {
     const int lane = threadIdx.x % kWave;
     const int gpr = w.ks / 2;
 #pragma unroll
-    for (int i = 0; i < kWaves; i++)
+    for (int i = 0; i < T; i++)
 #pragma unroll
         for (int g = 0; g < G; g++) out[i][g] = f32x4{0, 0, 0, 0};
 #pragma unroll
@@ -484,10 +490,10 @@ __device__ __forceinline__ void quarter_gemm(const TMat& w, Quarter<Q8, R>& qw, 
         if (q >= cnt) continue;
         const int p = p_lo + q;
         const bf16x8 (&bf)[G][2][3] = bq.f[q];
-        AFrag a[kWaves][2];
-        float sc[kWaves][4];
+        AFrag a[T][2];
+        float sc[T][4];
 #pragma unroll
-        for (int i = 0; i < kWaves; i++) {
+        for (int i = 0; i < T; i++) {
             const RawPair cur = qw.ring[q % R][i];
             if (R < kQuarterMax && q + R < cnt) qw.ring[q % R][i] = load_pair<Q8>(w, min(tb + i, w.rt - 1), p + R, lane);
             decode_pair<Q8>(cur, a[i][0], a[i][1]);
@@ -499,9 +505,9 @@ __device__ __forceinline__ void quarter_gemm(const TMat& w, Quarter<Q8, R>& qw, 
         }
         // Product by product across the tiles: consecutive MFMAs feed different
         // accumulators, and each accumulator still takes mma_step's order, k-step by k-step.
-        f32x4 tmp[kWaves][G];
+        f32x4 tmp[T][G];
 #pragma unroll
-        for (int i = 0; i < kWaves; i++)
+        for (int i = 0; i < T; i++)
 #pragma unroll
             for (int g = 0; g < G; g++) tmp[i][g] = GRP ? f32x4{0, 0, 0, 0} : out[i][g];
 #pragma unroll
@@ -511,10 +517,10 @@ __device__ __forceinline__ void quarter_gemm(const TMat& w, Quarter<Q8, R>& qw, 
 #pragma unroll
                 for (int g = 0; g < G; g++)
 #pragma unroll
-                    for (int i = 0; i < kWaves; i++)
+                    for (int i = 0; i < T; i++)
                         tmp[i][g] = mma_prod<Q8>(j, a[i][h], bf[g][h][0], bf[g][h][1], bf[g][h][2], tmp[i][g]);
 #pragma unroll
-        for (int i = 0; i < kWaves; i++)
+        for (int i = 0; i < T; i++)
 #pragma unroll
             for (int g = 0; g < G; g++) {
                 if (GRP) {
@@ -630,7 +636,7 @@ struct MixInArgs {
     const float* norm_w;
     const float* norm_b;
     TMat wx, wz, wxp;          // in_proj conv branch, gate branch; x_proj
-    int nxb;                   // conv-branch workgroups (64 channels each)
+    int nxb;                   // conv-branch workgroups (16 T channels each)
     float* conv_st;            // this layer's conv state, [slot][di][dc-1]
     const float* conv_w;
     const float* conv_b;
@@ -638,51 +644,59 @@ struct MixInArgs {
     uint32_t cap, n;
     float* u;                  // [n][di]
     float* z;                  // [n][di]
-    float* xpart;              // [nxb][cap][xr_pad]
+    float* xpart;              // [di / 32][cap][xr_pad] (32-channel x_proj partials)
     int di, dc, d, xr_pad;
     const __bf16* xw;          // pre-staged activations (RMSNorm path)
     const float* ssp;
     int tiles;
 };
 
-// in_proj for 4 row tiles x kInChunk streams.  The product is split over k: wave w
-// multiplies all four tiles over k-pairs [w np / 4, (w + 1) np / 4); the quarters meet in
-// LDS and wave w adds tile w's in wave order, q0 + q1 + q2 + q3, then finishes tile w.
-// Every operand is requested before the first wait: the weights of the wave's quarter,
-// the row scales, conv weights and this block's x_proj fragments, and the activations
-// (the wave's quarter of the pre-staged tiles copied into LDS, or the residual stream
-// normed here for LayerNorm models); the conv state follows while the product runs.
-template <bool Q8, bool Q8XP, bool PRE, bool GRP, int QP>
+// in_proj for T row tiles (T = 2 or 4) x kInChunk streams, 4 waves.  The product is split
+// over k: wave w multiplies the block's T tiles over k-pairs [w np / 4, (w + 1) np / 4).
+// The quarters meet in LDS and are added in wave order, q0 + q1 + q2 + q3; wave w then
+// finishes 4 T rows: tile w T / 4, rows 4 T (w % (4 / T)) .. + 4 T, E = T consecutive rows
+// (channels) per lane, lane l for stream l % 16.  Every vector load is issued up front,
+// in the order of first use: the quarter's weights and activations (the pre-staged tiles,
+// straight into registers), the RMS partials, row scales, conv weights, x_proj fragments
+// and the conv state.  A conv-branch block owns 16 T channels, T / 2 k-steps of x_proj,
+// and leaves k_scan one split-K partial per k-step (32 channels), whatever T is, so every
+// batch size sums the same partials.  Two tiles give more, smaller workgroups (small
+// batches); four read each stream's activations half as often.
+template <bool Q8, bool Q8XP, bool PRE, bool GRP, int QP, int T>
 __global__ __launch_bounds__(kBlock) void k_mix_in(MixInArgs a) {
-    constexpr int G = kInGroups;
+    static_assert(kInGroups == 1 && (T == 2 || T == 4) && kWaves == 4, "one stream group, 2 or 4 tiles");
+    constexpr int E = T;                   // rows per lane in the finish
+    constexpr int WT = kWaves / T;         // waves per tile in the finish
+    constexpr int KS = T / 2;              // x_proj k-steps per block
+    typedef float fE __attribute__((ext_vector_type(E)));
+    typedef __bf16 bfE __attribute__((ext_vector_type(E)));
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ float invs[kInChunk];
     __bf16* lds = (__bf16*)smem;
     const int lane = threadIdx.x % kWave, wave = wave_index();
     const uint32_t b0 = blockIdx.y * kInChunk;
-    const int ng = (int)min((uint32_t)G, (a.n - b0 + kRowTile - 1) / kRowTile);
     const bool conv_branch = (int)blockIdx.x < a.nxb;
     const TMat& w = conv_branch ? a.wx : a.wz;
-    const int tb = (conv_branch ? blockIdx.x : blockIdx.x - a.nxb) * kWaves;  // the block's first row tile
-    const int t = tb + wave;                                                   // the tile this wave finishes
-    const bool has_rows = t < w.rt;
-    const int tc = min(t, w.rt - 1);
-    const int j0 = t * kRowTile + (lane / 16) * 4;  // this lane's 4 consecutive channels
+    const int tb = (conv_branch ? blockIdx.x : blockIdx.x - a.nxb) * T;  // the block's first row tile
+    // The rows this wave finishes and this lane's E rows and stream.
+    const int tf = wave / WT;
+    const int r0 = (wave % WT) * (kRowTile / WT) + (lane / 16) * E;  // row within the tile
+    const int ch = (tb + tf) * kRowTile + r0;                        // channel of the first row
+    const uint32_t b = b0 + lane % 16;
+    const bool has_rows = tb + tf < w.rt;
     const int dc = a.dc;
     // QP > 0: every wave takes exactly QP k-pairs (w.ks = 2 kWaves QP, checked on the host).
     const int np = w.ks / 2;
     const int p_lo = QP > 0 ? wave * QP : wave * np / kWaves, p_hi = QP > 0 ? p_lo + QP : (wave + 1) * np / kWaves;
-    // Slots by scalar loads, first: they do not count on the vector memory counter, so
-    // waiting for them before the conv state loads leaves every vector load in flight.
-    // The slot list is allocated in whole kSlotWordAlign blocks; a word past n feeds only
-    // a stream that is never stored (and is clamped below like any other).
-    uint32_t slot_raw[G];
-#pragma unroll
-    for (int g = 0; g < G; g++) {
+    // The stream's slot by scalar loads, first: they do not count on the vector memory
+    // counter.  The slot list is allocated in whole kSlotWordAlign blocks; a word past n
+    // feeds only a stream that is never stored (and is clamped like any other).
+    uint32_t slot_raw;
+    {
         // Constant address space: the list is read-only for this kernel, and uniform loads
         // from that space always go through the scalar unit.
         const __attribute__((address_space(4))) uint32_t* sp =
-            (const __attribute__((address_space(4))) uint32_t*)(a.slots + b0 + g * kRowTile);
+            (const __attribute__((address_space(4))) uint32_t*)(a.slots + b0);
         uint32_t sv[kRowTile];
 #pragma unroll
         for (int q = 0; q < kRowTile; q += 4) {
@@ -694,205 +708,201 @@ __global__ __launch_bounds__(kBlock) void k_mix_in(MixInArgs a) {
             // back into a per-lane vector load of the selected word.
             asm volatile("" : "+s"(sv[q]), "+s"(sv[q + 1]), "+s"(sv[q + 2]), "+s"(sv[q + 3]));
         }
-        uint32_t mine = sv[0];
+        slot_raw = sv[0];
 #pragma unroll
-        for (int i = 1; i < kRowTile; i++) mine = lane % 16 == i ? sv[i] : mine;
-        slot_raw[g] = mine;
+        for (int i = 1; i < kRowTile; i++) slot_raw = lane % 16 == i ? sv[i] : slot_raw;
     }
-    SspLoad sl;
-    // Vector loads in the order of first use (they complete in order): the quarter's
-    // weights and activations, then what the epilogue reads.
     constexpr int R = Q8 ? kInRingQ8 : kInRingF32;
-    Quarter<Q8, R> qw;
-    quarter_prefetch<Q8, R>(w, qw, tb, p_lo, p_hi - p_lo);
-    BQuarter<G> bq;
+    Quarter<Q8, R, T> qw;
+    quarter_prefetch<Q8, R, T>(w, qw, tb, p_lo, p_hi - p_lo);
+    BQuarter<1> bq;
+    SspLoad sl;
     if constexpr (PRE) {
-        bquarter_load<G, QP>(bq, a.xw, b0 / kRowTile, ng, a.wx.ks, p_lo, p_hi - p_lo);
+        bquarter_load<1, QP>(bq, a.xw, b0 / kRowTile, 1, a.wx.ks, p_lo, p_hi - p_lo);
         sl = ssp_load(a.ssp, a.tiles, b0, a.n, kInChunk);
     }
-    // Per-row scale of the finished tile (Q8 without column groups).
-    float4 rsc = make_float4(1.0f, 1.0f, 1.0f, 1.0f);
-    if (Q8 && !GRP) rsc = *(const float4*)(w.scales + tc * kRowTile + (lane / 16) * 4);
+    // Per-row scales of the lane's rows (Q8 without column groups); rows past the matrix
+    // read its last ones and are never stored.
+    const int chc = min(ch, w.rt * kRowTile - E);
+    fE rsc;
+#pragma unroll
+    for (int e = 0; e < E; e++) rsc[e] = 1.0f;
+    if (Q8 && !GRP) rsc = *(const fE*)(w.scales + chc);
     // Conv weights and bias of the lane's channels (used when dc = 4), loaded by every lane
     // from indices clamped into the arrays: no branch in the load prologue.
-    float cwv[4][4], cbv[4];
+    f32x4 cwv[E];
+    fE cbv;
     {
-        const int jc = min(j0, a.di - 4);
-        const float4* cw4 = (const float4*)(a.conv_w + min(jc * 4, a.di * dc - 16));
+        const int jc = min(ch, a.di - E);
+        const f32x4* cw4 = (const f32x4*)(a.conv_w + min(jc * 4, a.di * dc - 4 * E));
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float4 v = cw4[i];
-            cwv[i][0] = v.x; cwv[i][1] = v.y; cwv[i][2] = v.z; cwv[i][3] = v.w;
-        }
-        const float4 b4 = *(const float4*)(a.conv_b + jc);
-        cbv[0] = b4.x; cbv[1] = b4.y; cbv[2] = b4.z; cbv[3] = b4.w;
+        for (int e = 0; e < E; e++) cwv[e] = cw4[e];
+        cbv = *(const fE*)(a.conv_b + jc);
     }
-    // x_proj fragments of this block's k-pair: row tiles wave, wave + 4 (x_proj has at
-    // most kMaxXr / 16 = 6 row tiles), with their scales.
-    // Loaded by every block from clamped, in-bounds tiles (a gate-branch block or a tile
-    // past x_proj's rows reads tile 0 / the last tile and never uses it); the scale index
-    // is r * gs + p for column groups and r for one scale per row, without a branch.
+    // x_proj fragments of this block's k-pair (T = 4) or k-step p (T = 2: half p % 2 of
+    // pair p / 2): row tiles wave and wave + 4 (x_proj has at most kMaxXr / 16 = 6 row
+    // tiles), with their scales; loaded by every block from clamped, in-bounds tiles (a
+    // gate-branch block or a tile past x_proj's rows reads the last one and never uses it).
+    // Column-group scales take the block's 64-column group, one scale per row r.
+    const int p = min((int)blockIdx.x, a.nxb - 1);
+    const int xpair = p * KS / 2;
     RawPair xpw[2];
     float4 xps[2];
     {
-        const int p = min((int)blockIdx.x, a.nxb - 1);
         const bool grp = a.wxp.group != a.wxp.cols;
-        const size_t gs = grp ? (size_t)(a.wxp.ks / 2) : 1, po = grp ? (size_t)p : 0;
+        const size_t gs = grp ? (size_t)(a.wxp.ks / 2) : 1, po = grp ? (size_t)xpair : 0;
 #pragma unroll
         for (int k = 0; k < 2; k++) {
             const int tp = min(wave + kWaves * k, a.wxp.rt - 1);
-            xpw[k] = load_pair<Q8XP>(a.wxp, tp, p, lane);
+            xpw[k] = load_pair<Q8XP>(a.wxp, tp, xpair, lane);
             const size_t r = (size_t)tp * kRowTile + (lane / 16) * 4;
             xps[k] = Q8XP ? make_float4(a.wxp.scales[r * gs + po], a.wxp.scales[(r + 1) * gs + po],
                                         a.wxp.scales[(r + 2) * gs + po], a.wxp.scales[(r + 3) * gs + po])
                           : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
         }
     }
-    uint32_t slot_of[G];
-#pragma unroll
-    for (int g = 0; g < G; g++) slot_of[g] = conv_branch ? clamp_slot(slot_raw[g], a.cap) : 0u;
-    // Conv state (used when dc = 4 on the conv branch): three loads per group, issued by
-    // every wave, without a branch, from addresses clamped into the state buffer.
+    // Conv state of the lane's channels (used when dc = 4 on the conv branch): three loads
+    // of E floats from an offset clamped into the state buffer; streamed (non-temporal), as
+    // the state is read and written once per step.
+    const uint32_t slot = conv_branch ? clamp_slot(slot_raw, a.cap) : 0u;
     const size_t conv_floats = (size_t)a.cap * a.di * (dc - 1);
-    // Streamed (non-temporal): the state is read and written once per step.
-    f32x4 stv[G][3];
+    fE stv[3];
+    {
+        const size_t off = min(((size_t)slot * a.di + min(ch, a.di - E)) * 3, conv_floats - 3 * E);
+        const fE* sp = (const fE*)(a.conv_st + off);
 #pragma unroll
-    for (int g = 0; g < G; g++) {
-        const size_t off = min(((size_t)slot_of[g] * a.di + min(j0, a.di - 4)) * 3, conv_floats - 12);
-        const f32x4* sp = (const f32x4*)(a.conv_st + off);
-#pragma unroll
-        for (int k = 0; k < 3; k++) stv[g][k] = __builtin_nontemporal_load(sp + k);
+        for (int k = 0; k < 3; k++) stv[k] = __builtin_nontemporal_load(sp + k);
     }
+    // Every load above is issued before anything that waits for one of them.
+    __builtin_amdgcn_sched_barrier(0);
     if constexpr (!PRE) {
         stage_normed(lds, a.x, a.norm_w, a.norm_b, a.d, a.wx.ks, b0, a.n, kInChunk);
-        bquarter_lds<G>(bq, lds, a.wx.ks, p_lo, p_hi - p_lo);
+        bquarter_lds<1>(bq, lds, a.wx.ks, p_lo, p_hi - p_lo);
     }
 
-    f32x4 q4[kWaves][G];
-    quarter_gemm<Q8, GRP, R, G>(w, qw, tb, bq, p_lo, p_hi - p_lo, q4);
+    f32x4 q4[T][1];
+    quarter_gemm<Q8, GRP, R, T, 1>(w, qw, tb, bq, p_lo, p_hi - p_lo, q4);
     // The RMS scales are first needed after the barrier below.
     if constexpr (PRE) ssp_reduce(sl, invs, a.tiles, a.d, kInChunk);
-    // Quarters through LDS: red[src wave][tile][g][lane] (on the LayerNorm path over the
-    // staged activations, once every wave has read them).
+    // Quarters through LDS: red[src wave][tile][lane] in the MFMA D layout (on the
+    // LayerNorm path over the staged activations, once every wave has read them).
     if constexpr (!PRE) __syncthreads();
     f32x4* red = (f32x4*)smem;
 #pragma unroll
-    for (int i = 0; i < kWaves; i++) {
-        if (i == wave) continue;
-#pragma unroll
-        for (int g = 0; g < G; g++) red[((wave * kWaves + i) * G + g) * kWave + lane] = q4[i][g];
-    }
+    for (int i = 0; i < T; i++) red[(wave * T + i) * kWave + lane] = q4[i][0];
     __syncthreads();
-    f32x4 acc[G];
-#pragma unroll
-    for (int g = 0; g < G; g++) {
-        f32x4 s{0, 0, 0, 0};
+    // Rows r0 .. r0 + E - 1 of stream lane % 16 sit in D-layout lane (lane % 16) + 16 (r0 / 4),
+    // components r0 % 4 .. r0 % 4 + E - 1.
+    float v[E];
+    {
+        const int src_lane = lane % 16 + 16 * (r0 / 4);
+        const float* rf = (const float*)red;
+        fE sum;
 #pragma unroll
         for (int src = 0; src < kWaves; src++) {
-            f32x4 v;
-            if (src == wave) {
-#pragma unroll
-                for (int i = 0; i < kWaves; i++)
-                    if (i == wave) v = q4[i][g];
-            } else {
-                v = red[((src * kWaves + wave) * G + g) * kWave + lane];
-            }
-            s = src == 0 ? v : s + v;
+            const fE x = *(const fE*)(rf + ((src * T + tf) * kWave + src_lane) * 4 + r0 % 4);
+            sum = src == 0 ? x : sum + x;
         }
-        const float rs[4] = {rsc.x, rsc.y, rsc.z, rsc.w};
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            float v = s[e];
-            if (Q8 && !GRP) v = v * rs[e];
-            if constexpr (PRE) v = v * invs[g * kRowTile + lane % 16];
-            acc[g][e] = v;
+        for (int e = 0; e < E; e++) {
+            float y = sum[e];
+            if (Q8 && !GRP) y = y * rsc[e];
+            if constexpr (PRE) y = y * invs[lane % 16];
+            v[e] = y;
         }
     }
     if (!conv_branch) {
-        if (has_rows && j0 < a.di) {
+        if (has_rows && b < a.n) {
+            fE zv;
 #pragma unroll
-            for (int g = 0; g < G; g++) {
-                const uint32_t b = b0 + g * kRowTile + lane % 16;
-                if (g >= ng) continue;
-                if (b < a.n) *(float4*)(a.z + (size_t)b * a.di + j0) = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
-            }
+            for (int e = 0; e < E; e++) zv[e] = v[e];
+            *(fE*)(a.z + (size_t)b * a.di + ch) = zv;
         }
         return;
     }
     // Conv branch: conv1d step + SiLU per (channel, stream), conv_silu_block order
-    // (model.rs:134-153) and silu_inplace's 256-channel body/tail rule (tensor.rs:1207-1211).
-    __syncthreads();  // every wave has read its quarters
+    // (model.rs:134-153).  silu_inplace takes lane_sigmoid for the 8-aligned body of each
+    // 256-channel block and the scalar sigmoid for the rest (tensor.rs:1207-1211); d_inner
+    // comes in whole 64-channel blocks here, so every channel is in a body.
+    float uv[E];
 #pragma unroll
-    for (int g = 0; g < G; g++) {
-        const uint32_t b = b0 + g * kRowTile + lane % 16;
-        float uv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (g < ng && has_rows && b < a.n && j0 < a.di) {
-            const uint32_t s = slot_of[g];
-            if (dc == 4) {
-                float st[12] = {stv[g][0].x, stv[g][0].y, stv[g][0].z, stv[g][0].w, stv[g][1].x, stv[g][1].y,
-                                stv[g][1].z, stv[g][1].w, stv[g][2].x, stv[g][2].y, stv[g][2].z, stv[g][2].w};
+    for (int e = 0; e < E; e++) uv[e] = 0.0f;
+    if (has_rows && b < a.n) {
+        if (dc == 4) {
+            float st[3 * E];
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const float xv = acc[g][i];
-                    float val = 0.0f;
-                    val += st[3 * i] * cwv[i][0];
-                    val += st[3 * i + 1] * cwv[i][1];
-                    val += st[3 * i + 2] * cwv[i][2];
-                    val += xv * cwv[i][3];
-                    val += cbv[i];
-                    st[3 * i] = st[3 * i + 1];
-                    st[3 * i + 1] = st[3 * i + 2];
-                    st[3 * i + 2] = xv;
-                    uv[i] = val;
-                }
-                f32x4* sp = (f32x4*)(a.conv_st + ((size_t)s * a.di + j0) * 3);
-                __builtin_nontemporal_store(f32x4{st[0], st[1], st[2], st[3]}, sp);
-                __builtin_nontemporal_store(f32x4{st[4], st[5], st[6], st[7]}, sp + 1);
-                __builtin_nontemporal_store(f32x4{st[8], st[9], st[10], st[11]}, sp + 2);
-            } else {
+            for (int k = 0; k < 3; k++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int j = j0 + i;
-                    float* st = a.conv_st + ((size_t)s * a.di + j) * (dc - 1);
-                    const float* cw = a.conv_w + (size_t)j * dc;
-                    const float xv = acc[g][i];
-                    float val = 0.0f;
-                    for (int k = 0; k < dc - 1; k++) val += st[k] * cw[k];
-                    val += xv * cw[dc - 1];
-                    val += a.conv_b[j];
-                    for (int k = 0; k + 2 < dc; k++) st[k] = st[k + 1];
-                    st[dc - 2] = xv;
-                    uv[i] = val;
-                }
+                for (int e = 0; e < E; e++) st[k * E + e] = stv[k][e];
+#pragma unroll
+            for (int e = 0; e < E; e++) {
+                const float xv = v[e];
+                float val = 0.0f;
+                val += st[3 * e] * cwv[e][0];
+                val += st[3 * e + 1] * cwv[e][1];
+                val += st[3 * e + 2] * cwv[e][2];
+                val += xv * cwv[e][3];
+                val += cbv[e];
+                st[3 * e] = st[3 * e + 1];
+                st[3 * e + 1] = st[3 * e + 2];
+                st[3 * e + 2] = xv;
+                uv[e] = val;
             }
+            fE* sp = (fE*)(a.conv_st + ((size_t)slot * a.di + ch) * 3);
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int j = j0 + i;
-                const int blk0 = j / 256 * 256;
-                const int len = min(256, a.di - blk0);
-                const bool body = (j - blk0) < len / 8 * 8;
-                const float val = uv[i];
-                const float sg = body ? lane_sigmoid_f(val) : 1.0f / (1.0f + exp_f(-val));
-                uv[i] = val * sg;
+            for (int k = 0; k < 3; k++) {
+                fE o;
+#pragma unroll
+                for (int e = 0; e < E; e++) o[e] = st[k * E + e];
+                __builtin_nontemporal_store(o, sp + k);
             }
-            *(float4*)(a.u + (size_t)b * a.di + j0) = make_float4(uv[0], uv[1], uv[2], uv[3]);
-        }
-        // u as the B operand of x_proj over this block's 64 channels: two k-steps.
-        const int cl = wave * kRowTile + (lane / 16) * 4;  // local channel of uv[0]
+        } else {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int c = cl + i, s = c / kKStep;
-            const int ln = (lane % 16) + kRowTile * ((c % kKStep) / 8);
-            const Limb3 t3 = split3(uv[i]);
-            __bf16* dst = lds + ((size_t)(g * 2 + s) * 3) * 512 + ln * 8 + (c % 8);
-            dst[0] = t3.h;
-            dst[512] = t3.m;
-            dst[1024] = t3.l;
+            for (int e = 0; e < E; e++) {
+                const int j = ch + e;
+                float* st = a.conv_st + ((size_t)slot * a.di + j) * (dc - 1);
+                const float* cw = a.conv_w + (size_t)j * dc;
+                const float xv = v[e];
+                float val = 0.0f;
+                for (int k = 0; k < dc - 1; k++) val += st[k] * cw[k];
+                val += xv * cw[dc - 1];
+                val += a.conv_b[j];
+                for (int k = 0; k + 2 < dc; k++) st[k] = st[k + 1];
+                st[dc - 2] = xv;
+                uv[e] = val;
+            }
         }
+        fE uo;
+#pragma unroll
+        for (int e = 0; e < E; e++) {
+            uv[e] = uv[e] * lane_sigmoid_f(uv[e]);
+            uo[e] = uv[e];
+        }
+        *(fE*)(a.u + (size_t)b * a.di + ch) = uo;
+    }
+    // u as the B operand of x_proj over this block's 16 T channels (KS k-steps), past the
+    // quarters: local channel c = 16 tf + r0 (+ e) of stream lane % 16 goes to k-step c / 32,
+    // B lane (lane % 16) + 16 ((c % 32) / 8), element c % 8; a lane's E channels share it.
+    __bf16* xop = lds + T * kWaves * kWave * 8;   // past red (bf16 elements)
+    {
+        const int c = tf * kRowTile + r0;
+        const int ln = lane % 16 + kRowTile * ((c % kKStep) / 8);
+        bfE h, m, l;
+#pragma unroll
+        for (int e = 0; e < E; e++) {
+            const Limb3 t3 = split3(uv[e]);
+            h[e] = t3.h;
+            m[e] = t3.m;
+            l[e] = t3.l;
+        }
+        __bf16* dst = xop + (c / kKStep) * 3 * 512 + ln * 8 + c % 8;
+        *(bfE*)dst = h;
+        *(bfE*)(dst + 512) = m;
+        *(bfE*)(dst + 1024) = l;
     }
     __syncthreads();
-    // Split-K partial of x_proj: rows of x_proj against this block's channels.
-    const int p = blockIdx.x;  // k-pair index of x_proj = conv-branch block
+    // Split-K partials of x_proj, one per k-step (32 channels): its row tiles against
+    // this block's channels; partial block p KS + s.
 #pragma unroll
     for (int k = 0; k < 2; k++) {
         const int tp = wave + kWaves * k;
@@ -901,16 +911,13 @@ __global__ __launch_bounds__(kBlock) void k_mix_in(MixInArgs a) {
         decode_pair<Q8XP>(xpw[k], a0, a1);
         const float xs[4] = {xps[k].x, xps[k].y, xps[k].z, xps[k].w};
 #pragma unroll
-        for (int g = 0; g < G; g++) {
-            if (g >= ng) continue;
-            const __bf16* f0 = lds + ((size_t)(g * 2) * 3) * 512 + lane * 8;
-            const __bf16* f1 = f0 + 3 * 512;
+        for (int s = 0; s < KS; s++) {
+            const AFrag& af = KS == 2 ? (s ? a1 : a0) : (p % 2 ? a1 : a0);
+            const __bf16* f = xop + s * 3 * 512 + lane * 8;
             f32x4 part{0, 0, 0, 0};
-            part = mma_step<Q8XP>(a0, lds_frag(f0), lds_frag(f0 + 512), lds_frag(f0 + 1024), part);
-            part = mma_step<Q8XP>(a1, lds_frag(f1), lds_frag(f1 + 512), lds_frag(f1 + 1024), part);
-            const uint32_t b = b0 + g * kRowTile + lane % 16;
+            part = mma_step<Q8XP>(af, lds_frag(f), lds_frag(f + 512), lds_frag(f + 1024), part);
             if (b < a.n) {
-                float* dst = a.xpart + ((size_t)p * a.cap + b) * a.xr_pad + tp * kRowTile + (lane / 16) * 4;
+                float* dst = a.xpart + ((size_t)(p * KS + s) * a.cap + b) * a.xr_pad + tp * kRowTile + (lane / 16) * 4;
                 *(float4*)dst = make_float4(part[0] * xs[0], part[1] * xs[1], part[2] * xs[2], part[3] * xs[3]);
             }
         }
@@ -1119,12 +1126,13 @@ __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
 // The scan instance for a layer shape: Mamba-130M's (dt_rank 48, 24 x_proj blocks) is
 // specialised, every other shape takes the generic kernel.
 const void* scan_fn(bool q8dt, bool fast, int dr, int nxb) {
-    const bool m130 = dr == 48 && nxb == 24;
+    // Mamba-130M: dt_rank 48, 48 x_proj blocks of 32 channels.
+    const bool m130 = dr == 48 && nxb == 48;
     if (q8dt) {
-        if (m130) return fast ? (const void*)k_scan<true, true, 48, 24> : (const void*)k_scan<true, false, 48, 24>;
+        if (m130) return fast ? (const void*)k_scan<true, true, 48, 48> : (const void*)k_scan<true, false, 48, 48>;
         return fast ? (const void*)k_scan<true, true, 0, 0> : (const void*)k_scan<true, false, 0, 0>;
     }
-    if (m130) return fast ? (const void*)k_scan<false, true, 48, 24> : (const void*)k_scan<false, false, 48, 24>;
+    if (m130) return fast ? (const void*)k_scan<false, true, 48, 48> : (const void*)k_scan<false, false, 48, 48>;
     return fast ? (const void*)k_scan<false, true, 0, 0> : (const void*)k_scan<false, false, 0, 0>;
 }
 
@@ -1556,43 +1564,50 @@ namespace {
 
 uint32_t stage_lds_bytes(int ks) { return (uint32_t)(kGroups * ks * 3 * kLimbBytes); }
 
-// k_mix_in: the k-quarter partials and the x_proj operand, and on the LayerNorm path the
+// k_mix_in: the k-quarter partials, then the x_proj operand, and on the LayerNorm path the
 // staged activations of kInGroups column groups (the same area, reused).
-uint32_t mix_in_lds_bytes(int ks, bool pre) {
+uint32_t mix_in_lds_bytes(int ks, bool pre, int tiles) {
     const uint32_t acts = pre ? 0u : kInGroups * ks * 3 * kLimbBytes;
-    const uint32_t quarters = kWaves * kWaves * kInGroups * kWave * sizeof(f32x4);
-    const uint32_t xp_operand = kInGroups * 2 * 3 * kLimbBytes;
-    return std::max(acts, std::max(quarters, xp_operand));
+    const uint32_t quarters = kWaves * tiles * kWave * sizeof(f32x4);
+    const uint32_t xp_operand = (tiles / 2) * 3 * kLimbBytes;
+    return std::max(acts, quarters + xp_operand);
 }
 
-template <bool Q8, bool Q8XP, bool PRE, bool GRP, int QP>
-const void* mix_in_fn5(uint32_t lds) {
-    allow_lds(k_mix_in<Q8, Q8XP, PRE, GRP, QP>, lds);
-    return (const void*)k_mix_in<Q8, Q8XP, PRE, GRP, QP>;
+template <bool Q8, bool Q8XP, bool PRE, bool GRP, int QP, int T>
+const void* mix_in_fn6(uint32_t lds) {
+    allow_lds(k_mix_in<Q8, Q8XP, PRE, GRP, QP, T>, lds);
+    return (const void*)k_mix_in<Q8, Q8XP, PRE, GRP, QP, T>;
 }
 
 // Three k-pairs per wave (d = 768, Mamba-130M) is compiled as a fixed shape.
 constexpr int kInFixedPairs = 3;
 
+// The fixed shape and four-tile blocks are compiled for the pre-staged (RMSNorm) path,
+// where the activations go straight to registers; the LayerNorm path keeps the general
+// two-tile kernel.
 template <bool Q8, bool Q8XP, bool PRE, bool GRP>
-const void* mix_in_fn4(uint32_t lds, bool fixed) {
-    return fixed ? mix_in_fn5<Q8, Q8XP, PRE, GRP, kInFixedPairs>(lds) : mix_in_fn5<Q8, Q8XP, PRE, GRP, 0>(lds);
+const void* mix_in_fn4(uint32_t lds, bool fixed, int tiles) {
+    if constexpr (PRE) {
+        if (tiles == 4)
+            return fixed ? mix_in_fn6<Q8, Q8XP, PRE, GRP, kInFixedPairs, 4>(lds) : mix_in_fn6<Q8, Q8XP, PRE, GRP, 0, 4>(lds);
+        return fixed ? mix_in_fn6<Q8, Q8XP, PRE, GRP, kInFixedPairs, 2>(lds) : mix_in_fn6<Q8, Q8XP, PRE, GRP, 0, 2>(lds);
+    } else {
+        return mix_in_fn6<Q8, Q8XP, PRE, GRP, 0, 2>(lds);
+    }
 }
 
-// The fixed shape pays off with pre-staged activations (the copy is unrolled); the
-// LayerNorm path keeps the general one.
 template <bool Q8, bool Q8XP>
-const void* mix_in_fn2(bool pre, bool grp, bool fixed, uint32_t lds) {
-    if (pre) return grp ? mix_in_fn4<Q8, Q8XP, true, Q8>(lds, fixed) : mix_in_fn4<Q8, Q8XP, true, false>(lds, fixed);
-    return grp ? mix_in_fn5<Q8, Q8XP, false, Q8, 0>(lds) : mix_in_fn5<Q8, Q8XP, false, false, 0>(lds);
+const void* mix_in_fn2(bool pre, bool grp, bool fixed, int tiles, uint32_t lds) {
+    if (pre)
+        return grp ? mix_in_fn4<Q8, Q8XP, true, Q8>(lds, fixed, tiles) : mix_in_fn4<Q8, Q8XP, true, false>(lds, fixed, tiles);
+    return grp ? mix_in_fn4<Q8, Q8XP, false, Q8>(lds, false, 2) : mix_in_fn4<Q8, Q8XP, false, false>(lds, false, 2);
 }
 
-// grp: Q8 in_proj with 64-column scale groups.
-const void* mix_in_fn(bool q8, bool q8xp, bool pre, bool grp, bool fixed, uint32_t lds) {
-    if (q8 && q8xp) return mix_in_fn2<true, true>(pre, grp, fixed, lds);
-    if (q8) return mix_in_fn2<true, false>(pre, grp, fixed, lds);
-    if (q8xp) return mix_in_fn2<false, true>(pre, false, fixed, lds);
-    return mix_in_fn2<false, false>(pre, false, fixed, lds);
+const void* mix_in_fn(bool q8, bool q8xp, bool pre, bool grp, bool fixed, int tiles, uint32_t lds) {
+    if (q8 && q8xp) return mix_in_fn2<true, true>(pre, grp, fixed, tiles, lds);
+    if (q8) return mix_in_fn2<true, false>(pre, grp, fixed, tiles, lds);
+    if (q8xp) return mix_in_fn2<false, true>(pre, false, fixed, tiles, lds);
+    return mix_in_fn2<false, false>(pre, false, fixed, tiles, lds);
 }
 
 template <bool Q8>
@@ -1663,11 +1678,16 @@ void build_step(const ModelView& m, Pool& p, const StepIO& io, std::vector<Launc
     const int out_g = n >= (uint32_t)kOutWideFrom ? 2 : 1;
     const uint32_t out_chunks = (n + out_g * kRowTile - 1) / (out_g * kRowTile);
     const int xr_pad = m.layers[0].x_proj.rt * kRowTile;
-    const int nxb = di / 64;
     out.clear();
     // RMSNorm models take the pre-staged activation path; LayerNorm models norm in the
     // consumer.
     const bool pre = m.layers[0].norm_b == nullptr && m.norm_f_b == nullptr;
+    // k_mix_in row tiles per workgroup and its conv-branch blocks; x_proj's split-K
+    // partials stay 32-channel blocks (nxp) either way, so a stream's arithmetic does not
+    // depend on the choice.
+    const int in_tiles = pre && n >= (uint32_t)kInWideFrom ? 4 : 2;
+    const int nxb = di / (kRowTile * in_tiles);
+    const int nxp = di / kXpBlock;
     const int ks_x = m.layers[0].in_x.ks, tiles = d / kRowTile;
     io_index = (int)out.size();
     out.push_back(embed_launch(*m.emb, p, io, m.layers[0].norm_w, pre ? p.xw : nullptr, p.ssp, ks_x, tiles));
@@ -1675,20 +1695,20 @@ void build_step(const ModelView& m, Pool& p, const StepIO& io, std::vector<Launc
     const size_t ssm_layer = (size_t)p.cap * di * 16;
     const bool q8 = m.layers[0].in_x.group != 0;
     const bool q8xp = m.layers[0].x_proj.group != 0;
-    const uint32_t lds_in = mix_in_lds_bytes(ks_x, pre);
+    const uint32_t lds_in = mix_in_lds_bytes(ks_x, pre, in_tiles);
     const bool grp = q8 && m.layers[0].in_x.group != m.layers[0].in_x.cols;
     const bool fixed = ks_x == 2 * kWaves * kInFixedPairs && m.layers[0].in_z.ks == ks_x;
-    const void* fin = mix_in_fn(q8, q8xp, pre, grp, fixed, lds_in);
+    const void* fin = mix_in_fn(q8, q8xp, pre, grp, fixed, in_tiles, lds_in);
     for (uint32_t li = 0; li < D.nl; li++) {
         const DLayer& L = m.layers[li];
         MixInArgs ma{p.x, L.norm_w, L.norm_b, L.in_x, L.in_z, L.x_proj, nxb, p.conv + li * conv_layer,
                      L.conv_w, L.conv_b, p.slots, p.cap, n, p.u, p.z, p.xpart, di, (int)D.dc, d, xr_pad,
                      p.xw, p.ssp, tiles};
-        const int zb = L.in_z.rt / kWaves;
+        const int zb = L.in_z.rt / in_tiles;
         out.push_back(Launch::make(fin, dim3(nxb + zb, in_chunks), dim3(kBlock), lds_in, KC_MIX_IN, ma));
-        ScanArgs sa{p.xpart, nxb, xr_pad, (int)D.xr(), p.u, p.z, p.ssm + li * ssm_layer, L.dt_w, L.dt_q,
+        ScanArgs sa{p.xpart, nxp, xr_pad, (int)D.xr(), p.u, p.z, p.ssm + li * ssm_layer, L.dt_w, L.dt_q,
                     L.dt_scales, L.dt_pad, L.dt_b, L.a_exp, L.d_vec, p.slots, p.cap, n, p.glimb, di, (int)D.dr};
-        const void* fs = scan_fn(L.dt_q != nullptr, !m.exact_scan, (int)D.dr, nxb);
+        const void* fs = scan_fn(L.dt_q != nullptr, !m.exact_scan, (int)D.dr, nxp);
         out.push_back(Launch::make(fs, dim3((di + kBlock - 1) / kBlock, n), dim3(kBlock), 0, KC_SCAN, sa));
         const float* nw_next = li + 1 < D.nl ? m.layers[li + 1].norm_w : m.norm_f_w;
         MixOutArgs oa{L.out_proj, p.glimb, p.x, n, d, nw_next, pre ? p.xw : nullptr, p.ssp, ks_x, tiles};
