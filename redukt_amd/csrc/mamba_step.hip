@@ -1155,7 +1155,10 @@ struct MixOutArgs {
 // weight and activation fragments requested at once; the eighths are added in wave order,
 // then the per-row scale, then the residual: x += (((q0 + q1) + q2) + ... + q7).  The new
 // residual rows then leave as the next projection's pre-staged activations.
-template <bool Q8, int G>
+// FIXED: every wave takes exactly kOutPairs k-pairs (w.ks = 2 kOutWaves kOutPairs, checked
+// on the host), one pass whose loads are all issued unconditionally (clamped group and
+// row indices), the epilogue operands after them, before the first wait.
+template <bool Q8, int G, bool FIXED>
 __global__ __launch_bounds__(kOutWaves * kWave) void k_mix_out(MixOutArgs a) {
     __shared__ f32x4 part[kOutWaves - 1][G][kWave];
     const int lane = threadIdx.x % kWave, wave = wave_index();
@@ -1169,10 +1172,86 @@ __global__ __launch_bounds__(kOutWaves * kWave) void k_mix_out(MixOutArgs a) {
     const int gpr = w.ks / 2;
     const uint32_t g0 = b0 / kRowTile;
     const int r0 = t * kRowTile + (lane / 16) * 4;
-    // Epilogue operands of wave 0, requested with the rest.
     float4 xv[G];
     float rs[4] = {1.0f, 1.0f, 1.0f, 1.0f};
     float4 w4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    f32x4 acc3[G][3];
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+        for (int o = 0; o < 3; o++) acc3[g][o] = f32x4{0, 0, 0, 0};
+    if constexpr (FIXED) {
+        RawPair raw[kOutPairs];
+        bf16x8 bfr[kOutPairs][G][2][3];
+        float sc[kOutPairs][4];
+#pragma unroll
+        for (int q = 0; q < kOutPairs; q++) {
+            const int p = wave * kOutPairs + q;
+            raw[q] = load_pair<Q8>(w, t, p, lane);
+#pragma unroll
+            for (int g = 0; g < G; g++) {
+                const uint32_t gg = g0 + (G > 1 ? (uint32_t)min(g, ng - 1) : 0u);
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const __bf16* f = a.glimb + (((size_t)gg * w.ks + 2 * p + h) * 3) * 512 + lane * 8;
+                    bfr[q][g][h][0] = lds_frag(f);
+                    bfr[q][g][h][1] = lds_frag(f + 512);
+                    bfr[q][g][h][2] = lds_frag(f + 1024);
+                }
+            }
+            if (grp) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) sc[q][i] = w.scales[(size_t)(t * kRowTile + (lane / 16) * 4 + i) * gpr + p];
+            }
+        }
+        // Epilogue operands (used by wave 0), loaded by every wave from clamped rows.
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            const uint32_t b = min(b0 + g * kRowTile + lane % 16, a.n - 1);
+            xv[g] = *(const float4*)(a.x + (size_t)b * a.d + r0);
+        }
+        if (Q8 && !grp) {
+            const float4 r4 = *(const float4*)(w.scales + t * kRowTile + (lane / 16) * 4);
+            rs[0] = r4.x; rs[1] = r4.y; rs[2] = r4.z; rs[3] = r4.w;
+        }
+        if (a.xw != nullptr) w4 = *(const float4*)(a.nw_next + r0);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int q = 0; q < kOutPairs; q++) {
+            AFrag a0, a1;
+            decode_pair<Q8>(raw[q], a0, a1);
+#pragma unroll
+            for (int g = 0; g < G; g++) {
+                if (g >= ng) continue;
+                if (grp) {
+                    f32x4 pp{0, 0, 0, 0};
+                    pp = mma_step<Q8>(a0, bfr[q][g][0][0], bfr[q][g][0][1], bfr[q][g][0][2], pp);
+                    pp = mma_step<Q8>(a1, bfr[q][g][1][0], bfr[q][g][1][1], bfr[q][g][1][2], pp);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) acc3[g][0][i] = __builtin_fmaf(pp[i], sc[q][i], acc3[g][0][i]);
+                } else {
+#pragma unroll
+                    for (int h = 0; h < 2; h++) {
+                        const AFrag& af = h ? a1 : a0;
+                        const bf16x8* bb = bfr[q][g][h];
+                        if (Q8) {
+                            acc3[g][0] = mma(af.h, bb[0], acc3[g][0]);
+                            acc3[g][1] = mma(af.h, bb[1], acc3[g][1]);
+                            acc3[g][2] = mma(af.h, bb[2], acc3[g][2]);
+                        } else {
+                            acc3[g][0] = mma(af.h, bb[0], acc3[g][0]);
+                            acc3[g][1] = mma(af.h, bb[1], acc3[g][1]);
+                            acc3[g][1] = mma(af.m, bb[0], acc3[g][1]);
+                            acc3[g][2] = mma(af.h, bb[2], acc3[g][2]);
+                            acc3[g][2] = mma(af.m, bb[1], acc3[g][2]);
+                            acc3[g][2] = mma(af.l, bb[0], acc3[g][2]);
+                        }
+                    }
+                }
+            }
+        }
+    } else {
+    // Epilogue operands of wave 0, requested with the rest.
     if (wave == 0) {
 #pragma unroll
         for (int g = 0; g < G; g++) {
@@ -1186,11 +1265,6 @@ __global__ __launch_bounds__(kOutWaves * kWave) void k_mix_out(MixOutArgs a) {
         }
         if (a.xw != nullptr && r0 < a.d) w4 = *(const float4*)(a.nw_next + r0);
     }
-    f32x4 acc3[G][3];
-#pragma unroll
-    for (int g = 0; g < G; g++)
-#pragma unroll
-        for (int o = 0; o < 3; o++) acc3[g][o] = f32x4{0, 0, 0, 0};
 #pragma unroll 1
     for (int pb = p_lo; pb < p_hi; pb += kOutPairs) {
         RawPair raw[kOutPairs];
@@ -1253,6 +1327,7 @@ __global__ __launch_bounds__(kOutWaves * kWave) void k_mix_out(MixOutArgs a) {
                 }
             }
         }
+    }
     }
     f32x4 acc[G];
 #pragma unroll
@@ -1603,6 +1678,16 @@ const void* mix_in_fn2(bool pre, bool grp, bool fixed, int tiles, uint32_t lds) 
     return grp ? mix_in_fn4<Q8, Q8XP, false, Q8>(lds, false, 2) : mix_in_fn4<Q8, Q8XP, false, false>(lds, false, 2);
 }
 
+// k_mix_out: the fixed shape (kOutPairs k-pairs per wave) where out_proj's k-steps fit it.
+const void* mix_out_fn(bool q8, int groups, bool fixed) {
+    if (q8) {
+        if (groups == 2) return fixed ? (const void*)k_mix_out<true, 2, true> : (const void*)k_mix_out<true, 2, false>;
+        return fixed ? (const void*)k_mix_out<true, 1, true> : (const void*)k_mix_out<true, 1, false>;
+    }
+    if (groups == 2) return fixed ? (const void*)k_mix_out<false, 2, true> : (const void*)k_mix_out<false, 2, false>;
+    return fixed ? (const void*)k_mix_out<false, 1, true> : (const void*)k_mix_out<false, 1, false>;
+}
+
 const void* mix_in_fn(bool q8, bool q8xp, bool pre, bool grp, bool fixed, int tiles, uint32_t lds) {
     if (q8 && q8xp) return mix_in_fn2<true, true>(pre, grp, fixed, tiles, lds);
     if (q8) return mix_in_fn2<true, false>(pre, grp, fixed, tiles, lds);
@@ -1712,8 +1797,7 @@ void build_step(const ModelView& m, Pool& p, const StepIO& io, std::vector<Launc
         out.push_back(Launch::make(fs, dim3((di + kBlock - 1) / kBlock, n), dim3(kBlock), 0, KC_SCAN, sa));
         const float* nw_next = li + 1 < D.nl ? m.layers[li + 1].norm_w : m.norm_f_w;
         MixOutArgs oa{L.out_proj, p.glimb, p.x, n, d, nw_next, pre ? p.xw : nullptr, p.ssp, ks_x, tiles};
-        const void* fo = q8 ? (out_g == 2 ? (const void*)k_mix_out<true, 2> : (const void*)k_mix_out<true, 1>)
-                            : (out_g == 2 ? (const void*)k_mix_out<false, 2> : (const void*)k_mix_out<false, 1>);
+        const void* fo = mix_out_fn(q8, out_g, m.layers[0].out_proj.ks == 2 * kOutWaves * kOutPairs);
         out.push_back(Launch::make(fo, dim3(L.out_proj.rt, out_chunks), dim3(kOutWaves * kWave), 0, KC_MIX_OUT, oa));
     }
     const TMat& H = *m.head;
