@@ -987,6 +987,7 @@ template <bool Q8DT, bool FAST, int DR, int NXB>
 __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
     static_assert(DR >= 0 && DR <= kMaxDr && NXB >= 0 && NXB <= kMaxNxb, "scan shape");
     __shared__ float zp[kMaxXr];
+    __shared__ float zq[(DR && NXB) ? kBlock / (DR + 32) : 1][kMaxXr];
     constexpr int kDr = DR ? DR : kMaxDr;
     constexpr int kNxb = NXB ? NXB : kMaxNxb;
     const int di = a.di, dr = DR ? DR : a.dr, nxb = NXB ? NXB : a.nxb;
@@ -1028,18 +1029,28 @@ __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
 #pragma unroll
         for (int q = 0; q < kRowVecs; q++) wraw[q] = buf_ld_i4(rd, j16, (uint32_t)(DR ? q : min(q, row_vecs - 1)) * 16u * diu);
     }
-    // x_proj partials of this stream, summed in block order.  Every thread loads and sums
-    // (threads past xr re-read row 0), only threads < xr store: the loads stay in
-    // straight-line code.  The partial array is < 4 GiB, so offsets are 32-bit.
+    // x_proj partials of this stream.  With a fixed shape, kParts threads share each
+    // output, thread (part, o) summing blocks [part kPer, (part + 1) kPer) in block order;
+    // the parts are then added in part order.  Otherwise thread o < xr sums all blocks in
+    // order.  Every thread loads (threads past the outputs re-read row 0, block 0), only
+    // output threads store: the loads stay in straight-line code.  The partial array is
+    // < 4 GiB, so offsets are 32-bit.
+    constexpr int kParts = (DR && NXB) ? kBlock / (DR + 32) : 1;
+    constexpr int kPer = (kNxb + kParts - 1) / kParts;
+    static_assert(!(DR && NXB) || kParts * kPer == NXB, "whole parts");
     const int r = threadIdx.x;
-    const bool part_lane = r < a.xr;
-    float pv[kNxb];
+    const int o = kParts > 1 ? r % (DR + 32) : r, part = kParts > 1 ? r / (DR + 32) : 0;
+    const bool part_lane = part < kParts && o < a.xr;
+    float pv[kPer];
     {
-        const uint32_t o0 = (b * (uint32_t)a.xr_pad + (uint32_t)(part_lane ? r : 0)) * 4u;
+        // The lane's first block goes into the per-lane offset; block i of the part is a
+        // uniform offset on top (a buffer access's scalar offset must be wave-uniform).
         const uint32_t pstride = (uint32_t)a.cap * (uint32_t)a.xr_pad * 4u;
+        const uint32_t o0 = (b * (uint32_t)a.xr_pad + (uint32_t)(part_lane ? o : 0)) * 4u +
+                            (uint32_t)(part_lane ? part * kPer : 0) * pstride;
         const BufRsrc rp = buf_rsrc(a.xpart, (uint32_t)nxb * pstride);
 #pragma unroll
-        for (int u = 0; u < kNxb; u++) pv[u] = buf_ld_f32(rp, o0, (uint32_t)(NXB ? u : min(u, nxb - 1)) * pstride);
+        for (int i = 0; i < kPer; i++) pv[i] = buf_ld_f32(rp, o0, (uint32_t)(NXB ? i : min(i, nxb - 1)) * pstride);
     }
     const uint32_t s = clamp_slot(slot_raw, a.cap);
     const BufRsrc rs = buf_rsrc(a.ssm + (size_t)s * 16 * diu, 16u * row4);
@@ -1049,11 +1060,20 @@ __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
     {
         float acc = 0.0f;
 #pragma unroll
-        for (int u = 0; u < kNxb; u++)
-            if (NXB || u < nxb) acc += pv[u];
-        if (part_lane) zp[r] = acc;
+        for (int i = 0; i < kPer; i++)
+            if (NXB || i < nxb) acc += pv[i];
+        if (part_lane) (kParts > 1 ? zq[part] : zp)[o] = acc;
     }
     __syncthreads();
+    if constexpr (kParts > 1) {
+        if (r < a.xr) {
+            float z = zq[0][r];
+#pragma unroll
+            for (int q = 1; q < kParts; q++) z = z + zq[q][r];
+            zp[r] = z;
+        }
+        __syncthreads();
+    }
     if (!live) return;
     float wdt[kRowVecs * (Q8DT ? 16 : 4)];
 #pragma unroll
