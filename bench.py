@@ -58,19 +58,19 @@ def weight_bytes(dims: rbin.MambaDims, profile: int) -> dict:
 
 def algorithmic_bytes(dims: rbin.MambaDims, profile: int, n: int) -> dict:
     """Compulsory HBM bytes of one launch of each kernel class at n streams: weights once,
-    every activation and state element read or written once."""
+    every activation and state element read or written once.  x_proj's output counts once
+    (written by mix_in, read by scan), not the split-K partials the kernels pass."""
     d, di, xr, V, dc = dims.d_model, dims.d_inner, dims.xr, dims.vocab, dims.d_conv
     w = weight_bytes(dims, profile)
     f = 4
-    nxb = di // 64
     emb_row = d * f if profile & 3 == 0 else d + (4 if profile & 3 == 2 else d // 64 * f)
     return {
         "embed": n * (emb_row + d * f),
-        # norm weights, in_proj, x_proj; x in; conv state in+out; conv w/b; u, z, x_proj partials out
+        # norm weights, in_proj, x_proj; x in; conv state in+out; conv w/b; u, z, x_proj output out
         "mix_in": d * f + w["in_proj"] + w["x_proj"] + n * d * f + n * 2 * di * (dc - 1) * f + di * (dc + 1) * f
-        + n * 2 * di * f + nxb * n * xr * f,
-        # partials in; dt_proj, dt_b, exp(A_log), D; u, z in; ssm state in+out; gated limbs out
-        "scan": nxb * n * xr * f + w["dt_proj"] + di * f + di * 16 * f + di * f + n * 2 * di * f
+        + n * 2 * di * f + n * xr * f,
+        # x_proj output in; dt_proj, dt_b, exp(A_log), D; u, z in; ssm state in+out; gated limbs out
+        "scan": n * xr * f + w["dt_proj"] + di * f + di * 16 * f + di * f + n * 2 * di * f
         + n * 2 * di * 16 * f + n * di * 3 * 2,
         # out_proj; gated limbs in; residual in+out
         "mix_out": w["out_proj"] + n * di * 3 * 2 + 2 * n * d * f,
