@@ -1536,11 +1536,36 @@ __global__ __launch_bounds__(kHwWaves * kWave) void k_head_ws(HeadArgs a) {
             raw.v[0] = p < np ? wq[p][i] : make_int4(0, 0, 0, 0);
             decode_pair<true>(raw, wd[p][i][0], wd[p][i][1]);
         }
+    // Group gi's logits leave one iteration later, right after group gi + 2's copy is
+    // requested: the wait at the top of an iteration (vector loads and stores share one
+    // counter) then finds them issued a whole product earlier instead of just before.
+    f32x4 held[kHwTiles];
+    auto store_group = [&](int g) {
+        const uint32_t b = (gb + g) * kRowTile + lane % 16;
+        const float inv = invs[g * kRowTile + lane % 16];
+#pragma unroll
+        for (int i = 0; i < kHwTiles; i++) {
+            const int t = t0 + i;
+            const int r0 = t * kRowTile + (lane / 16) * 4;
+            if (t >= w.rt || b >= a.n) continue;
+            const float v[4] = {held[i][0] * rsc[i].x * inv, held[i][1] * rsc[i].y * inv, held[i][2] * rsc[i].z * inv,
+                                held[i][3] * rsc[i].w * inv};
+            float* o = a.out + (size_t)b * V + r0;
+            // Logits are written once and read later (host copy, softmax): streamed.
+            if (r0 + 3 < V && (V & 3) == 0) {
+                __builtin_nontemporal_store(f32x4{v[0], v[1], v[2], v[3]}, (f32x4*)o);
+            } else {
+                for (int e = 0; e < 4; e++)
+                    if (r0 + e < V) __builtin_nontemporal_store(v[e], o + e);
+            }
+        }
+    };
 #pragma unroll 1
     for (int gi = 0; gi < ngr; gi++) {
-        __builtin_amdgcn_s_waitcnt(0);  // this wave's copies (and earlier stores) are done
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's copies and its stores of two groups back
         __syncthreads();                // every wave's copies of group gi, and reads of gi - 1
         if (gi + 1 < ngr) copy_group(smem + ((gi + 1) & 1) * buf_bytes, a.xw, gb + gi + 1, ks);
+        if (gi > 0) store_group(gi - 1);
         const __bf16* lds = (const __bf16*)(smem + (gi & 1) * buf_bytes);
         f32x4 acc[kHwTiles];
 #pragma unroll
@@ -1564,25 +1589,10 @@ __global__ __launch_bounds__(kHwWaves * kWave) void k_head_ws(HeadArgs a) {
                     for (int i = 0; i < kHwTiles; i++)
                         acc[i] = mma_prod<true>(j, wd[p][i][h], bf[h][0], bf[h][1], bf[h][2], acc[i]);
         }
-        const uint32_t b = (gb + gi) * kRowTile + lane % 16;
-        const float inv = invs[gi * kRowTile + lane % 16];
 #pragma unroll
-        for (int i = 0; i < kHwTiles; i++) {
-            const int t = t0 + i;
-            const int r0 = t * kRowTile + (lane / 16) * 4;
-            if (t >= w.rt || b >= a.n) continue;
-            const float v[4] = {acc[i][0] * rsc[i].x * inv, acc[i][1] * rsc[i].y * inv, acc[i][2] * rsc[i].z * inv,
-                                acc[i][3] * rsc[i].w * inv};
-            float* o = a.out + (size_t)b * V + r0;
-            // Logits are written once and read later (host copy, softmax): streamed.
-            if (r0 + 3 < V && (V & 3) == 0) {
-                __builtin_nontemporal_store(f32x4{v[0], v[1], v[2], v[3]}, (f32x4*)o);
-            } else {
-                for (int e = 0; e < 4; e++)
-                    if (r0 + e < V) __builtin_nontemporal_store(v[e], o + e);
-            }
-        }
+        for (int i = 0; i < kHwTiles; i++) held[i] = acc[i];
     }
+    if (ngr > 0) store_group(ngr - 1);
 }
 
 // ---------------------------------------------------------------- softmax
