@@ -116,16 +116,17 @@ def test_batch_invariance_any_n_position_slot(models, profile):
     with ffi.PluginBackend(models["reftest"], profile=profile) as be:
         v = be.vocab
         seq = [(13 * i + 5) % v for i in range(5)]
-        be.batch_init(64)
+        be.batch_init(72)
         alone = []
         for t in seq:
             g = np.empty((1, v), np.float32)
-            be.forward_batch([63], [t], g)
+            be.forward_batch([71], [t], g)
             alone.append(g[0].copy())
         rng = np.random.default_rng(1)
-        for n, pos in ((2, 1), (7, 3), (33, 32), (63, 0)):
+        # n >= 64 takes the four-tile in_proj blocks, n < 64 the two-tile ones
+        for n, pos in ((2, 1), (7, 3), (33, 32), (63, 0), (64, 40), (71, 70)):
             be.batch_reset(None)
-            slots = [int(s) for s in rng.permutation(63)[:n]]
+            slots = [int(s) for s in rng.permutation(71)[:n]]
             for i, t in enumerate(seq):
                 toks = [int(x) for x in rng.integers(0, v, n)]
                 toks[pos] = t
@@ -254,6 +255,18 @@ def test_mamba130m_parity(full_model, profile):
         outs = run_lockstep(be, orc, 4, 6, lambda s, t: int(toks[t, s]))
         worst = max(assert_parity(g, c, f"130M p{profile} step {t}") for t, (g, c) in enumerate(outs))
         print(f"Mamba-130M profile {profile}: worst max|dlogit|={worst[0]:.3e} L1={worst[1]:.3e}")
+        orc.close()
+
+
+def test_mamba130m_parity_64_streams(full_model):
+    # 64 streams take the four-tile in_proj blocks; the oracle checks every stream.
+    with ffi.PluginBackend(full_model, profile=6) as be:
+        orc = O.MambaOracle(full_model, 6, cap=64)
+        rng = np.random.default_rng(4)
+        toks = synth.zipf_tokens(rng, be.vocab, (2, 64))
+        outs = run_lockstep(be, orc, 64, 2, lambda s, t: int(toks[t, s]))
+        worst = max(assert_parity(g, c, f"130M n64 step {t}") for t, (g, c) in enumerate(outs))
+        print(f"Mamba-130M 64 streams: worst max|dlogit|={worst[0]:.3e} L1={worst[1]:.3e}")
         orc.close()
 
 
