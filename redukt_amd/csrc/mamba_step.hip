@@ -712,7 +712,8 @@ __global__ __launch_bounds__(kBlock) void k_mix_in(MixInArgs a) {
 #pragma unroll
         for (int i = 1; i < kRowTile; i++) slot_raw = lane % 16 == i ? sv[i] : slot_raw;
     }
-    constexpr int R = Q8 ? kInRingQ8 : kInRingF32;
+    // The ring holds a Q8 quarter whole: exactly QP pairs when the shape is fixed.
+    constexpr int R = Q8 ? (QP > 0 ? QP : kInRingQ8) : kInRingF32;
     Quarter<Q8, R, T> qw;
     quarter_prefetch<Q8, R, T>(w, qw, tb, p_lo, p_hi - p_lo);
     BQuarter<1> bq;
