@@ -64,7 +64,7 @@ constexpr int kMaxSegs = 8;
 constexpr int kMaxShiftMix = 6;
 
 __device__ __forceinline__ float block_sum256(float v, float* sh) {
-    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave, wave = wave_index();
     v = wave_sum(v);
     if (lane == 0) sh[wave] = v;
     __syncthreads();
@@ -174,7 +174,7 @@ __device__ __forceinline__ float activate(int act, float v, int r, int len) {
 // fragments requested at once; the eighths are added in wave order, then the row scale.
 template <bool Q8>
 __device__ __forceinline__ void proj_tile(const ProjSeg& sg, int t, uint32_t n, f32x4 (*part)[kWave]) {
-    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave, wave = wave_index();
     const uint32_t b0 = blockIdx.y * kRowTile;
     const TMat& w = sg.w;
     const int np = w.ks / 2;
@@ -262,11 +262,19 @@ __device__ __forceinline__ void proj_tile(const ProjSeg& sg, int t, uint32_t n, 
         return;
     }
     if (!ok) return;
+    float* o = sg.out + (size_t)b * sg.ld + r0;
+    if (r0 + 3 < w.rows && ((sg.ld | r0) & 3) == 0 && ((uintptr_t)sg.out & 15) == 0) {
+        // The lane's four rows in one 16-byte access (row-major out, 16-byte aligned rows).
+        f32x4 y = *(f32x4*)o;
+#pragma unroll
+        for (int i = 0; i < 4; i++) y[i] = sg.mode == PROJ_RESID ? y[i] + v[i] : v[i];
+        *(f32x4*)o = y;
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         if (r0 + i >= w.rows) continue;
-        float* o = sg.out + (size_t)b * sg.ld + r0 + i;
-        *o = sg.mode == PROJ_RESID ? *o + v[i] : v[i];
+        o[i] = sg.mode == PROJ_RESID ? o[i] + v[i] : v[i];
     }
 }
 
