@@ -956,8 +956,9 @@ struct ScanArgs {
 // x * log2 e; about 1e-7 relative) instead of the reference's portable exp, which is
 // about 30 VALU operations each and most of this kernel's instruction stream.  Every
 // other element-wise operation keeps the reference's arithmetic.  DR and NXB fix dt_rank
-// and the number of 64-channel x_proj blocks at compile time (0: taken from the
+// and the number of 32-channel x_proj partials at compile time (0: taken from the
 // arguments, bounded by kMaxDr / kMaxNxb), which removes the guards of the unrolled loops.
+// A thread runs SPT streams of one channel.
 // Raw buffer access: a descriptor with a uniform base and an exact byte size (gfx9 word 3:
 // 32-bit data format, untyped), a per-lane 32-bit byte offset and a uniform byte offset.
 // Offsets past the size read 0 and drop stores, so every descriptor covers its array.
@@ -984,11 +985,13 @@ __device__ __forceinline__ void buf_st_f32(float v, BufRsrc r, uint32_t voff, ui
 
 __device__ __forceinline__ float hw_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
 
-template <bool Q8DT, bool FAST, int DR, int NXB>
+template <bool Q8DT, bool FAST, int DR, int NXB, int SPT>
 __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
-    static_assert(DR >= 0 && DR <= kMaxDr && NXB >= 0 && NXB <= kMaxNxb, "scan shape");
-    __shared__ float zp[kMaxXr];
-    __shared__ float zq[(DR && NXB) ? kBlock / (DR + 32) : 1][kMaxXr];
+    static_assert(DR >= 0 && DR <= kMaxDr && NXB >= 0 && NXB <= kMaxNxb && SPT >= 1 && SPT <= 2, "scan shape");
+    // SPT streams per thread (streams SPT y .. SPT y + SPT - 1 of channel j): the channel's
+    // operands (exp(A_log), the dt_proj row, biases, D) are loaded and decoded once for all
+    // of them.  Every stream's arithmetic is the same whatever SPT is.
+    constexpr int kParts = (DR && NXB) ? 3 : 1;  // threads per x_proj output (fixed shape)
     constexpr int kDr = DR ? DR : kMaxDr;
     constexpr int kNxb = NXB ? NXB : kMaxNxb;
     const int di = a.di, dr = DR ? DR : a.dr, nxb = NXB ? NXB : a.nxb;
@@ -1001,13 +1004,18 @@ __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
     const uint32_t ju = (uint32_t)j, diu = (uint32_t)di;
     const uint32_t j4 = ju * 4u, j16 = ju * 16u;
     const uint32_t row4 = diu * 4u;  // bytes of one [di] row
-    const uint32_t b = blockIdx.y;
-    // Requested in this order, all before the first wait: the slot, the slot-independent
-    // per-channel operands, the x_proj partials, then the state once the slot is known
-    // (vector loads return in order, so waiting for the slot does not wait for the rest).
-    // Loads past a short row or partial list read its last element instead of branching;
-    // those values are never used.
-    const uint32_t slot_raw = a.slots[b];
+    const uint32_t bs0 = blockIdx.y * SPT;  // first stream; streams past n load stream n - 1
+    uint32_t bs[SPT];
+#pragma unroll
+    for (int s = 0; s < SPT; s++) bs[s] = min(bs0 + s, a.n - 1);
+    // Requested in this order, all before the first wait: the slots, the slot-independent
+    // operands, the x_proj partials, then the state once the slots are known (vector loads
+    // return in order, so waiting for the slots does not wait for the rest).  Loads past a
+    // short row or partial list read its last element instead of branching; those values
+    // are never used.
+    uint32_t slot_raw[SPT];
+#pragma unroll
+    for (int s = 0; s < SPT; s++) slot_raw[s] = a.slots[bs[s]];
     // State-major operands ([16][di]): for each n the wave's 64 channels are one
     // contiguous 256-byte run, so every load and store below is fully coalesced.
     float av[16];
@@ -1016,8 +1024,15 @@ __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
 #pragma unroll
         for (int n = 0; n < 16; n++) av[n] = buf_ld_f32(ra, j4, (uint32_t)n * row4);
     }
-    const float x = buf_ld_f32(buf_rsrc(a.u + (size_t)b * diu, row4), j4, 0);
-    const float zz = buf_ld_f32(buf_rsrc(a.z + (size_t)b * diu, row4), j4, 0);
+    float x[SPT], zz[SPT];
+    {
+        const BufRsrc ru = buf_rsrc(a.u, (uint32_t)a.n * row4), rz = buf_rsrc(a.z, (uint32_t)a.n * row4);
+#pragma unroll
+        for (int s = 0; s < SPT; s++) {
+            x[s] = buf_ld_f32(ru, j4, bs[s] * row4);
+            zz[s] = buf_ld_f32(rz, j4, bs[s] * row4);
+        }
+    }
     const float dv = buf_ld_f32(buf_rsrc(a.d_vec, row4), j4, 0);
     const float dtb = buf_ld_f32(buf_rsrc(a.dt_b, row4), j4, 0);
     const float dts = Q8DT ? buf_ld_f32(buf_rsrc(a.dt_scales, row4), j4, 0) : 1.0f;
@@ -1030,48 +1045,70 @@ __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
 #pragma unroll
         for (int q = 0; q < kRowVecs; q++) wraw[q] = buf_ld_i4(rd, j16, (uint32_t)(DR ? q : min(q, row_vecs - 1)) * 16u * diu);
     }
-    // x_proj partials of this stream.  With a fixed shape, kParts threads share each
-    // output, thread (part, o) summing blocks [part kPer, (part + 1) kPer) in block order;
-    // the parts are then added in part order.  Otherwise thread o < xr sums all blocks in
-    // order.  Every thread loads (threads past the outputs re-read row 0, block 0), only
-    // output threads store: the loads stay in straight-line code.  The partial array is
-    // < 4 GiB, so offsets are 32-bit.
-    constexpr int kParts = (DR && NXB) ? kBlock / (DR + 32) : 1;
+    // x_proj partials of the block's streams.  With a fixed shape, kParts threads share
+    // each (stream, output), item (s, part, o) summing blocks [part kPer, (part + 1) kPer)
+    // in block order; the parts are then added in part order.  Otherwise item (s, o) sums
+    // all blocks in order.  Thread r takes items r, r + kBlock, ...; every thread loads
+    // for all of its item slots (items past the last re-read row 0, block 0), only real
+    // items store: the loads stay in straight-line code.  The partial array is < 4 GiB,
+    // so offsets are 32-bit.
+    constexpr int kXrT = DR ? DR + 32 : kMaxXr;              // outputs per stream (bound)
     constexpr int kPer = (kNxb + kParts - 1) / kParts;
     static_assert(!(DR && NXB) || kParts * kPer == NXB, "whole parts");
+    constexpr int kItems = (SPT * kParts * kXrT + kBlock - 1) / kBlock;
+    // Item sums land at their item index, every slot written (unused items too) so that no
+    // branch separates the partial loads from their use; with one part the sums are zp.
+    __shared__ float zq[kItems * kBlock];
+    __shared__ float zp_parts[kParts > 1 ? SPT * kXrT : 1];
+    float* const zp = kParts > 1 ? zp_parts : zq;  // [SPT][kXrT]
+    const int xr = a.xr;
     const int r = threadIdx.x;
-    const int o = kParts > 1 ? r % (DR + 32) : r, part = kParts > 1 ? r / (DR + 32) : 0;
-    const bool part_lane = part < kParts && o < a.xr;
-    float pv[kPer];
+    float pv[kItems][kPer];
     {
-        // The lane's first block goes into the per-lane offset; block i of the part is a
-        // uniform offset on top (a buffer access's scalar offset must be wave-uniform).
         const uint32_t pstride = (uint32_t)a.cap * (uint32_t)a.xr_pad * 4u;
-        const uint32_t o0 = (b * (uint32_t)a.xr_pad + (uint32_t)(part_lane ? o : 0)) * 4u +
-                            (uint32_t)(part_lane ? part * kPer : 0) * pstride;
         const BufRsrc rp = buf_rsrc(a.xpart, (uint32_t)nxb * pstride);
 #pragma unroll
-        for (int i = 0; i < kPer; i++) pv[i] = buf_ld_f32(rp, o0, (uint32_t)(NXB ? i : min(i, nxb - 1)) * pstride);
-    }
-    const uint32_t s = clamp_slot(slot_raw, a.cap);
-    const BufRsrc rs = buf_rsrc(a.ssm + (size_t)s * 16 * diu, 16u * row4);
-    float st[16];
+        for (int it = 0; it < kItems; it++) {
+            const int item = r + kBlock * it;
+            const int o = item % kXrT, part = (item / kXrT) % kParts, s = item / (kXrT * kParts);
+            const bool real = s < SPT && o < xr;
+            // The lane's first block goes into the per-lane offset; block i of the part is a
+            // uniform offset on top (a buffer access's scalar offset must be wave-uniform).
+            const uint32_t ps = min(bs0 + (uint32_t)s, a.n - 1);  // the item's stream
+            const uint32_t o0 = real ? (ps * (uint32_t)a.xr_pad + (uint32_t)o) * 4u + (uint32_t)(part * kPer) * pstride : 0u;
 #pragma unroll
-    for (int n = 0; n < 16; n++) st[n] = buf_ld_f32<kStream>(rs, j4, (uint32_t)n * row4);
-    {
+            for (int i = 0; i < kPer; i++) pv[it][i] = buf_ld_f32(rp, o0, (uint32_t)(NXB ? i : min(i, nxb - 1)) * pstride);
+        }
+    }
+    float st[SPT][16];
+    BufRsrc rs[SPT];
+#pragma unroll
+    for (int s = 0; s < SPT; s++) {
+        rs[s] = buf_rsrc(a.ssm + (size_t)clamp_slot(slot_raw[s], a.cap) * 16 * diu, 16u * row4);
+#pragma unroll
+        for (int n = 0; n < 16; n++) st[s][n] = buf_ld_f32<kStream>(rs[s], j4, (uint32_t)n * row4);
+    }
+#pragma unroll
+    for (int it = 0; it < kItems; it++) {
         float acc = 0.0f;
 #pragma unroll
         for (int i = 0; i < kPer; i++)
-            if (NXB || i < nxb) acc += pv[i];
-        if (part_lane) (kParts > 1 ? zq[part] : zp)[o] = acc;
+            if (NXB || i < nxb) acc += pv[it][i];
+        zq[r + kBlock * it] = acc;
     }
     __syncthreads();
     if constexpr (kParts > 1) {
-        if (r < a.xr) {
-            float z = zq[0][r];
 #pragma unroll
-            for (int q = 1; q < kParts; q++) z = z + zq[q][r];
-            zp[r] = z;
+        for (int it = 0; it < (SPT * kXrT + kBlock - 1) / kBlock; it++) {
+            const int item = r + kBlock * it;
+            const int o = item % kXrT, s = item / kXrT;
+            if (s < SPT && o < xr) {
+                const float* q0 = zq + (size_t)s * kParts * kXrT + o;
+                float zsum = q0[0];
+#pragma unroll
+                for (int q = 1; q < kParts; q++) zsum = zsum + q0[q * kXrT];
+                zp[s * kXrT + o] = zsum;
+            }
         }
         __syncthreads();
     }
@@ -1088,73 +1125,91 @@ __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
             for (int e = 0; e < 4; e++) wdt[4 * q + e] = bits_to_f((uint32_t)wv[e]);
         }
     }
-    // dot_avx2_order (tensor.rs:1680-1693): eight lanes by column residue, fixed tree, tail.
-    // dt_rank <= 64 means a quantized dt_proj has one scale per row (a 64-column group
-    // spans the whole row or the group rule falls back to per-row), so the Q8 row is
-    // 0 + dot * scale (gemv.rs:490-502).  The row (padded to dt_pad columns) was loaded
-    // into wdt before the partial sums.
-    float dt;
-    {
-        const int body = dr / 8 * 8;
-        float l[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll
-        for (int c = 0; c + 8 <= kDr; c += 8) {
-            if (DR || c < body) {
-#pragma unroll
-                for (int i = 0; i < 8; i++) l[i] += wdt[c + i] * zp[c + i];
-            }
-        }
-        float sdot = ((l[0] + l[4]) + (l[2] + l[6])) + ((l[1] + l[5]) + (l[3] + l[7]));
-#pragma unroll
-        for (int c = DR / 8 * 8; c < kDr; c++)
-            if (c >= body && c < dr) sdot += wdt[c] * zp[c];
-        dt = Q8DT ? 0.0f + sdot * dts : sdot;
-    }
-    dt = softplus_f(dt + dtb);
-    const float* B = zp + dr;
-    const float* C = zp + dr + 16;
-    if (!(fabsf(dt) < 1e-6f)) {
-        const float dtx = dt * x;
-#pragma unroll
-        for (int k = 0; k < 16; k++) {
-            const float e = 0.0f - dt * av[k];
-            const float da = FAST ? hw_exp(e) : lane_exp_f(e);
-            st[k] = da * st[k] + dtx * B[k];
-        }
-#pragma unroll
-        for (int n = 0; n < 16; n++) buf_st_f32<kStream>(st[n], rs, j4, (uint32_t)n * row4);
-    }
-    float l[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) l[i] = st[i] * C[i] + st[i + 8] * C[i + 8];
-    const float y = ((l[0] + l[4]) + (l[1] + l[5])) + ((l[2] + l[6]) + (l[3] + l[7])) + dv * x;
     // Gate: the 8-aligned body of each 64-channel block takes the lane form
     // 1 / (1 + lane_exp(0 - z)), the tail 1 / (1 + exp(-z)); one exp_f serves both.
     const int blk0 = j / 64 * 64;
     const int len = min(64, di - blk0);
-    const bool body = (j - blk0) < len / 8 * 8;
-    const float sg = 1.0f / (1.0f + exp_f(body ? lane_exp_arg(0.0f - zz) : -zz));
-    const float gv = y * (zz * sg);
-    const Limb3 t3 = split3(gv);
-    const int g = b / kRowTile, sk = j / kKStep;
-    const int ln = (b % kRowTile) + kRowTile * ((j % kKStep) / 8);
-    __bf16* dst = a.glimb + ((((size_t)g * (di / kKStep) + sk) * 3) * 64 + ln) * 8 + (j % 8);
-    dst[0] = t3.h;
-    dst[512] = t3.m;
-    dst[1024] = t3.l;
+    const bool gate_body = (j - blk0) < len / 8 * 8;
+#pragma unroll
+    for (int s = 0; s < SPT; s++) {
+        const uint32_t b = bs0 + s;
+        if (b >= a.n) break;
+        const float* zps = zp + s * kXrT;
+        // dot_avx2_order (tensor.rs:1680-1693): eight lanes by column residue, fixed tree,
+        // tail.  dt_rank <= 64 means a quantized dt_proj has one scale per row (a 64-column
+        // group spans the whole row or the group rule falls back to per-row), so the Q8
+        // row is 0 + dot * scale (gemv.rs:490-502).
+        float dt;
+        {
+            const int body = dr / 8 * 8;
+            float l[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+            for (int c = 0; c + 8 <= kDr; c += 8) {
+                if (DR || c < body) {
+#pragma unroll
+                    for (int i = 0; i < 8; i++) l[i] += wdt[c + i] * zps[c + i];
+                }
+            }
+            float sdot = ((l[0] + l[4]) + (l[2] + l[6])) + ((l[1] + l[5]) + (l[3] + l[7]));
+#pragma unroll
+            for (int c = DR / 8 * 8; c < kDr; c++)
+                if (c >= body && c < dr) sdot += wdt[c] * zps[c];
+            dt = Q8DT ? 0.0f + sdot * dts : sdot;
+        }
+        dt = softplus_f(dt + dtb);
+        const float* B = zps + dr;
+        const float* C = zps + dr + 16;
+        if (!(fabsf(dt) < 1e-6f)) {
+            const float dtx = dt * x[s];
+#pragma unroll
+            for (int k = 0; k < 16; k++) {
+                const float e = 0.0f - dt * av[k];
+                const float da = FAST ? hw_exp(e) : lane_exp_f(e);
+                st[s][k] = da * st[s][k] + dtx * B[k];
+            }
+#pragma unroll
+            for (int n = 0; n < 16; n++) buf_st_f32<kStream>(st[s][n], rs[s], j4, (uint32_t)n * row4);
+        }
+        float l[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) l[i] = st[s][i] * C[i] + st[s][i + 8] * C[i + 8];
+        const float y = ((l[0] + l[4]) + (l[1] + l[5])) + ((l[2] + l[6]) + (l[3] + l[7])) + dv * x[s];
+        const float sg = 1.0f / (1.0f + exp_f(gate_body ? lane_exp_arg(0.0f - zz[s]) : -zz[s]));
+        const float gv = y * (zz[s] * sg);
+        const Limb3 t3 = split3(gv);
+        const int g = b / kRowTile, sk = j / kKStep;
+        const int ln = (b % kRowTile) + kRowTile * ((j % kKStep) / 8);
+        __bf16* dst = a.glimb + ((((size_t)g * (di / kKStep) + sk) * 3) * 64 + ln) * 8 + (j % 8);
+        dst[0] = t3.h;
+        dst[512] = t3.m;
+        dst[1024] = t3.l;
+    }
 }
 
-// The scan instance for a layer shape: Mamba-130M's (dt_rank 48, 24 x_proj blocks) is
-// specialised, every other shape takes the generic kernel.
-const void* scan_fn(bool q8dt, bool fast, int dr, int nxb) {
-    // Mamba-130M: dt_rank 48, 48 x_proj blocks of 32 channels.
+// Streams per scan thread by batch size: sharing a channel's operands pays once a launch
+// has several times more workgroups than the chip holds at once (measured on Mamba-130M:
+// 1-2 % from 256 streams, a loss below; four streams per thread lose everywhere, from the
+// halved occupancy).
+constexpr uint32_t kScanSpt2From = 256;
+
+uint32_t scan_spt(uint32_t n) { return n >= kScanSpt2From ? 2 : 1; }
+
+template <bool Q8DT, bool FAST, int DR, int NXB>
+const void* scan_fn_spt(uint32_t spt) {
+    if (spt == 2) return (const void*)k_scan<Q8DT, FAST, DR, NXB, 2>;
+    return (const void*)k_scan<Q8DT, FAST, DR, NXB, 1>;
+}
+
+// The scan instance for a layer shape: Mamba-130M's (dt_rank 48, 48 x_proj blocks of 32
+// channels) is specialised, every other shape takes the generic kernel.
+const void* scan_fn(bool q8dt, bool fast, int dr, int nxb, uint32_t spt) {
     const bool m130 = dr == 48 && nxb == 48;
     if (q8dt) {
-        if (m130) return fast ? (const void*)k_scan<true, true, 48, 48> : (const void*)k_scan<true, false, 48, 48>;
-        return fast ? (const void*)k_scan<true, true, 0, 0> : (const void*)k_scan<true, false, 0, 0>;
+        if (m130) return fast ? scan_fn_spt<true, true, 48, 48>(spt) : scan_fn_spt<true, false, 48, 48>(spt);
+        return fast ? scan_fn_spt<true, true, 0, 0>(spt) : scan_fn_spt<true, false, 0, 0>(spt);
     }
-    if (m130) return fast ? (const void*)k_scan<false, true, 48, 48> : (const void*)k_scan<false, false, 48, 48>;
-    return fast ? (const void*)k_scan<false, true, 0, 0> : (const void*)k_scan<false, false, 0, 0>;
+    if (m130) return fast ? scan_fn_spt<false, true, 48, 48>(spt) : scan_fn_spt<false, false, 48, 48>(spt);
+    return fast ? scan_fn_spt<false, true, 0, 0>(spt) : scan_fn_spt<false, false, 0, 0>(spt);
 }
 
 // ---------------------------------------------------------------- k_mix_out
@@ -1804,6 +1859,7 @@ void build_step(const ModelView& m, Pool& p, const StepIO& io, std::vector<Launc
     const int in_tiles = pre && n >= (uint32_t)kInWideFrom ? 4 : 2;
     const int nxb = di / (kRowTile * in_tiles);
     const int nxp = di / kXpBlock;
+    const uint32_t spt = scan_spt(n);
     const int ks_x = m.layers[0].in_x.ks, tiles = d / kRowTile;
     io_index = (int)out.size();
     out.push_back(embed_launch(*m.emb, p, io, m.layers[0].norm_w, pre ? p.xw : nullptr, p.ssp, ks_x, tiles));
@@ -1824,8 +1880,8 @@ void build_step(const ModelView& m, Pool& p, const StepIO& io, std::vector<Launc
         out.push_back(Launch::make(fin, dim3(nxb + zb, in_chunks), dim3(kBlock), lds_in, KC_MIX_IN, ma));
         ScanArgs sa{p.xpart, nxp, xr_pad, (int)D.xr(), p.u, p.z, p.ssm + li * ssm_layer, L.dt_w, L.dt_q,
                     L.dt_scales, L.dt_pad, L.dt_b, L.a_exp, L.d_vec, p.slots, p.cap, n, p.glimb, di, (int)D.dr};
-        const void* fs = scan_fn(L.dt_q != nullptr, !m.exact_scan, (int)D.dr, nxp);
-        out.push_back(Launch::make(fs, dim3((di + kBlock - 1) / kBlock, n), dim3(kBlock), 0, KC_SCAN, sa));
+        const void* fs = scan_fn(L.dt_q != nullptr, !m.exact_scan, (int)D.dr, nxp, spt);
+        out.push_back(Launch::make(fs, dim3((di + kBlock - 1) / kBlock, (n + spt - 1) / spt), dim3(kBlock), 0, KC_SCAN, sa));
         const float* nw_next = li + 1 < D.nl ? m.layers[li + 1].norm_w : m.norm_f_w;
         MixOutArgs oa{L.out_proj, p.glimb, p.x, n, d, nw_next, pre ? p.xw : nullptr, p.ssp, ks_x, tiles};
         const void* fo = mix_out_fn(q8, out_g, m.layers[0].out_proj.ks == 2 * kOutWaves * kOutPairs);

@@ -63,16 +63,6 @@ constexpr int kProjPairs = 3;    // k-pairs per wave and pass
 constexpr int kMaxSegs = 8;
 constexpr int kMaxShiftMix = 6;
 
-__device__ __forceinline__ float block_sum256(float v, float* sh) {
-    const int lane = threadIdx.x % kWave, wave = wave_index();
-    v = wave_sum(v);
-    if (lane == 0) sh[wave] = v;
-    __syncthreads();
-    const float t = ((sh[0] + sh[1]) + sh[2]) + sh[3];
-    __syncthreads();
-    return t;
-}
-
 // ---------------------------------------------------------------- LayerNorm + token shift
 
 struct ShiftArgs {
@@ -93,44 +83,77 @@ struct ShiftArgs {
 // (x - mean) * (1 / sqrt(var + 1e-5)) * w + b; the token shift of time_mixing_scratch
 // (model.rs:811-820) / channel_mixing_scratch (:920-921): xx = prev - ln,
 // input_m = ln + xx * mix_m; the slot's prev becomes ln (model.rs:663, 675).
+// NMIX = a.nmix (0: the ln output itself goes to out[0], no previous value).  Every
+// operand is requested before the first wait: the slot, x, the LayerNorm weights, the
+// mixes, then the slot's previous ln once the slot is known.  Channels past d re-read
+// channel d - 1 and are left out of the sums and the stores.
+template <int NMIX>
 __global__ __launch_bounds__(kBlock) void k_rwkv_shift(ShiftArgs a) {
-    __shared__ float sh[kBlock / kWave];
+    __shared__ float sh[2][kBlock / kWave];
     const uint32_t b = blockIdx.x;
     const int d = a.d;
     constexpr int kPer = 4;  // d <= 1024
-    float xv[kPer];
+    constexpr int kMix = NMIX ? NMIX : 1;
+    const int lane = threadIdx.x % kWave, wave = wave_index();
+    const uint32_t slot = NMIX ? clamp_slot(a.slots[b], a.cap) : 0u;
+    int cc[kPer];
+#pragma unroll
+    for (int q = 0; q < kPer; q++) cc[q] = min((int)threadIdx.x + kBlock * q, d - 1);
+    float xv[kPer], wv[kPer], bv[kPer], mv[kMix][kPer], pv[kPer];
     const float* xb = a.x + (size_t)b * d;
 #pragma unroll
     for (int q = 0; q < kPer; q++) {
-        const int c = threadIdx.x + kBlock * q;
-        xv[q] = c < d ? xb[c] : 0.0f;
+        xv[q] = xb[cc[q]];
+        wv[q] = a.ln_w[cc[q]];
+        bv[q] = a.ln_b[cc[q]];
     }
+#pragma unroll
+    for (int m = 0; m < NMIX; m++)
+#pragma unroll
+        for (int q = 0; q < kPer; q++) mv[m][q] = a.mix[m][cc[q]];
+    float* const pp = NMIX ? a.prev + slot * a.prev_stride : nullptr;
+#pragma unroll
+    for (int q = 0; q < kPer; q++) pv[q] = NMIX ? pp[cc[q]] : 0.0f;
+    bool in[kPer];
+#pragma unroll
+    for (int q = 0; q < kPer; q++) in[q] = (int)threadIdx.x + kBlock * q < d;
+    // Block sums: wave sums, then ((w0 + w1) + w2) + w3; each sum has its own LDS row, so
+    // one barrier per sum.
     float s = 0.0f;
 #pragma unroll
-    for (int q = 0; q < kPer; q++) s += xv[q];
-    const float mean = block_sum256(s, sh) / (float)d;
+    for (int q = 0; q < kPer; q++) s += in[q] ? xv[q] : 0.0f;
+    s = wave_sum(s);
+    if (lane == 0) sh[0][wave] = s;
+    __syncthreads();
+    const float mean = (((sh[0][0] + sh[0][1]) + sh[0][2]) + sh[0][3]) / (float)d;
     float vs = 0.0f;
 #pragma unroll
-    for (int q = 0; q < kPer; q++) {
-        const int c = threadIdx.x + kBlock * q;
-        if (c < d) vs += (xv[q] - mean) * (xv[q] - mean);
-    }
-    const float inv = 1.0f / sqrtf(block_sum256(vs, sh) / (float)d + 1e-5f);
-    const uint32_t slot = a.prev ? clamp_slot(a.slots[b], a.cap) : 0u;
+    for (int q = 0; q < kPer; q++)
+        if (in[q]) vs += (xv[q] - mean) * (xv[q] - mean);
+    vs = wave_sum(vs);
+    if (lane == 0) sh[1][wave] = vs;
+    __syncthreads();
+    const float inv = 1.0f / sqrtf((((sh[1][0] + sh[1][1]) + sh[1][2]) + sh[1][3]) / (float)d + 1e-5f);
 #pragma unroll
     for (int q = 0; q < kPer; q++) {
-        const int c = threadIdx.x + kBlock * q;
-        if (c >= d) continue;
-        const float ln = (xv[q] - mean) * inv * a.ln_w[c] + a.ln_b[c];
-        if (!a.prev) {
+        if (!in[q]) continue;
+        const int c = cc[q];
+        const float ln = (xv[q] - mean) * inv * wv[q] + bv[q];
+        if (NMIX == 0) {
             write_limb1(a.out[0], a.ks, b, c, ln);
             continue;
         }
-        float* pp = a.prev + slot * a.prev_stride + c;
-        const float xx = *pp - ln;
-        for (int m = 0; m < a.nmix; m++) write_limb1(a.out[m], a.ks, b, c, ln + xx * a.mix[m][c]);
-        *pp = ln;
+        const float xx = pv[q] - ln;
+#pragma unroll
+        for (int m = 0; m < NMIX; m++) write_limb1(a.out[m], a.ks, b, c, ln + xx * mv[m][q]);
+        pp[c] = ln;
     }
+}
+
+const void* shift_fn(int nmix) {
+    if (nmix == 6) return (const void*)k_rwkv_shift<6>;
+    if (nmix == 1) return (const void*)k_rwkv_shift<1>;
+    return (const void*)k_rwkv_shift<0>;
 }
 
 // ---------------------------------------------------------------- projections
@@ -420,7 +443,7 @@ void RwkvStep::build(Pool& p, const StepIO& io, std::vector<Launch>& out, int& i
             s1.mix[k] = L.mix[k];
             s1.out[k] = mixl[k];
         }
-        out.push_back(Launch::make((const void*)k_rwkv_shift, dim3(n), dim3(kBlock), 0, KC_SHIFT, s1));
+        out.push_back(Launch::make(shift_fn(s1.nmix), dim3(n), dim3(kBlock), 0, KC_SHIFT, s1));
         // receptance <- x_r, key <- x_k, value <- x_v; LoRA inputs x_w, x_a, x_g, x_v
         ProjBuilder p1;
         p1.add(L.r, mixl[0], PROJ_STORE, ACT_NONE, p.rkv, 3 * d, nullptr, 0);
@@ -445,7 +468,7 @@ void RwkvStep::build(Pool& p, const StepIO& io, std::vector<Launch>& out, int& i
         ShiftArgs s2{p.x, L.ln2_w, L.ln2_b, p.x_ffn + (size_t)l * d, state_stride, p.slots, p.cap, 1, {}, {}, z.ks_d, d};
         s2.mix[0] = L.ffn_x_k;
         s2.out[0] = p.ffnl;
-        out.push_back(Launch::make((const void*)k_rwkv_shift, dim3(n), dim3(kBlock), 0, KC_SHIFT, s2));
+        out.push_back(Launch::make(shift_fn(s2.nmix), dim3(n), dim3(kBlock), 0, KC_SHIFT, s2));
         ProjBuilder pk;
         pk.add(L.fk, p.ffnl, PROJ_LIMBS, ACT_RELU2, nullptr, 0, p.actl, z.ks_f);
         out.push_back(pk.launch(n));
@@ -458,7 +481,7 @@ void RwkvStep::build(Pool& p, const StepIO& io, std::vector<Launch>& out, int& i
     if (ws) {
         ShiftArgs sf{p.x, m.ln_out_w, m.ln_out_b, nullptr, 0, p.slots, p.cap, 0, {}, {}, z.ks_d, d};
         sf.out[0] = p.headl;
-        out.push_back(Launch::make((const void*)k_rwkv_shift, dim3(n), dim3(kBlock), 0, KC_SHIFT, sf));
+        out.push_back(Launch::make(shift_fn(sf.nmix), dim3(n), dim3(kBlock), 0, KC_SHIFT, sf));
     }
     head_i = (int)out.size();
     out.push_back(head_launch(H, p, io, p.x, m.ln_out_w, m.ln_out_b, ws ? p.headl : nullptr, nullptr, d, 0, ws));

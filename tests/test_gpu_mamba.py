@@ -135,6 +135,31 @@ def test_batch_invariance_any_n_position_slot(models, profile):
                 assert np.array_equal(bits(g[pos]), bits(alone[i])), (n, pos, i)
 
 
+@pytest.mark.parametrize("profile", [0, 6])
+def test_batch_invariance_streams_per_scan_thread(models, profile):
+    # From 256 streams a scan thread runs two streams of its channel, and with an odd
+    # count the last pair is half empty.  A stream's bits depend on neither.
+    with ffi.PluginBackend(models["reftest"], profile=profile) as be:
+        v = be.vocab
+        seq = [(29 * i + 3) % v for i in range(4)]
+        be.batch_init(520)
+        alone = []
+        for t in seq:
+            g = np.empty((1, v), np.float32)
+            be.forward_batch([519], [t], g)
+            alone.append(g[0].copy())
+        rng = np.random.default_rng(2)
+        for n, pos in ((255, 254), (256, 1), (257, 256), (259, 257), (513, 512), (519, 3)):
+            be.batch_reset(None)
+            slots = [int(s) for s in rng.permutation(519)[:n]]
+            for i, t in enumerate(seq):
+                toks = [int(x) for x in rng.integers(0, v, n)]
+                toks[pos] = t
+                g = np.empty((n, v), np.float32)
+                be.forward_batch(slots, toks, g)
+                assert np.array_equal(bits(g[pos]), bits(alone[i])), (n, pos, i)
+
+
 def test_run_to_run_bitwise(models):
     results = []
     for _ in range(2):
@@ -302,3 +327,16 @@ def test_mamba130m_reset_boundary_and_large_batch_invariance(full_model):
         g = np.empty((128, v), np.float32)
         be.forward_batch(slots, toks, g)
         assert np.array_equal(bits(g[77]), bits(alone[0]))
+        # And inside a 513-stream batch (two streams per scan thread, the last pair half
+        # empty), in a full pair and in the half-empty one.
+        be.batch_init(520)
+        be.forward_batch([519], [tok], alone)
+        for pos in (511, 512):
+            be.batch_reset(None)
+            slots = [int(s) for s in rng.permutation(519)[:512]]
+            slots.insert(pos, 519)
+            toks = [int(x) for x in synth.zipf_tokens(rng, v, 513)]
+            toks[pos] = tok
+            g = np.empty((513, v), np.float32)
+            be.forward_batch(slots, toks, g)
+            assert np.array_equal(bits(g[pos]), bits(alone[0])), pos
