@@ -153,25 +153,33 @@ def ensure_model(path: str) -> str:
     return path
 
 
-def cpu_baseline(path: str, profile: int, n: int, tokens: np.ndarray, budget_s: float, mamba: bool = True) -> dict:
+def cpu_baseline(path: str, profile: int, n: int, tokens: np.ndarray, budget_s: float, mamba: bool = True,
+                 probs: bool = False) -> dict:
     from oracle import oracle as O   # the CPU restatement; test/baseline infrastructure only
 
     threads = min(os.cpu_count() or 1, 16)
     O.set_threads(threads)
     m = O.MambaOracle(path, profile, cap=n) if mamba else O.RwkvOracle(path, profile, cap=n)
     slots = list(range(n))
-    m.forward(slots, [int(x) for x in tokens[0]])          # warm-up step
+    def fwd(t: int) -> None:
+        logits = m.forward(slots, [int(x) for x in tokens[t]])
+        if probs:                                           # softmax_into per stream, on the host
+            for r in logits:
+                O.softmax(r)
+
+    fwd(0)                                                  # warm-up step
     t0 = time.perf_counter()
-    m.forward(slots, [int(x) for x in tokens[1]])
+    fwd(1)
     one = time.perf_counter() - t0
     steps = max(1, min(len(tokens) - 2, int(budget_s / max(one, 1e-6))))
     t0 = time.perf_counter()
     for t in range(steps):
-        m.forward(slots, [int(x) for x in tokens[2 + t]])
+        fwd(2 + t)
     dt = time.perf_counter() - t0
     m.close()
     return {"value": round(n * steps / dt, 2), "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"CPU oracle, same weights and profile, {n} lockstep streams x {steps} steps "
+            "sample": f"CPU oracle{' + softmax per stream' if probs else ''}, same weights and profile, "
+                      f"{n} lockstep streams x {steps} steps "
                       f"({dt:.1f} s) after one warm-up step"}
 
 
@@ -193,6 +201,8 @@ def main() -> int:
                     help="after the probe pass, copy this many MiB device to device on the library's "
                          "stream (a copy of known size for scaling HBM byte counters)")
     ap.add_argument("--model", default=None, help="weight file (written with synthetic weights if absent)")
+    ap.add_argument("--probs", action="store_true",
+                    help="hand back the probability vector (softmax over the vocabulary) instead of logits")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -215,12 +225,12 @@ def main() -> int:
         path = ensure_model(args.model or os.path.join(tempfile.gettempdir(), "redukt_bench", "mamba130m.rbin"))
         tokens = synth.zipf_tokens(rng, dims.vocab, (total, n))
         exact = "-exactscan" if args.exact_scan else ""
-        vocab, workload = dims.vocab, f"mamba130m-{args.profile}{exact}-n{n}-zipf1.1"
+        vocab, workload = dims.vocab, f"mamba130m-{args.profile}{exact}-n{n}-zipf1.1{'-probs' if args.probs else ''}"
     else:
         dims = rwkv.RWKV7_0_1B
         path = ensure_rwkv(args.model or os.path.join(tempfile.gettempdir(), "redukt_bench", "rwkv7_0_1b.rbin"))
         tokens = rng.integers(0, 256, size=(total, n), dtype=np.uint32)   # byte-level ids
-        vocab, workload = dims.vocab, f"rwkv7-0.1b-{args.profile}-n{n}-bytes"
+        vocab, workload = dims.vocab, f"rwkv7-0.1b-{args.profile}-n{n}-bytes{'-probs' if args.probs else ''}"
 
     be = ffi.PluginBackend(path, 0, profile)
     be.batch_init(n)
@@ -241,7 +251,7 @@ def main() -> int:
             be.batch_reset(None)
             since = 0
         since += 1
-        be.forward_batch_device(n, d_slots.ptr, d_tokens.ptr + t * row, d_out.ptr)
+        be.forward_batch_device(n, d_slots.ptr, d_tokens.ptr + t * row, d_out.ptr, probs=args.probs)
 
     log(f"warm-up {W} steps, n={n}, profile={args.profile}")
     for t in range(W):
@@ -287,7 +297,7 @@ def main() -> int:
 
     classes = ffi.KERNEL_CLASSES if mamba else ffi.RWKV_KERNEL_CLASSES
     for name, cls in classes.items():
-        if name == "softmax":
+        if name == "softmax" and not args.probs:
             continue
         launches = launches_per_step(dims, name, mamba, profile)
         only = probe(cls | ffi.PROBE_CLASS_ONLY, 2 * P)
@@ -318,10 +328,10 @@ def main() -> int:
     out = np.empty((n, vocab), np.float32)
     slots = list(range(n))
     f_steps = min(64, K)
-    be.forward_batch(slots, [int(x) for x in tokens[0]], out)
+    be.forward_batch(slots, [int(x) for x in tokens[0]], out, probs=args.probs)
     t0 = time.perf_counter()
     for t in range(f_steps):
-        be.forward_batch(slots, [int(x) for x in tokens[t % total]], out)
+        be.forward_batch(slots, [int(x) for x in tokens[t % total]], out, probs=args.probs)
     ffi_tok_s = n * f_steps / (time.perf_counter() - t0)
     be.close()
     for b in (d_tokens, d_slots, d_out):
@@ -330,7 +340,7 @@ def main() -> int:
     cpu = None
     if not args.no_cpu_baseline:
         log("timing the CPU oracle on the host cores")
-        cpu = cpu_baseline(path, profile, n, tokens, args.cpu_seconds, mamba)
+        cpu = cpu_baseline(path, profile, n, tokens, args.cpu_seconds, mamba, args.probs)
 
     # HBM bytes per launch of the dominant kernel from the committed counter passes
     # (FETCH_SIZE / WRITE_SIZE scaled by a copy of known size), when they cover this workload.
@@ -343,6 +353,8 @@ def main() -> int:
             traffic = tj["bytes_per_launch"].get(dom)
 
     sb = step_bytes(dims, profile, n) if mamba else rwkv_step_bytes(dims, profile, n)
+    if args.probs:
+        sb += alg["softmax"]
     result = {
         "metric": METRIC if mamba else "RWKV-7 0.1B tok/s (lockstep streams, byte-level tokens)",
         "value": round(tok_s, 1),
@@ -358,7 +370,8 @@ def main() -> int:
         "data": "synthetic",
         "config": {"workload": workload, "layers": dims.n_layer,
                    "d_model": dims.d_model, "vocab": vocab, "streams": n, "weight_profile": args.profile,
-                   "reset_every": RESET_PERIOD, "reset_at_timed_step": reset_step, "parallelism": "none"},
+                   "reset_every": RESET_PERIOD, "reset_at_timed_step": reset_step,
+                   "output": "probabilities" if args.probs else "logits", "parallelism": "none"},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic},
         "cpu_baseline": cpu,

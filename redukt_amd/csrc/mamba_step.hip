@@ -82,7 +82,8 @@ constexpr int kInChunk = kInGroups * kRowTile;
 // 2 from there, so that a large batch fits the chip in one round of workgroups (one
 // 8-wave workgroup per CU).  A stream's arithmetic does not depend on the choice.
 constexpr int kOutWideFrom = 80;
-constexpr int kHeadTiles = 4;              // row tiles per wave in k_head
+constexpr int kHeadWaves = 8;              // waves per k_head workgroup (two per SIMD on one staged chunk)
+constexpr int kHeadTiles = 2;              // row tiles per wave in k_head
 // Weight k-pairs each wave keeps in flight (the product loop is unrolled by it): k_mix_in
 // holds its whole quarter of four Q8 row tiles of a d <= 1024 projection, k_head four
 // tiles' next eight pairs.
@@ -222,13 +223,13 @@ __device__ void stage_normed(__bf16* lds, const float* __restrict__ x, const flo
 // waits for vmcnt(0) and syncs before reading.
 
 __device__ __forceinline__ void stage_copy(unsigned char* lds, const __bf16* __restrict__ xw, uint32_t g0, int ng,
-                                           int ks) {
+                                           int ks, int waves = kWaves) {
     const int lane = threadIdx.x % kWave, wave = wave_index();
     const int blocks = ng * ks * 3;
     const __bf16* src = xw + (size_t)g0 * ks * 3 * 512 + lane * 8;
     lds_u8* dst = (lds_u8*)lds;
 #pragma unroll 4
-    for (int q = wave; q < blocks; q += kWaves)
+    for (int q = wave; q < blocks; q += waves)
         __builtin_amdgcn_global_load_lds((const void*)(src + (size_t)q * 512), (void __attribute__((address_space(3)))*)(dst + q * kLimbBytes),
                                          16, 0, 0);
 }
@@ -995,7 +996,12 @@ __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
     constexpr int kDr = DR ? DR : kMaxDr;
     constexpr int kNxb = NXB ? NXB : kMaxNxb;
     const int di = a.di, dr = DR ? DR : a.dr, nxb = NXB ? NXB : a.nxb;
-    const int j_raw = blockIdx.x * kBlock + threadIdx.x;
+    // The channel blocks of a stream group (SPT streams) run on one XCD, so the group's
+    // x_proj partials are fetched into one L2 and shared by its channel blocks.
+    const XcdTile xt = xcd_tile(blockIdx.x, ((uint32_t)di + kBlock - 1) / kBlock, (a.n + SPT - 1) / SPT);
+    if (!xt.live) return;
+    const uint32_t sy = xt.unit, cbx = xt.part;
+    const int j_raw = (int)cbx * kBlock + threadIdx.x;
     const bool live = j_raw < di;
     const int j = live ? j_raw : di - 1;
     // Buffer addressing: one descriptor per array (uniform base and exact byte size), the
@@ -1004,7 +1010,7 @@ __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
     const uint32_t ju = (uint32_t)j, diu = (uint32_t)di;
     const uint32_t j4 = ju * 4u, j16 = ju * 16u;
     const uint32_t row4 = diu * 4u;  // bytes of one [di] row
-    const uint32_t bs0 = blockIdx.y * SPT;  // first stream; streams past n load stream n - 1
+    const uint32_t bs0 = sy * SPT;  // first stream; streams past n load stream n - 1
     uint32_t bs[SPT];
 #pragma unroll
     for (int s = 0; s < SPT; s++) bs[s] = min(bs0 + s, a.n - 1);
@@ -1445,17 +1451,23 @@ struct HeadArgs {
 
 // Final norm (model.rs:745-752) and the LM head (model.rs:921-927, tied to the
 // embedding unless the file carries lm_head).  Each wave multiplies kHeadTiles row tiles
-// together, so every activation fragment read from LDS serves all of them.
+// together, so every activation fragment read from LDS serves all of them; kHeadWaves
+// waves share one staged chunk, two per SIMD (the chunk's LDS allows one workgroup per
+// CU).  The stream chunks of a row block run on one XCD (xcd_tile), which fetches the
+// block's weights into its L2 once for all of them.
 template <bool Q8, bool PRE>
-__global__ __launch_bounds__(kBlock) void k_head(HeadArgs a) {
+__global__ __launch_bounds__(kHeadWaves * kWave) void k_head(HeadArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ float invs[kChunk];
     __bf16* lds = (__bf16*)smem;
     const int lane = threadIdx.x % kWave, wave = wave_index();
-    const uint32_t b0 = blockIdx.y * kChunk;
+    const XcdTile xt = xcd_tile(blockIdx.x, (a.n + kChunk - 1) / kChunk,
+                                ((uint32_t)a.w.rt + kHeadWaves * kHeadTiles - 1) / (kHeadWaves * kHeadTiles));
+    if (!xt.live) return;
+    const uint32_t b0 = xt.part * kChunk;
     const int ng = (int)min((uint32_t)kGroups, (a.n - b0 + kRowTile - 1) / kRowTile);
     const int V = a.w.rows;
-    const int t_first = (blockIdx.x * kWaves + wave) * kHeadTiles;
+    const int t_first = ((int)xt.unit * kHeadWaves + wave) * kHeadTiles;
     SspLoad sl;
     if constexpr (PRE) sl = ssp_load(a.ssp, a.tiles, b0, a.n, kChunk);
     constexpr int R = Q8 ? kHeadRingQ8 : kHeadRingF32;
@@ -1468,7 +1480,7 @@ __global__ __launch_bounds__(kBlock) void k_head(HeadArgs a) {
     const int np = a.w.ks / 2;
     tiles_prefetch<Q8, kHeadTiles, R>(a.w, tl, 0, np);
     if constexpr (PRE) {
-        stage_copy(smem, a.xw, b0 / kRowTile, ng, a.w.ks);
+        stage_copy(smem, a.xw, b0 / kRowTile, ng, a.w.ks, kHeadWaves);
         ssp_reduce(sl, invs, a.tiles, a.d, kChunk);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
@@ -1511,7 +1523,8 @@ __global__ __launch_bounds__(kBlock) void k_head(HeadArgs a) {
 // once and keeps them for the whole kernel, walking the workgroup's column groups: group
 // g's activation tiles are copied into one LDS buffer while group g - 1 is multiplied
 // from the other.  Per tile and group: one accumulator over k-steps in order, limbs hi,
-// mid, lo per k-step; then the row scale and the stream's RMS scale.
+// mid, lo per k-step; then the row scale and the stream's RMS scale.  Above 128 streams
+// the chunks of a row block run on one XCD (xcd_tile) and share its L2.
 constexpr int kHwWaves = 8;    // waves per workgroup
 constexpr int kHwTiles = 2;    // row tiles per wave
 constexpr int kHwGroups = 8;   // column groups (16 streams) per workgroup
@@ -1535,9 +1548,13 @@ __global__ __launch_bounds__(kHwWaves * kWave) void k_head_ws(HeadArgs a) {
     const TMat& w = a.w;
     const int np = w.ks / 2, ks = w.ks;
     const int V = w.rows;
-    const uint32_t gb = blockIdx.y * kHwGroups;
-    const int ngr = (int)min((uint32_t)kHwGroups, (a.n + kRowTile - 1) / kRowTile - gb);
-    const int t0 = (blockIdx.x * kHwWaves + wave) * kHwTiles;
+    const uint32_t n_groups = (a.n + kRowTile - 1) / kRowTile;
+    const XcdTile xt = xcd_tile(blockIdx.x, (n_groups + kHwGroups - 1) / kHwGroups,
+                                ((uint32_t)w.rt + kHwWaves * kHwTiles - 1) / (kHwWaves * kHwTiles));
+    if (!xt.live) return;
+    const uint32_t gb = xt.part * kHwGroups;
+    const int ngr = (int)min((uint32_t)kHwGroups, n_groups - gb);
+    const int t0 = ((int)xt.unit * kHwWaves + wave) * kHwTiles;
     const size_t buf_bytes = (size_t)ks * 3 * kLimbBytes;
     // Requested first: the RMS partials of every stream of the workgroup, the weights and
     // row scales, the first group's activations.
@@ -1660,12 +1677,61 @@ struct SoftmaxArgs {
 
 // softmax_into (tensor.rs:1917-1933) per stream, in place: max, exp(l - max) with the
 // portable exp, the sum (fixed block tree instead of the sequential loop), division
-// by max(sum, FLT_EPSILON).
+// by max(sum, FLT_EPSILON).  Thread t owns elements t, t + 1024, ... and sums them in
+// that order; the wave sums then meet in wave order.  PER > 0 (vocab <= 1024 PER) holds
+// the thread's elements in registers, so the row is read once and written once; PER = 0
+// walks the row in memory for each phase.  Both give the same bits.
+constexpr int kSoftmaxPer = 50;  // vocab <= 51200 in registers (Mamba-130M: 50280)
+template <int PER>
 __global__ __launch_bounds__(1024) void k_softmax(SoftmaxArgs a) {
     __shared__ float sh[1024 / kWave];
     float* row = a.out + (size_t)blockIdx.x * a.vocab;
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     float mx = -INFINITY;
+    if constexpr (PER > 0) {
+        float v[PER];
+#pragma unroll
+        for (int k = 0; k < PER; k++) {
+            const int i = threadIdx.x + 1024 * k;
+            v[k] = i < a.vocab ? row[i] : -INFINITY;
+        }
+#pragma unroll
+        for (int k = 0; k < PER; k++) mx = fmaxf(mx, v[k]);
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
+        if (lane == 0) sh[wave] = mx;
+        __syncthreads();
+        mx = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < 1024 / kWave; w++) mx = fmaxf(mx, sh[w]);
+        __syncthreads();
+        if (mx == -INFINITY) {
+            const float u = 1.0f / (float)a.vocab;
+#pragma unroll
+            for (int k = 0; k < PER; k++)
+                if (threadIdx.x + 1024 * k < a.vocab) row[threadIdx.x + 1024 * k] = u;
+            return;
+        }
+        float s = 0.0f;
+#pragma unroll
+        for (int k = 0; k < PER; k++) {
+            if (threadIdx.x + 1024 * k < a.vocab) {
+                v[k] = exp_f(v[k] - mx);
+                s += v[k];
+            }
+        }
+        s = wave_sum(s);
+        if (lane == 0) sh[wave] = s;
+        __syncthreads();
+        float tsum = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 1024 / kWave; w++) tsum += sh[w];
+        const float denom = fmaxf(tsum, 1.1920929e-07f);
+#pragma unroll
+        for (int k = 0; k < PER; k++)
+            if (threadIdx.x + 1024 * k < a.vocab) __builtin_nontemporal_store(v[k] / denom, row + threadIdx.x + 1024 * k);
+        return;
+    }
     for (int i = threadIdx.x; i < a.vocab; i += 1024) mx = fmaxf(mx, row[i]);
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
@@ -1822,18 +1888,20 @@ Launch head_launch(const TMat& H, Pool& p, const StepIO& io, const float* x, con
         const int tiles_per_block = kHwWaves * kHwTiles;
         const uint32_t groups = (n + kRowTile - 1) / kRowTile;
         return Launch::make(head_ws_fn(H.ks / 2, lds_h),
-                            dim3((H.rt + tiles_per_block - 1) / tiles_per_block, (groups + kHwGroups - 1) / kHwGroups),
+                            dim3(xcd_grid((groups + kHwGroups - 1) / kHwGroups,
+                                          (H.rt + tiles_per_block - 1) / tiles_per_block)),
                             dim3(kHwWaves * kWave), lds_h, KC_HEAD, ha);
     }
     const uint32_t lds_h = stage_lds_bytes(H.ks);
-    const int tiles_per_block = kWaves * kHeadTiles;
+    const int tiles_per_block = kHeadWaves * kHeadTiles;
     return Launch::make(head_fn(H.group != 0, xw != nullptr, lds_h),
-                        dim3((H.rt + tiles_per_block - 1) / tiles_per_block, (n + kChunk - 1) / kChunk), dim3(kBlock),
-                        lds_h, KC_HEAD, ha);
+                        dim3(xcd_grid((n + kChunk - 1) / kChunk, (H.rt + tiles_per_block - 1) / tiles_per_block)),
+                        dim3(kHeadWaves * kWave), lds_h, KC_HEAD, ha);
 }
 
 Launch softmax_launch(float* out, int vocab, uint32_t n) {
-    return Launch::make((const void*)k_softmax, dim3(n), dim3(1024), 0, KC_SOFTMAX, SoftmaxArgs{out, vocab});
+    const void* f = vocab <= 1024 * kSoftmaxPer ? (const void*)k_softmax<kSoftmaxPer> : (const void*)k_softmax<0>;
+    return Launch::make(f, dim3(n), dim3(1024), 0, KC_SOFTMAX, SoftmaxArgs{out, vocab});
 }
 
 namespace {
@@ -1881,7 +1949,8 @@ void build_step(const ModelView& m, Pool& p, const StepIO& io, std::vector<Launc
         ScanArgs sa{p.xpart, nxp, xr_pad, (int)D.xr(), p.u, p.z, p.ssm + li * ssm_layer, L.dt_w, L.dt_q,
                     L.dt_scales, L.dt_pad, L.dt_b, L.a_exp, L.d_vec, p.slots, p.cap, n, p.glimb, di, (int)D.dr};
         const void* fs = scan_fn(L.dt_q != nullptr, !m.exact_scan, (int)D.dr, nxp, spt);
-        out.push_back(Launch::make(fs, dim3((di + kBlock - 1) / kBlock, (n + spt - 1) / spt), dim3(kBlock), 0, KC_SCAN, sa));
+        out.push_back(Launch::make(fs, dim3(xcd_grid((di + kBlock - 1) / kBlock, (n + spt - 1) / spt)), dim3(kBlock), 0,
+                                   KC_SCAN, sa));
         const float* nw_next = li + 1 < D.nl ? m.layers[li + 1].norm_w : m.norm_f_w;
         MixOutArgs oa{L.out_proj, p.glimb, p.x, n, d, nw_next, pre ? p.xw : nullptr, p.ssp, ks_x, tiles};
         const void* fo = mix_out_fn(q8, out_g, m.layers[0].out_proj.ks == 2 * kOutWaves * kOutPairs);
