@@ -78,9 +78,10 @@ constexpr int kInGroups = 1;               // column groups per k_mix_in workgro
 // Row tiles per k_mix_in workgroup: 2 up to kInWideFrom streams, 4 from there.
 constexpr int kInWideFrom = 64;
 constexpr int kInChunk = kInGroups * kRowTile;
-// Column groups (16 streams each) per k_mix_out workgroup: 1 up to kOutWideFrom streams,
-// 2 from there, so that a large batch fits the chip in one round of workgroups (one
-// 8-wave workgroup per CU).  A stream's arithmetic does not depend on the choice.
+// Column groups (16 streams each) per k_mix_out workgroup: F32 weights take 2 from
+// kOutWideFrom streams (their limb split then serves two groups), quantized weights always
+// take 1 (measured on Mamba-130M int8: one group is 1-7 % faster per step from 64 to
+// 1024 streams).  A stream's arithmetic does not depend on the choice.
 constexpr int kOutWideFrom = 80;
 constexpr int kHeadWaves = 8;              // waves per k_head workgroup (two per SIMD on one staged chunk)
 constexpr int kHeadTiles = 2;              // row tiles per wave in k_head
@@ -1914,7 +1915,7 @@ void build_step(const ModelView& m, Pool& p, const StepIO& io, std::vector<Launc
     const uint32_t n = io.n;
     const int d = (int)D.d, di = (int)D.di;
     const uint32_t in_chunks = (n + kInChunk - 1) / kInChunk;
-    const int out_g = n >= (uint32_t)kOutWideFrom ? 2 : 1;
+    const int out_g = m.layers[0].out_proj.group == 0 && n >= (uint32_t)kOutWideFrom ? 2 : 1;
     const uint32_t out_chunks = (n + out_g * kRowTile - 1) / (out_g * kRowTile);
     const int xr_pad = m.layers[0].x_proj.rt * kRowTile;
     out.clear();
