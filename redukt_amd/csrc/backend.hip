@@ -780,7 +780,16 @@ int32_t redukt_backend_get_rwkv_state(uint32_t slot, uint32_t layer, float* x_at
     const Pool& p = G.batch;
     if (x_att && hipMemcpy(x_att, p.x_att + row * d, d * 4, hipMemcpyDeviceToHost) != hipSuccess)
         return BACKEND_FORWARD_FAILED;
-    if (wkv && hipMemcpy(wkv, p.wkv + row * wl, wl * 4, hipMemcpyDeviceToHost) != hipSuccess) return BACKEND_FORWARD_FAILED;
+    if (wkv) {
+        // the pool holds each head as [j / 4][i][4]; the caller gets [head][i][j]
+        std::vector<float> t(wl);
+        if (hipMemcpy(t.data(), p.wkv + row * wl, wl * 4, hipMemcpyDeviceToHost) != hipSuccess) return BACKEND_FORWARD_FAILED;
+        const size_t n = R.n;
+        for (size_t hh = 0; hh < R.h; hh++)
+            for (size_t i = 0; i < n; i++)
+                for (size_t j = 0; j < n; j++)
+                    wkv[(hh * n + i) * n + j] = t[hh * n * n + ((j / 4) * n + i) * 4 + j % 4];
+    }
     if (x_ffn && hipMemcpy(x_ffn, p.x_ffn + row * d, d * 4, hipMemcpyDeviceToHost) != hipSuccess)
         return BACKEND_FORWARD_FAILED;
     return BACKEND_OK;

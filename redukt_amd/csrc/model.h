@@ -88,7 +88,7 @@ struct Pool {
     // RWKV-7 (allocated for RWKV-7 models only)
     float* x_att = nullptr;      // [slot][layer][d] time-mix token-shift input (ln1 output)
     float* x_ffn = nullptr;      // [slot][layer][d] channel-mix token-shift input (ln2 output)
-    float* wkv = nullptr;        // [slot][layer][head][i][j] WKV-7 state, row i, column j
+    float* wkv = nullptr;        // [slot][layer][head][j / 4][i][4] WKV-7 state S[i][j] (row i, column j)
     float* vfirst = nullptr;     // [cap][d] layer-0 value of the current token, per batch position
     float* rkv = nullptr;        // [cap][3d] receptance, key, value
     float* lorad = nullptr;      // [cap][4d] second LoRA stages: decay, a, g, v

@@ -342,11 +342,13 @@ __global__ __launch_bounds__(kHead) void k_rwkv_wkv(WkvArgs a) {
     const float r = rkv[c], k = rkv[d + c], v = rkv[2 * d + c];
     const float lw = ld[c], la = ld[d + c], g = ld[2 * d + c], lv = ld[3 * d + c];
     const float vf = a.layer != 0 ? a.vfirst[(size_t)b * d + c] : 0.0f;
-    float4* srow = (float4*)(a.wkv + slot * a.slot_stride + ((size_t)h * kHead + i) * kHead);
+    // The head's state is stored [j / 4][i][4]: lane i's float4 q holds S[i][4q .. 4q + 3],
+    // so each load and store of the wave is one contiguous 1 KB run.
+    float4* sbase = (float4*)(a.wkv + slot * a.slot_stride + (size_t)h * kHead * kHead);
     float S[kHead];
 #pragma unroll
     for (int q = 0; q < kHead / 4; q++) {
-        const float4 t4 = srow[q];
+        const float4 t4 = sbase[q * kHead + i];
         S[4 * q] = t4.x; S[4 * q + 1] = t4.y; S[4 * q + 2] = t4.z; S[4 * q + 3] = t4.w;
     }
     // Step 3: exp(-0.606531 * sigmoid(w0 + lora)) (decay_sigmoid_into, tensor.rs:1082-1101)
@@ -383,7 +385,7 @@ __global__ __launch_bounds__(kHead) void k_rwkv_wkv(WkvArgs a) {
 #pragma unroll
     for (int j = 0; j < kHead; j++) o += S[j] * sr[j];
 #pragma unroll
-    for (int q = 0; q < kHead / 4; q++) srow[q] = make_float4(S[4 * q], S[4 * q + 1], S[4 * q + 2], S[4 * q + 3]);
+    for (int q = 0; q < kHead / 4; q++) sbase[q * kHead + i] = make_float4(S[4 * q], S[4 * q + 1], S[4 * q + 2], S[4 * q + 3]);
     // Step 10: GroupNorm over the head, eps 64e-5 (group_norm_into :1400-1414)
     const float mean = wave_sum(o) / (float)kHead;
     const float var = wave_sum((o - mean) * (o - mean)) / (float)kHead;
