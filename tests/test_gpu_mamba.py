@@ -123,7 +123,8 @@ def test_batch_invariance_any_n_position_slot(models, profile):
             be.forward_batch([71], [t], g)
             alone.append(g[0].copy())
         rng = np.random.default_rng(1)
-        # n >= 64 takes the four-tile in_proj blocks, n < 64 the two-tile ones
+        # with int8 per-row weights (profile 6) n >= 64 takes the four-tile in_proj blocks,
+        # n < 64 the two-tile ones; F32 weights take the two-tile blocks at every n
         for n, pos in ((2, 1), (7, 3), (33, 32), (63, 0), (64, 40), (71, 70)):
             be.batch_reset(None)
             slots = [int(s) for s in rng.permutation(71)[:n]]
