@@ -239,6 +239,27 @@ def test_probability_vector(models):
         orc.close()
 
 
+@pytest.mark.parametrize("vocab", [51200, 51201])
+def test_probability_vector_both_softmax_forms(tmp_path, vocab):
+    # Up to 51,200 symbols a row of the softmax is held in registers, above it the kernel
+    # walks the row in memory for each phase; both must give the oracle's probabilities.
+    path = str(tmp_path / f"v{vocab}.rbin")
+    synth.write_synthetic_mamba(path, rbin.MambaDims(vocab=vocab, d_model=64, n_layer=1), seed=11)
+    with ffi.PluginBackend(path, profile=0) as be:
+        orc = O.MambaOracle(path, 0, cap=3)
+        be.batch_init(3)
+        for t in range(2):
+            toks = [(s * 4099 + t * 977 + 5) % vocab for s in range(3)]
+            pg = np.empty((3, vocab), np.float32)
+            be.forward_batch(list(range(3)), toks, pg, probs=True)
+            lc = orc.forward(list(range(3)), toks)
+            pc = np.stack([O.softmax(r) for r in lc])
+            l1 = np.abs(pg.astype(np.float64) - pc).sum(axis=1)
+            assert np.all(l1 <= TOL_L1), (vocab, t, l1)
+            assert np.all(np.abs(pg.astype(np.float64).sum(axis=1) - 1.0) < 1e-5)
+        orc.close()
+
+
 def test_device_resident_entry_point(models):
     with ffi.PluginBackend(models["base"], profile=2) as be:
         v = be.vocab
