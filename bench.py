@@ -83,8 +83,10 @@ def algorithmic_bytes(dims: rbin.MambaDims, profile: int, n: int) -> dict:
 def step_bytes(dims: rbin.MambaDims, profile: int, n: int) -> int:
     """Whole-step compulsory HBM bytes: weights once, state read+write, embedding rows,
     logits write (the B(N) of the workload description)."""
-    w = sum(weight_bytes(dims, profile).values())
+    wb = weight_bytes(dims, profile)
     L, d, di, dc = dims.n_layer, dims.d_model, dims.d_inner, dims.d_conv
+    # every layer's four projections, then the head (tied: the embedding) once
+    w = L * (wb["in_proj"] + wb["x_proj"] + wb["dt_proj"] + wb["out_proj"]) + wb["head"]
     # per layer: norm_w, conv_w, conv_b, dt_b, exp(A_log), D; then norm_f
     small = L * (d + di * dc + di + di + 16 * di + di) * 4 + d * 4
     state = 2 * L * di * ((dc - 1) + 16) * 4
