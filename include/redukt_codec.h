@@ -41,6 +41,9 @@ typedef enum {
     /* decoded symbol >= vocab (DecodeError::SymbolOutOfRange, coder.rs:19-20) */
     REDUKT_CODEC_SYMBOL_OUT_OF_RANGE = 3,
     REDUKT_CODEC_BUFFER_TOO_SMALL = 4,
+    /* the file was not finished: the backbone failed (forward / reset) while it was in
+     * flight or before it was admitted; its output is not valid (length 0) */
+    REDUKT_CODEC_INCOMPLETE = 5,
 } redukt_codec_status;
 
 /* Cumulative total of every probability-built CDF (coder.rs:12). */

@@ -81,7 +81,9 @@ uint64_t redukt_lockstep_stream_bound(uint64_t n_tokens);
  * the Mamba family is 4096).  Coded stream i goes to out[i] (capacity cap[i]);
  * out_len[i] receives its length (the needed length when it did not fit).  status, if
  * not NULL, receives one redukt_codec_status per file.  Returns OK when every file
- * succeeded, else the first failure. */
+ * succeeded, else the first failure.  When the backbone fails mid-run (FORWARD), every
+ * file still in flight and every file not yet admitted reports REDUKT_CODEC_INCOMPLETE
+ * with out_len 0; files finished before the failure keep their status and bytes. */
 int32_t redukt_lockstep_compress(redukt_lockstep* ls, uint32_t n_files, const uint32_t* const* tokens,
                                  const uint64_t* n_tokens, uint64_t reset_every, uint8_t* const* out,
                                  const uint64_t* cap, uint64_t* out_len, int32_t* status,

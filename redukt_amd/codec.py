@@ -30,6 +30,7 @@ class CodecStatus(enum.IntEnum):
     RANGE_UNDERFLOW = 2
     SYMBOL_OUT_OF_RANGE = 3
     BUFFER_TOO_SMALL = 4
+    INCOMPLETE = 5
 
 
 class CodecError(RuntimeError):

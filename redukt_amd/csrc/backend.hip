@@ -443,6 +443,7 @@ bool pool_alloc_rwkv(Pool& p, uint32_t cap) {
     const RwkvSizes z = rwkv_sizes(R, cap);
     p = Pool{};
     p.cap = cap;
+    p.scap = cap + 1;
     p.gcap = (cap + 15) / 16;
     bool ok = pool_carve(p, [&](Carve& c) {
         c.take(p.slots, slot_words(cap));
@@ -475,7 +476,9 @@ bool pool_alloc(Pool& p, uint32_t cap) {
     const size_t n = cap, d = D.d, di = D.di;
     p = Pool{};
     p.cap = cap;
+    p.scap = cap + 1;
     p.gcap = (cap + 15) / 16;
+    const size_t ns = p.scap;
     bool ok = pool_carve(p, [&](Carve& c) {
         c.take(p.slots, slot_words(cap));
         c.take(p.d_slots, n);
@@ -488,8 +491,8 @@ bool pool_alloc(Pool& p, uint32_t cap) {
         c.take(p.xpart, xpart_floats(D, cap));
         c.take(p.glimb, glimb_elems(D, cap));
         c.take(p.out, n * D.vocab);
-        c.take(p.conv, (size_t)D.nl * n * di * (D.dc - 1));
-        c.take(p.ssm, (size_t)D.nl * n * di * 16);
+        c.take(p.conv, (size_t)D.nl * ns * di * (D.dc - 1));
+        c.take(p.ssm, (size_t)D.nl * ns * di * 16);
     });
     ok = ok && hipHostMalloc((void**)&p.h_slots, sizeof(uint32_t) * n, hipHostMallocDefault) == hipSuccess;
     ok = ok && hipHostMalloc((void**)&p.h_tokens, sizeof(uint32_t) * n, hipHostMallocDefault) == hipSuccess;
@@ -802,13 +805,13 @@ int32_t redukt_backend_get_state(uint32_t slot, uint32_t layer, float* conv_out,
     if (hipStreamSynchronize(G.stream) != hipSuccess) return BACKEND_FORWARD_FAILED;
     const size_t cl = (size_t)G.dims.di * (G.dims.dc - 1), sl = (size_t)G.dims.di * 16;
     const Pool& p = G.batch;
-    if (conv_out && hipMemcpy(conv_out, p.conv + ((size_t)layer * p.cap + slot) * cl, cl * 4, hipMemcpyDeviceToHost) !=
+    if (conv_out && hipMemcpy(conv_out, p.conv + ((size_t)layer * p.scap + slot) * cl, cl * 4, hipMemcpyDeviceToHost) !=
                         hipSuccess)
         return BACKEND_FORWARD_FAILED;
     if (ssm_out) {
         // the pool holds [16][di] per slot; the caller gets [di][16]
         std::vector<float> sm(sl);
-        if (hipMemcpy(sm.data(), p.ssm + ((size_t)layer * p.cap + slot) * sl, sl * 4, hipMemcpyDeviceToHost) !=
+        if (hipMemcpy(sm.data(), p.ssm + ((size_t)layer * p.scap + slot) * sl, sl * 4, hipMemcpyDeviceToHost) !=
             hipSuccess)
             return BACKEND_FORWARD_FAILED;
         const size_t di = G.dims.di;

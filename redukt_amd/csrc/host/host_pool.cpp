@@ -13,7 +13,9 @@ namespace redukt_host {
 namespace {
 
 // Workers sleep on a generation counter; a job is published by bumping it.  Each worker
-// with id < job's width claims units through one shared atomic index.
+// with id < job's width claims units through one shared atomic index.  A job ends when
+// all of its units have run and no worker that took it is still draining, so a worker
+// can never carry one job's body or index over into the next job.
 class Pool {
 public:
     Pool() {
@@ -53,7 +55,10 @@ public:
         const size_t mine = drain(body, count);
         std::unique_lock<std::mutex> g(mu_);
         done_ += mine;
-        done_cv_.wait(g, [&] { return done_ == count_; });
+        // Every unit has run AND every worker that took this job has left drain(): a worker
+        // still inside drain() holds `body` and reads next_, so the job (and the next one's
+        // reset of next_ and done_) must wait for it.
+        done_cv_.wait(g, [&] { return done_ == count_ && busy_ == 0; });
         body_ = nullptr;
     }
 
@@ -77,12 +82,14 @@ private:
                 if (id >= width_ || body_ == nullptr) continue;
                 body = body_;
                 count = count_;
+                ++busy_;
             }
             const size_t n = drain(*body, count);
-            if (n) {
+            {
                 std::lock_guard<std::mutex> g(mu_);
                 done_ += n;
-                if (done_ == count_) done_cv_.notify_all();
+                --busy_;
+                if (done_ == count_ && busy_ == 0) done_cv_.notify_all();
             }
         }
     }
@@ -96,6 +103,7 @@ private:
     bool stop_ = false;
     const std::function<void(size_t)>* body_ = nullptr;
     size_t count_ = 0, done_ = 0;
+    unsigned busy_ = 0;  // workers between taking the current job and leaving drain()
     unsigned width_ = 0;
     std::atomic<size_t> next_{0};
 };

@@ -193,6 +193,22 @@ int32_t redukt_lockstep::run_lockstep(const Job& job, redukt_lockstep_stats& sta
     std::vector<uint32_t> active, fwd_slots, fwd_tokens, resets;
     active.reserve(slots);
     uint32_t next_file = 0;
+    // The backbone failed: every file still in a lane and every file not yet admitted is
+    // marked INCOMPLETE with no output, so a caller reading per-file status never takes a
+    // partial file for a finished one.
+    auto abort_run = [&]() {
+        for (Lane& l : lanes) {
+            if (l.file < 0) continue;
+            if (job.status) job.status[l.file] = REDUKT_CODEC_INCOMPLETE;
+            if (job.mode == Mode::Encode) job.out_len[l.file] = 0;
+            l.file = -1;
+        }
+        for (uint32_t f = next_file; f < job.n_files; ++f) {
+            if (job.status) job.status[f] = REDUKT_CODEC_INCOMPLETE;
+            if (job.mode == Mode::Encode) job.out_len[f] = 0;
+        }
+        return REDUKT_LOCKSTEP_FORWARD;
+    };
     for (;;) {
         // Admission: every free slot takes the next file, after a reset of its state.
         resets.clear();
@@ -207,7 +223,7 @@ int32_t redukt_lockstep::run_lockstep(const Job& job, redukt_lockstep_stats& sta
             resets.push_back(i);
         }
         if (!resets.empty() && api.batch_reset(resets.data(), uint32_t(resets.size())) != BACKEND_OK)
-            return REDUKT_LOCKSTEP_FORWARD;
+            return abort_run();
         active.clear();
         for (uint32_t i = 0; i < slots; ++i)
             if (lanes[i].file >= 0) active.push_back(i);
@@ -247,11 +263,11 @@ int32_t redukt_lockstep::run_lockstep(const Job& job, redukt_lockstep_stats& sta
             fwd_tokens.push_back(l.next_token);
         }
         if (!resets.empty() && api.batch_reset(resets.data(), uint32_t(resets.size())) != BACKEND_OK)
-            return REDUKT_LOCKSTEP_FORWARD;
+            return abort_run();
         if (!fwd_slots.empty() &&
             api.forward_batch(uint32_t(fwd_slots.size()), fwd_slots.data(), fwd_tokens.data(), logits.data(), vocab) !=
                 BACKEND_OK)
-            return REDUKT_LOCKSTEP_FORWARD;
+            return abort_run();
         stats.forward_secs += since(tb);
         ++stats.steps;
     }
@@ -282,7 +298,13 @@ int32_t redukt_lockstep::run_single(const Job& job, redukt_lockstep_stats& stats
             }
             ++l.since_reset;
             l.row = 0;
-            if (api.forward(l.next_token, logits.data(), vocab) != BACKEND_OK) return REDUKT_LOCKSTEP_FORWARD;
+            if (api.forward(l.next_token, logits.data(), vocab) != BACKEND_OK) {
+                for (uint32_t g = f; g < job.n_files; ++g) {
+                    if (job.status) job.status[g] = REDUKT_CODEC_INCOMPLETE;
+                    if (job.mode == Mode::Encode) job.out_len[g] = 0;
+                }
+                return REDUKT_LOCKSTEP_FORWARD;
+            }
             stats.forward_secs += since(tb);
             ++stats.steps;
         }

@@ -569,8 +569,10 @@ struct EmbedArgs {
 
 // x[b] = emb[token[b]] (Q8: q * scale), model.rs:93-101 / gemv.rs:285-295.  Block (0, b)
 // copies slot b into the step's slot list; with `check` it also validates the slot and
-// the token and looks for duplicate slots, recording failures in *err and clamping so
-// no index can leave its buffer.  Thread q of block (x, b) owns columns 4q' .. 4q'+3,
+// the token and looks for duplicate slots, recording failures in *err.  An entry with a
+// bad slot or token, or whose slot an earlier entry of the batch already names, is
+// routed to the pool's scratch slot (index cap), so it never touches a real slot's state
+// and no two streams of the step share one; its token is clamped into the vocabulary.  Thread q of block (x, b) owns columns 4q' .. 4q'+3,
 // q' = 256 x + q; with xw it also writes their x * w limbs and, four threads per
 // 16-column tile, the tile's sum of x^2 (sequential over the four, then xor 1, xor 2).
 __global__ __launch_bounds__(kBlock) void k_embed(EmbedArgs a) {
@@ -580,13 +582,24 @@ __global__ __launch_bounds__(kBlock) void k_embed(EmbedArgs a) {
     if (blockIdx.x == 0) {
         const uint32_t s = a.slots_in[b];
         if (a.check) {
-            bool dup = false;
+            __shared__ int earlier;
+            if (threadIdx.x == 0) earlier = 0;
+            __syncthreads();
+            bool dup = false, first_dup = false;
             for (uint32_t c = threadIdx.x; c < a.n; c += blockDim.x)
-                if (c != b && a.slots_in[c] == s) dup = true;
-            if (threadIdx.x == 0 && (tok >= (uint32_t)a.emb.rows || s >= a.cap)) atomicOr(a.err, 1u);
+                if (c != b && a.slots_in[c] == s) {
+                    dup = true;
+                    if (c < b) first_dup = true;
+                }
+            if (first_dup) earlier = 1;   // benign same-value race on the flag
+            const bool bad = tok >= (uint32_t)a.emb.rows || s >= a.cap;
+            if (threadIdx.x == 0 && bad) atomicOr(a.err, 1u);
             if (dup) atomicOr(a.err, 2u);
+            __syncthreads();
+            if (threadIdx.x == 0) a.slots[b] = bad || earlier ? a.cap : s;
+        } else if (threadIdx.x == 0) {
+            a.slots[b] = clamp_slot(s, a.cap);
         }
-        if (threadIdx.x == 0) a.slots[b] = clamp_slot(s, a.cap);
     }
     if (tok >= (uint32_t)a.emb.rows) tok = a.emb.rows - 1;
     const int k = 4 * (blockIdx.x * kBlock + threadIdx.x);
@@ -646,7 +659,8 @@ struct MixInArgs {
     const float* conv_w;
     const float* conv_b;
     const uint32_t* slots;
-    uint32_t cap, n;
+    uint32_t cap, n;           // batch rows of the scratch arrays, streams
+    uint32_t scap;             // state slots (conv state rows; the slot clamp bound)
     float* u;                  // [n][di]
     float* z;                  // [n][di]
     float* xpart;              // [di / 32][cap][xr_pad] (32-channel x_proj partials)
@@ -770,8 +784,8 @@ __global__ __launch_bounds__(kBlock) void k_mix_in(MixInArgs a) {
     // Conv state of the lane's channels (used when dc = 4 on the conv branch): three loads
     // of E floats from an offset clamped into the state buffer; streamed (non-temporal), as
     // the state is read and written once per step.
-    const uint32_t slot = conv_branch ? clamp_slot(slot_raw, a.cap) : 0u;
-    const size_t conv_floats = (size_t)a.cap * a.di * (dc - 1);
+    const uint32_t slot = conv_branch ? clamp_slot(slot_raw, a.scap) : 0u;
+    const size_t conv_floats = (size_t)a.scap * a.di * (dc - 1);
     fE stv[3];
     {
         const size_t off = min(((size_t)slot * a.di + min(ch, a.di - E)) * 3, conv_floats - 3 * E);
@@ -946,7 +960,8 @@ struct ScanArgs {
     const float* a_exp;    // [16][di]
     const float* d_vec;
     const uint32_t* slots;
-    uint32_t cap, n;
+    uint32_t cap, n;       // batch rows of the partials, streams
+    uint32_t scap;         // state slots (the slot clamp bound)
     __bf16* glimb;         // [groups][di/32][3][64][8]
     int di, dr;
 };
@@ -1094,7 +1109,7 @@ __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
     BufRsrc rs[SPT];
 #pragma unroll
     for (int s = 0; s < SPT; s++) {
-        rs[s] = buf_rsrc(a.ssm + (size_t)clamp_slot(slot_raw[s], a.cap) * 16 * diu, 16u * row4);
+        rs[s] = buf_rsrc(a.ssm + (size_t)clamp_slot(slot_raw[s], a.scap) * 16 * diu, 16u * row4);
 #pragma unroll
         for (int n = 0; n < 16; n++) st[s][n] = buf_ld_f32<kStream>(rs[s], j4, (uint32_t)n * row4);
     }
@@ -1936,8 +1951,8 @@ void build_step(const ModelView& m, Pool& p, const StepIO& io, std::vector<Launc
     const int ks_x = m.layers[0].in_x.ks, tiles = d / kRowTile;
     io_index = (int)out.size();
     out.push_back(embed_launch(*m.emb, p, io, m.layers[0].norm_w, pre ? p.xw : nullptr, p.ssp, ks_x, tiles));
-    const size_t conv_layer = (size_t)p.cap * di * (D.dc - 1);
-    const size_t ssm_layer = (size_t)p.cap * di * 16;
+    const size_t conv_layer = (size_t)p.scap * di * (D.dc - 1);
+    const size_t ssm_layer = (size_t)p.scap * di * 16;
     const bool q8 = m.layers[0].in_x.group != 0;
     const bool q8xp = m.layers[0].x_proj.group != 0;
     const uint32_t lds_in = mix_in_lds_bytes(ks_x, pre, in_tiles);
@@ -1947,12 +1962,12 @@ void build_step(const ModelView& m, Pool& p, const StepIO& io, std::vector<Launc
     for (uint32_t li = 0; li < D.nl; li++) {
         const DLayer& L = m.layers[li];
         MixInArgs ma{p.x, L.norm_w, L.norm_b, L.in_x, L.in_z, L.x_proj, nxb, p.conv + li * conv_layer,
-                     L.conv_w, L.conv_b, p.slots, p.cap, n, p.u, p.z, p.xpart, di, (int)D.dc, d, xr_pad,
+                     L.conv_w, L.conv_b, p.slots, p.cap, n, p.scap, p.u, p.z, p.xpart, di, (int)D.dc, d, xr_pad,
                      p.xw, p.ssp, tiles};
         const int zb = L.in_z.rt / in_tiles;
         out.push_back(Launch::make(fin, dim3(nxb + zb, in_chunks), dim3(kBlock), lds_in, KC_MIX_IN, ma));
         ScanArgs sa{p.xpart, nxp, xr_pad, (int)D.xr(), p.u, p.z, p.ssm + li * ssm_layer, L.dt_w, L.dt_q,
-                    L.dt_scales, L.dt_pad, L.dt_b, L.a_exp, L.d_vec, p.slots, p.cap, n, p.glimb, di, (int)D.dr};
+                    L.dt_scales, L.dt_pad, L.dt_b, L.a_exp, L.d_vec, p.slots, p.cap, n, p.scap, p.glimb, di, (int)D.dr};
         const void* fs = scan_fn(L.dt_q != nullptr, !m.exact_scan, (int)D.dr, nxp, spt);
         out.push_back(Launch::make(fs, dim3(xcd_grid((di + kBlock - 1) / kBlock, (n + spt - 1) / spt)), dim3(kBlock), 0,
                                    KC_SCAN, sa));
@@ -2109,6 +2124,9 @@ hipError_t StepRunner::run(const StepSource& src, Pool& p, const StepIO& io, hip
         if (graphs_.size() >= 8) {
             auto old = std::min_element(graphs_.begin(), graphs_.end(),
                                         [](const Graph& a, const Graph& b) { return a.last_use < b.last_use; });
+            // The stream-ordered entry point returns without waiting: the evicted graph
+            // may still be queued or running.
+            RDK_TRY(hipStreamSynchronize(st));
             destroy(*old);
             graphs_.erase(old);
         }
@@ -2171,10 +2189,10 @@ hipError_t enqueue_reset_rwkv(const RDims& D, Pool& P, const uint32_t* d_slots, 
 hipError_t enqueue_reset(const Dims& D, Pool& P, const uint32_t* d_slots, uint32_t n, hipStream_t st) {
     if (n == 0) return hipSuccess;
     const size_t conv_stride = (size_t)D.di * (D.dc - 1), ssm_stride = (size_t)D.di * 16;
-    ZeroArgs zc{P.conv, d_slots, P.cap, conv_stride, (size_t)P.cap * conv_stride, (int)D.nl};
+    ZeroArgs zc{P.conv, d_slots, P.cap, conv_stride, (size_t)P.scap * conv_stride, (int)D.nl};
     k_zero_slots<<<dim3((unsigned)((conv_stride + kBlock - 1) / kBlock), n), kBlock, 0, st>>>(zc);
     RDK_TRY(hipGetLastError());
-    ZeroArgs zs{P.ssm, d_slots, P.cap, ssm_stride, (size_t)P.cap * ssm_stride, (int)D.nl};
+    ZeroArgs zs{P.ssm, d_slots, P.cap, ssm_stride, (size_t)P.scap * ssm_stride, (int)D.nl};
     k_zero_slots<<<dim3((unsigned)((ssm_stride + kBlock - 1) / kBlock), n), kBlock, 0, st>>>(zs);
     return hipGetLastError();
 }

@@ -65,11 +65,16 @@ struct Dims {
 // the last stream of a ragged chunk too (those words only feed streams never stored).
 constexpr uint32_t kSlotWordAlign = 64;
 
-// State: conv [layer][slot][di][dc-1] and ssm [layer][slot][16][di] f32 (state-major, so
+// State: conv [layer][slot][di][dc-1] and ssm [layer][slot][16][di] f32 over scap slots (state-major, so
 // the scan's loads of one state index over 64 channels are contiguous); one slot's state
 // of one layer is one contiguous run either way (18 KB + 96 KB at Mamba-130M).
 struct Pool {
     uint32_t cap = 0;
+    // State slots: cap + 1.  Slot `cap` is a scratch slot no caller can name: a
+    // device-checked step (forward_batch_device) routes every invalid entry and every
+    // repeat of a slot already listed earlier in the batch there, so a bad entry never
+    // touches a real slot and no two streams of a step share one.
+    uint32_t scap = 0;
     uint32_t gcap = 0;           // stream groups of 16 covering cap
     void* block = nullptr;       // the one device allocation all device arrays below are carved from
     float* conv = nullptr;

@@ -40,8 +40,9 @@ RwkvSizes rwkv_sizes(const RDims& D, uint32_t cap) {
     auto ks_of = [](uint32_t cols) { return (int)((cols + kKAlign - 1) / kKAlign * (kKAlign / kKStep)); };
     z.ks_d = ks_of(D.d);
     z.ks_f = ks_of(D.f);
-    z.state_d = (size_t)cap * D.nl * D.d;
-    z.wkv = (size_t)cap * D.nl * D.h * D.n * D.n;
+    // Recurrent state over cap + 1 slots: slot cap is the pool's scratch slot.
+    z.state_d = (size_t)(cap + 1) * D.nl * D.d;
+    z.wkv = (size_t)(cap + 1) * D.nl * D.h * D.n * D.n;
     z.mixl = gcap * z.ks_d * 3 * 512;
     z.gatedl = z.mixl;
     z.actl = gcap * z.ks_f * 3 * 512;
@@ -72,7 +73,7 @@ struct ShiftArgs {
     float* prev;                 // slot s's previous ln output at prev + s * prev_stride (null: none)
     size_t prev_stride;
     const uint32_t* slots;
-    uint32_t cap;
+    uint32_t cap;                // state slots of the pool (the clamp bound)
     int nmix;                    // 0: the ln output itself goes to out[0]
     const float* mix[kMaxShiftMix];
     __bf16* out[kMaxShiftMix];
@@ -322,7 +323,7 @@ struct WkvArgs {
     size_t slot_stride;
     float* vfirst;           // [n][d]
     const uint32_t* slots;
-    uint32_t cap;
+    uint32_t cap;            // state slots of the pool (the clamp bound)
     __bf16* gated;           // B-fragment limbs with ks k-steps
     int ks, d, layer, g1k;
 };
@@ -440,7 +441,7 @@ void RwkvStep::build(Pool& p, const StepIO& io, std::vector<Launch>& out, int& i
     const size_t wkv_layer = (size_t)D.h * D.n * D.n;
     for (uint32_t l = 0; l < D.nl; l++) {
         const RLayer& L = m.layers[l];
-        ShiftArgs s1{p.x, L.ln1_w, L.ln1_b, p.x_att + (size_t)l * d, state_stride, p.slots, p.cap, 6, {}, {}, z.ks_d, d};
+        ShiftArgs s1{p.x, L.ln1_w, L.ln1_b, p.x_att + (size_t)l * d, state_stride, p.slots, p.scap, 6, {}, {}, z.ks_d, d};
         for (int k = 0; k < 6; k++) {
             s1.mix[k] = L.mix[k];
             s1.out[k] = mixl[k];
@@ -461,13 +462,13 @@ void RwkvStep::build(Pool& p, const StepIO& io, std::vector<Launch>& out, int& i
             if (k != kLoraV || l != 0) p2.add(L.l2[k], loral[k], PROJ_STORE, ACT_NONE, p.lorad + k * d, 4 * d, nullptr, 0);
         out.push_back(p2.launch(n));
         WkvArgs wa{p.rkv, p.lorad, L.w0, L.a0, L.v0, L.k_k, L.k_a, L.r_k, L.ln_x_w, L.ln_x_b,
-                   p.wkv + l * wkv_layer, (size_t)D.nl * wkv_layer, p.vfirst, p.slots, p.cap, p.gatedl, z.ks_d, d,
+                   p.wkv + l * wkv_layer, (size_t)D.nl * wkv_layer, p.vfirst, p.slots, p.scap, p.gatedl, z.ks_d, d,
                    (int)l, (int)D.g1k};
         out.push_back(Launch::make((const void*)k_rwkv_wkv, dim3(D.h, n), dim3(kHead), 0, KC_WKV, wa));
         ProjBuilder po;
         po.add(L.o, p.gatedl, PROJ_RESID, ACT_NONE, p.x, d, nullptr, 0);
         out.push_back(po.launch(n));
-        ShiftArgs s2{p.x, L.ln2_w, L.ln2_b, p.x_ffn + (size_t)l * d, state_stride, p.slots, p.cap, 1, {}, {}, z.ks_d, d};
+        ShiftArgs s2{p.x, L.ln2_w, L.ln2_b, p.x_ffn + (size_t)l * d, state_stride, p.slots, p.scap, 1, {}, {}, z.ks_d, d};
         s2.mix[0] = L.ffn_x_k;
         s2.out[0] = p.ffnl;
         out.push_back(Launch::make(shift_fn(s2.nmix), dim3(n), dim3(kBlock), 0, KC_SHIFT, s2));
@@ -481,7 +482,7 @@ void RwkvStep::build(Pool& p, const StepIO& io, std::vector<Launch>& out, int& i
     const TMat& H = *m.head;
     const bool ws = H.group != 0 && H.group == H.cols && H.ks / 2 <= 12;
     if (ws) {
-        ShiftArgs sf{p.x, m.ln_out_w, m.ln_out_b, nullptr, 0, p.slots, p.cap, 0, {}, {}, z.ks_d, d};
+        ShiftArgs sf{p.x, m.ln_out_w, m.ln_out_b, nullptr, 0, p.slots, p.scap, 0, {}, {}, z.ks_d, d};
         sf.out[0] = p.headl;
         out.push_back(Launch::make(shift_fn(sf.nmix), dim3(n), dim3(kBlock), 0, KC_SHIFT, sf));
     }

@@ -134,6 +134,8 @@ class Lockstep:
     def decompress(self, streams: Sequence[bytes], n_tokens: Sequence[int], reset_every: int = DEFAULT_RESET_EVERY
                    ) -> Tuple[List[np.ndarray], Stats]:
         n = len(streams)
+        if len(n_tokens) != n:
+            raise ValueError(f"decompress: {n} streams but {len(n_tokens)} token counts")
         data = [np.frombuffer(bytes(s), np.uint8).copy() for s in streams]
         slen = np.array([d.size for d in data] or [0], np.uint64)
         ntok = np.array(list(n_tokens) or [0], np.uint64)

@@ -21,3 +21,9 @@ def full_model(tmp_path_factory):
     p = str(tmp_path_factory.mktemp("mamba130m") / "model.rbin")
     synth.write_synthetic_mamba(p, rbin.MAMBA_130M, seed=0)
     return p
+
+
+# Worker pools stay within one GPU's share of host cores (16), whatever the machine
+# reports: the oracle's GEMV threads and the host library's coding threads.
+os.environ.setdefault("ORACLE_THREADS", str(min(os.cpu_count() or 1, 16)))
+os.environ.setdefault("REDUKT_HOST_THREADS", str(min(os.cpu_count() or 1, 16)))

@@ -4,7 +4,9 @@
  * it to mix(s * 0x100000001b3 + t + 1); the logits of state s are
  *   l[v] = float((mix(s ^ v * 0x9e3779b97f4a7c15) >> 40) % 4001) / 400 - 5    (f32 ops).
  * The weights file holds the vocabulary size as one little-endian u32.
- * FAKE_PLUGIN_ABI=1 in the environment makes abi_version() report a v1-only plugin. */
+ * FAKE_PLUGIN_ABI=1 in the environment makes abi_version() report a v1-only plugin.
+ * FAKE_PLUGIN_FAIL_AFTER=k makes every forward / forward_batch after the first k
+ * (counted since init) fail with FORWARD_FAILED. */
 #include <stdint.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -19,6 +21,13 @@ static uint32_t g_vocab;
 static uint64_t g_v1;
 static uint64_t* g_slot;
 static uint32_t g_cap;
+static uint64_t g_calls;
+
+/* 1 when this forward call must fail (FAKE_PLUGIN_FAIL_AFTER). */
+static int fail_now(void) {
+    const char* e = getenv("FAKE_PLUGIN_FAIL_AFTER");
+    return e && ++g_calls > (uint64_t)strtoull(e, NULL, 10);
+}
 
 static uint64_t mix(uint64_t z) {
     z += 0x9e3779b97f4a7c15ULL;
@@ -44,6 +53,7 @@ int redukt_backend_init(const uint8_t* path, int32_t dev, BackendInfo* info) {
     if (got != 1 || v == 0) return 4;
     g_vocab = v;
     g_v1 = 0;
+    g_calls = 0;
     if (info) {
         memset(info, 0, sizeof *info);
         info->ffi_version = 1;
@@ -55,7 +65,7 @@ int redukt_backend_init(const uint8_t* path, int32_t dev, BackendInfo* info) {
 }
 
 int redukt_backend_forward(uint32_t tok, float* out, uint32_t vocab) {
-    if (vocab != g_vocab || tok >= g_vocab || !out) return 2;
+    if (vocab != g_vocab || tok >= g_vocab || !out || fail_now()) return 2;
     g_v1 = step(g_v1, tok);
     logits_of(g_v1, out);
     return 0;
@@ -104,6 +114,7 @@ int32_t redukt_backend_forward_batch(uint32_t n, const uint32_t* slots, const ui
         for (uint32_t j = 0; j < i; ++j)
             if (slots[j] == slots[i]) return 5;
     }
+    if (fail_now()) return 2;
     for (uint32_t i = 0; i < n; ++i) {
         g_slot[slots[i]] = step(g_slot[slots[i]], toks[i]);
         logits_of(g_slot[slots[i]], out + (size_t)i * g_vocab);

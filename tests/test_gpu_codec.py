@@ -12,8 +12,8 @@ import numpy as np
 import pytest
 
 from oracle import codec as OC
-from redukt_amd import codec, ffi, hip, rbin, rwkv, synth
-from redukt_amd.lockstep import Lockstep
+from redukt_amd import archive, codec, ffi, hip, rbin, rwkv, synth
+from redukt_amd.lockstep import Lockstep, LockstepError
 
 pytestmark = pytest.mark.gpu
 
@@ -98,3 +98,49 @@ def test_mamba130m_lockstep_roundtrip(full_model):
     with Lockstep(full_model, profile=Q8ROW_ALL, slots=0) as single:
         ref, _ = single.compress(files[:4], reset_every=16)
     assert ref == out[:4]
+
+
+@pytest.mark.parametrize("reset_log2,lengths", [(12, (70, 33, 1, 90)), (8, (600, 260, 300, 513, 257))])
+def test_mamba130m_rdkt_v5_archives(full_model, reset_log2, lengths):
+    """GPU lockstep streams in RDKT v5 archives (src/application/codec.rs:540-580, 648-720):
+    HEADER (BACKBONE 3 = plugin, PROFILE 0x51 = int8 weights, RESET_LOG2) | STREAM |
+    CRC-32 of the original data.  Each archive is parsed and split, its CRC checked against
+    the decoded data, and the stream decoded back (the period read from the header) to the
+    original tokens byte for byte.  At RESET_LOG2 8 the files cross resets."""
+    files = token_files(50280, lengths, 10 + reset_log2)
+    reset_every = 1 << reset_log2
+    with Lockstep(full_model, profile=Q8ROW_ALL, slots=4) as ls:
+        streams, _ = ls.compress(files, reset_every=reset_every)
+    arcs = []
+    for f, stm in zip(files, streams):
+        payload = f.astype("<u4").tobytes()
+        h = archive.default_header(len(payload), backbone=archive.BACKBONE_PLUGIN, quant=1, reset_log2=reset_log2)
+        arc = archive.pack(h, stm, payload)
+        assert arc[:4] == b"RDKT" and arc[4] == 5
+        arcs.append(arc)
+    # decode side: header -> period and length, stream -> tokens, CRC of the restored data
+    heads, body = [], []
+    for arc in arcs:
+        h, stm, crc = archive.unpack(arc)
+        assert h.version == 5 and h.backbone == archive.BACKBONE_PLUGIN and h.quant == 1
+        assert h.reset_log2 == reset_log2 and h.has_crc and crc is not None
+        heads.append((h, crc))
+        body.append(stm)
+    assert body == streams
+    with Lockstep(full_model, profile=Q8ROW_ALL, slots=3) as ls:
+        back, _ = ls.decompress(body, [h.total_bytes // 4 for h, _ in heads], reset_every=heads[0][0].reset_every)
+    for f, b, (h, crc) in zip(files, back, heads):
+        data = b.astype("<u4").tobytes()
+        assert len(data) == h.total_bytes and archive.crc32(data) == crc
+        assert np.array_equal(f, b)
+    # A flipped bit early in a stream is caught: the decoder fails, or the restored data
+    # no longer match the archive's CRC.
+    bad = bytearray(arcs[0])
+    bad[heads[0][0].header_size + 1] ^= 0x10
+    h, stm, crc = archive.unpack(bytes(bad))
+    with Lockstep(full_model, profile=Q8ROW_ALL, slots=1) as ls:
+        try:
+            out, _ = ls.decompress([stm], [h.total_bytes // 4], reset_every=h.reset_every)
+            assert archive.crc32(out[0].astype("<u4").tobytes()) != crc
+        except LockstepError as e:
+            print(f"corrupted stream rejected by the decoder: {e}")

@@ -293,6 +293,51 @@ def test_device_resident_entry_point(models):
                 b.close()
 
 
+def _device_step(be, slots, toks, v):
+    d_s = hip.DeviceBuffer.from_array(np.array(slots, np.uint32))
+    d_t = hip.DeviceBuffer.from_array(np.array(toks, np.uint32))
+    d_o = hip.DeviceBuffer(len(slots) * v * 4)
+    try:
+        be.forward_batch_device(len(slots), d_s.ptr, d_t.ptr, d_o.ptr)
+        status = be.device_status()
+        return status, d_o.download(np.float32, len(slots) * v).reshape(len(slots), v)
+    finally:
+        for b in (d_s, d_t, d_o):
+            b.close()
+
+
+def test_device_check_contains_bad_entries(models):
+    # A device-checked step with a repeated slot or a bad token routes the offending entries
+    # to the pool's scratch slot: slots the call does not name keep their state bit for bit,
+    # and the valid entries (a repeated slot's first occurrence included) advance exactly as
+    # they would in a valid call.
+    dims = SMALL_BASE
+    with ffi.PluginBackend(models["base"], profile=6) as be:
+        v = be.vocab
+        be.batch_init(8)
+        state = lambda s: [be.get_state(s, l, dims.d_inner, 4) for l in range(dims.n_layer)]
+        def start():
+            be.batch_reset(None)
+            st, _ = _device_step(be, [7, 6, 5, 4, 0, 1, 2, 3], [(11 * i + 5) % v for i in range(8)], v)
+            assert st == ffi.BackendResult.OK
+        start()
+        snap = {s: state(s) for s in range(8)}
+        st, dup = _device_step(be, [7, 6, 7, 4, 2], [9, 8, 7, 6, v + 3], v)
+        assert st == ffi.BackendResult.INVALID_ARGUMENT
+        for s in (0, 1, 2, 3, 5):
+            for (c0, s0), (c1, s1) in zip(snap[s], state(s)):
+                assert np.array_equal(c0, c1) and np.array_equal(s0, s1), s
+        after = {s: state(s) for s in (7, 6, 4)}
+        start()
+        st, ok = _device_step(be, [7, 6, 4], [9, 8, 6], v)
+        assert st == ffi.BackendResult.OK
+        for pos_dup, pos_ok in ((0, 0), (1, 1), (3, 2)):
+            assert np.array_equal(bits(dup[pos_dup]), bits(ok[pos_ok])), pos_dup
+        for s in (7, 6, 4):
+            for (c0, s0), (c1, s1) in zip(after[s], state(s)):
+                assert np.array_equal(c0, c1) and np.array_equal(s0, s1), s
+
+
 @pytest.mark.parametrize("profile", [0, 1, 6, 14])
 def test_mamba130m_parity(full_model, profile):
     with ffi.PluginBackend(full_model, profile=profile) as be:
@@ -336,6 +381,11 @@ def test_mamba130m_reset_boundary_and_large_batch_invariance(full_model):
             if t == 0:
                 first = out.copy()
         assert np.array_equal(bits(out), bits(first))
+        # The restarted forward is a fresh stream's first forward: the oracle's from zero
+        # state, within the parity tolerance.
+        orc = O.MambaOracle(full_model, 6, cap=2)
+        assert_parity(out, orc.forward([0, 1], [int(x) for x in seq[4096]]), "forward 4097 vs oracle")
+        orc.close()
         # A stream inside a 128-stream batch gets the bits it gets alone, at full size.
         tok = int(seq[1, 0])
         be.batch_reset(None)

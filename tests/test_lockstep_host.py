@@ -162,3 +162,26 @@ def test_open_errors(fake, tmp_path):
     with pytest.raises(LockstepError) as e:
         Lockstep(str(tmp_path / "missing.bin"), plugin_path=so, slots=1)
     assert e.value.status == LockstepStatus.PLUGIN_INIT
+
+
+@pytest.mark.parametrize("slots", [0, 2])
+def test_backbone_failure_marks_unfinished_files(fake, monkeypatch, slots):
+    # forward fails mid-run: files finished before it keep OK and their bytes; every file in
+    # flight or never admitted reports INCOMPLETE, never OK.
+    so, w = fake
+    fs = files(6, (3, 40, 40, 40, 40))
+    monkeypatch.setenv("FAKE_PLUGIN_FAIL_AFTER", "12")
+    with Lockstep(w, plugin_path=so, slots=slots) as ls:
+        with pytest.raises(LockstepError) as e:
+            ls.compress(fs, reset_every=0)
+    assert e.value.status == LockstepStatus.FORWARD
+    st = e.value.file_status
+    assert st[0] == C.CodecStatus.OK
+    assert all(s == C.CodecStatus.INCOMPLETE for s in st[1:]), st
+
+
+def test_decompress_rejects_mismatched_lengths(fake):
+    so, w = fake
+    with Lockstep(w, plugin_path=so, slots=2) as ls:
+        with pytest.raises(ValueError):
+            ls.decompress([b"\x00" * 8, b"\x00" * 8], [4])
