@@ -2,16 +2,19 @@
 
 Default workload: Mamba-130M with int8 weight-only quantisation (per-output-row f32
 scales on in_proj, x_proj, dt_proj, out_proj and the tied head; f32 activations and
-state), 32 lockstep streams with independent Zipf(1.1) token ids, every stream's state
+state), 128 lockstep streams with independent Zipf(1.1) token ids, every stream's state
 reset at the 4096-token boundary (placed inside the timed region).  A step is one token
-for each of the 32 streams.  Inputs (weights, token ids, slots) are resident in HBM
+for each of the 128 streams.  Inputs (weights, token ids, slots) are resident in HBM
 before timing starts; logits stay on the device.
 
-Prints one JSON line.  `roofline` covers the dominant kernel (HIP events on the
+Prints one JSON line.  `value` is that workload's tokens/s.  `grid` adds the rest of the
+metric, Mamba-130M at 1, 32 and 128 streams with F32 and int8 weights: device tok/s
+(logits left on the device) and FFI tok/s (synchronous forward_batch into host memory).
+`roofline` covers the dominant kernel of the default workload (HIP events on the
 library's stream around all of a step's launches of that kernel issued back to back, in
-a probe pass after the timed region);
-`cpu_baseline` times the CPU oracle (a C restatement of the reference CPU path) on the
-host cores for a bounded sample of the same workload.
+a probe pass after the timed region); `cpu_baseline` times the CPU oracle (a C
+restatement of the reference CPU path) on the host cores for a bounded sample of the
+same workload, with all of one GPU's share of the cores and with one.
 """
 from __future__ import annotations
 
@@ -155,16 +158,37 @@ def ensure_model(path: str) -> str:
     return path
 
 
+def cpu_info() -> dict:
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count() or 1
+    return {"nproc": os.cpu_count() or 1, "affinity": avail, "model": model}
+
+
 def cpu_baseline(path: str, profile: int, n: int, tokens: np.ndarray, budget_s: float, mamba: bool = True,
                  probs: bool = False) -> dict:
+    """The oracle stepping the same workload on the host cores: first with one GPU's share
+    of them (16, or fewer if the process may use fewer), then one step on one thread."""
     from oracle import oracle as O   # the CPU restatement; test/baseline infrastructure only
 
-    threads = min(os.cpu_count() or 1, 16)
+    info = cpu_info()
+    threads = max(1, min(info["affinity"], 16))
     O.set_threads(threads)
     m = O.MambaOracle(path, profile, cap=n) if mamba else O.RwkvOracle(path, profile, cap=n)
     slots = list(range(n))
+
     def fwd(t: int) -> None:
-        logits = m.forward(slots, [int(x) for x in tokens[t]])
+        logits = m.forward(slots, [int(x) for x in tokens[t % len(tokens)]])
         if probs:                                           # softmax_into per stream, on the host
             for r in logits:
                 O.softmax(r)
@@ -173,16 +197,110 @@ def cpu_baseline(path: str, profile: int, n: int, tokens: np.ndarray, budget_s: 
     t0 = time.perf_counter()
     fwd(1)
     one = time.perf_counter() - t0
-    steps = max(1, min(len(tokens) - 2, int(budget_s / max(one, 1e-6))))
+    steps = max(1, int(budget_s / max(one, 1e-6)))
     t0 = time.perf_counter()
     for t in range(steps):
         fwd(2 + t)
     dt = time.perf_counter() - t0
+    # one thread, one step (the caches are warm from the steps above)
+    O.set_threads(1)
+    t1 = time.perf_counter()
+    fwd(2 + steps)
+    dt1 = time.perf_counter() - t1
+    O.set_threads(threads)
     m.close()
     return {"value": round(n * steps / dt, 2), "unit": "tok/s", "cores": threads, "kind": "port",
             "sample": f"CPU oracle{' + softmax per stream' if probs else ''}, same weights and profile, "
-                      f"{n} lockstep streams x {steps} steps "
-                      f"({dt:.1f} s) after one warm-up step"}
+                      f"{n} lockstep streams x {steps} steps ({dt:.1f} s) on {threads} threads after one "
+                      f"warm-up step; then 1 step on 1 thread ({dt1:.1f} s)",
+            "value_1_thread": round(n / dt1, 2), "nproc": info["nproc"], "affinity": info["affinity"],
+            "cpu_model": info["model"]}
+
+
+class Workload:
+    """One backend instance stepping n lockstep streams on device-resident inputs."""
+
+    def __init__(self, be, n: int, vocab: int, tokens: np.ndarray, probs: bool = False):
+        self.be, self.n, self.vocab, self.probs = be, n, vocab, probs
+        self.tokens = tokens
+        be.batch_init(n)
+        self.stream = be.stream()
+        self.d_tokens = hip.DeviceBuffer.from_array(tokens)
+        self.d_slots = hip.DeviceBuffer.from_array(np.arange(n, dtype=np.uint32))
+        self.d_out = hip.DeviceBuffer(n * vocab * 4)
+        self.since = 0
+
+    def step(self, t: int) -> None:
+        if self.since >= RESET_PERIOD:                 # PluginState::tick for every stream
+            self.be.batch_reset(None)
+            self.since = 0
+        self.since += 1
+        t %= len(self.tokens)
+        self.be.forward_batch_device(self.n, self.d_slots.ptr, self.d_tokens.ptr + t * self.n * 4, self.d_out.ptr,
+                                     probs=self.probs)
+
+    def timed(self, W: int, K: int, reset_at: int = -1):
+        """W untimed steps, then K steps between two HIP events on the library's stream.
+        With reset_at >= 0 the 4096-token boundary falls on timed step reset_at."""
+        self.since = RESET_PERIOD - W - reset_at if reset_at >= 0 else 0
+        for t in range(W):
+            self.step(t)
+        assert self.be.device_status() == ffi.BackendResult.OK
+        e0, e1 = hip.Event(), hip.Event()
+        hip.stream_sync(self.stream)
+        wall0 = time.perf_counter()
+        e0.record(self.stream)
+        for t in range(W, W + K):
+            self.step(t)
+        e1.record(self.stream)
+        e1.synchronize()
+        wall = time.perf_counter() - wall0
+        ms = e0.elapsed_ms(e1)
+        assert self.be.device_status() == ffi.BackendResult.OK
+        e0.close()
+        e1.close()
+        return ms, wall
+
+    def ffi_rate(self, steps: int) -> float:
+        """tok/s of the synchronous host-buffer entry point (D2H of n rows of logits)."""
+        out = np.empty((self.n, self.vocab), np.float32)
+        slots = list(range(self.n))
+        self.be.forward_batch(slots, [int(x) for x in self.tokens[0]], out, probs=self.probs)
+        t0 = time.perf_counter()
+        for t in range(steps):
+            self.be.forward_batch(slots, [int(x) for x in self.tokens[t % len(self.tokens)]], out, probs=self.probs)
+        return self.n * steps / (time.perf_counter() - t0)
+
+    def close(self) -> None:
+        for b in (self.d_tokens, self.d_slots, self.d_out):
+            b.close()
+
+
+def grid_rates(path: str, sizes, K: int, W: int, skip=None) -> dict:
+    """Mamba-130M at each batch size with F32 and int8 per-row weights: device tok/s, FFI
+    tok/s and the whole step's bytes over its time against the HBM peak."""
+    dims = rbin.MAMBA_130M
+    rng = np.random.default_rng(4321)
+    out = {}
+    for name in ("f32", "q8row-all"):
+        profile = PROFILES[name]
+        be = ffi.PluginBackend(path, 0, profile)
+        out[name] = {}
+        for n in sizes:
+            if skip == (name, n):
+                continue
+            toks = synth.zipf_tokens(rng, dims.vocab, (W + K + 1, n))
+            wl = Workload(be, n, dims.vocab, toks)
+            ms, _ = wl.timed(W, K)
+            us = ms / K * 1e3
+            sb = step_bytes(dims, profile, n)
+            out[name][str(n)] = {"tok_s": round(n * K / (ms / 1e3), 1), "us_per_step": round(us, 1),
+                                 "step_hbm_frac": round(sb / (us / 1e6) / 1e9 / HBM_PEAK_GBS, 4),
+                                 "ffi_tok_s": round(wl.ffi_rate(max(4, min(K, 32))), 1)}
+            log(f"grid {name} n={n}: {out[name][str(n)]}")
+            wl.close()
+        be.close()
+    return out
 
 
 def main() -> int:
@@ -190,19 +308,22 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1024)
     ap.add_argument("--warmup", type=int, default=32)
-    ap.add_argument("--streams", type=int, default=None, help="default 32 (Mamba), 64 (RWKV-7)")
+    ap.add_argument("--streams", type=int, default=None, help="default 128 (Mamba), 64 (RWKV-7)")
     ap.add_argument("--arch", default="mamba130m", choices=["mamba130m", "rwkv7-0.1b"],
                     help="rwkv7-0.1b: RWKV-7 0.1B, uniform byte-level tokens (not the headline metric)")
     ap.add_argument("--profile", default="q8row-all", choices=sorted(PROFILES))
     ap.add_argument("--exact-scan", action="store_true",
                     help="Mamba scan decay factors by the reference's portable exp (profile bit 3)")
     ap.add_argument("--probe-steps", type=int, default=8)
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-grid", action="store_true", help="skip the 1/32/128 x F32/int8 grid")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="after the probe pass, copy this many MiB device to device on the library's "
                          "stream (a copy of known size for scaling HBM byte counters)")
     ap.add_argument("--model", default=None, help="weight file (written with synthetic weights if absent)")
+    ap.add_argument("--split", type=int, default=None,
+                    help="most sub-batches a step is split into, each on its own HIP stream (REDUKT_GPU_SPLIT)")
     ap.add_argument("--probs", action="store_true",
                     help="hand back the probability vector (softmax over the vocabulary) instead of logits")
     args = ap.parse_args()
@@ -215,9 +336,11 @@ def main() -> int:
     if hip.device_count() < 1:
         print("bench.py: no GPU visible", file=sys.stderr)
         return 1
+    if args.split is not None:
+        os.environ["REDUKT_GPU_SPLIT"] = str(args.split)
 
     mamba = args.arch == "mamba130m"
-    n = args.streams or (32 if mamba else 64)
+    n = args.streams or (128 if mamba else 64)
     K, W = args.steps, args.warmup
     profile = PROFILES[args.profile] | (ffi.PROFILE_EXACT_SCAN if args.exact_scan else 0)
     rng = np.random.default_rng(1234)
@@ -235,41 +358,12 @@ def main() -> int:
         vocab, workload = dims.vocab, f"rwkv7-0.1b-{args.profile}-n{n}-bytes{'-probs' if args.probs else ''}"
 
     be = ffi.PluginBackend(path, 0, profile)
-    be.batch_init(n)
-    stream = be.stream()
-    d_tokens = hip.DeviceBuffer.from_array(tokens)
-    d_slots = hip.DeviceBuffer.from_array(np.arange(n, dtype=np.uint32))
-    d_out = hip.DeviceBuffer(n * vocab * 4)
-    row = n * 4
-
-    # Every stream starts at forward number `since0`, so the 4096-token boundary (reset
-    # before forward 4097) falls on timed step K // 2.
+    wl = Workload(be, n, vocab, tokens, probs=args.probs)
+    stream = wl.stream
+    # The 4096-token boundary (reset before forward 4097) falls on timed step K // 2.
     reset_step = K // 2
-    since = RESET_PERIOD - W - reset_step
-
-    def step(t: int) -> None:
-        nonlocal since
-        if since >= RESET_PERIOD:                      # PluginState::tick for every stream
-            be.batch_reset(None)
-            since = 0
-        since += 1
-        be.forward_batch_device(n, d_slots.ptr, d_tokens.ptr + t * row, d_out.ptr, probs=args.probs)
-
     log(f"warm-up {W} steps, n={n}, profile={args.profile}")
-    for t in range(W):
-        step(t)
-    assert be.device_status() == ffi.BackendResult.OK
-    e0, e1 = hip.Event(), hip.Event()
-    hip.stream_sync(stream)
-    wall0 = time.perf_counter()
-    e0.record(stream)
-    for t in range(W, W + K):
-        step(t)
-    e1.record(stream)
-    e1.synchronize()
-    wall = time.perf_counter() - wall0
-    ms = e0.elapsed_ms(e1)
-    assert be.device_status() == ffi.BackendResult.OK
+    ms, wall = wl.timed(W, K, reset_at=reset_step)
     tok_s = n * K / (ms / 1e3)
     log(f"timed {K} steps: {ms:.2f} ms on the stream ({ms / K * 1e3:.1f} us/step), wall {wall * 1e3:.1f} ms")
 
@@ -277,7 +371,8 @@ def main() -> int:
     # class: (1) class-only steps, all of a step's launches of the class back to back
     # between one event pair (avg_us: per-launch time with the event cost spread over the
     # launches; this is the roofline figure); (2) full steps with every launch of the class
-    # recording its own dispatch start and stop (dispatch_avg_us).
+    # recording its own dispatch start and stop (dispatch_avg_us).  Probed steps run
+    # unsplit, as direct launches.
     per_class = {}
     P = args.probe_steps
     t0 = W + K
@@ -287,7 +382,7 @@ def main() -> int:
         arr = (ctypes.c_void_p * len(evs))(*[e.h for e in evs])
         be.probe_kernel(cls, arr)
         for t in range(P):
-            step(t0 + t % (total - t0))
+            wl.step(t0 + t % (total - t0))
         used = be.probe_used()
         be.probe_kernel(0, None)
         hip.stream_sync(stream)
@@ -310,6 +405,7 @@ def main() -> int:
     dom = max(per_class, key=lambda k: per_class[k]["us_per_step"])
     avg_s = per_class[dom]["avg_us"] / 1e6
     achieved = alg[dom] / avg_s / 1e9
+    achieved_dispatch = alg[dom] / (per_class[dom]["dispatch_avg_us"] / 1e6) / 1e9
     for k, v in per_class.items():
         v["alg_bytes"] = alg[k]
         v["GBps"] = round(alg[k] / (v["avg_us"] / 1e6) / 1e9, 1)
@@ -326,18 +422,15 @@ def main() -> int:
         src.close()
         dst.close()
 
-    # FFI end-to-end rate (host buffers, D2H of n rows of logits, synchronous).
-    out = np.empty((n, vocab), np.float32)
-    slots = list(range(n))
-    f_steps = min(64, K)
-    be.forward_batch(slots, [int(x) for x in tokens[0]], out, probs=args.probs)
-    t0 = time.perf_counter()
-    for t in range(f_steps):
-        be.forward_batch(slots, [int(x) for x in tokens[t % total]], out, probs=args.probs)
-    ffi_tok_s = n * f_steps / (time.perf_counter() - t0)
+    ffi_tok_s = wl.ffi_rate(min(64, K))
+    wl.close()
     be.close()
-    for b in (d_tokens, d_slots, d_out):
-        b.close()
+
+    grid = None
+    if mamba and not args.no_grid and not args.probs and not args.exact_scan and args.model is None:
+        gk, gw = max(8, min(K, 64)), max(2, min(W, 8))
+        grid = grid_rates(path, (1, 32, 128), gk, gw)
+        grid["steps"], grid["warmup"] = gk, gw
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -345,14 +438,15 @@ def main() -> int:
         cpu = cpu_baseline(path, profile, n, tokens, args.cpu_seconds, mamba, args.probs)
 
     # HBM bytes per launch of the dominant kernel from the committed counter passes
-    # (FETCH_SIZE / WRITE_SIZE scaled by a copy of known size), when they cover this workload.
+    # (FETCH_SIZE / WRITE_SIZE scaled by a copy of known size), keyed by workload.
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "hbm_traffic.json")
     if os.path.exists(tpath):
         with open(tpath) as f:
             tj = json.load(f)
-        if tj.get("workload") == workload:
-            traffic = tj["bytes_per_launch"].get(dom)
+        entry = tj.get("workloads", {}).get(workload)
+        if entry:
+            traffic = entry["bytes_per_launch"].get(dom)
 
     sb = step_bytes(dims, profile, n) if mamba else rwkv_step_bytes(dims, profile, n)
     if args.probs:
@@ -373,9 +467,12 @@ def main() -> int:
         "config": {"workload": workload, "layers": dims.n_layer,
                    "d_model": dims.d_model, "vocab": vocab, "streams": n, "weight_profile": args.profile,
                    "reset_every": RESET_PERIOD, "reset_at_timed_step": reset_step,
-                   "output": "probabilities" if args.probs else "logits", "parallelism": "none"},
+                   "output": "probabilities" if args.probs else "logits", "parallelism": "none",
+                   "split_max": int(os.environ.get("REDUKT_GPU_SPLIT", "2"))},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic},
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "achieved_dispatch": round(achieved_dispatch, 1),
+                     "frac_dispatch": round(achieved_dispatch / HBM_PEAK_GBS, 4)},
         "cpu_baseline": cpu,
         "step_bytes": sb,
         "step_GBps": round(sb / (ms / K / 1e3) / 1e9, 1),
@@ -383,6 +480,7 @@ def main() -> int:
         "ffi_tok_s": round(ffi_tok_s, 1),
         "wall_ms": round(wall * 1e3, 2),
         "kernels": per_class,
+        "grid": grid,
     }
     print(json.dumps(result), flush=True)
     return 0

@@ -118,10 +118,12 @@ int32_t redukt_backend_forward_batch_probs(uint32_t n_streams, const uint32_t* s
 /* Stream-ordered step on device-resident inputs: d_slots, d_tokens and d_out are
  * device pointers (n_streams u32, n_streams u32, n_streams*vocab_size f32).  Nothing is
  * copied to or from the host and the call does not wait for the step to finish.
- * Slots and tokens are checked on the device: an invalid or duplicate entry sets a
- * sticky error that redukt_backend_device_status() reports and every index is clamped
- * into range, so a bad entry can never address memory outside the pool.  flags bit 0:
- * write probabilities instead of logits. */
+ * Slots and tokens are checked on the device (against every stream of the call): an
+ * invalid entry, or a slot an earlier entry already names, sets a sticky error that
+ * redukt_backend_device_status() reports and is stepped on a scratch slot of the pool
+ * instead of a real one, so it never touches another stream's state and no index leaves
+ * the pool; the valid entries (a repeated slot's first entry included) advance as in a
+ * valid call.  flags bit 0: write probabilities instead of logits. */
 int32_t redukt_backend_forward_batch_device(uint32_t n_streams, const uint32_t* d_slots, const uint32_t* d_tokens,
                                             float* d_out, uint32_t vocab_size, uint32_t flags);
 

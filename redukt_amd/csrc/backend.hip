@@ -7,6 +7,7 @@
 // reference recipe before upload.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -444,6 +445,7 @@ bool pool_alloc_rwkv(Pool& p, uint32_t cap) {
     p = Pool{};
     p.cap = cap;
     p.scap = cap + 1;
+    p.xcap = cap;
     p.gcap = (cap + 15) / 16;
     bool ok = pool_carve(p, [&](Carve& c) {
         c.take(p.slots, slot_words(cap));
@@ -477,6 +479,7 @@ bool pool_alloc(Pool& p, uint32_t cap) {
     p = Pool{};
     p.cap = cap;
     p.scap = cap + 1;
+    p.xcap = cap;
     p.gcap = (cap + 15) / 16;
     const size_t ns = p.scap;
     bool ok = pool_carve(p, [&](Carve& c) {
@@ -502,7 +505,7 @@ bool pool_alloc(Pool& p, uint32_t cap) {
 
 void free_model() {
     if (G.stream) (void)hipStreamSynchronize(G.stream);
-    G.runner.clear();
+    G.runner.release();
     pool_free(G.v1);
     pool_free(G.batch);
     dev_free_all();
@@ -583,6 +586,20 @@ uint32_t env_weight_profile() {
     return (uint32_t)strtoul(e, nullptr, 0) & 15u;
 }
 
+// REDUKT_GPU_SPLIT: most parts (sub-batches on their own streams) a step is split into.
+uint32_t env_split() {
+    const char* e = getenv("REDUKT_GPU_SPLIT");
+    if (!e || !*e) return kDefaultSplit;
+    return (uint32_t)strtoul(e, nullptr, 10);
+}
+
+// REDUKT_GPU_PART_MIN: fewest streams per part.
+uint32_t env_part_min() {
+    const char* e = getenv("REDUKT_GPU_PART_MIN");
+    if (!e || !*e) return kMinPartStreams;
+    return (uint32_t)strtoul(e, nullptr, 10);
+}
+
 uint32_t env_profile() {
     const char* x = getenv("REDUKT_GPU_EXACT_SCAN");
     return env_weight_profile() | (x && *x && strcmp(x, "0") ? BACKEND_PROFILE_EXACT_SCAN : 0u);
@@ -601,6 +618,7 @@ int init_common(const uint8_t* weights_path, int32_t device_id, uint32_t profile
         return BACKEND_INIT_FAILED;
     }
     G.profile = profile;
+    G.runner.set_split(env_split(), env_part_min());
     G.kind = file_kind(path);
     if ((G.kind == kKindRwkv ? load_rwkv(path, profile) : load_weights(path, profile)) != 0) {
         free_model();

@@ -555,12 +555,14 @@ __device__ __forceinline__ void apply_row_scales(const TMat& w, int t, f32x4 (&a
 struct EmbedArgs {
     TMat emb;
     float* x;                  // [n][d]
-    const uint32_t* tokens;    // caller's device pointers
+    const uint32_t* tokens;    // caller's device pointers, at this part's first row
     const uint32_t* slots_in;
     uint32_t* slots;           // validated copy used by the rest of the step
     uint32_t n, cap;
     int check;
     uint32_t* err;
+    const uint32_t* slots_all; // the whole step's slots (the check covers every part)
+    uint32_t n_all, b_off;     // streams of the whole step; this part's first row in it
     const float* nw0;          // layer 0 norm weight; with xw != null the pre-staged
     __bf16* xw;                // activations of layer 0 are produced here
     float* ssp;
@@ -585,11 +587,12 @@ __global__ __launch_bounds__(kBlock) void k_embed(EmbedArgs a) {
             __shared__ int earlier;
             if (threadIdx.x == 0) earlier = 0;
             __syncthreads();
+            const uint32_t gb = a.b_off + b;   // this entry's row in the whole step
             bool dup = false, first_dup = false;
-            for (uint32_t c = threadIdx.x; c < a.n; c += blockDim.x)
-                if (c != b && a.slots_in[c] == s) {
+            for (uint32_t c = threadIdx.x; c < a.n_all; c += blockDim.x)
+                if (c != gb && a.slots_all[c] == s) {
                     dup = true;
-                    if (c < b) first_dup = true;
+                    if (c < gb) first_dup = true;
                 }
             if (first_dup) earlier = 1;   // benign same-value race on the flag
             const bool bad = tok >= (uint32_t)a.emb.rows || s >= a.cap;
@@ -659,7 +662,7 @@ struct MixInArgs {
     const float* conv_w;
     const float* conv_b;
     const uint32_t* slots;
-    uint32_t cap, n;           // batch rows of the scratch arrays, streams
+    uint32_t cap, n;           // batch rows of the x_proj partials (their row stride), streams
     uint32_t scap;             // state slots (conv state rows; the slot clamp bound)
     float* u;                  // [n][di]
     float* z;                  // [n][di]
@@ -1893,7 +1896,9 @@ const void* head_ws_fn(int np, uint32_t lds) {
 Launch embed_launch(const TMat& emb, Pool& p, const StepIO& io, const float* nw0, __bf16* xw, float* ssp, int ks_x,
                     int tiles) {
     const int d = emb.cols;
-    EmbedArgs ea{emb, p.x, io.tokens, io.slots, p.slots, io.n, p.cap, io.check ? 1 : 0, io.err, nw0, xw, ssp, ks_x, tiles};
+    const uint32_t n_all = io.n_all ? io.n_all : io.n;
+    EmbedArgs ea{emb, p.x, io.tokens + io.b0, io.slots + io.b0, p.slots, io.n, p.cap, io.check ? 1 : 0, io.err,
+                 io.slots, n_all, io.b0, nw0, xw, ssp, ks_x, tiles};
     return Launch::make((const void*)k_embed, dim3((d + 4 * kBlock - 1) / (4 * kBlock), io.n), dim3(kBlock), 0, KC_EMBED,
                         ea);
 }
@@ -1901,7 +1906,7 @@ Launch embed_launch(const TMat& emb, Pool& p, const StepIO& io, const float* nw0
 Launch head_launch(const TMat& H, Pool& p, const StepIO& io, const float* x, const float* nw, const float* nb,
                    const __bf16* xw, const float* ssp, int d, int tiles, bool ws) {
     const uint32_t n = io.n;
-    HeadArgs ha{x, nw, nb, H, io.out, n, d, xw, ssp, tiles};
+    HeadArgs ha{x, nw, nb, H, io.out + (size_t)io.b0 * H.rows, n, d, xw, ssp, tiles};
     if (ws) {
         const uint32_t lds_h = 2 * (uint32_t)H.ks * 3 * kLimbBytes;
         const int tiles_per_block = kHwWaves * kHwTiles;
@@ -1927,11 +1932,30 @@ namespace {
 
 // The launches of one step, in stream order; io_index / head_index / softmax_index name
 // the launches whose arguments carry caller pointers.
-void build_step(const ModelView& m, Pool& p, const StepIO& io, std::vector<Launch>& out, int& io_index,
+// The scratch arrays of one part of a step (rows from b0, a multiple of 16): every
+// per-row array offset by b0 rows, every per-group array by b0 / 16 groups; the state,
+// the partials' row stride (cap) and everything else unchanged.
+Pool part_view(const Pool& p, const Dims& D, int ks_x, int xr_pad, uint32_t b0) {
+    Pool q = p;
+    if (b0 == 0) return q;
+    const size_t g0 = b0 / kRowTile;
+    q.x = p.x + (size_t)b0 * D.d;
+    q.xw = p.xw + g0 * ks_x * 3 * 512;
+    q.ssp = p.ssp + (size_t)b0 * (D.d / kRowTile);
+    q.u = p.u + (size_t)b0 * D.di;
+    q.z = p.z + (size_t)b0 * D.di;
+    q.xpart = p.xpart + (size_t)b0 * xr_pad;
+    q.glimb = p.glimb + g0 * (D.di / kKStep) * 3 * 512;
+    q.slots = p.slots + b0;
+    return q;
+}
+
+void build_step(const ModelView& m, Pool& pool, const StepIO& io, std::vector<Launch>& out, int& io_index,
                 int& head_index, int& softmax_index) {
     const Dims& D = *m.dims;
     const uint32_t n = io.n;
     const int d = (int)D.d, di = (int)D.di;
+    Pool p = part_view(pool, D, m.layers[0].in_x.ks, m.layers[0].x_proj.rt * kRowTile, io.b0);
     const uint32_t in_chunks = (n + kInChunk - 1) / kInChunk;
     const int out_g = m.layers[0].out_proj.group == 0 && n >= (uint32_t)kOutWideFrom ? 2 : 1;
     const uint32_t out_chunks = (n + out_g * kRowTile - 1) / (out_g * kRowTile);
@@ -1962,12 +1986,12 @@ void build_step(const ModelView& m, Pool& p, const StepIO& io, std::vector<Launc
     for (uint32_t li = 0; li < D.nl; li++) {
         const DLayer& L = m.layers[li];
         MixInArgs ma{p.x, L.norm_w, L.norm_b, L.in_x, L.in_z, L.x_proj, nxb, p.conv + li * conv_layer,
-                     L.conv_w, L.conv_b, p.slots, p.cap, n, p.scap, p.u, p.z, p.xpart, di, (int)D.dc, d, xr_pad,
+                     L.conv_w, L.conv_b, p.slots, p.xcap, n, p.scap, p.u, p.z, p.xpart, di, (int)D.dc, d, xr_pad,
                      p.xw, p.ssp, tiles};
         const int zb = L.in_z.rt / in_tiles;
         out.push_back(Launch::make(fin, dim3(nxb + zb, in_chunks), dim3(kBlock), lds_in, KC_MIX_IN, ma));
         ScanArgs sa{p.xpart, nxp, xr_pad, (int)D.xr(), p.u, p.z, p.ssm + li * ssm_layer, L.dt_w, L.dt_q,
-                    L.dt_scales, L.dt_pad, L.dt_b, L.a_exp, L.d_vec, p.slots, p.cap, n, p.scap, p.glimb, di, (int)D.dr};
+                    L.dt_scales, L.dt_pad, L.dt_b, L.a_exp, L.d_vec, p.slots, p.xcap, n, p.scap, p.glimb, di, (int)D.dr};
         const void* fs = scan_fn(L.dt_q != nullptr, !m.exact_scan, (int)D.dr, nxp, spt);
         out.push_back(Launch::make(fs, dim3(xcd_grid((di + kBlock - 1) / kBlock, (n + spt - 1) / spt)), dim3(kBlock), 0,
                                    KC_SCAN, sa));
@@ -1983,7 +2007,7 @@ void build_step(const ModelView& m, Pool& p, const StepIO& io, std::vector<Launc
     softmax_index = -1;
     if (io.probs) {
         softmax_index = (int)out.size();
-        out.push_back(softmax_launch(io.out, (int)D.vocab, n));
+        out.push_back(softmax_launch(io.out + (size_t)io.b0 * D.vocab, (int)D.vocab, n));
     }
 }
 
@@ -2021,12 +2045,52 @@ static bool use_graphs() {
     return on;
 }
 
-StepRunner::~StepRunner() { clear(); }
+StepRunner::~StepRunner() { release(); }
+
+void StepRunner::release() {
+    clear();
+    for (uint32_t k = 0; k < kMaxParts; k++) {
+        if (aux_[k]) (void)hipStreamDestroy(aux_[k]);
+        if (join_[k]) (void)hipEventDestroy(join_[k]);
+        aux_[k] = nullptr;
+        join_[k] = nullptr;
+    }
+    if (fork_) (void)hipEventDestroy(fork_);
+    fork_ = nullptr;
+}
+
+StepRunner& StepRunner::operator=(StepRunner&& o) noexcept {
+    if (this == &o) return *this;
+    release();
+    graphs_ = std::move(o.graphs_);
+    o.graphs_.clear();
+    clock_ = o.clock_;
+    split_ = o.split_;
+    min_part_ = o.min_part_;
+    for (uint32_t k = 0; k < kMaxParts; k++) {
+        aux_[k] = o.aux_[k];
+        join_[k] = o.join_[k];
+        o.aux_[k] = nullptr;
+        o.join_[k] = nullptr;
+    }
+    fork_ = o.fork_;
+    o.fork_ = nullptr;
+    return *this;
+}
+
+bool StepRunner::Graph::updatable() const {
+    for (uint32_t k = 0; k < nparts; k++)
+        if (!parts[k].updatable) return false;
+    return true;
+}
 
 void StepRunner::destroy(Graph& g) {
-    if (g.exec) (void)hipGraphExecDestroy(g.exec);
-    if (g.g) (void)hipGraphDestroy(g.g);
-    delete g.launches;
+    for (uint32_t k = 0; k < g.nparts; k++) {
+        Part& pt = g.parts[k];
+        if (pt.exec) (void)hipGraphExecDestroy(pt.exec);
+        if (pt.g) (void)hipGraphDestroy(pt.g);
+        delete pt.launches;
+    }
     g = Graph{};
 }
 
@@ -2035,10 +2099,37 @@ void StepRunner::clear() {
     graphs_.clear();
 }
 
-// Record one step as a graph by stream capture; the nodes whose arguments carry caller
+uint32_t StepRunner::parts_of(uint32_t n, uint32_t k, uint32_t* b0, uint32_t* cnt) {
+    // Whole 16-stream groups dealt as evenly as they go, the larger shares first; only the
+    // last part may end in a partial group.
+    const uint32_t groups = (n + kRowTile - 1) / kRowTile;
+    const uint32_t parts = std::max(1u, std::min(k, groups));
+    uint32_t g = 0;
+    for (uint32_t i = 0; i < parts; i++) {
+        const uint32_t take = groups / parts + (i < groups % parts ? 1 : 0);
+        b0[i] = g * kRowTile;
+        cnt[i] = std::min(n, (g + take) * kRowTile) - b0[i];
+        g += take;
+    }
+    return parts;
+}
+
+// Streams for parts 1.. and the fork / join events, created once, at the default priority
+// like the library's own stream.
+hipError_t StepRunner::streams_ready(hipStream_t st, uint32_t parts) {
+    (void)st;
+    if (parts <= 1) return hipSuccess;
+    if (!fork_) RDK_TRY(hipEventCreateWithFlags(&fork_, hipEventDisableTiming));
+    for (uint32_t k = 1; k < parts; k++) {
+        if (!aux_[k]) RDK_TRY(hipStreamCreateWithFlags(&aux_[k], hipStreamNonBlocking));
+        if (!join_[k]) RDK_TRY(hipEventCreateWithFlags(&join_[k], hipEventDisableTiming));
+    }
+    return hipSuccess;
+}
+
+// Record one part as a graph by stream capture; the nodes whose arguments carry caller
 // pointers are looked up in capture order and checked against their kernels.
-hipError_t StepRunner::capture(const std::vector<Launch>& seq, int io_i, int head_i, int sm_i, hipStream_t st,
-                               Graph& g) {
+hipError_t StepRunner::capture(const std::vector<Launch>& seq, hipStream_t st, Part& pt) {
     RDK_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
     hipError_t err = hipSuccess;
     for (const Launch& l : seq) {
@@ -2052,26 +2143,26 @@ hipError_t StepRunner::capture(const std::vector<Launch>& seq, int io_i, int hea
         if (graph) (void)hipGraphDestroy(graph);
         return err;
     }
-    g.g = graph;
+    pt.g = graph;
     size_t count = 0;
     RDK_TRY(hipGraphGetNodes(graph, nullptr, &count));
     std::vector<hipGraphNode_t> nodes(count);
     RDK_TRY(hipGraphGetNodes(graph, nodes.data(), &count));
-    g.updatable = count == seq.size();
+    pt.updatable = count == seq.size();
     auto pick = [&](int i, hipGraphNode_t& out) {
         out = nullptr;
-        if (i < 0 || !g.updatable) return;
+        if (i < 0 || !pt.updatable) return;
         hipKernelNodeParams kp{};
         if (hipGraphKernelNodeGetParams(nodes[i], &kp) == hipSuccess && kp.func == seq[i].fn) {
             out = nodes[i];
         } else {
-            g.updatable = false;
+            pt.updatable = false;
         }
     };
-    pick(io_i, g.io_node);
-    pick(head_i, g.head_node);
-    pick(sm_i, g.softmax_node);
-    return hipGraphInstantiate(&g.exec, graph, nullptr, nullptr, 0);
+    pick(pt.io_i, pt.io_node);
+    pick(pt.head_i, pt.head_node);
+    pick(pt.sm_i, pt.softmax_node);
+    return hipGraphInstantiate(&pt.exec, graph, nullptr, nullptr, 0);
 }
 
 void MambaStep::build(Pool& p, const StepIO& io, std::vector<Launch>& out, int& io_i, int& head_i, int& sm_i) const {
@@ -2079,22 +2170,21 @@ void MambaStep::build(Pool& p, const StepIO& io, std::vector<Launch>& out, int& 
 }
 
 hipError_t StepRunner::run(const StepSource& src, Pool& p, const StepIO& io, hipStream_t st, Probe* probe) {
-    std::unique_ptr<std::vector<Launch>> owned(new std::vector<Launch>());
-    std::vector<Launch>& seq = *owned;
-    int io_i = -1, head_i = -1, sm_i = -1;
-    src.build(p, io, seq, io_i, head_i, sm_i);
-    if (probe && probe->cls != KC_NONE && probe->only) {
-        const bool rec = probe->used + 2 <= probe->cap;
-        if (rec) RDK_TRY(hipEventRecord(probe->ev[probe->used], st));
-        for (const Launch& l : seq)
-            if (l.cls == probe->cls) RDK_TRY(launch_direct(l, st));
-        if (rec) {
-            RDK_TRY(hipEventRecord(probe->ev[probe->used + 1], st));
-            probe->used += 2;
-        }
-        return hipSuccess;
-    }
     if (probe && probe->cls != KC_NONE) {
+        std::vector<Launch> seq;
+        int io_i = -1, head_i = -1, sm_i = -1;
+        src.build(p, io, seq, io_i, head_i, sm_i);
+        if (probe->only) {
+            const bool rec = probe->used + 2 <= probe->cap;
+            if (rec) RDK_TRY(hipEventRecord(probe->ev[probe->used], st));
+            for (const Launch& l : seq)
+                if (l.cls == probe->cls) RDK_TRY(launch_direct(l, st));
+            if (rec) {
+                RDK_TRY(hipEventRecord(probe->ev[probe->used + 1], st));
+                probe->used += 2;
+            }
+            return hipSuccess;
+        }
         // Probed launches carry their own dispatch start/stop timestamps.
         for (const Launch& l : seq) {
             const bool on = l.cls == probe->cls && probe->used + 2 <= probe->cap;
@@ -2109,58 +2199,100 @@ hipError_t StepRunner::run(const StepSource& src, Pool& p, const StepIO& io, hip
         }
         return hipSuccess;
     }
-    if (!use_graphs()) {
-        for (const Launch& l : seq) RDK_TRY(launch_direct(l, st));
+    uint32_t b0[kMaxParts], cnt[kMaxParts];
+    const uint32_t want = std::min(split_, std::max(1u, io.n / min_part_));
+    const uint32_t nparts = parts_of(io.n, src.splittable() ? want : 1, b0, cnt);
+    RDK_TRY(streams_ready(st, nparts));
+    auto part_io = [&](uint32_t k) {
+        StepIO q = io;
+        q.b0 = b0[k];
+        q.n = cnt[k];
+        q.n_all = io.n;
+        return q;
+    };
+    auto stream_of = [&](uint32_t k) { return k == 0 ? st : aux_[k]; };
+    // Parts 1.. start after everything queued on st so far and st waits for all of them.
+    auto fork = [&]() -> hipError_t {
+        if (nparts == 1) return hipSuccess;
+        RDK_TRY(hipEventRecord(fork_, st));
+        for (uint32_t k = 1; k < nparts; k++) RDK_TRY(hipStreamWaitEvent(aux_[k], fork_, 0));
         return hipSuccess;
+    };
+    auto join = [&]() -> hipError_t {
+        for (uint32_t k = 1; k < nparts; k++) {
+            RDK_TRY(hipEventRecord(join_[k], aux_[k]));
+            RDK_TRY(hipStreamWaitEvent(st, join_[k], 0));
+        }
+        return hipSuccess;
+    };
+    if (!use_graphs()) {
+        RDK_TRY(fork());
+        for (uint32_t k = 0; k < nparts; k++) {
+            std::vector<Launch> seq;
+            int io_i = -1, head_i = -1, sm_i = -1;
+            src.build(p, part_io(k), seq, io_i, head_i, sm_i);
+            for (const Launch& l : seq) RDK_TRY(launch_direct(l, stream_of(k)));
+        }
+        return join();
     }
     auto same_io = [&](const Graph& g) {
         return g.tokens == io.tokens && g.slots == io.slots && g.out == io.out && g.err == io.err;
     };
     Graph* hit = nullptr;
     for (Graph& g : graphs_)
-        if (g.n == io.n && g.probs == io.probs && g.check == io.check && g.pool == &p && (g.updatable || same_io(g)))
+        if (g.n == io.n && g.split == split_ && g.probs == io.probs && g.check == io.check && g.pool == &p &&
+            (g.updatable() || same_io(g)))
             hit = &g;
     if (!hit) {
         if (graphs_.size() >= 8) {
             auto old = std::min_element(graphs_.begin(), graphs_.end(),
                                         [](const Graph& a, const Graph& b) { return a.last_use < b.last_use; });
-            // The stream-ordered entry point returns without waiting: the evicted graph
-            // may still be queued or running.
+            // The stream-ordered entry point returns without waiting: the evicted graphs
+            // may still be queued or running (st waits for every part).
             RDK_TRY(hipStreamSynchronize(st));
             destroy(*old);
             graphs_.erase(old);
         }
         Graph g;
         g.n = io.n;
+        g.split = split_;
         g.probs = io.probs;
         g.check = io.check;
         g.pool = &p;
-        const hipError_t e = capture(seq, io_i, head_i, sm_i, st, g);
-        if (e != hipSuccess) {
-            destroy(g);
-            return e;
+        g.nparts = nparts;
+        for (uint32_t k = 0; k < nparts; k++) {
+            Part& pt = g.parts[k];
+            pt.b0 = b0[k];
+            pt.n = cnt[k];
+            std::unique_ptr<std::vector<Launch>> seq(new std::vector<Launch>());
+            src.build(p, part_io(k), *seq, pt.io_i, pt.head_i, pt.sm_i);
+            const hipError_t e = capture(*seq, st, pt);
+            if (e != hipSuccess) {
+                destroy(g);
+                return e;
+            }
+            pt.launches = seq.release();
         }
-        g.launches = owned.release();
         graphs_.push_back(g);
         hit = &graphs_.back();
     } else if (!same_io(*hit)) {
-        // Same shape, other caller pointers: the new arguments replace the stored ones, so
-        // the graph's parameter storage stays alive with it.
-        std::vector<Launch>& keep = *hit->launches;
-        keep[io_i] = std::move(seq[io_i]);
-        keep[head_i] = std::move(seq[head_i]);
-        if (sm_i >= 0) keep[sm_i] = std::move(seq[sm_i]);
-        const std::vector<Launch>& cur = keep;
-        void* p_io[] = {cur[io_i].argp};
-        hipKernelNodeParams k_io = node_params(cur[io_i], p_io);
-        RDK_TRY(hipGraphExecKernelNodeSetParams(hit->exec, hit->io_node, &k_io));
-        void* p_h[] = {cur[head_i].argp};
-        hipKernelNodeParams k_h = node_params(cur[head_i], p_h);
-        RDK_TRY(hipGraphExecKernelNodeSetParams(hit->exec, hit->head_node, &k_h));
-        if (sm_i >= 0) {
-            void* p_s[] = {cur[sm_i].argp};
-            hipKernelNodeParams k_s = node_params(cur[sm_i], p_s);
-            RDK_TRY(hipGraphExecKernelNodeSetParams(hit->exec, hit->softmax_node, &k_s));
+        // Same shape, other caller pointers: each part's new arguments replace the stored
+        // ones, so the graph's parameter storage stays alive with it.
+        for (uint32_t k = 0; k < hit->nparts; k++) {
+            Part& pt = hit->parts[k];
+            std::vector<Launch> seq;
+            int io_i = -1, head_i = -1, sm_i = -1;
+            src.build(p, part_io(k), seq, io_i, head_i, sm_i);
+            std::vector<Launch>& keep = *pt.launches;
+            const int idx[3] = {pt.io_i, pt.head_i, pt.sm_i};
+            const hipGraphNode_t nodes[3] = {pt.io_node, pt.head_node, pt.softmax_node};
+            for (int j = 0; j < 3; j++) {
+                if (idx[j] < 0) continue;
+                keep[idx[j]] = std::move(seq[idx[j]]);
+                void* prm[] = {keep[idx[j]].argp};
+                hipKernelNodeParams kp = node_params(keep[idx[j]], prm);
+                RDK_TRY(hipGraphExecKernelNodeSetParams(pt.exec, nodes[j], &kp));
+            }
         }
     }
     hit->tokens = io.tokens;
@@ -2168,7 +2300,9 @@ hipError_t StepRunner::run(const StepSource& src, Pool& p, const StepIO& io, hip
     hit->out = io.out;
     hit->err = io.err;
     hit->last_use = ++clock_;
-    return hipGraphLaunch(hit->exec, st);
+    RDK_TRY(fork());
+    for (uint32_t k = 0; k < hit->nparts; k++) RDK_TRY(hipGraphLaunch(hit->parts[k].exec, stream_of(k)));
+    return join();
 }
 
 // Rwkv7State::reset (rwkv7/model.rs:135-140) for the listed slots: both token-shift

@@ -10,6 +10,8 @@
 
 #include <vector>
 
+#include "step.h"
+
 namespace rdk {
 
 constexpr int kRowTile = 16;   // MFMA M and N
@@ -76,6 +78,7 @@ struct Pool {
     // touches a real slot and no two streams of a step share one.
     uint32_t scap = 0;
     uint32_t gcap = 0;           // stream groups of 16 covering cap
+    uint32_t xcap = 0;           // batch rows of the x_proj partials (their row stride; cap unless carved smaller)
     void* block = nullptr;       // the one device allocation all device arrays below are carved from
     float* conv = nullptr;
     float* ssm = nullptr;
@@ -179,6 +182,9 @@ struct ModelView {
 
 // One step's inputs.  slots/tokens/out are device pointers; `check` validates slots
 // and tokens on the device into *err (bit 0: out of range, bit 1: duplicate slot).
+// A step may run as several parts (sub-batches of whole 16-stream groups): a part covers
+// batch rows [b0, b0 + n) of the step's n_all rows; slots, tokens and out always point at
+// row 0 of the whole step, and the device check of every part covers all n_all slots.
 struct StepIO {
     uint32_t n;
     const uint32_t* slots;
@@ -187,6 +193,8 @@ struct StepIO {
     bool probs;
     bool check;
     uint32_t* err;
+    uint32_t b0 = 0;
+    uint32_t n_all = 0;   // 0: n (one part)
 };
 
 // A linear sequence of kernel launches that is either issued directly on a stream or
@@ -199,12 +207,15 @@ struct StepSource {
     virtual ~StepSource() = default;
     virtual void build(Pool& p, const StepIO& io, std::vector<Launch>& out, int& io_i, int& head_i,
                        int& sm_i) const = 0;
+    // Whether build() accepts a part (io.b0 > 0 or io.n < io.n_all) of a step.
+    virtual bool splittable() const { return false; }
 };
 
 struct MambaStep final : StepSource {
     ModelView m;
     explicit MambaStep(const ModelView& v) : m(v) {}
     void build(Pool& p, const StepIO& io, std::vector<Launch>& out, int& io_i, int& head_i, int& sm_i) const override;
+    bool splittable() const override { return true; }
 };
 
 struct RwkvStep final : StepSource {
@@ -213,37 +224,78 @@ struct RwkvStep final : StepSource {
     void build(Pool& p, const StepIO& io, std::vector<Launch>& out, int& io_i, int& head_i, int& sm_i) const override;
 };
 
+// Most parts a step is split into: one per hardware queue a process gets by default.
+constexpr uint32_t kMaxParts = 4;
+// Streams per part at least: below it the parts' kernels are short enough that running
+// two of them at once loses more (each wave slower, the XCD-aware layouts interleaved
+// with another kernel's) than it overlaps.  Measured on Mamba-130M int8, parts per step:
+// 128 streams 702 / 645 / 687 / 1050 us for 1 / 2 / 3 / 4 parts, 1024 streams 2980 /
+// 2732 / - / 3245 us, 32 streams 379 / 456 us for 1 / 2.
+constexpr uint32_t kMinPartStreams = 64;
+// Parts per step by default (REDUKT_GPU_SPLIT overrides).
+constexpr uint32_t kDefaultSplit = 2;
+
 class StepRunner {
 public:
+    StepRunner() = default;
+    StepRunner(const StepRunner&) = delete;
+    StepRunner& operator=(const StepRunner&) = delete;
+    // Releases this runner's graphs, streams and events, then takes over o's.
+    StepRunner& operator=(StepRunner&& o) noexcept;
     ~StepRunner();
-    // Issue one step.  Builds (or reuses) the graph of this shape unless a probe is
-    // active, in which case the step is launched directly with events around the probed
-    // class.  Returns hipSuccess or the first error.
+    // Destroys every graph, stream and event of the runner.
+    void release();
+    // Issue one step.  Builds (or reuses) the graphs of this shape unless a probe is
+    // active, in which case the step is launched directly (as one part) with events around
+    // the probed class.  A splittable step of n streams runs as up to split() parts of whole
+    // 16-stream groups, part k on its own stream (part 0 on st), forked from and joined back
+    // into st by events, so the parts' kernels overlap.  Returns hipSuccess or the first error.
     hipError_t run(const StepSource& src, Pool& p, const StepIO& io, hipStream_t st, Probe* probe);
     void clear();
+    // Parts per step (1 .. kMaxParts) and the fewest streams a part may have; the streams
+    // and events are created on first use.
+    void set_split(uint32_t k, uint32_t min_part = kMinPartStreams) {
+        split_ = k < 1 ? 1 : (k > kMaxParts ? kMaxParts : k);
+        min_part_ = min_part < 1 ? 1 : min_part;
+    }
+    uint32_t split() const { return split_; }
+    // Rows [b0, b0 + n) of each part of a step of n streams split at most k ways.
+    static uint32_t parts_of(uint32_t n, uint32_t k, uint32_t* b0, uint32_t* cnt);
 
 private:
-    struct Graph {
-        uint32_t n = 0;
-        bool probs = false, check = false;
-        const Pool* pool = nullptr;
-        // Caller pointers the graph was last launched with; `updatable` when the nodes
-        // carrying them were found, so other pointers are set in place.
-        const uint32_t* tokens = nullptr;
-        const uint32_t* slots = nullptr;
-        const float* out = nullptr;
-        const uint32_t* err = nullptr;
+    struct Part {
+        uint32_t b0 = 0, n = 0;
         bool updatable = false;
         hipGraph_t g = nullptr;
         hipGraphExec_t exec = nullptr;
         hipGraphNode_t io_node = nullptr, head_node = nullptr, softmax_node = nullptr;
-        uint64_t last_use = 0;
         std::vector<Launch>* launches = nullptr;  // argument storage, alive as long as the graph
+        int io_i = -1, head_i = -1, sm_i = -1;
     };
-    hipError_t capture(const std::vector<Launch>& seq, int io_i, int head_i, int sm_i, hipStream_t st, Graph& g);
+    struct Graph {
+        uint32_t n = 0, split = 1;
+        bool probs = false, check = false;
+        const Pool* pool = nullptr;
+        // Caller pointers the graphs were last launched with; when every part's nodes that
+        // carry them were found (`updatable`), other pointers are set in place.
+        const uint32_t* tokens = nullptr;
+        const uint32_t* slots = nullptr;
+        const float* out = nullptr;
+        const uint32_t* err = nullptr;
+        uint32_t nparts = 0;
+        Part parts[kMaxParts];
+        uint64_t last_use = 0;
+        bool updatable() const;
+    };
+    hipError_t capture(const std::vector<Launch>& seq, hipStream_t st, Part& pt);
+    hipError_t streams_ready(hipStream_t st, uint32_t parts);
     void destroy(Graph& g);
     std::vector<Graph> graphs_;
     uint64_t clock_ = 0;
+    uint32_t split_ = 1, min_part_ = kMinPartStreams;
+    hipStream_t aux_[kMaxParts] = {};        // aux_[k] runs part k (k >= 1)
+    hipEvent_t fork_ = nullptr;
+    hipEvent_t join_[kMaxParts] = {};
 };
 
 // Zero the state of the n slots listed in d_slots (device).  Uses no memset, so it is

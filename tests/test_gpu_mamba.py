@@ -412,3 +412,77 @@ def test_mamba130m_reset_boundary_and_large_batch_invariance(full_model):
             g = np.empty((513, v), np.float32)
             be.forward_batch(slots, toks, g)
             assert np.array_equal(bits(g[pos]), bits(alone[0])), pos
+
+
+def _steps(path, profile, n, steps, seed, probs=False, cap=None):
+    rng = np.random.default_rng(seed)
+    with ffi.PluginBackend(path, profile=profile) as be:
+        v = be.vocab
+        be.batch_init(cap or n)
+        slots = [int(s) for s in rng.permutation(cap or n)[:n]]
+        outs = []
+        for _ in range(steps):
+            toks = [int(x) for x in rng.integers(0, v, n)]
+            g = np.empty((n, v), np.float32)
+            be.forward_batch(slots, toks, g, probs=probs)
+            outs.append(g)
+        return np.stack(outs)
+
+
+@pytest.mark.parametrize("split", [2, 4])
+@pytest.mark.parametrize("n,profile,probs", [(100, 6, False), (33, 0, True), (64, 2, False)])
+def test_split_steps_are_bitwise_identical(models, monkeypatch, split, n, profile, probs):
+    # A step split into parts of whole 16-stream groups, each part on its own stream,
+    # gives every stream the bits of the unsplit step (ragged last parts included).
+    monkeypatch.setenv("REDUKT_GPU_SPLIT", "1")
+    ref = _steps(models["reftest"], profile, n, 3, 5, probs, cap=n + 7)
+    monkeypatch.setenv("REDUKT_GPU_PART_MIN", "16")
+    monkeypatch.setenv("REDUKT_GPU_SPLIT", str(split))
+    got = _steps(models["reftest"], profile, n, 3, 5, probs, cap=n + 7)
+    assert np.array_equal(bits(ref), bits(got))
+
+
+def test_split_mamba130m_128_streams_bitwise(full_model, monkeypatch):
+    monkeypatch.setenv("REDUKT_GPU_SPLIT", "1")
+    ref = _steps(full_model, 6, 128, 2, 9)
+    monkeypatch.setenv("REDUKT_GPU_PART_MIN", "16")
+    monkeypatch.setenv("REDUKT_GPU_SPLIT", "4")
+    got = _steps(full_model, 6, 128, 2, 9)
+    assert np.array_equal(bits(ref), bits(got))
+
+
+def test_split_device_check_covers_every_part(models, monkeypatch):
+    # A slot repeated in two different parts is caught by the device check of the whole
+    # step: the later entry never touches the real slot, the first advances it exactly as a
+    # valid call does, and the slot the later position would otherwise name is untouched.
+    monkeypatch.setenv("REDUKT_GPU_SPLIT", "4")
+    monkeypatch.setenv("REDUKT_GPU_PART_MIN", "16")
+    dims = SMALL_BASE
+    with ffi.PluginBackend(models["base"], profile=0) as be:
+        v = be.vocab
+        be.batch_init(64)
+        state = lambda s: [be.get_state(s, l, dims.d_inner, 4) for l in range(dims.n_layer)]
+        first = [(7 * i + 1) % v for i in range(64)]
+        toks = [(5 * i + 2) % v for i in range(64)]
+
+        def start():
+            be.batch_reset(None)
+            st, _ = _device_step(be, list(range(64)), first, v)
+            assert st == ffi.BackendResult.OK
+
+        start()
+        s60 = state(60)
+        slots = list(range(64))
+        slots[60] = 3       # part 3 repeats part 0's slot 3
+        st, bad = _device_step(be, slots, toks, v)
+        assert st == ffi.BackendResult.INVALID_ARGUMENT
+        s3_bad = state(3)
+        for (c0, x0), (c1, x1) in zip(s60, state(60)):
+            assert np.array_equal(c0, c1) and np.array_equal(x0, x1)
+        start()
+        keep = [i for i in range(64) if i != 60]
+        st, good = _device_step(be, [slots[i] for i in keep], [toks[i] for i in keep], v)
+        assert st == ffi.BackendResult.OK
+        for (c0, x0), (c1, x1) in zip(s3_bad, state(3)):
+            assert np.array_equal(c0, c1) and np.array_equal(x0, x1)
+        assert np.array_equal(bits(bad[keep]), bits(good))
