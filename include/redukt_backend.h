@@ -127,6 +127,23 @@ int32_t redukt_backend_forward_batch_probs(uint32_t n_streams, const uint32_t* s
 int32_t redukt_backend_forward_batch_device(uint32_t n_streams, const uint32_t* d_slots, const uint32_t* d_tokens,
                                             float* d_out, uint32_t vocab_size, uint32_t flags);
 
+/* Allocation-free variant of redukt_backend_forward_batch_device.  No counterpart in the
+ * reference ABI: it is for callers that cannot allocate device memory around a step
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, checks and results as forward_batch_device; Mamba models only.  The
+ * per-step scratch (activations, x_proj partials, the validated slot list) comes from a
+ * 16 MiB device array the library holds on each device it runs on until the process ends;
+ * the recurrent state stays in the batch pool (batch_init).  The step runs as direct
+ * kernel launches on the library's stream: no graph, stream, event or device memory is
+ * created and no allocating routine is called.  The scratch bounds n_streams (44,736 bytes
+ * a stream at Mamba-130M: at most 374 streams); above it INVALID_ARGUMENT, nothing
+ * launched.  Every call on a device shares that scratch and clears the part it uses:
+ * calls are ordered on the library's stream, so only calls from several threads can
+ * overlap, and those race. */
+int32_t redukt_backend_forward_batch_device_noalloc(uint32_t n_streams, const uint32_t* d_slots,
+                                                    const uint32_t* d_tokens, float* d_out, uint32_t vocab_size,
+                                                    uint32_t flags);
+
 /* Wait for queued work; returns OK, or INVALID_ARGUMENT if a device-side check of
  * forward_batch_device failed since the last call (the flag is then cleared). */
 int32_t redukt_backend_device_status(void);

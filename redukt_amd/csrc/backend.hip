@@ -605,6 +605,62 @@ uint32_t env_profile() {
     return env_weight_profile() | (x && *x && strcmp(x, "0") ? BACKEND_PROFILE_EXACT_SCAN : 0u);
 }
 
+// ---------------------------------------------------------------- allocation-free step
+// The per-step scratch of redukt_backend_forward_batch_device_noalloc (activations, limbs,
+// x_proj partials, the validated slot list) lives in this file-scope device array, one
+// copy per device the library runs on, held until the process ends.  Host code uses only
+// the address hipGetSymbolAddress returns for the current device (noalloc_base), never the
+// array's name.  Every call clears the part it carves before the step, and every call on a
+// device shares it: calls that overlap on one device race (calls on the library's stream
+// are ordered, so only calls from several threads can overlap).
+constexpr size_t kNoAllocScratchBytes = (size_t)16 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+constexpr int kMaxDevices = 64;
+void* g_noalloc_base[kMaxDevices] = {};
+
+// Once per device, with that device current (the library's init).
+bool noalloc_setup(int device) {
+    if (device < 0 || device >= kMaxDevices) return false;
+    if (g_noalloc_base[device]) return true;
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+        log("no-alloc scratch: hipGetSymbolAddress failed (%s)", hipGetErrorString(e));
+        return false;
+    }
+    g_noalloc_base[device] = ptr;
+    return true;
+}
+
+// The batch pool's state with the per-step scratch of n streams carved from the device's
+// scratch array (the x_proj partials with row stride n); false if it does not fit.
+bool noalloc_view(Pool& v, uint32_t n, unsigned char* base, size_t* used) {
+    const Dims& D = G.dims;
+    v = G.batch;
+    v.xcap = n;
+    v.gcap = (n + 15) / 16;
+    Carve c;
+    c.base = base;
+    c.take(v.slots, slot_words(n));
+    c.take(v.x, (size_t)n * D.d);
+    c.take(v.xw, xw_elems(D, n));
+    c.take(v.ssp, ssp_floats(D, n));
+    c.take(v.u, (size_t)n * D.di);
+    c.take(v.z, (size_t)n * D.di);
+    c.take(v.xpart, xpart_floats(D, n));
+    c.take(v.glimb, glimb_elems(D, n));
+    *used = (c.off + 255) & ~(size_t)255;
+    v.out = nullptr;
+    v.d_slots = v.d_tokens = v.h_slots = v.h_tokens = nullptr;
+    v.seen = nullptr;
+    return *used <= kNoAllocScratchBytes;
+}
+
+__global__ __launch_bounds__(256) void k_clear(uint4* p, size_t n16) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (size_t)gridDim.x * 256)
+        p[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
 int init_common(const uint8_t* weights_path, int32_t device_id, uint32_t profile, BackendInfo* info_out) {
     if (!weights_path || !info_out) return BACKEND_INIT_FAILED;
     if (G.ready || G.stream) free_model();
@@ -617,6 +673,7 @@ int init_common(const uint8_t* weights_path, int32_t device_id, uint32_t profile
         free_model();
         return BACKEND_INIT_FAILED;
     }
+    (void)noalloc_setup(G.device);  // a failure only disables the allocation-free entry point
     G.profile = profile;
     G.runner.set_split(env_split(), env_part_min());
     G.kind = file_kind(path);
@@ -756,6 +813,31 @@ int32_t redukt_backend_forward_batch_device(uint32_t n_streams, const uint32_t* 
     return run_step(G.batch, n_streams, d_slots, d_tokens, d_out, (flags & 1u) != 0, true) == hipSuccess
                ? BACKEND_OK
                : BACKEND_FORWARD_FAILED;
+}
+
+int32_t redukt_backend_forward_batch_device_noalloc(uint32_t n_streams, const uint32_t* d_slots,
+                                                    const uint32_t* d_tokens, float* d_out, uint32_t vocab_size,
+                                                    uint32_t flags) {
+    if (!G.ready || G.batch.cap == 0) return BACKEND_INIT_FAILED;
+    if (G.kind != kKindMamba || vocab_size != G.dims.vocab || n_streams > G.batch.cap) return BACKEND_INVALID_ARGUMENT;
+    if (n_streams == 0) return BACKEND_OK;
+    if (!d_slots || !d_tokens || !d_out) return BACKEND_INVALID_ARGUMENT;
+    unsigned char* base = G.device < kMaxDevices ? (unsigned char*)g_noalloc_base[G.device] : nullptr;
+    if (!base) return BACKEND_INIT_FAILED;
+    Pool v;
+    size_t used = 0;
+    if (!noalloc_view(v, n_streams, base, &used)) {
+        log("forward_batch_device_noalloc: %u streams need %zu bytes of scratch, more than %zu", n_streams, used,
+            kNoAllocScratchBytes);
+        return BACKEND_INVALID_ARGUMENT;
+    }
+    const size_t n16 = used / 16;
+    hipLaunchKernelGGL(k_clear, dim3((unsigned)std::min<size_t>((n16 + 255) / 256, 1024)), dim3(256), 0, G.stream,
+                       (uint4*)base, n16);
+    if (hipGetLastError() != hipSuccess) return BACKEND_FORWARD_FAILED;
+    StepIO io{n_streams, d_slots, d_tokens, d_out, (flags & 1u) != 0, true, G.d_err};
+    const MambaStep src(model_view());
+    return G.runner.run_direct(src, v, io, G.stream) == hipSuccess ? BACKEND_OK : BACKEND_FORWARD_FAILED;
 }
 
 int32_t redukt_backend_device_status(void) {

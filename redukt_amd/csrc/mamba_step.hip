@@ -2057,6 +2057,7 @@ void StepRunner::release() {
     }
     if (fork_) (void)hipEventDestroy(fork_);
     fork_ = nullptr;
+    direct_.clear();
 }
 
 StepRunner& StepRunner::operator=(StepRunner&& o) noexcept {
@@ -2064,6 +2065,8 @@ StepRunner& StepRunner::operator=(StepRunner&& o) noexcept {
     release();
     graphs_ = std::move(o.graphs_);
     o.graphs_.clear();
+    direct_ = std::move(o.direct_);
+    o.direct_.clear();
     clock_ = o.clock_;
     split_ = o.split_;
     min_part_ = o.min_part_;
@@ -2167,6 +2170,13 @@ hipError_t StepRunner::capture(const std::vector<Launch>& seq, hipStream_t st, P
 
 void MambaStep::build(Pool& p, const StepIO& io, std::vector<Launch>& out, int& io_i, int& head_i, int& sm_i) const {
     build_step(m, p, io, out, io_i, head_i, sm_i);
+}
+
+hipError_t StepRunner::run_direct(const StepSource& src, Pool& p, const StepIO& io, hipStream_t st) {
+    int io_i = -1, head_i = -1, sm_i = -1;
+    src.build(p, io, direct_, io_i, head_i, sm_i);
+    for (const Launch& l : direct_) RDK_TRY(launch_direct(l, st));
+    return hipSuccess;
 }
 
 hipError_t StepRunner::run(const StepSource& src, Pool& p, const StepIO& io, hipStream_t st, Probe* probe) {

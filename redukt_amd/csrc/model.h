@@ -251,6 +251,9 @@ public:
     // 16-stream groups, part k on its own stream (part 0 on st), forked from and joined back
     // into st by events, so the parts' kernels overlap.  Returns hipSuccess or the first error.
     hipError_t run(const StepSource& src, Pool& p, const StepIO& io, hipStream_t st, Probe* probe);
+    // One step as direct launches on st, in one part: no graph is captured and no stream,
+    // event or device memory is created.
+    hipError_t run_direct(const StepSource& src, Pool& p, const StepIO& io, hipStream_t st);
     void clear();
     // Parts per step (1 .. kMaxParts) and the fewest streams a part may have; the streams
     // and events are created on first use.
@@ -296,6 +299,7 @@ private:
     hipStream_t aux_[kMaxParts] = {};        // aux_[k] runs part k (k >= 1)
     hipEvent_t fork_ = nullptr;
     hipEvent_t join_[kMaxParts] = {};
+    std::vector<Launch> direct_;             // run_direct's launch list (host storage, reused)
 };
 
 // Zero the state of the n slots listed in d_slots (device).  Uses no memset, so it is

@@ -41,7 +41,7 @@ V2_SYMBOLS = ("redukt_backend_abi_version", "redukt_backend_batch_init", "redukt
 V3_SYMBOLS = ("redukt_backend_init_ex", "redukt_backend_forward_batch_probs", "redukt_backend_forward_batch_device",
               "redukt_backend_device_status", "redukt_backend_stream", "redukt_backend_get_state",
               "redukt_backend_probe_kernel", "redukt_backend_probe_used", "redukt_backend_get_rwkv_state",
-              "redukt_backend_eval_math")
+              "redukt_backend_eval_math", "redukt_backend_forward_batch_device_noalloc")
 # redukt_backend_eval_math function codes: the portable element-wise functions
 MATH_FNS = {"exp": 0, "lane_exp": 1, "ln": 2, "softplus": 3, "lane_sigmoid": 4, "sigmoid": 5}
 
@@ -143,6 +143,8 @@ class PluginLibrary:
             L.redukt_backend_forward_batch_device.argtypes = [ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p,
                                                               ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32]
             L.redukt_backend_forward_batch_device.restype = ctypes.c_int32
+            L.redukt_backend_forward_batch_device_noalloc.argtypes = L.redukt_backend_forward_batch_device.argtypes
+            L.redukt_backend_forward_batch_device_noalloc.restype = ctypes.c_int32
             L.redukt_backend_device_status.argtypes = []
             L.redukt_backend_device_status.restype = ctypes.c_int32
             L.redukt_backend_stream.argtypes = []
@@ -344,6 +346,13 @@ class PluginBackend:
             n, d_slots, d_tokens, d_out, self.vocab, 1 if probs else 0))
         if res != BackendResult.OK:
             raise BackendError(res, "forward_batch_device")
+
+    def forward_batch_device_noalloc(self, n: int, d_slots: int, d_tokens: int, d_out: int,
+                                     probs: bool = False) -> BackendResult:
+        """The allocation-free device step; returns the result code (INVALID_ARGUMENT when n
+        does not fit the library's scratch)."""
+        return BackendResult.from_code(self.lib.lib.redukt_backend_forward_batch_device_noalloc(
+            n, d_slots, d_tokens, d_out, self.vocab, 1 if probs else 0))
 
     def device_status(self) -> BackendResult:
         return BackendResult.from_code(self.lib.lib.redukt_backend_device_status())
