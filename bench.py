@@ -36,7 +36,8 @@ from redukt_amd import ffi, hip, rbin, rwkv, synth  # noqa: E402
 METRIC = "Mamba-130M tok/s at batch 1/32/128 (F32 & Q8); % of HBM roofline"
 HBM_PEAK_GBS = 8000.0
 RESET_PERIOD = 4096
-PROFILES = {"f32": 0, "q8": 1, "q8row": 2, "q8row-all": 6, "q8-all": 5}
+PROFILES = {"f32": 0, "q8": 1, "q8row": 2, "q8row-all": 6, "q8-all": 5,
+            "f32-gemv": 16, "q8row-gemv": 18, "q8row-all-gemv": 22}
 
 
 def log(msg: str) -> None:
@@ -276,19 +277,22 @@ class Workload:
             b.close()
 
 
-def grid_rates(path: str, sizes, K: int, W: int, skip=None) -> dict:
-    """Mamba-130M at each batch size with F32 and int8 per-row weights: device tok/s, FFI
-    tok/s and the whole step's bytes over its time against the HBM peak."""
+# The grid of the metric: both weight profiles at 1, 32 and 128 streams on the matrix-core
+# family, and the wavefront-GEMV tier (the small-batch family) where it is competitive.
+GRID = {"f32": (1, 32, 128), "q8row-all": (1, 32, 128), "f32-gemv": (1, 32), "q8row-all-gemv": (1, 32)}
+
+
+def grid_rates(path: str, grid, K: int, W: int) -> dict:
+    """Mamba-130M at each batch size and weight profile: device tok/s, FFI tok/s and the
+    whole step's bytes over its time against the HBM peak."""
     dims = rbin.MAMBA_130M
     rng = np.random.default_rng(4321)
     out = {}
-    for name in ("f32", "q8row-all"):
+    for name, sizes in grid.items():
         profile = PROFILES[name]
         be = ffi.PluginBackend(path, 0, profile)
         out[name] = {}
         for n in sizes:
-            if skip == (name, n):
-                continue
             toks = synth.zipf_tokens(rng, dims.vocab, (W + K + 1, n))
             wl = Workload(be, n, dims.vocab, toks)
             ms, _ = wl.timed(W, K)
@@ -429,7 +433,7 @@ def main() -> int:
     grid = None
     if mamba and not args.no_grid and not args.probs and not args.exact_scan and args.model is None:
         gk, gw = max(8, min(K, 64)), max(2, min(W, 8))
-        grid = grid_rates(path, (1, 32, 128), gk, gw)
+        grid = grid_rates(path, GRID, gk, gw)
         grid["steps"], grid["warmup"] = gk, gw
 
     cpu = None

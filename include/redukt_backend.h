@@ -104,6 +104,14 @@ int32_t redukt_backend_forward_batch(uint32_t n_streams, const uint32_t* slots, 
  * exp (bit-identical element-wise scan) instead of the hardware exp2 (about 1e-7
  * relative; the default).  REDUKT_GPU_EXACT_SCAN=1 sets it for redukt_backend_init. */
 #define BACKEND_PROFILE_EXACT_SCAN 8u
+/* Profile bit 4: the Mamba projections on wavefront-GEMV kernels (f32 dot products on the
+ * vector ALUs, weights streamed in a GEMV layout) instead of the matrix cores: the
+ * small-batch tier.  The tier is fixed at init for every batch size, so a stream's bits do
+ * not depend on n within it (they differ between tiers, like between builds).  F32 or
+ * per-row int8 weights (low bits 0 or 2), RMSNorm Mamba models with d_conv 4 and
+ * d_model / d_inner in {64, 96, 128, 192, 256, 384, 768, 1024, 1536, 3072}; INIT_FAILED
+ * otherwise. */
+#define BACKEND_PROFILE_GEMV 16u
 
 /* redukt_backend_init with an explicit weight profile (the model file stays F32). */
 int32_t redukt_backend_init_ex(const uint8_t* weights_path, int32_t device_id, uint32_t profile,

@@ -52,6 +52,8 @@ struct Model {
     uint32_t profile = 0;
     std::vector<DLayer> layers;
     TMat emb, head_own;
+    GMat g_emb, g_head_own;   // the wavefront-GEMV tier's embedding / untied head
+    bool gemv = false;        // weight profile bit 4
     bool tied = true;
     float* norm_f_w = nullptr;
     float* norm_f_b = nullptr;
@@ -181,6 +183,49 @@ bool make_tmat(TMat& m, const float* w, int rows, int cols, int quant_group) {
     return m.w && m.scales;
 }
 
+// Lay a row-major [rows][cols] matrix out for the wavefront-GEMV kernels (see GMat) and
+// upload it, F32 or quantized with one scale per row (the Q8 recipe with group = cols).
+bool make_gmat(GMat& m, const float* w, int rows, int cols, bool q8) {
+    int rpi = 0, cpl = 0;
+    if (!gemv_shape(cols, rpi, cpl) || !gemv_cpl_supported(cpl)) return false;
+    m.rows = rows;
+    m.cols = cols;
+    m.rpi = rpi;
+    m.cpl = cpl;
+    m.blocks = (rows + rpi - 1) / rpi;
+    m.q8 = q8;
+    const int per = 64 / rpi;
+    const size_t n = (size_t)m.blocks * rpi * cols;
+    std::vector<int8_t> q;
+    std::vector<float> sc;
+    if (q8) quantize(w, rows, cols, cols, q, sc);
+    std::vector<int8_t> tq(q8 ? n : 0, 0);
+    std::vector<float> tf(q8 ? 0 : n, 0.0f);
+    for (int i = 0; i < m.blocks; i++)
+        for (int j = 0; j < cpl; j++)
+            for (int l = 0; l < 64; l++) {
+                const int row = i * rpi + l % rpi, k0 = 16 * (l / rpi + per * j);
+                if (row >= rows) continue;
+                const size_t idx = (size_t)i * cpl + j;
+                for (int e = 0; e < 16; e++) {
+                    const size_t src = (size_t)row * cols + k0 + e;
+                    if (q8)
+                        tq[(idx * 64 + l) * 16 + e] = q[src];
+                    else
+                        tf[((idx * 4 + e / 4) * 64 + l) * 4 + e % 4] = w[src];
+                }
+            }
+    if (q8) {
+        std::vector<float> scp((size_t)m.blocks * rpi, 0.0f);
+        for (int r = 0; r < rows; r++) scp[r] = sc[r];
+        m.w = dev_upload(tq.data(), tq.size());
+        m.scales = dev_upload(scp.data(), scp.size());
+        return m.w && m.scales;
+    }
+    m.w = dev_upload(tf.data(), tf.size());
+    return m.w != nullptr;
+}
+
 struct Reader {
     FILE* f;
     bool ok = true;
@@ -223,13 +268,27 @@ int load_weights(const std::string& path, uint32_t profile) {
     auto qgroup = [&](int cols) { return quant == 0 ? 0 : (quant == 0x7fffffff ? cols : quant); };
     const bool qsmall = quant != 0 && (profile & BACKEND_PROFILE_Q8_SMALL);
     const bool nb = D.flags & kFlagNormBias, uh = D.flags & kFlagUntiedHead;
+    const bool gemv = (profile & BACKEND_PROFILE_GEMV) != 0;
+    if (gemv) {
+        // The GEMV tier: F32 or per-row int8, RMSNorm, a 4-wide conv, shapes it is compiled for.
+        int r = 0, c = 0;
+        const bool shapes = gemv_shape((int)D.d, r, c) && gemv_cpl_supported(c) && gemv_shape((int)D.di, r, c) &&
+                            gemv_cpl_supported(c);
+        if ((profile & 3) == 1 || nb || D.dc != 4 || !shapes) {
+            log("the wavefront-GEMV tier needs F32 or per-row int8 weights, RMSNorm, d_conv 4 and compiled shapes");
+            fclose(f);
+            return -2;
+        }
+    }
+    G.gemv = gemv;
     const size_t V = D.vocab, d = D.d, di = D.di, dc = D.dc, dr = D.dr, xr = D.xr();
     log("rbin v%u: d=%u di=%u ds=%u dc=%u dr=%u nl=%u vs=%u flags=0x%02x tok=%u profile=%u", h[1], D.d, D.di, D.ds,
         D.dc, D.dr, D.nl, D.vocab, D.flags, D.tokenizer, profile);
     bool ok = true;
     {
         std::vector<float> e = rd.read(V * d);
-        ok = rd.ok && make_tmat(G.emb, e.data(), (int)V, (int)d, qgroup((int)d));
+        ok = rd.ok && (gemv ? make_gmat(G.g_emb, e.data(), (int)V, (int)d, quant != 0)
+                            : make_tmat(G.emb, e.data(), (int)V, (int)d, qgroup((int)d)));
     }
     G.layers.assign(D.nl, DLayer{});
     for (uint32_t i = 0; ok && i < D.nl; i++) {
@@ -239,14 +298,32 @@ int load_weights(const std::string& path, uint32_t profile) {
         if (ok && nb) { t = rd.read(d); ok = rd.ok && (L.norm_b = dev_upload(t.data(), d)); }
         if (ok) {
             t = rd.read(2 * di * d);
-            ok = rd.ok && make_tmat(L.in_x, t.data(), (int)di, (int)d, qgroup((int)d)) &&
-                 make_tmat(L.in_z, t.data() + di * d, (int)di, (int)d, qgroup((int)d));
+            if (gemv)
+                ok = rd.ok && make_gmat(L.g_in, t.data(), (int)(2 * di), (int)d, quant != 0);
+            else
+                ok = rd.ok && make_tmat(L.in_x, t.data(), (int)di, (int)d, qgroup((int)d)) &&
+                     make_tmat(L.in_z, t.data() + di * d, (int)di, (int)d, qgroup((int)d));
         }
         if (ok) { t = rd.read(di * dc); ok = rd.ok && (L.conv_w = dev_upload(t.data(), di * dc)); }
         if (ok) { t = rd.read(di); ok = rd.ok && (L.conv_b = dev_upload(t.data(), di)); }
         if (ok) {
             t = rd.read(xr * di);
-            ok = rd.ok && make_tmat(L.x_proj, t.data(), (int)xr, (int)di, qsmall ? qgroup((int)di) : 0);
+            if (gemv) {
+                // row-major for the GEMV tier's x_proj partials; the tile shape fields only
+                L.x_proj.rows = (int)xr;
+                L.x_proj.cols = (int)di;
+                L.x_proj.rt = (int)((xr + kRowTile - 1) / kRowTile);
+                if (qsmall) {
+                    std::vector<int8_t> q;
+                    std::vector<float> sc;
+                    quantize(t.data(), (int)xr, (int)di, (int)di, q, sc);
+                    ok = rd.ok && (L.xp_q = dev_upload(q.data(), q.size())) && (L.xp_scales = dev_upload(sc.data(), sc.size()));
+                } else {
+                    ok = rd.ok && (L.xp_w = dev_upload(t.data(), t.size())) != nullptr;
+                }
+            } else {
+                ok = rd.ok && make_tmat(L.x_proj, t.data(), (int)xr, (int)di, qsmall ? qgroup((int)di) : 0);
+            }
         }
         if (ok) {
             t = rd.read(di * dr);
@@ -282,7 +359,11 @@ int load_weights(const std::string& path, uint32_t profile) {
             ok = rd.ok && (L.a_exp = dev_upload(ta.data(), ta.size()));
         }
         if (ok) { t = rd.read(di); ok = rd.ok && (L.d_vec = dev_upload(t.data(), di)); }
-        if (ok) { t = rd.read(d * di); ok = rd.ok && make_tmat(L.out_proj, t.data(), (int)d, (int)di, qgroup((int)di)); }
+        if (ok) {
+            t = rd.read(d * di);
+            ok = rd.ok && (gemv ? make_gmat(L.g_out, t.data(), (int)d, (int)di, quant != 0)
+                                : make_tmat(L.out_proj, t.data(), (int)d, (int)di, qgroup((int)di)));
+        }
         if (ok && ((i + 1) % 8 == 0 || i + 1 == D.nl)) log("loaded layer %u/%u", i + 1, D.nl);
     }
     if (ok) { std::vector<float> t = rd.read(d); ok = rd.ok && (G.norm_f_w = dev_upload(t.data(), d)); }
@@ -290,7 +371,8 @@ int load_weights(const std::string& path, uint32_t profile) {
     G.tied = !uh;
     if (ok && uh) {
         std::vector<float> t = rd.read(V * d);
-        ok = rd.ok && make_tmat(G.head_own, t.data(), (int)V, (int)d, qgroup((int)d));
+        ok = rd.ok && (gemv ? make_gmat(G.g_head_own, t.data(), (int)V, (int)d, quant != 0)
+                            : make_tmat(G.head_own, t.data(), (int)V, (int)d, qgroup((int)d)));
     }
     fclose(f);
     return ok ? 0 : -1;
@@ -493,6 +575,7 @@ bool pool_alloc(Pool& p, uint32_t cap) {
         c.take(p.z, n * di);
         c.take(p.xpart, xpart_floats(D, cap));
         c.take(p.glimb, glimb_elems(D, cap));
+        c.take(p.g32, G.gemv ? n * di : 0);
         c.take(p.out, n * D.vocab);
         c.take(p.conv, (size_t)D.nl * ns * di * (D.dc - 1));
         c.take(p.ssm, (size_t)D.nl * ns * di * 16);
@@ -518,11 +601,20 @@ ModelView model_view() {
                      (G.profile & BACKEND_PROFILE_EXACT_SCAN) != 0};
 }
 
+GemvView gemv_view() {
+    return GemvView{&G.dims, G.layers.data(), &G.g_emb, G.tied ? &G.g_emb : &G.g_head_own, G.norm_f_w,
+                    (G.profile & BACKEND_PROFILE_EXACT_SCAN) != 0};
+}
+
 hipError_t run_step(Pool& p, uint32_t n, const uint32_t* slots, const uint32_t* tokens, float* out, bool probs,
                     bool check) {
     StepIO io{n, slots, tokens, out, probs, check, G.d_err};
     if (G.kind == kKindRwkv) {
         const RwkvStep src(RwkvView{&G.rdims, G.rlayers.data(), &G.r_emb, &G.r_head, G.ln_out_w, G.ln_out_b});
+        return G.runner.run(src, p, io, G.stream, &G.probe);
+    }
+    if (G.gemv) {
+        const GemvStep src(gemv_view());
         return G.runner.run(src, p, io, G.stream, &G.probe);
     }
     const MambaStep src(model_view());
@@ -583,7 +675,7 @@ uint32_t env_weight_profile() {
     if (!strcmp(e, "q8row")) return BACKEND_PROFILE_Q8_ROW;
     if (!strcmp(e, "q8row-all")) return BACKEND_PROFILE_Q8_ROW | BACKEND_PROFILE_Q8_SMALL;
     if (!strcmp(e, "q8-all")) return BACKEND_PROFILE_Q8_G64 | BACKEND_PROFILE_Q8_SMALL;
-    return (uint32_t)strtoul(e, nullptr, 0) & 15u;
+    return (uint32_t)strtoul(e, nullptr, 0) & 31u;
 }
 
 // REDUKT_GPU_SPLIT: most parts (sub-batches on their own streams) a step is split into.
@@ -649,6 +741,7 @@ bool noalloc_view(Pool& v, uint32_t n, unsigned char* base, size_t* used) {
     c.take(v.z, (size_t)n * D.di);
     c.take(v.xpart, xpart_floats(D, n));
     c.take(v.glimb, glimb_elems(D, n));
+    if (G.gemv) c.take(v.g32, (size_t)n * D.di);
     *used = (c.off + 255) & ~(size_t)255;
     v.out = nullptr;
     v.d_slots = v.d_tokens = v.h_slots = v.h_tokens = nullptr;
@@ -677,9 +770,15 @@ int init_common(const uint8_t* weights_path, int32_t device_id, uint32_t profile
     G.profile = profile;
     G.runner.set_split(env_split(), env_part_min());
     G.kind = file_kind(path);
-    if ((G.kind == kKindRwkv ? load_rwkv(path, profile) : load_weights(path, profile)) != 0) {
+    if (G.kind == kKindRwkv && (profile & BACKEND_PROFILE_GEMV)) {
+        log("the wavefront-GEMV tier serves Mamba models only");
         free_model();
-        return BACKEND_WEIGHTS_NOT_FOUND;
+        return BACKEND_INIT_FAILED;
+    }
+    const int lr = G.kind == kKindRwkv ? load_rwkv(path, profile) : load_weights(path, profile);
+    if (lr != 0) {
+        free_model();
+        return lr == -2 ? BACKEND_INIT_FAILED : BACKEND_WEIGHTS_NOT_FOUND;
     }
     if (hipMalloc((void**)&G.d_err, sizeof(uint32_t)) != hipSuccess) {
         G.d_err = nullptr;
@@ -795,7 +894,7 @@ int32_t redukt_backend_forward_batch(uint32_t n_streams, const uint32_t* slots, 
 
 int32_t redukt_backend_init_ex(const uint8_t* weights_path, int32_t device_id, uint32_t profile,
                                BackendInfo* info_out) {
-    if (profile > 15u) return BACKEND_INVALID_ARGUMENT;
+    if (profile > 31u) return BACKEND_INVALID_ARGUMENT;
     return init_common(weights_path, device_id, profile, info_out);
 }
 
@@ -836,6 +935,10 @@ int32_t redukt_backend_forward_batch_device_noalloc(uint32_t n_streams, const ui
                        (uint4*)base, n16);
     if (hipGetLastError() != hipSuccess) return BACKEND_FORWARD_FAILED;
     StepIO io{n_streams, d_slots, d_tokens, d_out, (flags & 1u) != 0, true, G.d_err};
+    if (G.gemv) {
+        const GemvStep src(gemv_view());
+        return G.runner.run_direct(src, v, io, G.stream) == hipSuccess ? BACKEND_OK : BACKEND_FORWARD_FAILED;
+    }
     const MambaStep src(model_view());
     return G.runner.run_direct(src, v, io, G.stream) == hipSuccess ? BACKEND_OK : BACKEND_FORWARD_FAILED;
 }

@@ -965,7 +965,8 @@ struct ScanArgs {
     const uint32_t* slots;
     uint32_t cap, n;       // batch rows of the partials, streams
     uint32_t scap;         // state slots (the slot clamp bound)
-    __bf16* glimb;         // [groups][di/32][3][64][8]
+    __bf16* glimb;         // [groups][di/32][3][64][8], or
+    float* g32;            // [n][di] f32 (the wavefront-GEMV tier)
     int di, dr;
 };
 
@@ -1204,6 +1205,10 @@ __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
         const float y = ((l[0] + l[4]) + (l[1] + l[5])) + ((l[2] + l[6]) + (l[3] + l[7])) + dv * x[s];
         const float sg = 1.0f / (1.0f + exp_f(gate_body ? lane_exp_arg(0.0f - zz[s]) : -zz[s]));
         const float gv = y * (zz[s] * sg);
+        if (a.g32 != nullptr) {
+            a.g32[(size_t)b * di + j] = gv;
+            continue;
+        }
         const Limb3 t3 = split3(gv);
         const int g = b / kRowTile, sk = j / kKStep;
         const int ln = (b % kRowTile) + kRowTile * ((j % kKStep) / 8);
@@ -1923,6 +1928,18 @@ Launch head_launch(const TMat& H, Pool& p, const StepIO& io, const float* x, con
                         dim3(kHeadWaves * kWave), lds_h, KC_HEAD, ha);
 }
 
+Launch scan_launch(const DLayer& L, const Dims& D, Pool& p, uint32_t n, bool exact, __bf16* glimb, float* g32,
+                   float* ssm_layer) {
+    const int di = (int)D.di, nxp = di / kXpBlock;
+    const int xr_pad = L.x_proj.rt * kRowTile;
+    const uint32_t spt = scan_spt(n);
+    ScanArgs sa{p.xpart, nxp, xr_pad, (int)D.xr(), p.u, p.z, ssm_layer, L.dt_w, L.dt_q, L.dt_scales, L.dt_pad, L.dt_b,
+                L.a_exp, L.d_vec, p.slots, p.xcap, n, p.scap, glimb, g32, di, (int)D.dr};
+    const void* fs = scan_fn(L.dt_q != nullptr, !exact, (int)D.dr, nxp, spt);
+    return Launch::make(fs, dim3(xcd_grid((di + kBlock - 1) / kBlock, (n + spt - 1) / spt)), dim3(kBlock), 0, KC_SCAN,
+                        sa);
+}
+
 Launch softmax_launch(float* out, int vocab, uint32_t n) {
     const void* f = vocab <= 1024 * kSoftmaxPer ? (const void*)k_softmax<kSoftmaxPer> : (const void*)k_softmax<0>;
     return Launch::make(f, dim3(n), dim3(1024), 0, KC_SOFTMAX, SoftmaxArgs{out, vocab});
@@ -1970,8 +1987,6 @@ void build_step(const ModelView& m, Pool& pool, const StepIO& io, std::vector<La
     const bool q8_row = m.layers[0].in_x.group != 0 && m.layers[0].in_x.group == m.layers[0].in_x.cols;
     const int in_tiles = pre && q8_row && n >= (uint32_t)kInWideFrom ? 4 : 2;
     const int nxb = di / (kRowTile * in_tiles);
-    const int nxp = di / kXpBlock;
-    const uint32_t spt = scan_spt(n);
     const int ks_x = m.layers[0].in_x.ks, tiles = d / kRowTile;
     io_index = (int)out.size();
     out.push_back(embed_launch(*m.emb, p, io, m.layers[0].norm_w, pre ? p.xw : nullptr, p.ssp, ks_x, tiles));
@@ -1990,11 +2005,7 @@ void build_step(const ModelView& m, Pool& pool, const StepIO& io, std::vector<La
                      p.xw, p.ssp, tiles};
         const int zb = L.in_z.rt / in_tiles;
         out.push_back(Launch::make(fin, dim3(nxb + zb, in_chunks), dim3(kBlock), lds_in, KC_MIX_IN, ma));
-        ScanArgs sa{p.xpart, nxp, xr_pad, (int)D.xr(), p.u, p.z, p.ssm + li * ssm_layer, L.dt_w, L.dt_q,
-                    L.dt_scales, L.dt_pad, L.dt_b, L.a_exp, L.d_vec, p.slots, p.xcap, n, p.scap, p.glimb, di, (int)D.dr};
-        const void* fs = scan_fn(L.dt_q != nullptr, !m.exact_scan, (int)D.dr, nxp, spt);
-        out.push_back(Launch::make(fs, dim3(xcd_grid((di + kBlock - 1) / kBlock, (n + spt - 1) / spt)), dim3(kBlock), 0,
-                                   KC_SCAN, sa));
+        out.push_back(scan_launch(L, D, p, n, m.exact_scan, p.glimb, nullptr, p.ssm + li * ssm_layer));
         const float* nw_next = li + 1 < D.nl ? m.layers[li + 1].norm_w : m.norm_f_w;
         MixOutArgs oa{L.out_proj, p.glimb, p.x, n, d, nw_next, pre ? p.xw : nullptr, p.ssp, ks_x, tiles};
         const void* fo = mix_out_fn(q8, out_g, m.layers[0].out_proj.ks == 2 * kOutWaves * kOutPairs);

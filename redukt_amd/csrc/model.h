@@ -36,6 +36,23 @@ struct TMat {
     size_t bytes() const;  // HBM bytes of weights + scales as stored
 };
 
+// A projection matrix in the layout of the wavefront-GEMV kernels (the small-batch tier).
+// K = cols is cut into 16-element chunks, CR = K / 16 per row.  A wave multiplies RPI rows
+// at a time (an iteration block); lane l owns row l % RPI of the block and the CPL chunks
+// c_j = l / RPI + (64 / RPI) j, j < CPL, so CPL * 64 = CR * RPI.  The lane's activation
+// slice (its chunks' K indices) is therefore the same for every block, and every load of
+// a wave is one contiguous run: block i, load j, lane l at ((i CPL + j) 64 + l) * chunk
+// bytes (Q8: 16 int8, F32: 16 f32).  Rows are padded to whole blocks with zeros.  Q8
+// scales are one per row ([rows]).
+struct GMat {
+    int rows = 0, cols = 0;
+    int rpi = 0, cpl = 0, blocks = 0;
+    bool q8 = false;
+    void* w = nullptr;
+    float* scales = nullptr;
+    size_t bytes() const;
+};
+
 struct DLayer {
     float* norm_w = nullptr;
     float* norm_b = nullptr;   // LayerNorm bias (flags bit 0) or null
@@ -54,6 +71,13 @@ struct DLayer {
     float* dt_b = nullptr;     // [di]
     float* a_exp = nullptr;    // [16][di] (state-major): exp(A_log), constant per load
     float* d_vec = nullptr;    // [di]
+    // The wavefront-GEMV tier (weight profile bit 4): in_proj rows [0, 2 di) and out_proj in
+    // GEMV layout, x_proj row-major [xr][di] (F32 in xp_w, or Q8 in xp_q with one scale per
+    // row in xp_scales); dt_proj as above.
+    GMat g_in, g_out;
+    float* xp_w = nullptr;
+    int8_t* xp_q = nullptr;
+    float* xp_scales = nullptr;
 };
 
 struct Dims {
@@ -87,6 +111,7 @@ struct Pool {
     float* z = nullptr;          // [cap][di] gate branch
     float* xpart = nullptr;      // [di/64][cap][xr_pad] split-K partials of x_proj
     __bf16* glimb = nullptr;     // [gcap][di/32][3][64][8] gated, 3 bf16 limbs, B-fragment tiles
+    float* g32 = nullptr;        // [cap][di] gated, f32 (the wavefront-GEMV tier)
     // Next projection's input, written by the producer of the residual stream (embedding,
     // out_proj): x * norm_w as 3 bf16 limbs in B-fragment tiles, [gcap][ks_d][3][64][8]
     // with ks_d = the k-steps of a d-column projection, plus per-16-column partial sums of
@@ -217,6 +242,26 @@ struct MambaStep final : StepSource {
     void build(Pool& p, const StepIO& io, std::vector<Launch>& out, int& io_i, int& head_i, int& sm_i) const override;
     bool splittable() const override { return true; }
 };
+
+// The Mamba step on the wavefront-GEMV kernels (weights in GMat layout).
+struct GemvView {
+    const Dims* dims;
+    const DLayer* layers;
+    const GMat* emb;        // the embedding in GEMV layout
+    const GMat* head;       // emb when tied
+    const float* norm_f_w;
+    bool exact_scan;
+};
+
+struct GemvStep final : StepSource {
+    GemvView m;
+    explicit GemvStep(const GemvView& v) : m(v) {}
+    void build(Pool& p, const StepIO& io, std::vector<Launch>& out, int& io_i, int& head_i, int& sm_i) const override;
+};
+
+// GEMV layout parameters of a K-column matrix: false if K is not a multiple of 16 or no
+// chunks-per-lane count up to 8 divides the lanes evenly.
+bool gemv_shape(int cols, int& rpi, int& cpl);
 
 struct RwkvStep final : StepSource {
     RwkvView m;

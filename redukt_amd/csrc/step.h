@@ -49,6 +49,14 @@ Launch embed_launch(const TMat& emb, Pool& p, const StepIO& io, const float* nw0
 Launch head_launch(const TMat& H, Pool& p, const StepIO& io, const float* x, const float* nw, const float* nb,
                    const __bf16* xw, const float* ssp, int d, int tiles, bool ws);
 Launch softmax_launch(float* out, int vocab, uint32_t n);
+// The scan of one layer over n streams of pool p (its x_proj partials, u, z and slots),
+// writing the gated vector as bf16 limb tiles (glimb) or as f32 rows (g32).
+struct DLayer;
+struct Dims;
+Launch scan_launch(const DLayer& L, const Dims& D, Pool& p, uint32_t n, bool exact, __bf16* glimb, float* g32,
+                   float* ssm_layer);
+// The wavefront-GEMV tier: whether a chunks-per-lane count is compiled.
+bool gemv_cpl_supported(int cpl);
 
 namespace {
 
