@@ -9,6 +9,10 @@
 
 #include <algorithm>
 #include <cmath>
+#include <condition_variable>
+#include <functional>
+#include <mutex>
+#include <thread>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -480,10 +484,108 @@ void dev_free_all() {
     G.arena_used = 0;
 }
 
+// Outputs reach host memory in rounds of up to kOutRoundBytes through a pinned buffer:
+// every chunk of a round is copied D2H at once, each with its own event, and the host
+// threads of copy_pool() move each chunk into the caller's buffer as soon as its DMA ends.
+// A round is cut into two chunks (at least kOutChunkBytes each): each D2H copy costs about
+// 8 us on top of its bytes (53 GB/s pinned), so the second chunk's DMA hides the first
+// chunk's host copy without paying that cost many times (6.4 MB: one copy 120 us, seven
+// 1 MB copies 175 us).
+constexpr size_t kOutChunkBytes = (size_t)1 << 20;
+constexpr size_t kOutChunksPerRound = 2;
+constexpr size_t kOutRoundBytes = (size_t)32 << 20;
+constexpr unsigned kCopyThreads = 4;   // the caller's thread and three helpers
+
+bool out_stage_alloc(Pool& p, size_t out_bytes) {
+    p.out_stage_bytes = std::min(kOutRoundBytes, (out_bytes + 255) & ~(size_t)255);
+    if (hipHostMalloc((void**)&p.h_out, p.out_stage_bytes, hipHostMallocDefault) != hipSuccess) {
+        p.h_out = nullptr;
+        return false;
+    }
+    static_assert(kOutRoundBytes / kOutChunkBytes <= sizeof(Pool::out_ev) / sizeof(hipEvent_t), "events per round");
+    const size_t chunks = (p.out_stage_bytes + kOutChunkBytes - 1) / kOutChunkBytes;
+    for (size_t c = 0; c < chunks; c++)
+        if (hipEventCreateWithFlags(&p.out_ev[c], hipEventDisableTiming) != hipSuccess) return false;
+    return true;
+}
+
+// Host threads that copy a round's chunks: one job per round, chunk c taken by thread
+// c % kCopyThreads (thread 0 is the caller).  A job ends when every helper that took it has
+// finished its chunks, so nothing of a job is touched after run() returns.
+class CopyPool {
+public:
+    ~CopyPool() {
+        {
+            std::lock_guard<std::mutex> g(mu_);
+            stop_ = true;
+            ++gen_;
+        }
+        cv_.notify_all();
+        for (auto& t : th_) t.join();
+    }
+    // body(c) for c in [0, chunks), spread over kCopyThreads threads; false if any failed.
+    bool run(size_t chunks, const std::function<bool(size_t)>& body) {
+        if (th_.empty())
+            for (unsigned i = 1; i < kCopyThreads; i++) th_.emplace_back([this, i] { loop(i); });
+        {
+            std::lock_guard<std::mutex> g(mu_);
+            body_ = &body;
+            chunks_ = chunks;
+            busy_ = kCopyThreads - 1;
+            ok_ = true;
+            ++gen_;
+        }
+        cv_.notify_all();
+        bool ok = true;
+        for (size_t c = 0; c < chunks; c += kCopyThreads) ok = body(c) && ok;
+        std::unique_lock<std::mutex> g(mu_);
+        done_.wait(g, [&] { return busy_ == 0; });
+        body_ = nullptr;
+        return ok && ok_;
+    }
+
+private:
+    void loop(unsigned id) {
+        uint64_t seen = 0;
+        for (;;) {
+            const std::function<bool(size_t)>* body;
+            size_t chunks;
+            {
+                std::unique_lock<std::mutex> g(mu_);
+                cv_.wait(g, [&] { return gen_ != seen; });
+                seen = gen_;
+                if (stop_) return;
+                body = body_;
+                chunks = chunks_;
+            }
+            bool ok = true;
+            for (size_t c = id; c < chunks; c += kCopyThreads) ok = (*body)(c) && ok;
+            std::lock_guard<std::mutex> g(mu_);
+            ok_ = ok_ && ok;
+            if (--busy_ == 0) done_.notify_all();
+        }
+    }
+    std::vector<std::thread> th_;
+    std::mutex mu_;
+    std::condition_variable cv_, done_;
+    uint64_t gen_ = 0;
+    bool stop_ = false, ok_ = true;
+    unsigned busy_ = 0;
+    const std::function<bool(size_t)>* body_ = nullptr;
+    size_t chunks_ = 0;
+};
+
+CopyPool& copy_pool() {
+    static CopyPool pool;
+    return pool;
+}
+
 void pool_free(Pool& p) {
     if (p.block) (void)hipFree(p.block);
     if (p.h_slots) (void)hipHostFree(p.h_slots);
-    if (p.h_tokens) (void)hipHostFree(p.h_tokens);
+    if (p.h_out) (void)hipHostFree(p.h_out);
+    for (hipEvent_t& e : p.out_ev)
+        if (e) (void)hipEventDestroy(e);
     free(p.seen);
     p = Pool{};
 }
@@ -518,6 +620,8 @@ bool pool_carve(Pool& p, F&& layout) {
     return true;
 }
 
+uint32_t vocab_of_model() { return G.dims.vocab; }
+
 size_t slot_words(uint32_t cap) { return ((size_t)cap + kSlotWordAlign - 1) / kSlotWordAlign * kSlotWordAlign; }
 
 bool pool_alloc_rwkv(Pool& p, uint32_t cap) {
@@ -531,8 +635,7 @@ bool pool_alloc_rwkv(Pool& p, uint32_t cap) {
     p.gcap = (cap + 15) / 16;
     bool ok = pool_carve(p, [&](Carve& c) {
         c.take(p.slots, slot_words(cap));
-        c.take(p.d_slots, n);
-        c.take(p.d_tokens, n);
+        c.take(p.d_slots, 2 * n);  // a step's n slots, then its n tokens (one H2D copy)
         c.take(p.x, n * d);
         c.take(p.vfirst, n * d);
         c.take(p.rkv, n * 3 * d);
@@ -548,9 +651,10 @@ bool pool_alloc_rwkv(Pool& p, uint32_t cap) {
         c.take(p.x_ffn, z.state_d);
         c.take(p.wkv, z.wkv);
     });
-    ok = ok && hipHostMalloc((void**)&p.h_slots, sizeof(uint32_t) * n, hipHostMallocDefault) == hipSuccess;
-    ok = ok && hipHostMalloc((void**)&p.h_tokens, sizeof(uint32_t) * n, hipHostMallocDefault) == hipSuccess;
+    ok = ok && hipHostMalloc((void**)&p.h_slots, sizeof(uint32_t) * 2 * n, hipHostMallocDefault) == hipSuccess;
+
     ok = ok && (p.seen = (uint8_t*)calloc(n, 1)) != nullptr;
+    ok = ok && out_stage_alloc(p, (size_t)n * vocab_of_model() * sizeof(float));
     return ok;
 }
 
@@ -566,8 +670,7 @@ bool pool_alloc(Pool& p, uint32_t cap) {
     const size_t ns = p.scap;
     bool ok = pool_carve(p, [&](Carve& c) {
         c.take(p.slots, slot_words(cap));
-        c.take(p.d_slots, n);
-        c.take(p.d_tokens, n);
+        c.take(p.d_slots, 2 * n);  // a step's n slots, then its n tokens (one H2D copy)
         c.take(p.x, n * d);
         c.take(p.xw, xw_elems(D, cap));
         c.take(p.ssp, ssp_floats(D, cap));
@@ -580,9 +683,10 @@ bool pool_alloc(Pool& p, uint32_t cap) {
         c.take(p.conv, (size_t)D.nl * ns * di * (D.dc - 1));
         c.take(p.ssm, (size_t)D.nl * ns * di * 16);
     });
-    ok = ok && hipHostMalloc((void**)&p.h_slots, sizeof(uint32_t) * n, hipHostMallocDefault) == hipSuccess;
-    ok = ok && hipHostMalloc((void**)&p.h_tokens, sizeof(uint32_t) * n, hipHostMallocDefault) == hipSuccess;
+    ok = ok && hipHostMalloc((void**)&p.h_slots, sizeof(uint32_t) * 2 * n, hipHostMallocDefault) == hipSuccess;
+
     ok = ok && (p.seen = (uint8_t*)calloc(n, 1)) != nullptr;
+    ok = ok && out_stage_alloc(p, (size_t)n * vocab_of_model() * sizeof(float));
     return ok;
 }
 
@@ -621,25 +725,50 @@ hipError_t run_step(Pool& p, uint32_t n, const uint32_t* slots, const uint32_t* 
     return G.runner.run(src, p, io, G.stream, &G.probe);
 }
 
+// The first `bytes` of the device array src into the caller's host buffer dst, through the
+// pool's pinned staging, a round at a time: all of a round's 1 MB chunks are queued D2H
+// (each followed by its event) behind the step, then the copy threads move each chunk into
+// dst once its event has completed, while the later chunks are still in flight.  Returns
+// when every byte is in dst.
+bool copy_out(Pool& p, void* dst, const void* src, size_t bytes) {
+    for (size_t r0 = 0; r0 < bytes; r0 += p.out_stage_bytes) {
+        const size_t rb = std::min(p.out_stage_bytes, bytes - r0);
+        const size_t cb = std::max(kOutChunkBytes, ((rb + kOutChunksPerRound - 1) / kOutChunksPerRound + 255) & ~(size_t)255);
+        const size_t chunks = (rb + cb - 1) / cb;
+        for (size_t c = 0; c < chunks; c++) {
+            const size_t off = c * cb, len = std::min(cb, rb - off);
+            if (hipMemcpyAsync(p.h_out + off, (const unsigned char*)src + r0 + off, len, hipMemcpyDeviceToHost,
+                               G.stream) != hipSuccess ||
+                hipEventRecord(p.out_ev[c], G.stream) != hipSuccess)
+                return false;
+        }
+        const bool ok = copy_pool().run(chunks, [&](size_t c) {
+            if (hipEventSynchronize(p.out_ev[c]) != hipSuccess) return false;
+            const size_t off = c * cb, len = std::min(cb, rb - off);
+            memcpy((unsigned char*)dst + r0 + off, p.h_out + off, len);
+            return true;
+        });
+        if (!ok) return false;
+    }
+    return true;
+}
+
 // pool_forward semantics (mamba_cuda.cu:604-635): validate on the host (nothing is
 // launched on INVALID_ARGUMENT), stage slots/tokens through pinned memory, enqueue the
-// step, copy the n rows back to the caller and wait.
+// step, copy the n rows back to the caller (through pinned staging, chunked) and wait.
 int pool_forward(Pool& p, uint32_t n, const uint32_t* slots, const uint32_t* tokens, float* out, bool probs) {
     memset(p.seen, 0, p.cap);
     for (uint32_t b = 0; b < n; b++) {
         if (slots[b] >= p.cap || p.seen[slots[b]] || tokens[b] >= G.dims.vocab) return BACKEND_INVALID_ARGUMENT;
         p.seen[slots[b]] = 1;
     }
+    // the n slots, then the n tokens, in one staging run and one copy
     memcpy(p.h_slots, slots, sizeof(uint32_t) * n);
-    memcpy(p.h_tokens, tokens, sizeof(uint32_t) * n);
-    const size_t ib = sizeof(uint32_t) * n;
-    if (hipMemcpyAsync(p.d_slots, p.h_slots, ib, hipMemcpyHostToDevice, G.stream) != hipSuccess ||
-        hipMemcpyAsync(p.d_tokens, p.h_tokens, ib, hipMemcpyHostToDevice, G.stream) != hipSuccess)
+    memcpy(p.h_slots + n, tokens, sizeof(uint32_t) * n);
+    if (hipMemcpyAsync(p.d_slots, p.h_slots, sizeof(uint32_t) * 2 * n, hipMemcpyHostToDevice, G.stream) != hipSuccess)
         return BACKEND_FORWARD_FAILED;
-    if (run_step(p, n, p.d_slots, p.d_tokens, p.out, probs, false) != hipSuccess) return BACKEND_FORWARD_FAILED;
-    if (hipMemcpyAsync(out, p.out, sizeof(float) * n * G.dims.vocab, hipMemcpyDeviceToHost, G.stream) != hipSuccess)
-        return BACKEND_FORWARD_FAILED;
-    if (hipStreamSynchronize(G.stream) != hipSuccess) return BACKEND_FORWARD_FAILED;
+    if (run_step(p, n, p.d_slots, p.d_slots + n, p.out, probs, false) != hipSuccess) return BACKEND_FORWARD_FAILED;
+    if (!copy_out(p, out, p.out, sizeof(float) * n * G.dims.vocab)) return BACKEND_FORWARD_FAILED;
     return BACKEND_OK;
 }
 
@@ -744,7 +873,7 @@ bool noalloc_view(Pool& v, uint32_t n, unsigned char* base, size_t* used) {
     if (G.gemv) c.take(v.g32, (size_t)n * D.di);
     *used = (c.off + 255) & ~(size_t)255;
     v.out = nullptr;
-    v.d_slots = v.d_tokens = v.h_slots = v.h_tokens = nullptr;
+    v.d_slots = v.h_slots = nullptr;
     v.seen = nullptr;
     return *used <= kNoAllocScratchBytes;
 }

@@ -133,10 +133,13 @@ struct Pool {
     __bf16* headl = nullptr;     // [gcap][ks_d][3][64][8] final LayerNorm output
     float* out = nullptr;        // [cap][vocab] logits or probabilities
     uint32_t* slots = nullptr;   // [cap] slots of the current step (validated copy)
-    uint32_t* d_slots = nullptr; // [cap] H2D staging targets of the synchronous entry points
-    uint32_t* d_tokens = nullptr;
-    uint32_t* h_slots = nullptr; // pinned staging
-    uint32_t* h_tokens = nullptr;
+    uint32_t* d_slots = nullptr; // [2 cap] H2D target of the synchronous entry points: n slots, then n tokens
+    uint32_t* h_slots = nullptr; // [2 cap] pinned staging of the same
+    // Pinned staging of the outputs handed back to host memory (up to one round of
+    // out_stage_bytes), with one completion event per 1 MB chunk of a round.
+    unsigned char* h_out = nullptr;
+    size_t out_stage_bytes = 0;
+    hipEvent_t out_ev[32] = {};
     uint8_t* seen = nullptr;     // host duplicate check, cap bytes
 };
 
