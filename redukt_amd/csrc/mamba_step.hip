@@ -102,6 +102,78 @@ constexpr int kOutWaves = 8;               // waves of k_mix_out
 constexpr int kOutPairs = 3;               // k-pairs per k_mix_out wave per pass
 static_assert(kSlotWordAlign % kInChunk == 0, "k_mix_in reads its chunk's slot words whole");
 
+// Raw buffer access: a descriptor with a uniform base and an exact byte size (gfx9 word 3:
+// 32-bit data format, untyped), a per-lane 32-bit byte offset and a uniform byte offset.
+// Offsets past the size read 0 and drop stores, so every descriptor covers its array.
+typedef __amdgpu_buffer_rsrc_t BufRsrc;
+constexpr int kBufWord3 = 0x00020000;
+__device__ __forceinline__ BufRsrc buf_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kBufWord3);
+}
+// Cache policy of a buffer access (gfx9 "aux" bits): kStream = nt, for data read or
+// written once per step (the recurrent state), so it does not displace reused lines.
+constexpr int kCached = 0, kStream = 2;
+template <int POLICY = kCached>
+__device__ __forceinline__ float buf_ld_f32(BufRsrc r, uint32_t voff, uint32_t soff) {
+    return bits_to_f(__builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, POLICY));
+}
+__device__ __forceinline__ int4 buf_ld_i4(BufRsrc r, uint32_t voff, uint32_t soff) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
+    return make_int4((int)v[0], (int)v[1], (int)v[2], (int)v[3]);
+}
+template <int POLICY = kCached>
+__device__ __forceinline__ void buf_st_f32(float v, BufRsrc r, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_buffer_store_b32(f_to_bits(v), r, (int)voff, (int)soff, POLICY);
+}
+
+__device__ __forceinline__ BufRsrc buf_rsrc_any(const void* base) { return buf_rsrc(base, 0x7fffffffu); }
+template <int POLICY = kCached>
+__device__ __forceinline__ int4 buf_ld_i4p(BufRsrc r, uint32_t voff, uint32_t soff) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, POLICY);
+    return make_int4((int)v[0], (int)v[1], (int)v[2], (int)v[3]);
+}
+__device__ __forceinline__ bf16x8 as_frag(int4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// ---------------------------------------------------------------- task synchronization
+
+// A layer kernel's body runs either as a kernel of its own (NoWait: its inputs were
+// complete when it started) or as a task of the persistent step kernel (FlowWait).  There
+// the previous phase's outputs are written during the same launch by other CUs of the
+// same XCD: the task first requests everything that does not depend on them (weights,
+// scales, recurrent state), then waits for the phase counter, then reads those outputs
+// past its CU's L1 (sc0, kAux), from the XCD's L2 where they were written.
+struct NoWait {
+    static constexpr bool kFlow = false;
+    static constexpr int kAux = kCached;
+    __device__ __forceinline__ void wait() const {}
+};
+
+// Spins of a wait before it gives up: a task that waits this long (tens of ms, far past
+// any phase) sets bit 2 of the error word and goes on, so every wave still exits.
+constexpr uint32_t kFlowSpinMax = 1u << 20;
+constexpr int kL1Bypass = 1;   // sc0: the load misses the CU's L1 and reads the XCD's L2
+
+struct FlowWait {
+    static constexpr bool kFlow = true;
+    static constexpr int kAux = kL1Bypass;
+    const uint32_t* counter;   // null: nothing to wait for
+    uint32_t target;
+    uint32_t* err;
+    __device__ __forceinline__ void wait() const {
+        if (threadIdx.x == 0 && counter != nullptr) {
+            uint32_t spins = 0;
+            while (__hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+                __builtin_amdgcn_s_sleep(1);
+                if (++spins > kFlowSpinMax) {
+                    atomicOr(err, 4u);
+                    break;
+                }
+            }
+        }
+        __syncthreads();
+    }
+};
+
 // ---------------------------------------------------------------- activation staging
 
 // Norm of the chunk's streams and their bf16 limbs into LDS in B-fragment order:
@@ -250,15 +322,25 @@ struct SspLoad {
 // Streams [b0, b0 + streams) of the workgroup; threads past them load a valid row that
 // is never used.  The loads are unconditional (clamped rows and tiles) so that they are
 // issued in straight-line code with the caller's other loads; ssp_reduce masks them.
+// AUX: the cache policy (L1-bypassing inside the persistent step kernel).
+template <int AUX = kCached>
 __device__ __forceinline__ SspLoad ssp_load(const float* __restrict__ ssp, int tiles, uint32_t b0, uint32_t n,
                                             int streams) {
     const int bb = threadIdx.x / kTps, sub = threadIdx.x % kTps;
     const uint32_t b = b0 + bb;
     const bool on = bb < streams && b < n;
     SspLoad r;
-    const float* p = ssp + (size_t)(on ? b : 0) * tiles;
+    if constexpr (AUX == kCached) {
+        const float* p = ssp + (size_t)(on ? b : 0) * tiles;
 #pragma unroll
-    for (int i = 0; i < kSspPerThread; i++) r.v[i] = p[min(sub + kTps * i, tiles - 1)];
+        for (int i = 0; i < kSspPerThread; i++) r.v[i] = p[min(sub + kTps * i, tiles - 1)];
+    } else {
+        const BufRsrc rs = buf_rsrc_any(ssp);
+        const uint32_t row = (on ? b : 0u) * (uint32_t)tiles;
+#pragma unroll
+        for (int i = 0; i < kSspPerThread; i++)
+            r.v[i] = buf_ld_f32<AUX>(rs, (row + (uint32_t)min(sub + kTps * i, tiles - 1)) * 4u, 0);
+    }
     return r;
 }
 
@@ -431,7 +513,7 @@ struct BQuarter {
     bf16x8 f[kQuarterMax][G][2][3];
 };
 
-template <int G, int CNT>
+template <int G, int CNT, int AUX = kCached>
 __device__ __forceinline__ void bquarter_load(BQuarter<G>& bq, const __bf16* __restrict__ xw, uint32_t g0, int ng,
                                               int ks, int p_lo, int cnt) {
     const int lane = threadIdx.x % kWave;
@@ -439,14 +521,21 @@ __device__ __forceinline__ void bquarter_load(BQuarter<G>& bq, const __bf16* __r
 #pragma unroll
     for (int g = 0; g < G; g++) {
         const int gg = G > 1 ? min(g, ng - 1) : g;
-        const __bf16* base = xw + ((size_t)(g0 + gg) * ks + 2 * p_lo) * 3 * 512 + lane * 8;
+        const __bf16* base = xw + ((size_t)(g0 + gg) * ks + 2 * p_lo) * 3 * 512;
+        const BufRsrc rb = buf_rsrc_any(base);
 #pragma unroll
         for (int q = 0; q < Q; q++) {
             const int qq = CNT > 0 ? q : quarter_slot(q, cnt);
 #pragma unroll
             for (int h = 0; h < 2; h++)
 #pragma unroll
-                for (int m = 0; m < 3; m++) bq.f[q][g][h][m] = lds_frag(base + ((2 * qq + h) * 3 + m) * 512);
+                for (int m = 0; m < 3; m++) {
+                    const int off = ((2 * qq + h) * 3 + m) * 512 + lane * 8;
+                    if constexpr (AUX == kCached)
+                        bq.f[q][g][h][m] = lds_frag(base + off);
+                    else
+                        bq.f[q][g][h][m] = as_frag(buf_ld_i4p<AUX>(rb, (uint32_t)off * 2u, 0));
+                }
         }
     }
 }
@@ -684,9 +773,10 @@ struct MixInArgs {
 // and leaves k_scan one split-K partial per k-step (32 channels), whatever T is, so every
 // batch size sums the same partials.  Two tiles give more, smaller workgroups (small
 // batches); four read each stream's activations half as often.
-template <bool Q8, bool Q8XP, bool PRE, bool GRP, int QP, int T>
-__global__ __launch_bounds__(kBlock) void k_mix_in(MixInArgs a) {
+template <bool Q8, bool Q8XP, bool PRE, bool GRP, int QP, int T, class SYNC>
+__device__ __forceinline__ void mix_in_body(const MixInArgs& a, uint32_t bx, uint32_t by, const SYNC& sync) {
     static_assert(kInGroups == 1 && (T == 2 || T == 4) && kWaves == 4, "one stream group, 2 or 4 tiles");
+    static_assert(!SYNC::kFlow || PRE, "persistent tasks take pre-staged activations");
     constexpr int E = T;                   // rows per lane in the finish
     constexpr int WT = kWaves / T;         // waves per tile in the finish
     constexpr int KS = T / 2;              // x_proj k-steps per block
@@ -696,10 +786,10 @@ __global__ __launch_bounds__(kBlock) void k_mix_in(MixInArgs a) {
     __shared__ float invs[kInChunk];
     __bf16* lds = (__bf16*)smem;
     const int lane = threadIdx.x % kWave, wave = wave_index();
-    const uint32_t b0 = blockIdx.y * kInChunk;
-    const bool conv_branch = (int)blockIdx.x < a.nxb;
+    const uint32_t b0 = by * kInChunk;
+    const bool conv_branch = (int)bx < a.nxb;
     const TMat& w = conv_branch ? a.wx : a.wz;
-    const int tb = (conv_branch ? blockIdx.x : blockIdx.x - a.nxb) * T;  // the block's first row tile
+    const int tb = (conv_branch ? (int)bx : (int)bx - a.nxb) * T;  // the block's first row tile
     // The rows this wave finishes and this lane's E rows and stream.
     const int tf = wave / WT;
     const int r0 = (wave % WT) * (kRowTile / WT) + (lane / 16) * E;  // row within the tile
@@ -740,7 +830,7 @@ __global__ __launch_bounds__(kBlock) void k_mix_in(MixInArgs a) {
     quarter_prefetch<Q8, R, T>(w, qw, tb, p_lo, p_hi - p_lo);
     BQuarter<1> bq;
     SspLoad sl;
-    if constexpr (PRE) {
+    if constexpr (PRE && !SYNC::kFlow) {
         bquarter_load<1, QP>(bq, a.xw, b0 / kRowTile, 1, a.wx.ks, p_lo, p_hi - p_lo);
         sl = ssp_load(a.ssp, a.tiles, b0, a.n, kInChunk);
     }
@@ -767,7 +857,7 @@ __global__ __launch_bounds__(kBlock) void k_mix_in(MixInArgs a) {
     // tiles), with their scales; loaded by every block from clamped, in-bounds tiles (a
     // gate-branch block or a tile past x_proj's rows reads the last one and never uses it).
     // Column-group scales take the block's 64-column group, one scale per row r.
-    const int p = min((int)blockIdx.x, a.nxb - 1);
+    const int p = min((int)bx, a.nxb - 1);
     const int xpair = p * KS / 2;
     RawPair xpw[2];
     float4 xps[2];
@@ -795,6 +885,13 @@ __global__ __launch_bounds__(kBlock) void k_mix_in(MixInArgs a) {
         const fE* sp = (const fE*)(a.conv_st + off);
 #pragma unroll
         for (int k = 0; k < 3; k++) stv[k] = __builtin_nontemporal_load(sp + k);
+    }
+    // As a task: the previous phase's outputs (the activation tiles and RMS partials) once
+    // its counter is complete, everything else already in flight.
+    if constexpr (PRE && SYNC::kFlow) {
+        sync.wait();
+        bquarter_load<1, QP, SYNC::kAux>(bq, a.xw, b0 / kRowTile, 1, a.wx.ks, p_lo, p_hi - p_lo);
+        sl = ssp_load<SYNC::kAux>(a.ssp, a.tiles, b0, a.n, kInChunk);
     }
     // Every load above is issued before anything that waits for one of them.
     __builtin_amdgcn_sched_barrier(0);
@@ -947,6 +1044,11 @@ __global__ __launch_bounds__(kBlock) void k_mix_in(MixInArgs a) {
     }
 }
 
+template <bool Q8, bool Q8XP, bool PRE, bool GRP, int QP, int T>
+__global__ __launch_bounds__(kBlock) void k_mix_in(MixInArgs a) {
+    mix_in_body<Q8, Q8XP, PRE, GRP, QP, T>(a, blockIdx.x, blockIdx.y, NoWait{});
+}
+
 // ---------------------------------------------------------------- k_scan
 
 struct ScanArgs {
@@ -983,34 +1085,10 @@ struct ScanArgs {
 // and the number of 32-channel x_proj partials at compile time (0: taken from the
 // arguments, bounded by kMaxDr / kMaxNxb), which removes the guards of the unrolled loops.
 // A thread runs SPT streams of one channel.
-// Raw buffer access: a descriptor with a uniform base and an exact byte size (gfx9 word 3:
-// 32-bit data format, untyped), a per-lane 32-bit byte offset and a uniform byte offset.
-// Offsets past the size read 0 and drop stores, so every descriptor covers its array.
-typedef __amdgpu_buffer_rsrc_t BufRsrc;
-constexpr int kBufWord3 = 0x00020000;
-__device__ __forceinline__ BufRsrc buf_rsrc(const void* base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kBufWord3);
-}
-// Cache policy of a buffer access (gfx9 "aux" bits): kStream = nt, for data read or
-// written once per step (the recurrent state), so it does not displace reused lines.
-constexpr int kCached = 0, kStream = 2;
-template <int POLICY = kCached>
-__device__ __forceinline__ float buf_ld_f32(BufRsrc r, uint32_t voff, uint32_t soff) {
-    return bits_to_f(__builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, POLICY));
-}
-__device__ __forceinline__ int4 buf_ld_i4(BufRsrc r, uint32_t voff, uint32_t soff) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
-    return make_int4((int)v[0], (int)v[1], (int)v[2], (int)v[3]);
-}
-template <int POLICY = kCached>
-__device__ __forceinline__ void buf_st_f32(float v, BufRsrc r, uint32_t voff, uint32_t soff) {
-    __builtin_amdgcn_raw_buffer_store_b32(f_to_bits(v), r, (int)voff, (int)soff, POLICY);
-}
-
 __device__ __forceinline__ float hw_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
 
-template <bool Q8DT, bool FAST, int DR, int NXB, int SPT>
-__global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
+template <bool Q8DT, bool FAST, int DR, int NXB, int SPT, class SYNC>
+__device__ __forceinline__ void scan_body(const ScanArgs& a, uint32_t sy, uint32_t cbx, const SYNC& sync) {
     static_assert(DR >= 0 && DR <= kMaxDr && NXB >= 0 && NXB <= kMaxNxb && SPT >= 1 && SPT <= 2, "scan shape");
     // SPT streams per thread (streams SPT y .. SPT y + SPT - 1 of channel j): the channel's
     // operands (exp(A_log), the dt_proj row, biases, D) are loaded and decoded once for all
@@ -1019,11 +1097,6 @@ __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
     constexpr int kDr = DR ? DR : kMaxDr;
     constexpr int kNxb = NXB ? NXB : kMaxNxb;
     const int di = a.di, dr = DR ? DR : a.dr, nxb = NXB ? NXB : a.nxb;
-    // The channel blocks of a stream group (SPT streams) run on one XCD, so the group's
-    // x_proj partials are fetched into one L2 and shared by its channel blocks.
-    const XcdTile xt = xcd_tile(blockIdx.x, ((uint32_t)di + kBlock - 1) / kBlock, (a.n + SPT - 1) / SPT);
-    if (!xt.live) return;
-    const uint32_t sy = xt.unit, cbx = xt.part;
     const int j_raw = (int)cbx * kBlock + threadIdx.x;
     const bool live = j_raw < di;
     const int j = live ? j_raw : di - 1;
@@ -1053,15 +1126,18 @@ __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
 #pragma unroll
         for (int n = 0; n < 16; n++) av[n] = buf_ld_f32(ra, j4, (uint32_t)n * row4);
     }
+    // The previous phase's outputs (u, z, the x_proj partials): requested here by a kernel
+    // of its own, after the wait by a task of the persistent step kernel.
     float x[SPT], zz[SPT];
-    {
+    auto load_uz = [&]() {
         const BufRsrc ru = buf_rsrc(a.u, (uint32_t)a.n * row4), rz = buf_rsrc(a.z, (uint32_t)a.n * row4);
 #pragma unroll
         for (int s = 0; s < SPT; s++) {
-            x[s] = buf_ld_f32(ru, j4, bs[s] * row4);
-            zz[s] = buf_ld_f32(rz, j4, bs[s] * row4);
+            x[s] = buf_ld_f32<SYNC::kAux>(ru, j4, bs[s] * row4);
+            zz[s] = buf_ld_f32<SYNC::kAux>(rz, j4, bs[s] * row4);
         }
-    }
+    };
+    if constexpr (!SYNC::kFlow) load_uz();
     const float dv = buf_ld_f32(buf_rsrc(a.d_vec, row4), j4, 0);
     const float dtb = buf_ld_f32(buf_rsrc(a.dt_b, row4), j4, 0);
     const float dts = Q8DT ? buf_ld_f32(buf_rsrc(a.dt_scales, row4), j4, 0) : 1.0f;
@@ -1093,7 +1169,7 @@ __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
     const int xr = a.xr;
     const int r = threadIdx.x;
     float pv[kItems][kPer];
-    {
+    auto load_parts = [&]() {
         const uint32_t pstride = (uint32_t)a.cap * (uint32_t)a.xr_pad * 4u;
         const BufRsrc rp = buf_rsrc(a.xpart, (uint32_t)nxb * pstride);
 #pragma unroll
@@ -1106,9 +1182,11 @@ __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
             const uint32_t ps = min(bs0 + (uint32_t)s, a.n - 1);  // the item's stream
             const uint32_t o0 = real ? (ps * (uint32_t)a.xr_pad + (uint32_t)o) * 4u + (uint32_t)(part * kPer) * pstride : 0u;
 #pragma unroll
-            for (int i = 0; i < kPer; i++) pv[it][i] = buf_ld_f32(rp, o0, (uint32_t)(NXB ? i : min(i, nxb - 1)) * pstride);
+            for (int i = 0; i < kPer; i++)
+                pv[it][i] = buf_ld_f32<SYNC::kAux>(rp, o0, (uint32_t)(NXB ? i : min(i, nxb - 1)) * pstride);
         }
-    }
+    };
+    if constexpr (!SYNC::kFlow) load_parts();
     float st[SPT][16];
     BufRsrc rs[SPT];
 #pragma unroll
@@ -1116,6 +1194,11 @@ __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
         rs[s] = buf_rsrc(a.ssm + (size_t)clamp_slot(slot_raw[s], a.scap) * 16 * diu, 16u * row4);
 #pragma unroll
         for (int n = 0; n < 16; n++) st[s][n] = buf_ld_f32<kStream>(rs[s], j4, (uint32_t)n * row4);
+    }
+    if constexpr (SYNC::kFlow) {
+        sync.wait();
+        load_uz();
+        load_parts();
     }
 #pragma unroll
     for (int it = 0; it < kItems; it++) {
@@ -1219,6 +1302,15 @@ __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
     }
 }
 
+// The channel blocks of a stream group (SPT streams) run on one XCD, so the group's x_proj
+// partials are fetched into one L2 and shared by its channel blocks.
+template <bool Q8DT, bool FAST, int DR, int NXB, int SPT>
+__global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
+    const XcdTile xt = xcd_tile(blockIdx.x, ((uint32_t)a.di + kBlock - 1) / kBlock, (a.n + SPT - 1) / SPT);
+    if (!xt.live) return;
+    scan_body<Q8DT, FAST, DR, NXB, SPT>(a, xt.unit, xt.part, NoWait{});
+}
+
 // Streams per scan thread by batch size: sharing a channel's operands pays once a launch
 // has several times more workgroups than the chip holds at once (measured on Mamba-130M:
 // 1-2 % from 256 streams, a loss below; four streams per thread lose everywhere, from the
@@ -1267,12 +1359,20 @@ struct MixOutArgs {
 // FIXED: every wave takes exactly kOutPairs k-pairs (w.ks = 2 kOutWaves kOutPairs, checked
 // on the host), one pass whose loads are all issued unconditionally (clamped group and
 // row indices), the epilogue operands after them, before the first wait.
-template <bool Q8, int G, bool FIXED>
-__global__ __launch_bounds__(kOutWaves * kWave) void k_mix_out(MixOutArgs a) {
+// WAVES < kOutWaves (a task of the persistent step kernel, 4 waves): each wave runs the
+// k-ranges of kOutWaves / WAVES of the kernel's waves (virtual waves w, w + WAVES, ...),
+// each in accumulators of its own, and the cross-wave sum takes them in the kernel's
+// order, so a task's arithmetic is the kernel's.  As a task the weights and scales are
+// requested first, the gated tiles and the residual rows after the wait.
+template <bool Q8, int G, bool FIXED, int WAVES, class SYNC>
+__device__ __forceinline__ void mix_out_body(const MixOutArgs& a, uint32_t t_blk, uint32_t by, const SYNC& sync) {
+    constexpr int VW = kOutWaves / WAVES;
+    static_assert(VW * WAVES == kOutWaves && (VW == 1 || FIXED), "virtual waves need the fixed shape");
+    static_assert(!SYNC::kFlow || FIXED, "persistent tasks take the fixed shape");
     __shared__ f32x4 part[kOutWaves - 1][G][kWave];
     const int lane = threadIdx.x % kWave, wave = wave_index();
-    const int t = blockIdx.x;
-    const uint32_t b0 = blockIdx.y * G * kRowTile;
+    const int t = (int)t_blk;
+    const uint32_t b0 = by * G * kRowTile;
     const int ng = (int)min((uint32_t)G, (a.n - b0 + kRowTile - 1) / kRowTile);
     const TMat& w = a.w;
     const int np = w.ks / 2;
@@ -1284,82 +1384,119 @@ __global__ __launch_bounds__(kOutWaves * kWave) void k_mix_out(MixOutArgs a) {
     float4 xv[G];
     float rs[4] = {1.0f, 1.0f, 1.0f, 1.0f};
     float4 w4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    f32x4 acc3[G][3];
+    f32x4 acc3v[VW][G][3];
 #pragma unroll
-    for (int g = 0; g < G; g++)
+    for (int v = 0; v < VW; v++)
 #pragma unroll
-        for (int o = 0; o < 3; o++) acc3[g][o] = f32x4{0, 0, 0, 0};
+        for (int g = 0; g < G; g++)
+#pragma unroll
+            for (int o = 0; o < 3; o++) acc3v[v][g][o] = f32x4{0, 0, 0, 0};
     if constexpr (FIXED) {
-        RawPair raw[kOutPairs];
-        bf16x8 bfr[kOutPairs][G][2][3];
-        float sc[kOutPairs][4];
-#pragma unroll
-        for (int q = 0; q < kOutPairs; q++) {
-            const int p = wave * kOutPairs + q;
-            raw[q] = load_pair<Q8>(w, t, p, lane);
+        RawPair raw[VW][kOutPairs];
+        bf16x8 bfr[VW][kOutPairs][G][2][3];
+        float sc[VW][kOutPairs][4];
+        const BufRsrc rg = buf_rsrc_any(a.glimb);
+        auto load_acts = [&](int v, int q) {
+            const int p = (wave + WAVES * v) * kOutPairs + q;
 #pragma unroll
             for (int g = 0; g < G; g++) {
                 const uint32_t gg = g0 + (G > 1 ? (uint32_t)min(g, ng - 1) : 0u);
 #pragma unroll
                 for (int h = 0; h < 2; h++) {
-                    const __bf16* f = a.glimb + (((size_t)gg * w.ks + 2 * p + h) * 3) * 512 + lane * 8;
-                    bfr[q][g][h][0] = lds_frag(f);
-                    bfr[q][g][h][1] = lds_frag(f + 512);
-                    bfr[q][g][h][2] = lds_frag(f + 1024);
+                    const size_t off = (((size_t)gg * w.ks + 2 * p + h) * 3) * 512 + lane * 8;
+#pragma unroll
+                    for (int m = 0; m < 3; m++) {
+                        if constexpr (SYNC::kAux == kCached)
+                            bfr[v][q][g][h][m] = lds_frag(a.glimb + off + m * 512);
+                        else
+                            bfr[v][q][g][h][m] = as_frag(buf_ld_i4p<SYNC::kAux>(rg, (uint32_t)(off + m * 512) * 2u, 0));
+                    }
                 }
             }
-            if (grp) {
+        };
+        auto load_x = [&]() {
+            const BufRsrc rx = buf_rsrc_any(a.x);
 #pragma unroll
-                for (int i = 0; i < 4; i++) sc[q][i] = w.scales[(size_t)(t * kRowTile + (lane / 16) * 4 + i) * gpr + p];
+            for (int g = 0; g < G; g++) {
+                const uint32_t b = min(b0 + g * kRowTile + lane % 16, a.n - 1);
+                if constexpr (SYNC::kAux == kCached) {
+                    xv[g] = *(const float4*)(a.x + (size_t)b * a.d + r0);
+                } else {
+                    const int4 v = buf_ld_i4p<SYNC::kAux>(rx, (b * (uint32_t)a.d + (uint32_t)r0) * 4u, 0);
+                    xv[g] = make_float4(bits_to_f((uint32_t)v.x), bits_to_f((uint32_t)v.y), bits_to_f((uint32_t)v.z),
+                                        bits_to_f((uint32_t)v.w));
+                }
             }
-        }
-        // Epilogue operands (used by wave 0), loaded by every wave from clamped rows.
+        };
 #pragma unroll
-        for (int g = 0; g < G; g++) {
-            const uint32_t b = min(b0 + g * kRowTile + lane % 16, a.n - 1);
-            xv[g] = *(const float4*)(a.x + (size_t)b * a.d + r0);
-        }
+        for (int v = 0; v < VW; v++)
+#pragma unroll
+            for (int q = 0; q < kOutPairs; q++) {
+                const int p = (wave + WAVES * v) * kOutPairs + q;
+                raw[v][q] = load_pair<Q8>(w, t, p, lane);
+                if constexpr (!SYNC::kFlow) load_acts(v, q);
+                if (grp) {
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        sc[v][q][i] = w.scales[(size_t)(t * kRowTile + (lane / 16) * 4 + i) * gpr + p];
+                }
+            }
+        // Epilogue operands (used by wave 0), loaded by every wave from clamped rows.
+        if constexpr (!SYNC::kFlow) load_x();
         if (Q8 && !grp) {
             const float4 r4 = *(const float4*)(w.scales + t * kRowTile + (lane / 16) * 4);
             rs[0] = r4.x; rs[1] = r4.y; rs[2] = r4.z; rs[3] = r4.w;
         }
         if (a.xw != nullptr) w4 = *(const float4*)(a.nw_next + r0);
+        if constexpr (SYNC::kFlow) {
+            sync.wait();
+#pragma unroll
+            for (int v = 0; v < VW; v++)
+#pragma unroll
+                for (int q = 0; q < kOutPairs; q++) load_acts(v, q);
+            load_x();
+        }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int q = 0; q < kOutPairs; q++) {
-            AFrag a0, a1;
-            decode_pair<Q8>(raw[q], a0, a1);
+        for (int v = 0; v < VW; v++) {
+            f32x4 (&acc3)[G][3] = acc3v[v];
 #pragma unroll
-            for (int g = 0; g < G; g++) {
-                if (g >= ng) continue;
-                if (grp) {
-                    f32x4 pp{0, 0, 0, 0};
-                    pp = mma_step<Q8>(a0, bfr[q][g][0][0], bfr[q][g][0][1], bfr[q][g][0][2], pp);
-                    pp = mma_step<Q8>(a1, bfr[q][g][1][0], bfr[q][g][1][1], bfr[q][g][1][2], pp);
+            for (int q = 0; q < kOutPairs; q++) {
+                AFrag a0, a1;
+                decode_pair<Q8>(raw[v][q], a0, a1);
 #pragma unroll
-                    for (int i = 0; i < 4; i++) acc3[g][0][i] = __builtin_fmaf(pp[i], sc[q][i], acc3[g][0][i]);
-                } else {
+                for (int g = 0; g < G; g++) {
+                    if (g >= ng) continue;
+                    if (grp) {
+                        f32x4 pp{0, 0, 0, 0};
+                        pp = mma_step<Q8>(a0, bfr[v][q][g][0][0], bfr[v][q][g][0][1], bfr[v][q][g][0][2], pp);
+                        pp = mma_step<Q8>(a1, bfr[v][q][g][1][0], bfr[v][q][g][1][1], bfr[v][q][g][1][2], pp);
 #pragma unroll
-                    for (int h = 0; h < 2; h++) {
-                        const AFrag& af = h ? a1 : a0;
-                        const bf16x8* bb = bfr[q][g][h];
-                        if (Q8) {
-                            acc3[g][0] = mma(af.h, bb[0], acc3[g][0]);
-                            acc3[g][1] = mma(af.h, bb[1], acc3[g][1]);
-                            acc3[g][2] = mma(af.h, bb[2], acc3[g][2]);
-                        } else {
-                            acc3[g][0] = mma(af.h, bb[0], acc3[g][0]);
-                            acc3[g][1] = mma(af.h, bb[1], acc3[g][1]);
-                            acc3[g][1] = mma(af.m, bb[0], acc3[g][1]);
-                            acc3[g][2] = mma(af.h, bb[2], acc3[g][2]);
-                            acc3[g][2] = mma(af.m, bb[1], acc3[g][2]);
-                            acc3[g][2] = mma(af.l, bb[0], acc3[g][2]);
+                        for (int i = 0; i < 4; i++) acc3[g][0][i] = __builtin_fmaf(pp[i], sc[v][q][i], acc3[g][0][i]);
+                    } else {
+#pragma unroll
+                        for (int h = 0; h < 2; h++) {
+                            const AFrag& af = h ? a1 : a0;
+                            const bf16x8* bb = bfr[v][q][g][h];
+                            if (Q8) {
+                                acc3[g][0] = mma(af.h, bb[0], acc3[g][0]);
+                                acc3[g][1] = mma(af.h, bb[1], acc3[g][1]);
+                                acc3[g][2] = mma(af.h, bb[2], acc3[g][2]);
+                            } else {
+                                acc3[g][0] = mma(af.h, bb[0], acc3[g][0]);
+                                acc3[g][1] = mma(af.h, bb[1], acc3[g][1]);
+                                acc3[g][1] = mma(af.m, bb[0], acc3[g][1]);
+                                acc3[g][2] = mma(af.h, bb[2], acc3[g][2]);
+                                acc3[g][2] = mma(af.m, bb[1], acc3[g][2]);
+                                acc3[g][2] = mma(af.l, bb[0], acc3[g][2]);
+                            }
                         }
                     }
                 }
             }
         }
     } else {
+    f32x4 (&acc3)[G][3] = acc3v[0];
     // Epilogue operands of wave 0, requested with the rest.
     if (wave == 0) {
 #pragma unroll
@@ -1438,19 +1575,25 @@ __global__ __launch_bounds__(kOutWaves * kWave) void k_mix_out(MixOutArgs a) {
         }
     }
     }
-    f32x4 acc[G];
+    f32x4 acc[VW][G];
 #pragma unroll
-    for (int g = 0; g < G; g++) acc[g] = (acc3[g][0] + acc3[g][1]) + acc3[g][2];
-    if (wave > 0) {
+    for (int v = 0; v < VW; v++)
 #pragma unroll
-        for (int g = 0; g < G; g++) part[wave - 1][g][lane] = acc[g];
+        for (int g = 0; g < G; g++) acc[v][g] = (acc3v[v][g][0] + acc3v[v][g][1]) + acc3v[v][g][2];
+#pragma unroll
+    for (int v = 0; v < VW; v++) {
+        const int vw = wave + WAVES * v;
+        if (vw > 0) {
+#pragma unroll
+            for (int g = 0; g < G; g++) part[vw - 1][g][lane] = acc[v][g];
+        }
     }
     __syncthreads();
     if (wave != 0) return;
 #pragma unroll
     for (int g = 0; g < G; g++) {
         if (g >= ng) continue;
-        f32x4 s = acc[g];
+        f32x4 s = acc[0][g];
         for (int q = 0; q < kOutWaves - 1; q++) s = s + part[q][g][lane];
         const uint32_t b = b0 + g * kRowTile + lane % 16;
         const bool ok = b < a.n && r0 < a.d;
@@ -1459,6 +1602,11 @@ __global__ __launch_bounds__(kOutWaves * kWave) void k_mix_out(MixOutArgs a) {
         if (ok) *(float4*)(a.x + (size_t)b * a.d + r0) = make_float4(nx[0], nx[1], nx[2], nx[3]);
         if (a.xw != nullptr) produce_tile(a.xw, a.ssp, a.ks_x, a.tiles, t, b, ok, nx, w4);
     }
+}
+
+template <bool Q8, int G, bool FIXED>
+__global__ __launch_bounds__(kOutWaves * kWave) void k_mix_out(MixOutArgs a) {
+    mix_out_body<Q8, G, FIXED, kOutWaves>(a, blockIdx.x, blockIdx.y, NoWait{});
 }
 
 // ---------------------------------------------------------------- k_head
