@@ -152,8 +152,10 @@ int32_t redukt_backend_forward_batch_device_noalloc(uint32_t n_streams, const ui
                                                     const uint32_t* d_tokens, float* d_out, uint32_t vocab_size,
                                                     uint32_t flags);
 
-/* Wait for queued work; returns OK, or INVALID_ARGUMENT if a device-side check of
- * forward_batch_device failed since the last call (the flag is then cleared). */
+/* Wait for queued work; returns OK, INVALID_ARGUMENT if a device-side check of
+ * forward_batch_device failed since the last call, or FORWARD_FAILED if the persistent
+ * step kernel gave up waiting for a phase or ran on an XCD it was not planned for (its
+ * outputs are then not to be used); the flag is cleared either way. */
 int32_t redukt_backend_device_status(void);
 
 /* The hipStream_t every kernel of the library is launched on, as an opaque pointer,
@@ -166,7 +168,10 @@ void* redukt_backend_stream(void);
  * 2 mix_in (norm + in_proj + conv + x_proj partials), 3 scan (dt_proj + selective scan +
  * gate), 4 mix_out (out_proj + residual), 5 head (final norm + LM head), 6 softmax;
  * RWKV-7: 7 shift (LayerNorm + token shift), 8 proj (matrix-core projections), 9 wkv (WKV-7
- * with GroupNorm, bonus and gate), plus 1, 5, 6.
+ * with GroupNorm, bonus and gate), plus 1, 5, 6.  Class 10 is the persistent step kernel
+ * (every layer of a Mamba step in one cooperative launch, where REDUKT_GPU_FLOW enables it):
+ * its launch is bracketed by an event pair recorded on the library's stream, and
+ * REDUKT_PROBE_CLASS_ONLY does not apply to it (the step runs whole).
  * Probed launches record their own dispatch start and stop (hipExtLaunchKernel), and
  * probed steps are launched kernel by kernel instead of from the step's hipGraph.
  * With REDUKT_PROBE_CLASS_ONLY or'ed into kernel_class, a probed step launches only the

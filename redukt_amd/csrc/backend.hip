@@ -814,6 +814,13 @@ uint32_t env_split() {
     return (uint32_t)strtoul(e, nullptr, 10);
 }
 
+// REDUKT_GPU_FLOW: smallest step (streams) that runs the persistent step kernel; 0 never.
+uint32_t env_flow_from() {
+    const char* e = getenv("REDUKT_GPU_FLOW");
+    if (!e || !*e) return kDefaultFlowFrom;
+    return (uint32_t)strtoul(e, nullptr, 10);
+}
+
 // REDUKT_GPU_PART_MIN: fewest streams per part.
 uint32_t env_part_min() {
     const char* e = getenv("REDUKT_GPU_PART_MIN");
@@ -898,6 +905,7 @@ int init_common(const uint8_t* weights_path, int32_t device_id, uint32_t profile
     (void)noalloc_setup(G.device);  // a failure only disables the allocation-free entry point
     G.profile = profile;
     G.runner.set_split(env_split(), env_part_min());
+    G.runner.set_flow(env_flow_from());
     G.kind = file_kind(path);
     if (G.kind == kKindRwkv && (profile & BACKEND_PROFILE_GEMV)) {
         log("the wavefront-GEMV tier serves Mamba models only");
@@ -1081,7 +1089,9 @@ int32_t redukt_backend_device_status(void) {
     if (err) {
         const uint32_t zero = 0;
         if (hipMemcpy(G.d_err, &zero, sizeof(zero), hipMemcpyHostToDevice) != hipSuccess) return BACKEND_FORWARD_FAILED;
-        return BACKEND_INVALID_ARGUMENT;
+        // bits 0-1: a bad slot or token, a repeated slot; above: the persistent step
+        // kernel gave up waiting for a phase or ran on an unexpected XCD
+        return (err & ~3u) ? BACKEND_FORWARD_FAILED : BACKEND_INVALID_ARGUMENT;
     }
     return BACKEND_OK;
 }

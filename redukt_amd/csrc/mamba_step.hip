@@ -33,6 +33,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <memory>
@@ -100,6 +101,7 @@ constexpr int kMaxXr = kMaxDr + 32;        // x_proj rows
 constexpr int kMaxNxb = 64;                // x_proj split-K blocks, d_inner / 32 (d_inner <= 2048)
 constexpr int kOutWaves = 8;               // waves of k_mix_out
 constexpr int kOutPairs = 3;               // k-pairs per k_mix_out wave per pass
+constexpr int kInFixedPairs = 3;           // k_mix_in's fixed shape: three k-pairs per wave (d = 768)
 static_assert(kSlotWordAlign % kInChunk == 0, "k_mix_in reads its chunk's slot words whole");
 
 // Raw buffer access: a descriptor with a uniform base and an exact byte size (gfx9 word 3:
@@ -140,17 +142,21 @@ __device__ __forceinline__ bf16x8 as_frag(int4 v) { return __builtin_bit_cast(bf
 // complete when it started) or as a task of the persistent step kernel (FlowWait).  There
 // the previous phase's outputs are written during the same launch by other CUs of the
 // same XCD: the task first requests everything that does not depend on them (weights,
-// scales, recurrent state), then waits for the phase counter, then reads those outputs
-// past its CU's L1 (sc0, kAux), from the XCD's L2 where they were written.
+// scales, recurrent state), then waits for the phase counter, invalidates its CU's L1
+// and reads those outputs (sc0, kAux) from the XCD's L2, where they were written.  The
+// producers' stores were complete (s_waitcnt) before the counter was raised, and the
+// counter is read with device-scope atomics.
 struct NoWait {
     static constexpr bool kFlow = false;
     static constexpr int kAux = kCached;
     __device__ __forceinline__ void wait() const {}
 };
 
-// Spins of a wait before it gives up: a task that waits this long (tens of ms, far past
-// any phase) sets bit 2 of the error word and goes on, so every wave still exits.
-constexpr uint32_t kFlowSpinMax = 1u << 20;
+// Polls of a wait before it gives up (each about a microsecond: 0.1 s or more, far past
+// any phase of a step of at most kFlowMaxStreams streams): the task then sets bit 2 of the
+// error word and goes on, and every later wait of the launch that finds the bit set gives
+// up within 1024 polls, so every wave exits soon after a first failure.
+constexpr uint32_t kFlowSpinMax = 1u << 17;
 constexpr int kL1Bypass = 1;   // sc0: the load misses the CU's L1 and reads the XCD's L2
 
 struct FlowWait {
@@ -164,13 +170,21 @@ struct FlowWait {
             uint32_t spins = 0;
             while (__hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
                 __builtin_amdgcn_s_sleep(1);
-                if (++spins > kFlowSpinMax) {
+                if ((++spins & 1023u) == 0 &&
+                    (spins > kFlowSpinMax || (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & 4u))) {
                     atomicOr(err, 4u);
                     break;
                 }
             }
         }
         __syncthreads();
+        // Lines of the previous phase's outputs that this CU read in an earlier layer (or
+        // that share a 128-byte line with them) must not be served from L1: invalidate
+        // the CU's L1 (work-group scope; the L2 keeps its lines, device scope would write
+        // back and drop the XCD's L2 and costs twice the step time).  Every earlier read
+        // of those lines has completed (each phase waited for the whole previous one), so
+        // no stale fill can land after this.
+        if (counter != nullptr) asm volatile("buffer_inv sc0" ::: "memory");
     }
 };
 
@@ -652,6 +666,8 @@ struct EmbedArgs {
     uint32_t* err;
     const uint32_t* slots_all; // the whole step's slots (the check covers every part)
     uint32_t n_all, b_off;     // streams of the whole step; this part's first row in it
+    uint32_t* zero;            // counters of the persistent step kernel to clear (or null):
+    uint32_t zero_n, zero_stride;  // zero[i * zero_stride] for i < zero_n
     const float* nw0;          // layer 0 norm weight; with xw != null the pre-staged
     __bf16* xw;                // activations of layer 0 are produced here
     float* ssp;
@@ -693,6 +709,8 @@ __global__ __launch_bounds__(kBlock) void k_embed(EmbedArgs a) {
             a.slots[b] = clamp_slot(s, a.cap);
         }
     }
+    if (a.zero != nullptr && blockIdx.x == 0)
+        for (uint32_t i = b * kBlock + threadIdx.x; i < a.zero_n; i += a.n * kBlock) a.zero[(size_t)i * a.zero_stride] = 0u;
     if (tok >= (uint32_t)a.emb.rows) tok = a.emb.rows - 1;
     const int k = 4 * (blockIdx.x * kBlock + threadIdx.x);
     const bool live = k < d;
@@ -1609,6 +1627,116 @@ __global__ __launch_bounds__(kOutWaves * kWave) void k_mix_out(MixOutArgs a) {
     mix_out_body<Q8, G, FIXED, kOutWaves>(a, blockIdx.x, blockIdx.y, NoWait{});
 }
 
+// ---------------------------------------------------------------- persistent step kernel
+
+// All layers of a step in one cooperative launch (int8 per-row weights, the Mamba-130M
+// shape).  Stream group g's every task runs on XCD g % nx (the XCD a workgroup runs on is
+// read from the hardware), so whatever one phase of a group hands to the next (activation
+// tiles and RMS partials, u, z, x_proj partials, gated tiles, the residual) is written to
+// and read from that XCD's L2.  XCD x's list is ordered by layer, then phase (in_proj,
+// scan, out_proj), then group, then the task's tile; its workgroups take the tasks in
+// list order from a ticket counter.  Every task depends only on tasks earlier in the list
+// (the previous phase of its group), and every workgroup is resident (cooperative
+// launch), so the earliest unfinished task always has its inputs and the list advances.  A task's body requests its
+// weights, scales and recurrent state, waits until the counter of the phase it reads
+// reaches that phase's task count, then reads those outputs past L1; after its stores it
+// adds one to its own phase's counter.  The bodies are the stand-alone kernels' (same
+// tiles, k-splits and orders), so a stream's bits do not depend on which path ran it.
+constexpr uint32_t kFlowCounterStride = 32;   // words between counters (one 128-byte line each)
+constexpr uint32_t kFlowMaxStreams = 4096;    // largest step the kernel serves (bounds every wait)
+constexpr uint32_t kFlowScanSpt = 2;          // streams per scan task thread
+
+struct FlowLayer {
+    MixInArgs mi;
+    ScanArgs sc;
+    MixOutArgs mo;
+};
+
+struct FlowArgs {
+    const FlowLayer* layers;  // [nl], device memory, read through the scalar unit
+    uint32_t nl, groups;
+    uint32_t* cnt;            // [nl][3][groups] phase counters, then [nx] task tickets, kFlowCounterStride words apart
+    uint32_t* err;
+    uint32_t mi_tasks, cb, mo_tasks;  // in_proj row blocks, scan channel blocks, out_proj row tiles (per group)
+    uint32_t nx;              // XCDs of the device
+    uint8_t xmap[16];         // XCC_ID -> XCD index 0 .. nx - 1 (0xff: not seen when the grid was planned)
+};
+
+// The XCD this wave runs on (hardware register XCC_ID, bits 3:0).
+__device__ __forceinline__ uint32_t xcc_id() { return __builtin_amdgcn_s_getreg(20 | (0 << 6) | (3 << 11)) & 0xfu; }
+
+// Workgroup w writes its XCC_ID to map[w]: the host learns the device's XCDs from one
+// launch of the persistent kernel's grid.
+__global__ __launch_bounds__(kBlock) void k_xcc_map(uint32_t* map) {
+    if (threadIdx.x == 0) map[blockIdx.x] = xcc_id();
+}
+
+// Which workgroup runs a task is decided at run time: the workgroups of XCD x take the
+// tasks of x's list in order from x's ticket counter (one device-scope atomic per task,
+// requested a task ahead).  The hardware deals workgroups to XCDs round-robin from where
+// the previous dispatch stopped, so the block index does not name the XCD; the ticket
+// order keeps every dependency on an earlier ticket, taken by a resident workgroup.
+template <bool Q8S, bool FAST>
+__global__ __launch_bounds__(kBlock, 2) void k_flow(FlowArgs f) {
+    __shared__ uint32_t s_next;
+    const uint32_t x = f.xmap[xcc_id()];
+    if (x >= f.nx) {
+        if (threadIdx.x == 0) atomicOr(f.err, 8u);
+        return;
+    }
+    const uint32_t ng = x < f.groups ? (f.groups - x + f.nx - 1) / f.nx : 0u;  // groups of this XCD
+    constexpr uint32_t kSpt = kFlowScanSpt;
+    const uint32_t mi = f.mi_tasks, sc = kRowTile / kSpt * f.cb, mo = f.mo_tasks;
+    const uint32_t per_layer = ng * (mi + sc + mo);
+    const uint32_t total = per_layer * f.nl;
+    uint32_t* const ticket = f.cnt + ((size_t)f.nl * 3 * f.groups + x) * kFlowCounterStride;
+    typedef const __attribute__((address_space(4))) FlowLayer* FlowLayerK;
+    const FlowLayerK layers = (FlowLayerK)f.layers;
+    if (threadIdx.x == 0) s_next = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    for (uint32_t i = s_next; i < total;) {
+        uint32_t ahead = 0;
+        if (threadIdx.x == 0) ahead = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t l = i / per_layer;
+        uint32_t r = i % per_layer;
+        uint32_t phase, gi, task;
+        if (r < ng * mi) {
+            phase = 0, gi = r / mi, task = r % mi;
+        } else if ((r -= ng * mi) < ng * sc) {
+            phase = 1, gi = r / sc, task = r % sc;
+        } else {
+            r -= ng * sc;
+            phase = 2, gi = r / mo, task = r % mo;
+        }
+        const uint32_t g = x + f.nx * gi;
+        auto counter = [&](uint32_t ll, uint32_t ph) {
+            return f.cnt + ((size_t)(ll * 3 + ph) * f.groups + g) * kFlowCounterStride;
+        };
+        const FlowLayer& L = *(const FlowLayer*)(layers + l);
+        if (phase == 0) {
+            const FlowWait w{l > 0 ? counter(l - 1, 2) : nullptr, mo, f.err};
+            mix_in_body<true, Q8S, true, false, kInFixedPairs, 4>(L.mi, task, g, w);
+        } else if (phase == 1) {
+            // kSpt streams per task: the tasks of streams past n (a last, partial group) only count
+            const uint32_t sy = g * (kRowTile / kSpt) + task / f.cb;
+            const FlowWait w{counter(l, 0), mi, f.err};
+            if (sy * kSpt < L.sc.n) scan_body<Q8S, FAST, 48, 48, kSpt>(L.sc, sy, task % f.cb, w);
+        } else {
+            const FlowWait w{counter(l, 1), sc, f.err};
+            mix_out_body<true, 1, true, kWaves>(L.mo, task, g, w);
+        }
+        // every store of the task has reached L2 before the counter says so
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            __hip_atomic_fetch_add(counter(l, phase), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            s_next = ahead;
+        }
+        __syncthreads();
+        i = s_next;
+    }
+}
+
 // ---------------------------------------------------------------- k_head
 
 struct HeadArgs {
@@ -1981,9 +2109,6 @@ const void* mix_in_fn6(uint32_t lds) {
     return (const void*)k_mix_in<Q8, Q8XP, PRE, GRP, QP, T>;
 }
 
-// Three k-pairs per wave (d = 768, Mamba-130M) is compiled as a fixed shape.
-constexpr int kInFixedPairs = 3;
-
 // The fixed shape and four-tile blocks are compiled for the pre-staged (RMSNorm) path,
 // where the activations go straight to registers; the LayerNorm path keeps the general
 // two-tile kernel.
@@ -2051,7 +2176,7 @@ Launch embed_launch(const TMat& emb, Pool& p, const StepIO& io, const float* nw0
     const int d = emb.cols;
     const uint32_t n_all = io.n_all ? io.n_all : io.n;
     EmbedArgs ea{emb, p.x, io.tokens + io.b0, io.slots + io.b0, p.slots, io.n, p.cap, io.check ? 1 : 0, io.err,
-                 io.slots, n_all, io.b0, nw0, xw, ssp, ks_x, tiles};
+                 io.slots, n_all, io.b0, nullptr, 0, 0, nw0, xw, ssp, ks_x, tiles};
     return Launch::make((const void*)k_embed, dim3((d + 4 * kBlock - 1) / (4 * kBlock), io.n), dim3(kBlock), 0, KC_EMBED,
                         ea);
 }
@@ -2076,13 +2201,23 @@ Launch head_launch(const TMat& H, Pool& p, const StepIO& io, const float* x, con
                         dim3(kHeadWaves * kWave), lds_h, KC_HEAD, ha);
 }
 
-Launch scan_launch(const DLayer& L, const Dims& D, Pool& p, uint32_t n, bool exact, __bf16* glimb, float* g32,
+namespace {
+
+ScanArgs scan_args(const DLayer& L, const Dims& D, const Pool& p, uint32_t n, __bf16* glimb, float* g32,
                    float* ssm_layer) {
     const int di = (int)D.di, nxp = di / kXpBlock;
     const int xr_pad = L.x_proj.rt * kRowTile;
+    return ScanArgs{p.xpart, nxp, xr_pad, (int)D.xr(), p.u, p.z, ssm_layer, L.dt_w, L.dt_q, L.dt_scales, L.dt_pad,
+                    L.dt_b, L.a_exp, L.d_vec, p.slots, p.xcap, n, p.scap, glimb, g32, di, (int)D.dr};
+}
+
+}  // namespace
+
+Launch scan_launch(const DLayer& L, const Dims& D, Pool& p, uint32_t n, bool exact, __bf16* glimb, float* g32,
+                   float* ssm_layer) {
+    const int di = (int)D.di, nxp = di / kXpBlock;
     const uint32_t spt = scan_spt(n);
-    ScanArgs sa{p.xpart, nxp, xr_pad, (int)D.xr(), p.u, p.z, ssm_layer, L.dt_w, L.dt_q, L.dt_scales, L.dt_pad, L.dt_b,
-                L.a_exp, L.d_vec, p.slots, p.xcap, n, p.scap, glimb, g32, di, (int)D.dr};
+    const ScanArgs sa = scan_args(L, D, p, n, glimb, g32, ssm_layer);
     const void* fs = scan_fn(L.dt_q != nullptr, !exact, (int)D.dr, nxp, spt);
     return Launch::make(fs, dim3(xcd_grid((di + kBlock - 1) / kBlock, (n + spt - 1) / spt)), dim3(kBlock), 0, KC_SCAN,
                         sa);
@@ -2115,6 +2250,25 @@ Pool part_view(const Pool& p, const Dims& D, int ks_x, int xr_pad, uint32_t b0) 
     return q;
 }
 
+// The arguments of layer li's three kernels for a step of n streams on the scratch of p
+// (the per-layer kernels and the persistent kernel's tasks take the same ones).
+FlowLayer layer_args(const ModelView& m, const Pool& p, uint32_t n, uint32_t li, int nxb) {
+    const Dims& D = *m.dims;
+    const DLayer& L = m.layers[li];
+    const int d = (int)D.d, di = (int)D.di;
+    const bool pre = m.layers[0].norm_b == nullptr && m.norm_f_b == nullptr;
+    const int xr_pad = m.layers[0].x_proj.rt * kRowTile;
+    const int ks_x = m.layers[0].in_x.ks, tiles = d / kRowTile;
+    const size_t conv_layer = (size_t)p.scap * di * (D.dc - 1);
+    const size_t ssm_layer = (size_t)p.scap * di * 16;
+    const float* nw_next = li + 1 < D.nl ? m.layers[li + 1].norm_w : m.norm_f_w;
+    return FlowLayer{
+        MixInArgs{p.x, L.norm_w, L.norm_b, L.in_x, L.in_z, L.x_proj, nxb, p.conv + li * conv_layer, L.conv_w, L.conv_b,
+                  p.slots, p.xcap, n, p.scap, p.u, p.z, p.xpart, di, (int)D.dc, d, xr_pad, p.xw, p.ssp, tiles},
+        scan_args(L, D, p, n, p.glimb, nullptr, p.ssm + li * ssm_layer),
+        MixOutArgs{L.out_proj, p.glimb, p.x, n, d, nw_next, pre ? p.xw : nullptr, p.ssp, ks_x, tiles}};
+}
+
 void build_step(const ModelView& m, Pool& pool, const StepIO& io, std::vector<Launch>& out, int& io_index,
                 int& head_index, int& softmax_index) {
     const Dims& D = *m.dims;
@@ -2124,7 +2278,6 @@ void build_step(const ModelView& m, Pool& pool, const StepIO& io, std::vector<La
     const uint32_t in_chunks = (n + kInChunk - 1) / kInChunk;
     const int out_g = m.layers[0].out_proj.group == 0 && n >= (uint32_t)kOutWideFrom ? 2 : 1;
     const uint32_t out_chunks = (n + out_g * kRowTile - 1) / (out_g * kRowTile);
-    const int xr_pad = m.layers[0].x_proj.rt * kRowTile;
     out.clear();
     // RMSNorm models take the pre-staged activation path; LayerNorm models norm in the
     // consumer.
@@ -2138,26 +2291,21 @@ void build_step(const ModelView& m, Pool& pool, const StepIO& io, std::vector<La
     const int ks_x = m.layers[0].in_x.ks, tiles = d / kRowTile;
     io_index = (int)out.size();
     out.push_back(embed_launch(*m.emb, p, io, m.layers[0].norm_w, pre ? p.xw : nullptr, p.ssp, ks_x, tiles));
-    const size_t conv_layer = (size_t)p.scap * di * (D.dc - 1);
-    const size_t ssm_layer = (size_t)p.scap * di * 16;
     const bool q8 = m.layers[0].in_x.group != 0;
     const bool q8xp = m.layers[0].x_proj.group != 0;
     const uint32_t lds_in = mix_in_lds_bytes(ks_x, pre, in_tiles);
     const bool grp = q8 && m.layers[0].in_x.group != m.layers[0].in_x.cols;
     const bool fixed = ks_x == 2 * kWaves * kInFixedPairs && m.layers[0].in_z.ks == ks_x;
     const void* fin = mix_in_fn(q8, q8xp, pre, grp, fixed, in_tiles, lds_in);
+    const size_t ssm_layer = (size_t)p.scap * di * 16;
     for (uint32_t li = 0; li < D.nl; li++) {
         const DLayer& L = m.layers[li];
-        MixInArgs ma{p.x, L.norm_w, L.norm_b, L.in_x, L.in_z, L.x_proj, nxb, p.conv + li * conv_layer,
-                     L.conv_w, L.conv_b, p.slots, p.xcap, n, p.scap, p.u, p.z, p.xpart, di, (int)D.dc, d, xr_pad,
-                     p.xw, p.ssp, tiles};
+        const FlowLayer la = layer_args(m, p, n, li, nxb);
         const int zb = L.in_z.rt / in_tiles;
-        out.push_back(Launch::make(fin, dim3(nxb + zb, in_chunks), dim3(kBlock), lds_in, KC_MIX_IN, ma));
+        out.push_back(Launch::make(fin, dim3(nxb + zb, in_chunks), dim3(kBlock), lds_in, KC_MIX_IN, la.mi));
         out.push_back(scan_launch(L, D, p, n, m.exact_scan, p.glimb, nullptr, p.ssm + li * ssm_layer));
-        const float* nw_next = li + 1 < D.nl ? m.layers[li + 1].norm_w : m.norm_f_w;
-        MixOutArgs oa{L.out_proj, p.glimb, p.x, n, d, nw_next, pre ? p.xw : nullptr, p.ssp, ks_x, tiles};
         const void* fo = mix_out_fn(q8, out_g, m.layers[0].out_proj.ks == 2 * kOutWaves * kOutPairs);
-        out.push_back(Launch::make(fo, dim3(L.out_proj.rt, out_chunks), dim3(kOutWaves * kWave), 0, KC_MIX_OUT, oa));
+        out.push_back(Launch::make(fo, dim3(L.out_proj.rt, out_chunks), dim3(kOutWaves * kWave), 0, KC_MIX_OUT, la.mo));
     }
     const TMat& H = *m.head;
     head_index = (int)out.size();
@@ -2172,6 +2320,7 @@ void build_step(const ModelView& m, Pool& pool, const StepIO& io, std::vector<La
 
 hipError_t launch_direct(const Launch& l, hipStream_t st) {
     void* params[] = {l.argp};
+    if (l.coop) return hipLaunchCooperativeKernel(l.fn, l.grid, l.block, params, l.lds, st);
     return hipLaunchKernel(l.fn, l.grid, l.block, params, l.lds, st);
 }
 
@@ -2224,6 +2373,9 @@ StepRunner& StepRunner::operator=(StepRunner&& o) noexcept {
     release();
     graphs_ = std::move(o.graphs_);
     o.graphs_.clear();
+    plans_ = std::move(o.plans_);
+    o.plans_.clear();
+    flow_from_ = o.flow_from_;
     direct_ = std::move(o.direct_);
     o.direct_.clear();
     clock_ = o.clock_;
@@ -2259,6 +2411,41 @@ void StepRunner::destroy(Graph& g) {
 void StepRunner::clear() {
     for (Graph& g : graphs_) destroy(g);
     graphs_.clear();
+    for (FlowPlan& f : plans_)
+        if (f.dev) (void)hipFree(f.dev);
+    plans_.clear();
+}
+
+// The persistent kernel's arguments for (p, n), made on first use (at most 8 kept, the
+// least recently used evicted once the stream has finished with it).  out->shape.grid == 0
+// when the kernel cannot run on this device.
+hipError_t StepRunner::flow_plan(const StepSource& src, Pool& p, uint32_t n, size_t bytes, hipStream_t st,
+                                 FlowPlan*& out) {
+    out = nullptr;
+    for (FlowPlan& f : plans_)
+        if (f.pool == &p && f.n == n) out = &f;
+    if (!out) {
+        if (plans_.size() >= 8) {
+            auto old = std::min_element(plans_.begin(), plans_.end(),
+                                        [](const FlowPlan& a, const FlowPlan& b) { return a.last_use < b.last_use; });
+            RDK_TRY(hipStreamSynchronize(st));
+            if (old->dev) RDK_TRY(hipFree(old->dev));
+            plans_.erase(old);
+        }
+        FlowPlan f;
+        f.pool = &p;
+        f.n = n;
+        RDK_TRY(hipMalloc(&f.dev, bytes));
+        const hipError_t e = src.flow_init(p, n, f.dev, &f.shape, st);
+        if (e != hipSuccess) {
+            (void)hipFree(f.dev);
+            return e;
+        }
+        plans_.push_back(f);
+        out = &plans_.back();
+    }
+    out->last_use = ++clock_;
+    return hipSuccess;
 }
 
 uint32_t StepRunner::parts_of(uint32_t n, uint32_t k, uint32_t* b0, uint32_t* cnt) {
@@ -2331,6 +2518,120 @@ void MambaStep::build(Pool& p, const StepIO& io, std::vector<Launch>& out, int& 
     build_step(m, p, io, out, io_i, head_i, sm_i);
 }
 
+// ---------------------------------------------------------------- persistent step kernel (host)
+
+namespace {
+
+// The shapes k_flow is compiled for: RMSNorm, int8 per-row in_proj and out_proj, x_proj
+// and dt_proj both int8 per-row or both F32, d = 768 (k_mix_in's fixed shape),
+// d_inner = 1536 (k_mix_out's fixed shape), dt_rank 48 and 48 x_proj blocks (the scan's).
+bool flow_fits(const ModelView& m) {
+    const Dims& D = *m.dims;
+    const DLayer& L = m.layers[0];
+    const bool pre = L.norm_b == nullptr && m.norm_f_b == nullptr;
+    const bool row = [](const TMat& w) { return w.group != 0 && w.group == w.cols; }(L.in_x);
+    const bool q8s = L.x_proj.group != 0;
+    return pre && row && L.in_z.group == L.in_z.cols && L.out_proj.group == L.out_proj.cols &&
+           (!q8s || L.x_proj.group == L.x_proj.cols) && q8s == (L.dt_q != nullptr) &&
+           L.in_x.ks == 2 * kWaves * kInFixedPairs && L.in_z.ks == L.in_x.ks &&
+           L.out_proj.ks == 2 * kOutWaves * kOutPairs && D.dr == 48 && D.di / kXpBlock == 48 &&
+           D.di % kBlock == 0 && L.in_x.rt % 4 == 0 && L.in_z.rt % 4 == 0;
+}
+
+const void* flow_fn(const ModelView& m) {
+    const bool q8s = m.layers[0].x_proj.group != 0, fast = !m.exact_scan;
+    if (q8s) return fast ? (const void*)k_flow<true, true> : (const void*)k_flow<true, false>;
+    return fast ? (const void*)k_flow<false, true> : (const void*)k_flow<false, false>;
+}
+
+size_t flow_table_bytes(uint32_t nl) { return ((size_t)nl * sizeof(FlowLayer) + 255) & ~(size_t)255; }
+// Phase counters, then one task ticket per XCC_ID value.
+uint32_t flow_counters(uint32_t nl, uint32_t n) { return nl * 3u * ((n + kRowTile - 1) / kRowTile) + 16u; }
+
+// Workgroups per CU of the persistent kernel: REDUKT_GPU_FLOW_WGS, else one below 512
+// streams (a second workgroup on a CU slows both: 0.87 vs 1.10 ms per step at 128
+// streams) and two from there (3.2 vs 5.0 ms at 1024), at most as many as fit.
+uint32_t flow_wgs_per_cu(uint32_t fit, uint32_t n) {
+    const char* e = getenv("REDUKT_GPU_FLOW_WGS");
+    const uint32_t want = e && *e ? (uint32_t)strtoul(e, nullptr, 10) : (n < 512 ? 1u : 2u);
+    return std::max(1u, std::min(want, fit));
+}
+
+}  // namespace
+
+size_t MambaStep::flow_bytes(const Pool& p, uint32_t n) const {
+    (void)p;
+    if (n == 0 || n > kFlowMaxStreams || !flow_fits(m)) return 0;
+    return flow_table_bytes(m.dims->nl) + (size_t)flow_counters(m.dims->nl, n) * kFlowCounterStride * 4;
+}
+
+hipError_t MambaStep::flow_init(Pool& p, uint32_t n, void* dev, FlowShape* shape, hipStream_t st) const {
+    *shape = FlowShape{};
+    const Dims& D = *m.dims;
+    const void* fn = flow_fn(m);
+    const uint32_t lds = mix_in_lds_bytes(m.layers[0].in_x.ks, true, 4);
+    RDK_TRY(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    int fit = 0, cus = 0, dev_id = 0;
+    RDK_TRY(hipGetDevice(&dev_id));
+    RDK_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev_id));
+    RDK_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(&fit, fn, kBlock, lds));
+    if (fit < 1 || cus < (int)kXcds || cus % kXcds != 0) {
+        fprintf(stderr, "[redukt-gpu-hip] persistent step kernel off: %d workgroups per CU fit, %d CUs\n", fit, cus);
+        return hipSuccess;
+    }
+    const uint32_t g = flow_wgs_per_cu((uint32_t)fit, n) * (uint32_t)cus;
+    // The device's XCDs, from one launch of the grid: the map goes to the counter area
+    // (at least nl * 3 * 32 >= g words; the step's embedding clears it before every use).
+    uint32_t* map = (uint32_t*)((unsigned char*)dev + flow_table_bytes(D.nl));
+    if ((size_t)flow_counters(D.nl, n) * kFlowCounterStride < g) return hipSuccess;
+    void* params[] = {&map};
+    RDK_TRY(hipLaunchCooperativeKernel((const void*)k_xcc_map, dim3(g), dim3(kBlock), params, 0, st));
+    RDK_TRY(hipStreamSynchronize(st));
+    std::vector<uint32_t> seen(g);
+    RDK_TRY(hipMemcpy(seen.data(), map, g * sizeof(uint32_t), hipMemcpyDeviceToHost));
+    FlowShape sh;
+    memset(sh.xmap, 0xff, sizeof(sh.xmap));
+    for (uint32_t w = 0; w < g; w++)
+        if (seen[w] < 16 && sh.xmap[seen[w]] == 0xff) sh.xmap[seen[w]] = (uint8_t)sh.nx++;
+    // The per-layer argument table, for the whole step (one part).
+    const int nxb = (int)D.di / (kRowTile * 4);
+    std::vector<FlowLayer> table;
+    table.reserve(D.nl);
+    for (uint32_t li = 0; li < D.nl; li++) table.push_back(layer_args(m, p, n, li, nxb));
+    RDK_TRY(hipMemcpy(dev, table.data(), table.size() * sizeof(FlowLayer), hipMemcpyHostToDevice));
+    sh.grid = g;
+    *shape = sh;
+    fprintf(stderr, "[redukt-gpu-hip] persistent step kernel: %u streams, %u workgroups on %u XCDs\n", n, g, sh.nx);
+    return hipSuccess;
+}
+
+void MambaStep::build_flow(Pool& p, const StepIO& io, void* dev, const FlowShape& shape, std::vector<Launch>& out) const {
+    const Dims& D = *m.dims;
+    const uint32_t n = io.n;
+    const int d = (int)D.d, tiles = d / kRowTile, ks_x = m.layers[0].in_x.ks;
+    const uint32_t groups = (n + kRowTile - 1) / kRowTile;
+    uint32_t* cnt = (uint32_t*)((unsigned char*)dev + flow_table_bytes(D.nl));
+    out.clear();
+    Launch e = embed_launch(*m.emb, p, io, m.layers[0].norm_w, p.xw, p.ssp, ks_x, tiles);
+    EmbedArgs* ea = (EmbedArgs*)e.argp;
+    ea->zero = cnt;
+    ea->zero_n = flow_counters(D.nl, n);
+    ea->zero_stride = kFlowCounterStride;
+    out.push_back(std::move(e));
+    const DLayer& L0 = m.layers[0];
+    FlowArgs fa{(const FlowLayer*)dev, D.nl, groups, cnt, io.err,
+                (uint32_t)((int)D.di / (kRowTile * 4) + L0.in_z.rt / 4), D.di / kBlock, (uint32_t)L0.out_proj.rt,
+                shape.nx, {}};
+    memcpy(fa.xmap, shape.xmap, sizeof(fa.xmap));
+    Launch f = Launch::make(flow_fn(m), dim3(shape.grid), dim3(kBlock), mix_in_lds_bytes(ks_x, true, 4), KC_FLOW, fa);
+    f.coop = true;
+    out.push_back(std::move(f));
+    const TMat& H = *m.head;
+    const bool ws = H.group != 0 && H.group == H.cols && H.ks / 2 <= 12;
+    out.push_back(head_launch(H, p, io, p.x, m.norm_f_w, m.norm_f_b, p.xw, p.ssp, d, tiles, ws));
+    if (io.probs) out.push_back(softmax_launch(io.out, (int)D.vocab, n));
+}
+
 hipError_t StepRunner::run_direct(const StepSource& src, Pool& p, const StepIO& io, hipStream_t st) {
     int io_i = -1, head_i = -1, sm_i = -1;
     src.build(p, io, direct_, io_i, head_i, sm_i);
@@ -2339,7 +2640,27 @@ hipError_t StepRunner::run_direct(const StepSource& src, Pool& p, const StepIO& 
 }
 
 hipError_t StepRunner::run(const StepSource& src, Pool& p, const StepIO& io, hipStream_t st, Probe* probe) {
-    if (probe && probe->cls != KC_NONE) {
+    const bool probing = probe && probe->cls != KC_NONE;
+    if (flow_from_ && io.n >= flow_from_ && (!probing || probe->cls == KC_FLOW)) {
+        const size_t fb = src.flow_bytes(p, io.n);
+        FlowPlan* pl = nullptr;
+        if (fb) RDK_TRY(flow_plan(src, p, io.n, fb, st, pl));
+        if (pl && pl->shape.grid) {
+            src.build_flow(p, io, pl->dev, pl->shape, direct_);
+            for (const Launch& l : direct_) {
+                // A probe of the persistent kernel brackets its launch with events on st.
+                const bool on = probing && l.cls == KC_FLOW && probe->used + 2 <= probe->cap;
+                if (on) RDK_TRY(hipEventRecord(probe->ev[probe->used], st));
+                RDK_TRY(launch_direct(l, st));
+                if (on) {
+                    RDK_TRY(hipEventRecord(probe->ev[probe->used + 1], st));
+                    probe->used += 2;
+                }
+            }
+            return hipSuccess;
+        }
+    }
+    if (probing) {
         std::vector<Launch> seq;
         int io_i = -1, head_i = -1, sm_i = -1;
         src.build(p, io, seq, io_i, head_i, sm_i);

@@ -148,7 +148,9 @@ enum KernelClass : uint32_t {
     KC_NONE = 0, KC_EMBED = 1, KC_MIX_IN = 2, KC_SCAN = 3, KC_MIX_OUT = 4, KC_HEAD = 5, KC_SOFTMAX = 6,
     // RWKV-7: LayerNorm + token shift, matrix-core projections, WKV-7 (with GroupNorm, bonus, gate)
     KC_SHIFT = 7, KC_PROJ = 8, KC_WKV = 9,
-    KC_COUNT = 10
+    // the persistent step kernel (every layer of a Mamba step in one launch)
+    KC_FLOW = 10,
+    KC_COUNT = 11
 };
 
 // Measurement hook: while cls != KC_NONE, every launch of that class records its dispatch
@@ -229,6 +231,13 @@ struct StepIO {
 // recorded once as a hipGraph and replayed.
 struct Launch;
 
+// The persistent step kernel's launch on this device: grid (0: it does not run here) and
+// the device's XCDs, as XCC_ID -> index 0 .. nx - 1 (0xff where no workgroup was seen).
+struct FlowShape {
+    uint32_t grid = 0, nx = 0;
+    uint8_t xmap[16] = {};
+};
+
 // Builds the launch list of one step of a model; io_i / head_i / sm_i name the launches
 // whose arguments carry the caller's pointers (embedding, head, softmax; -1 if absent).
 struct StepSource {
@@ -237,6 +246,18 @@ struct StepSource {
                        int& sm_i) const = 0;
     // Whether build() accepts a part (io.b0 > 0 or io.n < io.n_all) of a step.
     virtual bool splittable() const { return false; }
+    // The persistent step kernel (all layers in one cooperative launch), where the source
+    // has one for steps of n streams: flow_bytes() > 0 is the size of its device
+    // arguments (per-layer table, phase counters, task tickets), flow_init() writes them
+    // into `dev` once per pool and n and returns the launch shape (grid 0: the kernel
+    // cannot run on this device; the step then takes build()), and build_flow() makes the
+    // step's launch list around it.
+    virtual size_t flow_bytes(const Pool&, uint32_t) const { return 0; }
+    virtual hipError_t flow_init(Pool&, uint32_t, void*, FlowShape* shape, hipStream_t) const {
+        *shape = FlowShape{};
+        return hipSuccess;
+    }
+    virtual void build_flow(Pool&, const StepIO&, void*, const FlowShape&, std::vector<Launch>&) const {}
 };
 
 struct MambaStep final : StepSource {
@@ -244,6 +265,9 @@ struct MambaStep final : StepSource {
     explicit MambaStep(const ModelView& v) : m(v) {}
     void build(Pool& p, const StepIO& io, std::vector<Launch>& out, int& io_i, int& head_i, int& sm_i) const override;
     bool splittable() const override { return true; }
+    size_t flow_bytes(const Pool& p, uint32_t n) const override;
+    hipError_t flow_init(Pool& p, uint32_t n, void* dev, FlowShape* shape, hipStream_t st) const override;
+    void build_flow(Pool& p, const StepIO& io, void* dev, const FlowShape& shape, std::vector<Launch>& out) const override;
 };
 
 // The Mamba step on the wavefront-GEMV kernels (weights in GMat layout).
@@ -282,6 +306,9 @@ constexpr uint32_t kMaxParts = 4;
 constexpr uint32_t kMinPartStreams = 64;
 // Parts per step by default (REDUKT_GPU_SPLIT overrides).
 constexpr uint32_t kDefaultSplit = 2;
+// Smallest step that runs the persistent step kernel by default (REDUKT_GPU_FLOW
+// overrides; 0 = never).
+constexpr uint32_t kDefaultFlowFrom = 0;
 
 class StepRunner {
 public:
@@ -310,6 +337,9 @@ public:
         min_part_ = min_part < 1 ? 1 : min_part;
     }
     uint32_t split() const { return split_; }
+    // Steps of at least `from` streams (0: none) whose source has a persistent step kernel
+    // run it (direct launches, one part) instead of the per-layer graphs.
+    void set_flow(uint32_t from) { flow_from_ = from; }
     // Rows [b0, b0 + n) of each part of a step of n streams split at most k ways.
     static uint32_t parts_of(uint32_t n, uint32_t k, uint32_t* b0, uint32_t* cnt);
 
@@ -338,10 +368,21 @@ private:
         uint64_t last_use = 0;
         bool updatable() const;
     };
+    // The persistent step kernel's device arguments for one pool and batch size.
+    struct FlowPlan {
+        const Pool* pool = nullptr;
+        uint32_t n = 0;
+        FlowShape shape;            // grid 0: the kernel cannot run here, use the graphs
+        void* dev = nullptr;
+        uint64_t last_use = 0;
+    };
     hipError_t capture(const std::vector<Launch>& seq, hipStream_t st, Part& pt);
     hipError_t streams_ready(hipStream_t st, uint32_t parts);
+    hipError_t flow_plan(const StepSource& src, Pool& p, uint32_t n, size_t bytes, hipStream_t st, FlowPlan*& out);
     void destroy(Graph& g);
     std::vector<Graph> graphs_;
+    std::vector<FlowPlan> plans_;
+    uint32_t flow_from_ = 0;
     uint64_t clock_ = 0;
     uint32_t split_ = 1, min_part_ = kMinPartStreams;
     hipStream_t aux_[kMaxParts] = {};        // aux_[k] runs part k (k >= 1)

@@ -17,6 +17,7 @@ struct Launch {
     dim3 grid, block;
     uint32_t lds;
     uint32_t cls;
+    bool coop = false;   // cooperative launch (every workgroup resident at once); never captured
     std::unique_ptr<unsigned char[]> args;
     void* argp;
     template <typename A>

@@ -51,6 +51,7 @@ MATH_FNS = {"exp": 0, "lane_exp": 1, "ln": 2, "softplus": 3, "lane_sigmoid": 4, 
 KERNEL_CLASSES = {"embed": 1, "mix_in": 2, "scan": 3, "mix_out": 4, "head": 5, "softmax": 6}
 RWKV_KERNEL_CLASSES = {"embed": 1, "shift": 7, "proj": 8, "wkv": 9, "head": 5, "softmax": 6}
 PROBE_CLASS_ONLY = 0x100
+KC_FLOW = 10  # the persistent step kernel (REDUKT_GPU_FLOW), probed without PROBE_CLASS_ONLY
 
 
 class BackendResult(enum.IntEnum):
