@@ -485,16 +485,18 @@ void dev_free_all() {
 }
 
 // Outputs reach host memory in rounds of up to kOutRoundBytes through a pinned buffer:
-// every chunk of a round is copied D2H at once, each with its own event, and the host
-// threads of copy_pool() move each chunk into the caller's buffer as soon as its DMA ends.
-// A round is cut into two chunks (at least kOutChunkBytes each): each D2H copy costs about
-// 8 us on top of its bytes (53 GB/s pinned), so the second chunk's DMA hides the first
-// chunk's host copy without paying that cost many times (6.4 MB: one copy 120 us, seven
-// 1 MB copies 175 us).
-constexpr size_t kOutChunkBytes = (size_t)1 << 20;
-constexpr size_t kOutChunksPerRound = 2;
+// every chunk of a round is copied D2H at once, each with its own event, and all the host
+// threads of copy_pool() move each chunk into the caller's buffer, a slice each, as soon as
+// its DMA ends, while the next chunk's DMA runs.  Each D2H copy costs about 8 us on top of
+// its bytes (53 GB/s pinned; 6.4 MB: one copy 120 us, seven 1 MB copies 175 us), so a round
+// is cut into 2 to kOutMaxChunks chunks of about kOutChunkTarget bytes.  Measured on
+// Mamba-130M int8 (tok/s through forward_batch, 32 / 128 streams): one thread per chunk,
+// two chunks 47.6K / 77.5K; eight threads slicing every chunk, two chunks 55.2K / 97.5K,
+// four chunks 53.0K / 101.2K.
+constexpr size_t kOutChunkTarget = (size_t)4 << 20;
+constexpr size_t kOutMaxChunks = 4;
 constexpr size_t kOutRoundBytes = (size_t)32 << 20;
-constexpr unsigned kCopyThreads = 4;   // the caller's thread and three helpers
+constexpr unsigned kCopyThreads = 8;   // the caller's thread and seven helpers
 
 bool out_stage_alloc(Pool& p, size_t out_bytes) {
     p.out_stage_bytes = std::min(kOutRoundBytes, (out_bytes + 255) & ~(size_t)255);
@@ -502,16 +504,15 @@ bool out_stage_alloc(Pool& p, size_t out_bytes) {
         p.h_out = nullptr;
         return false;
     }
-    static_assert(kOutRoundBytes / kOutChunkBytes <= sizeof(Pool::out_ev) / sizeof(hipEvent_t), "events per round");
-    const size_t chunks = (p.out_stage_bytes + kOutChunkBytes - 1) / kOutChunkBytes;
-    for (size_t c = 0; c < chunks; c++)
+    static_assert(kOutMaxChunks <= sizeof(Pool::out_ev) / sizeof(hipEvent_t), "events per round");
+    for (size_t c = 0; c < kOutMaxChunks; c++)
         if (hipEventCreateWithFlags(&p.out_ev[c], hipEventDisableTiming) != hipSuccess) return false;
     return true;
 }
 
-// Host threads that copy a round's chunks: one job per round, chunk c taken by thread
-// c % kCopyThreads (thread 0 is the caller).  A job ends when every helper that took it has
-// finished its chunks, so nothing of a job is touched after run() returns.
+// Host threads that copy a round's chunks: one job per round, body(t) run once by each of
+// the kCopyThreads threads (t = 0 is the caller).  A job ends when every helper has
+// finished its part, so nothing of a job is touched after run() returns.
 class CopyPool {
 public:
     ~CopyPool() {
@@ -523,21 +524,19 @@ public:
         cv_.notify_all();
         for (auto& t : th_) t.join();
     }
-    // body(c) for c in [0, chunks), spread over kCopyThreads threads; false if any failed.
-    bool run(size_t chunks, const std::function<bool(size_t)>& body) {
+    // body(t) on each thread t in [0, kCopyThreads); false if any failed.
+    bool run(const std::function<bool(unsigned)>& body) {
         if (th_.empty())
             for (unsigned i = 1; i < kCopyThreads; i++) th_.emplace_back([this, i] { loop(i); });
         {
             std::lock_guard<std::mutex> g(mu_);
             body_ = &body;
-            chunks_ = chunks;
             busy_ = kCopyThreads - 1;
             ok_ = true;
             ++gen_;
         }
         cv_.notify_all();
-        bool ok = true;
-        for (size_t c = 0; c < chunks; c += kCopyThreads) ok = body(c) && ok;
+        const bool ok = body(0);
         std::unique_lock<std::mutex> g(mu_);
         done_.wait(g, [&] { return busy_ == 0; });
         body_ = nullptr;
@@ -548,18 +547,15 @@ private:
     void loop(unsigned id) {
         uint64_t seen = 0;
         for (;;) {
-            const std::function<bool(size_t)>* body;
-            size_t chunks;
+            const std::function<bool(unsigned)>* body;
             {
                 std::unique_lock<std::mutex> g(mu_);
                 cv_.wait(g, [&] { return gen_ != seen; });
                 seen = gen_;
                 if (stop_) return;
                 body = body_;
-                chunks = chunks_;
             }
-            bool ok = true;
-            for (size_t c = id; c < chunks; c += kCopyThreads) ok = (*body)(c) && ok;
+            const bool ok = (*body)(id);
             std::lock_guard<std::mutex> g(mu_);
             ok_ = ok_ && ok;
             if (--busy_ == 0) done_.notify_all();
@@ -571,8 +567,7 @@ private:
     uint64_t gen_ = 0;
     bool stop_ = false, ok_ = true;
     unsigned busy_ = 0;
-    const std::function<bool(size_t)>* body_ = nullptr;
-    size_t chunks_ = 0;
+    const std::function<bool(unsigned)>* body_ = nullptr;
 };
 
 CopyPool& copy_pool() {
@@ -725,15 +720,27 @@ hipError_t run_step(Pool& p, uint32_t n, const uint32_t* slots, const uint32_t* 
     return G.runner.run(src, p, io, G.stream, &G.probe);
 }
 
+// Wait for an event by polling it: the copy threads pick a chunk up within a microsecond of
+// its DMA's end (a blocking wait can sleep for tens of microseconds).
+bool event_wait(hipEvent_t e) {
+    for (;;) {
+        const hipError_t r = hipEventQuery(e);
+        if (r == hipSuccess) return true;
+        if (r != hipErrorNotReady) return false;
+        std::this_thread::yield();
+    }
+}
+
 // The first `bytes` of the device array src into the caller's host buffer dst, through the
-// pool's pinned staging, a round at a time: all of a round's 1 MB chunks are queued D2H
-// (each followed by its event) behind the step, then the copy threads move each chunk into
-// dst once its event has completed, while the later chunks are still in flight.  Returns
-// when every byte is in dst.
+// pool's pinned staging, a round at a time: all of a round's chunks are queued D2H (each
+// followed by its event) behind the step, then every copy thread walks the chunks in order,
+// waits for each one's event and moves its slice of the chunk into dst, while the later
+// chunks are still in flight.  Returns when every byte is in dst.
 bool copy_out(Pool& p, void* dst, const void* src, size_t bytes) {
     for (size_t r0 = 0; r0 < bytes; r0 += p.out_stage_bytes) {
         const size_t rb = std::min(p.out_stage_bytes, bytes - r0);
-        const size_t cb = std::max(kOutChunkBytes, ((rb + kOutChunksPerRound - 1) / kOutChunksPerRound + 255) & ~(size_t)255);
+        const size_t want = std::min(kOutMaxChunks, std::max<size_t>(2, (rb + kOutChunkTarget - 1) / kOutChunkTarget));
+        const size_t cb = ((rb + want - 1) / want + 255) & ~(size_t)255;
         const size_t chunks = (rb + cb - 1) / cb;
         for (size_t c = 0; c < chunks; c++) {
             const size_t off = c * cb, len = std::min(cb, rb - off);
@@ -742,10 +749,15 @@ bool copy_out(Pool& p, void* dst, const void* src, size_t bytes) {
                 hipEventRecord(p.out_ev[c], G.stream) != hipSuccess)
                 return false;
         }
-        const bool ok = copy_pool().run(chunks, [&](size_t c) {
-            if (hipEventSynchronize(p.out_ev[c]) != hipSuccess) return false;
-            const size_t off = c * cb, len = std::min(cb, rb - off);
-            memcpy((unsigned char*)dst + r0 + off, p.h_out + off, len);
+        const bool ok = copy_pool().run([&](unsigned t) {
+            for (size_t c = 0; c < chunks; c++) {
+                if (!event_wait(p.out_ev[c])) return false;
+                const size_t off = c * cb, len = std::min(cb, rb - off);
+                // slice t of the chunk, 64-byte aligned
+                const size_t per = ((len + kCopyThreads - 1) / kCopyThreads + 63) & ~(size_t)63;
+                const size_t s0 = std::min(len, (size_t)t * per), s1 = std::min(len, s0 + per);
+                if (s1 > s0) memcpy((unsigned char*)dst + r0 + off + s0, p.h_out + off + s0, s1 - s0);
+            }
             return true;
         });
         if (!ok) return false;

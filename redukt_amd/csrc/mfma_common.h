@@ -53,12 +53,13 @@ __device__ __forceinline__ int wave_index() { return __builtin_amdgcn_readfirstl
 
 __device__ __forceinline__ uint32_t clamp_slot(uint32_t s, uint32_t cap) { return s < cap ? s : cap - 1; }
 
-// Workgroups are dealt to the XCDs round-robin by linear index, and each XCD has its own L2.
-// A grid of `units` work units, each split into `parts` workgroups that read the same
-// operands, is laid out 1-D over parts x (units rounded up to a multiple of kXcds): linear
-// index L runs on XCD L % kXcds and takes part (L / kXcds) % parts of unit
-// kXcds ((L / kXcds) / parts) + L % kXcds.  The parts of a unit are then consecutive
-// workgroups of one XCD and share its L2.  `live` is false past the last unit.
+// Workgroups are dealt to the XCDs round-robin by linear index (starting from wherever the
+// previous dispatch stopped, so within one launch linear indices L and L + kXcds share an
+// XCD, whichever XCD that is), and each XCD has its own L2.  A grid of `units` work units,
+// each split into `parts` workgroups that read the same operands, is laid out 1-D over
+// parts x (units rounded up to a multiple of kXcds): linear index L takes part
+// (L / kXcds) % parts of unit kXcds ((L / kXcds) / parts) + L % kXcds.  The parts of a unit
+// are then workgroups of one XCD and share its L2.  `live` is false past the last unit.
 constexpr uint32_t kXcds = 8;
 struct XcdTile {
     uint32_t unit, part;

@@ -136,7 +136,7 @@ struct Pool {
     uint32_t* d_slots = nullptr; // [2 cap] H2D target of the synchronous entry points: n slots, then n tokens
     uint32_t* h_slots = nullptr; // [2 cap] pinned staging of the same
     // Pinned staging of the outputs handed back to host memory (up to one round of
-    // out_stage_bytes), with one completion event per 1 MB chunk of a round.
+    // out_stage_bytes), with one completion event per chunk of a round (at most four).
     unsigned char* h_out = nullptr;
     size_t out_stage_bytes = 0;
     hipEvent_t out_ev[32] = {};
