@@ -123,6 +123,21 @@ int32_t redukt_backend_init_ex(const uint8_t* weights_path, int32_t device_id, u
 int32_t redukt_backend_forward_batch_probs(uint32_t n_streams, const uint32_t* slots, const uint32_t* tokens,
                                            float* out_probs, uint32_t vocab_size);
 
+/* forward_batch that returns each stream's CDF (vocab + 1 cumulative u32 frequencies,
+ * total 2^24) instead of its logits: the host coding path's redukt_cdf_from_logits
+ * (codec.rs:785-798, coder.rs:43-81, the f64 exp of fmath.rs:340-430) computed on the
+ * device, bit for bit.  cdf_len must be vocab + 1; out_cdf holds n_streams * cdf_len u32.
+ * Same validation and state rules as forward_batch.  No reference counterpart: the
+ * reference's roadmap names the on-device CDF (docs/ROADMAP.md:2995) without an
+ * interface. */
+int32_t redukt_backend_forward_batch_cdf(uint32_t n_streams, const uint32_t* slots, const uint32_t* tokens,
+                                         uint32_t* out_cdf, uint32_t cdf_len);
+
+/* The device CDF on caller logits: d_logits [rows][n] f32 -> d_cdf [rows][n + 1] u32,
+ * both device pointers, stream-ordered on redukt_backend_stream() (the call does not
+ * wait).  1 <= n < 2^24.  For tests and for callers that hold logits on the device. */
+int32_t redukt_backend_cdf_from_logits_device(const float* d_logits, uint32_t rows, uint32_t n, uint32_t* d_cdf);
+
 /* Stream-ordered step on device-resident inputs: d_slots, d_tokens and d_out are
  * device pointers (n_streams u32, n_streams u32, n_streams*vocab_size f32).  Nothing is
  * copied to or from the host and the call does not wait for the step to finish.

@@ -68,6 +68,8 @@ struct Model {
     Pool v1, batch;
     StepRunner runner;
     uint32_t* d_err = nullptr;
+    void* cdf_mem = nullptr;     // the device CDF's scratch (and CDF rows), grown on demand
+    size_t cdf_bytes = 0;
     int device = 0;
     Probe probe;
 };
@@ -690,6 +692,7 @@ void free_model() {
     G.runner.release();
     pool_free(G.v1);
     pool_free(G.batch);
+    if (G.cdf_mem) (void)hipFree(G.cdf_mem);
     dev_free_all();
     if (G.stream) (void)hipStreamDestroy(G.stream);
     G = Model{};
@@ -1050,6 +1053,68 @@ int32_t redukt_backend_init_ex(const uint8_t* weights_path, int32_t device_id, u
 int32_t redukt_backend_forward_batch_probs(uint32_t n_streams, const uint32_t* slots, const uint32_t* tokens,
                                            float* out_probs, uint32_t vocab_size) {
     return forward_batch_impl(n_streams, slots, tokens, out_probs, vocab_size, true);
+}
+
+// ---------------------------------------------------------------- CDFs on the device
+// The CDF kernels' scratch (exp values and the two sums per row) and, for the host-buffer
+// entry point, the CDF rows themselves: one allocation, grown on demand (the stream is
+// synchronized before the old one is freed).
+bool cdf_space(uint32_t rows, uint32_t n, bool with_out, void** scratch, uint32_t** out) {
+    const size_t sb = (cdf_scratch_bytes(rows, n) + 255) & ~(size_t)255;
+    const size_t need = sb + (with_out ? (size_t)rows * (n + 1) * 4 : 0);
+    if (need > G.cdf_bytes) {
+        if (G.cdf_mem) {
+            if (hipStreamSynchronize(G.stream) != hipSuccess) return false;
+            (void)hipFree(G.cdf_mem);
+            G.cdf_mem = nullptr;
+            G.cdf_bytes = 0;
+        }
+        if (hipMalloc(&G.cdf_mem, need) != hipSuccess) {
+            G.cdf_mem = nullptr;
+            return false;
+        }
+        G.cdf_bytes = need;
+    }
+    *scratch = G.cdf_mem;
+    if (out) *out = (uint32_t*)((unsigned char*)G.cdf_mem + sb);
+    return true;
+}
+
+int32_t redukt_backend_forward_batch_cdf(uint32_t n_streams, const uint32_t* slots, const uint32_t* tokens,
+                                         uint32_t* out_cdf, uint32_t cdf_len) {
+    if (!G.ready || G.batch.cap == 0) return BACKEND_INIT_FAILED;
+    const uint32_t V = G.kind == kKindRwkv ? G.rdims.vocab : G.dims.vocab;
+    if (cdf_len != V + 1 || n_streams > G.batch.cap || V >= (1u << 24)) return BACKEND_INVALID_ARGUMENT;
+    if (n_streams == 0) return BACKEND_OK;
+    if (!slots || !tokens || !out_cdf) return BACKEND_INVALID_ARGUMENT;
+    Pool& p = G.batch;
+    memset(p.seen, 0, p.cap);
+    for (uint32_t b = 0; b < n_streams; b++) {
+        if (slots[b] >= p.cap || p.seen[slots[b]] || tokens[b] >= V) return BACKEND_INVALID_ARGUMENT;
+        p.seen[slots[b]] = 1;
+    }
+    void* scratch = nullptr;
+    uint32_t* d_cdf = nullptr;
+    if (!cdf_space(p.cap, V, true, &scratch, &d_cdf)) return BACKEND_FORWARD_FAILED;
+    memcpy(p.h_slots, slots, sizeof(uint32_t) * n_streams);
+    memcpy(p.h_slots + n_streams, tokens, sizeof(uint32_t) * n_streams);
+    if (hipMemcpyAsync(p.d_slots, p.h_slots, sizeof(uint32_t) * 2 * n_streams, hipMemcpyHostToDevice, G.stream) !=
+        hipSuccess)
+        return BACKEND_FORWARD_FAILED;
+    if (run_step(p, n_streams, p.d_slots, p.d_slots + n_streams, p.out, false, false) != hipSuccess ||
+        cdf_launch(p.out, n_streams, V, scratch, d_cdf, G.stream) != hipSuccess)
+        return BACKEND_FORWARD_FAILED;
+    if (!copy_out(p, out_cdf, d_cdf, sizeof(uint32_t) * n_streams * (size_t)(V + 1))) return BACKEND_FORWARD_FAILED;
+    return BACKEND_OK;
+}
+
+int32_t redukt_backend_cdf_from_logits_device(const float* d_logits, uint32_t rows, uint32_t n, uint32_t* d_cdf) {
+    if (!G.ready) return BACKEND_INIT_FAILED;
+    if (n == 0 || n >= (1u << 24) || (rows > 0 && (!d_logits || !d_cdf))) return BACKEND_INVALID_ARGUMENT;
+    if (rows == 0) return BACKEND_OK;
+    void* scratch = nullptr;
+    if (!cdf_space(rows, n, false, &scratch, nullptr)) return BACKEND_FORWARD_FAILED;
+    return cdf_launch(d_logits, rows, n, scratch, d_cdf, G.stream) == hipSuccess ? BACKEND_OK : BACKEND_FORWARD_FAILED;
 }
 
 int32_t redukt_backend_forward_batch_device(uint32_t n_streams, const uint32_t* d_slots, const uint32_t* d_tokens,

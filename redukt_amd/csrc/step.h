@@ -58,6 +58,10 @@ Launch scan_launch(const DLayer& L, const Dims& D, Pool& p, uint32_t n, bool exa
                    float* ssm_layer);
 // The wavefront-GEMV tier: whether a chunks-per-lane count is compiled.
 bool gemv_cpl_supported(int cpl);
+// Logits [rows][n] -> CDF [rows][n + 1] on the device, bit for bit the host coding path's
+// cdf_from_logits (cdf_step.hip); `scratch` holds cdf_scratch_bytes(rows, n).
+size_t cdf_scratch_bytes(uint32_t rows, uint32_t n);
+hipError_t cdf_launch(const float* logits, uint32_t rows, uint32_t n, void* scratch, uint32_t* cdf, hipStream_t st);
 
 namespace {
 

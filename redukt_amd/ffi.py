@@ -42,7 +42,8 @@ V2_SYMBOLS = ("redukt_backend_abi_version", "redukt_backend_batch_init", "redukt
 V3_SYMBOLS = ("redukt_backend_init_ex", "redukt_backend_forward_batch_probs", "redukt_backend_forward_batch_device",
               "redukt_backend_device_status", "redukt_backend_stream", "redukt_backend_get_state",
               "redukt_backend_probe_kernel", "redukt_backend_probe_used", "redukt_backend_get_rwkv_state",
-              "redukt_backend_eval_math", "redukt_backend_forward_batch_device_noalloc")
+              "redukt_backend_eval_math", "redukt_backend_forward_batch_device_noalloc",
+              "redukt_backend_forward_batch_cdf", "redukt_backend_cdf_from_logits_device")
 # redukt_backend_eval_math function codes: the portable element-wise functions
 MATH_FNS = {"exp": 0, "lane_exp": 1, "ln": 2, "softplus": 3, "lane_sigmoid": 4, "sigmoid": 5}
 
@@ -147,6 +148,11 @@ class PluginLibrary:
             L.redukt_backend_forward_batch_device.restype = ctypes.c_int32
             L.redukt_backend_forward_batch_device_noalloc.argtypes = L.redukt_backend_forward_batch_device.argtypes
             L.redukt_backend_forward_batch_device_noalloc.restype = ctypes.c_int32
+            L.redukt_backend_forward_batch_cdf.argtypes = [ctypes.c_uint32, _u32p, _u32p, _u32p, ctypes.c_uint32]
+            L.redukt_backend_forward_batch_cdf.restype = ctypes.c_int32
+            L.redukt_backend_cdf_from_logits_device.argtypes = [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
+                                                                ctypes.c_void_p]
+            L.redukt_backend_cdf_from_logits_device.restype = ctypes.c_int32
             L.redukt_backend_device_status.argtypes = []
             L.redukt_backend_device_status.restype = ctypes.c_int32
             L.redukt_backend_stream.argtypes = []
@@ -355,6 +361,25 @@ class PluginBackend:
         does not fit the library's scratch)."""
         return BackendResult.from_code(self.lib.lib.redukt_backend_forward_batch_device_noalloc(
             n, d_slots, d_tokens, d_out, self.vocab, 1 if probs else 0))
+
+    def forward_batch_cdf(self, slots: Sequence[int], tokens: Sequence[int], out: np.ndarray) -> None:
+        """forward_batch returning each stream's CDF (vocab + 1 u32) computed on the device."""
+        err = validate_batch_args(list(slots), list(tokens), len(slots) * self.vocab, self.vocab, self.pool.cap,
+                                  self.pool.seen)
+        if err is not None:
+            raise BackendError(err, "forward_batch_cdf")
+        if len(slots) == 0:
+            return
+        assert out.dtype == np.uint32 and out.flags.c_contiguous and out.size == len(slots) * (self.vocab + 1)
+        s = np.ascontiguousarray(slots, dtype=np.uint32)
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        res = BackendResult.from_code(self.lib.lib.redukt_backend_forward_batch_cdf(
+            len(s), _ptr(s, ctypes.c_uint32), _ptr(t, ctypes.c_uint32), _ptr(out, ctypes.c_uint32), self.vocab + 1))
+        if res != BackendResult.OK:
+            raise BackendError(res, "forward_batch_cdf")
+
+    def cdf_from_logits_device(self, d_logits: int, rows: int, n: int, d_cdf: int) -> BackendResult:
+        return BackendResult.from_code(self.lib.lib.redukt_backend_cdf_from_logits_device(d_logits, rows, n, d_cdf))
 
     def device_status(self) -> BackendResult:
         return BackendResult.from_code(self.lib.lib.redukt_backend_device_status())

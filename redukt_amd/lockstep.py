@@ -73,6 +73,8 @@ def _bind(lib: ctypes.CDLL) -> None:
         "redukt_lockstep_vocab": (ctypes.c_uint32, [vp]),
         "redukt_lockstep_backend_name": (ctypes.c_char_p, [vp]),
         "redukt_lockstep_stream_bound": (ctypes.c_uint64, [ctypes.c_uint64]),
+        "redukt_lockstep_set_device_cdf": (ctypes.c_int32, [vp, ctypes.c_int32]),
+        "redukt_lockstep_device_cdf": (ctypes.c_int32, [vp]),
         "redukt_lockstep_compress": (ctypes.c_int32, [vp, ctypes.c_uint32, pp, _u64p, ctypes.c_uint64, pp, _u64p,
                                                       _u64p, _i32p, ctypes.POINTER(_Stats)]),
         "redukt_lockstep_decompress": (ctypes.c_int32, [vp, ctypes.c_uint32, pp, _u64p, _u64p, ctypes.c_uint64, pp,
@@ -99,7 +101,8 @@ def stream_bound(n_tokens: int) -> int:
 
 class Lockstep:
     def __init__(self, weights_path: str, plugin_path: str = DEFAULT_PLUGIN, device_id: int = 0,
-                 profile: Optional[int] = None, slots: int = 0, threads: int = 0):
+                 profile: Optional[int] = None, slots: int = 0, threads: int = 0,
+                 device_cdf: Optional[bool] = None):
         self._lib = codec.load()
         _bind(self._lib)
         h = ctypes.c_void_p()
@@ -108,9 +111,18 @@ class Lockstep:
         if rc != 0:
             raise LockstepError(rc, f"open({plugin_path}, {weights_path}, slots={slots})")
         self._h = h
+        if device_cdf is not None:   # None: the driver's default (device CDFs from 64 slots)
+            rc = self._lib.redukt_lockstep_set_device_cdf(h, 1 if device_cdf else 0)
+            if rc != 0:
+                self.close()
+                raise LockstepError(rc, "set_device_cdf (the plugin has no forward_batch_cdf, or slots = 0)")
         self.slots = slots
         self.vocab = int(self._lib.redukt_lockstep_vocab(h))
         self.name = self._lib.redukt_lockstep_backend_name(h).decode()
+
+    @property
+    def device_cdf(self) -> bool:
+        return bool(self._lib.redukt_lockstep_device_cdf(self._h))
 
     def compress(self, files: Sequence[Sequence[int]], reset_every: int = DEFAULT_RESET_EVERY
                  ) -> Tuple[List[bytes], Stats]:

@@ -1,0 +1,138 @@
+"""The device CDF (logits -> u32 cumulative frequencies on the GPU) against the host coding
+path, through the C ABI.
+
+The range coder's frequencies depend on the last bit of every f64 operation of the CDF,
+so the bar is bit-exact equality with `redukt_cdf_from_logits` (libredukt_host.so), which
+the CPU tests pin to the oracle and the reference's exp goldens:
+
+* crafted rows through `redukt_backend_cdf_from_logits_device`: Gaussian logits at
+  several scales, vocabularies 1, 2, 256, 50,280, 50,281 (odd: the unpaired load path)
+  and 65,536, many-way ties for the maximum, a flat row (every share rounds up and the
+  fix-up wraps the last frequency, a reference quirk), -inf entries, rows whose exps
+  underflow into subnormals, a row with NaNs;
+* `redukt_backend_forward_batch_cdf` on Mamba-130M (int8 per-row) and RWKV-7 0.1B
+  against the host CDF of the same step's logits from `forward_batch` (batch invariance
+  makes a stream's logits the same on any slot);
+* the driver's lockstep bytes with the device CDF equal those with the host CDF.
+"""
+import numpy as np
+import pytest
+
+from redukt_amd import codec, ffi, hip, lockstep, rwkv, synth
+
+pytestmark = pytest.mark.gpu
+
+Q8ROW_ALL = ffi.PROFILE_Q8_ROW | ffi.PROFILE_Q8_SMALL
+
+
+def crafted_rows():
+    rng = np.random.default_rng(2024)
+    rows = []
+    for n, scale in ((50280, 1.0), (50280, 8.0), (50280, 0.05), (65536, 3.0), (256, 2.0), (50281, 1.5),
+                     (2, 1.0), (1, 1.0)):
+        rows.append(("gauss", (rng.standard_normal(n) * scale).astype(np.float32)))
+    t = (rng.standard_normal(50280)).astype(np.float32)
+    t[rng.choice(50280, 37, replace=False)] = t.max() + 1.0       # 37 equal maxima
+    rows.append(("ties", t))
+    rows.append(("flat", np.zeros(50280, np.float32)))             # every share rounds up
+    t = (rng.standard_normal(50280) * 2).astype(np.float32)
+    t[::7] = -np.inf
+    rows.append(("neg-inf", t))
+    t = (rng.standard_normal(50280) * 300).astype(np.float32)       # exps down to subnormal and 0
+    rows.append(("subnormal", t))
+    t = (rng.standard_normal(4096)).astype(np.float32)
+    t[[5, 100, 4000]] = np.nan
+    rows.append(("nan", t))
+    return rows
+
+
+@pytest.fixture(scope="module")
+def backend(full_model):
+    with ffi.PluginBackend(full_model, profile=Q8ROW_ALL) as be:
+        yield be
+
+
+ROWS = crafted_rows()
+
+
+@pytest.mark.parametrize("case", range(len(ROWS)), ids=[f"{i}-{r[0]}-{r[1].size}" for i, r in enumerate(ROWS)])
+def test_device_cdf_equals_host_cdf_on_crafted_rows(backend, case):
+    name, row = ROWS[case]
+    n = row.size
+    host = codec.cdf_from_logits(row)
+    reps = np.stack([row, row[::-1].copy()]) if n > 1 else row[None]
+    d_l = hip.DeviceBuffer.from_array(np.ascontiguousarray(reps, np.float32))
+    d_c = hip.DeviceBuffer(reps.shape[0] * (n + 1) * 4)
+    try:
+        assert backend.cdf_from_logits_device(d_l.ptr, reps.shape[0], n, d_c.ptr) == ffi.BackendResult.OK
+        hip.stream_sync(backend.stream())
+        got = d_c.download(np.uint32, reps.shape[0] * (n + 1)).reshape(reps.shape[0], n + 1)
+    finally:
+        d_l.close()
+        d_c.close()
+    assert np.array_equal(got[0], host), (name, int(np.flatnonzero(got[0] != host)[0]))
+    if reps.shape[0] > 1:
+        assert np.array_equal(got[1], codec.cdf_from_logits(reps[1])), name
+    assert got[0, 0] == 0 and got[0, -1] == (1 << 24)
+
+
+def test_device_cdf_rejects_bad_sizes(backend):
+    assert backend.cdf_from_logits_device(0, 1, 0, 0) == ffi.BackendResult.INVALID_ARGUMENT
+    assert backend.cdf_from_logits_device(0, 1, 1 << 24, 0) == ffi.BackendResult.INVALID_ARGUMENT
+    assert backend.cdf_from_logits_device(0, 0, 10, 0) == ffi.BackendResult.OK
+
+
+def step_pair(be, n, steps, seed):
+    """forward_batch_cdf on slots [0, n) and forward_batch on slots [n, 2n) with the same
+    tokens: the device CDFs and the host CDFs of the logits, step by step."""
+    rng = np.random.default_rng(seed)
+    V = be.vocab
+    for t in range(steps):
+        toks = [int(x) for x in rng.integers(0, min(V, 50280), n)]
+        cdf = np.empty((n, V + 1), np.uint32)
+        be.forward_batch_cdf(list(range(n)), toks, cdf)
+        logits = np.empty((n, V), np.float32)
+        be.forward_batch(list(range(n, 2 * n)), toks, logits)
+        host = codec.cdf_from_logits_batch(logits)
+        bad = [r for r in range(n) if not np.array_equal(cdf[r], host[r])]
+        assert not bad, (t, bad[:5])
+
+
+def test_forward_batch_cdf_mamba130m(backend):
+    backend.batch_init(64)
+    step_pair(backend, 32, 3, seed=9)
+
+
+def test_forward_batch_cdf_rejects_bad_arguments(backend):
+    backend.batch_init(8)
+    out = np.empty((2, backend.vocab + 1), np.uint32)
+    with pytest.raises(ffi.BackendError):
+        backend.forward_batch_cdf([0, 0], [1, 2], out)          # repeated slot
+    code = backend.lib.lib.redukt_backend_forward_batch_cdf(
+        1, ffi._ptr(np.zeros(1, np.uint32), ffi.ctypes.c_uint32), ffi._ptr(np.zeros(1, np.uint32), ffi.ctypes.c_uint32),
+        ffi._ptr(out, ffi.ctypes.c_uint32), backend.vocab)      # cdf_len one short
+    assert code == ffi.BackendResult.INVALID_ARGUMENT
+
+
+# The tests below open backends of their own: the library holds one model at a time, so
+# they come after every test of the shared `backend` fixture.
+def test_forward_batch_cdf_rwkv7(tmp_path):
+    p = str(tmp_path / "rwkv.rbin")
+    rwkv.write_synthetic(p, rwkv.RWKV7_0_1B, seed=1)
+    with ffi.PluginBackend(p, profile=2) as be:
+        be.batch_init(16)
+        step_pair(be, 8, 2, seed=3)
+
+
+def test_lockstep_device_cdf_bytes_equal_host_cdf(full_model):
+    rng = np.random.default_rng(77)
+    files = [[int(x) for x in synth.zipf_tokens(rng, 50280, (L,))] for L in (40, 17, 64, 1, 33)]
+    outs = {}
+    for dev in (False, True):
+        with lockstep.Lockstep(full_model, ffi.DEFAULT_LIB, profile=Q8ROW_ALL, slots=3, device_cdf=dev) as ls:
+            assert ls.device_cdf == dev
+            streams, _ = ls.compress(files)
+            back, _ = ls.decompress(streams, [len(f) for f in files])
+            assert [b.tolist() for b in back] == files
+            outs[dev] = streams
+    assert outs[True] == outs[False]

@@ -185,3 +185,16 @@ def test_decompress_rejects_mismatched_lengths(fake):
     with Lockstep(w, plugin_path=so, slots=2) as ls:
         with pytest.raises(ValueError):
             ls.decompress([b"\x00" * 8, b"\x00" * 8], [4])
+
+
+def test_device_cdf_needs_the_plugin_symbol(fake):
+    # the stand-in plugin exports no forward_batch_cdf: the driver keeps the host CDF and
+    # refuses to switch
+    so, w = fake
+    with Lockstep(w, plugin_path=so, slots=3) as ls:
+        assert not ls.device_cdf
+        out, _ = ls.compress(files(), reset_every=16)
+    with pytest.raises(LockstepError):
+        Lockstep(w, plugin_path=so, slots=3, device_cdf=True)
+    with Lockstep(w, plugin_path=so, slots=3, device_cdf=False) as ls:
+        assert ls.compress(files(), reset_every=16)[0] == out
