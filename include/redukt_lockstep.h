@@ -75,7 +75,7 @@ const char* redukt_lockstep_backend_name(const redukt_lockstep* ls);
 /* on = 1: Phase B takes each stream's CDF from the plugin's optional
  * redukt_backend_forward_batch_cdf (computed on the device, bit for bit the host CDF), so
  * Phase A only codes; on = 0: Phase B takes logits and Phase A builds the CDFs on the host.
- * open() turns it on from 64 slots when the plugin exports forward_batch_cdf.  The bytes
+ * open() turns it on for the lockstep path when the plugin exports forward_batch_cdf.  The bytes
  * are the same either way.  INVALID_ARG when the plugin does not export forward_batch_cdf
  * or the driver runs the single-stream path (slots = 0). */
 int32_t redukt_lockstep_set_device_cdf(redukt_lockstep* ls, int32_t on);

@@ -107,15 +107,27 @@ __device__ __forceinline__ uint64_t sat_u64(double v) {
 // One row's f32 probability, the host's p[i] = float(e[i] * inv_sum).
 __device__ __forceinline__ float prob_of(double e, double inv_sum) { return (float)(e * inv_sum); }
 
+constexpr uint32_t kSpan = 16;                      // consecutive elements per thread in a chunk
+constexpr uint32_t kChunk = kSpan * kCdfBlock;      // elements per chunk workgroup
+
+struct ChunkPart {
+    double max;        // the chunk's max (NaN loses; -inf if none)
+    uint64_t used;     // sum of the chunk's extra frequencies
+    uint64_t best;     // (largest frequency << 32) | its last index
+    uint32_t total;    // sum of the chunk's frequencies before the fix-up (u32, wrapping)
+    uint32_t pad;
+};
+
 struct CdfArgs {
     const float* logits;   // [rows][n]
-    uint32_t rows, n;
+    uint32_t rows, n, chunks;
     double* e;             // [rows][n] scratch: exp(logit - max)
     double* sums;          // [rows][2] scratch: sum of e, sum of the probabilities
+    ChunkPart* part;       // [rows][chunks] scratch
     uint32_t* cdf;         // [rows][n + 1]
 };
 
-// Block-wide reductions over kCdfBlock threads (8 waves... 4 waves of 64).
+// Block-wide reductions over kCdfBlock threads (four waves of 64).
 template <class T, class F>
 __device__ T block_reduce(T v, F op, T* sh) {
     const int lane = threadIdx.x % 64, w = threadIdx.x / 64;
@@ -126,175 +138,345 @@ __device__ T block_reduce(T v, F op, T* sh) {
     }
     if (lane == 0) sh[w] = v;
     __syncthreads();
-    if (threadIdx.x == 0) {
-        T r = sh[0];
-        for (int i = 1; i < kCdfBlock / 64; i++) r = op(r, sh[i]);
-        sh[kCdfBlock / 64] = r;
-    }
-    __syncthreads();
-    const T r = sh[kCdfBlock / 64];
+    T r = sh[0];
+#pragma unroll
+    for (int i = 1; i < kCdfBlock / 64; i++) r = op(r, sh[i]);
     __syncthreads();
     return r;
 }
 
-// Phase 1 (one workgroup per row): max over the row (f64::max, NaN loses; -inf if every
-// entry is NaN, as the host's fold), then e[i] = exp(logit[i] - max).
-__global__ __launch_bounds__(kCdfBlock) void k_cdf_exp(CdfArgs a) {
-    __shared__ double sh[kCdfBlock / 64 + 1];
-    const uint32_t row = blockIdx.x, n = a.n;
+__device__ __forceinline__ double max_nan_loses(double m, double v) { return (!isnan(v) && !(v <= m)) ? v : m; }
+
+// Phase 1a (chunk c of row r): the chunk's max (f64::max folding, NaN loses).
+__global__ __launch_bounds__(kCdfBlock) void k_cdf_max(CdfArgs a) {
+    __shared__ double sh[kCdfBlock / 64];
+    const uint32_t c = blockIdx.x, row = blockIdx.y, n = a.n;
     const float* l = a.logits + (size_t)row * n;
     double m = -__longlong_as_double(0x7ff0000000000000LL);
-    for (uint32_t i = threadIdx.x; i < n; i += kCdfBlock) {
-        const double v = (double)l[i];
-        if (!isnan(v) && !(v <= m)) m = v;
-    }
+    for (uint32_t i = c * kChunk + threadIdx.x; i < min(n, (c + 1) * kChunk); i += kCdfBlock)
+        m = max_nan_loses(m, (double)l[i]);
     // every partial is -inf or a number, so the combination order does not matter
     m = block_reduce<double>(m, [](double x, double y) { return (y <= x) ? x : y; }, sh);
+    if (threadIdx.x == 0) a.part[(size_t)row * a.chunks + c].max = m;
+}
+
+// Phase 1b (chunk c of row r): the row's max from the chunk maxima, then e = exp(logit - max).
+__global__ __launch_bounds__(kCdfBlock) void k_cdf_exp(CdfArgs a) {
+    const uint32_t c = blockIdx.x, row = blockIdx.y, n = a.n;
+    const ChunkPart* pr = a.part + (size_t)row * a.chunks;
+    double m = pr[0].max;
+    for (uint32_t i = 1; i < a.chunks; i++) m = (pr[i].max <= m) ? m : pr[i].max;
+    const float* l = a.logits + (size_t)row * n;
     double* e = a.e + (size_t)row * n;
-    for (uint32_t i = threadIdx.x; i < n; i += kCdfBlock) e[i] = exp_f64((double)l[i] - m, c_exp.v);
+    for (uint32_t i = c * kChunk + threadIdx.x; i < min(n, (c + 1) * kChunk); i += kCdfBlock)
+        e[i] = exp_f64((double)l[i] - m, c_exp.v);
 }
 
 // Phase 2 (one workgroup per row): the two sequential f64 sums, in index order:
 // sum = 0.0 + e[0] + e[1] + ... (codec.rs:791-794), then sum_p = -0.0 + p[0] + p[1] + ...
-// (coder.rs:45-46) with p[i] = float(e[i] * (1 / sum)).  Each is one dependent chain of adds,
-// run by wave 0 (every lane the same chain, lane 0's result kept) out of an LDS ring that
-// waves 1-3 fill from HBM kLead chunks ahead, so the chain waits on LDS (about a hundred
-// cycles, reads returned in order) instead of on memory.
-constexpr uint32_t kChunk = 1024;   // doubles per ring slot (8 KB)
-constexpr uint32_t kSlots = 4;
-constexpr uint32_t kLead = 2;       // chunks the producers run ahead of the chain
+// (coder.rs:45-46) with p[i] = float(e[i] * (1 / sum)).  Every term is >= +0 or NaN.
+//
+// A sequential sum of non-negative terms can be computed exactly in parallel between binade
+// changes of the running sum s.  While s stays in [2^E, 2^(E+1)), every double there is a
+// multiple of u = 2^(E-52), s = T u with T < 2^53, and fl(s + x) = (T + a) u with
+// a = round(x / u), as long as x / u is not a tie (fractional part exactly 1/2: then the
+// result depends on the parity of T) and T + a < 2^53 (else the result leaves the binade
+// and rounds on a coarser grid).  So a round takes 2048 terms, each thread forms a for 8
+// of them, a block-wide prefix sum gives every T, and the first term that is a tie, a NaN,
+// or takes T to 2^53 or beyond is an event: the terms before it are added as the integer
+// sum, the event itself with one real f64 add, and the next round starts after it (on the
+// new s's grid).  Below 2^-1022 the grid is the subnormal spacing 2^-1074 with the same
+// rule.  A round without an event adds all its terms.  The result is the sequential sum
+// bit for bit (an event changes s exactly as the sequential add does; between events the
+// integer sum is exact).  The running sum of these rows stays below 2^24 (each term <= 1,
+// n < 2^24), so the grid is always finer than 1.
+constexpr uint32_t kTerms = 8;                       // terms per thread per round
+constexpr uint32_t kRound = kTerms * kCdfBlock;      // terms per round
+constexpr uint32_t kNoEvent = 0xffffffffu;
+
+// LDS of a round, double-buffered by round parity so that a round's writes never meet the
+// previous round's reads (two barriers per round).
+struct SumShared {
+    uint64_t part[2][kCdfBlock / 64];   // per-wave totals
+    uint32_t first[2][kCdfBlock / 64];  // per-wave first event
+    uint64_t t_ev[2][kCdfBlock / 64];   // the grid count before that event
+    double x_ev[2][kCdfBlock / 64];     // that event's term
+    double s;                           // the fallback's result
+};
 
 template <class F>
-__device__ double ring_sum(const double* __restrict__ e, uint32_t n, double s, F f, double* ring) {
-    const uint32_t chunks = (n + kChunk - 1) / kChunk;
-    const uint32_t wave = threadIdx.x / 64, pt = threadIdx.x - 64;   // producer thread index (waves 1-3)
-    // a producer thread's share of a chunk: every load issued before the first store
-    constexpr uint32_t kProducers = kCdfBlock - 64;
-    constexpr uint32_t kPer = (kChunk + kProducers - 1) / kProducers;
-    auto produce = [&](uint32_t c) {
-        double* slot = ring + (c % kSlots) * kChunk;
-        const uint32_t base = c * kChunk, len = min(kChunk, n - base);
-        double t[kPer];
+__device__ double exact_seq_sum(const double* __restrict__ e, uint32_t n, double s, F f, SumShared& sh) {
+    const uint32_t t = threadIdx.x;
+    const int lane = t % 64, w = t / 64;
+    // The window's terms stay in registers (thread t: terms t kTerms .. + kTerms - 1), and
+    // the next window's loads are issued before the current one is summed.
+    double x[kTerms], xn[kTerms];
+    auto load = [&](double* dst, uint32_t k0) {
 #pragma unroll
-        for (uint32_t j = 0; j < kPer; j++) {
-            const uint32_t i = pt + j * kProducers;
-            t[j] = e[base + min(i, len - 1)];
-        }
-#pragma unroll
-        for (uint32_t j = 0; j < kPer; j++) {
-            const uint32_t i = pt + j * kProducers;
-            if (i < len) slot[i] = t[j];
-        }
+        for (uint32_t j = 0; j < kTerms; j++) dst[j] = e[min(k0 + t * kTerms + j, n - 1)];
     };
-    if (wave != 0)
-        for (uint32_t c = 0; c < kLead && c < chunks; c++) produce(c);
-    __syncthreads();
-    for (uint32_t c = 0; c < chunks; c++) {
-        if (wave != 0) {
-            if (c + kLead < chunks) produce(c + kLead);
-        } else {
-            const double* slot = ring + (c % kSlots) * kChunk;
-            const uint32_t len = min(kChunk, n - c * kChunk);
-            uint32_t i = 0;
-            for (; i + 32 <= len; i += 32) {
-                double v[32];
-#pragma unroll
-                for (int j = 0; j < 32; j++) v[j] = slot[i + j];
-#pragma unroll
-                for (int j = 0; j < 32; j++) s += f(v[j]);
+    load(x, 0);
+    uint32_t par = 0;
+    for (uint32_t k0 = 0; k0 < n; k0 += kRound) {
+        if (k0 + kRound < n) load(xn, k0 + kRound);
+        // rounds over this window: after an event the rest of the window is re-gridded
+        uint32_t from = 0;   // first term of the window not yet in s
+        while (from < kRound && k0 + from < n) {
+            if (isnan(s)) return s;   // stays NaN (only NaN-ness is used downstream)
+            if (!(s < 0x1p52)) {
+                // a grid of 1 or coarser (not reached by these rows): finish in order on one thread
+                __syncthreads();
+                if (t == 0) {
+                    for (uint32_t i = k0 + from; i < n; i++) s += f(e[i]);
+                    sh.s = s;
+                }
+                __syncthreads();
+                return sh.s;
             }
-            for (; i < len; i++) s += f(slot[i]);
+            // the grid of the current binade: terms scale by 2^ks into units of it
+            int ks;
+            uint64_t top;
+            if (s < 0x1p-1022) {
+                ks = 1074;
+                top = 1ull << 52;
+            } else {
+                ks = 52 - ilogb(s);
+                top = 1ull << 53;
+            }
+            const uint64_t T0 = (uint64_t)ldexp(s, ks);   // exact: s is on the grid
+            uint64_t a[kTerms];
+            uint32_t ev = kNoEvent;   // this thread's first event (index within the window)
+            uint64_t mine = 0;
+#pragma unroll
+            for (uint32_t j = 0; j < kTerms; j++) {
+                const uint32_t r = t * kTerms + j;
+                a[j] = 0;
+                if (r >= from && k0 + r < n) {
+                    const double q = ldexp(f(x[j]), ks);   // exact, or +inf past the double range
+                    bool event = !(q < 0x1p53);            // NaN, inf, or certainly past the binade
+                    if (!event) {
+                        const double m = floor(q), fr = q - m;
+                        event = fr == 0.5;
+                        a[j] = (uint64_t)m + (fr > 0.5 ? 1u : 0u);
+                    }
+                    if (event) {
+                        a[j] = 0;
+                        if (ev == kNoEvent) ev = r;
+                    }
+                }
+                mine += a[j];
+            }
+            // workgroup prefix of the grid counts (u64, wrapping: only values below 2^53
+            // before the first crossing are used)
+            uint64_t incl = mine;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const uint64_t up = __shfl_up(incl, o);
+                if (lane >= o) incl += up;
+            }
+            if (lane == 63) sh.part[par][w] = incl;
+            __syncthreads();
+            uint64_t before = incl - mine, total = 0;
+#pragma unroll
+            for (int i = 0; i < kCdfBlock / 64; i++) {
+                const uint64_t p = sh.part[par][i];
+                if (i < w) before += p;
+                total += p;
+            }
+            // crossings: the first term whose add takes T to the top of the binade
+            uint64_t T = T0 + before, T_ev = 0;
+            double x_ev = 0.0;
+#pragma unroll
+            for (uint32_t j = 0; j < kTerms; j++) {
+                const uint32_t r = t * kTerms + j;
+                const bool live = r >= from && k0 + r < n;
+                if (live && (r == ev || (r < ev && T + a[j] >= top))) {
+                    ev = r;
+                    T_ev = T;
+                    x_ev = x[j];
+                    break;
+                }
+                T += a[j];
+            }
+            uint32_t wev = ev;
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) wev = min(wev, (uint32_t)__shfl_xor((int)wev, o));
+            if (lane == 0) sh.first[par][w] = wev;
+            if (ev != kNoEvent && ev == wev) {
+                sh.t_ev[par][w] = T_ev;
+                sh.x_ev[par][w] = x_ev;
+            }
+            __syncthreads();
+            uint32_t first = kNoEvent;
+            int fw = 0;
+#pragma unroll
+            for (int i = kCdfBlock / 64 - 1; i >= 0; i--) {
+                const uint32_t v = sh.first[par][i];
+                if (v <= first) {
+                    first = v;
+                    fw = i;
+                }
+            }
+            if (first == kNoEvent) {
+                // no event: the window's remaining terms are the grid sum (T0 + total < 2^53)
+                s = ldexp((double)(T0 + total), -ks);
+                from = kRound;
+            } else {
+                // the event's add, done by every thread on the same operands
+                s = ldexp((double)sh.t_ev[par][fw], -ks) + f(sh.x_ev[par][fw]);
+                from = first + 1;
+            }
+            par ^= 1u;
         }
-        __syncthreads();
+#pragma unroll
+        for (uint32_t j = 0; j < kTerms; j++) x[j] = xn[j];
     }
     return s;
 }
 
 __global__ __launch_bounds__(kCdfBlock) void k_cdf_sums(CdfArgs a) {
-    __shared__ double ring[kSlots * kChunk];
-    static_assert(kLead < kSlots, "a slot is refilled only after the chain has left it");
+    __shared__ SumShared sh;
     const uint32_t row = blockIdx.x, n = a.n;
     const double* e = a.e + (size_t)row * n;
-    const double s = ring_sum(e, n, 0.0, [](double v) { return v; }, ring);
+    const double s = exact_seq_sum(e, n, 0.0, [](double v) { return v; }, sh);
     const double inv_sum = 1.0 / s;
-    const double sp = ring_sum(e, n, -0.0, [inv_sum](double v) { return (double)prob_of(v, inv_sum); }, ring);
+    const double sp = exact_seq_sum(e, n, -0.0, [inv_sum](double v) { return (double)prob_of(v, inv_sum); }, sh);
     if (threadIdx.x == 0) {
         a.sums[2 * row] = s;
         a.sums[2 * row + 1] = sp;
     }
 }
 
-// Phase 3 (one workgroup per row): Cdf::from_probs (coder.rs:43-81) from the two sums:
-// extra[i] = (u64)(p[i] * inv * rem + 0.5), freq[i] = 1 + extra[i]; the surplus or deficit
-// goes to the last of the largest frequencies; then the cumulative frequencies.  Thread t
-// owns the contiguous span [t * per, (t + 1) * per) for the prefix sums.
-__global__ __launch_bounds__(kCdfBlock) void k_cdf_freq(CdfArgs a) {
-    __shared__ uint64_t sh64[kCdfBlock / 64 + 1];
-    __shared__ uint32_t shu[kCdfBlock];
-    const uint32_t row = blockIdx.x, n = a.n;
-    const double* e = a.e + (size_t)row * n;
-    uint32_t* cdf = a.cdf + (size_t)row * (n + 1);
+// Phase 3, Cdf::from_probs (coder.rs:43-81) from the two sums: extra[i] =
+// (u64)(p[i] * inv * rem + 0.5) and freq[i] = 1 + extra[i]; the surplus or deficit goes to
+// the last of the largest frequencies; then the cumulative frequencies.  3a gathers each
+// chunk's used sum, its largest (frequency, last index) and its frequency total; 3b writes
+// the chunk's cumulative frequencies from those.  Every combination here is an integer sum
+// or a max, exact in any order.
+struct FreqRow {
+    double inv_sum, inv, rem;
+    uint64_t remaining;
+};
+__device__ __forceinline__ FreqRow freq_row(const CdfArgs& a, uint32_t row) {
+    FreqRow f;
     const double s = a.sums[2 * row], sum_p = a.sums[2 * row + 1];
-    const double inv_sum = 1.0 / s;
-    const uint64_t remaining = (uint64_t)kCdfTotal - n;
-    const double inv = sum_p > 0.0 ? 1.0 / sum_p : 0.0;
-    const double rem = (double)remaining;
-    auto extra_of = [&](uint32_t i) {
-        return sat_u64((double)prob_of(e[i], inv_sum) * inv * rem + 0.5);
-    };
-    // used (exact integer sum) and the fix-up position: the largest frequency, last index
-    // among equals; both reductions are order-independent.
-    uint64_t used = 0;
-    uint64_t best = 0;   // (freq << 32) | index: the larger freq, then the larger index
-    for (uint32_t i = threadIdx.x; i < n; i += kCdfBlock) {
-        const uint64_t x = extra_of(i);
+    f.inv_sum = 1.0 / s;
+    f.remaining = (uint64_t)kCdfTotal - a.n;
+    f.inv = sum_p > 0.0 ? 1.0 / sum_p : 0.0;
+    f.rem = (double)f.remaining;
+    return f;
+}
+__device__ __forceinline__ uint64_t extra_of(double e, const FreqRow& f) {
+    return sat_u64((double)prob_of(e, f.inv_sum) * f.inv * f.rem + 0.5);
+}
+
+__global__ __launch_bounds__(kCdfBlock) void k_cdf_freq_parts(CdfArgs a) {
+    __shared__ uint64_t sh64[kCdfBlock / 64];
+    __shared__ uint32_t sh32[kCdfBlock / 64];
+    const uint32_t c = blockIdx.x, row = blockIdx.y, n = a.n;
+    const FreqRow f = freq_row(a, row);
+    const double* e = a.e + (size_t)row * n;
+    uint64_t used = 0, best = 0;
+    uint32_t total = 0;
+    for (uint32_t i = c * kChunk + threadIdx.x; i < min(n, (c + 1) * kChunk); i += kCdfBlock) {
+        const uint64_t x = extra_of(e[i], f);
+        const uint32_t fr = 1u + (uint32_t)x;
         used += x;
-        const uint64_t key = ((uint64_t)(uint32_t)(1u + (uint32_t)x) << 32) | i;
+        total += fr;
+        const uint64_t key = ((uint64_t)fr << 32) | i;
         best = key > best ? key : best;
     }
     used = block_reduce<uint64_t>(used, [](uint64_t x, uint64_t y) { return x + y; }, sh64);
     best = block_reduce<uint64_t>(best, [](uint64_t x, uint64_t y) { return x > y ? x : y; }, sh64);
-    const int64_t diff = (int64_t)remaining - (int64_t)used;
-    const uint32_t at = (uint32_t)best;
-    auto freq_of = [&](uint32_t i) {
-        uint32_t f = 1u + (uint32_t)extra_of(i);
-        if (diff != 0 && i == at) f = (uint32_t)((int64_t)f + diff);
-        return f;
-    };
-    // prefix sums over contiguous spans (u32, wrapping like the host's)
-    const uint32_t per = (n + kCdfBlock - 1) / kCdfBlock;
-    const uint32_t i0 = min(n, threadIdx.x * per), i1 = min(n, i0 + per);
-    uint32_t tot = 0;
-    for (uint32_t i = i0; i < i1; i++) tot += freq_of(i);
-    shu[threadIdx.x] = tot;
-    __syncthreads();
+    total = block_reduce<uint32_t>(total, [](uint32_t x, uint32_t y) { return x + y; }, sh32);
     if (threadIdx.x == 0) {
-        uint32_t run = 0;
-        for (int t = 0; t < kCdfBlock; t++) {
-            const uint32_t v = shu[t];
-            shu[t] = run;
-            run += v;
+        ChunkPart& p = a.part[(size_t)row * a.chunks + c];
+        p.used = used;
+        p.best = best;
+        p.total = total;
+    }
+}
+
+__global__ __launch_bounds__(kCdfBlock) void k_cdf_freq_write(CdfArgs a) {
+    __shared__ uint32_t sh[kCdfBlock / 64];
+    __shared__ uint32_t stage[kChunk];   // the chunk's cumulative frequencies, stored out coalesced
+    const uint32_t c = blockIdx.x, row = blockIdx.y, n = a.n;
+    const FreqRow f = freq_row(a, row);
+    const ChunkPart* pr = a.part + (size_t)row * a.chunks;
+    uint64_t used = 0, best = 0;
+    uint32_t offset = 0;
+    for (uint32_t i = 0; i < a.chunks; i++) {
+        used += pr[i].used;
+        best = pr[i].best > best ? pr[i].best : best;
+        if (i < c) offset += pr[i].total;
+    }
+    const int64_t diff = (int64_t)f.remaining - (int64_t)used;
+    const uint32_t at = (uint32_t)best;
+    const uint32_t c0 = c * kChunk;
+    if (diff != 0 && at < c0) offset = (uint32_t)((int64_t)offset + diff);   // u32 wrap, as the host's sum
+    const double* e = a.e + (size_t)row * n;
+    uint32_t* cdf = a.cdf + (size_t)row * (n + 1);
+    // thread t: kSpan consecutive elements; exclusive scan of the thread totals
+    const uint32_t i0 = c0 + threadIdx.x * kSpan;
+    uint32_t fq[kSpan];
+    uint32_t mine = 0;
+#pragma unroll
+    for (uint32_t j = 0; j < kSpan; j++) {
+        const uint32_t i = i0 + j;
+        uint32_t v = 0;
+        if (i < n) {
+            v = 1u + (uint32_t)extra_of(e[i], f);
+            if (diff != 0 && i == at) v = (uint32_t)((int64_t)v + diff);
         }
-        cdf[0] = 0;
+        fq[j] = v;
+        mine += v;
+    }
+    const int lane = threadIdx.x % 64, w = threadIdx.x / 64;
+    uint32_t incl = mine;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t up = __shfl_up(incl, o);
+        if (lane >= o) incl += up;
+    }
+    if (lane == 63) sh[w] = incl;
+    __syncthreads();
+    uint32_t cum = offset + incl - mine;
+#pragma unroll
+    for (int i = 0; i < kCdfBlock / 64; i++)
+        if (i < w) cum += sh[i];
+    if (c == 0 && threadIdx.x == 0) cdf[0] = 0;
+#pragma unroll
+    for (uint32_t j = 0; j < kSpan; j++) {
+        cum += fq[j];
+        stage[threadIdx.x * kSpan + j] = cum;
     }
     __syncthreads();
-    uint32_t cum = shu[threadIdx.x];
-    for (uint32_t i = i0; i < i1; i++) {
-        cum += freq_of(i);
-        cdf[i + 1] = cum;
-    }
+    for (uint32_t r = threadIdx.x; r < kChunk && c0 + r < n; r += kCdfBlock) cdf[c0 + r + 1] = stage[r];
 }
 
 }  // namespace
 
-size_t cdf_scratch_bytes(uint32_t rows, uint32_t n) { return (size_t)rows * n * 8 + (size_t)rows * 16; }
+namespace {
+uint32_t cdf_chunks(uint32_t n) { return (n + kChunk - 1) / kChunk; }
+}  // namespace
+
+size_t cdf_scratch_bytes(uint32_t rows, uint32_t n) {
+    return (size_t)rows * n * 8 + (size_t)rows * 16 + (size_t)rows * cdf_chunks(n) * sizeof(ChunkPart);
+}
 
 hipError_t cdf_launch(const float* logits, uint32_t rows, uint32_t n, void* scratch, uint32_t* cdf, hipStream_t st) {
     if (rows == 0) return hipSuccess;
-    CdfArgs a{logits, rows, n, (double*)scratch, (double*)scratch + (size_t)rows * n, cdf};
-    k_cdf_exp<<<dim3(rows), dim3(kCdfBlock), 0, st>>>(a);
+    const uint32_t chunks = cdf_chunks(n);
+    double* e = (double*)scratch;
+    double* sums = e + (size_t)rows * n;
+    ChunkPart* part = (ChunkPart*)(sums + 2 * (size_t)rows);
+    CdfArgs a{logits, rows, n, chunks, e, sums, part, cdf};
+    const dim3 grid(chunks, rows);
+    k_cdf_max<<<grid, dim3(kCdfBlock), 0, st>>>(a);
+    k_cdf_exp<<<grid, dim3(kCdfBlock), 0, st>>>(a);
     k_cdf_sums<<<dim3(rows), dim3(kCdfBlock), 0, st>>>(a);
-    k_cdf_freq<<<dim3(rows), dim3(kCdfBlock), 0, st>>>(a);
+    k_cdf_freq_parts<<<grid, dim3(kCdfBlock), 0, st>>>(a);
+    k_cdf_freq_write<<<grid, dim3(kCdfBlock), 0, st>>>(a);
     return hipGetLastError();
 }
 

@@ -66,7 +66,7 @@ struct PluginApi {
 
 enum class Mode { Encode, Decode };
 
-constexpr uint32_t kDeviceCdfFrom = 64;   // slots from which Phase B takes CDFs from the plugin
+constexpr uint32_t kDeviceCdfFrom = 1;    // slots from which Phase B takes CDFs from the plugin
 
 // A slot's file in flight (lockstep.rs:71-97 without the context-mixing models).
 struct Lane {
@@ -387,9 +387,9 @@ extern "C" int32_t redukt_lockstep_open(const char* plugin_path, const char* wei
     ls->cdf.assign(rows * (size_t(ls->vocab) + 1), 0u);
     ls->uniform.assign(size_t(ls->vocab) + 1, 0u);
     redukt_cdf_uniform(ls->vocab, ls->uniform.data());
-    // The device CDF pays from 64 streams (Mamba-130M int8, 16 host threads: at 128 streams
-    // 2.45 ms per step against 1.28 ms forward + 2.60 ms host CDF; at 32 streams 1.59 ms
-    // against 0.59 + 0.91 ms).
+    // The device CDF is the faster path wherever the plugin has it (Mamba-130M int8, 16 host
+    // threads: forward_batch_cdf 0.93 ms per step at 32 streams against 0.58 ms forward +
+    // 0.71 ms host CDF, 1.77 ms at 128 streams against 1.27 + 2.60 ms).
     ls->device_cdf = ls->api.forward_batch_cdf != nullptr && slots >= kDeviceCdfFrom;
     *out = ls.release();
     return REDUKT_LOCKSTEP_OK;

@@ -111,7 +111,7 @@ class Lockstep:
         if rc != 0:
             raise LockstepError(rc, f"open({plugin_path}, {weights_path}, slots={slots})")
         self._h = h
-        if device_cdf is not None:   # None: the driver's default (device CDFs from 64 slots)
+        if device_cdf is not None:   # None: the driver's default (device CDFs where the plugin has them)
             rc = self._lib.redukt_lockstep_set_device_cdf(h, 1 if device_cdf else 0)
             if rc != 0:
                 self.close()
