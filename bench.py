@@ -263,13 +263,22 @@ class Workload:
         return ms, wall
 
     def ffi_rate(self, steps: int) -> float:
-        """tok/s of the synchronous host-buffer entry point (D2H of n rows of logits)."""
+        """tok/s of the synchronous host-buffer entry point (slots and tokens from host
+        memory, n rows of logits back into host memory), called through the C ABI with the
+        step's arrays ready, as a compiled host calls it; the library validates every call."""
         out = np.empty((self.n, self.vocab), np.float32)
-        slots = list(range(self.n))
-        self.be.forward_batch(slots, [int(x) for x in self.tokens[0]], out, probs=self.probs)
+        slots = np.arange(self.n, dtype=np.uint32)
+        toks = [np.ascontiguousarray(t, np.uint32) for t in self.tokens]
+        fn = (self.be.lib.lib.redukt_backend_forward_batch_probs if self.probs
+              else self.be.lib.lib.redukt_backend_forward_batch)
+        sp, op = ffi._ptr(slots, ctypes.c_uint32), ffi._ptr(out, ctypes.c_float)
+        tps = [ffi._ptr(t, ctypes.c_uint32) for t in toks]
+        assert fn(self.n, sp, tps[0], op, self.vocab) == 0
         t0 = time.perf_counter()
         for t in range(steps):
-            self.be.forward_batch(slots, [int(x) for x in self.tokens[t % len(self.tokens)]], out, probs=self.probs)
+            rc = fn(self.n, sp, tps[t % len(tps)], op, self.vocab)
+            if rc != 0:
+                raise ffi.BackendError(ffi.BackendResult.from_code(rc), "forward_batch")
         return self.n * steps / (time.perf_counter() - t0)
 
     def close(self) -> None:
