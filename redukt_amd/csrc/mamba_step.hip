@@ -87,6 +87,10 @@ constexpr int kInChunk = kInGroups * kRowTile;
 // take 1 (measured on Mamba-130M int8: one group is 1-7 % faster per step from 64 to
 // 1024 streams).  A stream's arithmetic does not depend on the choice.
 constexpr int kOutWideFrom = 80;
+// Chunk-major k_mix_out grid from this many streams per part (measured on Mamba-130M int8,
+// µs per step row-tile / chunk major: 256 streams 917 / 907, 512 streams 1469 / 1446, 1024
+// streams 2750 / 2700; 128 streams, two parts of 64, unchanged).
+constexpr int kOutGroupMajorFrom = 128;
 constexpr int kHeadWaves = 8;              // waves per k_head workgroup (two per SIMD on one staged chunk)
 constexpr int kHeadTiles = 2;              // row tiles per wave in k_head
 // Weight k-pairs each wave keeps in flight (the product loop is unrolled by it): k_mix_in
@@ -1367,6 +1371,7 @@ struct MixOutArgs {
     __bf16* xw;              // xw != null the next consumer's pre-staged activations are
     float* ssp;              // produced here
     int ks_x, tiles;
+    uint32_t gmajor = 0;     // grid (chunks, row tiles) instead of (row tiles, chunks)
 };
 
 // out_proj + residual.  Eight waves share one 16-row tile, each summing an eighth of the
@@ -1624,7 +1629,8 @@ __device__ __forceinline__ void mix_out_body(const MixOutArgs& a, uint32_t t_blk
 
 template <bool Q8, int G, bool FIXED>
 __global__ __launch_bounds__(kOutWaves * kWave) void k_mix_out(MixOutArgs a) {
-    mix_out_body<Q8, G, FIXED, kOutWaves>(a, blockIdx.x, blockIdx.y, NoWait{});
+    const uint32_t t_blk = a.gmajor ? blockIdx.y : blockIdx.x, by = a.gmajor ? blockIdx.x : blockIdx.y;
+    mix_out_body<Q8, G, FIXED, kOutWaves>(a, t_blk, by, NoWait{});
 }
 
 // ---------------------------------------------------------------- persistent step kernel
@@ -2278,6 +2284,13 @@ void build_step(const ModelView& m, Pool& pool, const StepIO& io, std::vector<La
     const uint32_t in_chunks = (n + kInChunk - 1) / kInChunk;
     const int out_g = m.layers[0].out_proj.group == 0 && n >= (uint32_t)kOutWideFrom ? 2 : 1;
     const uint32_t out_chunks = (n + out_g * kRowTile - 1) / (out_g * kRowTile);
+    // k_mix_out's XCD layout: workgroups L and L + 8 share an XCD (and its L2).  Row-tile
+    // major (the default) gives each XCD an eighth of the out_proj weights and every stream
+    // group's gated tiles; chunk major (from kOutGroupMajorFrom streams, when the chunks come
+    // in multiples of 8) gives each XCD an eighth of the stream groups and all the weights.
+    // The first repeats the gated tiles (N x 9 KB), the second the weights (1.2 MB at
+    // Mamba-130M int8), so the second reads less once N x 9 KB passes them.
+    const bool gmajor = n >= (uint32_t)kOutGroupMajorFrom && out_chunks % kXcds == 0;
     out.clear();
     // RMSNorm models take the pre-staged activation path; LayerNorm models norm in the
     // consumer.
@@ -2305,7 +2318,10 @@ void build_step(const ModelView& m, Pool& pool, const StepIO& io, std::vector<La
         out.push_back(Launch::make(fin, dim3(nxb + zb, in_chunks), dim3(kBlock), lds_in, KC_MIX_IN, la.mi));
         out.push_back(scan_launch(L, D, p, n, m.exact_scan, p.glimb, nullptr, p.ssm + li * ssm_layer));
         const void* fo = mix_out_fn(q8, out_g, m.layers[0].out_proj.ks == 2 * kOutWaves * kOutPairs);
-        out.push_back(Launch::make(fo, dim3(L.out_proj.rt, out_chunks), dim3(kOutWaves * kWave), 0, KC_MIX_OUT, la.mo));
+        MixOutArgs mo = la.mo;
+        mo.gmajor = gmajor ? 1u : 0u;
+        out.push_back(Launch::make(fo, gmajor ? dim3(out_chunks, L.out_proj.rt) : dim3(L.out_proj.rt, out_chunks),
+                                   dim3(kOutWaves * kWave), 0, KC_MIX_OUT, mo));
     }
     const TMat& H = *m.head;
     head_index = (int)out.size();
