@@ -87,10 +87,13 @@ constexpr int kInChunk = kInGroups * kRowTile;
 // take 1 (measured on Mamba-130M int8: one group is 1-7 % faster per step from 64 to
 // 1024 streams).  A stream's arithmetic does not depend on the choice.
 constexpr int kOutWideFrom = 80;
-// Chunk-major k_mix_out grid from this many streams per part (measured on Mamba-130M int8,
-// µs per step row-tile / chunk major: 256 streams 917 / 907, 512 streams 1469 / 1446, 1024
-// streams 2750 / 2700; 128 streams, two parts of 64, unchanged).
+// Chunk-major k_mix_out and k_mix_in grids from these many streams per part.  Measured on
+// Mamba-130M int8, µs per step with neither / k_mix_out / both chunk major: 256 streams
+// 917 / 907 / 907, 512 streams 1472 / 1451 / 1449, 1024 streams 2776 / 2723 / 2681; 128
+// streams (two parts of 64) unchanged.  k_mix_in chunk major from 128 streams per part
+// loses at 256 (922 against 908).
 constexpr int kOutGroupMajorFrom = 128;
+constexpr int kInGroupMajorFrom = 512;
 constexpr int kHeadWaves = 8;              // waves per k_head workgroup (two per SIMD on one staged chunk)
 constexpr int kHeadTiles = 2;              // row tiles per wave in k_head
 // Weight k-pairs each wave keeps in flight (the product loop is unrolled by it): k_mix_in
@@ -782,6 +785,7 @@ struct MixInArgs {
     const __bf16* xw;          // pre-staged activations (RMSNorm path)
     const float* ssp;
     int tiles;
+    uint32_t gmajor = 0;       // grid (chunks, blocks) instead of (blocks, chunks)
 };
 
 // in_proj for T row tiles (T = 2 or 4) x kInChunk streams, 4 waves.  The product is split
@@ -1068,7 +1072,8 @@ __device__ __forceinline__ void mix_in_body(const MixInArgs& a, uint32_t bx, uin
 
 template <bool Q8, bool Q8XP, bool PRE, bool GRP, int QP, int T>
 __global__ __launch_bounds__(kBlock) void k_mix_in(MixInArgs a) {
-    mix_in_body<Q8, Q8XP, PRE, GRP, QP, T>(a, blockIdx.x, blockIdx.y, NoWait{});
+    const uint32_t bx = a.gmajor ? blockIdx.y : blockIdx.x, by = a.gmajor ? blockIdx.x : blockIdx.y;
+    mix_in_body<Q8, Q8XP, PRE, GRP, QP, T>(a, bx, by, NoWait{});
 }
 
 // ---------------------------------------------------------------- k_scan
@@ -2291,6 +2296,9 @@ void build_step(const ModelView& m, Pool& pool, const StepIO& io, std::vector<La
     // The first repeats the gated tiles (N x 9 KB), the second the weights (1.2 MB at
     // Mamba-130M int8), so the second reads less once N x 9 KB passes them.
     const bool gmajor = n >= (uint32_t)kOutGroupMajorFrom && out_chunks % kXcds == 0;
+    // k_mix_in the same way: block major repeats each stream group's staged activations
+    // (74 KB) on every XCD, chunk major repeats the in_proj and x_proj weights (2.5 MB).
+    const bool in_gmajor = n >= (uint32_t)kInGroupMajorFrom && in_chunks % kXcds == 0;
     out.clear();
     // RMSNorm models take the pre-staged activation path; LayerNorm models norm in the
     // consumer.
@@ -2315,7 +2323,10 @@ void build_step(const ModelView& m, Pool& pool, const StepIO& io, std::vector<La
         const DLayer& L = m.layers[li];
         const FlowLayer la = layer_args(m, p, n, li, nxb);
         const int zb = L.in_z.rt / in_tiles;
-        out.push_back(Launch::make(fin, dim3(nxb + zb, in_chunks), dim3(kBlock), lds_in, KC_MIX_IN, la.mi));
+        MixInArgs mi = la.mi;
+        mi.gmajor = in_gmajor ? 1u : 0u;
+        out.push_back(Launch::make(fin, in_gmajor ? dim3(in_chunks, nxb + zb) : dim3(nxb + zb, in_chunks), dim3(kBlock),
+                                   lds_in, KC_MIX_IN, mi));
         out.push_back(scan_launch(L, D, p, n, m.exact_scan, p.glimb, nullptr, p.ssm + li * ssm_layer));
         const void* fo = mix_out_fn(q8, out_g, m.layers[0].out_proj.ks == 2 * kOutWaves * kOutPairs);
         MixOutArgs mo = la.mo;
