@@ -25,6 +25,9 @@ enum {
     ORC_PROFILE_Q8_G64 = 1,
     ORC_PROFILE_Q8_ROW = 2,
     ORC_PROFILE_Q8_SMALL = 4,
+    /* RWKV-7 with per-row int8 weights only: int8 activations as well (W8A8,
+     * tensor.rs:1791-1866), the reference's own RWKV-7 Q8 arithmetic. */
+    ORC_PROFILE_W8A8 = 32,
 };
 
 /* ---- scalar math (tensor.rs) ---- */
@@ -81,6 +84,11 @@ void  orc_mat_vec_small(float* out, const float* a, const float* v, int n);
 void  orc_wkv_head(float* S, int n, const float* r, const float* w, const float* kk, const float* a,
                    const float* v, const float* kmod, float* out, float* tmp);
 float orc_lane_sigmoidf(float x);
+/* W8A8 (tensor.rs:1791-1866): quantize v[0..n) to q with one scale (returned); then
+ * out[r] = (float)(exact int32 q[r]·vq) * (scales[r] * v_scale) for a per-row int8 matrix. */
+float orc_quantize_vec_i8(const float* v, int n, int8_t* q);
+void  orc_q8_matvec_a8(const int8_t* q, const float* scales, int rows, int cols, const int8_t* vq, float v_scale,
+                       float* out);
 
 /* ---- RWKV-7 model (rwkv7/model.rs) ---- */
 typedef struct OrcRwkv OrcRwkv;

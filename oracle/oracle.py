@@ -76,6 +76,9 @@ def lib() -> ctypes.CDLL:
         L.orc_l2_normalize_per_head.argtypes = [_f32p, ctypes.c_int, ctypes.c_int]
         L.orc_mat_vec_small.argtypes = [_f32p, _f32p, _f32p, ctypes.c_int]
         L.orc_wkv_head.argtypes = [_f32p, ctypes.c_int] + [_f32p] * 8
+        L.orc_quantize_vec_i8.argtypes = [_f32p, ctypes.c_int, _i8p]
+        L.orc_quantize_vec_i8.restype = ctypes.c_float
+        L.orc_q8_matvec_a8.argtypes = [_i8p, _f32p, ctypes.c_int, ctypes.c_int, _i8p, ctypes.c_float, _f32p]
         L.orc_lane_sigmoidf.argtypes = [ctypes.c_float]
         L.orc_lane_sigmoidf.restype = ctypes.c_float
         L.orc_set_threads.argtypes = [ctypes.c_int]
@@ -134,6 +137,25 @@ def quantize(w, group: int):
     g = ctypes.c_int(0)
     lib().orc_quantize(_p(w), rows, cols, group, _p(q, ctypes.c_int8), _p(sc), ctypes.byref(g))
     return q, sc.reshape(rows, -1), g.value
+
+
+def quantize_vec_i8(v):
+    """quantize_vec_i8_into: (int8 vector, scale)."""
+    v = f32c(v)
+    q = np.empty(v.size, np.int8)
+    sc = lib().orc_quantize_vec_i8(_p(v), v.size, _p(q, ctypes.c_int8))
+    return q, np.float32(sc)
+
+
+def q8_matvec_a8(q, scales, vq, v_scale) -> np.ndarray:
+    """The W8A8 product of a per-row int8 matrix with an already quantized vector."""
+    q = np.ascontiguousarray(q, np.int8)
+    scales = f32c(scales).reshape(-1)
+    vq = np.ascontiguousarray(vq, np.int8)
+    out = np.empty(q.shape[0], np.float32)
+    lib().orc_q8_matvec_a8(_p(q, ctypes.c_int8), _p(scales), q.shape[0], q.shape[1], _p(vq, ctypes.c_int8),
+                           float(v_scale), _p(out))
+    return out
 
 
 def gemv_f32(w, v) -> np.ndarray:

@@ -7,10 +7,12 @@
  * src/domain/tensor.rs (cited at each use) and the GEMV orders of the Mamba part:
  * f32 matrices in dot_avx2_order (tensor.rs:1680-1693, used by mat_vec_mul_into at
  * :1602-1705), int8 weight-only matrices in the q8w order (gemv.rs:490-502).  The reference
- * quantizes RWKV-7 as W8A8 (tensor.rs:105-143, 1819-1866); the int8 profiles here are the
- * weight-only recipe the GPU backend uses, applied to the same matrices the reference
- * quantizes (receptance, key, value, output, FFN key/value, head; LoRAs and the embedding
- * stay f32, model.rs:1004-1058).
+ * quantizes RWKV-7 as W8A8 (tensor.rs:105-143, 1791-1866): with profile bit 5 the per-row
+ * int8 matrices take that path (each input vector quantized to int8 with one scale, exact
+ * int32 dot products, one f32 rescale per row).  Without it the int8 profiles are the
+ * weight-only recipe of the Mamba path.  Either way the quantized matrices are the ones the
+ * reference quantizes (receptance, key, value, output, FFN key/value, head; LoRAs and the
+ * embedding stay f32, model.rs:1004-1058).
  *
  * Weight file: the RWKV-7 container of redukt_amd/rwkv.py (64-byte header, then f32
  * tensors in that module's tensor_order).
@@ -157,6 +159,40 @@ static void matvec_f32(float* out, const float* m, int rows, int cols, const flo
     for (int r = 0; r < rows; r++) out[r] = orc_dot_f32(m + (size_t)r * cols, v, cols);
 }
 
+/* quantize_vec_i8_into (tensor.rs:1791-1800): one scale for the whole vector, amax / 127
+ * (1 for a vector without a nonzero magnitude; NaNs never raise amax), then
+ * q = clamp(round(v * (1 / scale)), -127, 127) with Rust's round (half away from zero, as
+ * C's roundf) and its saturating `as i8` (NaN -> 0). */
+float orc_quantize_vec_i8(const float* v, int n, int8_t* q) {
+    float amax = 0.0f;
+    for (int i = 0; i < n; i++) {
+        const float a = fabsf(v[i]);
+        if (a > amax) amax = a;
+    }
+    const float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
+    const float inv = 1.0f / scale;
+    for (int i = 0; i < n; i++) {
+        float t = roundf(v[i] * inv);
+        if (t < -127.0f) t = -127.0f;
+        if (t > 127.0f) t = 127.0f;
+        q[i] = t != t ? 0 : (int8_t)t;
+    }
+    return scale;
+}
+
+/* q8_mat_vec_mul_scalar_into (tensor.rs:1838-1866): per row the exact int32 sum of
+ * q[r][c] * vq[c], then (float)sum * (scale[r] * v_scale).  The reference's VNNI and AVX2
+ * kernels (:238-330) reach the same integer sums, so every dispatch gives these bits. */
+void orc_q8_matvec_a8(const int8_t* q, const float* scales, int rows, int cols, const int8_t* vq, float v_scale,
+                      float* out) {
+    for (int r = 0; r < rows; r++) {
+        const int8_t* qr = q + (size_t)r * cols;
+        int32_t s = 0;
+        for (int c = 0; c < cols; c++) s += (int32_t)qr[c] * (int32_t)vq[c];
+        out[r] = (float)s * (scales[r] * v_scale);
+    }
+}
+
 /* ---- load ---- */
 
 static void layer_free(RLayer* L) {
@@ -180,6 +216,7 @@ void orc_rwkv_free(OrcRwkv* m) {
 
 OrcRwkv* orc_rwkv_load(const char* path, int profile) {
     if ((profile & 3) == 3) return NULL;
+    if ((profile & ORC_PROFILE_W8A8) && (profile & 3) != ORC_PROFILE_Q8_ROW) return NULL;  /* per-row only */
     FILE* f = fopen(path, "rb");
     if (!f) return NULL;
     uint32_t h[16];
@@ -277,7 +314,19 @@ int orc_rwkv_get_state(const OrcRwkv* m, uint32_t slot, uint32_t layer, float* x
 typedef struct {
     float *x, *ln, *xx, *xr, *xw, *xk, *xv, *xa, *xg, *r, *k, *v, *w, *a, *kk, *kmod, *vout;
     float *outv, *outn, *g, *lorad, *lora, *tm, *cm, *fproj, *fact, *kka, *negkk, *outh;
+    int8_t* vq;         /* the quantized input of a W8A8 projection (max(d, d_ffn)) */
 } Scratch;
+
+/* QuantMatrix::mat_vec_mul_into (quant.rs:321-330) of a quantized matrix: the W8A8 path
+ * with profile bit 5 (q8_mat_vec_mul_into, tensor.rs:1819-1836), else the weight-only one. */
+static void proj(const OrcRwkv* m, const Mat* w, const float* v, float* out, int8_t* vq) {
+    if (m->profile & ORC_PROFILE_W8A8) {
+        const float vs = orc_quantize_vec_i8(v, w->cols, vq);
+        orc_q8_matvec_a8(w->q, w->sc, w->rows, w->cols, vq, vs, out);
+    } else {
+        mat_rows(w, 0, w->rows, v, out);
+    }
+}
 
 /* time_mixing_scratch (model.rs:802-916) for one stream. */
 static void time_mixing(const OrcRwkv* m, const RLayer* L, int layer, Scratch* s, const float* x_prev,
@@ -294,9 +343,9 @@ static void time_mixing(const OrcRwkv* m, const RLayer* L, int layer, Scratch* s
         s->xg[i] = s->ln[i] + s->xx[i] * L->x_g[i];
     }
     /* Step 2: projections. */
-    mat_rows(&L->r, 0, d, s->xr, s->r);
-    mat_rows(&L->k, 0, d, s->xk, s->k);
-    mat_rows(&L->v, 0, d, s->xv, s->v);
+    proj(m, &L->r, s->xr, s->r, s->vq);
+    proj(m, &L->k, s->xk, s->k, s->vq);
+    proj(m, &L->v, s->xv, s->v, s->vq);
     /* Step 3: decay = exp(-0.606531 * sigmoid(w0 + w2·tanh(w1·xw))). */
     const int rw = (int)m->rw, ra = (int)m->ra, rv = (int)m->rv, rg = (int)m->rg;
     matvec_f32(s->lora, L->w1, rw, d, s->xw);
@@ -341,7 +390,7 @@ static void time_mixing(const OrcRwkv* m, const RLayer* L, int layer, Scratch* s
     }
     /* Step 12: gate and output projection. */
     for (int i = 0; i < d; i++) s->xx[i] = s->outn[i] * s->g[i];
-    mat_rows(&L->o, 0, d, s->xx, s->tm);
+    proj(m, &L->o, s->xx, s->tm, s->vq);
 }
 
 /* channel_mixing_scratch (model.rs:919-925; squared_relu_into tensor.rs:1386-1388). */
@@ -349,12 +398,12 @@ static void channel_mixing(const OrcRwkv* m, const RLayer* L, Scratch* s, const 
     const int d = (int)m->d, ff = (int)m->f;
     for (int i = 0; i < d; i++) s->xx[i] = x_prev[i] - s->ln[i];
     for (int i = 0; i < d; i++) s->xr[i] = s->ln[i] + s->xx[i] * L->ffn_x_k[i];
-    mat_rows(&L->fk, 0, ff, s->xr, s->fproj);
+    proj(m, &L->fk, s->xr, s->fproj, s->vq);
     for (int i = 0; i < ff; i++) {
         const float r = s->fproj[i] > 0.0f ? s->fproj[i] : 0.0f;  /* f32::max(x, 0): NaN -> 0 */
         s->fact[i] = r * r;
     }
-    mat_rows(&L->fv, 0, d, s->fact, s->cm);
+    proj(m, &L->fv, s->fact, s->cm, s->vq);
 }
 
 typedef struct {
@@ -376,7 +425,8 @@ static void stream_step(void* ctx, int b) {
     if ((int)m->rg > lmax) lmax = (int)m->rg;
     const size_t dsz = (size_t)d;
     float* buf = (float*)calloc(dsz * 24 + (size_t)lmax + 2 * (size_t)ff + 3 * (size_t)N, sizeof(float));  /* kka: 3N */
-    if (!buf) return;
+    int8_t* vq = (int8_t*)malloc(dsz > (size_t)ff ? dsz : (size_t)ff);
+    if (!buf || !vq) { free(buf); free(vq); return; }
     Scratch s;
     float* p = buf;
     float** dvecs[] = {&s.x, &s.ln, &s.xx, &s.xr, &s.xw, &s.xk, &s.xv, &s.xa, &s.xg, &s.r, &s.k, &s.v, &s.w,
@@ -388,6 +438,7 @@ static void stream_step(void* ctx, int b) {
     s.kka = p; p += N;
     s.negkk = p; p += N;
     s.outh = p;
+    s.vq = vq;
 
     memcpy(s.x, m->emb + (size_t)j->tokens[b] * d, sizeof(float) * d);
     float* vfirst = m->v_first + (size_t)slot * d;
@@ -407,8 +458,9 @@ static void stream_step(void* ctx, int b) {
         for (int c = 0; c < d; c++) s.x[c] += s.cm[c];
     }
     orc_layer_norm(s.ln, s.x, m->ln_out_w, m->ln_out_b, d, 1e-5f);
-    mat_rows(&m->head, 0, (int)m->vocab, s.ln, j->out + (size_t)b * m->vocab);
+    proj(m, &m->head, s.ln, j->out + (size_t)b * m->vocab, s.vq);
     free(buf);
+    free(vq);
 }
 
 int orc_rwkv_forward(OrcRwkv* m, uint32_t n, const uint32_t* slots, const uint32_t* tokens, float* out) {

@@ -17,14 +17,37 @@ def _ln(x, w, b, eps=1e-5):
     return (x - mu) / np.sqrt(var + eps) * w + b
 
 
+def _round_away(x):
+    return np.where(x < 0, -np.floor(-x + 0.5), np.floor(x + 0.5))
+
+
+class _A8:
+    """A per-row int8 matrix applied to an activation quantized with one scale per vector
+    (src/domain/tensor.rs:1791-1866), in float64: q(v) = clamp(round(v * 127 / max|v|)),
+    W v ~ (Wq q(v)) * s_row * max|v| / 127."""
+
+    def __init__(self, q, scales):
+        self.q = np.asarray(q, np.float64)
+        self.s = np.asarray(scales, np.float64).reshape(-1)
+
+    def __matmul__(self, v):
+        amax = float(np.max(np.abs(v))) if v.size else 0.0
+        scale = amax / 127.0 if amax > 0 else 1.0
+        qv = np.clip(_round_away(v / scale), -127, 127)
+        return (self.q @ qv) * self.s * scale
+
+
 class F64Rwkv:
-    def __init__(self, dims, tensors, mats=None):
+    def __init__(self, dims, tensors, mats=None, a8=None):
         """tensors: the file's f32 arrays; mats: optional replacements (float arrays) for the
-        quantized matrices, e.g. their dequantized values."""
+        quantized matrices, e.g. their dequantized values; a8: optional {name: (int8 matrix,
+        per-row scales)} applied with int8 activations instead."""
         self.dims = dims
         t = {k: np.asarray(v, np.float64) for k, v in tensors.items()}
         if mats:
             t.update({k: np.asarray(v, np.float64) for k, v in mats.items()})
+        if a8:
+            t.update({k: _A8(q, sc) for k, (q, sc) in a8.items()})
         self.t = t
         self.states = {}
 
