@@ -112,8 +112,17 @@ int32_t redukt_backend_forward_batch(uint32_t n_streams, const uint32_t* slots, 
  * d_model / d_inner in {64, 96, 128, 192, 256, 384, 768, 1024, 1536, 3072}; INIT_FAILED
  * otherwise. */
 #define BACKEND_PROFILE_GEMV 16u
+/* Profile bit 5: RWKV-7 in the reference's own int8 arithmetic, W8A8 (Q8Tensor and
+ * q8_mat_vec_mul_into, src/domain/tensor.rs:105-143, 1791-1866): every per-row int8
+ * projection quantizes its input vector to int8 with one scale, sums exact int32 products
+ * on the matrix cores and rescales once per row; the rest of the step keeps the reference's
+ * operation order, its sequential sums included, so the logits equal the CPU path's bit for
+ * bit.  Needs per-row weights (low bits 2) and LoRA ranks in multiples of 8; INIT_FAILED for
+ * Mamba models or another profile. */
+#define BACKEND_PROFILE_W8A8 32u
 
-/* redukt_backend_init with an explicit weight profile (the model file stays F32). */
+/* redukt_backend_init with an explicit weight profile (the model file stays F32); a profile
+ * with a bit above bit 5 -> INVALID_ARGUMENT. */
 int32_t redukt_backend_init_ex(const uint8_t* weights_path, int32_t device_id, uint32_t profile,
                                BackendInfo* info_out);
 

@@ -58,6 +58,7 @@ struct Model {
     TMat emb, head_own;
     GMat g_emb, g_head_own;   // the wavefront-GEMV tier's embedding / untied head
     bool gemv = false;        // weight profile bit 4
+    bool r_a8 = false;        // weight profile bit 5: the RWKV-7 W8A8 tier
     bool tied = true;
     float* norm_f_w = nullptr;
     float* norm_f_b = nullptr;
@@ -187,6 +188,20 @@ bool make_tmat(TMat& m, const float* w, int rows, int cols, int quant_group) {
     m.w = dev_upload(t.data(), t.size());
     m.scales = dev_upload(scp.data(), scp.size());
     return m.w && m.scales;
+}
+
+// Lay a row-major [rows][cols] f32 matrix out for the exact LoRA kernels (LMat:
+// [cols / 8][rows8][8]) and upload it; cols must be a multiple of 8.
+bool make_lmat(LMat& m, const float* w, int rows, int cols) {
+    if (cols % 8 != 0) return false;
+    m.rows = rows;
+    m.cols = cols;
+    m.rows8 = (rows + 7) / 8 * 8;
+    std::vector<float> t((size_t)m.rows8 * cols, 0.0f);
+    for (int r = 0; r < rows; r++)
+        for (int c = 0; c < cols; c++) t[((size_t)(c / 8) * m.rows8 + r) * 8 + c % 8] = w[(size_t)r * cols + c];
+    m.w = dev_upload(t.data(), t.size());
+    return m.w != nullptr;
 }
 
 // Lay a row-major [rows][cols] matrix out for the wavefront-GEMV kernels (see GMat) and
@@ -416,6 +431,12 @@ int load_rwkv(const std::string& path, uint32_t profile) {
     G.dims.d = R.d;
     G.dims.nl = R.nl;
     G.dims.tokenizer = h[14];
+    G.r_a8 = (profile & BACKEND_PROFILE_W8A8) != 0;
+    if (G.r_a8 && (R.lora[0] % 8 || R.lora[1] % 8 || R.lora[2] % 8 || R.lora[3] % 8)) {
+        log("the W8A8 tier needs LoRA ranks in multiples of 8");
+        fclose(f);
+        return -2;
+    }
     const int quant = (profile & 3) == 0 ? 0 : ((profile & 3) == 1 ? 64 : (int)0x7fffffff);
     auto qgroup = [&](int cols) { return quant == 0 ? 0 : (quant == 0x7fffffff ? cols : quant); };
     const size_t V = R.vocab, d = R.d, ff = R.f;
@@ -430,6 +451,13 @@ int load_rwkv(const std::string& path, uint32_t profile) {
         std::vector<float> t = rd.read(rows * cols);
         ok = ok && rd.ok && make_tmat(m, t.data(), (int)rows, (int)cols, group);
     };
+    // A LoRA stage: tiled for the matrix cores, or laid out for the exact kernels of the
+    // W8A8 tier.
+    auto lora = [&](RLayer& L, int k, bool first, size_t rows, size_t cols) {
+        std::vector<float> t = rd.read(rows * cols);
+        if (G.r_a8) ok = ok && rd.ok && make_lmat(first ? L.x1[k] : L.x2[k], t.data(), (int)rows, (int)cols);
+        else ok = ok && rd.ok && make_tmat(first ? L.l1[k] : L.l2[k], t.data(), (int)rows, (int)cols, 0);
+    };
     mat(G.r_emb, V, d, 0);
     G.rlayers.assign(R.nl, RLayer{});
     for (uint32_t i = 0; ok && i < R.nl; i++) {
@@ -437,16 +465,16 @@ int load_rwkv(const std::string& path, uint32_t profile) {
         vec(L.ln1_w); vec(L.ln1_b); vec(L.ln2_w); vec(L.ln2_b);
         for (int k = 0; k < 6; k++) vec(L.mix[k]);
         vec(L.w0);
-        mat(L.l1[kLoraW], R.lora[kLoraW], d, 0);
-        mat(L.l2[kLoraW], d, R.lora[kLoraW], 0);
+        lora(L, kLoraW, true, R.lora[kLoraW], d);
+        lora(L, kLoraW, false, d, R.lora[kLoraW]);
         vec(L.a0);
-        mat(L.l1[kLoraA], R.lora[kLoraA], d, 0);
-        mat(L.l2[kLoraA], d, R.lora[kLoraA], 0);
+        lora(L, kLoraA, true, R.lora[kLoraA], d);
+        lora(L, kLoraA, false, d, R.lora[kLoraA]);
         vec(L.v0);
-        mat(L.l1[kLoraV], R.lora[kLoraV], d, 0);
-        mat(L.l2[kLoraV], d, R.lora[kLoraV], 0);
-        mat(L.l1[kLoraG], R.lora[kLoraG], d, 0);
-        mat(L.l2[kLoraG], d, R.lora[kLoraG], 0);
+        lora(L, kLoraV, true, R.lora[kLoraV], d);
+        lora(L, kLoraV, false, d, R.lora[kLoraV]);
+        lora(L, kLoraG, true, R.lora[kLoraG], d);
+        lora(L, kLoraG, false, d, R.lora[kLoraG]);
         vec(L.k_k); vec(L.k_a); vec(L.r_k);
         mat(L.r, d, d, qgroup((int)d));
         mat(L.k, d, d, qgroup((int)d));
@@ -624,7 +652,7 @@ size_t slot_words(uint32_t cap) { return ((size_t)cap + kSlotWordAlign - 1) / kS
 bool pool_alloc_rwkv(Pool& p, uint32_t cap) {
     const RDims& R = G.rdims;
     const size_t n = cap, d = R.d;
-    const RwkvSizes z = rwkv_sizes(R, cap);
+    const RwkvSizes z = rwkv_sizes(R, cap, G.r_a8);
     p = Pool{};
     p.cap = cap;
     p.scap = cap + 1;
@@ -643,6 +671,11 @@ bool pool_alloc_rwkv(Pool& p, uint32_t cap) {
         c.take(p.ffnl, z.mixl);
         c.take(p.actl, z.actl);
         c.take(p.headl, z.mixl);
+        c.take(p.mixf, z.mixf);
+        c.take(p.lorah, z.lorah);
+        c.take(p.aq, z.aq);
+        c.take(p.as, z.as);
+        c.take(p.actf, z.actf);
         c.take(p.out, n * R.vocab);
         c.take(p.x_att, z.state_d);
         c.take(p.x_ffn, z.state_d);
@@ -712,7 +745,7 @@ hipError_t run_step(Pool& p, uint32_t n, const uint32_t* slots, const uint32_t* 
                     bool check) {
     StepIO io{n, slots, tokens, out, probs, check, G.d_err};
     if (G.kind == kKindRwkv) {
-        const RwkvStep src(RwkvView{&G.rdims, G.rlayers.data(), &G.r_emb, &G.r_head, G.ln_out_w, G.ln_out_b});
+        const RwkvStep src(RwkvView{&G.rdims, G.rlayers.data(), &G.r_emb, &G.r_head, G.ln_out_w, G.ln_out_b, G.r_a8});
         return G.runner.run(src, p, io, G.stream, &G.probe);
     }
     if (G.gemv) {
@@ -927,6 +960,11 @@ int init_common(const uint8_t* weights_path, int32_t device_id, uint32_t profile
         free_model();
         return BACKEND_INIT_FAILED;
     }
+    if ((profile & BACKEND_PROFILE_W8A8) && (G.kind != kKindRwkv || (profile & 3) != BACKEND_PROFILE_Q8_ROW)) {
+        log("the W8A8 tier serves RWKV-7 with per-row int8 weights only");
+        free_model();
+        return BACKEND_INIT_FAILED;
+    }
     const int lr = G.kind == kKindRwkv ? load_rwkv(path, profile) : load_weights(path, profile);
     if (lr != 0) {
         free_model();
@@ -949,7 +987,7 @@ int init_common(const uint8_t* weights_path, int32_t device_id, uint32_t profile
     info_out->hidden_dim = G.dims.d;
     static const char* names[2][3] = {{"hip-gfx950-mamba-f32", "hip-gfx950-mamba-q8", "hip-gfx950-mamba-q8row"},
                                        {"hip-gfx950-rwkv7-f32", "hip-gfx950-rwkv7-q8", "hip-gfx950-rwkv7-q8row"}};
-    const char* name = names[G.kind == kKindRwkv ? 1 : 0][profile & 3];
+    const char* name = G.r_a8 ? "hip-gfx950-rwkv7-w8a8" : names[G.kind == kKindRwkv ? 1 : 0][profile & 3];
     memcpy(info_out->name, name, strlen(name));
     size_t fr = 0, tot = 0;
     (void)hipMemGetInfo(&fr, &tot);
@@ -1046,7 +1084,7 @@ int32_t redukt_backend_forward_batch(uint32_t n_streams, const uint32_t* slots, 
 
 int32_t redukt_backend_init_ex(const uint8_t* weights_path, int32_t device_id, uint32_t profile,
                                BackendInfo* info_out) {
-    if (profile > 31u) return BACKEND_INVALID_ARGUMENT;
+    if (profile > 63u) return BACKEND_INVALID_ARGUMENT;   // bits 0-5
     return init_common(weights_path, device_id, profile, info_out);
 }
 

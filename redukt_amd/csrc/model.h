@@ -131,6 +131,12 @@ struct Pool {
     __bf16* ffnl = nullptr;      // [gcap][ks_d][3][64][8] channel-mix input
     __bf16* actl = nullptr;      // [gcap][ks_ffn][3][64][8] squared-ReLU activations
     __bf16* headl = nullptr;     // [gcap][ks_d][3][64][8] final LayerNorm output
+    // RWKV-7 W8A8 tier (instead of the limb buffers above)
+    float* mixf = nullptr;       // [4][cap][d] LoRA inputs x_w, x_a, x_g, x_v (f32)
+    float* lorah = nullptr;      // [cap][sum of ranks] first LoRA stages after their activation
+    int8_t* aq = nullptr;        // int8 activations: kAqAct x [rows16][dp], then [rows16][fp]
+    float* as = nullptr;         // their scales, kAqVecs x [cap]
+    float* actf = nullptr;       // [cap][d_ffn] squared-ReLU activations (f32)
     float* out = nullptr;        // [cap][vocab] logits or probabilities
     uint32_t* slots = nullptr;   // [cap] slots of the current step (validated copy)
     uint32_t* d_slots = nullptr; // [2 cap] H2D target of the synchronous entry points: n slots, then n tokens
@@ -173,6 +179,15 @@ struct RDims {
 
 enum { kLoraW = 0, kLoraA = 1, kLoraG = 2, kLoraV = 3 };
 
+// A LoRA matrix for the element-wise-exact kernels of the RWKV-7 W8A8 tier: f32, laid out
+// [cols / 8][rows8][8] (rows8 = rows rounded up to 8, zero rows past `rows`; cols a
+// multiple of 8), so the eight lanes that own the eight column residues of one row read 32
+// contiguous bytes and the wave's eight rows 256.
+struct LMat {
+    int rows = 0, cols = 0, rows8 = 0;
+    float* w = nullptr;
+};
+
 struct RLayer {
     float *ln1_w = nullptr, *ln1_b = nullptr, *ln2_w = nullptr, *ln2_b = nullptr;
     float* mix[6] = {};               // x_r, x_w, x_k, x_v, x_a, x_g
@@ -182,6 +197,7 @@ struct RLayer {
     TMat l1[4];                       // first LoRA stages [rank][d] (F32): w1, a1, g1, v1
     TMat l2[4];                       // second LoRA stages [d][rank] (F32): w2, a2, g2, v2
     TMat fk, fv;                      // [d_ffn][d], [d][d_ffn]
+    LMat x1[4], x2[4];                // the LoRA stages of the W8A8 tier (l1/l2 stay empty there)
 };
 
 struct RwkvView {
@@ -191,14 +207,22 @@ struct RwkvView {
     const TMat* head;      // [vocab][d]
     const float* ln_out_w;
     const float* ln_out_b;
+    bool a8;               // the W8A8 tier: int8 activations, element-wise exact
 };
 
-// Scratch and state sizes of an RWKV-7 pool of `cap` streams (elements).
+// Scratch and state sizes of an RWKV-7 pool of `cap` streams (elements).  The limb
+// buffers serve the matrix-core tiers, the a8 ones the W8A8 tier (the other set is empty).
 struct RwkvSizes {
     size_t state_d, wkv, mixl, loral, lora_off[4], gatedl, actl;
     int ks_d, ks_f, ks_lora[4];
+    // W8A8: padded row lengths of the int8 activations, their rows (cap rounded up to 16),
+    // the first LoRA stages' offsets in one [cap][lora_sum] row, and the buffer sizes
+    size_t dp, fp, rows16, lh_off[4], lora_sum, mixf, lorah, aq, as, actf;
 };
-RwkvSizes rwkv_sizes(const RDims& d, uint32_t cap);
+// int8 activation vectors of the W8A8 tier, each [rows16][dp] in Pool::aq (act: [rows16][fp]
+// after them), with one scale per stream in Pool::as.
+enum { kAqR = 0, kAqK = 1, kAqV = 2, kAqGated = 3, kAqFfn = 4, kAqHead = 5, kAqAct = 6, kAqVecs = 7 };
+RwkvSizes rwkv_sizes(const RDims& d, uint32_t cap, bool a8);
 
 struct ModelView {
     const Dims* dims;
@@ -294,6 +318,8 @@ struct RwkvStep final : StepSource {
     RwkvView m;
     explicit RwkvStep(const RwkvView& v) : m(v) {}
     void build(Pool& p, const StepIO& io, std::vector<Launch>& out, int& io_i, int& head_i, int& sm_i) const override;
+    // The W8A8 tier's step (rwkv_a8.hip).
+    void build_a8(Pool& p, const StepIO& io, std::vector<Launch>& out, int& io_i, int& head_i, int& sm_i) const;
 };
 
 // Most parts a step is split into: one per hardware queue a process gets by default.

@@ -28,13 +28,14 @@
 #include "mfma_common.h"
 #include "model.h"
 #include "portable_math.h"
+#include "rwkv_common.h"
 #include "step.h"
 
 #pragma clang fp contract(off)
 
 namespace rdk {
 
-RwkvSizes rwkv_sizes(const RDims& D, uint32_t cap) {
+RwkvSizes rwkv_sizes(const RDims& D, uint32_t cap, bool a8) {
     RwkvSizes z{};
     const size_t gcap = (cap + 15) / 16;
     auto ks_of = [](uint32_t cols) { return (int)((cols + kKAlign - 1) / kKAlign * (kKAlign / kKStep)); };
@@ -43,16 +44,30 @@ RwkvSizes rwkv_sizes(const RDims& D, uint32_t cap) {
     // Recurrent state over cap + 1 slots: slot cap is the pool's scratch slot.
     z.state_d = (size_t)(cap + 1) * D.nl * D.d;
     z.wkv = (size_t)(cap + 1) * D.nl * D.h * D.n * D.n;
-    z.mixl = gcap * z.ks_d * 3 * 512;
-    z.gatedl = z.mixl;
-    z.actl = gcap * z.ks_f * 3 * 512;
-    size_t off = 0;
+    size_t off = 0, loff = 0;
     for (int i = 0; i < 4; i++) {
         z.ks_lora[i] = ks_of(D.lora[i]);
         z.lora_off[i] = off;
         off += gcap * z.ks_lora[i] * 3 * 512;
+        z.lh_off[i] = loff;
+        loff += D.lora[i];
     }
-    z.loral = off;
+    z.lora_sum = loff;
+    z.dp = (size_t)z.ks_d * kKStep;
+    z.fp = (size_t)z.ks_f * kKStep;
+    z.rows16 = gcap * 16;
+    if (a8) {
+        z.mixf = 4 * (size_t)cap * D.d;
+        z.lorah = (size_t)cap * z.lora_sum;
+        z.aq = z.rows16 * (6 * z.dp + z.fp);
+        z.as = (size_t)kAqVecs * cap;
+        z.actf = (size_t)cap * D.f;
+    } else {
+        z.mixl = gcap * z.ks_d * 3 * 512;
+        z.gatedl = z.mixl;
+        z.actl = gcap * z.ks_f * 3 * 512;
+        z.loral = off;
+    }
     return z;
 }
 
@@ -160,7 +175,6 @@ const void* shift_fn(int nmix) {
 // ---------------------------------------------------------------- projections
 
 enum { PROJ_STORE = 0, PROJ_RESID = 1, PROJ_LIMBS = 2 };
-enum { ACT_NONE = 0, ACT_TANH = 1, ACT_SIGMOID = 2, ACT_RELU2 = 3 };
 
 struct ProjSeg {
     TMat w;
@@ -178,20 +192,6 @@ struct ProjArgs {
     int nseg;
     uint32_t n;
 };
-
-// tanh_inplace / sigmoid_inplace (tensor.rs:1007-1038) on element r of a length-`len`
-// vector: lane form on the 8-aligned body, portable form on the tail.
-__device__ __forceinline__ float activate(int act, float v, int r, int len) {
-    const bool body = r < len / 8 * 8;
-    if (act == ACT_TANH)
-        return body ? lane_sigmoid_f(v * 2.0f) * 2.0f - 1.0f : 2.0f * (1.0f / (1.0f + exp_f(-(2.0f * v)))) - 1.0f;
-    if (act == ACT_SIGMOID) return body ? lane_sigmoid_f(v) : 1.0f / (1.0f + exp_f(-v));
-    if (act == ACT_RELU2) {
-        const float r2 = v > 0.0f ? v : 0.0f;  // f32::max(v, 0): NaN -> 0
-        return r2 * r2;
-    }
-    return v;
-}
 
 // One 16-row tile x 16 streams.  Eight waves each take an eighth of the k-pairs (limb
 // orders in separate accumulators), with kProjPairs pairs of weight and activation
@@ -426,10 +426,14 @@ struct ProjBuilder {
 }  // namespace
 
 void RwkvStep::build(Pool& p, const StepIO& io, std::vector<Launch>& out, int& io_i, int& head_i, int& sm_i) const {
+    if (m.a8) {
+        build_a8(p, io, out, io_i, head_i, sm_i);
+        return;
+    }
     const RDims& D = *m.dims;
     const uint32_t n = io.n;
     const int d = (int)D.d;
-    const RwkvSizes z = rwkv_sizes(D, p.cap);
+    const RwkvSizes z = rwkv_sizes(D, p.cap, false);
     out.clear();
     io_i = (int)out.size();
     out.push_back(embed_launch(*m.emb, p, io, nullptr, nullptr, nullptr, 0, 0));

@@ -1,0 +1,185 @@
+"""The RWKV-7 W8A8 tier (profile bit 5 with per-row int8 weights) on the GPU, through the
+C ABI, against the oracle's W8A8 path (the reference's own RWKV-7 Q8 arithmetic,
+src/domain/tensor.rs:105-143, 1791-1866).
+
+Every matrix product of the tier is an exact integer sum and every other operation follows
+the reference's order, sums included, so the bar is bit-exact equality with the oracle:
+logits at every step and every stream, the recurrent state of every layer, on a small
+model, a g1k model and the full-width RWKV-7 0.1B (vocabulary 65,536), with periodic
+resets, slots in any order and batches of any size.  The probability vector is held to
+the tolerance of the other tiers (the softmax is shared with them).
+"""
+import dataclasses
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from redukt_amd import ffi, hip, rwkv
+
+pytestmark = pytest.mark.gpu
+
+A8 = ffi.PROFILE_Q8_ROW | ffi.PROFILE_W8A8
+SMALL = rwkv.RwkvDims(vocab=300, d_model=128, n_layer=2, head_size=64, d_ffn=256, lora_w=16, lora_a=16,
+                      lora_v=8, lora_g=32)
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+@pytest.fixture(scope="module")
+def models(tmp_path_factory):
+    assert hip.device_count() > 0, "no GPU visible"
+    d = tmp_path_factory.mktemp("rwkv_a8")
+    out = {"small": str(d / "small.rbin"), "g1k": str(d / "g1k.rbin"), "b01": str(d / "b01.rbin"),
+           "odd": str(d / "odd.rbin")}
+    rwkv.write_synthetic(out["small"], SMALL, seed=1)
+    rwkv.write_synthetic(out["g1k"], dataclasses.replace(SMALL, g1k=True, n_layer=3), seed=2)
+    rwkv.write_synthetic(out["b01"], rwkv.RWKV7_0_1B, seed=0)
+    rwkv.write_synthetic(out["odd"], dataclasses.replace(SMALL, lora_v=12), seed=3)
+    return out
+
+
+def first_diff(g, c):
+    bad = np.flatnonzero(bits(g).ravel() != bits(c).ravel())
+    if not bad.size:
+        return None
+    i = int(bad[0])
+    return i, float(g.ravel()[i]), float(c.ravel()[i]), int(bad.size)
+
+
+def run_equal(be, orc, n, steps, tok_fn, slots=None, states=()):
+    slots = slots or list(range(n))
+    for t in range(steps):
+        toks = [tok_fn(s, t) for s in range(n)]
+        g = np.empty((n, be.vocab), np.float32)
+        be.forward_batch(slots, toks, g)
+        c = orc.forward(slots, toks)
+        assert first_diff(g, c) is None, (t, first_diff(g, c))
+    for s in states:
+        for layer in range(orc.n_layer):
+            for got, want, what in zip(be.get_rwkv_state(s, layer, orc.d_model, orc.n_head), orc.state(s, layer),
+                                       ("x_att", "wkv", "x_ffn")):
+                assert np.array_equal(bits(got), bits(want)), (s, layer, what)
+
+
+@pytest.mark.parametrize("name", ["small", "g1k"])
+def test_w8a8_bit_exact_small(models, name):
+    path = models[name]
+    with ffi.PluginBackend(path, profile=A8) as be:
+        assert be.info.name_str() == "hip-gfx950-rwkv7-w8a8"
+        orc = O.RwkvOracle(path, A8, cap=19)
+        be.batch_init(19)
+        run_equal(be, orc, 19, 8, lambda s, t: (s * 37 + t * 101 + 3) % be.vocab, states=(0, 7, 18))
+        orc.close()
+
+
+def test_w8a8_bit_exact_rwkv7_0_1b(models):
+    path = models["b01"]
+    with ffi.PluginBackend(path, profile=A8) as be:
+        assert be.vocab == 65536
+        orc = O.RwkvOracle(path, A8, cap=40)
+        be.batch_init(40)
+        rng = np.random.default_rng(5)
+        # 40 streams: two full groups of 16 and a partial one; slots in scrambled order
+        slots = [int(s) for s in rng.permutation(40)]
+        orc_slots = slots
+        for t in range(4):
+            toks = [int(x) for x in rng.integers(0, 65536, 40)]
+            g = np.empty((40, 65536), np.float32)
+            be.forward_batch(slots, toks, g)
+            c = orc.forward(orc_slots, toks)
+            assert first_diff(g, c) is None, (t, first_diff(g, c))
+        for s in (slots[0], slots[39]):
+            for layer in (0, 11):
+                for got, want in zip(be.get_rwkv_state(s, layer, 768, 12), orc.state(s, layer)):
+                    assert np.array_equal(bits(got), bits(want)), (s, layer)
+        orc.close()
+
+
+def test_w8a8_batch_sizes_and_v1(models):
+    """One stream's bits do not depend on the batch it runs in, its position or its slot,
+    and the v1 single-stream entry point gives the same bits."""
+    path = models["small"]
+    with ffi.PluginBackend(path, profile=A8) as be:
+        v = be.vocab
+        seq = [(53 * i + 7) % v for i in range(6)]
+        out = np.empty(v, np.float32)
+        be.lib.lib.redukt_backend_reset_state()
+        v1 = []
+        for t in seq:
+            assert be.lib.lib.redukt_backend_forward(t, out.ctypes.data_as(ffi._f32p), v) == ffi.BackendResult.OK
+            v1.append(out.copy())
+        be.batch_init(40)
+        rng = np.random.default_rng(1)
+        for n, pos in ((1, 0), (16, 15), (17, 16), (40, 23)):
+            be.batch_reset(None)
+            slots = [int(s) for s in rng.permutation(40)[:n]]
+            for i, t in enumerate(seq):
+                toks = [int(x) for x in rng.integers(0, v, n)]
+                toks[pos] = t
+                g = np.empty((n, v), np.float32)
+                be.forward_batch(slots, toks, g)
+                assert np.array_equal(bits(g[pos]), bits(v1[i])), (n, pos, i)
+
+
+def test_w8a8_periodic_reset_and_probabilities(models):
+    """The host's tick schedule (plugin_backend/model.rs:44-49) against the oracle's
+    periodic reset, bit for bit; odd steps hand back the probability vector."""
+    path = models["small"]
+    with ffi.PluginBackend(path, profile=A8) as be:
+        orc = O.RwkvOracle(path, A8, cap=6)
+        orc.set_reset_every(3)
+        be.prepare_streams(6)
+        states = [be.create_state() for _ in range(6)]
+        assert [st.slot for st in states] == list(range(6))
+        for st in states:
+            st.set_reset_every(3)
+        for t in range(8):
+            toks = [(s * 31 + t * 17 + 1) % be.vocab for s in range(6)]
+            c = orc.forward(list(range(6)), toks)
+            g = np.empty((6, be.vocab), np.float32)
+            if t % 2 == 0:
+                be.forward_multi(toks, states, g)
+                assert first_diff(g, c) is None, (t, first_diff(g, c))
+            else:
+                for st in states:
+                    st.tick()
+                be.forward_batch([st.slot for st in states], toks, g, probs=True)
+                ref = np.stack([O.softmax(r) for r in c])
+                assert float(np.max(np.abs(g - ref).sum(axis=-1))) <= 1e-4
+                assert np.allclose(g.sum(axis=-1), 1.0, atol=1e-5)
+        orc.close()
+
+
+def test_w8a8_run_to_run(models):
+    runs = []
+    for _ in range(2):
+        with ffi.PluginBackend(models["small"], profile=A8) as be:
+            be.batch_init(8)
+            g = np.empty((8, be.vocab), np.float32)
+            outs = []
+            for t in range(4):
+                be.forward_batch(list(range(8)), [(s * 7 + t * 13) % be.vocab for s in range(8)], g)
+                outs.append(g.copy())
+            runs.append(np.stack(outs))
+    assert np.array_equal(bits(runs[0]), bits(runs[1]))
+
+
+def test_w8a8_init_rules(models, tmp_path):
+    lib = ffi.PluginLibrary()
+    try:
+        # Mamba models, group-64 weights and F32 have no W8A8 tier
+        mamba = str(tmp_path / "m.rbin")
+        from redukt_amd import rbin, synth
+        synth.write_synthetic_mamba(mamba, rbin.MambaDims(vocab=300, d_model=64, n_layer=1), seed=1)
+        for path, prof in ((mamba, A8), (models["small"], ffi.PROFILE_W8A8 | 1), (models["small"], ffi.PROFILE_W8A8),
+                           (models["odd"], A8)):
+            with pytest.raises(ffi.BackendError):
+                lib.init(path, profile=prof)
+            lib.free()
+        info = lib.init(models["odd"], profile=ffi.PROFILE_Q8_ROW)   # rank 12 is fine without W8A8
+        assert info.name_str() == "hip-gfx950-rwkv7-q8row"
+    finally:
+        lib.free()
