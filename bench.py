@@ -37,7 +37,7 @@ METRIC = "Mamba-130M tok/s at batch 1/32/128 (F32 & Q8); % of HBM roofline"
 HBM_PEAK_GBS = 8000.0
 RESET_PERIOD = 4096
 PROFILES = {"f32": 0, "q8": 1, "q8row": 2, "q8row-all": 6, "q8-all": 5,
-            "f32-gemv": 16, "q8row-gemv": 18, "q8row-all-gemv": 22}
+            "f32-gemv": 16, "q8row-gemv": 18, "q8row-all-gemv": 22, "q8row-w8a8": 34}
 
 
 def log(msg: str) -> None:
@@ -101,6 +101,8 @@ def launches_per_step(dims, name: str, mamba: bool, profile: int) -> int:
     L = dims.n_layer
     if mamba:
         return L if name in ("mix_in", "scan", "mix_out") else 1
+    if profile & ffi.PROFILE_W8A8:                        # + ln_out, staged as int8 for the head
+        return {"shift": 2 * L + 1, "proj": 5 * L, "wkv": L}.get(name, 1)
     ws = (profile & 3) == 2 and dims.d_model <= 768       # the weights-stationary head needs ln_out staged
     return {"shift": 2 * L + (1 if ws else 0), "proj": 5 * L, "wkv": L}.get(name, 1)
 
@@ -127,6 +129,17 @@ def rwkv_algorithmic_bytes(dims, profile: int, n: int) -> dict:
     d, f, V, L, H = dims.d_model, dims.d_ffn, dims.vocab, dims.n_layer, dims.n_head
     w = rwkv_weight_bytes(dims, profile)
     R = dims.lora_w + dims.lora_a + dims.lora_v + dims.lora_g
+    if profile & ffi.PROFILE_W8A8:
+        # int8 activations out of the LayerNorms (1 byte), f32 elsewhere.  Per stream and
+        # layer: r/k/v + LoRA 1 (3d int8 + 4d f32 in, 3d + R out), LoRA 2 (R in, 4d out), output
+        # (d f32 in, x read and written), FFN key (d int8 in, f out), FFN value (f in, x read
+        # and written)
+        proj = w["proj"] + n * L * (3 * d + 4 * (4 * d + 3 * d + R) + 4 * (R + 4 * d) + 4 * d + 4 * 2 * d + d
+                                    + 4 * f + 4 * f + 4 * 2 * d)
+        wkv = L * (n * (2 * H * 64 * 64 * 4 + 4 * (3 * d + 4 * d + 2 * d) + 4 * d) + 9 * d * 4)
+        shift = n * (L * (4 * 3 * d + 3 * d + 4 * 4 * d) + L * (4 * 3 * d + d) + 4 * d + d)
+        return {"embed": n * (w["emb_row"] + d * 4), "proj": proj // (5 * L), "wkv": wkv // L,
+                "shift": shift // (2 * L + 1), "head": w["head"] + n * d + n * V * 4, "softmax": 2 * n * V * 4}
     ws = (profile & 3) == 2 and d <= 768
     proj = w["proj"] + n * L * 4 * (7 * d + 3 * d + 2 * R + 4 * d + 3 * d + d + f + f + 2 * d)
     wkv = L * (n * (2 * H * 64 * 64 * 4 + 8 * d * 4 + 2 * d * 4) + 9 * d * 4)
@@ -475,7 +488,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "i8xi8->i32 + f32" if profile & ffi.PROFILE_W8A8 else "f32",
         "data": "synthetic",
         "config": {"workload": workload, "layers": dims.n_layer,
                    "d_model": dims.d_model, "vocab": vocab, "streams": n, "weight_profile": args.profile,

@@ -675,7 +675,9 @@ bool pool_alloc_rwkv(Pool& p, uint32_t cap) {
         c.take(p.lorah, z.lorah);
         c.take(p.aq, z.aq);
         c.take(p.as, z.as);
+        c.take(p.gatedf, z.gatedf);
         c.take(p.actf, z.actf);
+        c.take(p.pmax, z.pmax);
         c.take(p.out, n * R.vocab);
         c.take(p.x_att, z.state_d);
         c.take(p.x_ffn, z.state_d);

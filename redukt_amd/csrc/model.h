@@ -134,9 +134,11 @@ struct Pool {
     // RWKV-7 W8A8 tier (instead of the limb buffers above)
     float* mixf = nullptr;       // [4][cap][d] LoRA inputs x_w, x_a, x_g, x_v (f32)
     float* lorah = nullptr;      // [cap][sum of ranks] first LoRA stages after their activation
-    int8_t* aq = nullptr;        // int8 activations: kAqAct x [rows16][dp], then [rows16][fp]
+    int8_t* aq = nullptr;        // int8 activations, kAqAct x [rows16][dp], then [rows16][fp]
     float* as = nullptr;         // their scales, kAqVecs x [cap]
-    float* actf = nullptr;       // [cap][d_ffn] squared-ReLU activations (f32)
+    float* gatedf = nullptr;     // [rows16][dp] gated WKV output (f32)
+    float* actf = nullptr;       // [rows16][fp] squared-ReLU activations (f32)
+    float* pmax = nullptr;       // [rows16][heads] each head's largest magnitude in gatedf
     float* out = nullptr;        // [cap][vocab] logits or probabilities
     uint32_t* slots = nullptr;   // [cap] slots of the current step (validated copy)
     uint32_t* d_slots = nullptr; // [2 cap] H2D target of the synchronous entry points: n slots, then n tokens
@@ -215,13 +217,13 @@ struct RwkvView {
 struct RwkvSizes {
     size_t state_d, wkv, mixl, loral, lora_off[4], gatedl, actl;
     int ks_d, ks_f, ks_lora[4];
-    // W8A8: padded row lengths of the int8 activations, their rows (cap rounded up to 16),
-    // the first LoRA stages' offsets in one [cap][lora_sum] row, and the buffer sizes
-    size_t dp, fp, rows16, lh_off[4], lora_sum, mixf, lorah, aq, as, actf;
+    // W8A8: padded row lengths of the activations, their rows (cap rounded up to 16), the
+    // first LoRA stages' offsets in one [cap][lora_sum] row, and the buffer sizes
+    size_t dp, fp, rows16, lh_off[4], lora_sum, mixf, lorah, aq, as, gatedf, actf, pmax;
 };
-// int8 activation vectors of the W8A8 tier, each [rows16][dp] in Pool::aq (act: [rows16][fp]
-// after them), with one scale per stream in Pool::as.
-enum { kAqR = 0, kAqK = 1, kAqV = 2, kAqGated = 3, kAqFfn = 4, kAqHead = 5, kAqAct = 6, kAqVecs = 7 };
+// int8 activation vectors of the W8A8 tier in Pool::aq, [rows16][dp] each (kAqAct, the last:
+// [rows16][fp]), with one scale per stream in Pool::as.
+enum { kAqR = 0, kAqK = 1, kAqV = 2, kAqFfn = 3, kAqHead = 4, kAqAct = 5, kAqVecs = 6 };
 RwkvSizes rwkv_sizes(const RDims& d, uint32_t cap, bool a8);
 
 struct ModelView {

@@ -12,15 +12,22 @@
 //                  tiles); first LoRA stages w1 (tanh), a1, g1 (sigmoid), v1 in the lane
 //                  order of dot_avx2_order (tensor.rs:1676-1693)
 //   k_proj_a8      second LoRA stages w2, a2, g2, v2
-//   k_wkv_a8       one workgroup per stream, a wave per head: decay, a, l2-normalised key,
-//                  modified key, value mix, WKV-7, GroupNorm, bonus (sequential sums), gate;
-//                  the gated vector as int8
-//   k_proj_a8      output projection + residual
+//   k_wkv_a8       one wave per (head, stream): decay, a, l2-normalised key, modified key,
+//                  value mix, WKV-7, GroupNorm, bonus (sequential sums), gate; the gated
+//                  vector as f32 with each head's largest magnitude
+//   k_proj_a8      output projection + residual, quantizing the gated vector as it loads it
 //   k_shift_a8<1>  ln2 + channel-mix token shift -> int8
 //   k_proj_a8      FFN key, squared ReLU (f32)
 //   k_quant_a8     those activations -> int8
 //   k_proj_a8      FFN value + residual
 // then k_shift_a8<0> (ln_out -> int8), k_head_a8 and optionally the softmax.
+//
+// A vector that one workgroup produces whole (the LayerNorm outputs) is quantized there.  The
+// gated vector comes from one wave per head: it is written as f32 with each head's largest
+// magnitude, and every workgroup of the output projection takes the stream's scale from
+// those maxima (exact: a maximum does not depend on the order) and rounds the values it
+// loads.  The FFN activations (d_ffn long, from many workgroups) are rounded once by a pass
+// of their own, since the FFN value product would round them again in every row tile.
 //
 // Integer products are exact, so the k-order of the int8 matrix products is free: the
 // weight tiles of the int8 matrix-core tiers serve unchanged (the 16 bytes a lane holds for
@@ -30,6 +37,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <utility>
 
 #include "mfma_common.h"
 #include "model.h"
@@ -50,11 +58,13 @@ constexpr int kMaxD = kBlock * kPer;
 constexpr int kMix = 6;
 constexpr int kSegs = 8;
 constexpr int kHead = 64;
-constexpr int kMaxHeads = kMaxD / kHead;
 constexpr int kWaves = kBlock / kWave;
 constexpr int kWavePairs = 12;                   // int8 products: k-pairs a wave requests at once
-constexpr int kLoraRows = kBlock / 8;            // LoRA products: eight rows per wave
+constexpr int kWavePairsF = 4;                   // the same with f32 activations (16 floats a pair)
+constexpr int kLoraBatch = 48;                   // LoRA steps whose loads are requested at once
 constexpr int kHeadMaxPairs = kMaxD / 64;
+constexpr int kHeadTiles = 2;                    // head: row tiles per wave
+constexpr int kHeadRowPad = 32;                  // head: LDS row padding of the staged activations (bytes)
 
 // ---------------------------------------------------------------- int8 activations
 
@@ -90,15 +100,41 @@ __device__ __forceinline__ float wave_max(float v) {
 // Iterator::sum over f32, as the reference's layer_norm_into, group_norm_into,
 // l2_normalize_per_head_inplace and bonus take it (tensor.rs:1390-1424, model.rs:899-909):
 // ((0 + sh[0]) + sh[1]) + ..., each partial sum rounded in turn.  Every lane walks the whole
-// row (broadcast LDS reads), so every lane ends with the sum.
+// row (broadcast LDS reads, each block of 32 requested while the previous one is added), so
+// every lane ends with the sum.
+__device__ __forceinline__ void add32(float& s, const float4 (&v)[8]) {
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        s += v[j].x;
+        s += v[j].y;
+        s += v[j].z;
+        s += v[j].w;
+    }
+}
+
+__device__ __forceinline__ void load32(float4 (&v)[8], const float* p) {
+#pragma unroll
+    for (int j = 0; j < 8; j++) v[j] = *(const float4*)(p + 4 * j);
+}
+
 __device__ __forceinline__ float seq_sum(const float* sh, int n) {
     float s = 0.0f;
-    int i = 0;
-    for (; i + 8 <= n; i += 8) {
-        const float4 u = *(const float4*)(sh + i);
-        const float4 w = *(const float4*)(sh + i + 4);
-        s += u.x; s += u.y; s += u.z; s += u.w;
-        s += w.x; s += w.y; s += w.z; s += w.w;
+    // Pairs of 32-element blocks through two buffers: the next block is requested before the
+    // current one is added (the last request re-reads a block, unused).
+    const int n64 = n / 64 * 64;
+    float4 a[8], b[8];
+    if (n64 > 0) load32(a, sh);
+    for (int i = 0; i < n64; i += 64) {
+        load32(b, sh + i + 32);
+        add32(s, a);
+        load32(a, sh + min(i + 64, n64 - 32));
+        add32(s, b);
+    }
+    int i = n64;
+    if (i + 32 <= n) {
+        load32(a, sh + i);
+        add32(s, a);
+        i += 32;
     }
     for (; i < n; i++) s += sh[i];
     return s;
@@ -240,9 +276,12 @@ enum { MODE_STORE = 0, MODE_RESID = 1 };
 struct SegA8 {
     int kind, mode, act;
     TMat w;                  // SEG_A8: per-row int8 weight tiles
-    const int8_t* q;         // SEG_A8: int8 activations, stream b at q + b * kp
-    const float* qs;         // their scales
+    const int8_t* q;         // SEG_A8: int8 activations, stream b at q + b * kp, scales qs
+    const float* qs;
     int kp;
+    const float* qf;         // or f32 activations, stream b at qf + b * kp (q null), with the
+    const float* pmax;       // largest magnitude of each of their `nparts` pieces at pmax + b * nparts
+    int nparts;
     int wpt;                 // SEG_A8: waves per tile (1, 2 or 4), each a contiguous share of the k-pairs
     LMat l;                  // SEG_LORA
     const float* xf;         // SEG_LORA: f32 activations, stream b at xf + b * ldx
@@ -264,7 +303,7 @@ __device__ __forceinline__ i32x4 mma8(const int4& w, const int2& lo, const int2&
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, v, c, 0, 0, 0);
 }
 
-// acc += the products of k-pairs [p0, p1) of one tile (weights at A, the lane's
+// acc += the products of k-pairs [p0, p1) of one tile (weights at A, the lane's int8
 // activations at qb), requested kWavePairs at a time before the first product.
 __device__ __forceinline__ i32x4 a8_pairs(const int4* A, const int8_t* qb, int p0, int p1, i32x4 acc) {
     for (int c = p0; c < p1; c += kWavePairs) {
@@ -272,16 +311,67 @@ __device__ __forceinline__ i32x4 a8_pairs(const int4* A, const int8_t* qb, int p
         int2 lo[kWavePairs], hi[kWavePairs];
 #pragma unroll
         for (int j = 0; j < kWavePairs; j++) {
-            const int p = c + j < p1 ? c + j : p1 - 1;
-            w[j] = A[(size_t)p * 64];
-            lo[j] = *(const int2*)(qb + 64 * p);
-            hi[j] = *(const int2*)(qb + 64 * p + 32);
+            const int p = c + j;
+            if (p < p1) {
+                w[j] = A[(size_t)p * 64];
+                lo[j] = *(const int2*)(qb + 64 * p);
+                hi[j] = *(const int2*)(qb + 64 * p + 32);
+            }
         }
 #pragma unroll
         for (int j = 0; j < kWavePairs; j++)
             if (c + j < p1) acc = mma8(w[j], lo[j], hi[j], acc);
     }
     return acc;
+}
+
+__device__ __forceinline__ int pack4(float a, float b, float c, float d, float inv) {
+    return (int)((uint32_t)(uint8_t)q8_of(a, inv) | (uint32_t)(uint8_t)q8_of(b, inv) << 8 |
+                 (uint32_t)(uint8_t)q8_of(c, inv) << 16 | (uint32_t)(uint8_t)q8_of(d, inv) << 24);
+}
+
+// The same from f32 activations at fb, each rounded to int8 with the stream's 1 / scale as
+// it arrives (quantize_vec_i8_into's rule).
+__device__ __forceinline__ i32x4 a8_pairs_f(const int4* A, const float* fb, float inv, int p0, int p1, i32x4 acc) {
+    for (int c = p0; c < p1; c += kWavePairsF) {
+        int4 w[kWavePairsF];
+        float4 v[kWavePairsF][4];
+#pragma unroll
+        for (int j = 0; j < kWavePairsF; j++) {
+            const int p = c + j;
+            if (p < p1) {
+                w[j] = A[(size_t)p * 64];
+                v[j][0] = *(const float4*)(fb + 64 * p);
+                v[j][1] = *(const float4*)(fb + 64 * p + 4);
+                v[j][2] = *(const float4*)(fb + 64 * p + 32);
+                v[j][3] = *(const float4*)(fb + 64 * p + 36);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < kWavePairsF; j++) {
+            if (c + j >= p1) continue;
+            int2 lo, hi;
+            lo.x = pack4(v[j][0].x, v[j][0].y, v[j][0].z, v[j][0].w, inv);
+            lo.y = pack4(v[j][1].x, v[j][1].y, v[j][1].z, v[j][1].w, inv);
+            hi.x = pack4(v[j][2].x, v[j][2].y, v[j][2].z, v[j][2].w, inv);
+            hi.y = pack4(v[j][3].x, v[j][3].y, v[j][3].z, v[j][3].w, inv);
+            acc = mma8(w[j], lo, hi, acc);
+        }
+    }
+    return acc;
+}
+
+// The scale of stream b's f32 activations: q8_scale of the largest of its pieces' maxima.
+// The four lanes of the stream (kg = 0..3) each take a quarter of the pieces, then meet.
+__device__ __forceinline__ float pieces_scale(const float* pmax, int nparts, uint32_t b, int kg) {
+    const float* pm = pmax + (size_t)b * nparts;
+    float m = 0.0f;
+    for (int i = kg; i < nparts; i += 4) m = pm[i] > m ? pm[i] : m;
+    float t = __shfl_xor(m, 16, kWave);
+    m = t > m ? t : m;
+    t = __shfl_xor(m, 32, kWave);
+    m = t > m ? t : m;
+    return q8_scale(m);
 }
 
 // q8_mat_vec_mul_into (tensor.rs:1819-1866) for one 16-row tile x 16 streams: `wpt` waves
@@ -293,11 +383,23 @@ __device__ __forceinline__ void a8_tile(const SegA8& s, int t, int part, uint32_
     const uint32_t b = g * kRowTile + lane % 16;          // < rows16: the activation rows exist
     const int np = s.w.ks / 2;
     const bool live = t < s.w.rt;
+    const float sb = s.q != nullptr ? (b < n ? s.qs[b] : 1.0f) : pieces_scale(s.pmax, s.nparts, b, kg);
+    // The epilogue's operands are requested with the products' (they do not depend on them).
+    const int r0 = min(t, s.w.rt - 1) * kRowTile + kg * 4;
+    float sw[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) sw[i] = s.w.scales[r0 + i];
+    float* o = s.out + (size_t)b * s.ld + r0;
+    const bool vec = r0 + 3 < s.w.rows && ((s.ld | r0) & 3) == 0 && ((uintptr_t)s.out & 15) == 0;
+    f32x4 y = {0, 0, 0, 0};
+    if (live && part == 0 && vec && b < n && s.mode == MODE_RESID) y = *(f32x4*)o;
     i32x4 acc = {0, 0, 0, 0};
     if (live) {
         const int share = (np + s.wpt - 1) / s.wpt;
         const int p0 = part * share, p1 = min(np, p0 + share);
-        acc = a8_pairs((const int4*)s.w.w + (size_t)t * np * 64 + lane, s.q + (size_t)b * s.kp + 8 * kg, p0, p1, acc);
+        const int4* A = (const int4*)s.w.w + (size_t)t * np * 64 + lane;
+        if (s.q != nullptr) acc = a8_pairs(A, s.q + (size_t)b * s.kp + 8 * kg, p0, p1, acc);
+        else acc = a8_pairs_f(A, s.qf + (size_t)b * s.kp + 8 * kg, 1.0f / sb, p0, p1, acc);
     }
     if (s.wpt > 1) {
         if (part > 0) red[wave][lane] = acc;
@@ -306,14 +408,10 @@ __device__ __forceinline__ void a8_tile(const SegA8& s, int t, int part, uint32_
         for (int j = 1; j < s.wpt; j++) acc += red[wave + j][lane];
     }
     if (!live || b >= n) return;
-    const int r0 = t * kRowTile + kg * 4;
-    const float sb = s.qs[b];
     float v[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) v[i] = activate(s.act, (float)acc[i] * (s.w.scales[r0 + i] * sb), 0, 0);
-    float* o = s.out + (size_t)b * s.ld + r0;
-    if (r0 + 3 < s.w.rows && ((s.ld | r0) & 3) == 0 && ((uintptr_t)s.out & 15) == 0) {
-        f32x4 y = s.mode == MODE_RESID ? *(f32x4*)o : f32x4{0, 0, 0, 0};
+    for (int i = 0; i < 4; i++) v[i] = activate(s.act, (float)acc[i] * (sw[i] * sb), 0, 0);
+    if (vec) {
 #pragma unroll
         for (int i = 0; i < 4; i++) y[i] = s.mode == MODE_RESID ? y[i] + v[i] : v[i];
         *(f32x4*)o = y;
@@ -326,37 +424,79 @@ __device__ __forceinline__ void a8_tile(const SegA8& s, int t, int part, uint32_
     }
 }
 
-// mat_vec_mul_into over f32 (tensor.rs:1602-1693, dot_avx2_order) for eight rows of one
-// stream (the wave): lane l of a row's eight accumulates the columns c = l (mod 8) from +0
-// with one multiply and one add each, then hsum_f32_scalar ((a0 + a4) + (a2 + a6)) +
-// ((a1 + a5) + (a3 + a7)) over the eight lanes (each pairing one commutative add), then
-// the activation of the LoRA stage.
+// mat_vec_mul_into over f32 (tensor.rs:1602-1693, dot_avx2_order) for rows of one stream:
+// chain l of a row accumulates the columns c = l (mod 8) from +0 with one multiply and one
+// add each; then hsum_f32_scalar ((a0 + a4) + (a2 + a6)) + ((a1 + a5) + (a3 + a7)) (each
+// pairing one commutative add, so every lane that forms it gets the same bits) and the
+// activation of the LoRA stage.  Long rows (the first stages, K = d) take a lane per chain
+// (eight rows a wave, kLoraBatch steps requested at once); short rows (the second stages,
+// K = rank) take two lanes, chains 4h .. 4h + 3 on lane h, with 16-byte loads (32 rows a
+// wave, every step requested at once).
+template <int LPR>
 __device__ __forceinline__ void lora_rows(const SegA8& s, int rb, uint32_t b) {
-    const int lane = threadIdx.x % kWave, l = lane % 8;
-    const int r = rb * kLoraRows + wave_index() * 8 + lane / 8;
+    constexpr int kRowsPerWave = kWave / LPR, kCh = 8 / LPR;
+    const int lane = threadIdx.x % kWave, h = lane % LPR;
+    const int r = rb * (kWaves * kRowsPerWave) + wave_index() * kRowsPerWave + lane / LPR;
     const int rr = r < s.l.rows8 ? r : s.l.rows8 - 1;
     const int steps = s.l.cols / 8;
-    const float* w = s.l.w + (size_t)rr * 8 + l;
     const size_t wstep = (size_t)s.l.rows8 * 8;
-    const float* x = s.xf + (size_t)b * s.ldx + l;
-    float acc = 0.0f;
-    int i = 0;
-    for (; i + 8 <= steps; i += 8) {
-        float wv[8], xv[8];
+    const float* w = s.l.w + (size_t)rr * 8 + kCh * h;
+    const float* x = s.xf + (size_t)b * s.ldx + kCh * h;
+    float acc[kCh];
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            wv[u] = w[(i + u) * wstep];
-            xv[u] = x[8 * (i + u)];
+    for (int j = 0; j < kCh; j++) acc[j] = 0.0f;
+    if (LPR == 8) {
+        int i = 0;
+        for (; i + kLoraBatch <= steps; i += kLoraBatch) {
+            float wv[kLoraBatch], xv[kLoraBatch];
+#pragma unroll
+            for (int u = 0; u < kLoraBatch; u++) {
+                wv[u] = w[(i + u) * wstep];
+                xv[u] = x[8 * (i + u)];
+            }
+#pragma unroll
+            for (int u = 0; u < kLoraBatch; u++) acc[0] += wv[u] * xv[u];
         }
+        for (; i < steps; i++) acc[0] += w[i * wstep] * x[8 * i];
+    } else {
+        constexpr int kB = kLoraBatch / 4;
+        for (int i0 = 0; i0 < steps; i0 += kB) {
+            float4 wv[kB], xv[kB];
 #pragma unroll
-        for (int u = 0; u < 8; u++) acc += wv[u] * xv[u];
+            for (int u = 0; u < kB; u++) {
+                const int i = i0 + u;
+                if (i < steps) {
+                    wv[u] = *(const float4*)(w + i * wstep);
+                    xv[u] = *(const float4*)(x + 8 * i);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < kB; u++) {
+                if (i0 + u < steps) {
+                    acc[0] += wv[u].x * xv[u].x;
+                    acc[1] += wv[u].y * xv[u].y;
+                    acc[2] += wv[u].z * xv[u].z;
+                    acc[3] += wv[u].w * xv[u].w;
+                }
+            }
+        }
     }
-    for (; i < steps; i++) acc += w[i * wstep] * x[8 * i];
-    float h = acc + __shfl_xor(acc, 4, kWave);
-    h = h + __shfl_xor(h, 2, kWave);
-    h = h + __shfl_xor(h, 1, kWave);
-    if (l == 0 && r < s.l.rows) s.out[(size_t)b * s.ld + r] = activate(s.act, h, r, s.l.rows);
+    float sum;
+    if (LPR == 8) {
+        float t = acc[0] + __shfl_xor(acc[0], 4, kWave);
+        t = t + __shfl_xor(t, 2, kWave);
+        sum = t + __shfl_xor(t, 1, kWave);
+    } else {
+        float s4[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) s4[j] = acc[j] + __shfl_xor(acc[j], 1, kWave);
+        sum = (s4[0] + s4[2]) + (s4[1] + s4[3]);
+    }
+    if (h == 0 && r < s.l.rows) s.out[(size_t)b * s.ld + r] = activate(s.act, sum, r, s.l.rows);
 }
+
+// Lanes per row of a LoRA segment with `cols` columns.
+constexpr int lora_lpr(int cols) { return cols >= 256 ? 8 : 2; }
 
 __global__ __launch_bounds__(kBlock) void k_proj_a8(ProjA8Args a) {
     __shared__ i32x4 red[kWaves][kWave];
@@ -369,8 +509,10 @@ __global__ __launch_bounds__(kBlock) void k_proj_a8(ProjA8Args a) {
         const int wave = wave_index(), tpb = kWaves / s.wpt;
         const int t = (int)(local / a.groups) * tpb + wave / s.wpt;
         a8_tile(s, t, wave % s.wpt, local % a.groups, a.n, red);
+    } else if (lora_lpr(s.l.cols) == 8) {
+        lora_rows<8>(s, (int)(local / a.n), local % a.n);
     } else {
-        lora_rows(s, (int)(local / a.n), local % a.n);
+        lora_rows<2>(s, (int)(local / a.n), local % a.n);
     }
 }
 
@@ -385,24 +527,21 @@ struct WkvA8Args {
     float* vfirst;           // [n][d]
     const uint32_t* slots;
     uint32_t cap;            // state slots of the pool (the clamp bound)
-    int8_t* q;               // the gated vector as int8 [rows16][dp], its scale per stream
-    float* qs;
-    int dp, d, layer, g1k;
+    float* gated;            // the gated vector, stream b at gated + b * ldg
+    int ldg;
+    float* gmax;             // the largest |gated| of head h at gmax + b * heads + h
+    int heads, d, layer, g1k;
 };
 
-// time_mixing_scratch steps 3-12 after the projections (model.rs:827-912) for one stream:
-// wave h owns head h, lane i channel c = 64 h + i and row i of the head's state.  The sums
-// over a head (l2 norm, GroupNorm mean and variance, bonus) are sequential; the state
-// products t = S·(-kk) and out = S·r already run over j in order per lane.  Then the gated
-// vector goes to int8 for the output projection (its amax over all heads).
-__global__ __launch_bounds__(kMaxD) void k_wkv_a8(WkvA8Args a) {
-    __shared__ __align__(16) float sw[kMaxHeads][kHead], skka[kMaxHeads][kHead], snegkk[kMaxHeads][kHead];
-    __shared__ __align__(16) float skmod[kMaxHeads][kHead], sr[kMaxHeads][kHead];
-    __shared__ __align__(16) float sa[kMaxHeads][kHead], sb[kMaxHeads][kHead];
-    __shared__ float smax[kMaxHeads];
-    const int i = threadIdx.x % kHead, h = threadIdx.x / kHead;
-    const int heads = (int)blockDim.x / kHead;
-    const uint32_t b = blockIdx.x;
+// time_mixing_scratch steps 3-12 after the projections (model.rs:827-912) for one head of
+// one stream; lane i owns channel c = 64 h + i and row i of the head's state.  The sums over
+// the head (l2 norm, GroupNorm mean and variance, bonus) are sequential; the state products
+// t = S·(-kk) and out = S·r already run over j in order per lane.
+__global__ __launch_bounds__(kHead) void k_wkv_a8(WkvA8Args a) {
+    __shared__ __align__(16) float sw[kHead], skka[kHead], snegkk[kHead], skmod[kHead], sr[kHead];
+    __shared__ __align__(16) float sa[kHead], sb[kHead];
+    const int i = threadIdx.x, h = blockIdx.x;
+    const uint32_t b = blockIdx.y;
     const int d = a.d, c = h * kHead + i;
     const uint32_t slot = clamp_slot(a.slots[b], a.cap);
     const float* rkv = a.rkv + (size_t)b * 3 * d;
@@ -425,9 +564,9 @@ __global__ __launch_bounds__(kMaxD) void k_wkv_a8(WkvA8Args a) {
     // Step 6: kk = (k * k_k) / sqrt(sum over the head of (k * k_k)^2), 0 when the norm is
     // <= 1e-12 (l2_normalize_per_head_inplace :1416-1424)
     const float kk0 = k * a.k_k[c];
-    sa[h][i] = kk0 * kk0;
+    sa[i] = kk0 * kk0;
     __syncthreads();
-    const float norm = sqrtf(seq_sum(sa[h], kHead));
+    const float norm = sqrtf(seq_sum(sa, kHead));
     const float kk = kk0 * (norm > 1e-12f ? 1.0f / norm : 0.0f);
     // Step 7
     const float kmod = k * (1.0f + (aa - 1.0f) * a.k_a[c]);
@@ -440,61 +579,59 @@ __global__ __launch_bounds__(kMaxD) void k_wkv_a8(WkvA8Args a) {
         a.vfirst[(size_t)b * d + c] = v;
     }
     // Step 9: t = S·(-kk); S[i][j] = S[i][j] w[j] + t[i] (kk a)[j] + v_out[i] kmod[j]; out = S·r
-    sw[h][i] = w;
-    skka[h][i] = kk * aa;
-    snegkk[h][i] = -kk;
-    skmod[h][i] = kmod;
-    sr[h][i] = r;
+    sw[i] = w;
+    skka[i] = kk * aa;
+    snegkk[i] = -kk;
+    skmod[i] = kmod;
+    sr[i] = r;
     __syncthreads();
     float tt = 0.0f;
 #pragma unroll
-    for (int j = 0; j < kHead; j++) tt += S[j] * snegkk[h][j];
+    for (int j = 0; j < kHead; j++) tt += S[j] * snegkk[j];
 #pragma unroll
-    for (int j = 0; j < kHead; j++) S[j] = S[j] * sw[h][j] + tt * skka[h][j] + vout * skmod[h][j];
+    for (int j = 0; j < kHead; j++) S[j] = S[j] * sw[j] + tt * skka[j] + vout * skmod[j];
     float o = 0.0f;
 #pragma unroll
-    for (int j = 0; j < kHead; j++) o += S[j] * sr[h][j];
+    for (int j = 0; j < kHead; j++) o += S[j] * sr[j];
 #pragma unroll
     for (int q = 0; q < kHead / 4; q++) sbase[q * kHead + i] = make_float4(S[4 * q], S[4 * q + 1], S[4 * q + 2], S[4 * q + 3]);
     // Step 10: GroupNorm over the head, eps 64e-5 (group_norm_into :1400-1414); step 11:
     // bonus = sum over the head of r * k * r_k (k_mod for g1k models), times v_out
     const float ksrc = a.g1k ? kmod : k;
-    sa[h][i] = o;
-    sb[h][i] = r * ksrc * a.r_k[c];
+    sa[i] = o;
+    sb[i] = r * ksrc * a.r_k[c];
     __syncthreads();
     float osum, bonus;
-    seq_sum2_64(sa[h], sb[h], osum, bonus);
+    seq_sum2_64(sa, sb, osum, bonus);
     const float mean = osum / (float)kHead;
     __syncthreads();
-    sa[h][i] = (o - mean) * (o - mean);
+    sa[i] = (o - mean) * (o - mean);
     __syncthreads();
-    const float var = seq_sum(sa[h], kHead) / (float)kHead;
+    const float var = seq_sum(sa, kHead) / (float)kHead;
     float on = (o - mean) * (1.0f / sqrtf(var + 64e-5f)) * a.ln_x_w[c] + a.ln_x_b[c];
     on += bonus * vout;
-    // Step 12: gate, then int8 for the output projection
+    // Step 12: gate; the output projection quantizes it
     const float gated = on * g;
+    a.gated[(size_t)b * a.ldg + c] = gated;
     const float mx = wave_max(fold_abs(0.0f, gated));
-    if (i == 0) smax[h] = mx;
-    __syncthreads();
-    float amax = 0.0f;
-    for (int hh = 0; hh < heads; hh++) amax = smax[hh] > amax ? smax[hh] : amax;
-    const float scale = q8_scale(amax);
-    a.q[(size_t)b * a.dp + c] = q8_of(gated, 1.0f / scale);
-    if (threadIdx.x == 0) a.qs[b] = scale;
+    if (i == 0) a.gmax[(size_t)b * a.heads + h] = mx;
 }
 
 // ---------------------------------------------------------------- activations -> int8
 
 struct QuantA8Args {
-    const float* x;          // stream b at x + b * ld, K values
+    const float* x;          // stream b at x + b * ld, K values (K a multiple of 4)
     int ld, K;
     int8_t* q;               // [rows16][kp]
     int kp;
     float* qs;
 };
 
+// quantize_vec_i8_into (tensor.rs:1791-1800) of one stream's FFN activations: the vector
+// arrives from many workgroups of the FFN key product, so it is taken to int8 here, once,
+// for every row tile of the FFN value product.
 __global__ __launch_bounds__(kBlock) void k_quant_a8(QuantA8Args a) {
-    __shared__ float wm[kBlock / kWave];
+    __shared__ float wm[kWaves];
     const uint32_t b = blockIdx.x;
     const int lane = threadIdx.x % kWave, wave = wave_index();
     const float4* xb = (const float4*)(a.x + (size_t)b * a.ld);
@@ -509,14 +646,13 @@ __global__ __launch_bounds__(kBlock) void k_quant_a8(QuantA8Args a) {
     __syncthreads();
     float amax = 0.0f;
 #pragma unroll
-    for (int w = 0; w < kBlock / kWave; w++) amax = wm[w] > amax ? wm[w] : amax;
+    for (int w = 0; w < kWaves; w++) amax = wm[w] > amax ? wm[w] : amax;
     const float scale = q8_scale(amax);
     const float inv = 1.0f / scale;
-    uint32_t* qb = (uint32_t*)(a.q + (size_t)b * a.kp);
+    int* qb = (int*)(a.q + (size_t)b * a.kp);
     for (int c = threadIdx.x; c < k4; c += kBlock) {
         const float4 v = xb[c];
-        qb[c] = (uint32_t)(uint8_t)q8_of(v.x, inv) | (uint32_t)(uint8_t)q8_of(v.y, inv) << 8 |
-                (uint32_t)(uint8_t)q8_of(v.z, inv) << 16 | (uint32_t)(uint8_t)q8_of(v.w, inv) << 24;
+        qb[c] = pack4(v.x, v.y, v.z, v.w, inv);
     }
     if (threadIdx.x == 0) a.qs[b] = scale;
 }
@@ -533,49 +669,90 @@ struct HeadA8Args {
     uint32_t n, groups;
 };
 
-// The head as q8_mat_vec_mul_into: each wave keeps one 16-row tile's weights in registers
-// and walks every stream group.
+// 16-byte chunk ch of stream group g's int8 activations (zero past the group's chunks).
+template <int NP>
+__device__ __forceinline__ int4 head_chunk(const HeadA8Args& a, uint32_t g, int ch) {
+    if (ch >= kRowTile * NP * 4) return make_int4(0, 0, 0, 0);
+    const int row = ch / (NP * 4), col = ch % (NP * 4);
+    return *(const int4*)(a.q + (size_t)(g * kRowTile + row) * a.kp + 16 * col);
+}
+
+// The head as q8_mat_vec_mul_into: each wave keeps kHeadTiles row tiles' weights (NP k-pairs
+// each) in registers and walks every stream group; a group's int8 activations are staged in
+// LDS once for the workgroup (the next group's requested while this one is multiplied).
+template <int NP>
 __global__ __launch_bounds__(kBlock) void k_head_a8(HeadA8Args a) {
-    const int lane = threadIdx.x % kWave, kg = lane / 16;
-    const int t = (int)blockIdx.x * kWaves + wave_index();
-    if (t >= a.w.rt) return;
-    const int np = a.w.ks / 2;
-    int4 W[kHeadMaxPairs];
-    const int4* A = (const int4*)a.w.w + (size_t)t * np * 64 + lane;
+    constexpr int kRow = NP * 64 + kHeadRowPad;   // LDS row stride: row j starts 8j banks apart
+    constexpr int kChunks = kRowTile * NP * 4;    // 16-byte chunks of a group's activations
+    constexpr int kPer = (kChunks + kBlock - 1) / kBlock;
+    __shared__ __align__(16) int8_t sq[kRowTile * kRow];
+    const int lane = threadIdx.x % kWave, kg = lane / 16, wave = wave_index();
+    const int t0 = ((int)blockIdx.x * kWaves + wave) * kHeadTiles;
+    int4 W[kHeadTiles][NP];
+    float sw[kHeadTiles][4];
 #pragma unroll
-    for (int p = 0; p < kHeadMaxPairs; p++)
-        if (p < np) W[p] = A[(size_t)p * 64];
-    const int r0 = t * kRowTile + kg * 4;
-    float sw[4];
+    for (int j = 0; j < kHeadTiles; j++) {
+        const int t = min(t0 + j, a.w.rt - 1);
+        const int4* A = (const int4*)a.w.w + (size_t)t * NP * 64 + lane;
 #pragma unroll
-    for (int i = 0; i < 4; i++) sw[i] = a.w.scales[r0 + i];
-    const bool vec = r0 + 3 < a.w.rows && ((a.ld | r0) & 3) == 0 && ((uintptr_t)a.out & 15) == 0;
+        for (int p = 0; p < NP; p++) W[j][p] = A[(size_t)p * 64];
+#pragma unroll
+        for (int i = 0; i < 4; i++) sw[j][i] = a.w.scales[t * kRowTile + kg * 4 + i];
+    }
+    int4 stage[kPer];
+#pragma unroll
+    for (int u = 0; u < kPer; u++) stage[u] = head_chunk<NP>(a, 0, (int)threadIdx.x + kBlock * u);
     for (uint32_t g = 0; g < a.groups; g++) {
-        const uint32_t b = g * kRowTile + lane % 16;
-        const int8_t* qb = a.q + (size_t)b * a.kp + 8 * kg;
-        i32x4 acc0 = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};
+        __syncthreads();
 #pragma unroll
-        for (int p = 0; p < kHeadMaxPairs; p += 2) {
-            if (p < np) acc0 = mma8(W[p], *(const int2*)(qb + 64 * p), *(const int2*)(qb + 64 * p + 32), acc0);
-            if (p + 1 < np)
-                acc1 = mma8(W[p + 1], *(const int2*)(qb + 64 * p + 64), *(const int2*)(qb + 64 * p + 96), acc1);
+        for (int u = 0; u < kPer; u++) {
+            const int ch = (int)threadIdx.x + kBlock * u;
+            if (ch < kChunks) *(int4*)(sq + (ch / (NP * 4)) * kRow + 16 * (ch % (NP * 4))) = stage[u];
         }
-        const i32x4 acc = acc0 + acc1;
+        __syncthreads();
+        if (g + 1 < a.groups) {
+#pragma unroll
+            for (int u = 0; u < kPer; u++) stage[u] = head_chunk<NP>(a, g + 1, (int)threadIdx.x + kBlock * u);
+        }
+        i32x4 acc[kHeadTiles];
+#pragma unroll
+        for (int j = 0; j < kHeadTiles; j++) acc[j] = i32x4{0, 0, 0, 0};
+        const int8_t* qb = sq + (lane % 16) * kRow + 8 * kg;
+#pragma unroll
+        for (int p = 0; p < NP; p++) {
+            const int2 lo = *(const int2*)(qb + 64 * p), hi = *(const int2*)(qb + 64 * p + 32);
+#pragma unroll
+            for (int j = 0; j < kHeadTiles; j++) acc[j] = mma8(W[j][p], lo, hi, acc[j]);
+        }
+        const uint32_t b = g * kRowTile + lane % 16;
         if (b >= a.n) continue;
         const float sb = a.qs[b];
-        float* o = a.out + (size_t)b * a.ld + r0;
-        float v[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) v[i] = (float)acc[i] * (sw[i] * sb);
-        if (vec) {
-            *(f32x4*)o = f32x4{v[0], v[1], v[2], v[3]};
-        } else {
+        for (int j = 0; j < kHeadTiles; j++) {
+            const int t = t0 + j;
+            if (t >= a.w.rt) continue;
+            const int r0 = t * kRowTile + kg * 4;
+            float v[4];
 #pragma unroll
-            for (int i = 0; i < 4; i++)
-                if (r0 + i < a.w.rows) o[i] = v[i];
+            for (int i = 0; i < 4; i++) v[i] = (float)acc[j][i] * (sw[j][i] * sb);
+            float* o = a.out + (size_t)b * a.ld + r0;
+            if (r0 + 3 < a.w.rows && ((a.ld | r0) & 3) == 0 && ((uintptr_t)a.out & 15) == 0) {
+                *(f32x4*)o = f32x4{v[0], v[1], v[2], v[3]};
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    if (r0 + i < a.w.rows) o[i] = v[i];
+            }
         }
     }
 }
+
+template <int... P>
+const void* head_a8_pick(int np, std::integer_sequence<int, P...>) {
+    const void* fns[] = {(const void*)k_head_a8<P + 1>...};
+    return np >= 1 && np <= (int)sizeof...(P) ? fns[np - 1] : nullptr;
+}
+const void* head_a8_fn(int np) { return head_a8_pick(np, std::make_integer_sequence<int, kHeadMaxPairs>{}); }
 
 // ---------------------------------------------------------------- step assembly
 
@@ -584,7 +761,10 @@ struct ProjA8Builder {
     uint32_t blocks = 0;
     uint32_t n = 0, groups = 0;
     ProjA8Builder(uint32_t n_, uint32_t groups_) : n(n_), groups(groups_) {}
-    void a8(const TMat& w, const int8_t* q, const float* qs, int kp, int mode, int act, float* out, int ld) {
+    // An int8 product on int8 activations q (row kp bytes, scales qs), or on f32 activations
+    // qf (row kp floats) whose pieces' maxima are pmax.
+    SegA8& a8(const TMat& w, const int8_t* q, const float* qs, const float* qf, const float* pmax, int nparts, int kp,
+              int mode, int act, float* out, int ld) {
         SegA8& s = a.seg[a.nseg++];
         s.kind = SEG_A8;
         s.mode = mode;
@@ -592,19 +772,22 @@ struct ProjA8Builder {
         s.w = w;
         s.q = q;
         s.qs = qs;
+        s.qf = qf;
+        s.pmax = pmax;
+        s.nparts = nparts;
         s.kp = kp;
-        // Waves per tile: enough that a wave's share fits one request of kWavePairs, more
-        // while the launch has few tiles (each wave then waits on fewer requests in turn).
+        // Waves per tile: as many as keep at least three k-pairs a wave (at 64 streams a
+        // 768-column tile over four waves takes half the time it takes over two).
         const int np = w.ks / 2;
         int wpt = 1;
-        while (wpt < kWaves && (np + wpt - 1) / wpt > kWavePairs) wpt *= 2;
-        while (wpt < kWaves && (size_t)w.rt * groups * wpt < 1024 && np / (2 * wpt) >= 3) wpt *= 2;
+        while (wpt < kWaves && np / (2 * wpt) >= 3) wpt *= 2;
         s.wpt = wpt;
         s.out = out;
         s.ld = ld;
         s.blk0 = blocks;
         const int tpb = kWaves / wpt;
         blocks += (uint32_t)((w.rt + tpb - 1) / tpb) * groups;
+        return s;
     }
     void lora(const LMat& l, const float* xf, int ldx, int act, float* out, int ld) {
         SegA8& s = a.seg[a.nseg++];
@@ -617,7 +800,8 @@ struct ProjA8Builder {
         s.out = out;
         s.ld = ld;
         s.blk0 = blocks;
-        blocks += (uint32_t)((l.rows8 + kLoraRows - 1) / kLoraRows) * n;
+        const int rows_per_block = kBlock / lora_lpr(l.cols);
+        blocks += (uint32_t)((l.rows8 + rows_per_block - 1) / rows_per_block) * n;
     }
     Launch launch() {
         a.n = n;
@@ -632,18 +816,19 @@ void RwkvStep::build_a8(Pool& p, const StepIO& io, std::vector<Launch>& out, int
                         int& sm_i) const {
     const RDims& D = *m.dims;
     const uint32_t n = io.n;
-    const int d = (int)D.d, ff = (int)D.f;
+    const int d = (int)D.d;
     const RwkvSizes z = rwkv_sizes(D, p.cap, true);
     const uint32_t groups = (n + kRowTile - 1) / kRowTile;
     const int dp = (int)z.dp, fp = (int)z.fp;
     int8_t* aq[kAqVecs];
-    for (int k = 0; k < kAqVecs; k++) aq[k] = p.aq + (size_t)k * z.rows16 * z.dp;
+    for (int k = 0; k < kAqVecs; k++) aq[k] = p.aq + (size_t)k * z.rows16 * z.dp;   // act: the last, rows fp
     float* as[kAqVecs];
     for (int k = 0; k < kAqVecs; k++) as[k] = p.as + (size_t)k * p.cap;
     float* mixf[4];
     for (int k = 0; k < 4; k++) mixf[k] = p.mixf + (size_t)k * p.cap * d;
     float* lh[4];
     for (int k = 0; k < 4; k++) lh[k] = p.lorah + z.lh_off[k];
+    float* gmax = p.pmax;                                  // [rows16][heads]
     const int lsum = (int)z.lora_sum;
     const size_t state_stride = (size_t)D.nl * D.d;
     const size_t wkv_layer = (size_t)D.h * D.n * D.n;
@@ -668,9 +853,9 @@ void RwkvStep::build_a8(Pool& p, const StepIO& io, std::vector<Launch>& out, int
         s1.outf[3] = mixf[kLoraV];
         out.push_back(Launch::make(shift_a8_fn(6), dim3(n), dim3(kBlock), 0, KC_SHIFT, s1));
         ProjA8Builder p1(n, groups);
-        p1.a8(L.r, aq[kAqR], as[kAqR], dp, MODE_STORE, ACT_NONE, p.rkv, 3 * d);
-        p1.a8(L.k, aq[kAqK], as[kAqK], dp, MODE_STORE, ACT_NONE, p.rkv + d, 3 * d);
-        p1.a8(L.v, aq[kAqV], as[kAqV], dp, MODE_STORE, ACT_NONE, p.rkv + 2 * d, 3 * d);
+        p1.a8(L.r, aq[kAqR], as[kAqR], nullptr, nullptr, 0, dp, MODE_STORE, ACT_NONE, p.rkv, 3 * d);
+        p1.a8(L.k, aq[kAqK], as[kAqK], nullptr, nullptr, 0, dp, MODE_STORE, ACT_NONE, p.rkv + d, 3 * d);
+        p1.a8(L.v, aq[kAqV], as[kAqV], nullptr, nullptr, 0, dp, MODE_STORE, ACT_NONE, p.rkv + 2 * d, 3 * d);
         p1.lora(L.x1[kLoraW], mixf[kLoraW], d, ACT_TANH, lh[kLoraW], lsum);
         p1.lora(L.x1[kLoraA], mixf[kLoraA], d, ACT_NONE, lh[kLoraA], lsum);
         p1.lora(L.x1[kLoraG], mixf[kLoraG], d, ACT_SIGMOID, lh[kLoraG], lsum);
@@ -681,11 +866,11 @@ void RwkvStep::build_a8(Pool& p, const StepIO& io, std::vector<Launch>& out, int
             if (k != kLoraV || l != 0) p2.lora(L.x2[k], lh[k], lsum, ACT_NONE, p.lorad + k * d, 4 * d);
         out.push_back(p2.launch());
         WkvA8Args wa{p.rkv, p.lorad, L.w0, L.a0, L.v0, L.k_k, L.k_a, L.r_k, L.ln_x_w, L.ln_x_b,
-                     p.wkv + l * wkv_layer, (size_t)D.nl * wkv_layer, p.vfirst, p.slots, p.scap, aq[kAqGated],
-                     as[kAqGated], dp, d, (int)l, (int)D.g1k};
-        out.push_back(Launch::make((const void*)k_wkv_a8, dim3(n), dim3(D.h * kHead), 0, KC_WKV, wa));
+                     p.wkv + l * wkv_layer, (size_t)D.nl * wkv_layer, p.vfirst, p.slots, p.scap, p.gatedf, dp, gmax,
+                     (int)D.h, d, (int)l, (int)D.g1k};
+        out.push_back(Launch::make((const void*)k_wkv_a8, dim3(D.h, n), dim3(kHead), 0, KC_WKV, wa));
         ProjA8Builder po(n, groups);
-        po.a8(L.o, aq[kAqGated], as[kAqGated], dp, MODE_RESID, ACT_NONE, p.x, d);
+        po.a8(L.o, nullptr, nullptr, p.gatedf, gmax, (int)D.h, dp, MODE_RESID, ACT_NONE, p.x, d);
         out.push_back(po.launch());
         ShiftA8Args s2{p.x, L.ln2_w, L.ln2_b, p.x_ffn + (size_t)l * d, state_stride, p.slots, p.scap, {}, {}, {}, {},
                        d, dp};
@@ -694,12 +879,12 @@ void RwkvStep::build_a8(Pool& p, const StepIO& io, std::vector<Launch>& out, int
         s2.outs[0] = as[kAqFfn];
         out.push_back(Launch::make(shift_a8_fn(1), dim3(n), dim3(kBlock), 0, KC_SHIFT, s2));
         ProjA8Builder pk(n, groups);
-        pk.a8(L.fk, aq[kAqFfn], as[kAqFfn], dp, MODE_STORE, ACT_RELU2, p.actf, ff);
+        pk.a8(L.fk, aq[kAqFfn], as[kAqFfn], nullptr, nullptr, 0, dp, MODE_STORE, ACT_RELU2, p.actf, fp);
         out.push_back(pk.launch());
-        QuantA8Args qa{p.actf, ff, ff, aq[kAqAct], fp, as[kAqAct]};
+        QuantA8Args qa{p.actf, fp, (int)D.f, aq[kAqAct], fp, as[kAqAct]};
         out.push_back(Launch::make((const void*)k_quant_a8, dim3(n), dim3(kBlock), 0, KC_PROJ, qa));
         ProjA8Builder pv(n, groups);
-        pv.a8(L.fv, aq[kAqAct], as[kAqAct], fp, MODE_RESID, ACT_NONE, p.x, d);
+        pv.a8(L.fv, aq[kAqAct], as[kAqAct], nullptr, nullptr, 0, fp, MODE_RESID, ACT_NONE, p.x, d);
         out.push_back(pv.launch());
     }
     ShiftA8Args sf{p.x, m.ln_out_w, m.ln_out_b, nullptr, 0, p.slots, p.scap, {}, {}, {}, {}, d, dp};
@@ -709,8 +894,9 @@ void RwkvStep::build_a8(Pool& p, const StepIO& io, std::vector<Launch>& out, int
     const TMat& H = *m.head;
     head_i = (int)out.size();
     HeadA8Args ha{H, aq[kAqHead], as[kAqHead], dp, io.out + (size_t)io.b0 * D.vocab, (int)D.vocab, n, groups};
-    out.push_back(Launch::make((const void*)k_head_a8, dim3((H.rt + kWaves - 1) / kWaves),
-                               dim3(kBlock), 0, KC_HEAD, ha));
+    const int per_block = kWaves * kHeadTiles;
+    out.push_back(Launch::make(head_a8_fn(H.ks / 2), dim3((H.rt + per_block - 1) / per_block), dim3(kBlock), 0,
+                               KC_HEAD, ha));
     sm_i = -1;
     if (io.probs) {
         sm_i = (int)out.size();

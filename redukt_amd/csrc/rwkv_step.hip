@@ -59,9 +59,11 @@ RwkvSizes rwkv_sizes(const RDims& D, uint32_t cap, bool a8) {
     if (a8) {
         z.mixf = 4 * (size_t)cap * D.d;
         z.lorah = (size_t)cap * z.lora_sum;
-        z.aq = z.rows16 * (6 * z.dp + z.fp);
+        z.aq = z.rows16 * (kAqAct * z.dp + z.fp);
         z.as = (size_t)kAqVecs * cap;
-        z.actf = (size_t)cap * D.f;
+        z.gatedf = z.rows16 * z.dp;
+        z.actf = z.rows16 * z.fp;
+        z.pmax = z.rows16 * D.h;
     } else {
         z.mixl = gcap * z.ks_d * 3 * 512;
         z.gatedl = z.mixl;
