@@ -10,6 +10,7 @@
  * `group` columns (Q8wMatrix, src/domain/gemv.rs:244-273). */
 typedef struct {
     int rows, cols, group; /* group: 0 = F32 */
+    int fma;               /* GEMV in numeric contract 2 (fma-v1) instead of 1 */
     float* f;              /* F32 data (NULL for Q8) */
     int8_t* q;
     float* sc;

@@ -6,7 +6,10 @@
  * Numeric contract: the reference's "Plain" kernel family (numeric contracts 0/1,
  * src/domain/gemv.rs:13-21): IEEE f32, separate multiply and add, no contraction
  * (built with -ffp-contract=off), the reference's own portable exp/ln
- * (src/domain/tensor.rs:757-915), and the reference's accumulation orders.  Every
+ * (src/domain/tensor.rs:757-915), and the reference's accumulation orders.  With
+ * ORC_PROFILE_FMA the GEMVs take numeric contract 2 instead (the "Fma" kernel family,
+ * src/domain/gemv_fma.rs:1-26): the same orders, each acc + w*x one fused multiply-add
+ * (C99 fmaf, correctly rounded like the reference's fma_f32, gemv_fma.rs:61-96).  Every
  * function cites the reference code it restates.  Nothing here is shared with the
  * HIP product library.
  */
@@ -164,6 +167,39 @@ static float q8_row(const int8_t* q, const float* sc, int cols, int group, const
     return row_sum;
 }
 
+/* gemv_fma.rs:98-112 (dot_fma_scalar): the lane order of orc_dot_f32 with every
+ * acc + w*x one fused multiply-add, from +0; the horizontal sum with plain adds; the tail
+ * by fused multiply-adds.  Q8 weights convert to f32 exactly (gemv_fma.rs:8-13). */
+VEC_CLONES float orc_dot_f32_fma(const float* w, const float* v, int n) {
+    int body = n / 8 * 8;
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int c = 0; c < body; c += 8)
+        for (int l = 0; l < 8; l++) acc[l] = fmaf(w[c + l], v[c + l], acc[l]);
+    float s0 = acc[0] + acc[4], s1 = acc[1] + acc[5], s2 = acc[2] + acc[6], s3 = acc[3] + acc[7];
+    float s = (s0 + s2) + (s1 + s3);
+    for (int c = body; c < n; c++) s = fmaf(w[c], v[c], s);
+    return s;
+}
+
+VEC_CLONES static float group_dot_q8_fma(const int8_t* q, const float* v, int n) {
+    int body = n / 8 * 8;
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int c = 0; c < body; c += 8)
+        for (int l = 0; l < 8; l++) acc[l] = fmaf((float)q[c + l], v[c + l], acc[l]);
+    float s0 = acc[0] + acc[4], s1 = acc[1] + acc[5], s2 = acc[2] + acc[6], s3 = acc[3] + acc[7];
+    float s = (s0 + s2) + (s1 + s3);
+    for (int c = body; c < n; c++) s = fmaf((float)q[c], v[c], s);
+    return s;
+}
+
+/* gemv_fma.rs:121-134 (q8w_rows_fma_scalar): sum = fma(dot_g, scale_g, sum) from +0. */
+static float q8_row_fma(const int8_t* q, const float* sc, int cols, int group, const float* v) {
+    int gpr = cols / group;
+    float row_sum = 0.0f;
+    for (int g = 0; g < gpr; g++) row_sum = fmaf(group_dot_q8_fma(q + g * group, v + g * group, group), sc[g], row_sum);
+    return row_sum;
+}
+
 /* gemv.rs:256-273: group rule, scale = amax/127 (1 if amax == 0), q = clamp(round(w/scale)). */
 void orc_quantize(const float* w, int rows, int cols, int group, int8_t* q, float* scales, int* group_out) {
     if (!(group > 0 && group % 8 == 0 && cols % group == 0)) group = cols;
@@ -192,6 +228,15 @@ void orc_gemv_f32(const float* w, int rows, int cols, const float* v, float* out
 void orc_gemv_q8(const int8_t* q, const float* scales, int rows, int cols, int group, const float* v, float* out) {
     int gpr = cols / group;
     for (int r = 0; r < rows; r++) out[r] = q8_row(q + (size_t)r * cols, scales + (size_t)r * gpr, cols, group, v);
+}
+
+void orc_gemv_f32_fma(const float* w, int rows, int cols, const float* v, float* out) {
+    for (int r = 0; r < rows; r++) out[r] = orc_dot_f32_fma(w + (size_t)r * cols, v, cols);
+}
+
+void orc_gemv_q8_fma(const int8_t* q, const float* scales, int rows, int cols, int group, const float* v, float* out) {
+    int gpr = cols / group;
+    for (int r = 0; r < rows; r++) out[r] = q8_row_fma(q + (size_t)r * cols, scales + (size_t)r * gpr, cols, group, v);
 }
 
 /* ====================================================================
@@ -295,14 +340,18 @@ void mat_row(const Mat* m, int row, float* out) {
     for (int c = 0; c < m->cols; c++) out[c] = (float)q[c] * sc[c / m->group];
 }
 
-/* Rows [r0, r1) of out = M·v in the reference order (f32_rows / q8w_rows). */
+/* Rows [r0, r1) of out = M·v in the reference order (f32_rows / q8w_rows, or their
+ * contract-2 twins f32_rows_fma_scalar / q8w_rows_fma_scalar, gemv_fma.rs:115-134). */
 void mat_rows(const Mat* m, int r0, int r1, const float* v, float* out) {
     if (!m->group) {
-        for (int r = r0; r < r1; r++) out[r] = orc_dot_f32(m->f + (size_t)r * m->cols, v, m->cols);
+        for (int r = r0; r < r1; r++)
+            out[r] = m->fma ? orc_dot_f32_fma(m->f + (size_t)r * m->cols, v, m->cols)
+                            : orc_dot_f32(m->f + (size_t)r * m->cols, v, m->cols);
     } else {
         int gpr = m->cols / m->group;
         for (int r = r0; r < r1; r++)
-            out[r] = q8_row(m->q + (size_t)r * m->cols, m->sc + (size_t)r * gpr, m->cols, m->group, v);
+            out[r] = m->fma ? q8_row_fma(m->q + (size_t)r * m->cols, m->sc + (size_t)r * gpr, m->cols, m->group, v)
+                            : q8_row(m->q + (size_t)r * m->cols, m->sc + (size_t)r * gpr, m->cols, m->group, v);
     }
 }
 
@@ -383,6 +432,15 @@ OrcMamba* orc_mamba_load(const char* path, int profile, int* err) {
     }
     fclose(f);
     if (bad) { orc_mamba_free(m); return NULL; }
+    /* MambaModel::set_kernel (model.rs:955-967): the kernel family of every GEMV (in_proj,
+     * x_proj, dt_proj, out_proj, the head); the embedding lookup has no sum. */
+    int fma = (profile & ORC_PROFILE_FMA) != 0;
+    m->emb.fma = fma;
+    m->head_own.fma = fma;
+    for (uint32_t i = 0; i < m->nl; i++) {
+        Layer* L = &m->layers[i];
+        L->in_proj.fma = L->x_proj.fma = L->dt_proj.fma = L->out_proj.fma = fma;
+    }
     *err = 0;
     return m;
 }

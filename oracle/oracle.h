@@ -28,6 +28,12 @@ enum {
     /* RWKV-7 with per-row int8 weights only: int8 activations as well (W8A8,
      * tensor.rs:1791-1866), the reference's own RWKV-7 Q8 arithmetic. */
     ORC_PROFILE_W8A8 = 32,
+    /* Mamba: the reference-order tier of the GPU library.  The oracle always computes in
+     * the reference order, so this bit changes nothing here; it is accepted so that the
+     * oracle and the library take the same profile words. */
+    ORC_PROFILE_EXACT = 64,
+    /* Mamba: every GEMV in numeric contract 2 (fma-v1, gemv_fma.rs) instead of 1. */
+    ORC_PROFILE_FMA = 128,
 };
 
 /* ---- scalar math (tensor.rs) ---- */
@@ -45,6 +51,11 @@ void  orc_quantize(const float* w, int rows, int cols, int group, int8_t* q, flo
 void  orc_gemv_f32(const float* w, int rows, int cols, const float* v, float* out);
 void  orc_gemv_q8(const int8_t* q, const float* scales, int rows, int cols, int group,
                   const float* v, float* out);
+/* The same GEMVs in numeric contract 2 (fma-v1, gemv_fma.rs:98-134). */
+float orc_dot_f32_fma(const float* w, const float* v, int n);
+void  orc_gemv_f32_fma(const float* w, int rows, int cols, const float* v, float* out);
+void  orc_gemv_q8_fma(const int8_t* q, const float* scales, int rows, int cols, int group,
+                      const float* v, float* out);
 void  orc_rms_norm(float* x, const float* w, int n, float eps);
 void  orc_layer_norm(float* out, const float* x, const float* w, const float* b, int n, float eps);
 void  orc_ssm_d16(float* y, float* ss, const float* dt, const float* conv_out, const float* a_log,

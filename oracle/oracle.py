@@ -17,6 +17,10 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 # with a planted mistake in a child process).
 LIB_PATH = os.environ.get("ORACLE_LIB") or os.path.join(HERE, "liboracle.so")
 
+# Profile bits of the Mamba oracle beyond the weight quantisation (oracle.h).
+ORC_PROFILE_EXACT = 64   # accepted and ignored: the oracle always computes in the reference order
+ORC_PROFILE_FMA = 128    # every GEMV in numeric contract 2 (fma-v1)
+
 _u32p = ctypes.POINTER(ctypes.c_uint32)
 _f32p = ctypes.POINTER(ctypes.c_float)
 _i8p = ctypes.POINTER(ctypes.c_int8)
@@ -45,6 +49,10 @@ def lib() -> ctypes.CDLL:
                                    ctypes.POINTER(ctypes.c_int)]
         L.orc_gemv_f32.argtypes = [_f32p, ctypes.c_int, ctypes.c_int, _f32p, _f32p]
         L.orc_gemv_q8.argtypes = [_i8p, _f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int, _f32p, _f32p]
+        L.orc_dot_f32_fma.argtypes = [_f32p, _f32p, ctypes.c_int]
+        L.orc_dot_f32_fma.restype = ctypes.c_float
+        L.orc_gemv_f32_fma.argtypes = [_f32p, ctypes.c_int, ctypes.c_int, _f32p, _f32p]
+        L.orc_gemv_q8_fma.argtypes = [_i8p, _f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int, _f32p, _f32p]
         L.orc_rms_norm.argtypes = [_f32p, _f32p, ctypes.c_int, ctypes.c_float]
         L.orc_layer_norm.argtypes = [_f32p, _f32p, _f32p, _f32p, ctypes.c_int, ctypes.c_float]
         L.orc_ssm_d16.argtypes = [_f32p] * 8 + [ctypes.c_int]
@@ -123,9 +131,10 @@ def softmax(logits) -> np.ndarray:
     return out
 
 
-def dot(w, v) -> float:
+def dot(w, v, fma: bool = False) -> float:
+    """One dot product in the reference GEMV order, numeric contract 1 (or 2 with fma)."""
     w, v = f32c(w), f32c(v)
-    return lib().orc_dot_f32(_p(w), _p(v), w.size)
+    return (lib().orc_dot_f32_fma if fma else lib().orc_dot_f32)(_p(w), _p(v), w.size)
 
 
 def quantize(w, group: int):
@@ -158,18 +167,19 @@ def q8_matvec_a8(q, scales, vq, v_scale) -> np.ndarray:
     return out
 
 
-def gemv_f32(w, v) -> np.ndarray:
+def gemv_f32(w, v, fma: bool = False) -> np.ndarray:
     w, v = f32c(w), f32c(v)
     out = np.empty(w.shape[0], np.float32)
-    lib().orc_gemv_f32(_p(w), w.shape[0], w.shape[1], _p(v), _p(out))
+    (lib().orc_gemv_f32_fma if fma else lib().orc_gemv_f32)(_p(w), w.shape[0], w.shape[1], _p(v), _p(out))
     return out
 
 
-def gemv_q8(q, scales, group: int, v) -> np.ndarray:
+def gemv_q8(q, scales, group: int, v, fma: bool = False) -> np.ndarray:
     q = np.ascontiguousarray(q, dtype=np.int8)
     sc, v = f32c(scales), f32c(v)
     out = np.empty(q.shape[0], np.float32)
-    lib().orc_gemv_q8(_p(q, ctypes.c_int8), _p(sc), q.shape[0], q.shape[1], group, _p(v), _p(out))
+    (lib().orc_gemv_q8_fma if fma else lib().orc_gemv_q8)(_p(q, ctypes.c_int8), _p(sc), q.shape[0], q.shape[1],
+                                                           group, _p(v), _p(out))
     return out
 
 
