@@ -120,9 +120,23 @@ int32_t redukt_backend_forward_batch(uint32_t n_streams, const uint32_t* slots, 
  * bit.  Needs per-row weights (low bits 2) and LoRA ranks in multiples of 8; INIT_FAILED for
  * Mamba models or another profile. */
 #define BACKEND_PROFILE_W8A8 32u
+/* Profile bit 6: Mamba in the reference CPU path's own arithmetic, the reference-order tier.
+ * Every projection (in_proj, x_proj, dt_proj, out_proj, head) is the reference GEMV of each
+ * output row, f32_rows / q8w_rows (src/domain/gemv.rs:181-194, 459-502): eight accumulators
+ * by column residue, the fixed horizontal sum, the sequential tail, Q8 rows folded over
+ * their column groups; the norms are the reference's sequential sums
+ * (src/domain/tensor.rs:900-908, 1390-1398) and the scan takes the portable exp, so the
+ * logits and the recurrent state equal the CPU path's (numeric contract 1, the "Plain"
+ * kernel family) bit for bit, for F32, group-64 and per-row int8 weights alike.  Slower
+ * than the other tiers: its GEMVs run one output per thread on the vector ALUs. */
+#define BACKEND_PROFILE_EXACT 64u
+/* Profile bit 7: the reference-order tier in numeric contract 2 (fma-v1,
+ * src/domain/gemv_fma.rs:1-134): the same orders with every acc + w * x of a projection,
+ * and every sum + dot * scale of a Q8 row, one fused multiply-add.  Implies bit 6. */
+#define BACKEND_PROFILE_FMA 128u
 
 /* redukt_backend_init with an explicit weight profile (the model file stays F32); a profile
- * with a bit above bit 5 -> INVALID_ARGUMENT. */
+ * with a bit above bit 7 -> INVALID_ARGUMENT. */
 int32_t redukt_backend_init_ex(const uint8_t* weights_path, int32_t device_id, uint32_t profile,
                                BackendInfo* info_out);
 

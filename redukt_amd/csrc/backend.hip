@@ -57,7 +57,10 @@ struct Model {
     std::vector<DLayer> layers;
     TMat emb, head_own;
     GMat g_emb, g_head_own;   // the wavefront-GEMV tier's embedding / untied head
+    RowMat e_emb, e_head_own; // the reference-order tier's embedding / untied head
     bool gemv = false;        // weight profile bit 4
+    bool exact = false;       // weight profile bit 6 or 7: the reference-order tier
+    bool exact_fma = false;   // bit 7: its numeric contract 2 (fma-v1)
     bool r_a8 = false;        // weight profile bit 5: the RWKV-7 W8A8 tier
     bool tied = true;
     float* norm_f_w = nullptr;
@@ -247,6 +250,32 @@ bool make_gmat(GMat& m, const float* w, int rows, int cols, bool q8) {
     return m.w != nullptr;
 }
 
+// Upload a row-major [rows][cols] matrix as the reference holds it (RowMat): F32
+// (quant_group 0) or the Q8 recipe with quant_group columns per scale (cols = per row).
+bool make_rowmat(RowMat& m, const float* w, int rows, int cols, int quant_group) {
+    m.rows = rows;
+    m.cols = cols;
+    if (quant_group == 0) {
+        m.group = 0;
+        m.w = dev_upload(w, (size_t)rows * cols);
+        return m.w != nullptr;
+    }
+    std::vector<int8_t> q;
+    std::vector<float> sc;
+    m.group = quantize(w, rows, cols, quant_group, q, sc);
+    m.w = dev_upload(q.data(), q.size());
+    m.scales = dev_upload(sc.data(), sc.size());
+    return m.w && m.scales;
+}
+
+// The tile-shape fields of x_proj that size its outputs' row stride (xr_pad), for the tiers
+// that keep x_proj in another layout.
+void xproj_shape(TMat& t, int xr, int di) {
+    t.rows = xr;
+    t.cols = di;
+    t.rt = (xr + kRowTile - 1) / kRowTile;
+}
+
 struct Reader {
     FILE* f;
     bool ok = true;
@@ -302,14 +331,18 @@ int load_weights(const std::string& path, uint32_t profile) {
         }
     }
     G.gemv = gemv;
+    const bool exact = (profile & (BACKEND_PROFILE_EXACT | BACKEND_PROFILE_FMA)) != 0;
+    G.exact = exact;
+    G.exact_fma = (profile & BACKEND_PROFILE_FMA) != 0;
     const size_t V = D.vocab, d = D.d, di = D.di, dc = D.dc, dr = D.dr, xr = D.xr();
     log("rbin v%u: d=%u di=%u ds=%u dc=%u dr=%u nl=%u vs=%u flags=0x%02x tok=%u profile=%u", h[1], D.d, D.di, D.ds,
         D.dc, D.dr, D.nl, D.vocab, D.flags, D.tokenizer, profile);
     bool ok = true;
     {
         std::vector<float> e = rd.read(V * d);
-        ok = rd.ok && (gemv ? make_gmat(G.g_emb, e.data(), (int)V, (int)d, quant != 0)
-                            : make_tmat(G.emb, e.data(), (int)V, (int)d, qgroup((int)d)));
+        ok = rd.ok && (exact  ? make_rowmat(G.e_emb, e.data(), (int)V, (int)d, qgroup((int)d))
+                       : gemv ? make_gmat(G.g_emb, e.data(), (int)V, (int)d, quant != 0)
+                              : make_tmat(G.emb, e.data(), (int)V, (int)d, qgroup((int)d)));
     }
     G.layers.assign(D.nl, DLayer{});
     for (uint32_t i = 0; ok && i < D.nl; i++) {
@@ -319,7 +352,9 @@ int load_weights(const std::string& path, uint32_t profile) {
         if (ok && nb) { t = rd.read(d); ok = rd.ok && (L.norm_b = dev_upload(t.data(), d)); }
         if (ok) {
             t = rd.read(2 * di * d);
-            if (gemv)
+            if (exact)
+                ok = rd.ok && make_rowmat(L.e_in, t.data(), (int)(2 * di), (int)d, qgroup((int)d));
+            else if (gemv)
                 ok = rd.ok && make_gmat(L.g_in, t.data(), (int)(2 * di), (int)d, quant != 0);
             else
                 ok = rd.ok && make_tmat(L.in_x, t.data(), (int)di, (int)d, qgroup((int)d)) &&
@@ -329,11 +364,12 @@ int load_weights(const std::string& path, uint32_t profile) {
         if (ok) { t = rd.read(di); ok = rd.ok && (L.conv_b = dev_upload(t.data(), di)); }
         if (ok) {
             t = rd.read(xr * di);
-            if (gemv) {
+            if (exact) {
+                xproj_shape(L.x_proj, (int)xr, (int)di);
+                ok = rd.ok && make_rowmat(L.e_xp, t.data(), (int)xr, (int)di, qsmall ? qgroup((int)di) : 0);
+            } else if (gemv) {
                 // row-major for the GEMV tier's x_proj partials; the tile shape fields only
-                L.x_proj.rows = (int)xr;
-                L.x_proj.cols = (int)di;
-                L.x_proj.rt = (int)((xr + kRowTile - 1) / kRowTile);
+                xproj_shape(L.x_proj, (int)xr, (int)di);
                 if (qsmall) {
                     std::vector<int8_t> q;
                     std::vector<float> sc;
@@ -382,8 +418,9 @@ int load_weights(const std::string& path, uint32_t profile) {
         if (ok) { t = rd.read(di); ok = rd.ok && (L.d_vec = dev_upload(t.data(), di)); }
         if (ok) {
             t = rd.read(d * di);
-            ok = rd.ok && (gemv ? make_gmat(L.g_out, t.data(), (int)d, (int)di, quant != 0)
-                                : make_tmat(L.out_proj, t.data(), (int)d, (int)di, qgroup((int)di)));
+            ok = rd.ok && (exact  ? make_rowmat(L.e_out, t.data(), (int)d, (int)di, qgroup((int)di))
+                           : gemv ? make_gmat(L.g_out, t.data(), (int)d, (int)di, quant != 0)
+                                  : make_tmat(L.out_proj, t.data(), (int)d, (int)di, qgroup((int)di)));
         }
         if (ok && ((i + 1) % 8 == 0 || i + 1 == D.nl)) log("loaded layer %u/%u", i + 1, D.nl);
     }
@@ -392,8 +429,9 @@ int load_weights(const std::string& path, uint32_t profile) {
     G.tied = !uh;
     if (ok && uh) {
         std::vector<float> t = rd.read(V * d);
-        ok = rd.ok && (gemv ? make_gmat(G.g_head_own, t.data(), (int)V, (int)d, quant != 0)
-                            : make_tmat(G.head_own, t.data(), (int)V, (int)d, qgroup((int)d)));
+        ok = rd.ok && (exact  ? make_rowmat(G.e_head_own, t.data(), (int)V, (int)d, qgroup((int)d))
+                       : gemv ? make_gmat(G.g_head_own, t.data(), (int)V, (int)d, quant != 0)
+                              : make_tmat(G.head_own, t.data(), (int)V, (int)d, qgroup((int)d)));
     }
     fclose(f);
     return ok ? 0 : -1;
@@ -710,7 +748,8 @@ bool pool_alloc(Pool& p, uint32_t cap) {
         c.take(p.z, n * di);
         c.take(p.xpart, xpart_floats(D, cap));
         c.take(p.glimb, glimb_elems(D, cap));
-        c.take(p.g32, G.gemv ? n * di : 0);
+        c.take(p.g32, G.gemv || G.exact ? n * di : 0);
+        c.take(p.normed, G.exact ? n * d : 0);
         c.take(p.out, n * D.vocab);
         c.take(p.conv, (size_t)D.nl * ns * di * (D.dc - 1));
         c.take(p.ssm, (size_t)D.nl * ns * di * 16);
@@ -738,6 +777,11 @@ ModelView model_view() {
                      (G.profile & BACKEND_PROFILE_EXACT_SCAN) != 0};
 }
 
+ExactView exact_view() {
+    return ExactView{&G.dims, G.layers.data(), &G.e_emb, G.tied ? &G.e_emb : &G.e_head_own, G.norm_f_w, G.norm_f_b,
+                     G.exact_fma};
+}
+
 GemvView gemv_view() {
     return GemvView{&G.dims, G.layers.data(), &G.g_emb, G.tied ? &G.g_emb : &G.g_head_own, G.norm_f_w,
                     (G.profile & BACKEND_PROFILE_EXACT_SCAN) != 0};
@@ -752,6 +796,10 @@ hipError_t run_step(Pool& p, uint32_t n, const uint32_t* slots, const uint32_t* 
     }
     if (G.gemv) {
         const GemvStep src(gemv_view());
+        return G.runner.run(src, p, io, G.stream, &G.probe);
+    }
+    if (G.exact) {
+        const ExactStep src(exact_view());
         return G.runner.run(src, p, io, G.stream, &G.probe);
     }
     const MambaStep src(model_view());
@@ -854,7 +902,7 @@ uint32_t env_weight_profile() {
     if (!strcmp(e, "q8row")) return BACKEND_PROFILE_Q8_ROW;
     if (!strcmp(e, "q8row-all")) return BACKEND_PROFILE_Q8_ROW | BACKEND_PROFILE_Q8_SMALL;
     if (!strcmp(e, "q8-all")) return BACKEND_PROFILE_Q8_G64 | BACKEND_PROFILE_Q8_SMALL;
-    return (uint32_t)strtoul(e, nullptr, 0) & 31u;
+    return (uint32_t)strtoul(e, nullptr, 0) & 255u;
 }
 
 // REDUKT_GPU_SPLIT: most parts (sub-batches on their own streams) a step is split into.
@@ -927,7 +975,8 @@ bool noalloc_view(Pool& v, uint32_t n, unsigned char* base, size_t* used) {
     c.take(v.z, (size_t)n * D.di);
     c.take(v.xpart, xpart_floats(D, n));
     c.take(v.glimb, glimb_elems(D, n));
-    if (G.gemv) c.take(v.g32, (size_t)n * D.di);
+    if (G.gemv || G.exact) c.take(v.g32, (size_t)n * D.di);
+    if (G.exact) c.take(v.normed, (size_t)n * D.d);
     *used = (c.off + 255) & ~(size_t)255;
     v.out = nullptr;
     v.d_slots = v.h_slots = nullptr;
@@ -962,6 +1011,12 @@ int init_common(const uint8_t* weights_path, int32_t device_id, uint32_t profile
         free_model();
         return BACKEND_INIT_FAILED;
     }
+    if ((profile & (BACKEND_PROFILE_EXACT | BACKEND_PROFILE_FMA)) &&
+        (G.kind != kKindMamba || (profile & (BACKEND_PROFILE_GEMV | BACKEND_PROFILE_W8A8)))) {
+        log("the reference-order tier serves Mamba models only, apart from the GEMV and W8A8 tiers");
+        free_model();
+        return BACKEND_INIT_FAILED;
+    }
     if ((profile & BACKEND_PROFILE_W8A8) && (G.kind != kKindRwkv || (profile & 3) != BACKEND_PROFILE_Q8_ROW)) {
         log("the W8A8 tier serves RWKV-7 with per-row int8 weights only");
         free_model();
@@ -989,7 +1044,12 @@ int init_common(const uint8_t* weights_path, int32_t device_id, uint32_t profile
     info_out->hidden_dim = G.dims.d;
     static const char* names[2][3] = {{"hip-gfx950-mamba-f32", "hip-gfx950-mamba-q8", "hip-gfx950-mamba-q8row"},
                                        {"hip-gfx950-rwkv7-f32", "hip-gfx950-rwkv7-q8", "hip-gfx950-rwkv7-q8row"}};
-    const char* name = G.r_a8 ? "hip-gfx950-rwkv7-w8a8" : names[G.kind == kKindRwkv ? 1 : 0][profile & 3];
+    static const char* exact_names[2][3] = {
+        {"hip-gfx950-mamba-f32-ref", "hip-gfx950-mamba-q8-ref", "hip-gfx950-mamba-q8row-ref"},
+        {"hip-gfx950-mamba-f32-ref-fma", "hip-gfx950-mamba-q8-ref-fma", "hip-gfx950-mamba-q8row-ref-fma"}};
+    const char* name = G.r_a8    ? "hip-gfx950-rwkv7-w8a8"
+                       : G.exact ? exact_names[G.exact_fma ? 1 : 0][profile & 3]
+                                 : names[G.kind == kKindRwkv ? 1 : 0][profile & 3];
     memcpy(info_out->name, name, strlen(name));
     size_t fr = 0, tot = 0;
     (void)hipMemGetInfo(&fr, &tot);
@@ -1086,7 +1146,7 @@ int32_t redukt_backend_forward_batch(uint32_t n_streams, const uint32_t* slots, 
 
 int32_t redukt_backend_init_ex(const uint8_t* weights_path, int32_t device_id, uint32_t profile,
                                BackendInfo* info_out) {
-    if (profile > 63u) return BACKEND_INVALID_ARGUMENT;   // bits 0-5
+    if (profile > 255u) return BACKEND_INVALID_ARGUMENT;   // bits 0-7
     return init_common(weights_path, device_id, profile, info_out);
 }
 
@@ -1191,6 +1251,10 @@ int32_t redukt_backend_forward_batch_device_noalloc(uint32_t n_streams, const ui
     StepIO io{n_streams, d_slots, d_tokens, d_out, (flags & 1u) != 0, true, G.d_err};
     if (G.gemv) {
         const GemvStep src(gemv_view());
+        return G.runner.run_direct(src, v, io, G.stream) == hipSuccess ? BACKEND_OK : BACKEND_FORWARD_FAILED;
+    }
+    if (G.exact) {
+        const ExactStep src(exact_view());
         return G.runner.run_direct(src, v, io, G.stream) == hipSuccess ? BACKEND_OK : BACKEND_FORWARD_FAILED;
     }
     const MambaStep src(model_view());

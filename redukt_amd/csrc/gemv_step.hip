@@ -163,28 +163,7 @@ __global__ __launch_bounds__(kGBlock) void k_embed_g(EmbedGArgs a) {
     const uint32_t b = blockIdx.x;
     const GMat& g = a.emb;
     uint32_t tok = a.tokens[b];
-    {
-        const uint32_t s = a.slots_in[b];
-        if (a.check) {
-            __shared__ int earlier;
-            if (threadIdx.x == 0) earlier = 0;
-            __syncthreads();
-            bool dup = false, first_dup = false;
-            for (uint32_t c = threadIdx.x; c < a.n; c += blockDim.x)
-                if (c != b && a.slots_in[c] == s) {
-                    dup = true;
-                    if (c < b) first_dup = true;
-                }
-            if (first_dup) earlier = 1;
-            const bool bad = tok >= (uint32_t)g.rows || s >= a.cap;
-            if (threadIdx.x == 0 && bad) atomicOr(a.err, 1u);
-            if (dup) atomicOr(a.err, 2u);
-            __syncthreads();
-            if (threadIdx.x == 0) a.slots[b] = bad || earlier ? a.cap : s;
-        } else if (threadIdx.x == 0) {
-            a.slots[b] = clamp_slot(s, a.cap);
-        }
-    }
+    check_entry(a.slots_in, a.slots, a.n, b, tok < (uint32_t)g.rows, a.cap, a.check, a.err);
     if (tok >= (uint32_t)g.rows) tok = g.rows - 1;
     const int blk = (int)tok / g.rpi, rr = (int)tok % g.rpi, per = 64 / g.rpi;
     const float sc = g.q8 ? g.scales[tok] : 1.0f;

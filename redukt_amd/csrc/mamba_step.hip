@@ -1114,7 +1114,7 @@ struct ScanArgs {
 // A thread runs SPT streams of one channel.
 __device__ __forceinline__ float hw_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
 
-template <bool Q8DT, bool FAST, int DR, int NXB, int SPT, class SYNC>
+template <bool Q8DT, bool FAST, int DR, int NXB, int SPT, class SYNC, bool FMA = false>
 __device__ __forceinline__ void scan_body(const ScanArgs& a, uint32_t sy, uint32_t cbx, const SYNC& sync) {
     static_assert(DR >= 0 && DR <= kMaxDr && NXB >= 0 && NXB <= kMaxNxb && SPT >= 1 && SPT <= 2, "scan shape");
     // SPT streams per thread (streams SPT y .. SPT y + SPT - 1 of channel j): the channel's
@@ -1229,9 +1229,9 @@ __device__ __forceinline__ void scan_body(const ScanArgs& a, uint32_t sy, uint32
     }
 #pragma unroll
     for (int it = 0; it < kItems; it++) {
-        float acc = 0.0f;
+        float acc = pv[it][0];
 #pragma unroll
-        for (int i = 0; i < kPer; i++)
+        for (int i = 1; i < kPer; i++)
             if (NXB || i < nxb) acc += pv[it][i];
         zq[r + kBlock * it] = acc;
     }
@@ -1277,7 +1277,9 @@ __device__ __forceinline__ void scan_body(const ScanArgs& a, uint32_t sy, uint32
         // dot_avx2_order (tensor.rs:1680-1693): eight lanes by column residue, fixed tree,
         // tail.  dt_rank <= 64 means a quantized dt_proj has one scale per row (a 64-column
         // group spans the whole row or the group rule falls back to per-row), so the Q8
-        // row is 0 + dot * scale (gemv.rs:490-502).
+        // row is 0 + dot * scale (gemv.rs:490-502).  FMA: numeric contract 2, the same
+        // order with every acc + w * x and 0 + dot * scale one fused multiply-add
+        // (gemv_fma.rs:98-134).
         float dt;
         {
             const int body = dr / 8 * 8;
@@ -1286,14 +1288,15 @@ __device__ __forceinline__ void scan_body(const ScanArgs& a, uint32_t sy, uint32
             for (int c = 0; c + 8 <= kDr; c += 8) {
                 if (DR || c < body) {
 #pragma unroll
-                    for (int i = 0; i < 8; i++) l[i] += wdt[c + i] * zps[c + i];
+                    for (int i = 0; i < 8; i++)
+                        l[i] = FMA ? __builtin_fmaf(wdt[c + i], zps[c + i], l[i]) : l[i] + wdt[c + i] * zps[c + i];
                 }
             }
             float sdot = ((l[0] + l[4]) + (l[2] + l[6])) + ((l[1] + l[5]) + (l[3] + l[7]));
 #pragma unroll
             for (int c = DR / 8 * 8; c < kDr; c++)
-                if (c >= body && c < dr) sdot += wdt[c] * zps[c];
-            dt = Q8DT ? 0.0f + sdot * dts : sdot;
+                if (c >= body && c < dr) sdot = FMA ? __builtin_fmaf(wdt[c], zps[c], sdot) : sdot + wdt[c] * zps[c];
+            dt = Q8DT ? (FMA ? __builtin_fmaf(sdot, dts, 0.0f) : 0.0f + sdot * dts) : sdot;
         }
         dt = softplus_f(dt + dtb);
         const float* B = zps + dr;
@@ -1331,11 +1334,11 @@ __device__ __forceinline__ void scan_body(const ScanArgs& a, uint32_t sy, uint32
 
 // The channel blocks of a stream group (SPT streams) run on one XCD, so the group's x_proj
 // partials are fetched into one L2 and shared by its channel blocks.
-template <bool Q8DT, bool FAST, int DR, int NXB, int SPT>
+template <bool Q8DT, bool FAST, int DR, int NXB, int SPT, bool FMA = false>
 __global__ __launch_bounds__(kBlock) void k_scan(ScanArgs a) {
     const XcdTile xt = xcd_tile(blockIdx.x, ((uint32_t)a.di + kBlock - 1) / kBlock, (a.n + SPT - 1) / SPT);
     if (!xt.live) return;
-    scan_body<Q8DT, FAST, DR, NXB, SPT>(a, xt.unit, xt.part, NoWait{});
+    scan_body<Q8DT, FAST, DR, NXB, SPT, NoWait, FMA>(a, xt.unit, xt.part, NoWait{});
 }
 
 // Streams per scan thread by batch size: sharing a channel's operands pays once a launch
@@ -2234,6 +2237,16 @@ Launch scan_launch(const DLayer& L, const Dims& D, Pool& p, uint32_t n, bool exa
                         sa);
 }
 
+Launch scan_exact_launch(const DLayer& L, const Dims& D, Pool& p, uint32_t n, bool fma, float* g32, float* ssm_layer) {
+    const int di = (int)D.di;
+    ScanArgs sa = scan_args(L, D, p, n, nullptr, g32, ssm_layer);
+    sa.nxb = 1;   // one block: each stream's complete x_proj outputs
+    const bool q8 = L.dt_q != nullptr;
+    const void* fs = q8 ? (fma ? (const void*)k_scan<true, false, 0, 1, 1, true> : (const void*)k_scan<true, false, 0, 1, 1, false>)
+                        : (fma ? (const void*)k_scan<false, false, 0, 1, 1, true> : (const void*)k_scan<false, false, 0, 1, 1, false>);
+    return Launch::make(fs, dim3(xcd_grid((di + kBlock - 1) / kBlock, n)), dim3(kBlock), 0, KC_SCAN, sa);
+}
+
 Launch softmax_launch(float* out, int vocab, uint32_t n) {
     const void* f = vocab <= 1024 * kSoftmaxPer ? (const void*)k_softmax<kSoftmaxPer> : (const void*)k_softmax<0>;
     return Launch::make(f, dim3(n), dim3(1024), 0, KC_SOFTMAX, SoftmaxArgs{out, vocab});
@@ -2743,13 +2756,24 @@ hipError_t StepRunner::run(const StepSource& src, Pool& p, const StepIO& io, hip
         return hipSuccess;
     };
     if (!use_graphs()) {
-        RDK_TRY(fork());
+        static const uint32_t skew = [] {
+            const char* e = getenv("REDUKT_GPU_SKEW");
+            return e && *e ? (uint32_t)strtoul(e, nullptr, 10) : 0u;
+        }();
+        std::vector<Launch> seqs[kMaxParts];
         for (uint32_t k = 0; k < nparts; k++) {
-            std::vector<Launch> seq;
             int io_i = -1, head_i = -1, sm_i = -1;
-            src.build(p, part_io(k), seq, io_i, head_i, sm_i);
-            for (const Launch& l : seq) RDK_TRY(launch_direct(l, stream_of(k)));
+            src.build(p, part_io(k), seqs[k], io_i, head_i, sm_i);
         }
+        // Part 0's first `skew` kernels go ahead of the fork, so the other parts start
+        // that many kernels behind it.
+        const size_t ahead = std::min<size_t>(skew, seqs[0].size());
+        if (nparts > 1)
+            for (size_t i = 0; i < ahead; i++) RDK_TRY(launch_direct(seqs[0][i], st));
+        RDK_TRY(fork());
+        for (uint32_t k = 0; k < nparts; k++)
+            for (size_t i = (k == 0 && nparts > 1) ? ahead : 0; i < seqs[k].size(); i++)
+                RDK_TRY(launch_direct(seqs[k][i], stream_of(k)));
         return join();
     }
     auto same_io = [&](const Graph& g) {

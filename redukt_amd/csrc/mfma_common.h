@@ -53,6 +53,37 @@ __device__ __forceinline__ int wave_index() { return __builtin_amdgcn_readfirstl
 
 __device__ __forceinline__ uint32_t clamp_slot(uint32_t s, uint32_t cap) { return s < cap ? s : cap - 1; }
 
+// The device argument check of batch entry b of a step of n entries, run by every thread
+// of one workgroup: a token past the vocabulary (tok_ok false) or a slot past the pool
+// (error bit 0), or a slot that another entry also names (error bit 1, set for each of
+// them; the earliest keeps the slot), sends the entry to the scratch slot `cap`, which no
+// caller can name.  Thread 0 stores the slot the step uses; without `check` (entries the
+// host validated) the slot is only clamped.
+__device__ __forceinline__ void check_entry(const uint32_t* __restrict__ slots_in, uint32_t* __restrict__ slots,
+                                            uint32_t n, uint32_t b, bool tok_ok, uint32_t cap, int check,
+                                            uint32_t* err) {
+    const uint32_t s = slots_in[b];
+    if (check) {
+        __shared__ int earlier;
+        if (threadIdx.x == 0) earlier = 0;
+        __syncthreads();
+        bool dup = false, first_dup = false;
+        for (uint32_t c = threadIdx.x; c < n; c += blockDim.x)
+            if (c != b && slots_in[c] == s) {
+                dup = true;
+                if (c < b) first_dup = true;
+            }
+        if (first_dup) earlier = 1;
+        const bool bad = !tok_ok || s >= cap;
+        if (threadIdx.x == 0 && bad) atomicOr(err, 1u);
+        if (dup) atomicOr(err, 2u);
+        __syncthreads();
+        if (threadIdx.x == 0) slots[b] = bad || earlier ? cap : s;
+    } else if (threadIdx.x == 0) {
+        slots[b] = clamp_slot(s, cap);
+    }
+}
+
 // Workgroups are dealt to the XCDs round-robin by linear index (starting from wherever the
 // previous dispatch stopped, so within one launch linear indices L and L + kXcds share an
 // XCD, whichever XCD that is), and each XCD has its own L2.  A grid of `units` work units,

@@ -53,6 +53,17 @@ struct GMat {
     size_t bytes() const;
 };
 
+// A row-major [rows][cols] matrix for the reference-order tier: F32, or int8 with one f32
+// scale per `group` columns ([rows][cols / group]), the layout of the reference's own
+// Q8wMatrix (src/domain/gemv.rs:244-273).
+struct RowMat {
+    int rows = 0, cols = 0;
+    int group = 0;        // 0: F32; Q8: columns per scale
+    void* w = nullptr;
+    float* scales = nullptr;
+    size_t bytes() const { return w ? (size_t)rows * cols * (group ? 1 : 4) + (group ? (size_t)rows * (cols / group) * 4 : 0) : 0; }
+};
+
 struct DLayer {
     float* norm_w = nullptr;
     float* norm_b = nullptr;   // LayerNorm bias (flags bit 0) or null
@@ -75,6 +86,7 @@ struct DLayer {
     // GEMV layout, x_proj row-major [xr][di] (F32 in xp_w, or Q8 in xp_q with one scale per
     // row in xp_scales); dt_proj as above.
     GMat g_in, g_out;
+    RowMat e_in, e_xp, e_out;  // the reference-order tier's in_proj, x_proj and out_proj
     float* xp_w = nullptr;
     int8_t* xp_q = nullptr;
     float* xp_scales = nullptr;
@@ -111,7 +123,8 @@ struct Pool {
     float* z = nullptr;          // [cap][di] gate branch
     float* xpart = nullptr;      // [di/64][cap][xr_pad] split-K partials of x_proj
     __bf16* glimb = nullptr;     // [gcap][di/32][3][64][8] gated, 3 bf16 limbs, B-fragment tiles
-    float* g32 = nullptr;        // [cap][di] gated, f32 (the wavefront-GEMV tier)
+    float* g32 = nullptr;        // [cap][di] gated, f32 (the wavefront-GEMV and reference-order tiers)
+    float* normed = nullptr;     // [cap][d] a norm's output (the reference-order tier)
     // Next projection's input, written by the producer of the residual stream (embedding,
     // out_proj): x * norm_w as 3 bf16 limbs in B-fragment tiles, [gcap][ks_d][3][64][8]
     // with ks_d = the k-steps of a d-column projection, plus per-16-column partial sums of
@@ -158,7 +171,8 @@ enum KernelClass : uint32_t {
     KC_SHIFT = 7, KC_PROJ = 8, KC_WKV = 9,
     // the persistent step kernel (every layer of a Mamba step in one launch)
     KC_FLOW = 10,
-    KC_COUNT = 11
+    KC_NORM = 11, KC_XPROJ = 12,   // the reference-order tier's norms and x_proj
+    KC_COUNT = 13
 };
 
 // Measurement hook: while cls != KC_NONE, every launch of that class records its dispatch
@@ -315,6 +329,25 @@ struct GemvStep final : StepSource {
 // GEMV layout parameters of a K-column matrix: false if K is not a multiple of 16 or no
 // chunks-per-lane count up to 8 divides the lanes evenly.
 bool gemv_shape(int cols, int& rpi, int& cpl);
+
+struct ExactView {
+    const Dims* dims;
+    const DLayer* layers;
+    const RowMat* emb;
+    const RowMat* head;     // emb when tied
+    const float* norm_f_w;
+    const float* norm_f_b;
+    bool fma;               // numeric contract 2 (fma-v1) instead of 1
+};
+
+// The reference-order tier (weight profile bit 6; bit 7 for numeric contract 2): every
+// projection in the reference GEMV's own order, sequential norms, the portable exp in the
+// scan, one part per step.
+struct ExactStep final : StepSource {
+    ExactView m;
+    explicit ExactStep(const ExactView& v) : m(v) {}
+    void build(Pool& p, const StepIO& io, std::vector<Launch>& out, int& io_i, int& head_i, int& sm_i) const override;
+};
 
 struct RwkvStep final : StepSource {
     RwkvView m;

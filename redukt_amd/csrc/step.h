@@ -56,6 +56,10 @@ struct DLayer;
 struct Dims;
 Launch scan_launch(const DLayer& L, const Dims& D, Pool& p, uint32_t n, bool exact, __bf16* glimb, float* g32,
                    float* ssm_layer);
+// The scan of the reference-order tier: the complete x_proj outputs of each stream in
+// xpart (one block), the portable exp, the dt_proj dot in numeric contract 1 or (fma) 2,
+// the gated vector as f32 rows.
+Launch scan_exact_launch(const DLayer& L, const Dims& D, Pool& p, uint32_t n, bool fma, float* g32, float* ssm_layer);
 // The wavefront-GEMV tier: whether a chunks-per-lane count is compiled.
 bool gemv_cpl_supported(int cpl);
 // Logits [rows][n] -> CDF [rows][n + 1] on the device, bit for bit the host coding path's

@@ -153,9 +153,9 @@ def test_pre_init_error_paths_touch_no_device():
     assert L.redukt_backend_stream() is None
     info = ffi.BackendInfo()
     assert L.redukt_backend_init(None, 0, ctypes.byref(info)) == ffi.BackendResult.INIT_FAILED
-    # bits 0-5 are defined (quant, small-matrix quant, exact scan, GEMV tier, RWKV-7 W8A8);
-    # anything above is refused
-    assert L.redukt_backend_init_ex(b"x.rbin", 0, 64, ctypes.byref(info)) == ffi.BackendResult.INVALID_ARGUMENT
+    # bits 0-7 are defined (quant, small-matrix quant, exact scan, GEMV tier, RWKV-7 W8A8,
+    # the reference-order tier and its contract 2); anything above is refused
+    assert L.redukt_backend_init_ex(b"x.rbin", 0, 256, ctypes.byref(info)) == ffi.BackendResult.INVALID_ARGUMENT
     L.redukt_backend_reset_state()   # no model: a no-op
     L.redukt_backend_free()          # idempotent
 
