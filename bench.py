@@ -37,7 +37,8 @@ METRIC = "Mamba-130M tok/s at batch 1/32/128 (F32 & Q8); % of HBM roofline"
 HBM_PEAK_GBS = 8000.0
 RESET_PERIOD = 4096
 PROFILES = {"f32": 0, "q8": 1, "q8row": 2, "q8row-all": 6, "q8-all": 5,
-            "f32-gemv": 16, "q8row-gemv": 18, "q8row-all-gemv": 22, "q8row-w8a8": 34}
+            "f32-gemv": 16, "q8row-gemv": 18, "q8row-all-gemv": 22, "q8row-w8a8": 34,
+            "f32-ref": 64, "q8-ref": 65, "q8row-all-ref": 70, "f32-ref-fma": 192, "q8-ref-fma": 193}
 
 
 def log(msg: str) -> None:

@@ -250,20 +250,31 @@ bool make_gmat(GMat& m, const float* w, int rows, int cols, bool q8) {
     return m.w != nullptr;
 }
 
-// Upload a row-major [rows][cols] matrix as the reference holds it (RowMat): F32
-// (quant_group 0) or the Q8 recipe with quant_group columns per scale (cols = per row).
+// Upload a row-major [rows][cols] matrix for the reference-order tier (RowMat): F32
+// (quant_group 0) or the Q8 recipe with quant_group columns per scale (cols = per row),
+// each row's 32-column blocks interleaved by column residue (column c of a block at
+// 4 (c % 8) + c / 8).  Whole 32-column blocks only, in every row and every scale group.
 bool make_rowmat(RowMat& m, const float* w, int rows, int cols, int quant_group) {
     m.rows = rows;
     m.cols = cols;
+    if (cols % 32 != 0) return false;
+    auto inter = [&](size_t r, int c) { return r * cols + (size_t)(c & ~31) + (size_t)(4 * (c & 7) + ((c & 31) >> 3)); };
     if (quant_group == 0) {
         m.group = 0;
-        m.w = dev_upload(w, (size_t)rows * cols);
+        std::vector<float> t((size_t)rows * cols);
+        for (int r = 0; r < rows; r++)
+            for (int c = 0; c < cols; c++) t[inter(r, c)] = w[(size_t)r * cols + c];
+        m.w = dev_upload(t.data(), t.size());
         return m.w != nullptr;
     }
     std::vector<int8_t> q;
     std::vector<float> sc;
     m.group = quantize(w, rows, cols, quant_group, q, sc);
-    m.w = dev_upload(q.data(), q.size());
+    if (m.group % 32 != 0) return false;
+    std::vector<int8_t> t((size_t)rows * cols);
+    for (int r = 0; r < rows; r++)
+        for (int c = 0; c < cols; c++) t[inter(r, c)] = q[(size_t)r * cols + c];
+    m.w = dev_upload(t.data(), t.size());
     m.scales = dev_upload(sc.data(), sc.size());
     return m.w && m.scales;
 }

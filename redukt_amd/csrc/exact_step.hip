@@ -7,11 +7,12 @@
 // multiply-add).  Every projection output (row r, stream b) is the reference GEMV of that
 // row, f32_rows / q8w_rows (src/domain/gemv.rs:181-194, 459-502) or their contract-2
 // twins (gemv_fma.rs:98-134): eight accumulators by column residue from +0 over the
-// 8-aligned body in column order, the horizontal sum ((l0+l4)+(l2+l6)) + ((l1+l5)+(l3+l7)),
-// then the sequential tail; Q8 rows fold dot_g * scale_g over the column groups from +0.
-// One thread computes one output, so nothing depends on the launch shape, the batch or the
-// slot.  The norms are the reference's sequential sums (rms_norm_into, layer_norm_into:
-// src/domain/tensor.rs:900-908, 1390-1398), the scan takes the portable exp, and the
+// 8-aligned body in column order, the horizontal sum ((l0+l4)+(l2+l6)) + ((l1+l5)+(l3+l7))
+// (the tail is empty: every matrix here has whole 32-column blocks); Q8 rows fold
+// dot_g * scale_g over the column groups from +0.  Eight lanes compute one output, lane l
+// holding the reference's accumulator l, so nothing depends on the launch shape, the batch
+// or the slot.  The norms are the reference's sequential sums (rms_norm_into,
+// layer_norm_into: src/domain/tensor.rs:900-908, 1390-1398), the scan takes the portable exp, and the
 // element-wise code (conv, SiLU, softplus, the d16 recurrence, the gate, softmax) is the
 // other tiers', already the CPU path's bit for bit; so the logits are the CPU path's
 // logits.  Per layer:
@@ -40,6 +41,14 @@ namespace {
 constexpr int kEBlock = 256;      // threads (outputs) per workgroup
 constexpr int kNormMax = 1024;    // d_model limit of the loader
 
+// A RowMat stores each row in 32-column blocks interleaved by column residue: column c of
+// row r at r cols + 32 (c / 32) + 4 (c % 8) + (c % 32) / 8, so lane l of an output's eight
+// lanes finds its four columns of a block (l, l + 8, l + 16, l + 24) in one 16-byte (F32) or
+// 4-byte (Q8) run, and the eight lanes read the block's 32 columns contiguously.
+__device__ __forceinline__ size_t rowmat_index(size_t row_off, int c) {
+    return row_off + (size_t)(c & ~31) + (size_t)(4 * (c & 7) + ((c & 31) >> 3));
+}
+
 // ---------------------------------------------------------------- embedding
 
 struct EmbedEArgs {
@@ -64,13 +73,13 @@ __global__ __launch_bounds__(kEBlock) void k_embed_e(EmbedEArgs a) {
     if (tok >= (uint32_t)e.rows) tok = e.rows - 1;
     const int cols = e.cols;
     float* xo = a.x + (size_t)b * cols;
+    const size_t row_off = (size_t)tok * cols;
     if (e.group == 0) {
-        const float* row = (const float*)e.w + (size_t)tok * cols;
-        for (int c = threadIdx.x; c < cols; c += kEBlock) xo[c] = row[c];
+        for (int c = threadIdx.x; c < cols; c += kEBlock) xo[c] = ((const float*)e.w)[rowmat_index(row_off, c)];
     } else {
-        const int8_t* row = (const int8_t*)e.w + (size_t)tok * cols;
         const float* sc = e.scales + (size_t)tok * (cols / e.group);
-        for (int c = threadIdx.x; c < cols; c += kEBlock) xo[c] = (float)row[c] * sc[c / e.group];
+        for (int c = threadIdx.x; c < cols; c += kEBlock)
+            xo[c] = (float)((const int8_t*)e.w)[rowmat_index(row_off, c)] * sc[c / e.group];
     }
 }
 
@@ -153,33 +162,28 @@ __device__ __forceinline__ float madd(float w, float x, float acc) {
     return FMA ? __builtin_fmaf(w, x, acc) : acc + w * x;
 }
 
-// Eight weights of row `row` from column c (c a multiple of 8): F32 as stored, Q8 as the
-// exact f32 of each int8.
+// Lane l's four weights of the 32-column block at column c0, as exact f32.
 template <bool Q8>
-__device__ __forceinline__ void load8(const RowMat& m, size_t row_off, int c, float (&w)[8]) {
+__device__ __forceinline__ void load4(const RowMat& m, size_t row_off, int c0, int l, float (&w)[4]) {
+    const size_t at = row_off + (size_t)c0 + 4 * l;
     if (Q8) {
-        const uint2 q = *(const uint2*)((const int8_t*)m.w + row_off + c);
+        const uint32_t q = *(const uint32_t*)((const int8_t*)m.w + at);
 #pragma unroll
-        for (int i = 0; i < 8; i++) w[i] = (float)(int8_t)((i < 4 ? q.x : q.y) >> (8 * (i % 4)));
+        for (int j = 0; j < 4; j++) w[j] = (float)(int8_t)(q >> (8 * j));
     } else {
-        const float4* p = (const float4*)((const float*)m.w + row_off + c);
-        const float4 lo = p[0], hi = p[1];
-        w[0] = lo.x, w[1] = lo.y, w[2] = lo.z, w[3] = lo.w;
-        w[4] = hi.x, w[5] = hi.y, w[6] = hi.z, w[7] = hi.w;
+        const float4 v = *(const float4*)((const float*)m.w + at);
+        w[0] = v.x, w[1] = v.y, w[2] = v.z, w[3] = v.w;
     }
 }
 
-template <bool Q8>
-__device__ __forceinline__ float load1(const RowMat& m, size_t row_off, int c) {
-    return Q8 ? (float)((const int8_t*)m.w)[row_off + c] : ((const float*)m.w)[row_off + c];
-}
-
-// Thread t of workgroup (bx, by) computes row bx * kEBlock + t for streams [S by, S by + S);
-// the streams' input rows are staged in LDS (every thread reads the same words).  Per
-// (row, stream), over each column group in order (F32: the whole row, one group without a
-// scale): eight accumulators over the group's 8-aligned body, the fixed horizontal sum,
-// the sequential tail; Q8: sum = sum + dot * scale from +0.  Every operation in the
-// contract's arithmetic (madd), every add and product of contract 1 rounded on its own.
+// Eight lanes compute one output (row, S streams): lane l holds accumulator l of the
+// reference's eight, the columns c = l (mod 8) of each column group in order from +0; the
+// horizontal sum ((l0+l4)+(l2+l6)) + ((l1+l5)+(l3+l7)) is the xor butterfly 4, 2, 1 over
+// the eight lanes (IEEE addition is commutative, so each lane pair forms exactly the
+// reference's sums); Q8 rows then take sum = sum + dot * scale from +0.  Workgroup (bx, by)
+// holds rows [32 bx, 32 bx + 32) and streams [S by, S by + S), the streams' input rows
+// staged in LDS.  Every operation in the contract's arithmetic (madd).  Column counts and
+// groups are whole 32-column blocks (checked at load).
 template <bool Q8, bool FMA, int S, int EPI>
 __global__ __launch_bounds__(kEBlock) void k_gemv_e(GemvEArgs a) {
     extern __shared__ float acts[];   // [S][cols]
@@ -192,51 +196,40 @@ __global__ __launch_bounds__(kEBlock) void k_gemv_e(GemvEArgs a) {
         for (int c = threadIdx.x; c < cols; c += kEBlock) acts[s * cols + c] = src[c];
     }
     __syncthreads();
-    const int r = (int)blockIdx.x * kEBlock + (int)threadIdx.x;
-    if (r >= m.rows) return;
+    const int l = (int)threadIdx.x % 8;
+    const int r_raw = (int)blockIdx.x * (kEBlock / 8) + (int)threadIdx.x / 8;
+    const bool live = r_raw < m.rows;
+    const int r = live ? r_raw : m.rows - 1;   // every lane joins the butterflies
     const size_t row_off = (size_t)r * cols;
     const int group = Q8 ? m.group : cols;
     const int ng = cols / group;
-    const int body = group / 8 * 8;
     float res[S];
 #pragma unroll
     for (int s = 0; s < S; s++) res[s] = 0.0f;
     for (int g = 0; g < ng; g++) {
         const int c0 = g * group;
-        float acc[S][8];
+        float acc[S];
 #pragma unroll
-        for (int s = 0; s < S; s++)
-#pragma unroll
-            for (int l = 0; l < 8; l++) acc[s][l] = 0.0f;
+        for (int s = 0; s < S; s++) acc[s] = 0.0f;
 #pragma unroll 4
-        for (int c = c0; c < c0 + body; c += 8) {
-            float w[8];
-            load8<Q8>(m, row_off, c, w);
+        for (int c = c0; c < c0 + group; c += 32) {
+            float w[4];
+            load4<Q8>(m, row_off, c, l, w);
 #pragma unroll
-            for (int s = 0; s < S; s++) {
-                const float4 x0 = *(const float4*)(acts + s * cols + c);
-                const float4 x1 = *(const float4*)(acts + s * cols + c + 4);
-                acc[s][0] = madd<FMA>(w[0], x0.x, acc[s][0]);
-                acc[s][1] = madd<FMA>(w[1], x0.y, acc[s][1]);
-                acc[s][2] = madd<FMA>(w[2], x0.z, acc[s][2]);
-                acc[s][3] = madd<FMA>(w[3], x0.w, acc[s][3]);
-                acc[s][4] = madd<FMA>(w[4], x1.x, acc[s][4]);
-                acc[s][5] = madd<FMA>(w[5], x1.y, acc[s][5]);
-                acc[s][6] = madd<FMA>(w[6], x1.z, acc[s][6]);
-                acc[s][7] = madd<FMA>(w[7], x1.w, acc[s][7]);
-            }
+            for (int j = 0; j < 4; j++)
+#pragma unroll
+                for (int s = 0; s < S; s++) acc[s] = madd<FMA>(w[j], acts[s * cols + c + 8 * j + l], acc[s]);
         }
 #pragma unroll
         for (int s = 0; s < S; s++) {
-            float dot = ((acc[s][0] + acc[s][4]) + (acc[s][2] + acc[s][6])) +
-                        ((acc[s][1] + acc[s][5]) + (acc[s][3] + acc[s][7]));
-            for (int c = c0 + body; c < c0 + group; c++) dot = madd<FMA>(load1<Q8>(m, row_off, c), acts[s * cols + c], dot);
-            if (Q8)
-                res[s] = madd<FMA>(dot, m.scales[(size_t)r * ng + g], res[s]);
-            else
-                res[s] = dot;
+            float v = acc[s];
+            v = v + __shfl_xor(v, 4, 8);
+            v = v + __shfl_xor(v, 2, 8);
+            v = v + __shfl_xor(v, 1, 8);
+            res[s] = Q8 ? madd<FMA>(v, m.scales[(size_t)r * ng + g], res[s]) : v;
         }
     }
+    if (!live || l != 0) return;
 #pragma unroll
     for (int s = 0; s < S; s++) {
         const uint32_t b = b0 + (uint32_t)s;
@@ -292,8 +285,9 @@ Launch gemv_e_launch(const void* fn, int cls, const RowMat& w, const float* act,
     a.act = act;
     a.n = n;
     const uint32_t lds = S * (uint32_t)w.cols * 4u;
-    return Launch::make(fn, dim3((unsigned)((w.rows + kEBlock - 1) / kEBlock), (n + S - 1) / S), dim3(kEBlock), lds,
-                        (uint32_t)cls, a);
+    constexpr int rows_per_wg = kEBlock / 8;
+    return Launch::make(fn, dim3((unsigned)((w.rows + rows_per_wg - 1) / rows_per_wg), (n + S - 1) / S),
+                        dim3(kEBlock), lds, (uint32_t)cls, a);
 }
 
 }  // namespace
