@@ -301,8 +301,11 @@ class Workload:
 
 
 # The grid of the metric: both weight profiles at 1, 32 and 128 streams on the matrix-core
-# family, and the wavefront-GEMV tier (the small-batch family) where it is competitive.
-GRID = {"f32": (1, 32, 128), "q8row-all": (1, 32, 128), "f32-gemv": (1, 32), "q8row-all-gemv": (1, 32)}
+# family, the wavefront-GEMV tier (the small-batch family) where it is competitive, and the
+# reference-order tier (logits bit-identical to the CPU path) with the reference's own int8
+# profile (groups of 64).
+GRID = {"f32": (1, 32, 128), "q8row-all": (1, 32, 128), "f32-gemv": (1, 32), "q8row-all-gemv": (1, 32),
+        "q8-ref": (1, 32)}
 
 
 def grid_rates(path: str, grid, K: int, W: int) -> dict:

@@ -98,30 +98,45 @@ struct NormEArgs {
 // output.  RMSNorm (tensor.rs:900-908): inv = 1 / sqrt(sum(x^2) / d + 1e-5),
 // out = x * inv * w.  LayerNorm (tensor.rs:1390-1398, two passes): mean = sum(x) / d,
 // var = sum((x - mean)^2) / d, out = (x - mean) * (1 / sqrt(var + 1e-5)) * w + b.
+// The sequential sum of t[0 .. d) (d a multiple of 4) by one thread, in index order: the
+// reads go ahead in float4s, only the adds form the chain.
+__device__ __forceinline__ float seq_sum(const float* t, int d) {
+    float s = 0.0f;
+#pragma unroll 8
+    for (int i = 0; i < d; i += 4) {
+        const float4 v = *(const float4*)(t + i);
+        s = s + v.x;
+        s = s + v.y;
+        s = s + v.z;
+        s = s + v.w;
+    }
+    return s;
+}
+
 __global__ __launch_bounds__(kEBlock) void k_norm_e(NormEArgs a) {
-    __shared__ float xs[kNormMax];
+    __shared__ __align__(16) float xs[kNormMax];
+    __shared__ __align__(16) float tv[kNormMax];   // the terms of the sum in flight
     __shared__ float stat[2];
     const int d = a.d;
     const float* x = a.x + (size_t)blockIdx.x * d;
     for (int i = threadIdx.x; i < d; i += kEBlock) xs[i] = x[i];
     __syncthreads();
-    if (threadIdx.x == 0) {
-        if (a.bias == nullptr) {
-            float ss = 0.0f;
-            for (int i = 0; i < d; i++) ss += xs[i] * xs[i];
-            const float rms = sqrtf(ss / (float)d + 1e-5f);
+    if (a.bias == nullptr) {
+        // each term x * x rounded on its own, as in ss += x * x
+        for (int i = threadIdx.x; i < d; i += kEBlock) tv[i] = xs[i] * xs[i];
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            const float rms = sqrtf(seq_sum(tv, d) / (float)d + 1e-5f);
             stat[0] = 0.0f;
             stat[1] = 1.0f / rms;
-        } else {
-            float sum = 0.0f;
-            for (int i = 0; i < d; i++) sum += xs[i];
-            const float mean = sum / (float)d;
-            float vs = 0.0f;
-            for (int i = 0; i < d; i++) vs += (xs[i] - mean) * (xs[i] - mean);
-            const float var = vs / (float)d;
-            stat[0] = mean;
-            stat[1] = 1.0f / sqrtf(var + 1e-5f);
         }
+    } else {
+        if (threadIdx.x == 0) stat[0] = seq_sum(xs, d) / (float)d;
+        __syncthreads();
+        const float mean = stat[0];
+        for (int i = threadIdx.x; i < d; i += kEBlock) tv[i] = (xs[i] - mean) * (xs[i] - mean);
+        __syncthreads();
+        if (threadIdx.x == 0) stat[1] = 1.0f / sqrtf(seq_sum(tv, d) / (float)d + 1e-5f);
     }
     __syncthreads();
     float* o = a.out + (size_t)blockIdx.x * d;
