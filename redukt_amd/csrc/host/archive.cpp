@@ -67,7 +67,9 @@ bool mamba_family(uint8_t backbone) {
 // check_contract_backbone (codec.rs:448-457): fma-v1 exists for the Mamba family only.
 int32_t check_contract(uint8_t contract, uint8_t backbone, char* err, size_t cap) {
     if (contract == 2 && !mamba_family(backbone))
-        return fail(err, cap, "RDKT numeric contract fma-v1 is only defined for the Mamba family, not backbone %u",
+        return fail(err, cap,
+                    "archive asks for numeric contract 2 (fma-v1), which only Mamba backbones have; "
+                    "backbone byte is %u",
                     backbone);
     return REDUKT_CODEC_OK;
 }
@@ -75,14 +77,14 @@ int32_t check_contract(uint8_t contract, uint8_t backbone, char* err, size_t cap
 // parse_profile_byte (codec.rs:216-243).
 int32_t parse_profile(uint8_t b, uint8_t* quant, uint8_t* contract, char* err, size_t cap) {
     if (b & ~(kProfileQuantMask | kProfileContractMask | kProfileResetFlag))
-        return fail(err, cap, "RDKT v5 PROFILE has reserved bits set: 0x%02X", b);
+        return fail(err, cap, "archive PROFILE byte 0x%02X uses reserved bits", b);
     const uint8_t c = (b & kProfileContractMask) >> 4;
     if (c > 2)
-        return fail(err, cap, "RDKT v5 numeric contract %u not supported by this build (known: 0 = legacy libm, "
-                    "1 = fmath-v1, 2 = fma-v1)", c);
+        return fail(err, cap, "archive numeric contract %u is unknown here (this reader knows 0 legacy libm, "
+                    "1 fmath-v1, 2 fma-v1)", c);
     const uint8_t q = b & kProfileQuantMask;
     if (q > 1)
-        return fail(err, cap, "RDKT v5 weight profile code %u = %s - not supported by this build", q,
+        return fail(err, cap, "archive weight profile code %u (%s) has no decoder here", q,
                     q == 2 ? "Q6 (reserved)" : "unknown");
     *quant = q;
     *contract = c;
@@ -128,7 +130,7 @@ extern "C" int32_t redukt_rdkt_build_header(const redukt_rdkt_header* h, uint8_t
     if (h->contract > 2) return fail(err, err_cap, "unknown numeric contract %u", h->contract);
     if (h->backbone > REDUKT_RDKT_BACKBONE_PLUGIN) return fail(err, err_cap, "unknown backbone %u", h->backbone);
     if (h->reset_log2 && (h->reset_log2 < kResetMin || h->reset_log2 > kResetMax))
-        return fail(err, err_cap, "RESET_LOG2 out of range: %u (expected %u..=%u)", h->reset_log2, kResetMin,
+        return fail(err, err_cap, "reset period exponent %u lies outside %u..%u", h->reset_log2, kResetMin,
                     kResetMax);
     if (h->emb_method > 3) return fail(err, err_cap, "unknown emb-surgery method %u", h->emb_method);
     if (int32_t rc = check_contract(h->contract, h->backbone, err, err_cap)) return rc;
@@ -179,22 +181,25 @@ extern "C" int32_t redukt_rdkt_validate_magic(const uint8_t* data, size_t len, u
                                               size_t err_cap) {
     // codec.rs:177-210.
     if (!data && len) return fail(err, err_cap, "null data");
-    if (len < 8) return fail(err, err_cap, "invalid RDKT file (too short: %zu bytes)", len);
+    if (len < 8) return fail(err, err_cap, "%zu bytes cannot hold an archive header", len);
     const bool legacy = std::memcmp(data, "AZTH", 4) == 0;
-    if (!legacy && std::memcmp(data, "RDKT", 4) != 0) return fail(err, err_cap, "invalid RDKT file (bad magic)");
+    if (!legacy && std::memcmp(data, "RDKT", 4) != 0)
+        return fail(err, err_cap, "not an archive: the first four bytes are neither RDKT nor AZTH");
     const uint8_t ver = data[4];
     if (!legacy && ver < 5)
-        return fail(err, err_cap, "unsupported RDKT version %u (RDKT starts at 5; versions 2 to 4 exist only as "
-                    "legacy AZTH)", ver);
+        return fail(err, err_cap, "RDKT archives begin at version 5; version %u "
+                    "is only valid under the legacy AZTH magic", ver);
     size_t min_size;
     switch (ver) {
         case 2:
         case 3: min_size = kV23Header; break;
         case 4: min_size = kV4Base; break;
         case 5: min_size = kV5Base; break;
-        default: return fail(err, err_cap, "unsupported RDKT version %u (expected 2, 3, 4 or 5)", ver);
+        default: return fail(err, err_cap, "archive version %u is not one of 2, 3, 4, 5", ver);
     }
-    if (len < min_size) return fail(err, err_cap, "invalid RDKT v%u (too short: %zu < %zu)", ver, len, min_size);
+    if (len < min_size)
+        return fail(err, err_cap, "version-%u header needs more bytes than the %zu given (at least %zu)", ver, len,
+                    min_size);
     if (version) *version = ver;
     return REDUKT_CODEC_OK;
 }
@@ -216,7 +221,7 @@ extern "C" int32_t redukt_rdkt_parse_header(const uint8_t* data, size_t len, red
         r.token_count = rd_u32(data + 12);
         const float hp[3] = {rd_f32(data + 16), rd_f32(data + 20), rd_f32(data + 24)};
         for (float x : hp)
-            if (!std::isfinite(x)) return fail(err, err_cap, "invalid hyperparameter (NaN or Inf)");
+            if (!std::isfinite(x)) return fail(err, err_cap, "archive hyperparameter is not finite");
         r.bias_lr = hp[0];
         r.ngram_scale = hp[1];
         r.mix_eta = hp[2];
@@ -231,24 +236,28 @@ extern "C" int32_t redukt_rdkt_parse_header(const uint8_t* data, size_t len, red
         if (int32_t rc = parse_profile(data[13], &r.quant, &r.contract, err, err_cap)) return rc;
         off = kV5Base;
         if (data[13] & kProfileResetFlag) {
-            if (len < off + 1) return fail(err, err_cap, "RDKT v5 RESET_LOG2 truncated: %zu < %zu", len, off + 1);
+            if (len < off + 1)
+                return fail(err, err_cap, "archive ends inside its reset-period byte (%zu bytes, %zu needed)", len,
+                            off + 1);
             const uint8_t l = data[off];
             if (l < kResetMin || l > kResetMax)
-                return fail(err, err_cap, "RDKT v5 RESET_LOG2 out of range: %u (expected %u..=%u)", l, kResetMin,
+                return fail(err, err_cap, "archive reset period exponent %u lies outside %u..%u", l, kResetMin,
                             kResetMax);
             r.reset_log2 = l;
             off += 1;
         }
     }
     auto need = [&](size_t n, const char* what) {
-        if (len < off + n) return fail(err, err_cap, "RDKT v%u %s truncated: %zu < %zu", ver, what, len, off + n);
+        if (len < off + n)
+            return fail(err, err_cap, "version-%u archive ends inside its %s (%zu bytes, %zu needed)", ver, what, len,
+                        off + n);
         return int32_t(REDUKT_CODEC_OK);
     };
     if (flags & kFlagCustomHp) {
         if (int32_t rc = need(12, "custom HP")) return rc;
         const float hp[3] = {rd_f32(data + off), rd_f32(data + off + 4), rd_f32(data + off + 8)};
         for (float x : hp)
-            if (!std::isfinite(x)) return fail(err, err_cap, "invalid hyperparameter (NaN or Inf)");
+            if (!std::isfinite(x)) return fail(err, err_cap, "archive hyperparameter is not finite");
         r.bias_lr = hp[0];
         r.ngram_scale = hp[1];
         r.mix_eta = hp[2];
@@ -277,7 +286,8 @@ extern "C" int32_t redukt_rdkt_parse_header(const uint8_t* data, size_t len, red
     if (flags & kFlagBackbone) {
         if (int32_t rc = need(1, "backbone")) return rc;
         const uint8_t b = data[off++];
-        if (b > REDUKT_RDKT_BACKBONE_PLUGIN) return fail(err, err_cap, "RDKT v%u unknown backbone: %u", ver, b);
+        if (b > REDUKT_RDKT_BACKBONE_PLUGIN)
+            return fail(err, err_cap, "version-%u archive names backbone %u, which this reader does not know", ver, b);
         r.backbone = b;
     }
     r.enhanced_cm = (flags & kFlagEnhancedCm) != 0;

@@ -142,7 +142,7 @@ def test_parse_header_legacy():
 
 
 def test_parse_header_rejects_non_finite_hp():
-    with pytest.raises(A.ArchiveError, match="NaN or Inf"):
+    with pytest.raises(A.ArchiveError, match="not finite"):
         A.parse_header(make_v4_custom(100, float("nan"), 0.5, 0.01, b"", 0))
     f = bytearray(make_v3(100, 10, b"", 0))
     f[20:24] = f32(float("inf"))
@@ -187,17 +187,17 @@ def test_reset_period_roundtrips_through_header():
 def test_reset_log2_out_of_range_is_rejected(bad):
     h = bytearray(A.build_header(A.Header(total_bytes=10, backbone=A.BACKBONE_MAMBA, reset_log2=12, enhanced_cm=True)))
     h[14] = bad
-    with pytest.raises(A.ArchiveError, match="RESET_LOG2"):
+    with pytest.raises(A.ArchiveError, match="reset period exponent"):
         A.parse_header(with_payload(bytes(h)))
     if bad:  # 0 is "never" for the writer; the rest are refused there too
-        with pytest.raises(A.ArchiveError, match="RESET_LOG2"):
+        with pytest.raises(A.ArchiveError, match="reset period exponent"):
             A.build_header(A.Header(total_bytes=10, reset_log2=bad))
 
 
 def test_reset_flag_without_its_byte_is_truncated():
     h = bytearray(A.build_header(A.Header(total_bytes=10, backbone=A.BACKBONE_RWKV, reset_log2=0, enhanced_cm=True)))
     h[13] |= 0x40
-    with pytest.raises(A.ArchiveError, match="truncated"):
+    with pytest.raises(A.ArchiveError, match="ends inside"):
         A.parse_header(bytes(h))
 
 
@@ -219,11 +219,11 @@ def test_fma_contract_is_mamba_only():
     for quant, byte in ((0, 0x20), (1, 0x21)):
         h = A.build_header(all_fields(quant, contract=2))
         assert h[13] == byte and A.parse_header(with_payload(h)).contract == 2
-    with pytest.raises(A.ArchiveError, match="Mamba family"):
+    with pytest.raises(A.ArchiveError, match="only Mamba backbones"):
         A.build_header(A.Header(total_bytes=10, backbone=A.BACKBONE_RWKV, contract=2, reset_log2=0))
     h = bytearray(A.build_header(A.Header(total_bytes=10, backbone=A.BACKBONE_RWKV, reset_log2=0)))
     h[13] = 0x20
-    with pytest.raises(A.ArchiveError, match="Mamba family"):
+    with pytest.raises(A.ArchiveError, match="only Mamba backbones"):
         A.parse_header(with_payload(bytes(h)))
 
 
