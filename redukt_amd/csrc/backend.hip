@@ -930,6 +930,13 @@ uint32_t env_flow_from() {
     return (uint32_t)strtoul(e, nullptr, 10);
 }
 
+// REDUKT_GPU_SKEW: launches of part 0 ahead of the other parts of a split step.
+uint32_t env_skew() {
+    const char* e = getenv("REDUKT_GPU_SKEW");
+    if (!e || !*e) return kDefaultSkew;
+    return (uint32_t)strtoul(e, nullptr, 10);
+}
+
 // REDUKT_GPU_PART_MIN: fewest streams per part.
 uint32_t env_part_min() {
     const char* e = getenv("REDUKT_GPU_PART_MIN");
@@ -1016,6 +1023,7 @@ int init_common(const uint8_t* weights_path, int32_t device_id, uint32_t profile
     G.profile = profile;
     G.runner.set_split(env_split(), env_part_min());
     G.runner.set_flow(env_flow_from());
+    G.runner.set_skew(env_skew());
     G.kind = file_kind(path);
     if (G.kind == kKindRwkv && (profile & BACKEND_PROFILE_GEMV)) {
         log("the wavefront-GEMV tier serves Mamba models only");

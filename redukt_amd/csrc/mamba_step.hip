@@ -2420,6 +2420,7 @@ StepRunner& StepRunner::operator=(StepRunner&& o) noexcept {
     o.direct_.clear();
     clock_ = o.clock_;
     split_ = o.split_;
+    skew_ = o.skew_;
     min_part_ = o.min_part_;
     for (uint32_t k = 0; k < kMaxParts; k++) {
         aux_[k] = o.aux_[k];
@@ -2516,13 +2517,14 @@ hipError_t StepRunner::streams_ready(hipStream_t st, uint32_t parts) {
     return hipSuccess;
 }
 
-// Record one part as a graph by stream capture; the nodes whose arguments carry caller
-// pointers are looked up in capture order and checked against their kernels.
-hipError_t StepRunner::capture(const std::vector<Launch>& seq, hipStream_t st, Part& pt) {
+// Record launches [first, end) of one part as a graph by stream capture; the nodes whose
+// arguments carry caller pointers are looked up in capture order and checked against their
+// kernels (a launch before `first` is issued directly at every step).
+hipError_t StepRunner::capture(const std::vector<Launch>& seq, uint32_t first, hipStream_t st, Part& pt) {
     RDK_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
     hipError_t err = hipSuccess;
-    for (const Launch& l : seq) {
-        err = launch_direct(l, st);
+    for (size_t i = first; i < seq.size(); i++) {
+        err = launch_direct(seq[i], st);
         if (err != hipSuccess) break;
     }
     hipGraph_t graph = nullptr;
@@ -2537,13 +2539,13 @@ hipError_t StepRunner::capture(const std::vector<Launch>& seq, hipStream_t st, P
     RDK_TRY(hipGraphGetNodes(graph, nullptr, &count));
     std::vector<hipGraphNode_t> nodes(count);
     RDK_TRY(hipGraphGetNodes(graph, nodes.data(), &count));
-    pt.updatable = count == seq.size();
+    pt.updatable = count == seq.size() - first;
     auto pick = [&](int i, hipGraphNode_t& out) {
         out = nullptr;
-        if (i < 0 || !pt.updatable) return;
+        if (i < (int)first || !pt.updatable) return;
         hipKernelNodeParams kp{};
-        if (hipGraphKernelNodeGetParams(nodes[i], &kp) == hipSuccess && kp.func == seq[i].fn) {
-            out = nodes[i];
+        if (hipGraphKernelNodeGetParams(nodes[i - first], &kp) == hipSuccess && kp.func == seq[i].fn) {
+            out = nodes[i - first];
         } else {
             pt.updatable = false;
         }
@@ -2807,7 +2809,8 @@ hipError_t StepRunner::run(const StepSource& src, Pool& p, const StepIO& io, hip
             pt.n = cnt[k];
             std::unique_ptr<std::vector<Launch>> seq(new std::vector<Launch>());
             src.build(p, part_io(k), *seq, pt.io_i, pt.head_i, pt.sm_i);
-            const hipError_t e = capture(*seq, st, pt);
+            pt.lead = k == 0 && nparts > 1 ? std::min<uint32_t>(skew_, (uint32_t)seq->size()) : 0u;
+            const hipError_t e = capture(*seq, pt.lead, st, pt);
             if (e != hipSuccess) {
                 destroy(g);
                 return e;
@@ -2830,6 +2833,7 @@ hipError_t StepRunner::run(const StepSource& src, Pool& p, const StepIO& io, hip
             for (int j = 0; j < 3; j++) {
                 if (idx[j] < 0) continue;
                 keep[idx[j]] = std::move(seq[idx[j]]);
+                if (idx[j] < (int)pt.lead) continue;   // issued directly from keep at every step
                 void* prm[] = {keep[idx[j]].argp};
                 hipKernelNodeParams kp = node_params(keep[idx[j]], prm);
                 RDK_TRY(hipGraphExecKernelNodeSetParams(pt.exec, nodes[j], &kp));
@@ -2841,6 +2845,8 @@ hipError_t StepRunner::run(const StepSource& src, Pool& p, const StepIO& io, hip
     hit->out = io.out;
     hit->err = io.err;
     hit->last_use = ++clock_;
+    const Part& p0 = hit->parts[0];
+    for (uint32_t i = 0; i < p0.lead; i++) RDK_TRY(launch_direct((*p0.launches)[i], st));
     RDK_TRY(fork());
     for (uint32_t k = 0; k < hit->nparts; k++) RDK_TRY(hipGraphLaunch(hit->parts[k].exec, stream_of(k)));
     return join();

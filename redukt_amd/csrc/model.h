@@ -370,6 +370,7 @@ constexpr uint32_t kDefaultSplit = 2;
 // Smallest step that runs the persistent step kernel by default (REDUKT_GPU_FLOW
 // overrides; 0 = never).
 constexpr uint32_t kDefaultFlowFrom = 0;
+constexpr uint32_t kDefaultSkew = 1;
 
 class StepRunner {
 public:
@@ -401,6 +402,9 @@ public:
     // Steps of at least `from` streams (0: none) whose source has a persistent step kernel
     // run it (direct launches, one part) instead of the per-layer graphs.
     void set_flow(uint32_t from) { flow_from_ = from; }
+    // A split step issues the first `k` launches of part 0 before the other parts start, so
+    // the parts run that many kernels apart (0: all parts start together).
+    void set_skew(uint32_t k) { skew_ = k; }
     // Rows [b0, b0 + n) of each part of a step of n streams split at most k ways.
     static uint32_t parts_of(uint32_t n, uint32_t k, uint32_t* b0, uint32_t* cnt);
 
@@ -413,6 +417,7 @@ private:
         hipGraphNode_t io_node = nullptr, head_node = nullptr, softmax_node = nullptr;
         std::vector<Launch>* launches = nullptr;  // argument storage, alive as long as the graph
         int io_i = -1, head_i = -1, sm_i = -1;
+        uint32_t lead = 0;   // leading launches issued directly, ahead of the fork (the graph holds the rest)
     };
     struct Graph {
         uint32_t n = 0, split = 1;
@@ -437,7 +442,7 @@ private:
         void* dev = nullptr;
         uint64_t last_use = 0;
     };
-    hipError_t capture(const std::vector<Launch>& seq, hipStream_t st, Part& pt);
+    hipError_t capture(const std::vector<Launch>& seq, uint32_t first, hipStream_t st, Part& pt);
     hipError_t streams_ready(hipStream_t st, uint32_t parts);
     hipError_t flow_plan(const StepSource& src, Pool& p, uint32_t n, size_t bytes, hipStream_t st, FlowPlan*& out);
     void destroy(Graph& g);
@@ -446,6 +451,7 @@ private:
     uint32_t flow_from_ = 0;
     uint64_t clock_ = 0;
     uint32_t split_ = 1, min_part_ = kMinPartStreams;
+    uint32_t skew_ = 0;
     hipStream_t aux_[kMaxParts] = {};        // aux_[k] runs part k (k >= 1)
     hipEvent_t fork_ = nullptr;
     hipEvent_t join_[kMaxParts] = {};
