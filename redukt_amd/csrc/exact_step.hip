@@ -201,14 +201,14 @@ __device__ __forceinline__ void load4(const RowMat& m, size_t row_off, int c0, i
 // groups are whole 32-column blocks (checked at load).
 template <bool Q8, bool FMA, int S, int EPI>
 __global__ __launch_bounds__(kEBlock) void k_gemv_e(GemvEArgs a) {
-    extern __shared__ float acts[];   // [S][cols]
+    extern __shared__ __align__(16) float acts[];   // [S][cols], 32-column blocks interleaved like the rows
     const RowMat& m = a.w;
     const int cols = m.cols;
     const uint32_t b0 = blockIdx.y * S;
     for (int s = 0; s < S; s++) {
         const uint32_t b = min(b0 + (uint32_t)s, a.n - 1);
         const float* src = a.act + (size_t)b * cols;
-        for (int c = threadIdx.x; c < cols; c += kEBlock) acts[s * cols + c] = src[c];
+        for (int c = threadIdx.x; c < cols; c += kEBlock) acts[rowmat_index((size_t)s * cols, c)] = src[c];
     }
     __syncthreads();
     const int l = (int)threadIdx.x % 8;
@@ -231,9 +231,13 @@ __global__ __launch_bounds__(kEBlock) void k_gemv_e(GemvEArgs a) {
             float w[4];
             load4<Q8>(m, row_off, c, l, w);
 #pragma unroll
-            for (int j = 0; j < 4; j++)
-#pragma unroll
-                for (int s = 0; s < S; s++) acc[s] = madd<FMA>(w[j], acts[s * cols + c + 8 * j + l], acc[s]);
+            for (int s = 0; s < S; s++) {
+                const float4 x = *(const float4*)(acts + (size_t)s * cols + c + 4 * l);
+                acc[s] = madd<FMA>(w[0], x.x, acc[s]);
+                acc[s] = madd<FMA>(w[1], x.y, acc[s]);
+                acc[s] = madd<FMA>(w[2], x.z, acc[s]);
+                acc[s] = madd<FMA>(w[3], x.w, acc[s]);
+            }
         }
 #pragma unroll
         for (int s = 0; s < S; s++) {
@@ -292,10 +296,15 @@ const void* gemv_e_pick(uint32_t s, bool q8, bool fma) {
 }
 
 // Streams per workgroup: one for a single stream, four otherwise (their input rows in LDS:
-// 4 x d_inner floats at most 32 KB).  A stream's arithmetic does not depend on it.
+// 4 x d_inner floats at most 32 KB; sixteen, reading each row once per 16 streams, leave
+// too few workgroups: 32 streams 1.78 -> 2.38 ms per step).  A stream's arithmetic does not
+// depend on it.
 uint32_t exact_streams(uint32_t n) { return n == 1 ? 1u : 4u; }
 
-Launch gemv_e_launch(const void* fn, int cls, const RowMat& w, const float* act, uint32_t n, uint32_t S, GemvEArgs a) {
+Launch gemv_e_launch(const void* (*pick)(uint32_t, bool, bool), bool fma, int cls, const RowMat& w, const float* act,
+                     uint32_t n, GemvEArgs a) {
+    const uint32_t S = exact_streams(n);
+    const void* fn = pick(S, w.group != 0, fma);
     a.w = w;
     a.act = act;
     a.n = n;
@@ -311,7 +320,6 @@ void ExactStep::build(Pool& p, const StepIO& io, std::vector<Launch>& out, int& 
     const Dims& D = *m.dims;
     const uint32_t n = io.n;
     const int d = (int)D.d, di = (int)D.di;
-    const uint32_t S = exact_streams(n);
     const bool fma = m.fma;
     out.clear();
     io_i = (int)out.size();
@@ -333,16 +341,16 @@ void ExactStep::build(Pool& p, const StepIO& io, std::vector<Launch>& out, int& 
         gi.u = p.u;
         gi.z = p.z;
         gi.di = di;
-        out.push_back(gemv_e_launch(gemv_e_pick<kEpiIn>(S, L.e_in.group != 0, fma), KC_MIX_IN, L.e_in, p.normed, n, S, gi));
+        out.push_back(gemv_e_launch(gemv_e_pick<kEpiIn>, fma, KC_MIX_IN, L.e_in, p.normed, n, gi));
         GemvEArgs gx{};
         gx.out = p.xpart;
         gx.ostride = xr_pad;
-        out.push_back(gemv_e_launch(gemv_e_pick<kEpiPlain>(S, L.e_xp.group != 0, fma), KC_XPROJ, L.e_xp, p.u, n, S, gx));
+        out.push_back(gemv_e_launch(gemv_e_pick<kEpiPlain>, fma, KC_XPROJ, L.e_xp, p.u, n, gx));
         out.push_back(scan_exact_launch(L, D, p, n, fma, p.g32, p.ssm + li * ssm_layer));
         GemvEArgs go{};
         go.out = p.x;
         go.ostride = (uint32_t)d;
-        out.push_back(gemv_e_launch(gemv_e_pick<kEpiRes>(S, L.e_out.group != 0, fma), KC_MIX_OUT, L.e_out, p.g32, n, S, go));
+        out.push_back(gemv_e_launch(gemv_e_pick<kEpiRes>, fma, KC_MIX_OUT, L.e_out, p.g32, n, go));
     }
     out.push_back(Launch::make((const void*)k_norm_e, dim3(n), dim3(kEBlock), 0, KC_NORM,
                                NormEArgs{p.x, m.norm_f_w, m.norm_f_b, p.normed, d}));
@@ -350,7 +358,7 @@ void ExactStep::build(Pool& p, const StepIO& io, std::vector<Launch>& out, int& 
     GemvEArgs gh{};
     gh.out = io.out;
     gh.ostride = D.vocab;
-    out.push_back(gemv_e_launch(gemv_e_pick<kEpiPlain>(S, m.head->group != 0, fma), KC_HEAD, *m.head, p.normed, n, S, gh));
+    out.push_back(gemv_e_launch(gemv_e_pick<kEpiPlain>, fma, KC_HEAD, *m.head, p.normed, n, gh));
     sm_i = -1;
     if (io.probs) {
         sm_i = (int)out.size();

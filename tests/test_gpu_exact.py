@@ -18,7 +18,7 @@ import numpy as np
 import pytest
 
 from oracle import oracle as O
-from redukt_amd import ffi, hip, rbin, synth
+from redukt_amd import archive, ffi, hip, rbin, synth
 from redukt_amd.lockstep import Lockstep
 
 pytestmark = pytest.mark.gpu
@@ -150,6 +150,32 @@ def test_archive_coded_on_cpu_decodes_on_gpu(small, oracle_plugin, profile, cont
         back, _ = cpu.decompress(gpu_bytes, [len(f) for f in files], reset_every=64)
     for f, b in zip(files, back):
         assert np.array_equal(f, b)
+
+
+@pytest.mark.parametrize("quant,contract", [(1, 2), (0, 1)])
+def test_rdkt_archive_written_on_gpu_decodes_on_cpu(small, oracle_plugin, quant, contract):
+    """GPU-coded streams in RDKT v5 archives with the header of the CPU Mamba backbone
+    (BACKBONE 1, PROFILE = weight profile code + numeric contract, RESET_LOG2 8): the CPU side
+    takes its weight profile, contract and reset period from the header alone, decodes the
+    stream and checks the CRC-32 of the restored data (src/application/codec.rs:540-580,
+    648-720).  The files cross reset boundaries."""
+    path, dims = small["base"], SMALL["base"]
+    rng = np.random.default_rng(40 + quant)
+    files = [synth.zipf_tokens(rng, dims.vocab, (k,)).astype(np.uint32) for k in (300, 1, 90, 520)]
+    with Lockstep(path, profile=quant | EXACT | (FMA if contract == 2 else 0), slots=3, device_cdf=False) as gpu:
+        streams, _ = gpu.compress(files, reset_every=256)
+    for f, stm in zip(files, streams):
+        payload = f.astype("<u4").tobytes()
+        h = archive.default_header(len(payload), backbone=archive.BACKBONE_MAMBA, quant=quant, reset_log2=8)
+        h.contract = contract
+        arc = archive.pack(h, stm, payload)
+        hd, body, crc = archive.unpack(arc)
+        assert (hd.backbone, hd.quant, hd.contract, hd.reset_every) == (archive.BACKBONE_MAMBA, quant, contract, 256)
+        cpu_profile = hd.quant | (O.ORC_PROFILE_FMA if hd.contract == 2 else 0)
+        with Lockstep(path, plugin_path=oracle_plugin, profile=cpu_profile, slots=1) as cpu:
+            back, _ = cpu.decompress([body], [hd.total_bytes // 4], reset_every=hd.reset_every)
+        assert archive.crc32(back[0].astype("<u4").tobytes()) == crc
+        assert np.array_equal(back[0], f)
 
 
 def test_exact_tier_refuses_what_it_does_not_serve(small):
