@@ -26,6 +26,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "mfma_common.h"
 #include "model.h"
@@ -199,7 +200,10 @@ __device__ __forceinline__ void load4(const RowMat& m, size_t row_off, int c0, i
 // holds rows [32 bx, 32 bx + 32) and streams [S by, S by + S), the streams' input rows
 // staged in LDS.  Every operation in the contract's arithmetic (madd).  Column counts and
 // groups are whole 32-column blocks (checked at load).
-template <bool Q8, bool FMA, int S, int EPI>
+// NB > 0: the rows have exactly NB 32-column blocks, and each lane requests its whole
+// slice of the row (NB 4-byte int8 or 16-byte F32 runs) before the first product: a
+// matrix with few rows has few lanes, so each lane keeps many loads in flight.
+template <bool Q8, bool FMA, int S, int EPI, int NB>
 __global__ __launch_bounds__(kEBlock) void k_gemv_e(GemvEArgs a) {
     extern __shared__ __align__(16) float acts[];   // [S][cols], 32-column blocks interleaved like the rows
     const RowMat& m = a.w;
@@ -221,6 +225,54 @@ __global__ __launch_bounds__(kEBlock) void k_gemv_e(GemvEArgs a) {
     float res[S];
 #pragma unroll
     for (int s = 0; s < S; s++) res[s] = 0.0f;
+    // The eight lanes' horizontal sum of each stream's accumulator, then the group's fold.
+    auto finish_group = [&](float (&acc)[S], int g) {
+#pragma unroll
+        for (int s = 0; s < S; s++) {
+            float v = acc[s];
+            v = v + __shfl_xor(v, 4, 8);
+            v = v + __shfl_xor(v, 2, 8);
+            v = v + __shfl_xor(v, 1, 8);
+            res[s] = Q8 ? madd<FMA>(v, m.scales[(size_t)r * ng + g], res[s]) : v;
+            acc[s] = 0.0f;
+        }
+    };
+    if constexpr (NB > 0) {
+        typedef typename std::conditional<Q8, uint32_t, float4>::type Raw;
+        Raw raw[NB];
+#pragma unroll
+        for (int i = 0; i < NB; i++) {
+            const size_t at = row_off + 32 * (size_t)i + 4 * l;
+            if constexpr (Q8)
+                raw[i] = *(const uint32_t*)((const int8_t*)m.w + at);
+            else
+                raw[i] = *(const float4*)((const float*)m.w + at);
+        }
+        const int bpg = group / 32;
+        float acc[S];
+#pragma unroll
+        for (int s = 0; s < S; s++) acc[s] = 0.0f;
+        int g = 0;
+#pragma unroll
+        for (int i = 0; i < NB; i++) {
+            float w[4];
+            if constexpr (Q8) {
+#pragma unroll
+                for (int j = 0; j < 4; j++) w[j] = (float)(int8_t)(raw[i] >> (8 * j));
+            } else {
+                w[0] = raw[i].x, w[1] = raw[i].y, w[2] = raw[i].z, w[3] = raw[i].w;
+            }
+#pragma unroll
+            for (int s = 0; s < S; s++) {
+                const float4 x = *(const float4*)(acts + (size_t)s * cols + 32 * i + 4 * l);
+                acc[s] = madd<FMA>(w[0], x.x, acc[s]);
+                acc[s] = madd<FMA>(w[1], x.y, acc[s]);
+                acc[s] = madd<FMA>(w[2], x.z, acc[s]);
+                acc[s] = madd<FMA>(w[3], x.w, acc[s]);
+            }
+            if ((i + 1) % bpg == 0) finish_group(acc, g++);
+        }
+    } else
     for (int g = 0; g < ng; g++) {
         const int c0 = g * group;
         float acc[S];
@@ -239,14 +291,7 @@ __global__ __launch_bounds__(kEBlock) void k_gemv_e(GemvEArgs a) {
                 acc[s] = madd<FMA>(w[3], x.w, acc[s]);
             }
         }
-#pragma unroll
-        for (int s = 0; s < S; s++) {
-            float v = acc[s];
-            v = v + __shfl_xor(v, 4, 8);
-            v = v + __shfl_xor(v, 2, 8);
-            v = v + __shfl_xor(v, 1, 8);
-            res[s] = Q8 ? madd<FMA>(v, m.scales[(size_t)r * ng + g], res[s]) : v;
-        }
+        finish_group(acc, g);
     }
     if (!live || l != 0) return;
 #pragma unroll
@@ -284,15 +329,26 @@ __global__ __launch_bounds__(kEBlock) void k_gemv_e(GemvEArgs a) {
     }
 }
 
-template <int S, int EPI>
+template <int S, int EPI, int NB>
 const void* gemv_e_fn(bool q8, bool fma) {
-    if (q8) return fma ? (const void*)k_gemv_e<true, true, S, EPI> : (const void*)k_gemv_e<true, false, S, EPI>;
-    return fma ? (const void*)k_gemv_e<false, true, S, EPI> : (const void*)k_gemv_e<false, false, S, EPI>;
+    if (q8) return fma ? (const void*)k_gemv_e<true, true, S, EPI, NB> : (const void*)k_gemv_e<true, false, S, EPI, NB>;
+    return fma ? (const void*)k_gemv_e<false, true, S, EPI, NB> : (const void*)k_gemv_e<false, false, S, EPI, NB>;
+}
+
+// The row slice in flight whole for Mamba-130M's widths (768 and 1536 columns), the
+// generic loop for the others and for F32 batches (a whole F32 slice of 1536 columns
+// takes 200 registers: two waves per SIMD, slower from a few streams on).
+template <int S, int EPI>
+const void* gemv_e_nb(int cols, bool q8, bool fma) {
+    if (!q8 && S > 1) return gemv_e_fn<S, EPI, 0>(q8, fma);
+    if (cols == 768) return gemv_e_fn<S, EPI, 24>(q8, fma);
+    if (cols == 1536) return gemv_e_fn<S, EPI, 48>(q8, fma);
+    return gemv_e_fn<S, EPI, 0>(q8, fma);
 }
 
 template <int EPI>
-const void* gemv_e_pick(uint32_t s, bool q8, bool fma) {
-    return s == 1 ? gemv_e_fn<1, EPI>(q8, fma) : gemv_e_fn<4, EPI>(q8, fma);
+const void* gemv_e_pick(uint32_t s, int cols, bool q8, bool fma) {
+    return s == 1 ? gemv_e_nb<1, EPI>(cols, q8, fma) : gemv_e_nb<4, EPI>(cols, q8, fma);
 }
 
 // Streams per workgroup: one for a single stream, four otherwise (their input rows in LDS:
@@ -301,10 +357,10 @@ const void* gemv_e_pick(uint32_t s, bool q8, bool fma) {
 // depend on it.
 uint32_t exact_streams(uint32_t n) { return n == 1 ? 1u : 4u; }
 
-Launch gemv_e_launch(const void* (*pick)(uint32_t, bool, bool), bool fma, int cls, const RowMat& w, const float* act,
-                     uint32_t n, GemvEArgs a) {
+Launch gemv_e_launch(const void* (*pick)(uint32_t, int, bool, bool), bool fma, int cls, const RowMat& w,
+                     const float* act, uint32_t n, GemvEArgs a) {
     const uint32_t S = exact_streams(n);
-    const void* fn = pick(S, w.group != 0, fma);
+    const void* fn = pick(S, w.cols, w.group != 0, fma);
     a.w = w;
     a.act = act;
     a.n = n;
