@@ -127,8 +127,12 @@ int32_t redukt_backend_forward_batch(uint32_t n_streams, const uint32_t* slots, 
  * their column groups; the norms are the reference's sequential sums
  * (src/domain/tensor.rs:900-908, 1390-1398) and the scan takes the portable exp, so the
  * logits and the recurrent state equal the CPU path's (numeric contract 1, the "Plain"
- * kernel family) bit for bit, for F32, group-64 and per-row int8 weights alike.  Slower
- * than the other tiers: its GEMVs run one output per thread on the vector ALUs. */
+ * kernel family) bit for bit, for F32, group-64 and per-row int8 weights alike.  On an
+ * RWKV-7 model bit 6 alone (F32 weights) runs its step the same way: every projection in
+ * mat_vec_mul_into's dot_avx2_order (src/domain/tensor.rs:1602-1693), the element-wise code
+ * and the sums of the W8A8 tier; RWKV-7 with another low bit or bit 7 -> INIT_FAILED (its
+ * int8 arithmetic is bit 5's).  Slower than the other tiers: its GEMVs are f32 dot products
+ * on the vector ALUs, eight lanes per output. */
 #define BACKEND_PROFILE_EXACT 64u
 /* Profile bit 7: the reference-order tier in numeric contract 2 (fma-v1,
  * src/domain/gemv_fma.rs:1-134): the same orders with every acc + w * x of a projection,

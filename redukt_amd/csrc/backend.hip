@@ -51,6 +51,7 @@ struct Model {
     RDims rdims;                // RWKV-7
     std::vector<RLayer> rlayers;
     TMat r_emb, r_head;
+    RowMat r_e_head;            // the RWKV-7 reference-order tier's head
     float* ln_out_w = nullptr;
     float* ln_out_b = nullptr;
     uint32_t profile = 0;
@@ -62,6 +63,7 @@ struct Model {
     bool exact = false;       // weight profile bit 6 or 7: the reference-order tier
     bool exact_fma = false;   // bit 7: its numeric contract 2 (fma-v1)
     bool r_a8 = false;        // weight profile bit 5: the RWKV-7 W8A8 tier
+    bool r_exact = false;     // bit 6 on an RWKV-7 model: its F32 reference-order tier
     bool tied = true;
     float* norm_f_w = nullptr;
     float* norm_f_b = nullptr;
@@ -481,8 +483,15 @@ int load_rwkv(const std::string& path, uint32_t profile) {
     G.dims.nl = R.nl;
     G.dims.tokenizer = h[14];
     G.r_a8 = (profile & BACKEND_PROFILE_W8A8) != 0;
-    if (G.r_a8 && (R.lora[0] % 8 || R.lora[1] % 8 || R.lora[2] % 8 || R.lora[3] % 8)) {
-        log("the W8A8 tier needs LoRA ranks in multiples of 8");
+    G.r_exact = (profile & BACKEND_PROFILE_EXACT) != 0;
+    if ((G.r_a8 || G.r_exact) && (R.lora[0] % 8 || R.lora[1] % 8 || R.lora[2] % 8 || R.lora[3] % 8)) {
+        log("the W8A8 and reference-order tiers need LoRA ranks in multiples of 8");
+        fclose(f);
+        return -2;
+    }
+    // the reference-order projections stage four streams' input rows in LDS (64 KB at most)
+    if (G.r_exact && (R.f % 32 != 0 || R.f > 4096)) {
+        log("the reference-order tier needs d_ffn in whole 32-column blocks, at most 4096");
         fclose(f);
         return -2;
     }
@@ -500,11 +509,21 @@ int load_rwkv(const std::string& path, uint32_t profile) {
         std::vector<float> t = rd.read(rows * cols);
         ok = ok && rd.ok && make_tmat(m, t.data(), (int)rows, (int)cols, group);
     };
+    // A projection: tiled for the matrix cores, or F32 rows for the reference-order tier.
+    auto proj = [&](TMat& m, RowMat& e, size_t rows, size_t cols) {
+        if (!G.r_exact) {
+            mat(m, rows, cols, qgroup((int)cols));
+            return;
+        }
+        std::vector<float> t = rd.read(rows * cols);
+        ok = ok && rd.ok && make_rowmat(e, t.data(), (int)rows, (int)cols, 0);
+    };
     // A LoRA stage: tiled for the matrix cores, or laid out for the exact kernels of the
-    // W8A8 tier.
+    // W8A8 and reference-order tiers.
     auto lora = [&](RLayer& L, int k, bool first, size_t rows, size_t cols) {
         std::vector<float> t = rd.read(rows * cols);
-        if (G.r_a8) ok = ok && rd.ok && make_lmat(first ? L.x1[k] : L.x2[k], t.data(), (int)rows, (int)cols);
+        if (G.r_a8 || G.r_exact)
+            ok = ok && rd.ok && make_lmat(first ? L.x1[k] : L.x2[k], t.data(), (int)rows, (int)cols);
         else ok = ok && rd.ok && make_tmat(first ? L.l1[k] : L.l2[k], t.data(), (int)rows, (int)cols, 0);
     };
     mat(G.r_emb, V, d, 0);
@@ -525,18 +544,18 @@ int load_rwkv(const std::string& path, uint32_t profile) {
         lora(L, kLoraG, true, R.lora[kLoraG], d);
         lora(L, kLoraG, false, d, R.lora[kLoraG]);
         vec(L.k_k); vec(L.k_a); vec(L.r_k);
-        mat(L.r, d, d, qgroup((int)d));
-        mat(L.k, d, d, qgroup((int)d));
-        mat(L.v, d, d, qgroup((int)d));
-        mat(L.o, d, d, qgroup((int)d));
+        proj(L.r, L.e_r, d, d);
+        proj(L.k, L.e_k, d, d);
+        proj(L.v, L.e_v, d, d);
+        proj(L.o, L.e_o, d, d);
         vec(L.ln_x_w); vec(L.ln_x_b); vec(L.ffn_x_k);
-        mat(L.fk, ff, d, qgroup((int)d));
-        mat(L.fv, d, ff, qgroup((int)ff));
+        proj(L.fk, L.e_fk, ff, d);
+        proj(L.fv, L.e_fv, d, ff);
         if (ok && ((i + 1) % 4 == 0 || i + 1 == R.nl)) log("loaded layer %u/%u", i + 1, R.nl);
     }
     vec(G.ln_out_w);
     vec(G.ln_out_b);
-    mat(G.r_head, V, d, qgroup((int)d));
+    proj(G.r_head, G.r_e_head, V, d);
     if (ok) {
         char extra;
         ok = fread(&extra, 1, 1, f) == 0;
@@ -701,7 +720,7 @@ size_t slot_words(uint32_t cap) { return ((size_t)cap + kSlotWordAlign - 1) / kS
 bool pool_alloc_rwkv(Pool& p, uint32_t cap) {
     const RDims& R = G.rdims;
     const size_t n = cap, d = R.d;
-    const RwkvSizes z = rwkv_sizes(R, cap, G.r_a8);
+    const RwkvSizes z = rwkv_sizes(R, cap, G.r_a8 || G.r_exact, G.r_exact);
     p = Pool{};
     p.cap = cap;
     p.scap = cap + 1;
@@ -802,7 +821,8 @@ hipError_t run_step(Pool& p, uint32_t n, const uint32_t* slots, const uint32_t* 
                     bool check) {
     StepIO io{n, slots, tokens, out, probs, check, G.d_err};
     if (G.kind == kKindRwkv) {
-        const RwkvStep src(RwkvView{&G.rdims, G.rlayers.data(), &G.r_emb, &G.r_head, G.ln_out_w, G.ln_out_b, G.r_a8});
+        const RwkvStep src(RwkvView{&G.rdims, G.rlayers.data(), &G.r_emb, &G.r_head, G.ln_out_w, G.ln_out_b, G.r_a8,
+                                    G.r_exact, &G.r_e_head});
         return G.runner.run(src, p, io, G.stream, &G.probe);
     }
     if (G.gemv) {
@@ -1030,9 +1050,17 @@ int init_common(const uint8_t* weights_path, int32_t device_id, uint32_t profile
         free_model();
         return BACKEND_INIT_FAILED;
     }
-    if ((profile & (BACKEND_PROFILE_EXACT | BACKEND_PROFILE_FMA)) &&
-        (G.kind != kKindMamba || (profile & (BACKEND_PROFILE_GEMV | BACKEND_PROFILE_W8A8)))) {
-        log("the reference-order tier serves Mamba models only, apart from the GEMV and W8A8 tiers");
+    if ((profile & (BACKEND_PROFILE_EXACT | BACKEND_PROFILE_FMA)) && G.kind == kKindMamba &&
+        (profile & (BACKEND_PROFILE_GEMV | BACKEND_PROFILE_W8A8))) {
+        log("the reference-order tier is a tier of its own, apart from the GEMV and W8A8 tiers");
+        free_model();
+        return BACKEND_INIT_FAILED;
+    }
+    // RWKV-7 in the reference's arithmetic: F32 in numeric contract 1 here (the reference's
+    // RWKV-7 GEMVs have no fma-v1 twin), int8 as the W8A8 tier
+    if ((profile & (BACKEND_PROFILE_EXACT | BACKEND_PROFILE_FMA)) && G.kind == kKindRwkv &&
+        ((profile & (BACKEND_PROFILE_FMA | BACKEND_PROFILE_W8A8)) || (profile & 3) != 0)) {
+        log("RWKV-7's reference-order tier is F32 in numeric contract 1 (profile 64); its int8 one is the W8A8 tier");
         free_model();
         return BACKEND_INIT_FAILED;
     }
@@ -1066,8 +1094,9 @@ int init_common(const uint8_t* weights_path, int32_t device_id, uint32_t profile
     static const char* exact_names[2][3] = {
         {"hip-gfx950-mamba-f32-ref", "hip-gfx950-mamba-q8-ref", "hip-gfx950-mamba-q8row-ref"},
         {"hip-gfx950-mamba-f32-ref-fma", "hip-gfx950-mamba-q8-ref-fma", "hip-gfx950-mamba-q8row-ref-fma"}};
-    const char* name = G.r_a8    ? "hip-gfx950-rwkv7-w8a8"
-                       : G.exact ? exact_names[G.exact_fma ? 1 : 0][profile & 3]
+    const char* name = G.r_a8      ? "hip-gfx950-rwkv7-w8a8"
+                       : G.r_exact ? "hip-gfx950-rwkv7-f32-ref"
+                       : G.exact   ? exact_names[G.exact_fma ? 1 : 0][profile & 3]
                                  : names[G.kind == kKindRwkv ? 1 : 0][profile & 3];
     memcpy(info_out->name, name, strlen(name));
     size_t fr = 0, tot = 0;

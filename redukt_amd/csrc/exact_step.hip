@@ -22,7 +22,8 @@
 //   k_scan    : shared with the other tiers (dt_proj in the contract's order);
 //   k_gemv_e  : out_proj and the residual add;
 // and per step k_embed_e (row gather or Q8 dequantisation, device argument check), the
-// final norm, the head, and optionally the shared softmax.
+// final norm, the head, and optionally the shared softmax.  exact_gemv_launch hands the same
+// F32 projection to the RWKV-7 step of this tier (rwkv_a8.hip).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -152,13 +153,13 @@ __global__ __launch_bounds__(kEBlock) void k_norm_e(NormEArgs a) {
 
 // ---------------------------------------------------------------- projections
 
-enum : int { kEpiPlain = 0, kEpiIn = 1, kEpiRes = 2 };
+enum : int { kEpiPlain = EXACT_STORE, kEpiIn = 1, kEpiRes = EXACT_RESID, kEpiRelu2 = EXACT_RELU2 };
 
 struct GemvEArgs {
     RowMat w;               // [rows][cols]
     const float* act;       // [n][cols] input rows
     uint32_t n;
-    float* out;             // kEpiPlain: out[b * ostride + r]; kEpiRes: the residual x [n][rows]
+    float* out;             // kEpiPlain, kEpiRelu2: out[b * ostride + r]; kEpiRes: the residual x [n][rows]
     uint32_t ostride;
     // kEpiIn: rows below di are the conv branch (conv1d + SiLU into u, the conv state
     // updated), the rest the gate branch (z).
@@ -305,6 +306,10 @@ __global__ __launch_bounds__(kEBlock) void k_gemv_e(GemvEArgs a) {
             // x += W_out * gated (model.rs:714-719): the residual add after the projection
             float* xp = a.out + (size_t)b * a.ostride + r;
             *xp = *xp + y;
+        } else if (EPI == kEpiRelu2) {
+            // squared_relu_into (tensor.rs:1386-1388): max(y, 0)^2, a NaN to 0
+            const float t = y > 0.0f ? y : 0.0f;
+            a.out[(size_t)b * a.ostride + r] = t * t;
         } else if (r >= a.di) {
             a.z[(size_t)b * a.di + (r - a.di)] = y;
         } else {
@@ -371,6 +376,17 @@ Launch gemv_e_launch(const void* (*pick)(uint32_t, int, bool, bool), bool fma, i
 }
 
 }  // namespace
+
+Launch exact_gemv_launch(const RowMat& w, const float* act, uint32_t n, float* out, uint32_t ostride, int epi,
+                         uint32_t cls) {
+    GemvEArgs a{};
+    a.out = out;
+    a.ostride = ostride;
+    const void* (*pick)(uint32_t, int, bool, bool) = epi == EXACT_RESID   ? gemv_e_pick<kEpiRes>
+                                                      : epi == EXACT_RELU2 ? gemv_e_pick<kEpiRelu2>
+                                                                           : gemv_e_pick<kEpiPlain>;
+    return gemv_e_launch(pick, false, (int)cls, w, act, n, a);
+}
 
 void ExactStep::build(Pool& p, const StepIO& io, std::vector<Launch>& out, int& io_i, int& head_i, int& sm_i) const {
     const Dims& D = *m.dims;

@@ -145,7 +145,7 @@ struct Pool {
     __bf16* actl = nullptr;      // [gcap][ks_ffn][3][64][8] squared-ReLU activations
     __bf16* headl = nullptr;     // [gcap][ks_d][3][64][8] final LayerNorm output
     // RWKV-7 W8A8 tier (instead of the limb buffers above)
-    float* mixf = nullptr;       // [4][cap][d] LoRA inputs x_w, x_a, x_g, x_v (f32)
+    float* mixf = nullptr;       // [4][cap][d] LoRA inputs x_w, x_a, x_g, x_v (f32); reference-order tier: [6][cap][d], then x_r, x_k
     float* lorah = nullptr;      // [cap][sum of ranks] first LoRA stages after their activation
     int8_t* aq = nullptr;        // int8 activations, kAqAct x [rows16][dp], then [rows16][fp]
     float* as = nullptr;         // their scales, kAqVecs x [cap]
@@ -213,7 +213,8 @@ struct RLayer {
     TMat l1[4];                       // first LoRA stages [rank][d] (F32): w1, a1, g1, v1
     TMat l2[4];                       // second LoRA stages [d][rank] (F32): w2, a2, g2, v2
     TMat fk, fv;                      // [d_ffn][d], [d][d_ffn]
-    LMat x1[4], x2[4];                // the LoRA stages of the W8A8 tier (l1/l2 stay empty there)
+    LMat x1[4], x2[4];                // the LoRA stages of the W8A8 and reference-order tiers (l1/l2 stay empty there)
+    RowMat e_r, e_k, e_v, e_o, e_fk, e_fv;   // the reference-order tier's projections (the TMats stay empty there)
 };
 
 struct RwkvView {
@@ -224,10 +225,13 @@ struct RwkvView {
     const float* ln_out_w;
     const float* ln_out_b;
     bool a8;               // the W8A8 tier: int8 activations, element-wise exact
+    bool exact;            // the reference-order tier: F32 projections in the reference GEMV's order
+    const RowMat* e_head;  // its head [vocab][d]
 };
 
 // Scratch and state sizes of an RWKV-7 pool of `cap` streams (elements).  The limb
-// buffers serve the matrix-core tiers, the a8 ones the W8A8 tier (the other set is empty).
+// buffers serve the matrix-core tiers, the a8 ones the W8A8 and reference-order tiers (the
+// other set is empty); the reference-order tier keeps six f32 token-shift outputs in mixf.
 struct RwkvSizes {
     size_t state_d, wkv, mixl, loral, lora_off[4], gatedl, actl;
     int ks_d, ks_f, ks_lora[4];
@@ -238,7 +242,7 @@ struct RwkvSizes {
 // int8 activation vectors of the W8A8 tier in Pool::aq, [rows16][dp] each (kAqAct, the last:
 // [rows16][fp]), with one scale per stream in Pool::as.
 enum { kAqR = 0, kAqK = 1, kAqV = 2, kAqFfn = 3, kAqHead = 4, kAqAct = 5, kAqVecs = 6 };
-RwkvSizes rwkv_sizes(const RDims& d, uint32_t cap, bool a8);
+RwkvSizes rwkv_sizes(const RDims& d, uint32_t cap, bool a8, bool exact = false);
 
 struct ModelView {
     const Dims* dims;
@@ -349,12 +353,21 @@ struct ExactStep final : StepSource {
     void build(Pool& p, const StepIO& io, std::vector<Launch>& out, int& io_i, int& head_i, int& sm_i) const override;
 };
 
+// One F32 projection of the reference-order tier in numeric contract 1 (exact_step.hip),
+// for the RWKV-7 step: row r of stream b is the reference's dot_avx2_order of W's row r and
+// the stream's input row act + b * w.cols, then stored at out[b * ostride + r] (EXACT_STORE),
+// added to it (EXACT_RESID), or stored through the squared ReLU (EXACT_RELU2).
+enum ExactEpi : int { EXACT_STORE = 0, EXACT_RESID = 2, EXACT_RELU2 = 3 };
+Launch exact_gemv_launch(const RowMat& w, const float* act, uint32_t n, float* out, uint32_t ostride, int epi,
+                         uint32_t cls);
+
 struct RwkvStep final : StepSource {
     RwkvView m;
     explicit RwkvStep(const RwkvView& v) : m(v) {}
     void build(Pool& p, const StepIO& io, std::vector<Launch>& out, int& io_i, int& head_i, int& sm_i) const override;
-    // The W8A8 tier's step (rwkv_a8.hip).
+    // The W8A8 tier's step and the reference-order tier's (rwkv_a8.hip).
     void build_a8(Pool& p, const StepIO& io, std::vector<Launch>& out, int& io_i, int& head_i, int& sm_i) const;
+    void build_ref(Pool& p, const StepIO& io, std::vector<Launch>& out, int& io_i, int& head_i, int& sm_i) const;
 };
 
 // Most parts a step is split into: one per hardware queue a process gets by default.

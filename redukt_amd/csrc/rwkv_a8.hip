@@ -29,6 +29,13 @@
 // loads.  The FFN activations (d_ffn long, from many workgroups) are rounded once by a pass
 // of their own, since the FFN value product would round them again in every row tile.
 //
+// The reference-order tier (F32 weights, profile bit 6) runs the same element-wise kernels
+// with every projection an F32 GEMV in the reference's dot_avx2_order (mat_vec_mul_into,
+// tensor.rs:1602-1693; exact_gemv_launch, eight lanes per output): k_shift_a8 hands all six
+// token-shift inputs over as f32, and the receptance, key, value, output, FFN and head
+// products replace the int8 ones (the FFN key's squared ReLU in its epilogue), so the
+// logits are the CPU path's F32 logits bit for bit.
+//
 // Integer products are exact, so the k-order of the int8 matrix products is free: the
 // weight tiles of the int8 matrix-core tiers serve unchanged (the 16 bytes a lane holds for
 // k-pair p are row r's columns 64p + 8g + [0, 8) and 64p + 32 + 8g + [0, 8), g = lane / 16)
@@ -897,6 +904,77 @@ void RwkvStep::build_a8(Pool& p, const StepIO& io, std::vector<Launch>& out, int
     const int per_block = kWaves * kHeadTiles;
     out.push_back(Launch::make(head_a8_fn(H.ks / 2), dim3((H.rt + per_block - 1) / per_block), dim3(kBlock), 0,
                                KC_HEAD, ha));
+    sm_i = -1;
+    if (io.probs) {
+        sm_i = (int)out.size();
+        out.push_back(softmax_launch(io.out, (int)D.vocab, n));
+    }
+}
+
+void RwkvStep::build_ref(Pool& p, const StepIO& io, std::vector<Launch>& out, int& io_i, int& head_i,
+                         int& sm_i) const {
+    const RDims& D = *m.dims;
+    const uint32_t n = io.n;
+    const int d = (int)D.d, f = (int)D.f;
+    const RwkvSizes z = rwkv_sizes(D, p.cap, true, true);
+    // mixf: x_w, x_a, x_g, x_v (the LoRA inputs, x_v also the value input), then x_r, x_k;
+    // the channel mix's input and ln_out reuse x_r's buffer once the receptance has read it
+    float* mixf[6];
+    for (int k = 0; k < 6; k++) mixf[k] = p.mixf + (size_t)k * p.cap * d;
+    float* const xr = mixf[4];
+    float* const xk = mixf[5];
+    float* lh[4];
+    for (int k = 0; k < 4; k++) lh[k] = p.lorah + z.lh_off[k];
+    const int lsum = (int)z.lora_sum;
+    const size_t state_stride = (size_t)D.nl * D.d;
+    const size_t wkv_layer = (size_t)D.h * D.n * D.n;
+    out.clear();
+    io_i = (int)out.size();
+    out.push_back(embed_launch(*m.emb, p, io, nullptr, nullptr, nullptr, 0, 0));
+    for (uint32_t l = 0; l < D.nl; l++) {
+        const RLayer& L = m.layers[l];
+        ShiftA8Args s1{p.x, L.ln1_w, L.ln1_b, p.x_att + (size_t)l * d, state_stride, p.slots, p.scap, {}, {}, {}, {},
+                       d, d};
+        for (int k = 0; k < kMix; k++) s1.mix[k] = L.mix[k];
+        s1.outf[0] = xr;
+        s1.outf[1] = mixf[kLoraW];
+        s1.outf[2] = xk;
+        s1.outf[3] = mixf[kLoraV];
+        s1.outf[4] = mixf[kLoraA];
+        s1.outf[5] = mixf[kLoraG];
+        out.push_back(Launch::make(shift_a8_fn(6), dim3(n), dim3(kBlock), 0, KC_SHIFT, s1));
+        out.push_back(exact_gemv_launch(L.e_r, xr, n, p.rkv, 3u * d, EXACT_STORE, KC_PROJ));
+        out.push_back(exact_gemv_launch(L.e_k, xk, n, p.rkv + d, 3u * d, EXACT_STORE, KC_PROJ));
+        out.push_back(exact_gemv_launch(L.e_v, mixf[kLoraV], n, p.rkv + 2 * d, 3u * d, EXACT_STORE, KC_PROJ));
+        ProjA8Builder p1(n, 0);
+        p1.lora(L.x1[kLoraW], mixf[kLoraW], d, ACT_TANH, lh[kLoraW], lsum);
+        p1.lora(L.x1[kLoraA], mixf[kLoraA], d, ACT_NONE, lh[kLoraA], lsum);
+        p1.lora(L.x1[kLoraG], mixf[kLoraG], d, ACT_SIGMOID, lh[kLoraG], lsum);
+        if (l != 0) p1.lora(L.x1[kLoraV], mixf[kLoraV], d, ACT_NONE, lh[kLoraV], lsum);
+        out.push_back(p1.launch());
+        ProjA8Builder p2(n, 0);
+        for (int k = 0; k < 4; k++)
+            if (k != kLoraV || l != 0) p2.lora(L.x2[k], lh[k], lsum, ACT_NONE, p.lorad + k * d, 4 * d);
+        out.push_back(p2.launch());
+        // the gated vector in f32 rows of d (its per-head maxima are not used here)
+        WkvA8Args wa{p.rkv, p.lorad, L.w0, L.a0, L.v0, L.k_k, L.k_a, L.r_k, L.ln_x_w, L.ln_x_b,
+                     p.wkv + l * wkv_layer, (size_t)D.nl * wkv_layer, p.vfirst, p.slots, p.scap, p.gatedf, d, p.pmax,
+                     (int)D.h, d, (int)l, (int)D.g1k};
+        out.push_back(Launch::make((const void*)k_wkv_a8, dim3(D.h, n), dim3(kHead), 0, KC_WKV, wa));
+        out.push_back(exact_gemv_launch(L.e_o, p.gatedf, n, p.x, (uint32_t)d, EXACT_RESID, KC_PROJ));
+        ShiftA8Args s2{p.x, L.ln2_w, L.ln2_b, p.x_ffn + (size_t)l * d, state_stride, p.slots, p.scap, {}, {}, {}, {},
+                       d, d};
+        s2.mix[0] = L.ffn_x_k;
+        s2.outf[0] = xr;
+        out.push_back(Launch::make(shift_a8_fn(1), dim3(n), dim3(kBlock), 0, KC_SHIFT, s2));
+        out.push_back(exact_gemv_launch(L.e_fk, xr, n, p.actf, (uint32_t)f, EXACT_RELU2, KC_PROJ));
+        out.push_back(exact_gemv_launch(L.e_fv, p.actf, n, p.x, (uint32_t)d, EXACT_RESID, KC_PROJ));
+    }
+    ShiftA8Args sf{p.x, m.ln_out_w, m.ln_out_b, nullptr, 0, p.slots, p.scap, {}, {}, {}, {}, d, d};
+    sf.outf[0] = xr;
+    out.push_back(Launch::make(shift_a8_fn(0), dim3(n), dim3(kBlock), 0, KC_SHIFT, sf));
+    head_i = (int)out.size();
+    out.push_back(exact_gemv_launch(*m.e_head, xr, n, io.out + (size_t)io.b0 * D.vocab, D.vocab, EXACT_STORE, KC_HEAD));
     sm_i = -1;
     if (io.probs) {
         sm_i = (int)out.size();

@@ -35,7 +35,7 @@
 
 namespace rdk {
 
-RwkvSizes rwkv_sizes(const RDims& D, uint32_t cap, bool a8) {
+RwkvSizes rwkv_sizes(const RDims& D, uint32_t cap, bool a8, bool exact) {
     RwkvSizes z{};
     const size_t gcap = (cap + 15) / 16;
     auto ks_of = [](uint32_t cols) { return (int)((cols + kKAlign - 1) / kKAlign * (kKAlign / kKStep)); };
@@ -57,7 +57,7 @@ RwkvSizes rwkv_sizes(const RDims& D, uint32_t cap, bool a8) {
     z.fp = (size_t)z.ks_f * kKStep;
     z.rows16 = gcap * 16;
     if (a8) {
-        z.mixf = 4 * (size_t)cap * D.d;
+        z.mixf = (exact ? 6 : 4) * (size_t)cap * D.d;
         z.lorah = (size_t)cap * z.lora_sum;
         z.aq = z.rows16 * (kAqAct * z.dp + z.fp);
         z.as = (size_t)kAqVecs * cap;
@@ -428,6 +428,10 @@ struct ProjBuilder {
 }  // namespace
 
 void RwkvStep::build(Pool& p, const StepIO& io, std::vector<Launch>& out, int& io_i, int& head_i, int& sm_i) const {
+    if (m.exact) {
+        build_ref(p, io, out, io_i, head_i, sm_i);
+        return;
+    }
     if (m.a8) {
         build_a8(p, io, out, io_i, head_i, sm_i);
         return;

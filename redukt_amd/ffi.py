@@ -36,7 +36,7 @@ PROFILE_Q8_SMALL = 4
 PROFILE_EXACT_SCAN = 8  # Mamba scan decay by the portable exp instead of the hardware exp2
 PROFILE_GEMV = 16       # Mamba projections on the wavefront-GEMV kernels (the small-batch tier)
 PROFILE_W8A8 = 32       # RWKV-7 in the reference's own W8A8 arithmetic (with PROFILE_Q8_ROW), bit-exact
-PROFILE_EXACT = 64      # Mamba in the reference GEMV orders, numeric contract 1: logits bit-exact to the CPU path
+PROFILE_EXACT = 64      # the reference GEMV orders, numeric contract 1: logits bit-exact to the CPU path (Mamba; RWKV-7 F32)
 PROFILE_FMA = 128       # the same in numeric contract 2 (fma-v1); implies PROFILE_EXACT
 
 V1_SYMBOLS = ("redukt_backend_init", "redukt_backend_forward", "redukt_backend_reset_state", "redukt_backend_free")

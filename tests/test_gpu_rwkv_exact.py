@@ -1,13 +1,16 @@
-"""The RWKV-7 W8A8 tier (profile bit 5 with per-row int8 weights) on the GPU, through the
-C ABI, against the oracle's W8A8 path (the reference's own RWKV-7 Q8 arithmetic,
-src/domain/tensor.rs:105-143, 1791-1866).
+"""RWKV-7 in the reference's own arithmetic on the GPU, through the C ABI, against the
+oracle: the W8A8 tier (profile bit 5 with per-row int8 weights) against the oracle's W8A8
+path (the reference's RWKV-7 Q8 arithmetic, src/domain/tensor.rs:105-143, 1791-1866), and
+the F32 reference-order tier (profile bit 6) against the oracle's F32 path (every
+projection in mat_vec_mul_into's dot_avx2_order, tensor.rs:1602-1693).
 
-Every matrix product of the tier is an exact integer sum and every other operation follows
-the reference's order, sums included, so the bar is bit-exact equality with the oracle:
-logits at every step and every stream, the recurrent state of every layer, on a small
-model, a g1k model and the full-width RWKV-7 0.1B (vocabulary 65,536), with periodic
-resets, slots in any order and batches of any size.  The probability vector is held to
-the tolerance of the other tiers (the softmax is shared with them).
+In both tiers every matrix product is either an exact integer sum or the reference's own
+f32 dot order, and every other operation follows the reference's order, sums included, so
+the bar is bit-exact equality with the oracle: logits at every step and every stream, the
+recurrent state of every layer, on a small model, a g1k model and the full-width RWKV-7
+0.1B (vocabulary 65,536), with periodic resets, slots in any order and batches of any size.
+The probability vector is held to the tolerance of the other tiers (the softmax is shared
+with them).
 """
 import dataclasses
 
@@ -20,6 +23,9 @@ from redukt_amd import ffi, hip, rwkv
 pytestmark = pytest.mark.gpu
 
 A8 = ffi.PROFILE_Q8_ROW | ffi.PROFILE_W8A8
+REF = ffi.PROFILE_EXACT
+# tier: (library profile, oracle profile, backend name)
+TIERS = {"w8a8": (A8, A8, "hip-gfx950-rwkv7-w8a8"), "f32-ref": (REF, 0, "hip-gfx950-rwkv7-f32-ref")}
 SMALL = rwkv.RwkvDims(vocab=300, d_model=128, n_layer=2, head_size=64, d_ffn=256, lora_w=16, lora_a=16,
                       lora_v=8, lora_g=32)
 
@@ -64,22 +70,29 @@ def run_equal(be, orc, n, steps, tok_fn, slots=None, states=()):
                 assert np.array_equal(bits(got), bits(want)), (s, layer, what)
 
 
+@pytest.fixture(params=sorted(TIERS))
+def tier(request):
+    return TIERS[request.param]
+
+
 @pytest.mark.parametrize("name", ["small", "g1k"])
-def test_w8a8_bit_exact_small(models, name):
+def test_bit_exact_small(models, name, tier):
     path = models[name]
-    with ffi.PluginBackend(path, profile=A8) as be:
-        assert be.info.name_str() == "hip-gfx950-rwkv7-w8a8"
-        orc = O.RwkvOracle(path, A8, cap=19)
+    prof, oprof, label = tier
+    with ffi.PluginBackend(path, profile=prof) as be:
+        assert be.info.name_str() == label
+        orc = O.RwkvOracle(path, oprof, cap=19)
         be.batch_init(19)
         run_equal(be, orc, 19, 8, lambda s, t: (s * 37 + t * 101 + 3) % be.vocab, states=(0, 7, 18))
         orc.close()
 
 
-def test_w8a8_bit_exact_rwkv7_0_1b(models):
+def test_bit_exact_rwkv7_0_1b(models, tier):
     path = models["b01"]
-    with ffi.PluginBackend(path, profile=A8) as be:
+    prof, oprof, _ = tier
+    with ffi.PluginBackend(path, profile=prof) as be:
         assert be.vocab == 65536
-        orc = O.RwkvOracle(path, A8, cap=40)
+        orc = O.RwkvOracle(path, oprof, cap=40)
         be.batch_init(40)
         rng = np.random.default_rng(5)
         # 40 streams: two full groups of 16 and a partial one; slots in scrambled order
@@ -98,11 +111,11 @@ def test_w8a8_bit_exact_rwkv7_0_1b(models):
         orc.close()
 
 
-def test_w8a8_batch_sizes_and_v1(models):
+def test_batch_sizes_and_v1(models, tier):
     """One stream's bits do not depend on the batch it runs in, its position or its slot,
     and the v1 single-stream entry point gives the same bits."""
     path = models["small"]
-    with ffi.PluginBackend(path, profile=A8) as be:
+    with ffi.PluginBackend(path, profile=tier[0]) as be:
         v = be.vocab
         seq = [(53 * i + 7) % v for i in range(6)]
         out = np.empty(v, np.float32)
@@ -124,12 +137,13 @@ def test_w8a8_batch_sizes_and_v1(models):
                 assert np.array_equal(bits(g[pos]), bits(v1[i])), (n, pos, i)
 
 
-def test_w8a8_periodic_reset_and_probabilities(models):
+def test_periodic_reset_and_probabilities(models, tier):
     """The host's tick schedule (plugin_backend/model.rs:44-49) against the oracle's
     periodic reset, bit for bit; odd steps hand back the probability vector."""
     path = models["small"]
-    with ffi.PluginBackend(path, profile=A8) as be:
-        orc = O.RwkvOracle(path, A8, cap=6)
+    prof, oprof, _ = tier
+    with ffi.PluginBackend(path, profile=prof) as be:
+        orc = O.RwkvOracle(path, oprof, cap=6)
         orc.set_reset_every(3)
         be.prepare_streams(6)
         states = [be.create_state() for _ in range(6)]
@@ -153,10 +167,10 @@ def test_w8a8_periodic_reset_and_probabilities(models):
         orc.close()
 
 
-def test_w8a8_run_to_run(models):
+def test_run_to_run(models, tier):
     runs = []
     for _ in range(2):
-        with ffi.PluginBackend(models["small"], profile=A8) as be:
+        with ffi.PluginBackend(models["small"], profile=tier[0]) as be:
             be.batch_init(8)
             g = np.empty((8, be.vocab), np.float32)
             outs = []
@@ -181,5 +195,20 @@ def test_w8a8_init_rules(models, tmp_path):
             lib.free()
         info = lib.init(models["odd"], profile=ffi.PROFILE_Q8_ROW)   # rank 12 is fine without W8A8
         assert info.name_str() == "hip-gfx950-rwkv7-q8row"
+    finally:
+        lib.free()
+
+
+def test_reference_order_init_rules(models):
+    """RWKV-7's reference-order tier is F32 in numeric contract 1 only: its int8 arithmetic
+    is the W8A8 tier's, and the reference's RWKV-7 GEMVs have no fma-v1 twin."""
+    lib = ffi.PluginLibrary()
+    try:
+        for path, prof in ((models["small"], REF | ffi.PROFILE_Q8_G64), (models["small"], REF | ffi.PROFILE_Q8_ROW),
+                           (models["small"], REF | ffi.PROFILE_FMA), (models["small"], ffi.PROFILE_FMA),
+                           (models["small"], REF | A8), (models["odd"], REF)):
+            with pytest.raises(ffi.BackendError):
+                lib.init(path, profile=prof)
+            lib.free()
     finally:
         lib.free()
