@@ -23,6 +23,22 @@ def full_model(tmp_path_factory):
     return p
 
 
+@pytest.fixture(scope="session")
+def oracle_plugin(tmp_path_factory):
+    """The CPU oracle behind the reference's plugin ABI (tests/oracle_plugin.c), for Mamba
+    and RWKV-7 files.  Linked -z nodelete: the driver unloads a plugin when it closes, and
+    the oracle's worker threads must not outlive the code and state of an unloaded copy."""
+    import subprocess
+
+    here = os.path.join(ROOT, "tests")
+    d = tmp_path_factory.mktemp("oracle_plugin")
+    so = str(d / "liboracle_plugin.so")
+    odir = os.path.join(ROOT, "oracle")
+    subprocess.run(["gcc", "-O2", "-std=gnu11", "-shared", "-fPIC", "-I", odir, os.path.join(here, "oracle_plugin.c"),
+                    "-o", so, "-L", odir, "-loracle", "-Wl,-rpath," + odir, "-Wl,-z,nodelete"], check=True)
+    return so
+
+
 # Worker pools stay within one GPU's share of host cores (16), whatever the machine
 # reports: the oracle's GEMV threads and the host library's coding threads.
 os.environ.setdefault("ORACLE_THREADS", str(min(os.cpu_count() or 1, 16)))

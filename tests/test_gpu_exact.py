@@ -12,7 +12,6 @@ sequential norms and the portable exp in the scan, so:
   the GPU codes the same bytes: the reference's numeric contracts carry across devices.
 """
 import os
-import subprocess
 
 import numpy as np
 import pytest
@@ -23,8 +22,6 @@ from redukt_amd.lockstep import Lockstep
 
 pytestmark = pytest.mark.gpu
 
-HERE = os.path.dirname(os.path.abspath(__file__))
-ROOT = os.path.dirname(HERE)
 EXACT = ffi.PROFILE_EXACT
 FMA = ffi.PROFILE_FMA
 SMALL = {"reftest": rbin.MambaDims(vocab=1200, d_model=64, n_layer=2),
@@ -116,19 +113,6 @@ def test_exact_tier_v1_and_batch_and_reset(small):
             g = np.empty((3, dims.vocab), np.float32)
             be.forward_batch([2, 11, 7], toks, g)
             assert np.array_equal(bits(g[1]), bits(want[i])), ("batch", i)
-
-
-@pytest.fixture(scope="module")
-def oracle_plugin(tmp_path_factory):
-    """The CPU oracle behind the reference's plugin ABI (tests/oracle_plugin.c).  Linked
-    -z nodelete: the driver unloads a plugin when it closes, and the oracle's worker
-    threads must not outlive the code and state of an unloaded copy."""
-    d = tmp_path_factory.mktemp("oracle_plugin")
-    so = str(d / "liboracle_plugin.so")
-    odir = os.path.join(ROOT, "oracle")
-    subprocess.run(["gcc", "-O2", "-std=gnu11", "-shared", "-fPIC", "-I", odir, os.path.join(HERE, "oracle_plugin.c"),
-                    "-o", so, "-L", odir, "-loracle", "-Wl,-rpath," + odir, "-Wl,-z,nodelete"], check=True)
-    return so
 
 
 @pytest.mark.parametrize("profile,contract", [(0, 1), (1, 2), (6, 1)])

@@ -10,7 +10,9 @@ the bar is bit-exact equality with the oracle: logits at every step and every st
 recurrent state of every layer, on a small model, a g1k model and the full-width RWKV-7
 0.1B (vocabulary 65,536), with periodic resets, slots in any order and batches of any size.
 The probability vector is held to the tolerance of the other tiers (the softmax is shared
-with them).
+with them).  Since the bits are the CPU path's, an archive coded on the CPU (the oracle
+behind the plugin ABI) decodes on the GPU, the GPU codes the same bytes, and an RDKT v5
+archive of the RWKV-7 backbone written on the GPU decodes on the CPU from its header alone.
 """
 import dataclasses
 
@@ -18,7 +20,8 @@ import numpy as np
 import pytest
 
 from oracle import oracle as O
-from redukt_amd import ffi, hip, rwkv
+from redukt_amd import archive, ffi, hip, rwkv
+from redukt_amd.lockstep import Lockstep
 
 pytestmark = pytest.mark.gpu
 
@@ -26,6 +29,8 @@ A8 = ffi.PROFILE_Q8_ROW | ffi.PROFILE_W8A8
 REF = ffi.PROFILE_EXACT
 # tier: (library profile, oracle profile, backend name)
 TIERS = {"w8a8": (A8, A8, "hip-gfx950-rwkv7-w8a8"), "f32-ref": (REF, 0, "hip-gfx950-rwkv7-f32-ref")}
+# the RDKT header's weight-profile code of each tier (the reference's RWKV-7 Q8 is W8A8)
+QUANT_CODE = {A8: 1, REF: 0}
 SMALL = rwkv.RwkvDims(vocab=300, d_model=128, n_layer=2, head_size=64, d_ffn=256, lora_w=16, lora_a=16,
                       lora_v=8, lora_g=32)
 
@@ -212,3 +217,34 @@ def test_reference_order_init_rules(models):
             lib.free()
     finally:
         lib.free()
+
+
+def test_archives_cross_devices(models, oracle_plugin, tier):
+    """Lockstep coding of several files (crossing reset boundaries) on the CPU oracle and on
+    the GPU gives the same bytes, each side decodes the other's, and GPU streams packed
+    into RDKT v5 archives of the RWKV-7 backbone (BACKBONE 0, PROFILE from the tier,
+    RESET_LOG2 8) decode on the CPU with the weight profile taken from the header and the
+    restored data's CRC-32 (src/application/codec.rs:540-580, 648-720)."""
+    prof, oprof, _ = tier
+    path = models["g1k"]
+    rng = np.random.default_rng(9 + prof)
+    files = [rng.integers(0, SMALL.vocab, k).astype(np.uint32) for k in (300, 1, 90, 520)]
+    print(f"rwkv cross-device round trip profile {prof}", flush=True)
+    with Lockstep(path, plugin_path=oracle_plugin, profile=oprof, slots=3) as cpu:
+        cpu_bytes, _ = cpu.compress(files, reset_every=256)
+    with Lockstep(path, profile=prof, slots=3) as gpu:
+        gpu_bytes, _ = gpu.compress(files, reset_every=256)
+        assert gpu_bytes == cpu_bytes, "the GPU codes other bytes than the CPU"
+        back, _ = gpu.decompress(cpu_bytes, [len(f) for f in files], reset_every=256)
+    for f, b in zip(files, back):
+        assert np.array_equal(f, b)
+    for f, stm in zip(files, gpu_bytes):
+        payload = f.astype("<u4").tobytes()
+        h = archive.default_header(len(payload), backbone=archive.BACKBONE_RWKV, quant=QUANT_CODE[prof], reset_log2=8)
+        hd, body, crc = archive.unpack(archive.pack(h, stm, payload))
+        assert (hd.backbone, hd.quant, hd.contract, hd.reset_every) == (archive.BACKBONE_RWKV, QUANT_CODE[prof], 1, 256)
+        cpu_profile = A8 if hd.quant == 1 else 0
+        with Lockstep(path, plugin_path=oracle_plugin, profile=cpu_profile, slots=1) as cpu:
+            back, _ = cpu.decompress([body], [hd.total_bytes // 4], reset_every=hd.reset_every)
+        assert archive.crc32(back[0].astype("<u4").tobytes()) == crc
+        assert np.array_equal(back[0], f)
