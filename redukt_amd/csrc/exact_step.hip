@@ -195,10 +195,9 @@ __device__ __forceinline__ void load4(const RowMat& m, size_t row_off, int c0, i
 
 // Eight lanes compute one output (row, S streams): lane l holds accumulator l of the
 // reference's eight, the columns c = l (mod 8) of each column group in order from +0; the
-// horizontal sum ((l0+l4)+(l2+l6)) + ((l1+l5)+(l3+l7)) is the xor butterfly 4, 2, 1 over
-// the eight lanes (IEEE addition is commutative, so each lane pair forms exactly the
-// reference's sums); Q8 rows then take sum = sum + dot * scale from +0.  Workgroup (bx, by)
-// holds rows [32 bx, 32 bx + 32) and streams [S by, S by + S), the streams' input rows
+// horizontal sum ((l0+l4)+(l2+l6)) + ((l1+l5)+(l3+l7)) is formed in lane 0 of the eight
+// by three DPP adds (hsum8_lane0); Q8 rows then take sum = sum + dot * scale from +0.
+// Workgroup (bx, by) holds rows [32 bx, 32 bx + 32) and streams [S by, S by + S), the streams' input rows
 // staged in LDS.  Every operation in the contract's arithmetic (madd).  Column counts and
 // groups are whole 32-column blocks (checked at load).
 // NB > 0: the rows have exactly NB 32-column blocks, and each lane requests its whole
@@ -219,21 +218,19 @@ __global__ __launch_bounds__(kEBlock) void k_gemv_e(GemvEArgs a) {
     const int l = (int)threadIdx.x % 8;
     const int r_raw = (int)blockIdx.x * (kEBlock / 8) + (int)threadIdx.x / 8;
     const bool live = r_raw < m.rows;
-    const int r = live ? r_raw : m.rows - 1;   // every lane joins the butterflies
+    const int r = live ? r_raw : m.rows - 1;   // every lane joins the horizontal sums
     const size_t row_off = (size_t)r * cols;
     const int group = Q8 ? m.group : cols;
     const int ng = cols / group;
     float res[S];
 #pragma unroll
     for (int s = 0; s < S; s++) res[s] = 0.0f;
-    // The eight lanes' horizontal sum of each stream's accumulator, then the group's fold.
+    // The eight lanes' horizontal sum of each stream's accumulator, then the group's fold
+    // (both complete in lane 0 of the eight, the lane that stores).
     auto finish_group = [&](float (&acc)[S], int g) {
 #pragma unroll
         for (int s = 0; s < S; s++) {
-            float v = acc[s];
-            v = v + __shfl_xor(v, 4, 8);
-            v = v + __shfl_xor(v, 2, 8);
-            v = v + __shfl_xor(v, 1, 8);
+            const float v = hsum8_lane0(acc[s]);
             res[s] = Q8 ? madd<FMA>(v, m.scales[(size_t)r * ng + g], res[s]) : v;
             acc[s] = 0.0f;
         }

@@ -47,6 +47,27 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// v moved between lanes by the DPP control word CTRL (within rows of 16 lanes; a lane
+// without a source reads 0).
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+constexpr int kDppRowShl4 = 0x104;     // lane i reads lane i + 4
+constexpr int kDppQuadXor2 = 0x4E;     // quad_perm [2, 3, 0, 1]: lane i reads lane i ^ 2
+constexpr int kDppQuadXor1 = 0xB1;     // quad_perm [1, 0, 3, 2]: lane i reads lane i ^ 1
+
+// The horizontal sum ((a0 + a4) + (a2 + a6)) + ((a1 + a5) + (a3 + a7)) of lanes 8k .. 8k + 7
+// (lane 8k + l holding a_l), complete in lane 8k: each add pairs the same two values as
+// that expression (IEEE addition is commutative).  The other seven lanes end with values of
+// no use.
+__device__ __forceinline__ float hsum8_lane0(float v) {
+    v = v + dpp_move<kDppRowShl4>(v);
+    v = v + dpp_move<kDppQuadXor2>(v);
+    v = v + dpp_move<kDppQuadXor1>(v);
+    return v;
+}
+
 // The wave's index within its workgroup as a wave-uniform (scalar) value: indices derived
 // from it stay in scalar registers instead of being recomputed per lane.
 __device__ __forceinline__ int wave_index() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave)); }

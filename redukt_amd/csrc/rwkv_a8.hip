@@ -488,15 +488,14 @@ __device__ __forceinline__ void lora_rows(const SegA8& s, int rb, uint32_t b) {
             }
         }
     }
+    // complete in lane h = 0 of the row, the lane that stores
     float sum;
     if (LPR == 8) {
-        float t = acc[0] + __shfl_xor(acc[0], 4, kWave);
-        t = t + __shfl_xor(t, 2, kWave);
-        sum = t + __shfl_xor(t, 1, kWave);
+        sum = hsum8_lane0(acc[0]);
     } else {
         float s4[4];
 #pragma unroll
-        for (int j = 0; j < 4; j++) s4[j] = acc[j] + __shfl_xor(acc[j], 1, kWave);
+        for (int j = 0; j < 4; j++) s4[j] = acc[j] + dpp_move<kDppQuadXor1>(acc[j]);
         sum = (s4[0] + s4[2]) + (s4[1] + s4[3]);
     }
     if (h == 0 && r < s.l.rows) s.out[(size_t)b * s.ld + r] = activate(s.act, sum, r, s.l.rows);

@@ -82,6 +82,15 @@ def test_exact_tier_equals_oracle_bit_for_bit(small, name, profile, contract):
 
 @pytest.mark.parametrize("contract", [1, 2])
 @pytest.mark.parametrize("profile", [0, 1])
+def test_exact_tier_wide_batch(small, profile, contract):
+    # 37 streams: the projections' workgroups of four streams and the head's of eight, each
+    # with a partial last group; slots scrambled over a pool of 40
+    slots = [int(s) for s in np.random.default_rng(3).permutation(40)[:37]]
+    check_bitwise(small["base"], SMALL["base"], profile, contract, n=37, steps=3, slots=slots, seed=11)
+
+
+@pytest.mark.parametrize("contract", [1, 2])
+@pytest.mark.parametrize("profile", [0, 1])
 def test_exact_tier_mamba130m_equals_oracle(full_model, profile, contract):
     check_bitwise(full_model, rbin.MAMBA_130M, profile, contract, n=3, steps=3, seed=profile + 5 * contract)
 
