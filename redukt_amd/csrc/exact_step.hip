@@ -350,18 +350,23 @@ const void* gemv_e_nb(int cols, bool q8, bool fma) {
 
 template <int EPI>
 const void* gemv_e_pick(uint32_t s, int cols, bool q8, bool fma) {
+    if (s == 8) return gemv_e_nb<8, EPI>(cols, q8, fma);
     return s == 1 ? gemv_e_nb<1, EPI>(cols, q8, fma) : gemv_e_nb<4, EPI>(cols, q8, fma);
 }
 
 // Streams per workgroup: one for a single stream, four otherwise (their input rows in LDS:
 // 4 x d_inner floats at most 32 KB; sixteen, reading each row once per 16 streams, leave
-// too few workgroups: 32 streams 1.78 -> 2.38 ms per step).  A stream's arithmetic does not
-// depend on it.
+// too few workgroups: 32 streams 1.78 -> 2.38 ms per step; eight at 64 and 128 streams
+// double the out_proj time).  The head, with 50K rows, takes eight from 16 streams on
+// (its weights read half as often: Mamba-130M F32 at 128 streams 643 -> 422 us; sixteen
+// 597 us).  A stream's arithmetic does not depend on it.
 uint32_t exact_streams(uint32_t n) { return n == 1 ? 1u : 4u; }
+constexpr uint32_t kHeadStreams = 8;
 
 Launch gemv_e_launch(const void* (*pick)(uint32_t, int, bool, bool), bool fma, int cls, const RowMat& w,
-                     const float* act, uint32_t n, GemvEArgs a) {
-    const uint32_t S = exact_streams(n);
+                     const float* act, uint32_t n, GemvEArgs a, uint32_t s_wide = 0) {
+    // s_wide streams per workgroup once the batch fills two such workgroups
+    const uint32_t S = s_wide && n >= 2 * s_wide ? s_wide : exact_streams(n);
     const void* fn = pick(S, w.cols, w.group != 0, fma);
     a.w = w;
     a.act = act;
@@ -382,7 +387,7 @@ Launch exact_gemv_launch(const RowMat& w, const float* act, uint32_t n, float* o
     const void* (*pick)(uint32_t, int, bool, bool) = epi == EXACT_RESID   ? gemv_e_pick<kEpiRes>
                                                       : epi == EXACT_RELU2 ? gemv_e_pick<kEpiRelu2>
                                                                            : gemv_e_pick<kEpiPlain>;
-    return gemv_e_launch(pick, false, (int)cls, w, act, n, a);
+    return gemv_e_launch(pick, false, (int)cls, w, act, n, a, cls == KC_HEAD ? kHeadStreams : 0);
 }
 
 void ExactStep::build(Pool& p, const StepIO& io, std::vector<Launch>& out, int& io_i, int& head_i, int& sm_i) const {
@@ -427,7 +432,7 @@ void ExactStep::build(Pool& p, const StepIO& io, std::vector<Launch>& out, int& 
     GemvEArgs gh{};
     gh.out = io.out;
     gh.ostride = D.vocab;
-    out.push_back(gemv_e_launch(gemv_e_pick<kEpiPlain>, fma, KC_HEAD, *m.head, p.normed, n, gh));
+    out.push_back(gemv_e_launch(gemv_e_pick<kEpiPlain>, fma, KC_HEAD, *m.head, p.normed, n, gh, kHeadStreams));
     sm_i = -1;
     if (io.probs) {
         sm_i = (int)out.size();
