@@ -102,8 +102,8 @@ def launches_per_step(dims, name: str, mamba: bool, profile: int) -> int:
     L = dims.n_layer
     if mamba:
         return L if name in ("mix_in", "scan", "mix_out") else 1
-    if profile & ffi.PROFILE_EXACT:                       # r, k, v, two LoRA stages, o, FFN key, value
-        return {"shift": 2 * L + 1, "proj": 8 * L, "wkv": L}.get(name, 1)
+    if profile & ffi.PROFILE_EXACT:                       # r/k/v, two LoRA stages, o, FFN key, value
+        return {"shift": 2 * L + 1, "proj": 6 * L, "wkv": L}.get(name, 1)
     if profile & ffi.PROFILE_W8A8:                        # + ln_out, staged as int8 for the head;
         return {"shift": 2 * L + 1, "proj": 6 * L, "wkv": L}.get(name, 1)   # proj: five products + k_quant_a8
     ws = (profile & 3) == 2 and dims.d_model <= 768       # the weights-stationary head needs ln_out staged

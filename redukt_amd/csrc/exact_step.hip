@@ -171,6 +171,11 @@ struct GemvEArgs {
     float* u;
     float* z;
     int di;
+    // Products 1 and 2 of a launch of three of one shape (grid z; product 0 is w, act,
+    // out): rows w_more[z - 1], input rows act_more[z - 1], outputs from out + out_more[z - 1].
+    RowMat w_more[2];
+    const float* act_more[2];
+    uint32_t out_more[2];
 };
 
 // acc + w * x in the contract's arithmetic.
@@ -206,12 +211,15 @@ __device__ __forceinline__ void load4(const RowMat& m, size_t row_off, int c0, i
 template <bool Q8, bool FMA, int S, int EPI, int NB>
 __global__ __launch_bounds__(kEBlock) void k_gemv_e(GemvEArgs a) {
     extern __shared__ __align__(16) float acts[];   // [S][cols], 32-column blocks interleaved like the rows
-    const RowMat& m = a.w;
+    const uint32_t z = blockIdx.z;
+    const RowMat& m = z == 0 ? a.w : z == 1 ? a.w_more[0] : a.w_more[1];
+    const float* const act = z == 0 ? a.act : z == 1 ? a.act_more[0] : a.act_more[1];
+    float* const out = z == 0 ? a.out : a.out + (z == 1 ? a.out_more[0] : a.out_more[1]);
     const int cols = m.cols;
     const uint32_t b0 = blockIdx.y * S;
     for (int s = 0; s < S; s++) {
         const uint32_t b = min(b0 + (uint32_t)s, a.n - 1);
-        const float* src = a.act + (size_t)b * cols;
+        const float* src = act + (size_t)b * cols;
         for (int c = threadIdx.x; c < cols; c += kEBlock) acts[rowmat_index((size_t)s * cols, c)] = src[c];
     }
     __syncthreads();
@@ -298,15 +306,15 @@ __global__ __launch_bounds__(kEBlock) void k_gemv_e(GemvEArgs a) {
         if (b >= a.n) break;
         const float y = res[s];
         if (EPI == kEpiPlain) {
-            a.out[(size_t)b * a.ostride + r] = y;
+            out[(size_t)b * a.ostride + r] = y;
         } else if (EPI == kEpiRes) {
             // x += W_out * gated (model.rs:714-719): the residual add after the projection
-            float* xp = a.out + (size_t)b * a.ostride + r;
+            float* xp = out + (size_t)b * a.ostride + r;
             *xp = *xp + y;
         } else if (EPI == kEpiRelu2) {
             // squared_relu_into (tensor.rs:1386-1388): max(y, 0)^2, a NaN to 0
             const float t = y > 0.0f ? y : 0.0f;
-            a.out[(size_t)b * a.ostride + r] = t * t;
+            out[(size_t)b * a.ostride + r] = t * t;
         } else if (r >= a.di) {
             a.z[(size_t)b * a.di + (r - a.di)] = y;
         } else {
@@ -364,7 +372,7 @@ uint32_t exact_streams(uint32_t n) { return n == 1 ? 1u : 4u; }
 constexpr uint32_t kHeadStreams = 8;
 
 Launch gemv_e_launch(const void* (*pick)(uint32_t, int, bool, bool), bool fma, int cls, const RowMat& w,
-                     const float* act, uint32_t n, GemvEArgs a, uint32_t s_wide = 0) {
+                     const float* act, uint32_t n, GemvEArgs a, uint32_t s_wide = 0, uint32_t products = 1) {
     // s_wide streams per workgroup once the batch fills two such workgroups
     const uint32_t S = s_wide && n >= 2 * s_wide ? s_wide : exact_streams(n);
     const void* fn = pick(S, w.cols, w.group != 0, fma);
@@ -373,7 +381,7 @@ Launch gemv_e_launch(const void* (*pick)(uint32_t, int, bool, bool), bool fma, i
     a.n = n;
     const uint32_t lds = S * (uint32_t)w.cols * 4u;
     constexpr int rows_per_wg = kEBlock / 8;
-    return Launch::make(fn, dim3((unsigned)((w.rows + rows_per_wg - 1) / rows_per_wg), (n + S - 1) / S),
+    return Launch::make(fn, dim3((unsigned)((w.rows + rows_per_wg - 1) / rows_per_wg), (n + S - 1) / S, products),
                         dim3(kEBlock), lds, (uint32_t)cls, a);
 }
 
@@ -388,6 +396,19 @@ Launch exact_gemv_launch(const RowMat& w, const float* act, uint32_t n, float* o
                                                       : epi == EXACT_RELU2 ? gemv_e_pick<kEpiRelu2>
                                                                            : gemv_e_pick<kEpiPlain>;
     return gemv_e_launch(pick, false, (int)cls, w, act, n, a, cls == KC_HEAD ? kHeadStreams : 0);
+}
+
+Launch exact_gemv3_launch(const RowMat* const (&w)[3], const float* const (&act)[3], uint32_t n, float* out,
+                          const uint32_t (&out_off)[3], uint32_t ostride, uint32_t cls) {
+    GemvEArgs a{};
+    a.out = out + out_off[0];
+    a.ostride = ostride;
+    for (int k = 0; k < 2; k++) {
+        a.w_more[k] = *w[k + 1];
+        a.act_more[k] = act[k + 1];
+        a.out_more[k] = out_off[k + 1] - out_off[0];
+    }
+    return gemv_e_launch(gemv_e_pick<kEpiPlain>, false, (int)cls, *w[0], act[0], n, a, 0, 3);
 }
 
 void ExactStep::build(Pool& p, const StepIO& io, std::vector<Launch>& out, int& io_i, int& head_i, int& sm_i) const {

@@ -360,6 +360,10 @@ struct ExactStep final : StepSource {
 enum ExactEpi : int { EXACT_STORE = 0, EXACT_RESID = 2, EXACT_RELU2 = 3 };
 Launch exact_gemv_launch(const RowMat& w, const float* act, uint32_t n, float* out, uint32_t ostride, int epi,
                          uint32_t cls);
+// Three such products of one shape in one launch (EXACT_STORE), product k's outputs from
+// out + out_off[k] (out_off ascending).
+Launch exact_gemv3_launch(const RowMat* const (&w)[3], const float* const (&act)[3], uint32_t n, float* out,
+                          const uint32_t (&out_off)[3], uint32_t ostride, uint32_t cls);
 
 struct RwkvStep final : StepSource {
     RwkvView m;

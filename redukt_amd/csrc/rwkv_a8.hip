@@ -31,7 +31,8 @@
 //
 // The reference-order tier (F32 weights, profile bit 6) runs the same element-wise kernels
 // with every projection an F32 GEMV in the reference's dot_avx2_order (mat_vec_mul_into,
-// tensor.rs:1602-1693; exact_gemv_launch, eight lanes per output): k_shift_a8 hands all six
+// tensor.rs:1602-1693; exact_gemv_launch, eight lanes per output; receptance, key and value
+// in one launch): k_shift_a8 hands all six
 // token-shift inputs over as f32, and the receptance, key, value, output, FFN and head
 // products replace the int8 ones (the FFN key's squared ReLU in its epilogue), so the
 // logits are the CPU path's F32 logits bit for bit.
@@ -942,9 +943,11 @@ void RwkvStep::build_ref(Pool& p, const StepIO& io, std::vector<Launch>& out, in
         s1.outf[4] = mixf[kLoraA];
         s1.outf[5] = mixf[kLoraG];
         out.push_back(Launch::make(shift_a8_fn(6), dim3(n), dim3(kBlock), 0, KC_SHIFT, s1));
-        out.push_back(exact_gemv_launch(L.e_r, xr, n, p.rkv, 3u * d, EXACT_STORE, KC_PROJ));
-        out.push_back(exact_gemv_launch(L.e_k, xk, n, p.rkv + d, 3u * d, EXACT_STORE, KC_PROJ));
-        out.push_back(exact_gemv_launch(L.e_v, mixf[kLoraV], n, p.rkv + 2 * d, 3u * d, EXACT_STORE, KC_PROJ));
+        // receptance, key and value in one launch
+        const RowMat* const rkv_w[3] = {&L.e_r, &L.e_k, &L.e_v};
+        const float* const rkv_in[3] = {xr, xk, mixf[kLoraV]};
+        const uint32_t rkv_off[3] = {0u, (uint32_t)d, 2u * d};
+        out.push_back(exact_gemv3_launch(rkv_w, rkv_in, n, p.rkv, rkv_off, 3u * d, KC_PROJ));
         ProjA8Builder p1(n, 0);
         p1.lora(L.x1[kLoraW], mixf[kLoraW], d, ACT_TANH, lh[kLoraW], lsum);
         p1.lora(L.x1[kLoraA], mixf[kLoraA], d, ACT_NONE, lh[kLoraA], lsum);
