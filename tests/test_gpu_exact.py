@@ -89,6 +89,12 @@ def test_exact_tier_wide_batch(small, profile, contract):
     check_bitwise(small["base"], SMALL["base"], profile, contract, n=37, steps=3, slots=slots, seed=11)
 
 
+def test_exact_tier_long_horizon(small):
+    # 8 streams for 600 steps, int8 groups of 64 in contract 2: every logit of every step
+    # and the final state bit for bit (no drift however long the recurrence runs)
+    check_bitwise(small["base"], SMALL["base"], 1, 2, n=8, steps=600, seed=21)
+
+
 @pytest.mark.parametrize("contract", [1, 2])
 @pytest.mark.parametrize("profile", [0, 1])
 def test_exact_tier_mamba130m_equals_oracle(full_model, profile, contract):

@@ -92,6 +92,17 @@ def test_bit_exact_small(models, name, tier):
         orc.close()
 
 
+def test_long_horizon(models, tier):
+    """8 streams for 400 steps on the g1k model: every logit and the final state, bit for bit."""
+    path = models["g1k"]
+    prof, oprof, _ = tier
+    with ffi.PluginBackend(path, profile=prof) as be:
+        orc = O.RwkvOracle(path, oprof, cap=8)
+        be.batch_init(8)
+        run_equal(be, orc, 8, 400, lambda s, t: (s * 97 + t * 31 + 11) % be.vocab, states=(0, 5))
+        orc.close()
+
+
 def test_bit_exact_rwkv7_0_1b(models, tier):
     path = models["b01"]
     prof, oprof, _ = tier
