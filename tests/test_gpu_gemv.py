@@ -1,7 +1,8 @@
 """The wavefront-GEMV tier (weight profile bit 4) on the GPU, through the C ABI.
 
 The tier computes the Mamba projections as f32 dot products on the vector ALUs (the
-small-batch family); it is chosen at init, never by n (SURVEY hard part (a), option 2), so:
+small-batch family); it is chosen at init, never by n (the batch-invariance rule of
+PLUGIN-FFI-V2.md:97-101: a stream's logits may not depend on the batch it runs in), so:
 
 * logits within max |err| <= 1e-3 and probability L1 <= 1e-4 of the CPU oracle (the oracle
   knows one arithmetic for the model; the tier bit only changes how the GPU computes it),
