@@ -933,6 +933,12 @@ uint32_t env_weight_profile() {
     if (!strcmp(e, "q8row")) return BACKEND_PROFILE_Q8_ROW;
     if (!strcmp(e, "q8row-all")) return BACKEND_PROFILE_Q8_ROW | BACKEND_PROFILE_Q8_SMALL;
     if (!strcmp(e, "q8-all")) return BACKEND_PROFILE_Q8_G64 | BACKEND_PROFILE_Q8_SMALL;
+    // the bit-exact tiers under the reference's own profile names and numeric contracts
+    if (!strcmp(e, "f32-ref")) return BACKEND_PROFILE_F32 | BACKEND_PROFILE_EXACT;
+    if (!strcmp(e, "q8-ref")) return BACKEND_PROFILE_Q8_G64 | BACKEND_PROFILE_EXACT;
+    if (!strcmp(e, "f32-ref-fma")) return BACKEND_PROFILE_F32 | BACKEND_PROFILE_EXACT | BACKEND_PROFILE_FMA;
+    if (!strcmp(e, "q8-ref-fma")) return BACKEND_PROFILE_Q8_G64 | BACKEND_PROFILE_EXACT | BACKEND_PROFILE_FMA;
+    if (!strcmp(e, "q8row-w8a8")) return BACKEND_PROFILE_Q8_ROW | BACKEND_PROFILE_W8A8;
     return (uint32_t)strtoul(e, nullptr, 0) & 255u;
 }
 

@@ -177,6 +177,19 @@ def test_rdkt_archive_written_on_gpu_decodes_on_cpu(small, oracle_plugin, quant,
         assert np.array_equal(back[0], f)
 
 
+@pytest.mark.parametrize("name,label", [("f32-ref", "hip-gfx950-mamba-f32-ref"), ("q8-ref", "hip-gfx950-mamba-q8-ref"),
+                                        ("f32-ref-fma", "hip-gfx950-mamba-f32-ref-fma"),
+                                        ("q8-ref-fma", "hip-gfx950-mamba-q8-ref-fma")])
+def test_named_profiles_from_the_environment(small, monkeypatch, name, label):
+    # the v1 init takes its weight profile from REDUKT_GPU_PROFILE, by name
+    monkeypatch.setenv("REDUKT_GPU_PROFILE", name)
+    lib = ffi.PluginLibrary()
+    try:
+        assert lib.init(small["base"]).name_str() == label
+    finally:
+        lib.free()
+
+
 def test_exact_tier_refuses_what_it_does_not_serve(small):
     lib = ffi.PluginLibrary()
     info = ffi.BackendInfo()

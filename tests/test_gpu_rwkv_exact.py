@@ -215,6 +215,16 @@ def test_w8a8_init_rules(models, tmp_path):
         lib.free()
 
 
+@pytest.mark.parametrize("name", sorted(TIERS))
+def test_named_profiles_from_the_environment(models, monkeypatch, name):
+    monkeypatch.setenv("REDUKT_GPU_PROFILE", {"w8a8": "q8row-w8a8", "f32-ref": "f32-ref"}[name])
+    lib = ffi.PluginLibrary()
+    try:
+        assert lib.init(models["small"]).name_str() == TIERS[name][2]
+    finally:
+        lib.free()
+
+
 def test_reference_order_init_rules(models):
     """RWKV-7's reference-order tier is F32 in numeric contract 1 only: its int8 arithmetic
     is the W8A8 tier's, and the reference's RWKV-7 GEMVs have no fma-v1 twin."""
