@@ -198,3 +198,32 @@ def test_device_cdf_needs_the_plugin_symbol(fake):
         Lockstep(w, plugin_path=so, slots=3, device_cdf=True)
     with Lockstep(w, plugin_path=so, slots=3, device_cdf=False) as ls:
         assert ls.compress(files(), reset_every=16)[0] == out
+
+
+@pytest.mark.parametrize("kind", ["mamba", "rwkv7"])
+def test_oracle_plugin_round_trip_on_the_cpu(oracle_plugin, tmp_path, kind):
+    """The CPU oracle behind the plugin ABI (tests/oracle_plugin.c) drives the lockstep
+    coder end to end on the host: batched compress, then decompress, byte-exact, for both
+    model kinds the plugin tells apart by the file header; batched and single-stream
+    coding give the same bytes."""
+    from redukt_amd import rbin, rwkv, synth
+
+    path = str(tmp_path / f"{kind}.rbin")
+    if kind == "mamba":
+        synth.write_synthetic_mamba(path, rbin.MambaDims(vocab=300, d_model=64, n_layer=2), seed=4)
+        vocab = 300
+    else:
+        dims = rwkv.RwkvDims(vocab=260, d_model=64, n_layer=2, head_size=64, d_ffn=128, lora_w=8, lora_a=8,
+                             lora_v=8, lora_g=16)
+        rwkv.write_synthetic(path, dims, seed=4)
+        vocab = 260
+    rng = np.random.default_rng(6)
+    files = [rng.integers(0, vocab, k).astype(np.uint32) for k in (70, 1, 40)]
+    with Lockstep(path, plugin_path=oracle_plugin, slots=2) as ls:
+        streams, _ = ls.compress(files, reset_every=32)
+        back, _ = ls.decompress(streams, [len(f) for f in files], reset_every=32)
+    for f, b in zip(files, back):
+        assert np.array_equal(f, b)
+    with Lockstep(path, plugin_path=oracle_plugin, slots=0) as single:
+        one, _ = single.compress(files, reset_every=32)
+    assert one == streams
