@@ -306,13 +306,14 @@ def _device_step(be, slots, toks, v):
             b.close()
 
 
-def test_device_check_contains_bad_entries(models):
+@pytest.mark.parametrize("profile", [6, ffi.PROFILE_Q8_G64 | ffi.PROFILE_EXACT | ffi.PROFILE_FMA])
+def test_device_check_contains_bad_entries(models, profile):
     # A device-checked step with a repeated slot or a bad token routes the offending entries
     # to the pool's scratch slot: slots the call does not name keep their state bit for bit,
     # and the valid entries (a repeated slot's first occurrence included) advance exactly as
-    # they would in a valid call.
+    # they would in a valid call (on the matrix-core tier and the reference-order tier).
     dims = SMALL_BASE
-    with ffi.PluginBackend(models["base"], profile=6) as be:
+    with ffi.PluginBackend(models["base"], profile=profile) as be:
         v = be.vocab
         be.batch_init(8)
         state = lambda s: [be.get_state(s, l, dims.d_inner, 4) for l in range(dims.n_layer)]

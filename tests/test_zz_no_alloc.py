@@ -42,7 +42,8 @@ def _run(be, noalloc, calls, probs, state_slots, dims):
     return outs, states
 
 
-@pytest.mark.parametrize("which,profile,probs", [("small", 0, False), ("small", 6, True), ("m130", Q8ROW_ALL, False)])
+@pytest.mark.parametrize("which,profile,probs", [("small", 0, False), ("small", 6, True), ("m130", Q8ROW_ALL, False),
+                                                  ("small", ffi.PROFILE_Q8_G64 | ffi.PROFILE_EXACT | ffi.PROFILE_FMA, False)])
 def test_noalloc_step_equals_device_step(tmp_path, full_model, which, profile, probs):
     if which == "small":
         dims = rbin.MambaDims(vocab=1000, d_model=96, n_layer=3)
