@@ -269,3 +269,61 @@ def test_archives_cross_devices(models, oracle_plugin, tier):
             back, _ = cpu.decompress([body], [hd.total_bytes // 4], reset_every=hd.reset_every)
         assert archive.crc32(back[0].astype("<u4").tobytes()) == crc
         assert np.array_equal(back[0], f)
+
+
+def _device_step(be, slots, toks):
+    v = be.vocab
+    d_s = hip.DeviceBuffer.from_array(np.array(slots, np.uint32))
+    d_t = hip.DeviceBuffer.from_array(np.array(toks, np.uint32))
+    d_o = hip.DeviceBuffer(len(slots) * v * 4)
+    try:
+        be.forward_batch_device(len(slots), d_s.ptr, d_t.ptr, d_o.ptr)
+        status = be.device_status()
+        return status, d_o.download(np.float32, len(slots) * v).reshape(len(slots), v)
+    finally:
+        for b in (d_s, d_t, d_o):
+            b.close()
+
+
+@pytest.mark.parametrize("profile", [ffi.PROFILE_Q8_ROW, A8, REF])
+def test_device_check_contains_bad_entries(models, profile):
+    """RWKV-7 through forward_batch_device (matrix-core int8, W8A8 and F32 reference-order
+    tiers): a valid call equals forward_batch bit for bit; a call with a repeated slot and a
+    bad token reports INVALID_ARGUMENT, leaves the slots it does not name untouched, and
+    advances its valid entries exactly as a valid call would."""
+    d, h = SMALL.d_model, SMALL.d_model // 64
+    with ffi.PluginBackend(models["small"], profile=profile) as be:
+        v = be.vocab
+        be.batch_init(8)
+        state = lambda s: [be.get_rwkv_state(s, l, d, h) for l in range(SMALL.n_layer)]
+        first = [(13 * i + 5) % v for i in range(8)]
+
+        def start():
+            be.batch_reset(None)
+            st, out = _device_step(be, [7, 6, 5, 4, 0, 1, 2, 3], first)
+            assert st == ffi.BackendResult.OK
+            return out
+
+        dev = start()
+        be.batch_reset(None)
+        host = np.empty((8, v), np.float32)
+        be.forward_batch([7, 6, 5, 4, 0, 1, 2, 3], first, host)
+        assert np.array_equal(bits(dev), bits(host))
+        start()
+        snap = {s: state(s) for s in range(8)}
+        st, dup = _device_step(be, [7, 6, 7, 4, 2], [9, 8, 7, 6, v + 3])
+        assert st == ffi.BackendResult.INVALID_ARGUMENT
+        for s in (0, 1, 2, 3, 5):
+            for a, b in zip(snap[s], state(s)):
+                for x, y in zip(a, b):
+                    assert np.array_equal(bits(x), bits(y)), s
+        after = {s: state(s) for s in (7, 6, 4)}
+        start()
+        st, ok = _device_step(be, [7, 6, 4], [9, 8, 6])
+        assert st == ffi.BackendResult.OK
+        for pos_dup, pos_ok in ((0, 0), (1, 1), (3, 2)):
+            assert np.array_equal(bits(dup[pos_dup]), bits(ok[pos_ok])), pos_dup
+        for s in (7, 6, 4):
+            for a, b in zip(after[s], state(s)):
+                for x, y in zip(a, b):
+                    assert np.array_equal(bits(x), bits(y)), s
