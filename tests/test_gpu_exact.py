@@ -89,6 +89,22 @@ def test_exact_tier_wide_batch(small, profile, contract):
     check_bitwise(small["base"], SMALL["base"], profile, contract, n=37, steps=3, slots=slots, seed=11)
 
 
+def test_exact_tier_probability_vector(small):
+    # forward_batch_probs on the reference-order tier: the shared softmax of bit-identical
+    # logits, within the probability tolerance of the oracle's softmax
+    path, dims = small["base"], SMALL["base"]
+    with ffi.PluginBackend(path, profile=1 | EXACT | FMA) as be:
+        orc = O.MambaOracle(path, 1 | O.ORC_PROFILE_FMA, cap=6)
+        be.batch_init(6)
+        for t in range(3):
+            toks = [(s * 41 + t * 17 + 2) % dims.vocab for s in range(6)]
+            g = np.empty((6, dims.vocab), np.float32)
+            be.forward_batch(list(range(6)), toks, g, probs=True)
+            ref = np.stack([O.softmax(r) for r in orc.forward(list(range(6)), toks)])
+            assert float(np.max(np.abs(g - ref).sum(axis=-1))) <= 1e-4
+        orc.close()
+
+
 def test_exact_tier_long_horizon(small):
     # 8 streams for 600 steps, int8 groups of 64 in contract 2: every logit of every step
     # and the final state bit for bit (no drift however long the recurrence runs)
@@ -130,8 +146,10 @@ def test_exact_tier_v1_and_batch_and_reset(small):
             assert np.array_equal(bits(g[1]), bits(want[i])), ("batch", i)
 
 
-@pytest.mark.parametrize("profile,contract", [(0, 1), (1, 2), (6, 1)])
-def test_archive_coded_on_cpu_decodes_on_gpu(small, oracle_plugin, profile, contract):
+@pytest.mark.parametrize("profile,contract,device_cdf", [(0, 1, False), (1, 2, False), (1, 2, True), (6, 1, False)])
+def test_archive_coded_on_cpu_decodes_on_gpu(small, oracle_plugin, profile, contract, device_cdf):
+    # device_cdf: the GPU side also builds each step's CDF on the device (the same bits as
+    # the host's CDF of the same logits)
     path, dims = small["base"], SMALL["base"]
     rng = np.random.default_rng(17 + profile)
     files = [synth.zipf_tokens(rng, dims.vocab, (k,)).astype(np.uint32) for k in (90, 1, 33, 140)]
@@ -139,7 +157,7 @@ def test_archive_coded_on_cpu_decodes_on_gpu(small, oracle_plugin, profile, cont
     print(f"cross-device round trip profile {profile} contract {contract}", flush=True)
     with Lockstep(path, plugin_path=oracle_plugin, profile=prof, slots=3) as cpu:
         cpu_bytes, _ = cpu.compress(files, reset_every=64)
-    with Lockstep(path, profile=prof | EXACT, slots=3, device_cdf=False) as gpu:
+    with Lockstep(path, profile=prof | EXACT, slots=3, device_cdf=device_cdf) as gpu:
         gpu_bytes, _ = gpu.compress(files, reset_every=64)
         assert gpu_bytes == cpu_bytes, "the GPU codes other bytes than the CPU"
         back, _ = gpu.decompress(cpu_bytes, [len(f) for f in files], reset_every=64)
