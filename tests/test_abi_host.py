@@ -41,6 +41,23 @@ def test_header_declares_reference_symbols():
     assert len(syms) == len(ffi.V1_SYMBOLS + ffi.V2_SYMBOLS + ffi.V3_SYMBOLS)
 
 
+def test_profile_bits_match_the_header():
+    """Every weight-profile bit the header defines has the same value in the Python mirror,
+    and the oracle's profile constants agree with both."""
+    from oracle import oracle as O
+
+    text = open(HEADER).read()
+    defs = {k: int(v) for k, v in re.findall(r"#define BACKEND_PROFILE_(\w+) (\d+)u", text)}
+    assert len(defs) == 9
+    for name, value in defs.items():
+        assert getattr(ffi, "PROFILE_" + name) == value, name
+    for name in ("EXACT", "FMA"):
+        assert getattr(O, "ORC_PROFILE_" + name) == defs[name], name
+    orc = dict(re.findall(r"ORC_PROFILE_(\w+) = (\d+)", open(os.path.join(ROOT, "oracle", "oracle.h")).read()))
+    for name in ("F32", "Q8_G64", "Q8_ROW", "Q8_SMALL", "W8A8", "EXACT", "FMA"):
+        assert int(orc[name]) == defs[name], name
+
+
 def test_library_exports_every_declared_symbol(raw_lib):
     for s in declared_symbols():
         assert hasattr(raw_lib, s), f"missing export {s}"
