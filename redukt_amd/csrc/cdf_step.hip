@@ -397,9 +397,14 @@ __global__ __launch_bounds__(kCdfBlock) void k_cdf_freq_parts(CdfArgs a) {
     }
 }
 
+// LDS index of a chunk position: one pad word per 32, so that both the coalesced pass
+// (thread t at t + 256 j) and the per-thread pass (thread t at 16 t + j) meet no bank
+// conflicts.
+__device__ __forceinline__ uint32_t pad_ix(uint32_t p) { return p + p / 32; }
+
 __global__ __launch_bounds__(kCdfBlock) void k_cdf_freq_write(CdfArgs a) {
     __shared__ uint32_t sh[kCdfBlock / 64];
-    __shared__ uint32_t stage[kChunk];   // the chunk's cumulative frequencies, stored out coalesced
+    __shared__ uint32_t lfq[kChunk + kChunk / 32];   // the chunk's frequencies, then its cumulative ones
     const uint32_t c = blockIdx.x, row = blockIdx.y, n = a.n;
     const FreqRow f = freq_row(a, row);
     const ChunkPart* pr = a.part + (size_t)row * a.chunks;
@@ -416,20 +421,25 @@ __global__ __launch_bounds__(kCdfBlock) void k_cdf_freq_write(CdfArgs a) {
     if (diff != 0 && at < c0) offset = (uint32_t)((int64_t)offset + diff);   // u32 wrap, as the host's sum
     const double* e = a.e + (size_t)row * n;
     uint32_t* cdf = a.cdf + (size_t)row * (n + 1);
-    // thread t: kSpan consecutive elements; exclusive scan of the thread totals
-    const uint32_t i0 = c0 + threadIdx.x * kSpan;
-    uint32_t fq[kSpan];
-    uint32_t mine = 0;
+    // the chunk's frequencies, read coalesced (element c0 + t + 256 j)
 #pragma unroll
     for (uint32_t j = 0; j < kSpan; j++) {
-        const uint32_t i = i0 + j;
+        const uint32_t p = threadIdx.x + kCdfBlock * j, i = c0 + p;
         uint32_t v = 0;
         if (i < n) {
             v = 1u + (uint32_t)extra_of(e[i], f);
             if (diff != 0 && i == at) v = (uint32_t)((int64_t)v + diff);
         }
-        fq[j] = v;
-        mine += v;
+        lfq[pad_ix(p)] = v;
+    }
+    __syncthreads();
+    // thread t: kSpan consecutive elements; exclusive scan of the thread totals
+    uint32_t fq[kSpan];
+    uint32_t mine = 0;
+#pragma unroll
+    for (uint32_t j = 0; j < kSpan; j++) {
+        fq[j] = lfq[pad_ix(threadIdx.x * kSpan + j)];
+        mine += fq[j];
     }
     const int lane = threadIdx.x % 64, w = threadIdx.x / 64;
     uint32_t incl = mine;
@@ -448,10 +458,10 @@ __global__ __launch_bounds__(kCdfBlock) void k_cdf_freq_write(CdfArgs a) {
 #pragma unroll
     for (uint32_t j = 0; j < kSpan; j++) {
         cum += fq[j];
-        stage[threadIdx.x * kSpan + j] = cum;
+        lfq[pad_ix(threadIdx.x * kSpan + j)] = cum;   // each thread rewrites only its own positions
     }
     __syncthreads();
-    for (uint32_t r = threadIdx.x; r < kChunk && c0 + r < n; r += kCdfBlock) cdf[c0 + r + 1] = stage[r];
+    for (uint32_t r = threadIdx.x; r < kChunk && c0 + r < n; r += kCdfBlock) cdf[c0 + r + 1] = lfq[pad_ix(r)];
 }
 
 }  // namespace
