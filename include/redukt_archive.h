@@ -62,14 +62,19 @@ uint32_t redukt_crc32_update(uint32_t state, const uint8_t* data, size_t len);
 uint32_t redukt_crc32(const uint8_t* data, size_t len);
 
 /* Fills *h with the reference writer's defaults: v5, fmath-v1, default hyperparameters,
- * no preprocessing, the given backbone, quant and reset period. */
+ * no preprocessing, the given backbone, quant and reset period, resolved as the reference
+ * compressor resolves them (codec.rs:140-147, 694-717): quant is kept for the Mamba family
+ * only (RWKV and the GPU plugin write F32: a plugin's own quantisation is part of its
+ * configuration, not of the archive), and RWKV gets no reset period. */
 void redukt_rdkt_default_header(redukt_rdkt_header* h, uint32_t total_bytes, uint8_t backbone, uint8_t quant,
                                 uint8_t reset_log2);
 
 /* Writes the v5 header of *h into out (capacity cap); *len receives its size (also when
  * it does not fit, with REDUKT_CODEC_BUFFER_TOO_SMALL).  INVALID_ARG, with a message in
- * err, for an unknown quant / contract / backbone, a RESET_LOG2 outside 8..20 or the
- * fma-v1 contract on a backbone outside the Mamba family. */
+ * err, for an unknown quant / contract / backbone, a RESET_LOG2 outside 8..20, the
+ * fma-v1 contract on a backbone outside the Mamba family, a non-F32 quant outside the
+ * Mamba family, or a reset period on RWKV: headers the reference decoder would refuse or
+ * that its compressor never writes. */
 int32_t redukt_rdkt_build_header(const redukt_rdkt_header* h, uint8_t* out, size_t cap, size_t* len, char* err,
                                  size_t err_cap);
 
@@ -81,6 +86,12 @@ int32_t redukt_rdkt_validate_magic(const uint8_t* data, size_t len, uint8_t* ver
  * non-finite hyperparameters) returns INVALID_ARG with the reason in err. */
 int32_t redukt_rdkt_parse_header(const uint8_t* data, size_t len, redukt_rdkt_header* h, char* err,
                                  size_t err_cap);
+
+/* resolve_decompress_profile (codec.rs:719-741) without a --quant override: the weight
+ * profile a decoder takes from the header.  INVALID_ARG for a non-F32 profile on any
+ * backbone outside the Mamba family (RWKV, the GPU plugin), as the reference refuses it
+ * ("only Mamba supports profiles"); else *quant receives the header's quant. */
+int32_t redukt_rdkt_decode_profile(const redukt_rdkt_header* h, uint8_t* quant, char* err, size_t err_cap);
 
 /* extract_stream_and_crc_v: the stream is data[*stream_off .. *stream_off + *stream_len);
  * for v3+ the trailing 4 bytes are the stored CRC (*has_crc = 1). */

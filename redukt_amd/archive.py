@@ -53,7 +53,10 @@ class Header:
 
     @property
     def reset_every(self) -> int:
-        return 0 if self.reset_log2 == 0 else 1 << self.reset_log2
+        """The period a decoder replays: RWKV ignores any period (model_loader.rs:121-128)."""
+        if self.reset_log2 == 0 or self.backbone == BACKBONE_RWKV:
+            return 0
+        return 1 << self.reset_log2
 
     def _to_c(self) -> _Header:
         c = _Header()
@@ -88,6 +91,8 @@ def _lib():
             "redukt_rdkt_validate_magic": (ctypes.c_int32, [u8p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_uint8),
                                                             ctypes.c_char_p, ctypes.c_size_t]),
             "redukt_rdkt_parse_header": (ctypes.c_int32, [u8p, ctypes.c_size_t, hp, ctypes.c_char_p, ctypes.c_size_t]),
+            "redukt_rdkt_decode_profile": (ctypes.c_int32, [hp, ctypes.POINTER(ctypes.c_uint8), ctypes.c_char_p,
+                                                            ctypes.c_size_t]),
             "redukt_rdkt_split": (ctypes.c_int32, [u8p, ctypes.c_size_t, ctypes.c_uint32, ctypes.c_uint8,
                                                    ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t),
                                                    ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(ctypes.c_uint8)]),
@@ -147,6 +152,17 @@ def parse_header(data: bytes) -> Header:
     return Header._from_c(c)
 
 
+def decode_profile(h: Header) -> int:
+    """The weight profile a decoder takes from the header (resolve_decompress_profile,
+    codec.rs:719-741): refuses a non-F32 profile outside the Mamba family."""
+    c = h._to_c()
+    q = ctypes.c_uint8(0)
+    err = ctypes.create_string_buffer(256)
+    if _lib().redukt_rdkt_decode_profile(ctypes.byref(c), ctypes.byref(q), err, 256) != 0:
+        raise ArchiveError(err.value.decode())
+    return int(q.value)
+
+
 def split(data: bytes, header_size: int, version: int) -> Tuple[bytes, Optional[int]]:
     """(stream, stored CRC or None for v2)."""
     a, p = _buf(data)
@@ -163,6 +179,9 @@ def pack(header: Header, stream: bytes, payload: bytes) -> bytes:
 
 
 def unpack(data: bytes) -> Tuple[Header, bytes, Optional[int]]:
+    """Header, stream and stored CRC of an archive a decoder accepts: the header parsed,
+    its weight profile resolved for decoding (non-F32 outside the Mamba family refused)."""
     h = parse_header(data)
+    decode_profile(h)
     stream, crc = split(data, h.header_size, h.version)
     return h, stream, crc

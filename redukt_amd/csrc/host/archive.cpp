@@ -117,9 +117,12 @@ extern "C" void redukt_rdkt_default_header(redukt_rdkt_header* h, uint32_t total
     h->has_crc = 1;
     h->total_bytes = total_bytes;
     h->backbone = backbone;
-    h->quant = quant;
+    // resolve_compress_profile (codec.rs:706-717): only the Mamba family records a weight
+    // profile; RWKV and the GPU plugin always write F32, whatever their own quantisation.
+    h->quant = mamba_family(backbone) ? quant : 0;
     h->contract = 1;  // fmath-v1: the exp of every CDF (NumericContract::CURRENT)
-    h->reset_log2 = reset_log2;
+    // resolve_reset_log2 (codec.rs:140-147, 694-703): RWKV never resets.
+    h->reset_log2 = backbone == REDUKT_RDKT_BACKBONE_RWKV ? 0 : reset_log2;
 }
 
 extern "C" int32_t redukt_rdkt_build_header(const redukt_rdkt_header* h, uint8_t* out, size_t cap, size_t* len,
@@ -134,6 +137,12 @@ extern "C" int32_t redukt_rdkt_build_header(const redukt_rdkt_header* h, uint8_t
                     kResetMax);
     if (h->emb_method > 3) return fail(err, err_cap, "unknown emb-surgery method %u", h->emb_method);
     if (int32_t rc = check_contract(h->contract, h->backbone, err, err_cap)) return rc;
+    if (h->quant && !mamba_family(h->backbone))
+        return fail(err, err_cap,
+                    "backbone %u records no weight profile (only the Mamba family does); its archives carry F32",
+                    h->backbone);
+    if (h->reset_log2 && h->backbone == REDUKT_RDKT_BACKBONE_RWKV)
+        return fail(err, err_cap, "RWKV archives carry no reset period (RWKV never resets its state)");
 
     const bool custom_hp = f32_bits(h->bias_lr) != f32_bits(kDefaultBiasLr) ||
                            f32_bits(h->ngram_scale) != f32_bits(kDefaultNgramScale) ||
@@ -313,5 +322,17 @@ extern "C" int32_t redukt_rdkt_split(const uint8_t* data, size_t len, uint32_t h
     *stream_len = payload - 4;
     if (crc) *crc = rd_u32(data + len - 4);
     if (has_crc) *has_crc = 1;
+    return REDUKT_CODEC_OK;
+}
+
+extern "C" int32_t redukt_rdkt_decode_profile(const redukt_rdkt_header* h, uint8_t* quant, char* err, size_t err_cap) {
+    // resolve_decompress_profile with no --quant override (codec.rs:719-741).
+    if (!h) return fail(err, err_cap, "null header");
+    if (!mamba_family(h->backbone) && h->quant != 0)
+        return fail(err, err_cap,
+                    "version-%u archive gives backbone %u the weight profile %s; only Mamba backbones carry a "
+                    "profile other than F32",
+                    h->version, h->backbone, h->quant == 1 ? "Q8" : "?");
+    if (quant) *quant = h->quant;
     return REDUKT_CODEC_OK;
 }

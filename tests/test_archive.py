@@ -295,5 +295,43 @@ def test_plugin_archive_defaults_and_pack():
     hh, stream, crc = A.unpack(file)
     assert stream == b"\x01\x02\x03" and crc == A.crc32(payload)
     assert (hh.backbone, hh.quant, hh.contract, hh.reset_every, hh.header_size) == (3, 0, 1, 4096, len(raw))
+    # resolve_compress_profile (codec.rs:706-717): the plugin's own int8 weights are part of
+    # its configuration, not of the archive; asking for Q8 still writes PROFILE 0x50
     q8 = A.build_header(A.default_header(1, A.BACKBONE_PLUGIN, 1, 12))
-    assert q8[13] == 0x51
+    assert q8 == MAGIC_V5 + struct.pack("<I", 1) + bytes([0x40, 0x50, 12, 3])
+    assert A.build_header(A.default_header(1, A.BACKBONE_PLUGIN, 0, 0))[13] == 0x10
+    # RWKV: PROFILE 0x10, no reset byte, no backbone byte (FORMAT-SPEC.md:224-226)
+    rw = A.build_header(A.default_header(77, A.BACKBONE_RWKV, 1, 12))
+    assert rw == MAGIC_V5 + struct.pack("<I", 77) + bytes([0x00, 0x10])
+    assert A.unpack(A.pack(A.default_header(77, A.BACKBONE_RWKV, 1, 12), b"", b"x"))[0].reset_every == 0
+    # the Mamba family keeps its profile
+    assert A.build_header(A.default_header(1, A.BACKBONE_MAMBA, 1, 12))[13] == 0x51
+
+
+def test_writer_refuses_what_the_reference_never_writes():
+    with pytest.raises(A.ArchiveError, match="no weight profile"):
+        A.build_header(A.Header(total_bytes=10, backbone=A.BACKBONE_PLUGIN, quant=1, reset_log2=12))
+    with pytest.raises(A.ArchiveError, match="no weight profile"):
+        A.build_header(A.Header(total_bytes=10, backbone=A.BACKBONE_RWKV, quant=1, reset_log2=0))
+    with pytest.raises(A.ArchiveError, match="no reset period"):
+        A.build_header(A.Header(total_bytes=10, backbone=A.BACKBONE_RWKV, reset_log2=12))
+
+
+@pytest.mark.parametrize("backbone,byte", [(A.BACKBONE_PLUGIN, 0x51), (A.BACKBONE_PLUGIN, 0x11),
+                                           (A.BACKBONE_RWKV, 0x11), (A.BACKBONE_RWKV, 0x01)])
+def test_non_f32_profile_outside_mamba_is_refused_on_decode(backbone, byte):
+    """resolve_decompress_profile (codec.rs:719-741, test at :3202-3212): a Q8 PROFILE on the
+    plugin or RWKV backbone parses but is refused before decoding."""
+    reset = 12 if byte & 0x40 else 0
+    h = bytearray(A.build_header(A.default_header(10, backbone, 0, reset)))
+    h[13] = byte  # what a writer outside these rules would put there
+    f = with_payload(bytes(h))
+    hp = A.parse_header(f)  # the header itself is well formed
+    assert (hp.backbone, hp.quant) == (backbone, 1)
+    with pytest.raises(A.ArchiveError, match="only Mamba backbones carry a profile"):
+        A.decode_profile(hp)
+    with pytest.raises(A.ArchiveError, match="only Mamba backbones carry a profile"):
+        A.unpack(f)
+    # the same byte on a Mamba backbone decodes as Q8
+    m = bytearray(A.build_header(A.default_header(10, A.BACKBONE_MAMBA, 1, 12)))
+    assert A.decode_profile(A.parse_header(with_payload(bytes(m)))) == 1

@@ -102,11 +102,14 @@ def test_mamba130m_lockstep_roundtrip(full_model):
 
 @pytest.mark.parametrize("reset_log2,lengths", [(12, (70, 33, 1, 90)), (8, (600, 260, 300, 513, 257))])
 def test_mamba130m_rdkt_v5_archives(full_model, reset_log2, lengths):
-    """GPU lockstep streams in RDKT v5 archives (src/application/codec.rs:540-580, 648-720):
-    HEADER (BACKBONE 3 = plugin, PROFILE 0x51 = int8 weights, RESET_LOG2) | STREAM |
-    CRC-32 of the original data.  Each archive is parsed and split, its CRC checked against
-    the decoded data, and the stream decoded back (the period read from the header) to the
-    original tokens byte for byte.  At RESET_LOG2 8 the files cross resets."""
+    """GPU lockstep streams in RDKT v5 archives (src/application/codec.rs:540-580, 648-741):
+    HEADER (BACKBONE 3 = plugin, PROFILE 0x50, RESET_LOG2) | STREAM | CRC-32 of the
+    original data.  The plugin's int8 weights are its configuration (REDUKT_GPU_PROFILE),
+    not part of the archive: the reference writes QUANT = F32 for every plugin archive and
+    refuses any other (FORMAT-SPEC.md:224-240).  Each archive is parsed and split, its CRC
+    checked against the decoded data, and the stream decoded back by the same plugin
+    configuration (the period read from the header) to the original tokens byte for byte.
+    At RESET_LOG2 8 the files cross resets."""
     files = token_files(50280, lengths, 10 + reset_log2)
     reset_every = 1 << reset_log2
     with Lockstep(full_model, profile=Q8ROW_ALL, slots=4) as ls:
@@ -114,15 +117,15 @@ def test_mamba130m_rdkt_v5_archives(full_model, reset_log2, lengths):
     arcs = []
     for f, stm in zip(files, streams):
         payload = f.astype("<u4").tobytes()
-        h = archive.default_header(len(payload), backbone=archive.BACKBONE_PLUGIN, quant=1, reset_log2=reset_log2)
+        h = archive.default_header(len(payload), backbone=archive.BACKBONE_PLUGIN, quant=0, reset_log2=reset_log2)
         arc = archive.pack(h, stm, payload)
-        assert arc[:4] == b"RDKT" and arc[4] == 5
+        assert arc[:4] == b"RDKT" and arc[4] == 5 and arc[12:16] == bytes([0x40, 0x50, reset_log2, 3])
         arcs.append(arc)
     # decode side: header -> period and length, stream -> tokens, CRC of the restored data
     heads, body = [], []
     for arc in arcs:
         h, stm, crc = archive.unpack(arc)
-        assert h.version == 5 and h.backbone == archive.BACKBONE_PLUGIN and h.quant == 1
+        assert h.version == 5 and h.backbone == archive.BACKBONE_PLUGIN and h.quant == 0
         assert h.reset_log2 == reset_log2 and h.has_crc and crc is not None
         heads.append((h, crc))
         body.append(stm)

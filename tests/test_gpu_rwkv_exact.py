@@ -30,7 +30,6 @@ REF = ffi.PROFILE_EXACT
 # tier: (library profile, oracle profile, backend name)
 TIERS = {"w8a8": (A8, A8, "hip-gfx950-rwkv7-w8a8"), "f32-ref": (REF, 0, "hip-gfx950-rwkv7-f32-ref")}
 # the RDKT header's weight-profile code of each tier (the reference's RWKV-7 Q8 is W8A8)
-QUANT_CODE = {A8: 1, REF: 0}
 SMALL = rwkv.RwkvDims(vocab=300, d_model=128, n_layer=2, head_size=64, d_ffn=256, lora_w=16, lora_a=16,
                       lora_v=8, lora_g=32)
 
@@ -243,9 +242,12 @@ def test_reference_order_init_rules(models):
 def test_archives_cross_devices(models, oracle_plugin, tier):
     """Lockstep coding of several files (crossing reset boundaries) on the CPU oracle and on
     the GPU gives the same bytes, each side decodes the other's, and GPU streams packed
-    into RDKT v5 archives of the RWKV-7 backbone (BACKBONE 0, PROFILE from the tier,
-    RESET_LOG2 8) decode on the CPU with the weight profile taken from the header and the
-    restored data's CRC-32 (src/application/codec.rs:540-580, 648-720)."""
+    into RDKT v5 archives of the RWKV-7 backbone decode on the CPU with the restored data's
+    CRC-32 (src/application/codec.rs:540-580, 648-741).  Those archives are what the
+    reference writes for RWKV (FORMAT-SPEC.md:224-240): BACKBONE 0, PROFILE 0x10 (RWKV's
+    quantisation is not part of the format: both ends run the same configuration) and no
+    reset period (RWKV never resets, model_loader.rs:121-128), so their streams are coded
+    without resets."""
     prof, oprof, _ = tier
     path = models["g1k"]
     rng = np.random.default_rng(9 + prof)
@@ -259,13 +261,16 @@ def test_archives_cross_devices(models, oracle_plugin, tier):
         back, _ = gpu.decompress(cpu_bytes, [len(f) for f in files], reset_every=256)
     for f, b in zip(files, back):
         assert np.array_equal(f, b)
-    for f, stm in zip(files, gpu_bytes):
+    with Lockstep(path, profile=prof, slots=3) as gpu:
+        arc_streams, _ = gpu.compress(files, reset_every=0)
+    for f, stm in zip(files, arc_streams):
         payload = f.astype("<u4").tobytes()
-        h = archive.default_header(len(payload), backbone=archive.BACKBONE_RWKV, quant=QUANT_CODE[prof], reset_log2=8)
-        hd, body, crc = archive.unpack(archive.pack(h, stm, payload))
-        assert (hd.backbone, hd.quant, hd.contract, hd.reset_every) == (archive.BACKBONE_RWKV, QUANT_CODE[prof], 1, 256)
-        cpu_profile = A8 if hd.quant == 1 else 0
-        with Lockstep(path, plugin_path=oracle_plugin, profile=cpu_profile, slots=1) as cpu:
+        h = archive.default_header(len(payload), backbone=archive.BACKBONE_RWKV, quant=0, reset_log2=0)
+        arc = archive.pack(h, stm, payload)
+        assert arc[12:14] == bytes([0x00, 0x10])
+        hd, body, crc = archive.unpack(arc)
+        assert (hd.backbone, hd.quant, hd.contract, hd.reset_every) == (archive.BACKBONE_RWKV, 0, 1, 0)
+        with Lockstep(path, plugin_path=oracle_plugin, profile=oprof, slots=1) as cpu:
             back, _ = cpu.decompress([body], [hd.total_bytes // 4], reset_every=hd.reset_every)
         assert archive.crc32(back[0].astype("<u4").tobytes()) == crc
         assert np.array_equal(back[0], f)
