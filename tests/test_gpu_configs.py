@@ -7,12 +7,13 @@ seeded weights and tokens: max |logit error| <= 1e-3 and probability-vector L1 <
 * Mamba-130M F32, one stream, 1024 tokens through the v1 entry point
   (redukt_backend_forward), compared at every token: recurrent-state drift over the
   whole horizon.
-* Mamba-130M int8 per-row, 32 lockstep streams, 256 steps, every step compared.
+* Mamba-130M int8 per-row, 32 lockstep streams, 256 steps, every step compared, on the
+  matrix-core tier and on the wavefront-GEMV tier.
 * Mamba-130M F32, 128 streams, probability vector through forward_batch_probs
   (softmax_into, src/domain/tensor.rs:1917-1933), every row; one stream alone equals the
   same stream inside the 128-stream batch, bit for bit (PLUGIN-FFI-V2.md:97-101).
 * Mamba-130M int8 per-row, 1024 streams, every row; one stream's bits alone == in the
-  batch.
+  batch; on both tiers.
 * RWKV-7 0.1B at its real vocabulary (65,536), 64 streams, F32 and int8 weight-only.
 """
 import numpy as np
@@ -64,11 +65,16 @@ def test_mamba130m_f32_single_stream_1024_tokens(full_model):
     print(f"Mamba-130M F32 v1, {n_tok} tokens: worst max|dlogit|={worst[0]:.3e} L1={worst[1]:.3e}")
 
 
-def test_mamba130m_q8_32_streams_256_steps(full_model):
+TIERS = [pytest.param(0, id="matrix-core"), pytest.param(ffi.PROFILE_GEMV, id="gemv")]
+
+
+@pytest.mark.parametrize("tier", TIERS)
+def test_mamba130m_q8_32_streams_256_steps(full_model, tier):
     n, steps = 32, 256
     rng = np.random.default_rng(102)
     toks = synth.zipf_tokens(rng, 50280, (steps, n))
-    with ffi.PluginBackend(full_model, profile=Q8ROW_ALL) as be:
+    print(f"int8 per-row, {n} streams x {steps} steps, tier bits {tier}", flush=True)
+    with ffi.PluginBackend(full_model, profile=Q8ROW_ALL | tier) as be:
         orc = O.MambaOracle(full_model, Q8ROW_ALL, cap=n)
         be.batch_init(n)
         slots = list(range(n))
@@ -133,11 +139,17 @@ def test_mamba130m_f32_128_streams_probability_vector(full_model):
     print(f"Mamba-130M F32, {n} streams, probability vector: worst L1={worst:.3e}")
 
 
-def test_mamba130m_q8_1024_streams(full_model):
+@pytest.mark.parametrize("tier", TIERS)
+def test_mamba130m_q8_1024_streams(full_model, tier):
+    """The large-batch workload (1024 streams), on the matrix-core tier and on the
+    wavefront-GEMV tier, whose projections are then 1024-column skinny GEMMs computed as
+    dot products on the vector ALUs: every row against the oracle, one stream alone equal
+    to the same stream inside the batch."""
     n = 1024
     rng = np.random.default_rng(104)
     toks = synth.zipf_tokens(rng, 50280, (2, n))
-    with ffi.PluginBackend(full_model, profile=Q8ROW_ALL) as be:
+    print(f"int8 per-row, {n} streams, tier bits {tier}", flush=True)
+    with ffi.PluginBackend(full_model, profile=Q8ROW_ALL | tier) as be:
         orc = O.MambaOracle(full_model, Q8ROW_ALL, cap=n)
         be.batch_init(n + 1)
         slots = list(range(n))
