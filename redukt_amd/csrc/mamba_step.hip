@@ -143,19 +143,51 @@ __device__ __forceinline__ int4 buf_ld_i4p(BufRsrc r, uint32_t voff, uint32_t so
 }
 __device__ __forceinline__ bf16x8 as_frag(int4 v) { return __builtin_bit_cast(bf16x8, v); }
 
+// A store of what one phase hands to the next (u, z, x_proj partials, gated tiles, the
+// residual and its pre-staged activations).  kCached: a plain store (the per-layer
+// kernels, whose consumers start after the kernel boundary).  kCoherent (sc1): written
+// through to the device's coherence point, so that a task of the persistent step kernel
+// on any XCD reads it once the producer's phase counter says it is complete.  base is
+// uniform, byte_off < 2 GiB.
+constexpr int kCoherent = 16;
+template <int AUX, class T>
+__device__ __forceinline__ void st_hand(void* base, size_t byte_off, const T& v) {
+    if constexpr (AUX == kCached) {
+        *(T*)((unsigned char*)base + byte_off) = v;
+    } else {
+        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        const BufRsrc r = buf_rsrc_any(base);
+        const int off = (int)byte_off;
+        if constexpr (sizeof(T) == 16)
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, off, 0, AUX);
+        else if constexpr (sizeof(T) == 8)
+            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), r, off, 0, AUX);
+        else if constexpr (sizeof(T) == 4)
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, off, 0, AUX);
+        else {
+            static_assert(sizeof(T) == 2, "2, 4, 8 or 16 bytes");
+            __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, v), r, off, 0, AUX);
+        }
+    }
+}
+
 // ---------------------------------------------------------------- task synchronization
 
 // A layer kernel's body runs either as a kernel of its own (NoWait: its inputs were
 // complete when it started) or as a task of the persistent step kernel (FlowWait).  There
-// the previous phase's outputs are written during the same launch by other CUs of the
-// same XCD: the task first requests everything that does not depend on them (weights,
-// scales, recurrent state), then waits for the phase counter, invalidates its CU's L1
-// and reads those outputs (sc0, kAux) from the XCD's L2, where they were written.  The
-// producers' stores were complete (s_waitcnt) before the counter was raised, and the
-// counter is read with device-scope atomics.
+// the previous phase's outputs are written during the same launch by workgroups on any
+// XCD: the task first requests everything that does not depend on them (weights, scales,
+// recurrent state), then waits for the phase counter and reads those outputs.  Every
+// layer of a step hands over through buffers of its own (written once per step), so no
+// L2 or L1 holds a line of them from before the producers wrote it: a consumer's first
+// read misses and fetches the written-through (kStAux = sc1) value from the coherence
+// point.  The producers' stores were complete (s_waitcnt) before the counter was raised,
+// and the counter is read with device-scope atomics.
 struct NoWait {
     static constexpr bool kFlow = false;
     static constexpr int kAux = kCached;
+    static constexpr int kStAux = kCached;
     __device__ __forceinline__ void wait() const {}
 };
 
@@ -164,11 +196,11 @@ struct NoWait {
 // error word and goes on, and every later wait of the launch that finds the bit set gives
 // up within 1024 polls, so every wave exits soon after a first failure.
 constexpr uint32_t kFlowSpinMax = 1u << 17;
-constexpr int kL1Bypass = 1;   // sc0: the load misses the CU's L1 and reads the XCD's L2
 
 struct FlowWait {
     static constexpr bool kFlow = true;
-    static constexpr int kAux = kL1Bypass;
+    static constexpr int kAux = kCached;
+    static constexpr int kStAux = kCoherent;
     const uint32_t* counter;   // null: nothing to wait for
     uint32_t target;
     uint32_t* err;
@@ -184,14 +216,10 @@ struct FlowWait {
                 }
             }
         }
+        // No cache maintenance follows: the lines the task reads next belong to this
+        // layer's own hand-over buffers, which no CU or XCD has read in this launch before
+        // the counter was complete (the kernel boundary invalidated what earlier steps read).
         __syncthreads();
-        // Lines of the previous phase's outputs that this CU read in an earlier layer (or
-        // that share a 128-byte line with them) must not be served from L1: invalidate
-        // the CU's L1 (work-group scope; the L2 keeps its lines, device scope would write
-        // back and drop the XCD's L2 and costs twice the step time).  Every earlier read
-        // of those lines has completed (each phase waited for the whole previous one), so
-        // no stale fill can land after this.
-        if (counter != nullptr) asm volatile("buffer_inv sc0" ::: "memory");
     }
 };
 
@@ -381,6 +409,7 @@ __device__ __forceinline__ void ssp_reduce(const SspLoad& r, float* invs, int ti
 // x * w into column group b / 16 of xw and the tile's sum of x^2 for stream b into ssp
 // (sequential over the lane's four values, then xor 16, xor 32).  All lanes must call it;
 // `ok` masks the stores.
+template <int AUX = kCached>
 __device__ __forceinline__ void produce_tile(__bf16* __restrict__ xw, float* __restrict__ ssp, int ks, int tiles,
                                              int t, uint32_t b, bool ok, const float (&xv)[4], const float4& w4) {
     const int lane = threadIdx.x % kWave;
@@ -395,8 +424,8 @@ __device__ __forceinline__ void produce_tile(__bf16* __restrict__ xw, float* __r
     ss += __shfl_xor(ss, 16, kWave);
     ss += __shfl_xor(ss, 32, kWave);
     if (!ok) return;
-    write_limbs4(xw, ks, t, b, v);
-    if (lane < 16) ssp[(size_t)b * tiles + t] = ss;
+    write_limbs4<AUX>(xw, ks, t, b, v);
+    if (lane < 16) st_hand<AUX>(ssp, ((size_t)b * tiles + t) * 4, ss);
 }
 
 // Row tiles a wave multiplies together, with a ring of their next R weight k-pairs
@@ -962,7 +991,7 @@ __device__ __forceinline__ void mix_in_body(const MixInArgs& a, uint32_t bx, uin
             fE zv;
 #pragma unroll
             for (int e = 0; e < E; e++) zv[e] = v[e];
-            *(fE*)(a.z + (size_t)b * a.di + ch) = zv;
+            st_hand<SYNC::kStAux>(a.z, ((size_t)b * a.di + ch) * 4, zv);
         }
         return;
     }
@@ -1024,7 +1053,7 @@ __device__ __forceinline__ void mix_in_body(const MixInArgs& a, uint32_t bx, uin
             uv[e] = uv[e] * lane_sigmoid_f(uv[e]);
             uo[e] = uv[e];
         }
-        *(fE*)(a.u + (size_t)b * a.di + ch) = uo;
+        st_hand<SYNC::kStAux>(a.u, ((size_t)b * a.di + ch) * 4, uo);
     }
     // u as the B operand of x_proj over this block's 16 T channels (KS k-steps), past the
     // quarters: local channel c = 16 tf + r0 (+ e) of stream lane % 16 goes to k-step c / 32,
@@ -1063,8 +1092,9 @@ __device__ __forceinline__ void mix_in_body(const MixInArgs& a, uint32_t bx, uin
             f32x4 part{0, 0, 0, 0};
             part = mma_step<Q8XP>(af, lds_frag(f), lds_frag(f + 512), lds_frag(f + 1024), part);
             if (b < a.n) {
-                float* dst = a.xpart + ((size_t)(p * KS + s) * a.cap + b) * a.xr_pad + tp * kRowTile + (lane / 16) * 4;
-                *(float4*)dst = make_float4(part[0] * xs[0], part[1] * xs[1], part[2] * xs[2], part[3] * xs[3]);
+                const size_t dst = ((size_t)(p * KS + s) * a.cap + b) * a.xr_pad + tp * kRowTile + (lane / 16) * 4;
+                st_hand<SYNC::kStAux>(a.xpart, dst * 4,
+                                      make_float4(part[0] * xs[0], part[1] * xs[1], part[2] * xs[2], part[3] * xs[3]));
             }
         }
     }
@@ -1325,10 +1355,10 @@ __device__ __forceinline__ void scan_body(const ScanArgs& a, uint32_t sy, uint32
         const Limb3 t3 = split3(gv);
         const int g = b / kRowTile, sk = j / kKStep;
         const int ln = (b % kRowTile) + kRowTile * ((j % kKStep) / 8);
-        __bf16* dst = a.glimb + ((((size_t)g * (di / kKStep) + sk) * 3) * 64 + ln) * 8 + (j % 8);
-        dst[0] = t3.h;
-        dst[512] = t3.m;
-        dst[1024] = t3.l;
+        const size_t dst = ((((size_t)g * (di / kKStep) + sk) * 3) * 64 + ln) * 8 + (j % 8);
+        st_hand<SYNC::kStAux>(a.glimb, dst * 2, t3.h);
+        st_hand<SYNC::kStAux>(a.glimb, (dst + 512) * 2, t3.m);
+        st_hand<SYNC::kStAux>(a.glimb, (dst + 1024) * 2, t3.l);
     }
 }
 
@@ -1372,7 +1402,7 @@ const void* scan_fn(bool q8dt, bool fast, int dr, int nxb, uint32_t spt) {
 struct MixOutArgs {
     TMat w;                  // out_proj [d][di]
     const __bf16* glimb;     // gated limbs, B fragments
-    float* x;                // [n][d] residual, updated in place
+    float* x;                // [n][d] residual, updated in place (or written to x_out)
     uint32_t n;
     int d;
     const float* nw_next;    // next norm weight (next layer's, or the final norm's); with
@@ -1380,6 +1410,7 @@ struct MixOutArgs {
     float* ssp;              // produced here
     int ks_x, tiles;
     uint32_t gmajor = 0;     // grid (chunks, row tiles) instead of (row tiles, chunks)
+    float* x_out = nullptr;  // the updated residual's rows, when not x itself
 };
 
 // out_proj + residual.  Eight waves share one 16-row tile, each summing an eighth of the
@@ -1630,8 +1661,9 @@ __device__ __forceinline__ void mix_out_body(const MixOutArgs& a, uint32_t t_blk
         const bool ok = b < a.n && r0 < a.d;
         const float nx[4] = {xv[g].x + s[0] * rs[0], xv[g].y + s[1] * rs[1], xv[g].z + s[2] * rs[2],
                              xv[g].w + s[3] * rs[3]};
-        if (ok) *(float4*)(a.x + (size_t)b * a.d + r0) = make_float4(nx[0], nx[1], nx[2], nx[3]);
-        if (a.xw != nullptr) produce_tile(a.xw, a.ssp, a.ks_x, a.tiles, t, b, ok, nx, w4);
+        if (ok) st_hand<SYNC::kStAux>(a.x_out ? a.x_out : a.x, ((size_t)b * a.d + r0) * 4,
+                                      make_float4(nx[0], nx[1], nx[2], nx[3]));
+        if (a.xw != nullptr) produce_tile<SYNC::kStAux>(a.xw, a.ssp, a.ks_x, a.tiles, t, b, ok, nx, w4);
     }
 }
 
@@ -1644,20 +1676,24 @@ __global__ __launch_bounds__(kOutWaves * kWave) void k_mix_out(MixOutArgs a) {
 // ---------------------------------------------------------------- persistent step kernel
 
 // All layers of a step in one cooperative launch (int8 per-row weights, the Mamba-130M
-// shape).  Stream group g's every task runs on XCD g % nx (the XCD a workgroup runs on is
-// read from the hardware), so whatever one phase of a group hands to the next (activation
-// tiles and RMS partials, u, z, x_proj partials, gated tiles, the residual) is written to
-// and read from that XCD's L2.  XCD x's list is ordered by layer, then phase (in_proj,
-// scan, out_proj), then group, then the task's tile; its workgroups take the tasks in
-// list order from a ticket counter.  Every task depends only on tasks earlier in the list
-// (the previous phase of its group), and every workgroup is resident (cooperative
-// launch), so the earliest unfinished task always has its inputs and the list advances.  A task's body requests its
+// shape).  Every phase of every stream group is spread over all XCDs: task t of a
+// (layer, phase, group) runs on XCD t % nx (the XCD a workgroup runs on is read from the
+// hardware), so tile t of in_proj or out_proj reads its weights into one XCD's L2 for
+// all groups, and the groups' phases overlap on every XCD (one group's scan runs while
+// the next group's in_proj still does).  XCD x's list holds its tasks ordered by layer,
+// then phase (in_proj, scan, out_proj), then group, then tile; its workgroups take them
+// in list order from a ticket counter.  Every task depends only on tasks earlier in that
+// global order (the previous phase of its group), and every workgroup is resident
+// (cooperative launch), so the globally earliest unfinished task always has its inputs
+// and its ticket's holder reaches it: the step advances.  A task's body requests its
 // weights, scales and recurrent state, waits until the counter of the phase it reads
-// reaches that phase's task count, then reads those outputs past L1; after its stores it
-// adds one to its own phase's counter.  The bodies are the stand-alone kernels' (same
-// tiles, k-splits and orders), so a stream's bits do not depend on which path ran it.
+// reaches that phase's task count, then reads those outputs (each layer hands over
+// through buffers of its own, written through to the coherence point); after its stores
+// are complete it adds one to its own phase's counter.  The bodies are the stand-alone
+// kernels' (same tiles, k-splits and orders), so a stream's bits do not depend on which
+// path ran it.
 constexpr uint32_t kFlowCounterStride = 32;   // words between counters (one 128-byte line each)
-constexpr uint32_t kFlowMaxStreams = 4096;    // largest step the kernel serves (bounds every wait)
+constexpr uint32_t kFlowMaxStreams = 1024;    // largest step the kernel serves (bounds every wait and its buffers)
 constexpr uint32_t kFlowScanSpt = 2;          // streams per scan task thread
 
 struct FlowLayer {
@@ -1672,7 +1708,7 @@ struct FlowArgs {
     uint32_t* cnt;            // [nl][3][groups] phase counters, then [nx] task tickets, kFlowCounterStride words apart
     uint32_t* err;
     uint32_t mi_tasks, cb, mo_tasks;  // in_proj row blocks, scan channel blocks, out_proj row tiles (per group)
-    uint32_t nx;              // XCDs of the device
+    uint32_t nx;              // XCDs of the device (divides each phase's tasks per group)
     uint8_t xmap[16];         // XCC_ID -> XCD index 0 .. nx - 1 (0xff: not seen when the grid was planned)
 };
 
@@ -1698,12 +1734,13 @@ __global__ __launch_bounds__(kBlock, 2) void k_flow(FlowArgs f) {
         if (threadIdx.x == 0) atomicOr(f.err, 8u);
         return;
     }
-    const uint32_t ng = x < f.groups ? (f.groups - x + f.nx - 1) / f.nx : 0u;  // groups of this XCD
     constexpr uint32_t kSpt = kFlowScanSpt;
-    const uint32_t mi = f.mi_tasks, sc = kRowTile / kSpt * f.cb, mo = f.mo_tasks;
-    const uint32_t per_layer = ng * (mi + sc + mo);
+    const uint32_t G = f.groups, nx = f.nx;
+    // Tasks of one (layer, phase, group) on this XCD: tiles x, x + nx, ...
+    const uint32_t mi = f.mi_tasks / nx, sc = kRowTile / kSpt * f.cb / nx, mo = f.mo_tasks / nx;
+    const uint32_t per_layer = G * (mi + sc + mo);
     const uint32_t total = per_layer * f.nl;
-    uint32_t* const ticket = f.cnt + ((size_t)f.nl * 3 * f.groups + x) * kFlowCounterStride;
+    uint32_t* const ticket = f.cnt + ((size_t)f.nl * 3 * G + x) * kFlowCounterStride;
     typedef const __attribute__((address_space(4))) FlowLayer* FlowLayerK;
     const FlowLayerK layers = (FlowLayerK)f.layers;
     if (threadIdx.x == 0) s_next = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1713,33 +1750,33 @@ __global__ __launch_bounds__(kBlock, 2) void k_flow(FlowArgs f) {
         if (threadIdx.x == 0) ahead = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const uint32_t l = i / per_layer;
         uint32_t r = i % per_layer;
-        uint32_t phase, gi, task;
-        if (r < ng * mi) {
-            phase = 0, gi = r / mi, task = r % mi;
-        } else if ((r -= ng * mi) < ng * sc) {
-            phase = 1, gi = r / sc, task = r % sc;
+        uint32_t phase, g, k;
+        if (r < G * mi) {
+            phase = 0, g = r / mi, k = r % mi;
+        } else if ((r -= G * mi) < G * sc) {
+            phase = 1, g = r / sc, k = r % sc;
         } else {
-            r -= ng * sc;
-            phase = 2, gi = r / mo, task = r % mo;
+            r -= G * sc;
+            phase = 2, g = r / mo, k = r % mo;
         }
-        const uint32_t g = x + f.nx * gi;
+        const uint32_t task = x + nx * k;
         auto counter = [&](uint32_t ll, uint32_t ph) {
-            return f.cnt + ((size_t)(ll * 3 + ph) * f.groups + g) * kFlowCounterStride;
+            return f.cnt + ((size_t)(ll * 3 + ph) * G + g) * kFlowCounterStride;
         };
         const FlowLayer& L = *(const FlowLayer*)(layers + l);
         if (phase == 0) {
-            const FlowWait w{l > 0 ? counter(l - 1, 2) : nullptr, mo, f.err};
+            const FlowWait w{l > 0 ? counter(l - 1, 2) : nullptr, f.mo_tasks, f.err};
             mix_in_body<true, Q8S, true, false, kInFixedPairs, 4>(L.mi, task, g, w);
         } else if (phase == 1) {
             // kSpt streams per task: the tasks of streams past n (a last, partial group) only count
             const uint32_t sy = g * (kRowTile / kSpt) + task / f.cb;
-            const FlowWait w{counter(l, 0), mi, f.err};
+            const FlowWait w{counter(l, 0), f.mi_tasks, f.err};
             if (sy * kSpt < L.sc.n) scan_body<Q8S, FAST, 48, 48, kSpt>(L.sc, sy, task % f.cb, w);
         } else {
-            const FlowWait w{counter(l, 1), sc, f.err};
+            const FlowWait w{counter(l, 1), kRowTile / kSpt * f.cb, f.err};
             mix_out_body<true, 1, true, kWaves>(L.mo, task, g, w);
         }
-        // every store of the task has reached L2 before the counter says so
+        // every store of the task is complete at the coherence point before the counter says so
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         if (threadIdx.x == 0) {
@@ -2589,6 +2626,52 @@ const void* flow_fn(const ModelView& m) {
 size_t flow_table_bytes(uint32_t nl) { return ((size_t)nl * sizeof(FlowLayer) + 255) & ~(size_t)255; }
 // Phase counters, then one task ticket per XCC_ID value.
 uint32_t flow_counters(uint32_t nl, uint32_t n) { return nl * 3u * ((n + kRowTile - 1) / kRowTile) + 16u; }
+size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+// The hand-over buffers of one layer of the persistent step kernel, rows rounded up to
+// whole 16-stream groups, every array 256-byte aligned (so no cache line holds two
+// groups' or two arrays' data): region l holds layer l's input (the residual x and its
+// pre-staged activations xw / ssp) and what its phases pass on (u, z, the x_proj
+// partials, the gated tiles); layer l's out_proj writes region l + 1's x / xw / ssp and
+// region nl holds the head's input.
+struct FlowRegion {
+    float* x;
+    __bf16* xw;
+    float* ssp;
+    float* u;
+    float* z;
+    float* xpart;
+    __bf16* glimb;
+};
+
+size_t flow_region(const ModelView& m, uint32_t n, unsigned char* base, FlowRegion* r) {
+    const Dims& D = *m.dims;
+    const size_t groups = (n + kRowTile - 1) / kRowTile, rows = groups * kRowTile;
+    const size_t ks_x = (size_t)m.layers[0].in_x.ks, xr_pad = (size_t)m.layers[0].x_proj.rt * kRowTile;
+    const size_t sizes[7] = {rows * D.d * 4, groups * ks_x * 3 * 512 * 2, rows * (D.d / kRowTile) * 4,
+                             rows * D.di * 4, rows * D.di * 4, (D.di / kXpBlock) * rows * xr_pad * 4,
+                             groups * (D.di / kKStep) * 3 * 512 * 2};
+    size_t off = 0;
+    void* at[7];
+    for (int i = 0; i < 7; i++) {
+        at[i] = base ? base + off : nullptr;
+        off += align256(sizes[i]);
+    }
+    if (r) *r = FlowRegion{(float*)at[0], (__bf16*)at[1], (float*)at[2], (float*)at[3], (float*)at[4],
+                           (float*)at[5], (__bf16*)at[6]};
+    return off;
+}
+
+size_t flow_regions_at(uint32_t nl, uint32_t n) {
+    return align256(flow_table_bytes(nl) + (size_t)flow_counters(nl, n) * kFlowCounterStride * 4);
+}
+
+FlowRegion flow_region_of(const ModelView& m, uint32_t n, void* dev, uint32_t l) {
+    FlowRegion r;
+    const size_t one = flow_region(m, n, nullptr, nullptr);
+    flow_region(m, n, (unsigned char*)dev + flow_regions_at(m.dims->nl, n) + l * one, &r);
+    return r;
+}
 
 // Workgroups per CU of the persistent kernel: REDUKT_GPU_FLOW_WGS, else one below 512
 // streams (a second workgroup on a CU slows both: 0.87 vs 1.10 ms per step at 128
@@ -2604,7 +2687,7 @@ uint32_t flow_wgs_per_cu(uint32_t fit, uint32_t n) {
 size_t MambaStep::flow_bytes(const Pool& p, uint32_t n) const {
     (void)p;
     if (n == 0 || n > kFlowMaxStreams || !flow_fits(m)) return 0;
-    return flow_table_bytes(m.dims->nl) + (size_t)flow_counters(m.dims->nl, n) * kFlowCounterStride * 4;
+    return flow_regions_at(m.dims->nl, n) + (size_t)(m.dims->nl + 1) * flow_region(m, n, nullptr, nullptr);
 }
 
 hipError_t MambaStep::flow_init(Pool& p, uint32_t n, void* dev, FlowShape* shape, hipStream_t st) const {
@@ -2635,11 +2718,38 @@ hipError_t MambaStep::flow_init(Pool& p, uint32_t n, void* dev, FlowShape* shape
     memset(sh.xmap, 0xff, sizeof(sh.xmap));
     for (uint32_t w = 0; w < g; w++)
         if (seen[w] < 16 && sh.xmap[seen[w]] == 0xff) sh.xmap[seen[w]] = (uint8_t)sh.nx++;
-    // The per-layer argument table, for the whole step (one part).
+    // Each XCD takes the same number of tasks of every (layer, phase, group).
+    const DLayer& L0 = m.layers[0];
     const int nxb = (int)D.di / (kRowTile * 4);
+    const uint32_t tasks[3] = {(uint32_t)(nxb + L0.in_z.rt / 4), kRowTile / kFlowScanSpt * (D.di / kBlock),
+                               (uint32_t)L0.out_proj.rt};
+    if (sh.nx == 0 || tasks[0] % sh.nx || tasks[1] % sh.nx || tasks[2] % sh.nx) {
+        fprintf(stderr, "[redukt-gpu-hip] persistent step kernel off: %u XCDs do not divide the phases' tasks\n",
+                sh.nx);
+        return hipSuccess;
+    }
+    // The per-layer argument table, for the whole step (one part): layer li reads and
+    // writes its own hand-over region and leaves the next layer's input in region li + 1.
     std::vector<FlowLayer> table;
     table.reserve(D.nl);
-    for (uint32_t li = 0; li < D.nl; li++) table.push_back(layer_args(m, p, n, li, nxb));
+    const uint32_t rows = (n + kRowTile - 1) / kRowTile * kRowTile;
+    for (uint32_t li = 0; li < D.nl; li++) {
+        const FlowRegion r = flow_region_of(m, n, dev, li), next = flow_region_of(m, n, dev, li + 1);
+        Pool q = p;
+        q.x = r.x;
+        q.xw = r.xw;
+        q.ssp = r.ssp;
+        q.u = r.u;
+        q.z = r.z;
+        q.xpart = r.xpart;
+        q.glimb = r.glimb;
+        q.xcap = rows;
+        FlowLayer fl = layer_args(m, q, n, li, nxb);
+        fl.mo.x_out = next.x;
+        fl.mo.xw = next.xw;
+        fl.mo.ssp = next.ssp;
+        table.push_back(fl);
+    }
     RDK_TRY(hipMemcpy(dev, table.data(), table.size() * sizeof(FlowLayer), hipMemcpyHostToDevice));
     sh.grid = g;
     *shape = sh;
@@ -2653,8 +2763,11 @@ void MambaStep::build_flow(Pool& p, const StepIO& io, void* dev, const FlowShape
     const int d = (int)D.d, tiles = d / kRowTile, ks_x = m.layers[0].in_x.ks;
     const uint32_t groups = (n + kRowTile - 1) / kRowTile;
     uint32_t* cnt = (uint32_t*)((unsigned char*)dev + flow_table_bytes(D.nl));
+    const FlowRegion first = flow_region_of(m, n, dev, 0), last = flow_region_of(m, n, dev, D.nl);
     out.clear();
-    Launch e = embed_launch(*m.emb, p, io, m.layers[0].norm_w, p.xw, p.ssp, ks_x, tiles);
+    Pool q = p;
+    q.x = first.x;   // the embedding writes layer 0's input region
+    Launch e = embed_launch(*m.emb, q, io, m.layers[0].norm_w, first.xw, first.ssp, ks_x, tiles);
     EmbedArgs* ea = (EmbedArgs*)e.argp;
     ea->zero = cnt;
     ea->zero_n = flow_counters(D.nl, n);
@@ -2670,7 +2783,7 @@ void MambaStep::build_flow(Pool& p, const StepIO& io, void* dev, const FlowShape
     out.push_back(std::move(f));
     const TMat& H = *m.head;
     const bool ws = H.group != 0 && H.group == H.cols && H.ks / 2 <= 12;
-    out.push_back(head_launch(H, p, io, p.x, m.norm_f_w, m.norm_f_b, p.xw, p.ssp, d, tiles, ws));
+    out.push_back(head_launch(H, p, io, last.x, m.norm_f_w, m.norm_f_b, last.xw, last.ssp, d, tiles, ws));
     if (io.probs) out.push_back(softmax_launch(io.out, (int)D.vocab, n));
 }
 

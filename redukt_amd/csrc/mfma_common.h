@@ -228,6 +228,7 @@ __device__ __forceinline__ bf16x8 lds_frag(const __bf16* base) { return *(const 
 // the MFMA D layout (r0 = 16 t + 4 (lane / 16), stream b = column lane % 16), written as the
 // B operand of a following product whose k runs over those rows: buffer
 // [b / 16][k-step][3 limbs][64 lanes][8] with `ks` k-steps.
+template <int AUX = 0>
 __device__ __forceinline__ void write_limbs4(__bf16* __restrict__ buf, int ks, int t, uint32_t b, const float (&v)[4]) {
     typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
     const int lane = threadIdx.x % kWave;
@@ -242,9 +243,20 @@ __device__ __forceinline__ void write_limbs4(__bf16* __restrict__ buf, int ks, i
     const int rr = (t % 2) * kRowTile + (lane / 16) * 4;  // row within k-step t / 2
     const int ln = (int)(b % kRowTile) + kRowTile * (rr / 8);
     __bf16* dst = buf + ((((size_t)(b / kRowTile) * ks + t / 2) * 3) * 64 + ln) * 8 + rr % 8;
-    *(bf16x4*)dst = h;
-    *(bf16x4*)(dst + 512) = m;
-    *(bf16x4*)(dst + 1024) = l;
+    if constexpr (AUX == 0) {
+        *(bf16x4*)dst = h;
+        *(bf16x4*)(dst + 512) = m;
+        *(bf16x4*)(dst + 1024) = l;
+    } else {
+        // written through to the device's coherence point with cache policy AUX (the
+        // persistent step kernel's hand-over); buf is uniform and the offset < 2 GiB
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        const auto r = __builtin_amdgcn_make_buffer_rsrc(buf, (short)0, 0x7fffffff, 0x00020000);
+        const int off = (int)((dst - buf) * 2);
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, h), r, off, 0, AUX);
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, m), r, off + 1024, 0, AUX);
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, l), r, off + 2048, 0, AUX);
+    }
 }
 
 // Limbs of one value (stream b, column k) into a B-fragment buffer with `ks` k-steps.
