@@ -7,7 +7,8 @@
 // manipulation plus IEEE double adds and multiplies, one rounding each), the same
 // products and conversions.  Three things are order-dependent and are kept in order:
 //   * the two f64 sums (sum of exp, then sum of the f32 probabilities): each is one
-//     sequential chain of adds in index order, run by one lane per row (k_cdf_sums);
+//     sequential chain of adds in index order, formed exactly by one workgroup per row in
+//     integer rounds on the running sum's grid (k_cdf_sums);
 //   * the argmax of the fix-up takes the last of equal maxima, a reduction whose result
 //     does not depend on the order it is combined in;
 //   * `used` and the cumulative frequencies are integer sums (exact in any order).
@@ -181,7 +182,7 @@ __global__ __launch_bounds__(kCdfBlock) void k_cdf_exp(CdfArgs a) {
 // multiple of u = 2^(E-52), s = T u with T < 2^53, and fl(s + x) = (T + a) u with
 // a = round(x / u), as long as x / u is not a tie (fractional part exactly 1/2: then the
 // result depends on the parity of T) and T + a < 2^53 (else the result leaves the binade
-// and rounds on a coarser grid).  So a round takes 2048 terms, each thread forms a for 8
+// and rounds on a coarser grid).  So a round takes 4096 terms, each thread forms a for 4
 // of them, a block-wide prefix sum gives every T, and the first term that is a tie, a NaN,
 // or takes T to 2^53 or beyond is an event: the terms before it are added as the integer
 // sum, the event itself with one real f64 add, and the next round starts after it (on the
@@ -189,36 +190,74 @@ __global__ __launch_bounds__(kCdfBlock) void k_cdf_exp(CdfArgs a) {
 // rule.  A round without an event adds all its terms.  The result is the sequential sum
 // bit for bit (an event changes s exactly as the sequential add does; between events the
 // integer sum is exact).  The running sum of these rows stays below 2^24 (each term <= 1,
-// n < 2^24), so the grid is always finer than 1.
-constexpr uint32_t kTerms = 8;                       // terms per thread per round
-constexpr uint32_t kRound = kTerms * kCdfBlock;      // terms per round
+// n < 2^24), so the grid is always finer than 1.  The grid counts are integer-valued f64
+// (no integer conversion is a single instruction for 64 bits): a sum of non-negative
+// integers is exact whenever its result is below 2^53, and rounding is monotone, so a sum
+// that reaches 2^53 still reads as >= 2^53 - the crossing test needs no more.  Prefixes
+// are formed by adding, never by subtracting, so that this holds for each of them.
+constexpr uint32_t kSumBlock = 1024;                 // threads of a row's workgroup
+constexpr uint32_t kSumWaves = kSumBlock / 64;
+constexpr uint32_t kTerms = 4;                       // terms per thread per round
+constexpr uint32_t kRound = kTerms * kSumBlock;      // terms per round
 constexpr uint32_t kNoEvent = 0xffffffffu;
+
+// A 64-bit value moved across lanes by DPP (each 32-bit half; lanes without a source
+// read 0): a few cycles, against an LDS round trip for a lane permute.
+template <int CTRL, int ROWS = 0xf>
+__device__ __forceinline__ double dpp_f64(double v) {
+    const uint64_t b = as_u64(v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, CTRL, ROWS, 0xf, true);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), CTRL, ROWS, 0xf, true);
+    return as_f64(((uint64_t)hi << 32) | lo);
+}
+// The same value in every lane, made visibly uniform (scalar registers): the round loop's
+// control values come from LDS, and without this the compiler treats the loop as divergent
+// (exec masking, and copies of the prefetched terms that wait for their loads every round).
+__device__ __forceinline__ uint32_t uni(uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)v); }
+__device__ __forceinline__ double uni(double v) {
+    const uint64_t b = as_u64(v);
+    const uint32_t lo = uni((uint32_t)b), hi = uni((uint32_t)(b >> 32));
+    return as_f64(((uint64_t)hi << 32) | lo);
+}
+
+// Inclusive prefix sum over the wave's 64 lanes: shifts by 1, 2, 4, 8 within each row of
+// 16 lanes, then the last lane of row 0 / 2 into rows 1 / 3 and lane 31 into rows 2 and 3.
+__device__ __forceinline__ double wave_incl_sum(double v) {
+    v += dpp_f64<0x111>(v);          // row_shr:1
+    v += dpp_f64<0x112>(v);          // row_shr:2
+    v += dpp_f64<0x114>(v);          // row_shr:4
+    v += dpp_f64<0x118>(v);          // row_shr:8
+    v += dpp_f64<0x142, 0xa>(v);     // row_bcast:15 into rows 1 and 3
+    v += dpp_f64<0x143, 0xc>(v);     // row_bcast:31 into rows 2 and 3
+    return v;
+}
 
 // LDS of a round, double-buffered by round parity so that a round's writes never meet the
 // previous round's reads (two barriers per round).
 struct SumShared {
-    uint64_t part[2][kCdfBlock / 64];   // per-wave totals
-    uint32_t first[2][kCdfBlock / 64];  // per-wave first event
-    uint64_t t_ev[2][kCdfBlock / 64];   // the grid count before that event
-    double x_ev[2][kCdfBlock / 64];     // that event's term
-    double s;                           // the fallback's result
+    double part[2][kSumWaves];     // per-wave totals
+    uint32_t first[2][kSumWaves];  // per-wave first event
+    double t_ev[2][kSumWaves];     // the grid count before that event
+    double x_ev[2][kSumWaves];     // that event's term
+    double s;                      // the fallback's result
 };
 
 template <class F>
 __device__ double exact_seq_sum(const double* __restrict__ e, uint32_t n, double s, F f, SumShared& sh) {
     const uint32_t t = threadIdx.x;
     const int lane = t % 64, w = t / 64;
-    // The window's terms stay in registers (thread t: terms t kTerms .. + kTerms - 1), and
-    // the next window's loads are issued before the current one is summed.
-    double x[kTerms], xn[kTerms];
-    auto load = [&](double* dst, uint32_t k0) {
-#pragma unroll
-        for (uint32_t j = 0; j < kTerms; j++) dst[j] = e[min(k0 + t * kTerms + j, n - 1)];
-    };
-    load(x, 0);
+    // The window's terms stay in registers (thread t: terms t kTerms .. + kTerms - 1),
+    // loaded whole before the window's first round: no load is in flight inside the round
+    // loop, so no round waits for memory (a load kept in flight across rounds makes every
+    // round wait for it).
     uint32_t par = 0;
     for (uint32_t k0 = 0; k0 < n; k0 += kRound) {
-        if (k0 + kRound < n) load(xn, k0 + kRound);
+        double fx[kTerms];
+#pragma unroll
+        for (uint32_t j = 0; j < kTerms; j++) fx[j] = e[min(k0 + t * kTerms + j, n - 1)];
+#pragma unroll
+        for (uint32_t j = 0; j < kTerms; j++) fx[j] = f(fx[j]);
+        __builtin_amdgcn_s_waitcnt(0);
         // rounds over this window: after an event the rest of the window is re-gridded
         uint32_t from = 0;   // first term of the window not yet in s
         while (from < kRound && k0 + from < n) {
@@ -231,60 +270,56 @@ __device__ double exact_seq_sum(const double* __restrict__ e, uint32_t n, double
                     sh.s = s;
                 }
                 __syncthreads();
-                return sh.s;
+                return uni(sh.s);
             }
             // the grid of the current binade: terms scale by 2^ks into units of it
             int ks;
-            uint64_t top;
+            double top;
             if (s < 0x1p-1022) {
                 ks = 1074;
-                top = 1ull << 52;
+                top = 0x1p52;
             } else {
                 ks = 52 - ilogb(s);
-                top = 1ull << 53;
+                top = 0x1p53;
             }
-            const uint64_t T0 = (uint64_t)ldexp(s, ks);   // exact: s is on the grid
-            uint64_t a[kTerms];
+            const double T0 = ldexp(s, ks);   // exact and integer-valued: s is on the grid
+            double a[kTerms];
             uint32_t ev = kNoEvent;   // this thread's first event (index within the window)
-            uint64_t mine = 0;
+            double mine = 0.0;
 #pragma unroll
             for (uint32_t j = 0; j < kTerms; j++) {
                 const uint32_t r = t * kTerms + j;
-                a[j] = 0;
+                a[j] = 0.0;
                 if (r >= from && k0 + r < n) {
-                    const double q = ldexp(f(x[j]), ks);   // exact, or +inf past the double range
+                    const double q = ldexp(fx[j], ks);     // exact, or +inf past the double range
                     bool event = !(q < 0x1p53);            // NaN, inf, or certainly past the binade
                     if (!event) {
                         const double m = floor(q), fr = q - m;
                         event = fr == 0.5;
-                        a[j] = (uint64_t)m + (fr > 0.5 ? 1u : 0u);
+                        a[j] = fr > 0.5 ? m + 1.0 : m;
                     }
                     if (event) {
-                        a[j] = 0;
+                        a[j] = 0.0;
                         if (ev == kNoEvent) ev = r;
                     }
                 }
                 mine += a[j];
             }
-            // workgroup prefix of the grid counts (u64, wrapping: only values below 2^53
-            // before the first crossing are used)
-            uint64_t incl = mine;
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) {
-                const uint64_t up = __shfl_up(incl, o);
-                if (lane >= o) incl += up;
-            }
+            // workgroup prefix of the grid counts: the lane's exclusive prefix in its wave
+            // (the inclusive prefix of the lane before it), then the waves before it
+            const double incl = wave_incl_sum(mine);
             if (lane == 63) sh.part[par][w] = incl;
+            const double before = dpp_f64<0x138>(incl);   // wave_shr:1 (lane 0 reads 0)
             __syncthreads();
-            uint64_t before = incl - mine, total = 0;
+            double waves = 0.0, total = 0.0;
 #pragma unroll
-            for (int i = 0; i < kCdfBlock / 64; i++) {
-                const uint64_t p = sh.part[par][i];
-                if (i < w) before += p;
+            for (int i = 0; i < (int)kSumWaves; i++) {
+                const double p = sh.part[par][i];
+                if (i < w) waves += p;
                 total += p;
             }
             // crossings: the first term whose add takes T to the top of the binade
-            uint64_t T = T0 + before, T_ev = 0;
+            double T = (T0 + waves) + before, T_ev = 0.0;
             double x_ev = 0.0;
 #pragma unroll
             for (uint32_t j = 0; j < kTerms; j++) {
@@ -293,52 +328,56 @@ __device__ double exact_seq_sum(const double* __restrict__ e, uint32_t n, double
                 if (live && (r == ev || (r < ev && T + a[j] >= top))) {
                     ev = r;
                     T_ev = T;
-                    x_ev = x[j];
+                    x_ev = fx[j];
                     break;
                 }
                 T += a[j];
             }
-            uint32_t wev = ev;
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) wev = min(wev, (uint32_t)__shfl_xor((int)wev, o));
-            if (lane == 0) sh.first[par][w] = wev;
-            if (ev != kNoEvent && ev == wev) {
-                sh.t_ev[par][w] = T_ev;
-                sh.x_ev[par][w] = x_ev;
+            // the wave's first event sits in its lowest lane that has one (lanes hold
+            // consecutive terms)
+            const uint64_t has = __ballot(ev != kNoEvent);
+            if (lane == 0) sh.first[par][w] = kNoEvent;
+            if (has != 0) {
+                const int src = __builtin_ctzll(has);
+                if (lane == src) {
+                    sh.first[par][w] = ev;
+                    sh.t_ev[par][w] = T_ev;
+                    sh.x_ev[par][w] = x_ev;
+                }
             }
             __syncthreads();
             uint32_t first = kNoEvent;
             int fw = 0;
 #pragma unroll
-            for (int i = kCdfBlock / 64 - 1; i >= 0; i--) {
+            for (int i = (int)kSumWaves - 1; i >= 0; i--) {
                 const uint32_t v = sh.first[par][i];
                 if (v <= first) {
                     first = v;
                     fw = i;
                 }
             }
+            first = uni(first);
             if (first == kNoEvent) {
                 // no event: the window's remaining terms are the grid sum (T0 + total < 2^53)
-                s = ldexp((double)(T0 + total), -ks);
+                s = uni(ldexp(T0 + total, -ks));
                 from = kRound;
             } else {
                 // the event's add, done by every thread on the same operands
-                s = ldexp((double)sh.t_ev[par][fw], -ks) + f(sh.x_ev[par][fw]);
+                fw = (int)uni((uint32_t)fw);
+                s = uni(ldexp(sh.t_ev[par][fw], -ks) + sh.x_ev[par][fw]);
                 from = first + 1;
             }
             par ^= 1u;
         }
-#pragma unroll
-        for (uint32_t j = 0; j < kTerms; j++) x[j] = xn[j];
     }
     return s;
 }
 
-__global__ __launch_bounds__(kCdfBlock) void k_cdf_sums(CdfArgs a) {
+__global__ __launch_bounds__(kSumBlock) void k_cdf_sums(CdfArgs a) {
     __shared__ SumShared sh;
     const uint32_t row = blockIdx.x, n = a.n;
     const double* e = a.e + (size_t)row * n;
-    const double s = exact_seq_sum(e, n, 0.0, [](double v) { return v; }, sh);
+    const double s = uni(exact_seq_sum(e, n, 0.0, [](double v) { return v; }, sh));
     const double inv_sum = 1.0 / s;
     const double sp = exact_seq_sum(e, n, -0.0, [inv_sum](double v) { return (double)prob_of(v, inv_sum); }, sh);
     if (threadIdx.x == 0) {
@@ -484,7 +523,7 @@ hipError_t cdf_launch(const float* logits, uint32_t rows, uint32_t n, void* scra
     const dim3 grid(chunks, rows);
     k_cdf_max<<<grid, dim3(kCdfBlock), 0, st>>>(a);
     k_cdf_exp<<<grid, dim3(kCdfBlock), 0, st>>>(a);
-    k_cdf_sums<<<dim3(rows), dim3(kCdfBlock), 0, st>>>(a);
+    k_cdf_sums<<<dim3(rows), dim3(kSumBlock), 0, st>>>(a);
     k_cdf_freq_parts<<<grid, dim3(kCdfBlock), 0, st>>>(a);
     k_cdf_freq_write<<<grid, dim3(kCdfBlock), 0, st>>>(a);
     return hipGetLastError();
