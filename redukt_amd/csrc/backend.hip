@@ -594,7 +594,7 @@ void dev_free_all() {
 constexpr size_t kOutChunkTarget = (size_t)4 << 20;
 constexpr size_t kOutMaxChunks = 4;
 constexpr size_t kOutRoundBytes = (size_t)32 << 20;
-constexpr unsigned kCopyThreads = 8;   // the caller's thread and seven helpers
+constexpr unsigned kCopyThreadsMax = 8;   // the caller's thread and at most seven helpers
 
 bool out_stage_alloc(Pool& p, size_t out_bytes) {
     p.out_stage_bytes = std::min(kOutRoundBytes, (out_bytes + 255) & ~(size_t)255);
@@ -609,8 +609,11 @@ bool out_stage_alloc(Pool& p, size_t out_bytes) {
 }
 
 // Host threads that copy a round's chunks: one job per round, body(t) run once by each of
-// the kCopyThreads threads (t = 0 is the caller).  A job ends when every helper has
-// finished its part, so nothing of a job is touched after run() returns.
+// the threads() threads (t = 0 is the caller).  A job ends when every helper has finished
+// its part, so nothing of a job is touched after run() returns.  The helpers start on first
+// use: REDUKT_HOST_THREADS of them counting the caller (else the CPU count), at most
+// kCopyThreadsMax; a helper that cannot be started (a thread limit) leaves the job to the
+// threads that did start, down to the caller alone, so no exception leaves the library.
 class CopyPool {
 public:
     ~CopyPool() {
@@ -622,14 +625,18 @@ public:
         cv_.notify_all();
         for (auto& t : th_) t.join();
     }
-    // body(t) on each thread t in [0, kCopyThreads); false if any failed.
+    unsigned threads() {
+        if (!started_) start();
+        return 1u + (unsigned)th_.size();
+    }
+    // body(t) on each thread t in [0, threads()); false if any failed.
     bool run(const std::function<bool(unsigned)>& body) {
-        if (th_.empty())
-            for (unsigned i = 1; i < kCopyThreads; i++) th_.emplace_back([this, i] { loop(i); });
+        const unsigned nt = threads();
+        if (nt == 1) return body(0);
         {
             std::lock_guard<std::mutex> g(mu_);
             body_ = &body;
-            busy_ = kCopyThreads - 1;
+            busy_ = nt - 1;
             ok_ = true;
             ++gen_;
         }
@@ -642,6 +649,19 @@ public:
     }
 
 private:
+    void start() {
+        started_ = true;
+        unsigned want = std::thread::hardware_concurrency();
+        if (const char* e = getenv("REDUKT_HOST_THREADS"))
+            if (*e) want = (unsigned)strtoul(e, nullptr, 10);
+        want = std::max(1u, std::min(want, kCopyThreadsMax));
+        try {
+            th_.reserve(want - 1);
+            for (unsigned i = 1; i < want; i++) th_.emplace_back([this, i] { loop(i); });
+        } catch (...) {
+            // run with the helpers that started
+        }
+    }
     void loop(unsigned id) {
         uint64_t seen = 0;
         for (;;) {
@@ -663,7 +683,7 @@ private:
     std::mutex mu_;
     std::condition_variable cv_, done_;
     uint64_t gen_ = 0;
-    bool stop_ = false, ok_ = true;
+    bool stop_ = false, ok_ = true, started_ = false;
     unsigned busy_ = 0;
     const std::function<bool(unsigned)>* body_ = nullptr;
 };
@@ -850,9 +870,10 @@ bool event_wait(hipEvent_t e) {
 
 // The first `bytes` of the device array src into the caller's host buffer dst, through the
 // pool's pinned staging, a round at a time: all of a round's chunks are queued D2H (each
-// followed by its event) behind the step, then every copy thread walks the chunks in order,
-// waits for each one's event and moves its slice of the chunk into dst, while the later
-// chunks are still in flight.  Returns when every byte is in dst.
+// followed by its event) behind the step; the caller alone polls for the first chunk (which
+// lands only after the whole step), then every copy thread walks the chunks in order, waits
+// for each one's event and moves its slice of the chunk into dst, while the later chunks
+// are still in flight.  Returns when every byte is in dst.
 bool copy_out(Pool& p, void* dst, const void* src, size_t bytes) {
     for (size_t r0 = 0; r0 < bytes; r0 += p.out_stage_bytes) {
         const size_t rb = std::min(p.out_stage_bytes, bytes - r0);
@@ -866,12 +887,14 @@ bool copy_out(Pool& p, void* dst, const void* src, size_t bytes) {
                 hipEventRecord(p.out_ev[c], G.stream) != hipSuccess)
                 return false;
         }
+        if (!event_wait(p.out_ev[0])) return false;
+        const unsigned nt = copy_pool().threads();
         const bool ok = copy_pool().run([&](unsigned t) {
             for (size_t c = 0; c < chunks; c++) {
-                if (!event_wait(p.out_ev[c])) return false;
+                if (c > 0 && !event_wait(p.out_ev[c])) return false;
                 const size_t off = c * cb, len = std::min(cb, rb - off);
                 // slice t of the chunk, 64-byte aligned
-                const size_t per = ((len + kCopyThreads - 1) / kCopyThreads + 63) & ~(size_t)63;
+                const size_t per = ((len + nt - 1) / nt + 63) & ~(size_t)63;
                 const size_t s0 = std::min(len, (size_t)t * per), s1 = std::min(len, s0 + per);
                 if (s1 > s0) memcpy((unsigned char*)dst + r0 + off + s0, p.h_out + off + s0, s1 - s0);
             }
@@ -1249,7 +1272,7 @@ int32_t redukt_backend_forward_batch_cdf(uint32_t n_streams, const uint32_t* slo
     }
     void* scratch = nullptr;
     uint32_t* d_cdf = nullptr;
-    if (!cdf_space(p.cap, V, true, &scratch, &d_cdf)) return BACKEND_FORWARD_FAILED;
+    if (!cdf_space(n_streams, V, true, &scratch, &d_cdf)) return BACKEND_FORWARD_FAILED;
     memcpy(p.h_slots, slots, sizeof(uint32_t) * n_streams);
     memcpy(p.h_slots + n_streams, tokens, sizeof(uint32_t) * n_streams);
     if (hipMemcpyAsync(p.d_slots, p.h_slots, sizeof(uint32_t) * 2 * n_streams, hipMemcpyHostToDevice, G.stream) !=
