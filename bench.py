@@ -484,11 +484,16 @@ def main() -> int:
     log("per kernel class: " + json.dumps(per_class))
 
     if args.copy_calibration_mib > 0:
+        # copies of known size for scaling byte counters: the runtime's copy, then the
+        # library's probe copy with 4- and 16-byte lanes, default and streaming policy
+        # (k_copy_probe<policy, bytes per lane>, the recurrent state's shape is <2, 4>)
         nb = args.copy_calibration_mib << 20
         src, dst = hip.DeviceBuffer(nb), hip.DeviceBuffer(nb)
         hip.copy_d2d_async(dst.ptr, src.ptr, nb, stream)
+        for mode in range(4):
+            assert be.lib.lib.redukt_backend_copy_probe(dst.ptr, src.ptr, nb, mode) == 0
         hip.stream_sync(stream)
-        log(f"copy calibration: {nb} bytes device to device")
+        log(f"copy calibration: {nb} bytes device to device, runtime copy and 4 probe copies")
         src.close()
         dst.close()
 

@@ -245,6 +245,16 @@ int32_t redukt_backend_get_rwkv_state(uint32_t slot, uint32_t layer, float* x_at
 #define REDUKT_MATH_FN_COUNT 6u
 int32_t redukt_backend_eval_math(uint32_t fn, const float* x, float* y, uint32_t n);
 
+/* Measurement hook, no counterpart in the reference: copies `bytes` from device memory src
+ * to device memory dst on the library's stream (the default stream before init) with a
+ * kernel whose lanes move 4 bytes per load and store (mode bit 1 clear) or 16 (set), with
+ * the default cache policy (mode bit 0 clear) or the streaming one the recurrent state uses
+ * (set).  Hardware byte counters (FETCH_SIZE, WRITE_SIZE) read on such a copy of known
+ * size give the scale for kernels whose traffic has that shape.  Stream-ordered: returns
+ * once the copy is queued.  INVALID_ARGUMENT for a mode above 3, bytes not a multiple of
+ * 16 or not below 2^31, or a null pointer with bytes > 0. */
+int32_t redukt_backend_copy_probe(void* dst, const void* src, uint64_t bytes, uint32_t mode);
+
 #ifdef __cplusplus
 }
 #endif

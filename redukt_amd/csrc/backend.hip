@@ -1157,6 +1157,23 @@ __global__ void k_eval_math(uint32_t fn, const float* __restrict__ x, float* __r
     }
     y[i] = r;
 }
+
+// The copy of redukt_backend_copy_probe: W bytes per lane per load and store, cache policy
+// AUX (0 default, 2 streaming), a grid-stride loop over buffer descriptors of the exact size.
+template <int AUX, int W>
+__global__ __launch_bounds__(256) void k_copy_probe(const void* src, void* dst, uint32_t bytes) {
+    const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(src), (short)0, (int)bytes, 0x00020000);
+    const auto rd = __builtin_amdgcn_make_buffer_rsrc(dst, (short)0, (int)bytes, 0x00020000);
+    const uint32_t stride = gridDim.x * blockDim.x * W;
+    for (uint32_t o = (blockIdx.x * blockDim.x + threadIdx.x) * W; o < bytes; o += stride) {
+        if constexpr (W == 16)
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_amdgcn_raw_buffer_load_b128(rs, (int)o, 0, AUX), rd, (int)o,
+                                                   0, AUX);
+        else
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_amdgcn_raw_buffer_load_b32(rs, (int)o, 0, AUX), rd, (int)o,
+                                                  0, AUX);
+    }
+}
 }  // namespace
 
 extern "C" {
@@ -1435,6 +1452,18 @@ int32_t redukt_backend_eval_math(uint32_t fn, const float* x, float* y, uint32_t
     if (e == hipSuccess) e = hipMemcpy(y, d + n, bytes, hipMemcpyDeviceToHost);
     (void)hipFree(d);
     return e == hipSuccess ? BACKEND_OK : BACKEND_FORWARD_FAILED;
+}
+
+int32_t redukt_backend_copy_probe(void* dst, const void* src, uint64_t bytes, uint32_t mode) {
+    if (mode > 3 || bytes % 16 || bytes >= (1ull << 31) || (bytes && (!dst || !src))) return BACKEND_INVALID_ARGUMENT;
+    if (bytes == 0) return BACKEND_OK;
+    const hipStream_t st = G.ready ? G.stream : nullptr;
+    const uint32_t b = (uint32_t)bytes;
+    const void* fns[4] = {(const void*)k_copy_probe<0, 4>, (const void*)k_copy_probe<2, 4>,
+                          (const void*)k_copy_probe<0, 16>, (const void*)k_copy_probe<2, 16>};
+    void* args[] = {(void*)&src, (void*)&dst, (void*)&b};
+    return hipLaunchKernel(fns[mode], dim3(1024), dim3(256), args, 0, st) == hipSuccess ? BACKEND_OK
+                                                                                      : BACKEND_FORWARD_FAILED;
 }
 
 }  // extern "C"

@@ -46,7 +46,8 @@ V3_SYMBOLS = ("redukt_backend_init_ex", "redukt_backend_forward_batch_probs", "r
               "redukt_backend_device_status", "redukt_backend_stream", "redukt_backend_get_state",
               "redukt_backend_probe_kernel", "redukt_backend_probe_used", "redukt_backend_get_rwkv_state",
               "redukt_backend_eval_math", "redukt_backend_forward_batch_device_noalloc",
-              "redukt_backend_forward_batch_cdf", "redukt_backend_cdf_from_logits_device")
+              "redukt_backend_forward_batch_cdf", "redukt_backend_cdf_from_logits_device",
+              "redukt_backend_copy_probe")
 # redukt_backend_eval_math function codes: the portable element-wise functions
 MATH_FNS = {"exp": 0, "lane_exp": 1, "ln": 2, "softplus": 3, "lane_sigmoid": 4, "sigmoid": 5}
 
@@ -170,6 +171,8 @@ class PluginLibrary:
             L.redukt_backend_probe_used.restype = ctypes.c_uint32
             L.redukt_backend_eval_math.argtypes = [ctypes.c_uint32, _f32p, _f32p, ctypes.c_uint32]
             L.redukt_backend_eval_math.restype = ctypes.c_int32
+            L.redukt_backend_copy_probe.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32]
+            L.redukt_backend_copy_probe.restype = ctypes.c_int32
 
     def eval_math(self, fn: str, x: np.ndarray) -> np.ndarray:
         """One portable element-wise function evaluated on the device (test hook)."""

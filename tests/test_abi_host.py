@@ -168,6 +168,10 @@ def test_pre_init_error_paths_touch_no_device():
     assert L.redukt_backend_device_status() == ffi.BackendResult.INIT_FAILED
     assert L.redukt_backend_get_state(0, 0, None, None) == ffi.BackendResult.INIT_FAILED
     assert L.redukt_backend_stream() is None
+    # the measurement copy validates its arguments before anything reaches the GPU
+    assert L.redukt_backend_copy_probe(None, None, 0, 0) == ffi.BackendResult.OK
+    for dst, src, nbytes, mode in ((None, None, 16, 0), (1, 1, 15, 0), (1, 1, 16, 4), (1, 1, 1 << 31, 1)):
+        assert L.redukt_backend_copy_probe(dst, src, nbytes, mode) == ffi.BackendResult.INVALID_ARGUMENT
     info = ffi.BackendInfo()
     assert L.redukt_backend_init(None, 0, ctypes.byref(info)) == ffi.BackendResult.INIT_FAILED
     # bits 0-7 are defined (quant, small-matrix quant, exact scan, GEMV tier, RWKV-7 W8A8,
