@@ -195,11 +195,20 @@ __global__ __launch_bounds__(kCdfBlock) void k_cdf_exp(CdfArgs a) {
 // integers is exact whenever its result is below 2^53, and rounding is monotone, so a sum
 // that reaches 2^53 still reads as >= 2^53 - the crossing test needs no more.  Prefixes
 // are formed by adding, never by subtracting, so that this holds for each of them.
+//
+// The running sum of a row doubles about once per binade, and most of those crossings (and
+// most ties, when the terms are still close to the sum) fall in the row's first few hundred
+// terms: a round each.  So the first kHead terms are added one by one, in order, by one
+// wave, from the registers of the lanes that loaded them (real f64 adds, the sequential sum
+// itself), and the rounds start after them.
 constexpr uint32_t kSumBlock = 1024;                 // threads of a row's workgroup
 constexpr uint32_t kSumWaves = kSumBlock / 64;
 constexpr uint32_t kTerms = 4;                       // terms per thread per round
 constexpr uint32_t kRound = kTerms * kSumBlock;      // terms per round
+constexpr uint32_t kHeadLanes = 64;                  // lanes of wave 0 whose terms form the head
+constexpr uint32_t kHead = kHeadLanes * kTerms;      // terms added one by one
 constexpr uint32_t kNoEvent = 0xffffffffu;
+static_assert(kHeadLanes <= 64 && kHead <= kRound, "the head lies in wave 0's terms of the first window");
 
 // A 64-bit value moved across lanes by DPP (each 32-bit half; lanes without a source
 // read 0): a few cycles, against an LDS round trip for a lane permute.
@@ -217,6 +226,14 @@ __device__ __forceinline__ uint32_t uni(uint32_t v) { return (uint32_t)__builtin
 __device__ __forceinline__ double uni(double v) {
     const uint64_t b = as_u64(v);
     const uint32_t lo = uni((uint32_t)b), hi = uni((uint32_t)(b >> 32));
+    return as_f64(((uint64_t)hi << 32) | lo);
+}
+
+// Lane L's copy of v, in every lane (a constant lane: two scalar reads).
+__device__ __forceinline__ double lane_f64(double v, int L) {
+    const uint64_t b = as_u64(v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, L);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), L);
     return as_f64(((uint64_t)hi << 32) | lo);
 }
 
@@ -242,24 +259,53 @@ struct SumShared {
     double s;                      // the fallback's result
 };
 
+// A barrier for the rounds' LDS traffic only: LDS operations complete (lgkmcnt 0), then
+// s_barrier.  __syncthreads would also wait for every global load in flight (vmcnt 0), and
+// the next window's terms are loaded while this window's rounds run.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(0xc07f);   // vmcnt and expcnt at their maxima, lgkmcnt 0
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 template <class F>
 __device__ double exact_seq_sum(const double* __restrict__ e, uint32_t n, double s, F f, SumShared& sh) {
     const uint32_t t = threadIdx.x;
     const int lane = t % 64, w = t / 64;
-    // The window's terms stay in registers (thread t: terms t kTerms .. + kTerms - 1),
-    // loaded whole before the window's first round: no load is in flight inside the round
-    // loop, so no round waits for memory (a load kept in flight across rounds makes every
-    // round wait for it).
+    // The window's terms stay in registers (thread t: terms t kTerms .. + kTerms - 1).
+    // The next window's terms are requested before this window's first round and arrive
+    // while its rounds run; the rounds wait only for LDS.
     uint32_t par = 0;
+    double nx[kTerms];
+#pragma unroll
+    for (uint32_t j = 0; j < kTerms; j++) nx[j] = e[min(t * kTerms + j, n - 1)];
     for (uint32_t k0 = 0; k0 < n; k0 += kRound) {
         double fx[kTerms];
-#pragma unroll
-        for (uint32_t j = 0; j < kTerms; j++) fx[j] = e[min(k0 + t * kTerms + j, n - 1)];
-#pragma unroll
-        for (uint32_t j = 0; j < kTerms; j++) fx[j] = f(fx[j]);
         __builtin_amdgcn_s_waitcnt(0);
+#pragma unroll
+        for (uint32_t j = 0; j < kTerms; j++) fx[j] = f(nx[j]);
+        if (k0 + kRound < n) {
+#pragma unroll
+            for (uint32_t j = 0; j < kTerms; j++) nx[j] = e[min(k0 + kRound + t * kTerms + j, n - 1)];
+        }
         // rounds over this window: after an event the rest of the window is re-gridded
         uint32_t from = 0;   // first term of the window not yet in s
+        if (k0 == 0 && n >= kHead) {
+            // the head: terms 0 .. kHead - 1 in order (lane L holds terms L kTerms ..)
+            if (w == 0) {
+                double acc = s;
+#pragma unroll
+                for (int L = 0; L < (int)kHeadLanes; L++) {
+#pragma unroll
+                    for (uint32_t j = 0; j < kTerms; j++) acc += lane_f64(fx[j], L);
+                }
+                if (lane == 0) sh.s = acc;
+            }
+            lds_barrier();
+            s = uni(sh.s);
+            from = kHead;
+            lds_barrier();   // sh.s is read before any later write to it
+        }
         while (from < kRound && k0 + from < n) {
             if (isnan(s)) return s;   // stays NaN (only NaN-ness is used downstream)
             if (!(s < 0x1p52)) {
@@ -292,15 +338,14 @@ __device__ double exact_seq_sum(const double* __restrict__ e, uint32_t n, double
                 a[j] = 0.0;
                 if (r >= from && k0 + r < n) {
                     const double q = ldexp(fx[j], ks);     // exact, or +inf past the double range
-                    bool event = !(q < 0x1p53);            // NaN, inf, or certainly past the binade
-                    if (!event) {
-                        const double m = floor(q), fr = q - m;
-                        event = fr == 0.5;
-                        a[j] = fr > 0.5 ? m + 1.0 : m;
-                    }
+                    // round half to even: every non-tie rounds as fl(s + x) does; q - m is exact
+                    const double m = rint(q);
+                    // NaN, inf or certainly past the binade; or a tie
+                    const bool event = !(q < 0x1p53) || fabs(q - m) == 0.5;
                     if (event) {
-                        a[j] = 0.0;
                         if (ev == kNoEvent) ev = r;
+                    } else {
+                        a[j] = m;
                     }
                 }
                 mine += a[j];
@@ -310,7 +355,7 @@ __device__ double exact_seq_sum(const double* __restrict__ e, uint32_t n, double
             const double incl = wave_incl_sum(mine);
             if (lane == 63) sh.part[par][w] = incl;
             const double before = dpp_f64<0x138>(incl);   // wave_shr:1 (lane 0 reads 0)
-            __syncthreads();
+            lds_barrier();
             double waves = 0.0, total = 0.0;
 #pragma unroll
             for (int i = 0; i < (int)kSumWaves; i++) {
@@ -325,13 +370,14 @@ __device__ double exact_seq_sum(const double* __restrict__ e, uint32_t n, double
             for (uint32_t j = 0; j < kTerms; j++) {
                 const uint32_t r = t * kTerms + j;
                 const bool live = r >= from && k0 + r < n;
-                if (live && (r == ev || (r < ev && T + a[j] >= top))) {
+                const double Tn = T + a[j];
+                if (live && (r == ev || (r < ev && Tn >= top))) {
                     ev = r;
                     T_ev = T;
                     x_ev = fx[j];
                     break;
                 }
-                T += a[j];
+                T = Tn;
             }
             // the wave's first event sits in its lowest lane that has one (lanes hold
             // consecutive terms)
@@ -345,7 +391,7 @@ __device__ double exact_seq_sum(const double* __restrict__ e, uint32_t n, double
                     sh.x_ev[par][w] = x_ev;
                 }
             }
-            __syncthreads();
+            lds_barrier();
             uint32_t first = kNoEvent;
             int fw = 0;
 #pragma unroll

@@ -6,8 +6,9 @@ so the bar is bit-exact equality with `redukt_cdf_from_logits` (libredukt_host.s
 the CPU tests pin to the oracle and the reference's exp goldens:
 
 * crafted rows through `redukt_backend_cdf_from_logits_device`: Gaussian logits at
-  several scales, vocabularies 1, 2, 256, 50,280, 50,281 (odd: the unpaired load path)
-  and 65,536, many-way ties for the maximum, a flat row (every share rounds up and the
+  several scales, vocabularies 1, 2, 255-257 (around the terms the sums add one by one),
+  8,192 and 8,193 (one round's window), 50,280, 50,281 (odd: the unpaired load path) and
+  65,536, many-way ties for the maximum, a flat row (every share rounds up and the
   fix-up wraps the last frequency, a reference quirk), -inf entries, rows whose exps
   underflow into subnormals, a row with NaNs;
 * `redukt_backend_forward_batch_cdf` on Mamba-130M (int8 per-row) and RWKV-7 0.1B
@@ -29,7 +30,7 @@ def crafted_rows():
     rng = np.random.default_rng(2024)
     rows = []
     for n, scale in ((50280, 1.0), (50280, 8.0), (50280, 0.05), (65536, 3.0), (256, 2.0), (50281, 1.5),
-                     (2, 1.0), (1, 1.0)):
+                     (2, 1.0), (1, 1.0), (255, 1.0), (257, 1.0), (8192, 2.0), (8193, 0.5)):
         rows.append(("gauss", (rng.standard_normal(n) * scale).astype(np.float32)))
     t = (rng.standard_normal(50280)).astype(np.float32)
     t[rng.choice(50280, 37, replace=False)] = t.max() + 1.0       # 37 equal maxima

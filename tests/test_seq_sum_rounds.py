@@ -14,7 +14,7 @@ import math
 import numpy as np
 import pytest
 
-ROUND = 64   # terms per round (the device takes 2048; the rule does not depend on it)
+ROUND = 64   # terms per round (the device takes 8192; the rule does not depend on it)
 
 
 def sequential(x, s0):
@@ -32,13 +32,20 @@ def ldexp_inf(v, k):
         return math.inf
 
 
-def rounds_sum(x, s0, window=ROUND):
+def rounds_sum(x, s0, window=ROUND, head=0):
+    """The device's steps: the first `head` terms added one by one (when the row has that
+    many), then rounds over windows of `window` terms, the first window starting after the
+    head."""
     x = [float(v) for v in x]
     n = len(x)
     s = float(s0)
+    if n >= head > 0:
+        assert head <= window
+        for v in x[:head]:
+            s = float(np.float64(s) + np.float64(v))
     k0 = 0
     while k0 < n:
-        frm = 0
+        frm = head if (k0 == 0 and n >= head) else 0
         while frm < window and k0 + frm < n:
             if math.isnan(s):
                 return s
@@ -127,6 +134,21 @@ def test_window_size_does_not_matter(window):
     rng = np.random.default_rng(11)
     x = np.exp(rng.standard_normal(2500) * 4)
     assert same(rounds_sum(x, 0.0, window), sequential(x, 0.0))
+
+
+@pytest.mark.parametrize("head,window", [(1, 1), (16, 64), (64, 64), (256, 1000), (256, 8192)])
+def test_a_sequential_head_then_rounds(head, window):
+    # the head ends inside or at the end of the first window; rows shorter than the head go
+    # to the rounds alone; ties and crossings sit on both sides of the head's end
+    rng = np.random.default_rng(head + window)
+    half = 2.0 ** -53
+    x = np.concatenate([np.exp(rng.standard_normal(300) * 3), [1.0] + [half, 2.0 ** -52] * 20,
+                        np.exp(rng.standard_normal(2000))])
+    for row in (x, x[:head - 1] if head > 1 else x[:0], x[:head], x[:head + 3]):
+        for s0 in (0.0, -0.0):
+            assert same(rounds_sum(row, s0, window, head), sequential(row, s0))
+    p = (x * (1.0 / sequential(x, 0.0))).astype(np.float32).astype(np.float64)
+    assert same(rounds_sum(p, -0.0, window, head), sequential(p, -0.0))
 
 
 def test_a_missed_tie_is_caught():
