@@ -256,7 +256,8 @@ struct SumShared {
     uint32_t first[2][kSumWaves];  // per-wave first event
     double t_ev[2][kSumWaves];     // the grid count before that event
     double x_ev[2][kSumWaves];     // that event's term
-    double s;                      // the fallback's result
+    double s;                      // the head's or the fallback's result
+    double head[kHead];            // the head's terms in order
 };
 
 // A barrier for the rounds' LDS traffic only: LDS operations complete (lgkmcnt 0), then
@@ -291,20 +292,30 @@ __device__ double exact_seq_sum(const double* __restrict__ e, uint32_t n, double
         // rounds over this window: after an event the rest of the window is re-gridded
         uint32_t from = 0;   // first term of the window not yet in s
         if (k0 == 0 && n >= kHead) {
-            // the head: terms 0 .. kHead - 1 in order (lane L holds terms L kTerms ..)
+            // the head: terms 0 .. kHead - 1 in order.  Wave 0 holds them (lane L: terms
+            // L kTerms ..); it stores them to LDS in order and every lane reads them back
+            // (same address: a broadcast) into one chain of adds.
             if (w == 0) {
+#pragma unroll
+                for (uint32_t j = 0; j < kTerms; j++)
+                    if (lane < (int)kHeadLanes) sh.head[lane * kTerms + j] = fx[j];
+                __builtin_amdgcn_s_waitcnt(0xc07f);   // this wave's LDS stores done
+                __builtin_amdgcn_wave_barrier();
                 double acc = s;
+#pragma unroll 2
+                for (uint32_t i = 0; i < kHead; i += 16) {
+                    double v[16];
 #pragma unroll
-                for (int L = 0; L < (int)kHeadLanes; L++) {
+                    for (uint32_t k = 0; k < 16; k++) v[k] = sh.head[i + k];
 #pragma unroll
-                    for (uint32_t j = 0; j < kTerms; j++) acc += lane_f64(fx[j], L);
+                    for (uint32_t k = 0; k < 16; k++) acc += v[k];
                 }
                 if (lane == 0) sh.s = acc;
             }
             lds_barrier();
             s = uni(sh.s);
             from = kHead;
-            lds_barrier();   // sh.s is read before any later write to it
+            lds_barrier();   // sh.s and sh.head are read before any later write to them
         }
         while (from < kRound && k0 + from < n) {
             if (isnan(s)) return s;   // stays NaN (only NaN-ness is used downstream)
@@ -329,26 +340,25 @@ __device__ double exact_seq_sum(const double* __restrict__ e, uint32_t n, double
                 top = 0x1p53;
             }
             const double T0 = ldexp(s, ks);   // exact and integer-valued: s is on the grid
-            double a[kTerms];
-            uint32_t ev = kNoEvent;   // this thread's first event (index within the window)
+            double a[kTerms];   // grid counts; 0 for events and for terms outside the round
+            double c[kTerms];   // this thread's inclusive prefix of them
+            bool live[kTerms];
+            uint32_t ev = kNoEvent;   // this thread's first tie or NaN (index within the window)
             double mine = 0.0;
+            // (straight-line: selects, no branches per term)
 #pragma unroll
             for (uint32_t j = 0; j < kTerms; j++) {
                 const uint32_t r = t * kTerms + j;
-                a[j] = 0.0;
-                if (r >= from && k0 + r < n) {
-                    const double q = ldexp(fx[j], ks);     // exact, or +inf past the double range
-                    // round half to even: every non-tie rounds as fl(s + x) does; q - m is exact
-                    const double m = rint(q);
-                    // NaN, inf or certainly past the binade; or a tie
-                    const bool event = !(q < 0x1p53) || fabs(q - m) == 0.5;
-                    if (event) {
-                        if (ev == kNoEvent) ev = r;
-                    } else {
-                        a[j] = m;
-                    }
-                }
+                live[j] = r >= from && k0 + r < n;
+                const double q = ldexp(fx[j], ks);     // exact, or +inf past the double range
+                // round half to even: every non-tie rounds as fl(s + x) does; q - m is exact
+                const double m = rint(q);
+                // NaN, inf or certainly past the binade; or a tie
+                const bool bad = !(q < 0x1p53) || fabs(q - m) == 0.5;
+                ev = (live[j] && bad && ev == kNoEvent) ? r : ev;
+                a[j] = (live[j] && !bad) ? m : 0.0;
                 mine += a[j];
+                c[j] = mine;
             }
             // workgroup prefix of the grid counts: the lane's exclusive prefix in its wave
             // (the inclusive prefix of the lane before it), then the waves before it
@@ -356,29 +366,30 @@ __device__ double exact_seq_sum(const double* __restrict__ e, uint32_t n, double
             if (lane == 63) sh.part[par][w] = incl;
             const double before = dpp_f64<0x138>(incl);   // wave_shr:1 (lane 0 reads 0)
             lds_barrier();
-            double waves = 0.0, total = 0.0;
+            // lanes 0 .. kSumWaves - 1 read one wave's total each; their inclusive prefix gives
+            // the waves before this one and the workgroup's total
+            double wp = lane < (int)kSumWaves ? sh.part[par][lane] : 0.0;
+            wp += dpp_f64<0x111>(wp);   // row_shr:1, 2, 4, 8 within lanes 0 .. 15
+            wp += dpp_f64<0x112>(wp);
+            wp += dpp_f64<0x114>(wp);
+            wp += dpp_f64<0x118>(wp);
+            static_assert(kSumWaves <= 16, "the wave totals fit one DPP row");
+            const double waves = w > 0 ? lane_f64(wp, (int)uni((uint32_t)(w - 1))) : 0.0;
+            const double total = lane_f64(wp, (int)kSumWaves - 1);
+            // crossings: the first term whose add takes T to the top of the binade, or this
+            // thread's first tie or NaN, whichever comes first (lowest j wins)
+            const double base = (T0 + waves) + before;
+            uint32_t evn = kNoEvent;
+            double T_ev = 0.0, x_ev = 0.0;
 #pragma unroll
-            for (int i = 0; i < (int)kSumWaves; i++) {
-                const double p = sh.part[par][i];
-                if (i < w) waves += p;
-                total += p;
+            for (int j = (int)kTerms - 1; j >= 0; j--) {
+                const uint32_t r = t * kTerms + (uint32_t)j;
+                const bool hit = live[j] && (r == ev || (r < ev && base + c[j] >= top));
+                evn = hit ? r : evn;
+                T_ev = hit ? (j > 0 ? base + c[j - 1] : base) : T_ev;
+                x_ev = hit ? fx[j] : x_ev;
             }
-            // crossings: the first term whose add takes T to the top of the binade
-            double T = (T0 + waves) + before, T_ev = 0.0;
-            double x_ev = 0.0;
-#pragma unroll
-            for (uint32_t j = 0; j < kTerms; j++) {
-                const uint32_t r = t * kTerms + j;
-                const bool live = r >= from && k0 + r < n;
-                const double Tn = T + a[j];
-                if (live && (r == ev || (r < ev && Tn >= top))) {
-                    ev = r;
-                    T_ev = T;
-                    x_ev = fx[j];
-                    break;
-                }
-                T = Tn;
-            }
+            ev = evn;
             // the wave's first event sits in its lowest lane that has one (lanes hold
             // consecutive terms)
             const uint64_t has = __ballot(ev != kNoEvent);
@@ -392,26 +403,20 @@ __device__ double exact_seq_sum(const double* __restrict__ e, uint32_t n, double
                 }
             }
             lds_barrier();
-            uint32_t first = kNoEvent;
-            int fw = 0;
-#pragma unroll
-            for (int i = (int)kSumWaves - 1; i >= 0; i--) {
-                const uint32_t v = sh.first[par][i];
-                if (v <= first) {
-                    first = v;
-                    fw = i;
-                }
-            }
-            first = uni(first);
-            if (first == kNoEvent) {
+            // the round's first event is the first event of the lowest wave that has one
+            const uint32_t fv = lane < (int)kSumWaves ? sh.first[par][lane] : kNoEvent;
+            const uint64_t hasw = __ballot(fv != kNoEvent);
+            if (hasw == 0) {
                 // no event: the window's remaining terms are the grid sum (T0 + total < 2^53)
                 s = uni(ldexp(T0 + total, -ks));
                 from = kRound;
             } else {
                 // the event's add, done by every thread on the same operands
-                fw = (int)uni((uint32_t)fw);
-                s = uni(ldexp(sh.t_ev[par][fw], -ks) + sh.x_ev[par][fw]);
-                from = first + 1;
+                const int fw = (int)uni((uint32_t)__builtin_ctzll(hasw));
+                const double tv = lane < (int)kSumWaves ? sh.t_ev[par][lane] : 0.0;
+                const double xv = lane < (int)kSumWaves ? sh.x_ev[par][lane] : 0.0;
+                s = uni(ldexp(lane_f64(tv, fw), -ks) + lane_f64(xv, fw));
+                from = (uint32_t)__builtin_amdgcn_readlane((int)fv, fw) + 1;
             }
             par ^= 1u;
         }
