@@ -1673,6 +1673,113 @@ __global__ __launch_bounds__(kOutWaves * kWave) void k_mix_out(MixOutArgs a) {
     mix_out_body<Q8, G, FIXED, kOutWaves>(a, t_blk, by, NoWait{});
 }
 
+// out_proj + residual for TT row tiles of one stream group (the fixed shape: kOutPairs
+// k-pairs per wave).  Each wave multiplies all TT tiles over its k-pairs against the same
+// gated fragments, so a workgroup reads its group's gated tiles once for TT tiles instead
+// of once per tile.  Per tile the arithmetic is mix_out_body's: the same k-split over the
+// eight waves, the same products into the same accumulators, the eighths added in wave
+// order, then the row scale and the residual; so a stream's bits do not depend on TT.
+// Wave i < TT finishes tile TT t_blk + i.
+template <bool Q8, int TT>
+__device__ __forceinline__ void mix_out_tiles(const MixOutArgs& a, uint32_t t_blk, uint32_t by) {
+    __shared__ f32x4 part[kOutWaves][TT][kWave];
+    const int lane = threadIdx.x % kWave, wave = wave_index();
+    const TMat& w = a.w;
+    const int t0 = (int)t_blk * TT;
+    const uint32_t b0 = by * kRowTile;
+    const bool grp = Q8 && w.group != w.cols;
+    const int gpr = w.ks / 2;
+    RawPair raw[kOutPairs][TT];
+    bf16x8 bfr[kOutPairs][2][3];
+    float sc[kOutPairs][TT][4];
+#pragma unroll
+    for (int q = 0; q < kOutPairs; q++) {
+        const int p = wave * kOutPairs + q;
+#pragma unroll
+        for (int i = 0; i < TT; i++) raw[q][i] = load_pair<Q8>(w, min(t0 + i, w.rt - 1), p, lane);
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const __bf16* f = a.glimb + (((size_t)by * w.ks + 2 * p + h) * 3) * 512 + lane * 8;
+#pragma unroll
+            for (int m = 0; m < 3; m++) bfr[q][h][m] = lds_frag(f + m * 512);
+        }
+        if (grp) {
+#pragma unroll
+            for (int i = 0; i < TT; i++)
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    sc[q][i][e] = w.scales[(size_t)(min(t0 + i, w.rt - 1) * kRowTile + (lane / 16) * 4 + e) * gpr + p];
+        }
+    }
+    // Epilogue operands of the tile this wave finishes (waves past TT load tile TT - 1's).
+    const int tf = min(t0 + min(wave, TT - 1), w.rt - 1);
+    const int r0 = tf * kRowTile + (lane / 16) * 4;
+    const uint32_t b = b0 + lane % 16;
+    const float4 xv = *(const float4*)(a.x + (size_t)min(b, a.n - 1) * a.d + r0);
+    float rs[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+    if (Q8 && !grp) {
+        const float4 r4 = *(const float4*)(w.scales + r0);
+        rs[0] = r4.x; rs[1] = r4.y; rs[2] = r4.z; rs[3] = r4.w;
+    }
+    const float4 w4 = a.xw != nullptr ? *(const float4*)(a.nw_next + r0) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    __builtin_amdgcn_sched_barrier(0);
+    f32x4 acc3[TT][3];
+#pragma unroll
+    for (int i = 0; i < TT; i++)
+#pragma unroll
+        for (int o = 0; o < 3; o++) acc3[i][o] = f32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int q = 0; q < kOutPairs; q++) {
+#pragma unroll
+        for (int i = 0; i < TT; i++) {
+            AFrag a0, a1;
+            decode_pair<Q8>(raw[q][i], a0, a1);
+            if (grp) {
+                f32x4 pp{0, 0, 0, 0};
+                pp = mma_step<Q8>(a0, bfr[q][0][0], bfr[q][0][1], bfr[q][0][2], pp);
+                pp = mma_step<Q8>(a1, bfr[q][1][0], bfr[q][1][1], bfr[q][1][2], pp);
+#pragma unroll
+                for (int e = 0; e < 4; e++) acc3[i][0][e] = __builtin_fmaf(pp[e], sc[q][i][e], acc3[i][0][e]);
+            } else {
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const AFrag& af = h ? a1 : a0;
+                    const bf16x8* bb = bfr[q][h];
+                    if (Q8) {
+                        acc3[i][0] = mma(af.h, bb[0], acc3[i][0]);
+                        acc3[i][1] = mma(af.h, bb[1], acc3[i][1]);
+                        acc3[i][2] = mma(af.h, bb[2], acc3[i][2]);
+                    } else {
+                        acc3[i][0] = mma(af.h, bb[0], acc3[i][0]);
+                        acc3[i][1] = mma(af.h, bb[1], acc3[i][1]);
+                        acc3[i][1] = mma(af.m, bb[0], acc3[i][1]);
+                        acc3[i][2] = mma(af.h, bb[2], acc3[i][2]);
+                        acc3[i][2] = mma(af.m, bb[1], acc3[i][2]);
+                        acc3[i][2] = mma(af.l, bb[0], acc3[i][2]);
+                    }
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < TT; i++) part[wave][i][lane] = (acc3[i][0] + acc3[i][1]) + acc3[i][2];
+    __syncthreads();
+    if (wave >= TT || t0 + wave >= w.rt) return;
+    f32x4 s = part[0][wave][lane];
+#pragma unroll
+    for (int q = 1; q < kOutWaves; q++) s = s + part[q][wave][lane];
+    const bool ok = b < a.n && r0 < a.d;
+    const float nx[4] = {xv.x + s[0] * rs[0], xv.y + s[1] * rs[1], xv.z + s[2] * rs[2], xv.w + s[3] * rs[3]};
+    if (ok) *(float4*)((a.x_out ? a.x_out : a.x) + (size_t)b * a.d + r0) = make_float4(nx[0], nx[1], nx[2], nx[3]);
+    if (a.xw != nullptr) produce_tile(a.xw, a.ssp, a.ks_x, a.tiles, tf, b, ok, nx, w4);
+}
+
+template <bool Q8, int TT>
+__global__ __launch_bounds__(kOutWaves * kWave) void k_mix_out_t(MixOutArgs a) {
+    const uint32_t t_blk = a.gmajor ? blockIdx.y : blockIdx.x, by = a.gmajor ? blockIdx.x : blockIdx.y;
+    mix_out_tiles<Q8, TT>(a, t_blk, by);
+}
+
 // ---------------------------------------------------------------- persistent step kernel
 
 // All layers of a step in one cooperative launch (int8 per-row weights, the Mamba-130M
@@ -2191,6 +2298,27 @@ const void* mix_out_fn(bool q8, int groups, bool fixed) {
     return fixed ? (const void*)k_mix_out<false, 1, true> : (const void*)k_mix_out<false, 1, false>;
 }
 
+const void* mix_out_t_fn(int tt) {
+    return tt == 4 ? (const void*)k_mix_out_t<true, 4> : tt == 3 ? (const void*)k_mix_out_t<true, 3>
+                                                               : (const void*)k_mix_out_t<true, 2>;
+}
+
+// Row tiles per out_proj workgroup (quantized weights).  A step split into parts runs two
+// parts' kernels at once, and their reads of the gated tiles (a group's tiles are read once
+// per workgroup) compete for the caches' bandwidth: there two tiles per workgroup read them
+// half as often (Mamba-130M int8 at 128 streams, two parts of 64: 624.8 -> 613.5 µs per
+// step; 1024 streams unchanged).  One part alone loses by the halved number of workgroups
+// (64 streams 470.8 -> 480.2 µs), so it keeps one tile; so do F32 weights, whose tiles
+// outweigh the gated ones (128 streams 918 -> 962 µs with two).  REDUKT_GPU_OUT_TILES=1..4
+// overrides the choice for quantized weights.
+int out_tiles(bool q8, uint32_t n, uint32_t n_all) {
+    const char* e = getenv("REDUKT_GPU_OUT_TILES");
+    const int v = e && *e ? atoi(e) : 0;
+    const int forced = v >= 1 && v <= 4 ? v : 0;
+    if (!q8) return 1;
+    return forced ? forced : (n_all > n ? 2 : 1);
+}
+
 const void* mix_in_fn(bool q8, bool q8xp, bool pre, bool grp, bool fixed, int tiles, uint32_t lds) {
     if (q8 && q8xp) return mix_in_fn2<true, true>(pre, grp, fixed, tiles, lds);
     if (q8) return mix_in_fn2<true, false>(pre, grp, fixed, tiles, lds);
@@ -2368,6 +2496,7 @@ void build_step(const ModelView& m, Pool& pool, const StepIO& io, std::vector<La
     const bool grp = q8 && m.layers[0].in_x.group != m.layers[0].in_x.cols;
     const bool fixed = ks_x == 2 * kWaves * kInFixedPairs && m.layers[0].in_z.ks == ks_x;
     const void* fin = mix_in_fn(q8, q8xp, pre, grp, fixed, in_tiles, lds_in);
+    const int tt = out_tiles(q8, n, io.n_all ? io.n_all : n);
     const size_t ssm_layer = (size_t)p.scap * di * 16;
     for (uint32_t li = 0; li < D.nl; li++) {
         const DLayer& L = m.layers[li];
@@ -2378,9 +2507,16 @@ void build_step(const ModelView& m, Pool& pool, const StepIO& io, std::vector<La
         out.push_back(Launch::make(fin, in_gmajor ? dim3(in_chunks, nxb + zb) : dim3(nxb + zb, in_chunks), dim3(kBlock),
                                    lds_in, KC_MIX_IN, mi));
         out.push_back(scan_launch(L, D, p, n, m.exact_scan, p.glimb, nullptr, p.ssm + li * ssm_layer));
-        const void* fo = mix_out_fn(q8, out_g, m.layers[0].out_proj.ks == 2 * kOutWaves * kOutPairs);
+        const bool ofixed = m.layers[0].out_proj.ks == 2 * kOutWaves * kOutPairs;
         MixOutArgs mo = la.mo;
         mo.gmajor = gmajor ? 1u : 0u;
+        if (ofixed && out_g == 1 && tt > 1 && L.out_proj.rt % tt == 0) {
+            const uint32_t blocks = (uint32_t)(L.out_proj.rt / tt);
+            out.push_back(Launch::make(mix_out_t_fn(tt), gmajor ? dim3(out_chunks, blocks) : dim3(blocks, out_chunks),
+                                       dim3(kOutWaves * kWave), 0, KC_MIX_OUT, mo));
+            continue;
+        }
+        const void* fo = mix_out_fn(q8, out_g, ofixed);
         out.push_back(Launch::make(fo, gmajor ? dim3(out_chunks, L.out_proj.rt) : dim3(L.out_proj.rt, out_chunks),
                                    dim3(kOutWaves * kWave), 0, KC_MIX_OUT, mo));
     }

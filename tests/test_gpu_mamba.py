@@ -452,6 +452,18 @@ def test_split_mamba130m_128_streams_bitwise(full_model, monkeypatch):
     assert np.array_equal(bits(ref), bits(got))
 
 
+@pytest.mark.parametrize("tiles", [2, 3, 4])
+def test_out_proj_tiles_per_workgroup_are_bitwise_identical(full_model, monkeypatch, tiles):
+    # out_proj workgroups covering several row tiles (read each stream group's gated tiles
+    # once for all of them) give every stream the bits of one tile per workgroup.
+    monkeypatch.setenv("REDUKT_GPU_SPLIT", "1")
+    monkeypatch.setenv("REDUKT_GPU_OUT_TILES", "1")
+    ref = _steps(full_model, 6, 48, 2, 11)
+    monkeypatch.setenv("REDUKT_GPU_OUT_TILES", str(tiles))
+    got = _steps(full_model, 6, 48, 2, 11)
+    assert np.array_equal(bits(ref), bits(got))
+
+
 def test_split_device_check_covers_every_part(models, monkeypatch):
     # A slot repeated in two different parts is caught by the device check of the whole
     # step: the later entry never touches the real slot, the first advances it exactly as a
