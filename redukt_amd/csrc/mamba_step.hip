@@ -2573,11 +2573,11 @@ void StepRunner::release() {
     for (uint32_t k = 0; k < kMaxParts; k++) {
         if (aux_[k]) (void)hipStreamDestroy(aux_[k]);
         if (join_[k]) (void)hipEventDestroy(join_[k]);
+        if (fork_[k]) (void)hipEventDestroy(fork_[k]);
         aux_[k] = nullptr;
         join_[k] = nullptr;
+        fork_[k] = nullptr;
     }
-    if (fork_) (void)hipEventDestroy(fork_);
-    fork_ = nullptr;
     direct_.clear();
 }
 
@@ -2598,11 +2598,11 @@ StepRunner& StepRunner::operator=(StepRunner&& o) noexcept {
     for (uint32_t k = 0; k < kMaxParts; k++) {
         aux_[k] = o.aux_[k];
         join_[k] = o.join_[k];
+        fork_[k] = o.fork_[k];
         o.aux_[k] = nullptr;
         o.join_[k] = nullptr;
+        o.fork_[k] = nullptr;
     }
-    fork_ = o.fork_;
-    o.fork_ = nullptr;
     return *this;
 }
 
@@ -2682,10 +2682,10 @@ uint32_t StepRunner::parts_of(uint32_t n, uint32_t k, uint32_t* b0, uint32_t* cn
 hipError_t StepRunner::streams_ready(hipStream_t st, uint32_t parts) {
     (void)st;
     if (parts <= 1) return hipSuccess;
-    if (!fork_) RDK_TRY(hipEventCreateWithFlags(&fork_, hipEventDisableTiming));
-    for (uint32_t k = 1; k < parts; k++) {
-        if (!aux_[k]) RDK_TRY(hipStreamCreateWithFlags(&aux_[k], hipStreamNonBlocking));
-        if (!join_[k]) RDK_TRY(hipEventCreateWithFlags(&join_[k], hipEventDisableTiming));
+    for (uint32_t k = 0; k < parts; k++) {
+        if (k > 0 && !aux_[k]) RDK_TRY(hipStreamCreateWithFlags(&aux_[k], hipStreamNonBlocking));
+        if (k > 0 && !join_[k]) RDK_TRY(hipEventCreateWithFlags(&join_[k], hipEventDisableTiming));
+        if (k + 1 < parts && !fork_[k]) RDK_TRY(hipEventCreateWithFlags(&fork_[k], hipEventDisableTiming));
     }
     return hipSuccess;
 }
@@ -2992,11 +2992,14 @@ hipError_t StepRunner::run(const StepSource& src, Pool& p, const StepIO& io, hip
         return q;
     };
     auto stream_of = [&](uint32_t k) { return k == 0 ? st : aux_[k]; };
-    // Parts 1.. start after everything queued on st so far and st waits for all of them.
-    auto fork = [&]() -> hipError_t {
-        if (nparts == 1) return hipSuccess;
-        RDK_TRY(hipEventRecord(fork_, st));
-        for (uint32_t k = 1; k < nparts; k++) RDK_TRY(hipStreamWaitEvent(aux_[k], fork_, 0));
+    // Part k > 0 starts once part k - 1 has issued its lead (so after everything queued on
+    // st so far), and st waits for every part.
+    auto start_part = [&](uint32_t k) -> hipError_t {
+        if (k > 0) RDK_TRY(hipStreamWaitEvent(aux_[k], fork_[k - 1], 0));
+        return hipSuccess;
+    };
+    auto after_lead = [&](uint32_t k) -> hipError_t {
+        if (k + 1 < nparts) RDK_TRY(hipEventRecord(fork_[k], stream_of(k)));
         return hipSuccess;
     };
     auto join = [&]() -> hipError_t {
@@ -3016,15 +3019,15 @@ hipError_t StepRunner::run(const StepSource& src, Pool& p, const StepIO& io, hip
             int io_i = -1, head_i = -1, sm_i = -1;
             src.build(p, part_io(k), seqs[k], io_i, head_i, sm_i);
         }
-        // Part 0's first `skew` kernels go ahead of the fork, so the other parts start
-        // that many kernels behind it.
-        const size_t ahead = std::min<size_t>(skew, seqs[0].size());
-        if (nparts > 1)
-            for (size_t i = 0; i < ahead; i++) RDK_TRY(launch_direct(seqs[0][i], st));
-        RDK_TRY(fork());
-        for (uint32_t k = 0; k < nparts; k++)
-            for (size_t i = (k == 0 && nparts > 1) ? ahead : 0; i < seqs[k].size(); i++)
-                RDK_TRY(launch_direct(seqs[k][i], stream_of(k)));
+        // Each part but the last issues its first `skew` kernels before the next part
+        // starts, so consecutive parts run that many kernels apart.
+        for (uint32_t k = 0; k < nparts; k++) {
+            RDK_TRY(start_part(k));
+            const size_t ahead = k + 1 < nparts ? std::min<size_t>(skew, seqs[k].size()) : 0;
+            for (size_t i = 0; i < ahead; i++) RDK_TRY(launch_direct(seqs[k][i], stream_of(k)));
+            RDK_TRY(after_lead(k));
+            for (size_t i = ahead; i < seqs[k].size(); i++) RDK_TRY(launch_direct(seqs[k][i], stream_of(k)));
+        }
         return join();
     }
     auto same_io = [&](const Graph& g) {
@@ -3058,7 +3061,7 @@ hipError_t StepRunner::run(const StepSource& src, Pool& p, const StepIO& io, hip
             pt.n = cnt[k];
             std::unique_ptr<std::vector<Launch>> seq(new std::vector<Launch>());
             src.build(p, part_io(k), *seq, pt.io_i, pt.head_i, pt.sm_i);
-            pt.lead = k == 0 && nparts > 1 ? std::min<uint32_t>(skew_, (uint32_t)seq->size()) : 0u;
+            pt.lead = k + 1 < nparts ? std::min<uint32_t>(skew_, (uint32_t)seq->size()) : 0u;
             const hipError_t e = capture(*seq, pt.lead, st, pt);
             if (e != hipSuccess) {
                 destroy(g);
@@ -3094,10 +3097,13 @@ hipError_t StepRunner::run(const StepSource& src, Pool& p, const StepIO& io, hip
     hit->out = io.out;
     hit->err = io.err;
     hit->last_use = ++clock_;
-    const Part& p0 = hit->parts[0];
-    for (uint32_t i = 0; i < p0.lead; i++) RDK_TRY(launch_direct((*p0.launches)[i], st));
-    RDK_TRY(fork());
-    for (uint32_t k = 0; k < hit->nparts; k++) RDK_TRY(hipGraphLaunch(hit->parts[k].exec, stream_of(k)));
+    for (uint32_t k = 0; k < hit->nparts; k++) {
+        const Part& pk = hit->parts[k];
+        RDK_TRY(start_part(k));
+        for (uint32_t i = 0; i < pk.lead; i++) RDK_TRY(launch_direct((*pk.launches)[i], stream_of(k)));
+        RDK_TRY(after_lead(k));
+        RDK_TRY(hipGraphLaunch(pk.exec, stream_of(k)));
+    }
     return join();
 }
 

@@ -419,8 +419,9 @@ public:
     // Steps of at least `from` streams (0: none) whose source has a persistent step kernel
     // run it (direct launches, one part) instead of the per-layer graphs.
     void set_flow(uint32_t from) { flow_from_ = from; }
-    // A split step issues the first `k` launches of part 0 before the other parts start, so
-    // the parts run that many kernels apart (0: all parts start together).
+    // A split step issues the first `k` launches of each part but the last before the next
+    // part starts, so consecutive parts run that many kernels apart (0: all parts start
+    // together).
     void set_skew(uint32_t k) { skew_ = k; }
     // Rows [b0, b0 + n) of each part of a step of n streams split at most k ways.
     static uint32_t parts_of(uint32_t n, uint32_t k, uint32_t* b0, uint32_t* cnt);
@@ -434,7 +435,7 @@ private:
         hipGraphNode_t io_node = nullptr, head_node = nullptr, softmax_node = nullptr;
         std::vector<Launch>* launches = nullptr;  // argument storage, alive as long as the graph
         int io_i = -1, head_i = -1, sm_i = -1;
-        uint32_t lead = 0;   // leading launches issued directly, ahead of the fork (the graph holds the rest)
+        uint32_t lead = 0;   // leading launches issued directly, before the next part starts (the graph holds the rest)
     };
     struct Graph {
         uint32_t n = 0, split = 1;
@@ -470,7 +471,7 @@ private:
     uint32_t split_ = 1, min_part_ = kMinPartStreams;
     uint32_t skew_ = 0;
     hipStream_t aux_[kMaxParts] = {};        // aux_[k] runs part k (k >= 1)
-    hipEvent_t fork_ = nullptr;
+    hipEvent_t fork_[kMaxParts] = {};        // recorded on part k's stream after its lead; part k + 1 waits for it
     hipEvent_t join_[kMaxParts] = {};
     std::vector<Launch> direct_;             // run_direct's launch list (host storage, reused)
 };
