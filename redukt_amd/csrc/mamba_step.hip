@@ -196,23 +196,39 @@ struct NoWait {
 // error word and goes on, and every later wait of the launch that finds the bit set gives
 // up within 1024 polls, so every wave exits soon after a first failure.
 constexpr uint32_t kFlowSpinMax = 1u << 17;
+constexpr uint32_t kFlowCounterStride = 32;   // words between counters (one 128-byte line each)
+// A phase counter is kFlowSlices counters, one per XCD (XCD x adds to slice x % kFlowSlices):
+// the tasks of a phase end within a microsecond or so of each other, and their device-scope
+// adds to one address are performed one after the other; on eight addresses they overlap.
+constexpr uint32_t kFlowSlices = 8;
 
 struct FlowWait {
     static constexpr bool kFlow = true;
     static constexpr int kAux = kCached;
     static constexpr int kStAux = kCoherent;
-    const uint32_t* counter;   // null: nothing to wait for
-    uint32_t target;
+    const uint32_t* counter;   // slice 0 of the phase counter; null: nothing to wait for
+    uint32_t target;           // sum of the slices when the phase is complete
     uint32_t* err;
     __device__ __forceinline__ void wait() const {
-        if (threadIdx.x == 0 && counter != nullptr) {
+        // Wave 0 polls: lane s < kFlowSlices reads slice s, the wave sums them.
+        if (threadIdx.x < kWave && counter != nullptr) {
+            const uint32_t lane = threadIdx.x;
+            const uint32_t* slice = counter + min(lane, kFlowSlices - 1) * kFlowCounterStride;
             uint32_t spins = 0;
-            while (__hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+            for (;;) {
+                uint32_t v = __hip_atomic_load(slice, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                uint32_t sum = 0;
+#pragma unroll
+                for (uint32_t j = 0; j < kFlowSlices; j++) sum += __builtin_amdgcn_readlane(v, j);
+                if (sum >= target) break;
                 __builtin_amdgcn_s_sleep(1);
-                if ((++spins & 1023u) == 0 &&
-                    (spins > kFlowSpinMax || (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & 4u))) {
-                    atomicOr(err, 4u);
-                    break;
+                if ((++spins & 1023u) == 0) {
+                    const uint32_t e = __builtin_amdgcn_readfirstlane(
+                        __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+                    if (spins > kFlowSpinMax || (e & 4u)) {
+                        if (lane == 0) atomicOr(err, 4u);
+                        break;
+                    }
                 }
             }
         }
@@ -1799,7 +1815,6 @@ __global__ __launch_bounds__(kOutWaves * kWave) void k_mix_out_t(MixOutArgs a) {
 // are complete it adds one to its own phase's counter.  The bodies are the stand-alone
 // kernels' (same tiles, k-splits and orders), so a stream's bits do not depend on which
 // path ran it.
-constexpr uint32_t kFlowCounterStride = 32;   // words between counters (one 128-byte line each)
 constexpr uint32_t kFlowMaxStreams = 1024;    // largest step the kernel serves (bounds every wait and its buffers)
 constexpr uint32_t kFlowScanSpt = 2;          // streams per scan task thread
 
@@ -1812,7 +1827,7 @@ struct FlowLayer {
 struct FlowArgs {
     const FlowLayer* layers;  // [nl], device memory, read through the scalar unit
     uint32_t nl, groups;
-    uint32_t* cnt;            // [nl][3][groups] phase counters, then [nx] task tickets, kFlowCounterStride words apart
+    uint32_t* cnt;            // [nl][3][groups][kFlowSlices] phase counters, then [nx] task tickets, kFlowCounterStride words apart
     uint32_t* err;
     uint32_t mi_tasks, cb, mo_tasks;  // in_proj row blocks, scan channel blocks, out_proj row tiles (per group)
     uint32_t nx;              // XCDs of the device (divides each phase's tasks per group)
@@ -1830,7 +1845,7 @@ __global__ __launch_bounds__(kBlock) void k_xcc_map(uint32_t* map) {
 
 // Which workgroup runs a task is decided at run time: the workgroups of XCD x take the
 // tasks of x's list in order from x's ticket counter (one device-scope atomic per task,
-// requested a task ahead).  The hardware deals workgroups to XCDs round-robin from where
+// requested when the previous task's body is done).  The hardware deals workgroups to XCDs round-robin from where
 // the previous dispatch stopped, so the block index does not name the XCD; the ticket
 // order keeps every dependency on an earlier ticket, taken by a resident workgroup.
 template <bool Q8S, bool FAST>
@@ -1847,14 +1862,12 @@ __global__ __launch_bounds__(kBlock, 2) void k_flow(FlowArgs f) {
     const uint32_t mi = f.mi_tasks / nx, sc = kRowTile / kSpt * f.cb / nx, mo = f.mo_tasks / nx;
     const uint32_t per_layer = G * (mi + sc + mo);
     const uint32_t total = per_layer * f.nl;
-    uint32_t* const ticket = f.cnt + ((size_t)f.nl * 3 * G + x) * kFlowCounterStride;
+    uint32_t* const ticket = f.cnt + ((size_t)f.nl * 3 * G * kFlowSlices + x) * kFlowCounterStride;
     typedef const __attribute__((address_space(4))) FlowLayer* FlowLayerK;
     const FlowLayerK layers = (FlowLayerK)f.layers;
     if (threadIdx.x == 0) s_next = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     for (uint32_t i = s_next; i < total;) {
-        uint32_t ahead = 0;
-        if (threadIdx.x == 0) ahead = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const uint32_t l = i / per_layer;
         uint32_t r = i % per_layer;
         uint32_t phase, g, k;
@@ -1868,7 +1881,7 @@ __global__ __launch_bounds__(kBlock, 2) void k_flow(FlowArgs f) {
         }
         const uint32_t task = x + nx * k;
         auto counter = [&](uint32_t ll, uint32_t ph) {
-            return f.cnt + ((size_t)(ll * 3 + ph) * G + g) * kFlowCounterStride;
+            return f.cnt + ((size_t)(ll * 3 + ph) * G + g) * kFlowSlices * kFlowCounterStride;
         };
         const FlowLayer& L = *(const FlowLayer*)(layers + l);
         if (phase == 0) {
@@ -1883,11 +1896,17 @@ __global__ __launch_bounds__(kBlock, 2) void k_flow(FlowArgs f) {
             const FlowWait w{counter(l, 1), kRowTile / kSpt * f.cb, f.err};
             mix_out_body<true, 1, true, kWaves>(L.mo, task, g, w);
         }
+        // The next ticket is taken only once this task's body is done, so a workgroup never
+        // holds two tasks at once (two of one phase would run one after the other); its
+        // round trip overlaps the drain of the task's stores.
+        uint32_t ahead = 0;
+        if (threadIdx.x == 0) ahead = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         // every store of the task is complete at the coherence point before the counter says so
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         if (threadIdx.x == 0) {
-            __hip_atomic_fetch_add(counter(l, phase), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_fetch_add(counter(l, phase) + (x % kFlowSlices) * kFlowCounterStride, 1u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
             s_next = ahead;
         }
         __syncthreads();
@@ -2760,8 +2779,8 @@ const void* flow_fn(const ModelView& m) {
 }
 
 size_t flow_table_bytes(uint32_t nl) { return ((size_t)nl * sizeof(FlowLayer) + 255) & ~(size_t)255; }
-// Phase counters, then one task ticket per XCC_ID value.
-uint32_t flow_counters(uint32_t nl, uint32_t n) { return nl * 3u * ((n + kRowTile - 1) / kRowTile) + 16u; }
+// Phase counters (kFlowSlices each), then one task ticket per XCC_ID value.
+uint32_t flow_counters(uint32_t nl, uint32_t n) { return nl * 3u * ((n + kRowTile - 1) / kRowTile) * kFlowSlices + 16u; }
 size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 // The hand-over buffers of one layer of the persistent step kernel, rows rounded up to
