@@ -380,8 +380,9 @@ constexpr uint32_t kMaxParts = 4;
 // two of them at once loses more (each wave slower, the XCD-aware layouts interleaved
 // with another kernel's) than it overlaps.  Measured on Mamba-130M int8, parts per step:
 // 128 streams 702 / 645 / 687 / 1050 us for 1 / 2 / 3 / 4 parts, 1024 streams 2980 /
-// 2732 / - / 3245 us, 32 streams 379 / 456 us for 1 / 2.
-constexpr uint32_t kMinPartStreams = 64;
+// 2732 / - / 3245 us, 32 streams 379 / 456 us for 1 / 2; one / two parts at 96 streams
+// 653 / 571 us, at 112 684 / 589 us, at 80 493 / 543 us.
+constexpr uint32_t kMinPartStreams = 48;
 // Parts per step by default (REDUKT_GPU_SPLIT overrides).
 constexpr uint32_t kDefaultSplit = 2;
 // Smallest step that runs the persistent step kernel by default (REDUKT_GPU_FLOW

@@ -452,6 +452,17 @@ def test_split_mamba130m_128_streams_bitwise(full_model, monkeypatch):
     assert np.array_equal(bits(ref), bits(got))
 
 
+def test_default_split_mamba130m_112_streams_bitwise(full_model, monkeypatch):
+    # The default split of 112 streams (parts of 64 and 48 streams, out_proj at two row
+    # tiles per workgroup) gives every stream the bits of the unsplit step.
+    monkeypatch.setenv("REDUKT_GPU_SPLIT", "1")
+    ref = _steps(full_model, 6, 112, 2, 13)
+    monkeypatch.delenv("REDUKT_GPU_SPLIT")
+    monkeypatch.delenv("REDUKT_GPU_PART_MIN", raising=False)
+    got = _steps(full_model, 6, 112, 2, 13)
+    assert np.array_equal(bits(ref), bits(got))
+
+
 @pytest.mark.parametrize("tiles", [2, 3, 4])
 def test_out_proj_tiles_per_workgroup_are_bitwise_identical(full_model, monkeypatch, tiles):
     # out_proj workgroups covering several row tiles (read each stream group's gated tiles
