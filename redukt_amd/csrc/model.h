@@ -369,6 +369,8 @@ struct RwkvStep final : StepSource {
     RwkvView m;
     explicit RwkvStep(const RwkvView& v) : m(v) {}
     void build(Pool& p, const StepIO& io, std::vector<Launch>& out, int& io_i, int& head_i, int& sm_i) const override;
+    // The matrix-core tier runs a step as parts; the W8A8 and reference-order tiers in one.
+    bool splittable() const override { return !m.exact && !m.a8; }
     // The W8A8 tier's step and the reference-order tier's (rwkv_a8.hip).
     void build_a8(Pool& p, const StepIO& io, std::vector<Launch>& out, int& io_i, int& head_i, int& sm_i) const;
     void build_ref(Pool& p, const StepIO& io, std::vector<Launch>& out, int& io_i, int& head_i, int& sm_i) const;

@@ -427,26 +427,40 @@ struct ProjBuilder {
 
 }  // namespace
 
-void RwkvStep::build(Pool& p, const StepIO& io, std::vector<Launch>& out, int& io_i, int& head_i, int& sm_i) const {
+void RwkvStep::build(Pool& pool, const StepIO& io, std::vector<Launch>& out, int& io_i, int& head_i, int& sm_i) const {
     if (m.exact) {
-        build_ref(p, io, out, io_i, head_i, sm_i);
+        build_ref(pool, io, out, io_i, head_i, sm_i);
         return;
     }
     if (m.a8) {
-        build_a8(p, io, out, io_i, head_i, sm_i);
+        build_a8(pool, io, out, io_i, head_i, sm_i);
         return;
     }
     const RDims& D = *m.dims;
     const uint32_t n = io.n;
     const int d = (int)D.d;
-    const RwkvSizes z = rwkv_sizes(D, p.cap, false);
+    const RwkvSizes z = rwkv_sizes(D, pool.cap, false);
+    // The scratch of this part of the step (rows from b0, a multiple of 16): every per-row
+    // array offset by b0 rows, every limb buffer by b0 / 16 groups; the recurrent state is
+    // indexed by slot and stays whole.
+    const size_t b0 = io.b0, g0 = b0 / kRowTile, limb_group = 3 * 512;
+    Pool p = pool;
+    p.x = pool.x + b0 * d;
+    p.rkv = pool.rkv + b0 * 3 * d;
+    p.lorad = pool.lorad + b0 * 4 * d;
+    p.vfirst = pool.vfirst + b0 * d;
+    p.slots = pool.slots + b0;
+    p.gatedl = pool.gatedl + g0 * z.ks_d * limb_group;
+    p.ffnl = pool.ffnl + g0 * z.ks_d * limb_group;
+    p.headl = pool.headl + g0 * z.ks_d * limb_group;
+    p.actl = pool.actl + g0 * z.ks_f * limb_group;
     out.clear();
     io_i = (int)out.size();
     out.push_back(embed_launch(*m.emb, p, io, nullptr, nullptr, nullptr, 0, 0));
     __bf16* mixl[6];
-    for (int k = 0; k < 6; k++) mixl[k] = p.mixl + k * z.mixl;
+    for (int k = 0; k < 6; k++) mixl[k] = pool.mixl + k * z.mixl + g0 * z.ks_d * limb_group;
     __bf16* loral[4];
-    for (int k = 0; k < 4; k++) loral[k] = p.loral + z.lora_off[k];
+    for (int k = 0; k < 4; k++) loral[k] = pool.loral + z.lora_off[k] + g0 * z.ks_lora[k] * limb_group;
     const size_t state_stride = (size_t)D.nl * D.d;
     const size_t wkv_layer = (size_t)D.h * D.n * D.n;
     for (uint32_t l = 0; l < D.nl; l++) {
@@ -501,7 +515,7 @@ void RwkvStep::build(Pool& p, const StepIO& io, std::vector<Launch>& out, int& i
     sm_i = -1;
     if (io.probs) {
         sm_i = (int)out.size();
-        out.push_back(softmax_launch(io.out, (int)D.vocab, n));
+        out.push_back(softmax_launch(io.out + b0 * D.vocab, (int)D.vocab, n));
     }
 }
 

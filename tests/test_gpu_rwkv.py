@@ -166,3 +166,31 @@ def test_rwkv7_0_1b_layers_parity(wide_model, profile):
         for t, (g, c) in enumerate(outs):
             assert_parity(g, c, f"0.1B p{profile} step {t}")
         orc.close()
+
+
+def _rwkv_steps(path, profile, n, steps, seed, probs=False):
+    rng = np.random.default_rng(seed)
+    with ffi.PluginBackend(path, profile=profile) as be:
+        be.batch_init(n + 5)
+        slots = [int(s) for s in rng.permutation(n + 5)[:n]]
+        outs = []
+        for _ in range(steps):
+            toks = [int(x) for x in rng.integers(0, be.vocab, n)]
+            g = np.empty((n, be.vocab), np.float32)
+            be.forward_batch(slots, toks, g, probs=probs)
+            outs.append(g)
+        return np.stack(outs)
+
+
+@pytest.mark.parametrize("split", [2, 4])
+@pytest.mark.parametrize("profile,probs", [(0, False), (2, True), (2 | ffi.PROFILE_W8A8, False)])
+def test_rwkv_split_steps_are_bitwise_identical(rwkv_models, monkeypatch, split, profile, probs):
+    # A step split into parts of whole 16-stream groups (a ragged last part included), each
+    # part on its own stream, gives every stream the bits of the unsplit step; the W8A8 tier
+    # runs its steps in one part whatever the split asks.
+    monkeypatch.setenv("REDUKT_GPU_SPLIT", "1")
+    ref = _rwkv_steps(rwkv_models["g1k"], profile, 50, 3, 17, probs)
+    monkeypatch.setenv("REDUKT_GPU_PART_MIN", "16")
+    monkeypatch.setenv("REDUKT_GPU_SPLIT", str(split))
+    got = _rwkv_steps(rwkv_models["g1k"], profile, 50, 3, 17, probs)
+    assert np.array_equal(bits(ref), bits(got))
