@@ -195,6 +195,9 @@ struct ProjArgs {
     uint32_t n;
 };
 
+template <bool Q8>
+__device__ __forceinline__ void proj_finish(const ProjSeg& sg, int t, f32x4 s, uint32_t n);
+
 // One 16-row tile x 16 streams.  Eight waves each take an eighth of the k-pairs (limb
 // orders in separate accumulators), with kProjPairs pairs of weight and activation
 // fragments requested at once; the eighths are added in wave order, then the row scale.
@@ -272,6 +275,17 @@ __device__ __forceinline__ void proj_tile(const ProjSeg& sg, int t, uint32_t n, 
     if (wave != 0) return;
     f32x4 s = acc;
     for (int q = 0; q < kProjWaves - 1; q++) s = s + part[q][lane];
+    proj_finish<Q8>(sg, t, s, n);
+}
+
+// The epilogue of row tile t from its summed products s (one wave): the row scale, then
+// the segment's output (limbs after the activation, a store, or a residual add).
+template <bool Q8>
+__device__ __forceinline__ void proj_finish(const ProjSeg& sg, int t, f32x4 s, uint32_t n) {
+    const int lane = threadIdx.x % kWave;
+    const uint32_t b0 = blockIdx.y * kRowTile;
+    const TMat& w = sg.w;
+    const bool grp = Q8 && w.group != w.cols;
     const int r0 = t * kRowTile + (lane / 16) * 4;
     const uint32_t b = b0 + lane % 16;
     float v[4];
@@ -313,6 +327,128 @@ __global__ __launch_bounds__(kProjWaves * kWave) void k_proj(ProjArgs a) {
     const int t = blockIdx.x - sg.tile0;
     if (sg.w.group) proj_tile<true>(sg, t, a.n, part);
     else proj_tile<false>(sg, t, a.n, part);
+}
+
+// TT row tiles x 16 streams per workgroup: each wave multiplies all TT tiles over its
+// eighth of the k-pairs with one load of the activation fragments, every tile's products
+// in proj_tile's order; the eight waves' sums go through LDS and wave i < TT adds tile i's
+// in wave order (wave 0's first, as proj_tile does), so every output has proj_tile's bits.
+// Tiles past the segment's last load its last tile's weights and store nothing.
+template <bool Q8, int TT>
+__device__ __forceinline__ void proj_tiles(const ProjSeg& sg, int tb, uint32_t n, f32x4 (*part)[TT][kWave]) {
+    const int lane = threadIdx.x % kWave, wave = wave_index();
+    const uint32_t b0 = blockIdx.y * kRowTile;
+    const TMat& w = sg.w;
+    const int np = w.ks / 2;
+    const int p_lo = wave * np / kProjWaves, p_hi = (wave + 1) * np / kProjWaves;
+    const bool grp = Q8 && w.group != w.cols;
+    const int gpr = w.ks / 2;
+    const uint32_t g0 = b0 / kRowTile;
+    const int t0 = tb * TT;
+    // k-pairs requested per pass (batching only: the products' order is the same)
+    constexpr int PP = TT >= 4 ? 1 : kProjPairs;
+    int tl[TT];
+#pragma unroll
+    for (int i = 0; i < TT; i++) tl[i] = min(t0 + i, w.rt - 1);
+    f32x4 acc3[TT][3];
+#pragma unroll
+    for (int i = 0; i < TT; i++)
+#pragma unroll
+        for (int o = 0; o < 3; o++) acc3[i][o] = f32x4{0, 0, 0, 0};
+#pragma unroll 1
+    for (int pb = p_lo; pb < p_hi; pb += PP) {
+        RawPair raw[PP][TT];
+        bf16x8 bfr[PP][2][3];
+        float sc[PP][TT][4];
+#pragma unroll
+        for (int q = 0; q < PP; q++) {
+            const int p = pb + q;
+            if (p >= p_hi) break;
+#pragma unroll
+            for (int i = 0; i < TT; i++) raw[q][i] = load_pair<Q8>(w, tl[i], p, lane);
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const __bf16* f = sg.in + (((size_t)g0 * w.ks + 2 * p + h) * 3) * 512 + lane * 8;
+                bfr[q][h][0] = lds_frag(f);
+                bfr[q][h][1] = lds_frag(f + 512);
+                bfr[q][h][2] = lds_frag(f + 1024);
+            }
+            if (grp) {
+#pragma unroll
+                for (int i = 0; i < TT; i++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        sc[q][i][e] = w.scales[(size_t)(tl[i] * kRowTile + (lane / 16) * 4 + e) * gpr + p];
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < PP; q++) {
+            const int p = pb + q;
+            if (p >= p_hi) break;
+#pragma unroll
+            for (int i = 0; i < TT; i++) {
+                AFrag a0, a1;
+                decode_pair<Q8>(raw[q][i], a0, a1);
+                if (grp) {
+                    f32x4 pp{0, 0, 0, 0};
+                    pp = mma_step<Q8>(a0, bfr[q][0][0], bfr[q][0][1], bfr[q][0][2], pp);
+                    pp = mma_step<Q8>(a1, bfr[q][1][0], bfr[q][1][1], bfr[q][1][2], pp);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) acc3[i][0][e] = __builtin_fmaf(pp[e], sc[q][i][e], acc3[i][0][e]);
+                } else {
+#pragma unroll
+                    for (int h = 0; h < 2; h++) {
+                        const AFrag& af = h ? a1 : a0;
+                        const bf16x8* bb = bfr[q][h];
+                        if (Q8) {
+                            acc3[i][0] = mma(af.h, bb[0], acc3[i][0]);
+                            acc3[i][1] = mma(af.h, bb[1], acc3[i][1]);
+                            acc3[i][2] = mma(af.h, bb[2], acc3[i][2]);
+                        } else {
+                            acc3[i][0] = mma(af.h, bb[0], acc3[i][0]);
+                            acc3[i][1] = mma(af.h, bb[1], acc3[i][1]);
+                            acc3[i][1] = mma(af.m, bb[0], acc3[i][1]);
+                            acc3[i][2] = mma(af.h, bb[2], acc3[i][2]);
+                            acc3[i][2] = mma(af.m, bb[1], acc3[i][2]);
+                            acc3[i][2] = mma(af.l, bb[0], acc3[i][2]);
+                        }
+                    }
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < TT; i++) part[wave][i][lane] = (acc3[i][0] + acc3[i][1]) + acc3[i][2];
+    __syncthreads();
+    if (wave >= TT || t0 + wave >= w.rt) return;
+    f32x4 s = part[0][wave][lane];
+    for (int q = 1; q < kProjWaves; q++) s = s + part[q][wave][lane];
+    proj_finish<Q8>(sg, t0 + wave, s, n);
+}
+
+template <int TT>
+__global__ __launch_bounds__(kProjWaves * kWave) void k_proj_t(ProjArgs a) {
+    __shared__ f32x4 part[kProjWaves][TT][kWave];
+    int si = 0;
+    for (int i = 1; i < a.nseg; i++)
+        if ((int)blockIdx.x >= a.seg[i].tile0) si = i;
+    const ProjSeg sg = a.seg[si];
+    const int tb = blockIdx.x - sg.tile0;
+    if (sg.w.group) proj_tiles<true, TT>(sg, tb, a.n, part);
+    else proj_tiles<false, TT>(sg, tb, a.n, part);
+}
+
+// Row tiles per projection workgroup (1: k_proj): four when the step runs as parts (n of
+// n_all streams), whose launches share the device, one otherwise.  Measured at RWKV-7 0.1B,
+// µs per step for one / two / four tiles, int8 per-row: 64 streams in one part 747 / 802 /
+// 797, 128 streams in two parts 1042 / 1025 / 973, 256 streams 1571 / 1509 / 1303; F32:
+// 64 streams 922 / 1012 / 1060, 128 1313 / 1304 / 1305, 256 2045 / 1988 / 1911.
+// REDUKT_GPU_PROJ_TILES = 1, 2 or 4 forces a count.
+int proj_tiles_for(uint32_t n, uint32_t n_all) {
+    const char* e = getenv("REDUKT_GPU_PROJ_TILES");
+    const int v = e && *e ? atoi(e) : 0;
+    if (v == 1 || v == 2 || v == 4) return v;
+    return n_all > n ? 4 : 1;
 }
 
 // ---------------------------------------------------------------- WKV-7
@@ -404,7 +540,9 @@ __global__ __launch_bounds__(kHead) void k_rwkv_wkv(WkvArgs a) {
 
 struct ProjBuilder {
     ProjArgs a{};
-    int tiles = 0;
+    int tiles = 0;   // workgroups along x
+    int tt = 1;      // row tiles per workgroup
+    explicit ProjBuilder(int tiles_per_wg = 1) : tt(tiles_per_wg) {}
     void add(const TMat& w, const __bf16* in, int mode, int act, float* out, int ld, __bf16* lout, int lks) {
         ProjSeg& s = a.seg[a.nseg++];
         s.w = w;
@@ -416,12 +554,12 @@ struct ProjBuilder {
         s.lout = lout;
         s.lks = lks;
         s.tile0 = tiles;
-        tiles += w.rt;
+        tiles += (w.rt + tt - 1) / tt;
     }
     Launch launch(uint32_t n) {
         a.n = n;
-        return Launch::make((const void*)k_proj, dim3(tiles, (n + kRowTile - 1) / kRowTile), dim3(kProjWaves * kWave), 0,
-                            KC_PROJ, a);
+        const void* f = tt == 4 ? (const void*)k_proj_t<4> : tt == 2 ? (const void*)k_proj_t<2> : (const void*)k_proj;
+        return Launch::make(f, dim3(tiles, (n + kRowTile - 1) / kRowTile), dim3(kProjWaves * kWave), 0, KC_PROJ, a);
     }
 };
 
@@ -463,6 +601,7 @@ void RwkvStep::build(Pool& pool, const StepIO& io, std::vector<Launch>& out, int
     for (int k = 0; k < 4; k++) loral[k] = pool.loral + z.lora_off[k] + g0 * z.ks_lora[k] * limb_group;
     const size_t state_stride = (size_t)D.nl * D.d;
     const size_t wkv_layer = (size_t)D.h * D.n * D.n;
+    const int tt = proj_tiles_for(n, io.n_all ? io.n_all : n);
     for (uint32_t l = 0; l < D.nl; l++) {
         const RLayer& L = m.layers[l];
         ShiftArgs s1{p.x, L.ln1_w, L.ln1_b, p.x_att + (size_t)l * d, state_stride, p.slots, p.scap, 6, {}, {}, z.ks_d, d};
@@ -472,7 +611,7 @@ void RwkvStep::build(Pool& pool, const StepIO& io, std::vector<Launch>& out, int
         }
         out.push_back(Launch::make(shift_fn(s1.nmix), dim3(n), dim3(kBlock), 0, KC_SHIFT, s1));
         // receptance <- x_r, key <- x_k, value <- x_v; LoRA inputs x_w, x_a, x_g, x_v
-        ProjBuilder p1;
+        ProjBuilder p1(tt);
         p1.add(L.r, mixl[0], PROJ_STORE, ACT_NONE, p.rkv, 3 * d, nullptr, 0);
         p1.add(L.k, mixl[2], PROJ_STORE, ACT_NONE, p.rkv + d, 3 * d, nullptr, 0);
         p1.add(L.v, mixl[3], PROJ_STORE, ACT_NONE, p.rkv + 2 * d, 3 * d, nullptr, 0);
@@ -481,7 +620,7 @@ void RwkvStep::build(Pool& pool, const StepIO& io, std::vector<Launch>& out, int
         p1.add(L.l1[kLoraG], mixl[5], PROJ_LIMBS, ACT_SIGMOID, nullptr, 0, loral[kLoraG], z.ks_lora[kLoraG]);
         if (l != 0) p1.add(L.l1[kLoraV], mixl[3], PROJ_LIMBS, ACT_NONE, nullptr, 0, loral[kLoraV], z.ks_lora[kLoraV]);
         out.push_back(p1.launch(n));
-        ProjBuilder p2;
+        ProjBuilder p2(tt);
         for (int k = 0; k < 4; k++)
             if (k != kLoraV || l != 0) p2.add(L.l2[k], loral[k], PROJ_STORE, ACT_NONE, p.lorad + k * d, 4 * d, nullptr, 0);
         out.push_back(p2.launch(n));
@@ -489,17 +628,17 @@ void RwkvStep::build(Pool& pool, const StepIO& io, std::vector<Launch>& out, int
                    p.wkv + l * wkv_layer, (size_t)D.nl * wkv_layer, p.vfirst, p.slots, p.scap, p.gatedl, z.ks_d, d,
                    (int)l, (int)D.g1k};
         out.push_back(Launch::make((const void*)k_rwkv_wkv, dim3(D.h, n), dim3(kHead), 0, KC_WKV, wa));
-        ProjBuilder po;
+        ProjBuilder po(tt);
         po.add(L.o, p.gatedl, PROJ_RESID, ACT_NONE, p.x, d, nullptr, 0);
         out.push_back(po.launch(n));
         ShiftArgs s2{p.x, L.ln2_w, L.ln2_b, p.x_ffn + (size_t)l * d, state_stride, p.slots, p.scap, 1, {}, {}, z.ks_d, d};
         s2.mix[0] = L.ffn_x_k;
         s2.out[0] = p.ffnl;
         out.push_back(Launch::make(shift_fn(s2.nmix), dim3(n), dim3(kBlock), 0, KC_SHIFT, s2));
-        ProjBuilder pk;
+        ProjBuilder pk(tt);
         pk.add(L.fk, p.ffnl, PROJ_LIMBS, ACT_RELU2, nullptr, 0, p.actl, z.ks_f);
         out.push_back(pk.launch(n));
-        ProjBuilder pv;
+        ProjBuilder pv(tt);
         pv.add(L.fv, p.actl, PROJ_RESID, ACT_NONE, p.x, d, nullptr, 0);
         out.push_back(pv.launch(n));
     }

@@ -194,3 +194,26 @@ def test_rwkv_split_steps_are_bitwise_identical(rwkv_models, monkeypatch, split,
     monkeypatch.setenv("REDUKT_GPU_SPLIT", str(split))
     got = _rwkv_steps(rwkv_models["g1k"], profile, 50, 3, 17, probs)
     assert np.array_equal(bits(ref), bits(got))
+
+
+@pytest.mark.parametrize("tiles", [2, 4])
+@pytest.mark.parametrize("profile", [0, 1, 2])
+def test_rwkv_projection_tiles_per_workgroup_are_bitwise_identical(rwkv_models, monkeypatch, tiles, profile):
+    # Projection workgroups covering several row tiles (one load of the activation
+    # fragments for all of them; segments of one tile, LoRA ranks below 16 rows, included)
+    # give every stream the bits of one tile per workgroup.
+    monkeypatch.setenv("REDUKT_GPU_SPLIT", "1")
+    monkeypatch.setenv("REDUKT_GPU_PROJ_TILES", "1")
+    ref = _rwkv_steps(rwkv_models["g1k"], profile, 50, 3, 19, True)
+    monkeypatch.setenv("REDUKT_GPU_PROJ_TILES", str(tiles))
+    got = _rwkv_steps(rwkv_models["g1k"], profile, 50, 3, 19, True)
+    assert np.array_equal(bits(ref), bits(got))
+
+
+@pytest.mark.parametrize("tiles", [2, 4])
+def test_rwkv7_0_1b_projection_tiles_bitwise(wide_model, monkeypatch, tiles):
+    monkeypatch.setenv("REDUKT_GPU_PROJ_TILES", "1")
+    ref = _rwkv_steps(wide_model, 2, 20, 2, 23)
+    monkeypatch.setenv("REDUKT_GPU_PROJ_TILES", str(tiles))
+    got = _rwkv_steps(wide_model, 2, 20, 2, 23)
+    assert np.array_equal(bits(ref), bits(got))
