@@ -468,6 +468,24 @@ struct WkvArgs {
 
 constexpr int kHead = 64;
 
+// The sum of v over the 64 lanes of a wave, in every lane: lanes paired by DPP inside each
+// row of 16 (i ^ 1, i ^ 2, then the mirrored quads and halves; each add pairs equal partial
+// sums in both orders, which IEEE addition makes equal), then the four row sums
+// (r0 + r1) + (r2 + r3).  Every lane must be active.  Four VALU moves and four lane reads,
+// against six LDS permutes for a butterfly over __shfl_xor.
+__device__ __forceinline__ float wave_sum_rows(float v) {
+    v = v + dpp_move<kDppQuadXor1>(v);
+    v = v + dpp_move<kDppQuadXor2>(v);
+    v = v + dpp_move<0x141>(v);  // row_half_mirror: lane i reads lane 7 - i of its half-row
+    v = v + dpp_move<0x140>(v);  // row_mirror: lane i reads lane 15 - i of its row
+    const int b = __builtin_bit_cast(int, v);
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+    return (r0 + r1) + (r2 + r3);
+}
+
 // time_mixing_scratch steps 3-12 after the projections (model.rs:827-912) for one head of
 // one stream; lane i owns channel c = 64 h + i and row i of the head's state.
 __global__ __launch_bounds__(kHead) void k_rwkv_wkv(WkvArgs a) {
@@ -496,7 +514,7 @@ __global__ __launch_bounds__(kHead) void k_rwkv_wkv(WkvArgs a) {
     const float aa = lane_sigmoid_f(a.a0[c] + la);
     // Step 6: kk = (k * k_k) / |k * k_k| per head, 0 when the norm is <= 1e-12 (:1416-1424)
     const float kk0 = k * a.k_k[c];
-    const float norm = sqrtf(wave_sum(kk0 * kk0));
+    const float norm = sqrtf(wave_sum_rows(kk0 * kk0));
     const float kk = kk0 * (norm > 1e-12f ? 1.0f / norm : 0.0f);
     // Step 7
     const float kmod = k * (1.0f + (aa - 1.0f) * a.k_a[c]);
@@ -515,23 +533,27 @@ __global__ __launch_bounds__(kHead) void k_rwkv_wkv(WkvArgs a) {
     skmod[i] = kmod;
     sr[i] = r;
     __syncthreads();
-    float tt = 0.0f;
+    // The two state dot products with four partial sums (column j into sum j % 4), added
+    // (p0 + p1) + (p2 + p3): four short chains instead of one of 64.
+    float tp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int j = 0; j < kHead; j++) tt += S[j] * snegkk[j];
+    for (int j = 0; j < kHead; j++) tp[j % 4] += S[j] * snegkk[j];
+    const float tt = (tp[0] + tp[1]) + (tp[2] + tp[3]);
 #pragma unroll
     for (int j = 0; j < kHead; j++) S[j] = S[j] * sw[j] + tt * skka[j] + vout * skmod[j];
-    float o = 0.0f;
+    float op[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int j = 0; j < kHead; j++) o += S[j] * sr[j];
+    for (int j = 0; j < kHead; j++) op[j % 4] += S[j] * sr[j];
+    const float o = (op[0] + op[1]) + (op[2] + op[3]);
 #pragma unroll
     for (int q = 0; q < kHead / 4; q++) sbase[q * kHead + i] = make_float4(S[4 * q], S[4 * q + 1], S[4 * q + 2], S[4 * q + 3]);
     // Step 10: GroupNorm over the head, eps 64e-5 (group_norm_into :1400-1414)
-    const float mean = wave_sum(o) / (float)kHead;
-    const float var = wave_sum((o - mean) * (o - mean)) / (float)kHead;
+    const float mean = wave_sum_rows(o) / (float)kHead;
+    const float var = wave_sum_rows((o - mean) * (o - mean)) / (float)kHead;
     float on = (o - mean) * (1.0f / sqrtf(var + 64e-5f)) * a.ln_x_w[c] + a.ln_x_b[c];
     // Step 11: bonus = sum over the head of r * k * r_k (k_mod for g1k models), times v_out
     const float ksrc = a.g1k ? kmod : k;
-    on += wave_sum(r * ksrc * a.r_k[c]) * vout;
+    on += wave_sum_rows(r * ksrc * a.r_k[c]) * vout;
     // Step 12: gate; the output projection follows as a matrix-core product
     write_limb1(a.gated, a.ks, b, c, on * g);
 }
