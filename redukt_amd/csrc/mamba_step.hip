@@ -179,11 +179,14 @@ __device__ __forceinline__ void st_hand(void* base, size_t byte_off, const T& v)
 // the previous phase's outputs are written during the same launch by workgroups on any
 // XCD: the task first requests everything that does not depend on them (weights, scales,
 // recurrent state), then waits for the phase counter and reads those outputs.  Every
-// layer of a step hands over through buffers of its own (written once per step), so no
-// L2 or L1 holds a line of them from before the producers wrote it: a consumer's first
-// read misses and fetches the written-through (kStAux = sc1) value from the coherence
-// point.  The producers' stores were complete (s_waitcnt) before the counter was raised,
-// and the counter is read with device-scope atomics.
+// layer of a step hands over through buffers of its own (written once per step), the
+// producers write through to the coherence point (kStAux = sc1), their stores are complete
+// (s_waitcnt) before the counter is raised, and the counter is read with device-scope
+// atomics.  The consumers read with device scope too (kAux = sc1): some lines have writers
+// on several XCDs (a stream's RMS partials of all 48 out_proj tiles, the gated limbs of
+// 8 streams written by 4 scan tasks), and the L2 of an XCD that wrote part of such a line
+// may hold it with the other XCDs' bytes from before they were written (default loads
+// read such stale bytes now and then: one stream's logits differed at 150 streams).
 struct NoWait {
     static constexpr bool kFlow = false;
     static constexpr int kAux = kCached;
@@ -204,7 +207,7 @@ constexpr uint32_t kFlowSlices = 8;
 
 struct FlowWait {
     static constexpr bool kFlow = true;
-    static constexpr int kAux = kCached;
+    static constexpr int kAux = kCoherent;
     static constexpr int kStAux = kCoherent;
     const uint32_t* counter;   // slice 0 of the phase counter; null: nothing to wait for
     uint32_t target;           // sum of the slices when the phase is complete
@@ -1831,6 +1834,7 @@ struct FlowArgs {
     uint32_t* err;
     uint32_t mi_tasks, cb, mo_tasks;  // in_proj row blocks, scan channel blocks, out_proj row tiles (per group)
     uint32_t nx;              // XCDs of the device (divides each phase's tasks per group)
+    uint32_t fixed;           // 1: static assignment (every phase has the same tasks per group and XCD)
     uint8_t xmap[16];         // XCC_ID -> XCD index 0 .. nx - 1 (0xff: not seen when the grid was planned)
 };
 
@@ -1848,6 +1852,30 @@ __global__ __launch_bounds__(kBlock) void k_xcc_map(uint32_t* map) {
 // requested when the previous task's body is done).  The hardware deals workgroups to XCDs round-robin from where
 // the previous dispatch stopped, so the block index does not name the XCD; the ticket
 // order keeps every dependency on an earlier ticket, taken by a resident workgroup.
+// Phase ph of layer l for group g: kFlowSlices counters, one per XCD.
+__device__ __forceinline__ uint32_t* flow_counter(const FlowArgs& f, uint32_t l, uint32_t ph, uint32_t g) {
+    return f.cnt + ((size_t)(l * 3 + ph) * f.groups + g) * kFlowSlices * kFlowCounterStride;
+}
+
+// Task `task` of phase `phase` of layer l for stream group g: its wait and its body.
+template <bool Q8S, bool FAST>
+__device__ __forceinline__ void flow_task(const FlowArgs& f, const FlowLayer& L, uint32_t l, uint32_t phase, uint32_t g,
+                                          uint32_t task) {
+    constexpr uint32_t kSpt = kFlowScanSpt;
+    if (phase == 0) {
+        const FlowWait w{l > 0 ? flow_counter(f, l - 1, 2, g) : nullptr, f.mo_tasks, f.err};
+        mix_in_body<true, Q8S, true, false, kInFixedPairs, 4>(L.mi, task, g, w);
+    } else if (phase == 1) {
+        // kSpt streams per task: the tasks of streams past n (a last, partial group) only count
+        const uint32_t sy = g * (kRowTile / kSpt) + task / f.cb;
+        const FlowWait w{flow_counter(f, l, 0, g), f.mi_tasks, f.err};
+        if (sy * kSpt < L.sc.n) scan_body<Q8S, FAST, 48, 48, kSpt>(L.sc, sy, task % f.cb, w);
+    } else {
+        const FlowWait w{flow_counter(f, l, 1, g), kRowTile / kSpt * f.cb, f.err};
+        mix_out_body<true, 1, true, kWaves>(L.mo, task, g, w);
+    }
+}
+
 template <bool Q8S, bool FAST>
 __global__ __launch_bounds__(kBlock, 2) void k_flow(FlowArgs f) {
     __shared__ uint32_t s_next;
@@ -1867,6 +1895,28 @@ __global__ __launch_bounds__(kBlock, 2) void k_flow(FlowArgs f) {
     const FlowLayerK layers = (FlowLayerK)f.layers;
     if (threadIdx.x == 0) s_next = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
+    if (f.fixed) {
+        // Static assignment (mi == sc == mo): the workgroup's ticket s names its group,
+        // s / mi, and its task, x + nx (s % mi), in every phase of every layer; it runs them
+        // layer by layer, waiting only for its own group's counters, so each phase of a group
+        // runs all its tasks at once.  Tickets past the groups' tasks exit.  Every group's
+        // tasks are held by resident workgroups (the grid is the device's full occupancy and
+        // the host planned G mi <= grid / nx).
+        const uint32_t slot = __builtin_amdgcn_readfirstlane(s_next);
+        if (slot >= G * mi) return;
+        const uint32_t g = slot / mi, task = x + nx * (slot % mi);
+        for (uint32_t l = 0; l < f.nl; l++)
+            for (uint32_t phase = 0; phase < 3; phase++) {
+                flow_task<Q8S, FAST>(f, *(const FlowLayer*)(layers + l), l, phase, g, task);
+                // every store of the task is complete at the coherence point before the counter says so
+                __builtin_amdgcn_s_waitcnt(0);
+                __syncthreads();
+                if (threadIdx.x == 0)
+                    __hip_atomic_fetch_add(flow_counter(f, l, phase, g) + (x % kFlowSlices) * kFlowCounterStride, 1u,
+                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        return;
+    }
     for (uint32_t i = s_next; i < total;) {
         const uint32_t l = i / per_layer;
         uint32_t r = i % per_layer;
@@ -1880,22 +1930,7 @@ __global__ __launch_bounds__(kBlock, 2) void k_flow(FlowArgs f) {
             phase = 2, g = r / mo, k = r % mo;
         }
         const uint32_t task = x + nx * k;
-        auto counter = [&](uint32_t ll, uint32_t ph) {
-            return f.cnt + ((size_t)(ll * 3 + ph) * G + g) * kFlowSlices * kFlowCounterStride;
-        };
-        const FlowLayer& L = *(const FlowLayer*)(layers + l);
-        if (phase == 0) {
-            const FlowWait w{l > 0 ? counter(l - 1, 2) : nullptr, f.mo_tasks, f.err};
-            mix_in_body<true, Q8S, true, false, kInFixedPairs, 4>(L.mi, task, g, w);
-        } else if (phase == 1) {
-            // kSpt streams per task: the tasks of streams past n (a last, partial group) only count
-            const uint32_t sy = g * (kRowTile / kSpt) + task / f.cb;
-            const FlowWait w{counter(l, 0), f.mi_tasks, f.err};
-            if (sy * kSpt < L.sc.n) scan_body<Q8S, FAST, 48, 48, kSpt>(L.sc, sy, task % f.cb, w);
-        } else {
-            const FlowWait w{counter(l, 1), kRowTile / kSpt * f.cb, f.err};
-            mix_out_body<true, 1, true, kWaves>(L.mo, task, g, w);
-        }
+        flow_task<Q8S, FAST>(f, *(const FlowLayer*)(layers + l), l, phase, g, task);
         // The next ticket is taken only once this task's body is done, so a workgroup never
         // holds two tasks at once (two of one phase would run one after the other); its
         // round trip overlaps the drain of the task's stores.
@@ -1905,8 +1940,8 @@ __global__ __launch_bounds__(kBlock, 2) void k_flow(FlowArgs f) {
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         if (threadIdx.x == 0) {
-            __hip_atomic_fetch_add(counter(l, phase) + (x % kFlowSlices) * kFlowCounterStride, 1u, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_fetch_add(flow_counter(f, l, phase, g) + (x % kFlowSlices) * kFlowCounterStride, 1u,
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             s_next = ahead;
         }
         __syncthreads();
@@ -2831,10 +2866,30 @@ FlowRegion flow_region_of(const ModelView& m, uint32_t n, void* dev, uint32_t l)
 // Workgroups per CU of the persistent kernel: REDUKT_GPU_FLOW_WGS, else one below 512
 // streams (a second workgroup on a CU slows both: 0.87 vs 1.10 ms per step at 128
 // streams) and two from there (3.2 vs 5.0 ms at 1024), at most as many as fit.
-uint32_t flow_wgs_per_cu(uint32_t fit, uint32_t n) {
+// REDUKT_GPU_FLOW_STATIC=0: the persistent kernel keeps the ticket order even where the
+// static assignment applies.
+bool flow_static_wanted() {
+    const char* e = getenv("REDUKT_GPU_FLOW_STATIC");
+    return !(e && *e && !strcmp(e, "0"));
+}
+
+// Workgroups per CU of the persistent kernel: REDUKT_GPU_FLOW_WGS, else 2 (when 2 fit) for
+// a static assignment of slots_per_xcd > 0, else 1 below 512 streams and 2 from there.
+uint32_t flow_wgs_per_cu(uint32_t fit, uint32_t n, uint32_t slots_per_xcd) {
     const char* e = getenv("REDUKT_GPU_FLOW_WGS");
-    const uint32_t want = e && *e ? (uint32_t)strtoul(e, nullptr, 10) : (n < 512 ? 1u : 2u);
-    return std::max(1u, std::min(want, fit));
+    if (e && *e) return std::max(1u, std::min((uint32_t)strtoul(e, nullptr, 10), fit));
+    return std::max(1u, std::min(slots_per_xcd || n >= 512 ? 2u : 1u, fit));
+}
+
+// The static assignment's task slots per XCD (0: it does not apply): every phase has the
+// same number of tasks per group, a multiple of the XCD count.
+uint32_t flow_static_slots(const ModelView& m, uint32_t n, uint32_t nx) {
+    const Dims& D = *m.dims;
+    const DLayer& L0 = m.layers[0];
+    const uint32_t mi = (uint32_t)((int)D.di / (kRowTile * 4) + L0.in_z.rt / 4);
+    const uint32_t sc = kRowTile / kFlowScanSpt * (D.di / kBlock), mo = (uint32_t)L0.out_proj.rt;
+    if (!flow_static_wanted() || nx == 0 || mi != sc || sc != mo || mi % nx) return 0;
+    return (n + kRowTile - 1) / kRowTile * (mi / nx);
 }
 
 }  // namespace
@@ -2859,7 +2914,13 @@ hipError_t MambaStep::flow_init(Pool& p, uint32_t n, void* dev, FlowShape* shape
         fprintf(stderr, "[redukt-gpu-hip] persistent step kernel off: %d workgroups per CU fit, %d CUs\n", fit, cus);
         return hipSuccess;
     }
-    const uint32_t g = flow_wgs_per_cu((uint32_t)fit, n) * (uint32_t)cus;
+    // The static assignment where one workgroup per CU cannot hold its slots (there the ticket
+    // order would run each phase in several rounds) and two can: measured on Mamba-130M int8,
+    // µs per step static / ticket order: 128 streams 715 / 757; one stream 431 / 407, 16
+    // streams 488 / 477, 64 streams 520 / 507 (where one per CU holds them).
+    const uint32_t slots = flow_static_slots(m, n, kXcds);
+    const bool fixed = slots > (uint32_t)cus / kXcds && fit >= 2 && slots <= 2u * (uint32_t)cus / kXcds;
+    const uint32_t g = flow_wgs_per_cu((uint32_t)fit, n, fixed ? slots : 0u) * (uint32_t)cus;
     // The device's XCDs, from one launch of the grid: the map goes to the counter area
     // (at least nl * 3 * 32 >= g words; the step's embedding clears it before every use).
     uint32_t* map = (uint32_t*)((unsigned char*)dev + flow_table_bytes(D.nl));
@@ -2908,7 +2969,9 @@ hipError_t MambaStep::flow_init(Pool& p, uint32_t n, void* dev, FlowShape* shape
     RDK_TRY(hipMemcpy(dev, table.data(), table.size() * sizeof(FlowLayer), hipMemcpyHostToDevice));
     sh.grid = g;
     *shape = sh;
-    fprintf(stderr, "[redukt-gpu-hip] persistent step kernel: %u streams, %u workgroups on %u XCDs\n", n, g, sh.nx);
+    sh.fixed = fixed && flow_static_slots(m, n, sh.nx) == slots && slots <= g / sh.nx ? 1u : 0u;
+    fprintf(stderr, "[redukt-gpu-hip] persistent step kernel: %u streams, %u workgroups on %u XCDs, %s\n", n, g, sh.nx,
+            sh.fixed ? "static tasks" : "ticket order");
     return hipSuccess;
 }
 
@@ -2931,7 +2994,7 @@ void MambaStep::build_flow(Pool& p, const StepIO& io, void* dev, const FlowShape
     const DLayer& L0 = m.layers[0];
     FlowArgs fa{(const FlowLayer*)dev, D.nl, groups, cnt, io.err,
                 (uint32_t)((int)D.di / (kRowTile * 4) + L0.in_z.rt / 4), D.di / kBlock, (uint32_t)L0.out_proj.rt,
-                shape.nx, {}};
+                shape.nx, shape.fixed, {}};
     memcpy(fa.xmap, shape.xmap, sizeof(fa.xmap));
     Launch f = Launch::make(flow_fn(m), dim3(shape.grid), dim3(kBlock), mix_in_lds_bytes(ks_x, true, 4), KC_FLOW, fa);
     f.coop = true;

@@ -279,6 +279,7 @@ struct Launch;
 // the device's XCDs, as XCC_ID -> index 0 .. nx - 1 (0xff where no workgroup was seen).
 struct FlowShape {
     uint32_t grid = 0, nx = 0;
+    uint32_t fixed = 0;   // 1: static task assignment (see k_flow)
     uint8_t xmap[16] = {};
 };
 
