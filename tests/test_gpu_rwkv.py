@@ -217,3 +217,29 @@ def test_rwkv7_0_1b_projection_tiles_bitwise(wide_model, monkeypatch, tiles):
     monkeypatch.setenv("REDUKT_GPU_PROJ_TILES", str(tiles))
     got = _rwkv_steps(wide_model, 2, 20, 2, 23)
     assert np.array_equal(bits(ref), bits(got))
+
+
+@pytest.mark.parametrize("profile", [0, 2])
+def test_rwkv_batch_invariance_across_split_sizes(rwkv_models, profile):
+    # Default settings: below 96 streams one part with one projection tile per workgroup,
+    # from 96 two parts with four; a stream's bits depend on neither its batch, its
+    # position nor its slot.
+    with ffi.PluginBackend(rwkv_models["small"], profile=profile) as be:
+        v = be.vocab
+        seq = [(53 * i + 7) % v for i in range(4)]
+        be.batch_init(140)
+        alone = []
+        for t in seq:
+            g = np.empty((1, v), np.float32)
+            be.forward_batch([139], [t], g)
+            alone.append(g[0].copy())
+        rng = np.random.default_rng(4)
+        for n, pos in ((95, 94), (96, 0), (113, 64), (139, 100)):
+            be.batch_reset(None)
+            slots = [int(s) for s in rng.permutation(139)[:n]]
+            for i, t in enumerate(seq):
+                toks = [int(x) for x in rng.integers(0, v, n)]
+                toks[pos] = t
+                g = np.empty((n, v), np.float32)
+                be.forward_batch(slots, toks, g)
+                assert np.array_equal(bits(g[pos]), bits(alone[i])), (n, pos, i)
