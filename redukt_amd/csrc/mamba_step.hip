@@ -1851,11 +1851,6 @@ __global__ __launch_bounds__(kBlock) void k_xcc_map(uint32_t* map) {
     if (threadIdx.x == 0) map[blockIdx.x] = xcc_id();
 }
 
-// Which workgroup runs a task is decided at run time: the workgroups of XCD x take the
-// tasks of x's list in order from x's ticket counter (one device-scope atomic per task,
-// requested when the previous task's body is done).  The hardware deals workgroups to XCDs round-robin from where
-// the previous dispatch stopped, so the block index does not name the XCD; the ticket
-// order keeps every dependency on an earlier ticket, taken by a resident workgroup.
 // Phase ph of layer l for group g: kFlowSlices counters, one per XCD.
 __device__ __forceinline__ uint32_t* flow_counter(const FlowArgs& f, uint32_t l, uint32_t ph, uint32_t g) {
     return f.cnt + ((size_t)(l * 3 + ph) * f.groups + g) * kFlowSlices * kFlowCounterStride;
@@ -1880,6 +1875,13 @@ __device__ __forceinline__ void flow_task(const FlowArgs& f, const FlowLayer& L,
     }
 }
 
+// Which workgroup runs a task is decided at run time: the workgroups of XCD x take the
+// tasks of x's list in order from x's ticket counter (one device-scope atomic per task,
+// requested when the previous task's body is done), or, with f.fixed, one ticket each that
+// names a group and a task index for the whole step.  The hardware deals workgroups to
+// XCDs round-robin from where the previous dispatch stopped, so the block index does not
+// name the XCD; the ticket order keeps every dependency on an earlier ticket, taken by a
+// resident workgroup.
 template <bool Q8S, bool FAST>
 __global__ __launch_bounds__(kBlock, 2) void k_flow(FlowArgs f) {
     __shared__ uint32_t s_next;
