@@ -243,3 +243,29 @@ def test_rwkv_batch_invariance_across_split_sizes(rwkv_models, profile):
                 g = np.empty((n, v), np.float32)
                 be.forward_batch(slots, toks, g)
                 assert np.array_equal(bits(g[pos]), bits(alone[i])), (n, pos, i)
+
+
+def test_rwkv7_0_1b_q8row_64_streams_2048_tokens(wide_model):
+    # The RWKV-7 int8 per-row workload at its full horizon: 64 lockstep streams of uniform
+    # byte ids for 2,048 tokens (RWKV-7 0.1B layers, vocabulary cut to 4,096), every 4th
+    # stream (16 of them) compared with the oracle at every token within the logit and
+    # probability tolerances; drift in the 64x64 WKV state or the token-shift state would
+    # show as a growing error.  About a minute of oracle steps on 16 host threads.
+    n, steps = 64, 2048
+    watch = list(range(0, n, 4))
+    rng = np.random.default_rng(2048)
+    toks = rng.integers(0, 256, size=(steps, n))
+    with ffi.PluginBackend(wide_model, profile=2) as be:
+        orc = O.RwkvOracle(wide_model, 2, cap=len(watch))
+        be.batch_init(n)
+        g = np.empty((n, be.vocab), np.float32)
+        worst = 0.0
+        for t in range(steps):
+            row = [int(x) for x in toks[t]]
+            be.forward_batch(list(range(n)), row, g)
+            c = orc.forward(list(range(len(watch))), [row[s] for s in watch])
+            err, _ = assert_parity(g[watch], c, f"step {t}")
+            worst = max(worst, err)
+            if t % 256 == 255:
+                print(f"step {t + 1}: max |dlogit| so far {worst:.2e}", flush=True)
+        orc.close()
