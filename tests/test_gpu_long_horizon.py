@@ -11,7 +11,13 @@ resets on its own schedule (MambaState::maybe_periodic_reset, model.rs:315-320).
   horizon, and after the reset the stream's logits equal a fresh stream's fed the same
   tokens, bit for bit.
 
-Each test is about a minute of single-stream oracle steps on 16 host threads.
+* cfg3's workload at its full horizon: F32, 128 lockstep streams x 2,048 tokens with the
+  probability vector handed back every step, 8 streams against the oracle's softmax at every
+  token (L1 <= 1e-4).
+* cfg5's workload at its full horizon: int8 per-row, 1,024 lockstep streams x 512 tokens in
+  two parts of 512, 8 streams across both parts against the oracle at every token.
+
+Each test is up to about a minute of oracle steps on 16 host threads.
 """
 import numpy as np
 import pytest
@@ -92,3 +98,58 @@ def test_mamba130m_q8row_32_streams_4100_tokens_across_the_reset(full_model):
         assert np.array_equal(one[0].view(np.uint32), last.view(np.uint32))
     orc.close()
     print(f"stream {watch}: worst max|dlogit|={worst[0]:.3e} L1={worst[1]:.3e} (token {worst[2]})")
+
+
+def test_mamba130m_f32_128_streams_2048_tokens_probability_vector(full_model):
+    # cfg3's workload at its full horizon: Mamba-130M F32, 128 lockstep streams x 2,048
+    # Zipf(1.1) tokens, the probability vector handed back every step; every 16th stream
+    # (8 of them) against the oracle's softmax at every token (L1 <= 1e-4, rows summing to 1).
+    n, steps = 128, 2048
+    watch = list(range(0, n, 16))
+    toks = synth.zipf_tokens(np.random.default_rng(303), rbin.MAMBA_130M.vocab, (steps, n))
+    orc = O.MambaOracle(full_model, 0, cap=len(watch))
+    print(f"F32, {n} streams x {steps} tokens, probabilities of streams {watch} against the oracle", flush=True)
+    with ffi.PluginBackend(full_model, profile=0) as be:
+        be.batch_init(n)
+        p = np.empty((n, be.vocab), np.float32)
+        worst = 0.0
+        for t in range(steps):
+            tl = [int(x) for x in toks[t]]
+            be.forward_batch(list(range(n)), tl, p, probs=True)
+            c = orc.forward(list(range(len(watch))), [tl[s] for s in watch])
+            ref = np.stack([O.softmax(r) for r in c]).astype(np.float64)
+            got = p[watch].astype(np.float64)
+            l1 = np.abs(got - ref).sum(axis=1)
+            assert np.all(l1 <= TOL_L1), (t, float(l1.max()))
+            assert np.all(np.abs(got.sum(axis=1) - 1.0) < 1e-5), t
+            worst = max(worst, float(l1.max()))
+            if t % 512 == 511:
+                print(f"token {t + 1}: worst L1 so far {worst:.2e}", flush=True)
+    orc.close()
+
+
+def test_mamba130m_q8row_1024_streams_512_tokens(full_model):
+    # cfg5's workload at its full horizon: Mamba-130M int8 per-row on every projection,
+    # 1,024 lockstep streams x 512 Zipf(1.1) tokens (two parts of 512 streams, every
+    # projection a 512-column skinny GEMM); 8 streams spread over both parts against the
+    # oracle at every token.
+    n, steps = 1024, 512
+    watch = [0, 137, 300, 511, 512, 700, 901, 1023]
+    toks = synth.zipf_tokens(np.random.default_rng(505), rbin.MAMBA_130M.vocab, (steps, n))
+    orc = O.MambaOracle(full_model, Q8ROW_ALL, cap=len(watch))
+    print(f"int8 per-row, {n} streams x {steps} tokens, streams {watch} against the oracle", flush=True)
+    with ffi.PluginBackend(full_model, profile=Q8ROW_ALL) as be:
+        be.batch_init(n)
+        g = np.empty((n, be.vocab), np.float32)
+        worst = (0.0, 0.0)
+        for t in range(steps):
+            tl = [int(x) for x in toks[t]]
+            be.forward_batch(list(range(n)), tl, g)
+            c = orc.forward(list(range(len(watch))), [tl[s] for s in watch])
+            err = float(np.max(np.abs(g[watch].astype(np.float64) - c)))
+            l1 = float(np.max(np.abs(probs64(g[watch]) - probs64(c)).sum(axis=-1)))
+            assert err <= TOL_ABS and l1 <= TOL_L1, f"token {t}: max|dlogit|={err:.3e} L1={l1:.3e}"
+            worst = (max(worst[0], err), max(worst[1], l1))
+            if t % 128 == 127:
+                print(f"token {t + 1}: worst max|dlogit| {worst[0]:.2e} L1 {worst[1]:.2e}", flush=True)
+    orc.close()
