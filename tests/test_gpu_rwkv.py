@@ -245,8 +245,9 @@ def test_rwkv_batch_invariance_across_split_sizes(rwkv_models, profile):
                 assert np.array_equal(bits(g[pos]), bits(alone[i])), (n, pos, i)
 
 
-def test_rwkv7_0_1b_q8row_64_streams_2048_tokens(wide_model):
-    # The RWKV-7 int8 per-row workload at its full horizon: 64 lockstep streams of uniform
+@pytest.mark.parametrize("profile", [0, 2])
+def test_rwkv7_0_1b_64_streams_2048_tokens(wide_model, profile):
+    # The RWKV-7 workload (F32 and int8 per-row) at its full horizon: 64 lockstep streams of uniform
     # byte ids for 2,048 tokens (RWKV-7 0.1B layers, vocabulary cut to 4,096), every 4th
     # stream (16 of them) compared with the oracle at every token within the logit and
     # probability tolerances; drift in the 64x64 WKV state or the token-shift state would
@@ -255,8 +256,8 @@ def test_rwkv7_0_1b_q8row_64_streams_2048_tokens(wide_model):
     watch = list(range(0, n, 4))
     rng = np.random.default_rng(2048)
     toks = rng.integers(0, 256, size=(steps, n))
-    with ffi.PluginBackend(wide_model, profile=2) as be:
-        orc = O.RwkvOracle(wide_model, 2, cap=len(watch))
+    with ffi.PluginBackend(wide_model, profile=profile) as be:
+        orc = O.RwkvOracle(wide_model, profile, cap=len(watch))
         be.batch_init(n)
         g = np.empty((n, be.vocab), np.float32)
         worst = 0.0
