@@ -160,6 +160,16 @@ int32_t redukt_backend_forward_batch_probs(uint32_t n_streams, const uint32_t* s
 int32_t redukt_backend_forward_batch_cdf(uint32_t n_streams, const uint32_t* slots, const uint32_t* tokens,
                                          uint32_t* out_cdf, uint32_t cdf_len);
 
+/* forward_batch_cdf for a caller that knows each stream's next symbol (compression): the
+ * same CDF rows are computed on the device, and only what the range coder reads of each
+ * (coder.rs:163-177) comes back: out_bounds[3b .. 3b + 2] = cdf[next_syms[b]],
+ * cdf[next_syms[b] + 1] and cdf[vocab_size], the total.  12 bytes per stream instead of
+ * 4 (vocab + 1).  vocab_size must be the model's; next_syms[b] < vocab_size.  Same
+ * validation and state rules as forward_batch.  No reference counterpart (an extension of
+ * the CDF entry point above). */
+int32_t redukt_backend_forward_batch_cdf_sym(uint32_t n_streams, const uint32_t* slots, const uint32_t* tokens,
+                                             const uint32_t* next_syms, uint32_t* out_bounds, uint32_t vocab_size);
+
 /* The device CDF on caller logits: d_logits [rows][n] f32 -> d_cdf [rows][n + 1] u32,
  * both device pointers, stream-ordered on redukt_backend_stream() (the call does not
  * wait).  1 <= n < 2^24.  For tests and for callers that hold logits on the device. */

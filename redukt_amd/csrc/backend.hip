@@ -1253,9 +1253,11 @@ int32_t redukt_backend_forward_batch_probs(uint32_t n_streams, const uint32_t* s
 // The CDF kernels' scratch (exp values and the two sums per row) and, for the host-buffer
 // entry point, the CDF rows themselves: one allocation, grown on demand (the stream is
 // synchronized before the old one is freed).
-bool cdf_space(uint32_t rows, uint32_t n, bool with_out, void** scratch, uint32_t** out) {
+bool cdf_space(uint32_t rows, uint32_t n, bool with_out, void** scratch, uint32_t** out, uint32_t** pick = nullptr) {
     const size_t sb = (cdf_scratch_bytes(rows, n) + 255) & ~(size_t)255;
-    const size_t need = sb + (with_out ? (size_t)rows * (n + 1) * 4 : 0);
+    const size_t ob = with_out ? ((size_t)rows * (n + 1) * 4 + 255) & ~(size_t)255 : 0;
+    // pick: the next symbols (rows u32), then the coder's three values per row
+    const size_t need = sb + ob + (pick ? (size_t)rows * 4 * 4 : 0);
     if (need > G.cdf_bytes) {
         if (G.cdf_mem) {
             if (hipStreamSynchronize(G.stream) != hipSuccess) return false;
@@ -1271,6 +1273,7 @@ bool cdf_space(uint32_t rows, uint32_t n, bool with_out, void** scratch, uint32_
     }
     *scratch = G.cdf_mem;
     if (out) *out = (uint32_t*)((unsigned char*)G.cdf_mem + sb);
+    if (pick) *pick = (uint32_t*)((unsigned char*)G.cdf_mem + sb + ob);
     return true;
 }
 
@@ -1299,6 +1302,41 @@ int32_t redukt_backend_forward_batch_cdf(uint32_t n_streams, const uint32_t* slo
         cdf_launch(p.out, n_streams, V, scratch, d_cdf, G.stream) != hipSuccess)
         return BACKEND_FORWARD_FAILED;
     if (!copy_out(p, out_cdf, d_cdf, sizeof(uint32_t) * n_streams * (size_t)(V + 1))) return BACKEND_FORWARD_FAILED;
+    return BACKEND_OK;
+}
+
+int32_t redukt_backend_forward_batch_cdf_sym(uint32_t n_streams, const uint32_t* slots, const uint32_t* tokens,
+                                             const uint32_t* next_syms, uint32_t* out_bounds, uint32_t vocab_size) {
+    if (!G.ready || G.batch.cap == 0) return BACKEND_INIT_FAILED;
+    const uint32_t V = G.kind == kKindRwkv ? G.rdims.vocab : G.dims.vocab;
+    if (vocab_size != V || n_streams > G.batch.cap || V >= (1u << 24)) return BACKEND_INVALID_ARGUMENT;
+    if (n_streams == 0) return BACKEND_OK;
+    if (!slots || !tokens || !next_syms || !out_bounds) return BACKEND_INVALID_ARGUMENT;
+    Pool& p = G.batch;
+    memset(p.seen, 0, p.cap);
+    for (uint32_t b = 0; b < n_streams; b++) {
+        if (slots[b] >= p.cap || p.seen[slots[b]] || tokens[b] >= V || next_syms[b] >= V) return BACKEND_INVALID_ARGUMENT;
+        p.seen[slots[b]] = 1;
+    }
+    void* scratch = nullptr;
+    uint32_t *d_cdf = nullptr, *d_pick = nullptr;
+    if (!cdf_space(n_streams, V, true, &scratch, &d_cdf, &d_pick)) return BACKEND_FORWARD_FAILED;
+    uint32_t* const d_sym = d_pick;
+    uint32_t* const d_bounds = d_pick + n_streams;
+    memcpy(p.h_slots, slots, sizeof(uint32_t) * n_streams);
+    memcpy(p.h_slots + n_streams, tokens, sizeof(uint32_t) * n_streams);
+    if (hipMemcpyAsync(p.d_slots, p.h_slots, sizeof(uint32_t) * 2 * n_streams, hipMemcpyHostToDevice, G.stream) !=
+            hipSuccess ||
+        hipMemcpyAsync(d_sym, next_syms, sizeof(uint32_t) * n_streams, hipMemcpyHostToDevice, G.stream) != hipSuccess)
+        return BACKEND_FORWARD_FAILED;
+    if (run_step(p, n_streams, p.d_slots, p.d_slots + n_streams, p.out, false, false) != hipSuccess ||
+        cdf_launch(p.out, n_streams, V, scratch, d_cdf, G.stream) != hipSuccess ||
+        cdf_pick_launch(d_cdf, n_streams, V, d_sym, d_bounds, G.stream) != hipSuccess)
+        return BACKEND_FORWARD_FAILED;
+    if (hipMemcpyAsync(out_bounds, d_bounds, sizeof(uint32_t) * 3 * n_streams, hipMemcpyDeviceToHost, G.stream) !=
+            hipSuccess ||
+        hipStreamSynchronize(G.stream) != hipSuccess)
+        return BACKEND_FORWARD_FAILED;
     return BACKEND_OK;
 }
 

@@ -580,4 +580,28 @@ hipError_t cdf_launch(const float* logits, uint32_t rows, uint32_t n, void* scra
     return hipGetLastError();
 }
 
+namespace {
+// What the range coder reads of row r when its next symbol is known (coder.rs:163-177 via
+// encode_symbol): out[3r] = cdf[r][sym[r]], out[3r + 1] = cdf[r][sym[r] + 1], out[3r + 2] =
+// cdf[r][n], the total.  The host checked sym[r] < n; the clamp keeps every read inside
+// the row whatever it holds.
+__global__ __launch_bounds__(256) void k_cdf_pick(const uint32_t* __restrict__ cdf, uint32_t rows, uint32_t n,
+                                                  const uint32_t* __restrict__ sym, uint32_t* __restrict__ out) {
+    const uint32_t r = blockIdx.x * 256u + threadIdx.x;
+    if (r >= rows) return;
+    const uint32_t s = min(sym[r], n - 1);
+    const uint32_t* row = cdf + (size_t)r * (n + 1);
+    out[3 * (size_t)r] = row[s];
+    out[3 * (size_t)r + 1] = row[s + 1];
+    out[3 * (size_t)r + 2] = row[n];
+}
+}  // namespace
+
+hipError_t cdf_pick_launch(const uint32_t* cdf, uint32_t rows, uint32_t n, const uint32_t* sym, uint32_t* out,
+                           hipStream_t st) {
+    if (rows == 0) return hipSuccess;
+    k_cdf_pick<<<dim3((rows + 255) / 256), dim3(256), 0, st>>>(cdf, rows, n, sym, out);
+    return hipGetLastError();
+}
+
 }  // namespace rdk

@@ -7,6 +7,7 @@
 #include <dlfcn.h>
 
 #include <chrono>
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <new>
@@ -38,6 +39,9 @@ struct PluginApi {
     int32_t (*init_ex)(const uint8_t*, int32_t, uint32_t, BackendInfo*) = nullptr;
     // optional: forward_batch that hands back each stream's CDF computed on the device
     int32_t (*forward_batch_cdf)(uint32_t, const uint32_t*, const uint32_t*, uint32_t*, uint32_t) = nullptr;
+    // optional: the same, handing back only the coder's three values for a known next symbol
+    int32_t (*forward_batch_cdf_sym)(uint32_t, const uint32_t*, const uint32_t*, const uint32_t*, uint32_t*,
+                                     uint32_t) = nullptr;
     bool v2 = false;
 
     template <class F>
@@ -59,6 +63,7 @@ struct PluginApi {
         bind(forward_batch, "redukt_backend_forward_batch");
         bind(init_ex, "redukt_backend_init_ex");
         bind(forward_batch_cdf, "redukt_backend_forward_batch_cdf");
+        bind(forward_batch_cdf_sym, "redukt_backend_forward_batch_cdf_sym");
         v2 = abi_version && batch_init && batch_reset && forward_batch && abi_version() >= 2;
         return true;
     }
@@ -110,9 +115,14 @@ struct redukt_lockstep {
     // Phase B takes the CDFs from the plugin (forward_batch_cdf, rows in forward order)
     // instead of logits; Phase A then only codes.
     bool device_cdf = false;
+    // Compression with device CDFs takes, where the plugin has it, only the three values of
+    // each row the coder reads for the lane's next symbol (forward_batch_cdf_sym): 12 bytes
+    // a stream cross from the device instead of the whole row.
+    bool sym_cdf = false;
     std::vector<float> logits;
     std::vector<uint32_t> cdf;
     std::vector<uint32_t> uniform;
+    std::vector<uint32_t> bounds;  // [row][3] of the last forward_batch_cdf_sym
 
     const uint32_t* cdf_row(uint32_t i) const { return cdf.data() + size_t(i) * (vocab + 1); }
     uint32_t* cdf_row(uint32_t i) { return cdf.data() + size_t(i) * (vocab + 1); }
@@ -131,7 +141,11 @@ struct redukt_lockstep {
         }
         int32_t st;
         uint32_t tok = 0;
-        if (job.mode == Mode::Encode) {
+        if (job.mode == Mode::Encode && l.pos > 0 && device_cdf && sym_cdf) {
+            tok = job.tokens[l.file][l.pos];
+            const uint32_t* b = bounds.data() + size_t(l.row) * 3;
+            st = tok < vocab ? l.enc.encode(b[0], b[1], b[2]) : REDUKT_CODEC_INVALID_ARG;  // as encode_symbol
+        } else if (job.mode == Mode::Encode) {
             tok = job.tokens[l.file][l.pos];
             st = l.enc.encode_symbol(tok, c, vocab);
         } else {
@@ -200,7 +214,8 @@ int32_t overall(const Job& job, const std::vector<int32_t>& st) {
 int32_t redukt_lockstep::run_lockstep(const Job& job, redukt_lockstep_stats& stats) {
     // lockstep.rs:163-265 (run_lockstep).
     std::vector<Lane> lanes(slots);
-    std::vector<uint32_t> active, fwd_slots, fwd_tokens, resets;
+    std::vector<uint32_t> active, fwd_slots, fwd_tokens, fwd_syms, resets;
+    const bool pick = job.mode == Mode::Encode && device_cdf && sym_cdf;
     active.reserve(slots);
     uint32_t next_file = 0;
     // The backbone failed: every file still in a lane and every file not yet admitted is
@@ -259,6 +274,7 @@ int32_t redukt_lockstep::run_lockstep(const Job& job, redukt_lockstep_stats& sta
         const auto tb = Clock::now();
         fwd_slots.clear();
         fwd_tokens.clear();
+        fwd_syms.clear();
         resets.clear();
         for (uint32_t i : active) {
             Lane& l = lanes[i];
@@ -271,14 +287,21 @@ int32_t redukt_lockstep::run_lockstep(const Job& job, redukt_lockstep_stats& sta
             l.row = uint32_t(fwd_slots.size());
             fwd_slots.push_back(i);
             fwd_tokens.push_back(l.next_token);
+            if (pick) {
+                // the symbol Phase A codes next (an out-of-range one is refused there, per file)
+                const uint32_t next = job.tokens[l.file][l.pos];
+                fwd_syms.push_back(next < vocab ? next : 0u);
+            }
         }
         if (!resets.empty() && api.batch_reset(resets.data(), uint32_t(resets.size())) != BACKEND_OK)
             return abort_run();
         if (!fwd_slots.empty()) {
             const uint32_t nf = uint32_t(fwd_slots.size());
-            const int32_t rc = device_cdf
-                                   ? api.forward_batch_cdf(nf, fwd_slots.data(), fwd_tokens.data(), cdf.data(), vocab + 1)
-                                   : api.forward_batch(nf, fwd_slots.data(), fwd_tokens.data(), logits.data(), vocab);
+            const int32_t rc =
+                pick ? api.forward_batch_cdf_sym(nf, fwd_slots.data(), fwd_tokens.data(), fwd_syms.data(), bounds.data(),
+                                                 vocab)
+                : device_cdf ? api.forward_batch_cdf(nf, fwd_slots.data(), fwd_tokens.data(), cdf.data(), vocab + 1)
+                             : api.forward_batch(nf, fwd_slots.data(), fwd_tokens.data(), logits.data(), vocab);
             if (rc != BACKEND_OK) return abort_run();
         }
         stats.forward_secs += since(tb);
@@ -391,6 +414,10 @@ extern "C" int32_t redukt_lockstep_open(const char* plugin_path, const char* wei
     // threads: forward_batch_cdf 0.93 ms per step at 32 streams against 0.58 ms forward +
     // 0.71 ms host CDF, 1.77 ms at 128 streams against 1.27 + 2.60 ms).
     ls->device_cdf = ls->api.forward_batch_cdf != nullptr && slots >= kDeviceCdfFrom;
+    // REDUKT_LOCKSTEP_CDF_SYM=0: compression takes whole device CDF rows like decompression.
+    const char* e = getenv("REDUKT_LOCKSTEP_CDF_SYM");
+    ls->sym_cdf = ls->api.forward_batch_cdf_sym != nullptr && !(e && *e && !strcmp(e, "0"));
+    ls->bounds.assign(rows * 3, 0u);
     *out = ls.release();
     return REDUKT_LOCKSTEP_OK;
 }

@@ -66,6 +66,9 @@ bool gemv_cpl_supported(int cpl);
 // cdf_from_logits (cdf_step.hip); `scratch` holds cdf_scratch_bytes(rows, n).
 size_t cdf_scratch_bytes(uint32_t rows, uint32_t n);
 hipError_t cdf_launch(const float* logits, uint32_t rows, uint32_t n, void* scratch, uint32_t* cdf, hipStream_t st);
+// out[3r .. 3r + 2] = cdf[r][sym[r]], cdf[r][sym[r] + 1], cdf[r][n] for rows r (cdf rows of n + 1).
+hipError_t cdf_pick_launch(const uint32_t* cdf, uint32_t rows, uint32_t n, const uint32_t* sym, uint32_t* out,
+                           hipStream_t st);
 
 namespace {
 

@@ -115,6 +115,38 @@ def test_forward_batch_cdf_rejects_bad_arguments(backend):
     assert code == ffi.BackendResult.INVALID_ARGUMENT
 
 
+def test_forward_batch_cdf_sym_equals_the_rows(backend):
+    # The coder's three values per stream for a known next symbol equal the full device CDF
+    # row's entries (the same tokens on other slots), symbols 0 and V - 1 included.
+    backend.batch_init(64)
+    V = backend.vocab
+    rng = np.random.default_rng(12)
+    n = 29
+    for t in range(3):
+        toks = [int(x) for x in rng.integers(0, V, n)]
+        syms = [int(x) for x in rng.integers(0, V, n)]
+        syms[0], syms[-1] = 0, V - 1
+        rows = np.empty((n, V + 1), np.uint32)
+        backend.forward_batch_cdf(list(range(n)), toks, rows)
+        got = np.empty(3 * n, np.uint32)
+        assert backend.forward_batch_cdf_sym(list(range(n, 2 * n)), toks, syms, got) == ffi.BackendResult.OK
+        want = np.stack([[rows[b, syms[b]], rows[b, syms[b] + 1], rows[b, V]] for b in range(n)]).reshape(-1)
+        assert np.array_equal(got, want), t
+
+
+def test_forward_batch_cdf_sym_rejects_bad_arguments(backend):
+    backend.batch_init(8)
+    V = backend.vocab
+    got = np.empty(6, np.uint32)
+    assert backend.forward_batch_cdf_sym([0, 1], [1, 2], [3, V], got) == ffi.BackendResult.INVALID_ARGUMENT
+    assert backend.forward_batch_cdf_sym([0, 0], [1, 2], [3, 4], got) == ffi.BackendResult.INVALID_ARGUMENT
+    code = backend.lib.lib.redukt_backend_forward_batch_cdf_sym(
+        2, ffi._ptr(np.array([0, 1], np.uint32), ffi.ctypes.c_uint32),
+        ffi._ptr(np.array([1, 2], np.uint32), ffi.ctypes.c_uint32),
+        ffi._ptr(np.array([3, 4], np.uint32), ffi.ctypes.c_uint32), ffi._ptr(got, ffi.ctypes.c_uint32), V + 1)
+    assert code == ffi.BackendResult.INVALID_ARGUMENT   # vocab_size not the model's
+
+
 # The tests below open backends of their own: the library holds one model at a time, so
 # they come after every test of the shared `backend` fixture.
 def test_forward_batch_cdf_rwkv7(tmp_path):
@@ -125,15 +157,18 @@ def test_forward_batch_cdf_rwkv7(tmp_path):
         step_pair(be, 8, 2, seed=3)
 
 
-def test_lockstep_device_cdf_bytes_equal_host_cdf(full_model):
+def test_lockstep_device_cdf_bytes_equal_host_cdf(full_model, monkeypatch):
+    # Host CDFs, device CDF rows, and device CDFs handing back only the coder's three values
+    # per stream (compression's default): the same archives, each decoding to its file.
     rng = np.random.default_rng(77)
     files = [[int(x) for x in synth.zipf_tokens(rng, 50280, (L,))] for L in (40, 17, 64, 1, 33)]
     outs = {}
-    for dev in (False, True):
+    for dev, sym in ((False, "1"), (True, "0"), (True, "1")):
+        monkeypatch.setenv("REDUKT_LOCKSTEP_CDF_SYM", sym)
         with lockstep.Lockstep(full_model, ffi.DEFAULT_LIB, profile=Q8ROW_ALL, slots=3, device_cdf=dev) as ls:
             assert ls.device_cdf == dev
             streams, _ = ls.compress(files)
             back, _ = ls.decompress(streams, [len(f) for f in files])
             assert [b.tolist() for b in back] == files
-            outs[dev] = streams
-    assert outs[True] == outs[False]
+            outs[(dev, sym)] = streams
+    assert outs[(True, "1")] == outs[(False, "1")] == outs[(True, "0")]
