@@ -170,6 +170,18 @@ int32_t redukt_backend_forward_batch_cdf(uint32_t n_streams, const uint32_t* slo
 int32_t redukt_backend_forward_batch_cdf_sym(uint32_t n_streams, const uint32_t* slots, const uint32_t* tokens,
                                              const uint32_t* next_syms, uint32_t* out_bounds, uint32_t vocab_size);
 
+/* forward_batch_cdf for a range decoder that knows each stream's target cumulative
+ * frequency (decompression; the target is the decoder's get_freq value for a total of
+ * REDUKT_CDF_TOTAL, which every device CDF row sums to): the same CDF rows are computed on
+ * the device and searched there as decode_symbol searches them (coder.rs:100-115);
+ * out_found[4b .. 4b + 3] = s, cdf[s], cdf[s + 1] and cdf[vocab_size], the total, with s
+ * the symbol found (s = vocab_size and both bounds the total when targets[b] >= the
+ * total).  16 bytes per stream instead of 4 (vocab + 1).  vocab_size must be the model's.
+ * Same validation and state rules as forward_batch.  No reference counterpart (an
+ * extension of the CDF entry point above). */
+int32_t redukt_backend_forward_batch_cdf_find(uint32_t n_streams, const uint32_t* slots, const uint32_t* tokens,
+                                              const uint32_t* targets, uint32_t* out_found, uint32_t vocab_size);
+
 /* The device CDF on caller logits: d_logits [rows][n] f32 -> d_cdf [rows][n + 1] u32,
  * both device pointers, stream-ordered on redukt_backend_stream() (the call does not
  * wait).  1 <= n < 2^24.  For tests and for callers that hold logits on the device. */

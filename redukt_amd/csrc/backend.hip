@@ -1256,8 +1256,9 @@ int32_t redukt_backend_forward_batch_probs(uint32_t n_streams, const uint32_t* s
 bool cdf_space(uint32_t rows, uint32_t n, bool with_out, void** scratch, uint32_t** out, uint32_t** pick = nullptr) {
     const size_t sb = (cdf_scratch_bytes(rows, n) + 255) & ~(size_t)255;
     const size_t ob = with_out ? ((size_t)rows * (n + 1) * 4 + 255) & ~(size_t)255 : 0;
-    // pick: the next symbols (rows u32), then the coder's three values per row
-    const size_t need = sb + ob + (pick ? (size_t)rows * 4 * 4 : 0);
+    // pick: the next symbols or decoder targets (rows u32), then the coder's three or four
+    // values per row
+    const size_t need = sb + ob + (pick ? (size_t)rows * 5 * 4 : 0);
     if (need > G.cdf_bytes) {
         if (G.cdf_mem) {
             if (hipStreamSynchronize(G.stream) != hipSuccess) return false;
@@ -1334,6 +1335,41 @@ int32_t redukt_backend_forward_batch_cdf_sym(uint32_t n_streams, const uint32_t*
         cdf_pick_launch(d_cdf, n_streams, V, d_sym, d_bounds, G.stream) != hipSuccess)
         return BACKEND_FORWARD_FAILED;
     if (hipMemcpyAsync(out_bounds, d_bounds, sizeof(uint32_t) * 3 * n_streams, hipMemcpyDeviceToHost, G.stream) !=
+            hipSuccess ||
+        hipStreamSynchronize(G.stream) != hipSuccess)
+        return BACKEND_FORWARD_FAILED;
+    return BACKEND_OK;
+}
+
+int32_t redukt_backend_forward_batch_cdf_find(uint32_t n_streams, const uint32_t* slots, const uint32_t* tokens,
+                                              const uint32_t* targets, uint32_t* out_found, uint32_t vocab_size) {
+    if (!G.ready || G.batch.cap == 0) return BACKEND_INIT_FAILED;
+    const uint32_t V = G.kind == kKindRwkv ? G.rdims.vocab : G.dims.vocab;
+    if (vocab_size != V || n_streams > G.batch.cap || V >= (1u << 24)) return BACKEND_INVALID_ARGUMENT;
+    if (n_streams == 0) return BACKEND_OK;
+    if (!slots || !tokens || !targets || !out_found) return BACKEND_INVALID_ARGUMENT;
+    Pool& p = G.batch;
+    memset(p.seen, 0, p.cap);
+    for (uint32_t b = 0; b < n_streams; b++) {
+        if (slots[b] >= p.cap || p.seen[slots[b]] || tokens[b] >= V) return BACKEND_INVALID_ARGUMENT;
+        p.seen[slots[b]] = 1;
+    }
+    void* scratch = nullptr;
+    uint32_t *d_cdf = nullptr, *d_pick = nullptr;
+    if (!cdf_space(n_streams, V, true, &scratch, &d_cdf, &d_pick)) return BACKEND_FORWARD_FAILED;
+    uint32_t* const d_cum = d_pick;
+    uint32_t* const d_found = d_pick + n_streams;
+    memcpy(p.h_slots, slots, sizeof(uint32_t) * n_streams);
+    memcpy(p.h_slots + n_streams, tokens, sizeof(uint32_t) * n_streams);
+    if (hipMemcpyAsync(p.d_slots, p.h_slots, sizeof(uint32_t) * 2 * n_streams, hipMemcpyHostToDevice, G.stream) !=
+            hipSuccess ||
+        hipMemcpyAsync(d_cum, targets, sizeof(uint32_t) * n_streams, hipMemcpyHostToDevice, G.stream) != hipSuccess)
+        return BACKEND_FORWARD_FAILED;
+    if (run_step(p, n_streams, p.d_slots, p.d_slots + n_streams, p.out, false, false) != hipSuccess ||
+        cdf_launch(p.out, n_streams, V, scratch, d_cdf, G.stream) != hipSuccess ||
+        cdf_find_launch(d_cdf, n_streams, V, d_cum, d_found, G.stream) != hipSuccess)
+        return BACKEND_FORWARD_FAILED;
+    if (hipMemcpyAsync(out_found, d_found, sizeof(uint32_t) * 4 * n_streams, hipMemcpyDeviceToHost, G.stream) !=
             hipSuccess ||
         hipStreamSynchronize(G.stream) != hipSuccess)
         return BACKEND_FORWARD_FAILED;

@@ -604,4 +604,67 @@ hipError_t cdf_pick_launch(const uint32_t* cdf, uint32_t rows, uint32_t n, const
     return hipGetLastError();
 }
 
+namespace {
+// The symbol the range decoder finds in row r for its target cum[r] (coder.rs:100-115, the
+// binary search of decode_symbol) with what it reads next: out[4r] = s, out[4r + 1] =
+// cdf[r][s], out[4r + 2] = cdf[r][s + 1], out[4r + 3] = cdf[r][n]; s = n (both bounds
+// cdf[r][n]) when cum[r] >= cdf[r][n].  One wave a row takes six levels of the search
+// per round trip to memory: lane k (1..63) is node k of those levels' tree in heap order
+// (children 2k: hi = mid, 2k + 1: lo = mid + 1), works out its node's interval from the
+// bits of k and evaluates the node's test; the wave then walks the tree from the ballot.
+// Every decision is the host search's own (the same mid of the same interval), so the
+// result equals it for any row contents, monotone or not.
+constexpr uint32_t kFindRows = 4;   // rows (waves) a workgroup
+
+__global__ __launch_bounds__(64 * kFindRows) void k_cdf_find(const uint32_t* __restrict__ cdf, uint32_t rows,
+                                                              uint32_t n, const uint32_t* __restrict__ cum,
+                                                              uint32_t* __restrict__ out) {
+    const uint32_t r = blockIdx.x * kFindRows + threadIdx.x / 64, lane = threadIdx.x % 64;
+    if (r >= rows) return;   // whole waves
+    const uint32_t* row = cdf + (size_t)r * (n + 1);
+    const uint32_t t = cum[r];
+    uint32_t lo = 0, hi = n;
+    while (lo < hi) {
+        bool right = false;
+        if (lane > 0) {
+            uint32_t a = lo, b = hi;
+            for (int d = 30 - __clz(lane); d >= 0 && a < b; d--) {   // path bits below the leading one
+                const uint32_t m = a + (b - a) / 2;
+                if ((lane >> d) & 1)
+                    a = m + 1;
+                else
+                    b = m;
+            }
+            if (a < b) right = row[a + (b - a) / 2 + 1] <= t;
+        }
+        const uint64_t bits = __ballot(right);
+        for (uint32_t level = 0, node = 1; level < 6 && lo < hi; level++) {
+            const uint32_t m = lo + (hi - lo) / 2;
+            if ((bits >> node) & 1) {
+                lo = m + 1;
+                node = 2 * node + 1;
+            } else {
+                hi = m;
+                node = 2 * node;
+            }
+        }
+    }
+    if (lane == 0) {
+        const uint32_t total = row[n];
+        uint32_t* o = out + 4 * (size_t)r;
+        o[0] = lo;
+        o[1] = lo < n ? row[lo] : total;
+        o[2] = lo < n ? row[lo + 1] : total;
+        o[3] = total;
+    }
+}
+}  // namespace
+
+hipError_t cdf_find_launch(const uint32_t* cdf, uint32_t rows, uint32_t n, const uint32_t* cum, uint32_t* out,
+                           hipStream_t st) {
+    if (rows == 0) return hipSuccess;
+    k_cdf_find<<<dim3((rows + kFindRows - 1) / kFindRows), dim3(64 * kFindRows), 0, st>>>(cdf, rows, n, cum, out);
+    return hipGetLastError();
+}
+
 }  // namespace rdk

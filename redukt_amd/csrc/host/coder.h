@@ -100,17 +100,23 @@ struct redukt_rc_decoder {
         for (int i = 0; i < 4; ++i) code = (code << 8) | next_byte();
     }
 
-    // get_freq + lookup + update (coder.rs:249-286); vocab > 0 also rejects
-    // symbols >= vocab after the update, as decode_symbol_checked does.
-    int32_t decode(const uint32_t* cdf, uint32_t n, uint32_t vocab, uint32_t* sym) {
-        const uint32_t total = cdf[n];
+    // get_freq (coder.rs:249-262): the cumulative frequency to look up in a CDF of this
+    // total.  The state is unchanged.
+    int32_t target(uint32_t total, uint32_t* cum) const {
         if (total == 0) return REDUKT_CODEC_INVALID_ARG;
         const uint32_t r = range / total;
         if (r == 0) return REDUKT_CODEC_RANGE_UNDERFLOW;
-        const uint32_t cum = std::min((code - low) / r, total - 1);
-        const uint32_t s = redukt_cdf_lookup(cdf, n, cum);
+        *cum = std::min((code - low) / r, total - 1);
+        return REDUKT_CODEC_OK;
+    }
+
+    // update (coder.rs:264-286) with the symbol s the lookup found for target()'s value
+    // and its bounds lo = cdf[s], hi = cdf[s + 1] (read only when s < n), after target()
+    // returned OK for this total; vocab > 0 also rejects symbols >= vocab after the update,
+    // as decode_symbol_checked does.
+    int32_t finish(uint32_t s, uint32_t lo, uint32_t hi, uint32_t total, uint32_t n, uint32_t vocab, uint32_t* sym) {
         if (s >= n) return REDUKT_CODEC_INVALID_ARG;  // cdf does not end at its total
-        const uint32_t lo = cdf[s], hi = cdf[s + 1];
+        const uint32_t r = range / total;
         low += r * lo;
         range = hi < total ? r * (hi - lo) : range - r * lo;
         while (range < redukt_host::kRenorm) {
@@ -121,5 +127,15 @@ struct redukt_rc_decoder {
         if (vocab && s >= vocab) return REDUKT_CODEC_SYMBOL_OUT_OF_RANGE;
         *sym = s;
         return REDUKT_CODEC_OK;
+    }
+
+    // get_freq + lookup + update (coder.rs:249-286).
+    int32_t decode(const uint32_t* cdf, uint32_t n, uint32_t vocab, uint32_t* sym) {
+        const uint32_t total = cdf[n];
+        uint32_t cum = 0;
+        const int32_t st = target(total, &cum);
+        if (st != REDUKT_CODEC_OK) return st;
+        const uint32_t s = redukt_cdf_lookup(cdf, n, cum);
+        return s < n ? finish(s, cdf[s], cdf[s + 1], total, n, vocab, sym) : REDUKT_CODEC_INVALID_ARG;
     }
 };

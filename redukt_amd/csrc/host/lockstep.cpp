@@ -42,6 +42,9 @@ struct PluginApi {
     // optional: the same, handing back only the coder's three values for a known next symbol
     int32_t (*forward_batch_cdf_sym)(uint32_t, const uint32_t*, const uint32_t*, const uint32_t*, uint32_t*,
                                      uint32_t) = nullptr;
+    // optional: the same, searching each row on the device for the decoder's target
+    int32_t (*forward_batch_cdf_find)(uint32_t, const uint32_t*, const uint32_t*, const uint32_t*, uint32_t*,
+                                      uint32_t) = nullptr;
     bool v2 = false;
 
     template <class F>
@@ -64,6 +67,7 @@ struct PluginApi {
         bind(init_ex, "redukt_backend_init_ex");
         bind(forward_batch_cdf, "redukt_backend_forward_batch_cdf");
         bind(forward_batch_cdf_sym, "redukt_backend_forward_batch_cdf_sym");
+        bind(forward_batch_cdf_find, "redukt_backend_forward_batch_cdf_find");
         v2 = abi_version && batch_init && batch_reset && forward_batch && abi_version() >= 2;
         return true;
     }
@@ -82,6 +86,7 @@ struct Lane {
     int32_t status = REDUKT_CODEC_OK;
     uint64_t since_reset = 0;  // PluginState::tick schedule
     uint32_t row = 0;          // logits row of this lane's last forward
+    int32_t target_status = REDUKT_CODEC_OK;  // the decoder target's status for that forward
     redukt_rc_encoder enc;
     redukt_rc_decoder dec;
 };
@@ -117,12 +122,15 @@ struct redukt_lockstep {
     bool device_cdf = false;
     // Compression with device CDFs takes, where the plugin has it, only the three values of
     // each row the coder reads for the lane's next symbol (forward_batch_cdf_sym): 12 bytes
-    // a stream cross from the device instead of the whole row.
+    // a stream cross from the device instead of the whole row.  Decompression likewise
+    // sends each lane's decoder target and takes back the symbol found with its bounds
+    // (forward_batch_cdf_find, 16 bytes a stream).
     bool sym_cdf = false;
+    bool find_cdf = false;
     std::vector<float> logits;
     std::vector<uint32_t> cdf;
     std::vector<uint32_t> uniform;
-    std::vector<uint32_t> bounds;  // [row][3] of the last forward_batch_cdf_sym
+    std::vector<uint32_t> bounds;  // [row][3] of the last forward_batch_cdf_sym, [row][4] of _find
 
     const uint32_t* cdf_row(uint32_t i) const { return cdf.data() + size_t(i) * (vocab + 1); }
     uint32_t* cdf_row(uint32_t i) { return cdf.data() + size_t(i) * (vocab + 1); }
@@ -148,6 +156,15 @@ struct redukt_lockstep {
         } else if (job.mode == Mode::Encode) {
             tok = job.tokens[l.file][l.pos];
             st = l.enc.encode_symbol(tok, c, vocab);
+        } else if (l.pos > 0 && device_cdf && find_cdf) {
+            // Phase B took the target for a total of REDUKT_CDF_TOTAL, the total of every
+            // device row; a row that says otherwise is refused like a CDF that does not end
+            // at its total.
+            const uint32_t* b = bounds.data() + size_t(l.row) * 4;
+            st = l.target_status != REDUKT_CODEC_OK ? l.target_status
+                 : b[3] != REDUKT_CDF_TOTAL         ? REDUKT_CODEC_INVALID_ARG
+                                                    : l.dec.finish(b[0], b[1], b[2], b[3], vocab, vocab, &tok);
+            if (st == REDUKT_CODEC_OK) job.tokens_out[l.file][l.pos] = tok;
         } else {
             st = l.dec.decode(c, vocab, vocab, &tok);
             if (st == REDUKT_CODEC_OK) job.tokens_out[l.file][l.pos] = tok;
@@ -216,6 +233,7 @@ int32_t redukt_lockstep::run_lockstep(const Job& job, redukt_lockstep_stats& sta
     std::vector<Lane> lanes(slots);
     std::vector<uint32_t> active, fwd_slots, fwd_tokens, fwd_syms, resets;
     const bool pick = job.mode == Mode::Encode && device_cdf && sym_cdf;
+    const bool find = job.mode == Mode::Decode && device_cdf && find_cdf;
     active.reserve(slots);
     uint32_t next_file = 0;
     // The backbone failed: every file still in a lane and every file not yet admitted is
@@ -291,6 +309,12 @@ int32_t redukt_lockstep::run_lockstep(const Job& job, redukt_lockstep_stats& sta
                 // the symbol Phase A codes next (an out-of-range one is refused there, per file)
                 const uint32_t next = job.tokens[l.file][l.pos];
                 fwd_syms.push_back(next < vocab ? next : 0u);
+            } else if (find) {
+                // the decoder's target for the symbol Phase A decodes next (the state does not
+                // change before then); a failure there is that symbol's status
+                uint32_t cum = 0;
+                l.target_status = l.dec.target(REDUKT_CDF_TOTAL, &cum);
+                fwd_syms.push_back(l.target_status == REDUKT_CODEC_OK ? cum : 0u);
             }
         }
         if (!resets.empty() && api.batch_reset(resets.data(), uint32_t(resets.size())) != BACKEND_OK)
@@ -300,6 +324,8 @@ int32_t redukt_lockstep::run_lockstep(const Job& job, redukt_lockstep_stats& sta
             const int32_t rc =
                 pick ? api.forward_batch_cdf_sym(nf, fwd_slots.data(), fwd_tokens.data(), fwd_syms.data(), bounds.data(),
                                                  vocab)
+                : find ? api.forward_batch_cdf_find(nf, fwd_slots.data(), fwd_tokens.data(), fwd_syms.data(),
+                                                    bounds.data(), vocab)
                 : device_cdf ? api.forward_batch_cdf(nf, fwd_slots.data(), fwd_tokens.data(), cdf.data(), vocab + 1)
                              : api.forward_batch(nf, fwd_slots.data(), fwd_tokens.data(), logits.data(), vocab);
             if (rc != BACKEND_OK) return abort_run();
@@ -414,10 +440,12 @@ extern "C" int32_t redukt_lockstep_open(const char* plugin_path, const char* wei
     // threads: forward_batch_cdf 0.93 ms per step at 32 streams against 0.58 ms forward +
     // 0.71 ms host CDF, 1.77 ms at 128 streams against 1.27 + 2.60 ms).
     ls->device_cdf = ls->api.forward_batch_cdf != nullptr && slots >= kDeviceCdfFrom;
-    // REDUKT_LOCKSTEP_CDF_SYM=0: compression takes whole device CDF rows like decompression.
+    // REDUKT_LOCKSTEP_CDF_SYM=0: compression and decompression take whole device CDF rows.
     const char* e = getenv("REDUKT_LOCKSTEP_CDF_SYM");
-    ls->sym_cdf = ls->api.forward_batch_cdf_sym != nullptr && !(e && *e && !strcmp(e, "0"));
-    ls->bounds.assign(rows * 3, 0u);
+    const bool rows_only = e && *e && !strcmp(e, "0");
+    ls->sym_cdf = ls->api.forward_batch_cdf_sym != nullptr && !rows_only;
+    ls->find_cdf = ls->api.forward_batch_cdf_find != nullptr && !rows_only;
+    ls->bounds.assign(rows * 4, 0u);
     *out = ls.release();
     return REDUKT_LOCKSTEP_OK;
 }

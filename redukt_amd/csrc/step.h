@@ -69,6 +69,10 @@ hipError_t cdf_launch(const float* logits, uint32_t rows, uint32_t n, void* scra
 // out[3r .. 3r + 2] = cdf[r][sym[r]], cdf[r][sym[r] + 1], cdf[r][n] for rows r (cdf rows of n + 1).
 hipError_t cdf_pick_launch(const uint32_t* cdf, uint32_t rows, uint32_t n, const uint32_t* sym, uint32_t* out,
                            hipStream_t st);
+// The decoder's symbol for each row's target cumulative frequency, with its two bounds and
+// the row's total (4 u32 a row).
+hipError_t cdf_find_launch(const uint32_t* cdf, uint32_t rows, uint32_t n, const uint32_t* cum, uint32_t* out,
+                           hipStream_t st);
 
 namespace {
 

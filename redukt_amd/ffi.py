@@ -47,7 +47,8 @@ V3_SYMBOLS = ("redukt_backend_init_ex", "redukt_backend_forward_batch_probs", "r
               "redukt_backend_probe_kernel", "redukt_backend_probe_used", "redukt_backend_get_rwkv_state",
               "redukt_backend_eval_math", "redukt_backend_forward_batch_device_noalloc",
               "redukt_backend_forward_batch_cdf", "redukt_backend_cdf_from_logits_device",
-              "redukt_backend_copy_probe", "redukt_backend_forward_batch_cdf_sym")
+              "redukt_backend_copy_probe", "redukt_backend_forward_batch_cdf_sym",
+              "redukt_backend_forward_batch_cdf_find")
 # redukt_backend_eval_math function codes: the portable element-wise functions
 MATH_FNS = {"exp": 0, "lane_exp": 1, "ln": 2, "softplus": 3, "lane_sigmoid": 4, "sigmoid": 5}
 
@@ -157,6 +158,9 @@ class PluginLibrary:
             L.redukt_backend_forward_batch_cdf_sym.argtypes = [ctypes.c_uint32, _u32p, _u32p, _u32p, _u32p,
                                                                ctypes.c_uint32]
             L.redukt_backend_forward_batch_cdf_sym.restype = ctypes.c_int32
+            L.redukt_backend_forward_batch_cdf_find.argtypes = [ctypes.c_uint32, _u32p, _u32p, _u32p, _u32p,
+                                                                ctypes.c_uint32]
+            L.redukt_backend_forward_batch_cdf_find.restype = ctypes.c_int32
             L.redukt_backend_cdf_from_logits_device.argtypes = [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
                                                                 ctypes.c_void_p]
             L.redukt_backend_cdf_from_logits_device.restype = ctypes.c_int32
@@ -396,6 +400,19 @@ class PluginBackend:
         t = np.ascontiguousarray(tokens, dtype=np.uint32)
         y = np.ascontiguousarray(next_syms, dtype=np.uint32)
         return BackendResult.from_code(self.lib.lib.redukt_backend_forward_batch_cdf_sym(
+            len(s), _ptr(s, ctypes.c_uint32), _ptr(t, ctypes.c_uint32), _ptr(y, ctypes.c_uint32),
+            _ptr(out, ctypes.c_uint32), self.vocab))
+
+    def forward_batch_cdf_find(self, slots: Sequence[int], tokens: Sequence[int], targets: Sequence[int],
+                               out: np.ndarray) -> BackendResult:
+        """forward_batch_cdf returning, per stream, the symbol the range decoder finds for its
+        target cumulative frequency with that symbol's two bounds and the total (out: 4 u32
+        a stream); returns the result code."""
+        assert out.dtype == np.uint32 and out.flags.c_contiguous and out.size == 4 * len(slots)
+        s = np.ascontiguousarray(slots, dtype=np.uint32)
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        y = np.ascontiguousarray(targets, dtype=np.uint32)
+        return BackendResult.from_code(self.lib.lib.redukt_backend_forward_batch_cdf_find(
             len(s), _ptr(s, ctypes.c_uint32), _ptr(t, ctypes.c_uint32), _ptr(y, ctypes.c_uint32),
             _ptr(out, ctypes.c_uint32), self.vocab))
 

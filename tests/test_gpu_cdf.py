@@ -14,7 +14,10 @@ the CPU tests pin to the oracle and the reference's exp goldens:
 * `redukt_backend_forward_batch_cdf` on Mamba-130M (int8 per-row) and RWKV-7 0.1B
   against the host CDF of the same step's logits from `forward_batch` (batch invariance
   makes a stream's logits the same on any slot);
-* the driver's lockstep bytes with the device CDF equal those with the host CDF.
+* `redukt_backend_forward_batch_cdf_sym` and `_find` (what the coder reads of each row for
+  a known symbol or a decoder target) against the full rows and the host search;
+* the driver's lockstep bytes with the device CDF equal those with the host CDF, and
+  damaged archives decode to the same tokens on every path.
 """
 import numpy as np
 import pytest
@@ -147,6 +150,51 @@ def test_forward_batch_cdf_sym_rejects_bad_arguments(backend):
     assert code == ffi.BackendResult.INVALID_ARGUMENT   # vocab_size not the model's
 
 
+def test_forward_batch_cdf_find_equals_the_host_search(backend):
+    # The symbol the device finds for a decoder target, with its two bounds and the total,
+    # equals the host search (redukt_cdf_lookup) over the full device CDF row of the same
+    # tokens on other slots: targets 0 and total - 1, each bound of random symbols, random
+    # values, and targets at and beyond the total (s = V, both bounds the total).
+    backend.batch_init(64)
+    V = backend.vocab
+    T = 1 << 24
+    rng = np.random.default_rng(13)
+    n = 31
+    for t in range(3):
+        toks = [int(x) for x in rng.integers(0, V, n)]
+        rows = np.empty((n, V + 1), np.uint32)
+        backend.forward_batch_cdf(list(range(n)), toks, rows)
+        assert np.all(rows[:, V] == T)
+        syms = rng.integers(0, V, n)
+        targets = rng.integers(0, T, n).astype(np.uint32)
+        targets[:4] = [0, T - 1, T, 2**32 - 1]
+        for b in range(4, 12):
+            targets[b] = rows[b, syms[b]]            # a symbol's first value
+        for b in range(12, 20):
+            targets[b] = rows[b, syms[b] + 1] - 1    # a symbol's last value
+        got = np.empty(4 * n, np.uint32)
+        assert backend.forward_batch_cdf_find(list(range(n, 2 * n)), toks, targets, got) == ffi.BackendResult.OK
+        want = []
+        for b in range(n):
+            s = codec.lookup(rows[b], int(targets[b]))
+            want += [s, rows[b, s], rows[b, s + 1], T] if s < V else [V, T, T, T]
+        assert np.array_equal(got, np.array(want, np.uint32)), t
+        assert got[0] == 0 and got[4 * 2] == V and got[4 * 3] == V
+
+
+def test_forward_batch_cdf_find_rejects_bad_arguments(backend):
+    backend.batch_init(8)
+    V = backend.vocab
+    got = np.empty(8, np.uint32)
+    assert backend.forward_batch_cdf_find([0, 1], [1, V], [3, 4], got) == ffi.BackendResult.INVALID_ARGUMENT
+    assert backend.forward_batch_cdf_find([0, 0], [1, 2], [3, 4], got) == ffi.BackendResult.INVALID_ARGUMENT
+    code = backend.lib.lib.redukt_backend_forward_batch_cdf_find(
+        2, ffi._ptr(np.array([0, 1], np.uint32), ffi.ctypes.c_uint32),
+        ffi._ptr(np.array([1, 2], np.uint32), ffi.ctypes.c_uint32),
+        ffi._ptr(np.array([3, 4], np.uint32), ffi.ctypes.c_uint32), ffi._ptr(got, ffi.ctypes.c_uint32), V - 1)
+    assert code == ffi.BackendResult.INVALID_ARGUMENT   # vocab_size not the model's
+
+
 # The tests below open backends of their own: the library holds one model at a time, so
 # they come after every test of the shared `backend` fixture.
 def test_forward_batch_cdf_rwkv7(tmp_path):
@@ -158,11 +206,15 @@ def test_forward_batch_cdf_rwkv7(tmp_path):
 
 
 def test_lockstep_device_cdf_bytes_equal_host_cdf(full_model, monkeypatch):
-    # Host CDFs, device CDF rows, and device CDFs handing back only the coder's three values
-    # per stream (compression's default): the same archives, each decoding to its file.
+    # Host CDFs, device CDF rows, and the device paths that hand back only what the coder
+    # reads (three values for compression's known symbol, the symbol found and its bounds
+    # for decompression's target: the defaults): the same archives, each decoding to its
+    # file.  Damaged archives (bytes flipped, a stream cut short, one empty, more tokens
+    # asked for than were coded) drive the decoders through arbitrary states: all three
+    # decode them to the same tokens.
     rng = np.random.default_rng(77)
     files = [[int(x) for x in synth.zipf_tokens(rng, 50280, (L,))] for L in (40, 17, 64, 1, 33)]
-    outs = {}
+    outs, bad = {}, {}
     for dev, sym in ((False, "1"), (True, "0"), (True, "1")):
         monkeypatch.setenv("REDUKT_LOCKSTEP_CDF_SYM", sym)
         with lockstep.Lockstep(full_model, ffi.DEFAULT_LIB, profile=Q8ROW_ALL, slots=3, device_cdf=dev) as ls:
@@ -171,4 +223,10 @@ def test_lockstep_device_cdf_bytes_equal_host_cdf(full_model, monkeypatch):
             back, _ = ls.decompress(streams, [len(f) for f in files])
             assert [b.tolist() for b in back] == files
             outs[(dev, sym)] = streams
+            damaged = [bytes(x ^ 0x5A if i % 3 == 1 else x for i, x in enumerate(streams[0])), streams[2][:5], b"",
+                       streams[3], streams[4]]
+            got, _ = ls.decompress(damaged, [40, 64, 20, 30, 33])
+            bad[(dev, sym)] = [g.tolist() for g in got]
     assert outs[(True, "1")] == outs[(False, "1")] == outs[(True, "0")]
+    assert bad[(True, "1")] == bad[(False, "1")] == bad[(True, "0")]
+    assert bad[(False, "1")][0] != files[0] and bad[(False, "1")][4] == files[4]
