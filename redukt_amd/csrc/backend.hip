@@ -597,7 +597,9 @@ constexpr size_t kOutRoundBytes = (size_t)32 << 20;
 constexpr unsigned kCopyThreadsMax = 8;   // the caller's thread and at most seven helpers
 
 bool out_stage_alloc(Pool& p, size_t out_bytes) {
-    p.out_stage_bytes = std::min(kOutRoundBytes, (out_bytes + 255) & ~(size_t)255);
+    // at least 4 u32 a stream: the CDF readers' results come back through it in one piece
+    p.out_stage_bytes = std::max(std::min(kOutRoundBytes, (out_bytes + 255) & ~(size_t)255),
+                                 ((size_t)p.cap * 16 + 255) & ~(size_t)255);
     if (hipHostMalloc((void**)&p.h_out, p.out_stage_bytes, hipHostMallocDefault) != hipSuccess) {
         p.h_out = nullptr;
         return false;
@@ -748,7 +750,7 @@ bool pool_alloc_rwkv(Pool& p, uint32_t cap) {
     p.gcap = (cap + 15) / 16;
     bool ok = pool_carve(p, [&](Carve& c) {
         c.take(p.slots, slot_words(cap));
-        c.take(p.d_slots, 2 * n);  // a step's n slots, then its n tokens (one H2D copy)
+        c.take(p.d_slots, 3 * n);  // a step's n slots, its n tokens, then a word per stream for the CDF readers (one H2D copy)
         c.take(p.x, n * d);
         c.take(p.vfirst, n * d);
         c.take(p.rkv, n * 3 * d);
@@ -771,7 +773,7 @@ bool pool_alloc_rwkv(Pool& p, uint32_t cap) {
         c.take(p.x_ffn, z.state_d);
         c.take(p.wkv, z.wkv);
     });
-    ok = ok && hipHostMalloc((void**)&p.h_slots, sizeof(uint32_t) * 2 * n, hipHostMallocDefault) == hipSuccess;
+    ok = ok && hipHostMalloc((void**)&p.h_slots, sizeof(uint32_t) * 3 * n, hipHostMallocDefault) == hipSuccess;
 
     ok = ok && (p.seen = (uint8_t*)calloc(n, 1)) != nullptr;
     ok = ok && out_stage_alloc(p, (size_t)n * vocab_of_model() * sizeof(float));
@@ -790,7 +792,7 @@ bool pool_alloc(Pool& p, uint32_t cap) {
     const size_t ns = p.scap;
     bool ok = pool_carve(p, [&](Carve& c) {
         c.take(p.slots, slot_words(cap));
-        c.take(p.d_slots, 2 * n);  // a step's n slots, then its n tokens (one H2D copy)
+        c.take(p.d_slots, 3 * n);  // a step's n slots, its n tokens, then a word per stream for the CDF readers (one H2D copy)
         c.take(p.x, n * d);
         c.take(p.xw, xw_elems(D, cap));
         c.take(p.ssp, ssp_floats(D, cap));
@@ -804,7 +806,7 @@ bool pool_alloc(Pool& p, uint32_t cap) {
         c.take(p.conv, (size_t)D.nl * ns * di * (D.dc - 1));
         c.take(p.ssm, (size_t)D.nl * ns * di * 16);
     });
-    ok = ok && hipHostMalloc((void**)&p.h_slots, sizeof(uint32_t) * 2 * n, hipHostMallocDefault) == hipSuccess;
+    ok = ok && hipHostMalloc((void**)&p.h_slots, sizeof(uint32_t) * 3 * n, hipHostMallocDefault) == hipSuccess;
 
     ok = ok && (p.seen = (uint8_t*)calloc(n, 1)) != nullptr;
     ok = ok && out_stage_alloc(p, (size_t)n * vocab_of_model() * sizeof(float));
@@ -1256,9 +1258,8 @@ int32_t redukt_backend_forward_batch_probs(uint32_t n_streams, const uint32_t* s
 bool cdf_space(uint32_t rows, uint32_t n, bool with_out, void** scratch, uint32_t** out, uint32_t** pick = nullptr) {
     const size_t sb = (cdf_scratch_bytes(rows, n) + 255) & ~(size_t)255;
     const size_t ob = with_out ? ((size_t)rows * (n + 1) * 4 + 255) & ~(size_t)255 : 0;
-    // pick: the next symbols or decoder targets (rows u32), then the coder's three or four
-    // values per row
-    const size_t need = sb + ob + (pick ? (size_t)rows * 5 * 4 : 0);
+    // pick: the coder's three or four values per row
+    const size_t need = sb + ob + (pick ? (size_t)rows * 4 * 4 : 0);
     if (need > G.cdf_bytes) {
         if (G.cdf_mem) {
             if (hipStreamSynchronize(G.stream) != hipSuccess) return false;
@@ -1306,74 +1307,59 @@ int32_t redukt_backend_forward_batch_cdf(uint32_t n_streams, const uint32_t* slo
     return BACKEND_OK;
 }
 
-int32_t redukt_backend_forward_batch_cdf_sym(uint32_t n_streams, const uint32_t* slots, const uint32_t* tokens,
-                                             const uint32_t* next_syms, uint32_t* out_bounds, uint32_t vocab_size) {
+namespace {
+// forward_batch_cdf_sym and _find: one H2D copy of the slots, the tokens and each stream's
+// next symbol (sym) or decoder target (find) through the pool's pinned staging; the step,
+// the device CDF and the kernel that reads the rows; `per` u32 a stream back through the
+// pinned output staging, waited for by polling its event.
+int32_t forward_batch_cdf_read(uint32_t n_streams, const uint32_t* slots, const uint32_t* tokens,
+                               const uint32_t* third, uint32_t* out, uint32_t vocab_size, bool find) {
     if (!G.ready || G.batch.cap == 0) return BACKEND_INIT_FAILED;
     const uint32_t V = G.kind == kKindRwkv ? G.rdims.vocab : G.dims.vocab;
     if (vocab_size != V || n_streams > G.batch.cap || V >= (1u << 24)) return BACKEND_INVALID_ARGUMENT;
     if (n_streams == 0) return BACKEND_OK;
-    if (!slots || !tokens || !next_syms || !out_bounds) return BACKEND_INVALID_ARGUMENT;
+    if (!slots || !tokens || !third || !out) return BACKEND_INVALID_ARGUMENT;
     Pool& p = G.batch;
     memset(p.seen, 0, p.cap);
     for (uint32_t b = 0; b < n_streams; b++) {
-        if (slots[b] >= p.cap || p.seen[slots[b]] || tokens[b] >= V || next_syms[b] >= V) return BACKEND_INVALID_ARGUMENT;
+        if (slots[b] >= p.cap || p.seen[slots[b]] || tokens[b] >= V || (!find && third[b] >= V))
+            return BACKEND_INVALID_ARGUMENT;
         p.seen[slots[b]] = 1;
     }
+    const size_t per = find ? 4 : 3;
+    const size_t out_bytes = sizeof(uint32_t) * per * n_streams;
+    if (out_bytes > p.out_stage_bytes) return BACKEND_FORWARD_FAILED;   // staging holds >= 4 u32 a stream
     void* scratch = nullptr;
-    uint32_t *d_cdf = nullptr, *d_pick = nullptr;
-    if (!cdf_space(n_streams, V, true, &scratch, &d_cdf, &d_pick)) return BACKEND_FORWARD_FAILED;
-    uint32_t* const d_sym = d_pick;
-    uint32_t* const d_bounds = d_pick + n_streams;
+    uint32_t *d_cdf = nullptr, *d_out = nullptr;
+    if (!cdf_space(n_streams, V, true, &scratch, &d_cdf, &d_out)) return BACKEND_FORWARD_FAILED;
     memcpy(p.h_slots, slots, sizeof(uint32_t) * n_streams);
     memcpy(p.h_slots + n_streams, tokens, sizeof(uint32_t) * n_streams);
-    if (hipMemcpyAsync(p.d_slots, p.h_slots, sizeof(uint32_t) * 2 * n_streams, hipMemcpyHostToDevice, G.stream) !=
-            hipSuccess ||
-        hipMemcpyAsync(d_sym, next_syms, sizeof(uint32_t) * n_streams, hipMemcpyHostToDevice, G.stream) != hipSuccess)
+    memcpy(p.h_slots + 2 * n_streams, third, sizeof(uint32_t) * n_streams);
+    if (hipMemcpyAsync(p.d_slots, p.h_slots, sizeof(uint32_t) * 3 * n_streams, hipMemcpyHostToDevice, G.stream) !=
+        hipSuccess)
         return BACKEND_FORWARD_FAILED;
+    const uint32_t* d_third = p.d_slots + 2 * n_streams;
     if (run_step(p, n_streams, p.d_slots, p.d_slots + n_streams, p.out, false, false) != hipSuccess ||
         cdf_launch(p.out, n_streams, V, scratch, d_cdf, G.stream) != hipSuccess ||
-        cdf_pick_launch(d_cdf, n_streams, V, d_sym, d_bounds, G.stream) != hipSuccess)
+        (find ? cdf_find_launch(d_cdf, n_streams, V, d_third, d_out, G.stream)
+              : cdf_pick_launch(d_cdf, n_streams, V, d_third, d_out, G.stream)) != hipSuccess)
         return BACKEND_FORWARD_FAILED;
-    if (hipMemcpyAsync(out_bounds, d_bounds, sizeof(uint32_t) * 3 * n_streams, hipMemcpyDeviceToHost, G.stream) !=
-            hipSuccess ||
-        hipStreamSynchronize(G.stream) != hipSuccess)
+    if (hipMemcpyAsync(p.h_out, d_out, out_bytes, hipMemcpyDeviceToHost, G.stream) != hipSuccess ||
+        hipEventRecord(p.out_ev[0], G.stream) != hipSuccess || !event_wait(p.out_ev[0]))
         return BACKEND_FORWARD_FAILED;
+    memcpy(out, p.h_out, out_bytes);
     return BACKEND_OK;
+}
+}  // namespace
+
+int32_t redukt_backend_forward_batch_cdf_sym(uint32_t n_streams, const uint32_t* slots, const uint32_t* tokens,
+                                             const uint32_t* next_syms, uint32_t* out_bounds, uint32_t vocab_size) {
+    return forward_batch_cdf_read(n_streams, slots, tokens, next_syms, out_bounds, vocab_size, false);
 }
 
 int32_t redukt_backend_forward_batch_cdf_find(uint32_t n_streams, const uint32_t* slots, const uint32_t* tokens,
                                               const uint32_t* targets, uint32_t* out_found, uint32_t vocab_size) {
-    if (!G.ready || G.batch.cap == 0) return BACKEND_INIT_FAILED;
-    const uint32_t V = G.kind == kKindRwkv ? G.rdims.vocab : G.dims.vocab;
-    if (vocab_size != V || n_streams > G.batch.cap || V >= (1u << 24)) return BACKEND_INVALID_ARGUMENT;
-    if (n_streams == 0) return BACKEND_OK;
-    if (!slots || !tokens || !targets || !out_found) return BACKEND_INVALID_ARGUMENT;
-    Pool& p = G.batch;
-    memset(p.seen, 0, p.cap);
-    for (uint32_t b = 0; b < n_streams; b++) {
-        if (slots[b] >= p.cap || p.seen[slots[b]] || tokens[b] >= V) return BACKEND_INVALID_ARGUMENT;
-        p.seen[slots[b]] = 1;
-    }
-    void* scratch = nullptr;
-    uint32_t *d_cdf = nullptr, *d_pick = nullptr;
-    if (!cdf_space(n_streams, V, true, &scratch, &d_cdf, &d_pick)) return BACKEND_FORWARD_FAILED;
-    uint32_t* const d_cum = d_pick;
-    uint32_t* const d_found = d_pick + n_streams;
-    memcpy(p.h_slots, slots, sizeof(uint32_t) * n_streams);
-    memcpy(p.h_slots + n_streams, tokens, sizeof(uint32_t) * n_streams);
-    if (hipMemcpyAsync(p.d_slots, p.h_slots, sizeof(uint32_t) * 2 * n_streams, hipMemcpyHostToDevice, G.stream) !=
-            hipSuccess ||
-        hipMemcpyAsync(d_cum, targets, sizeof(uint32_t) * n_streams, hipMemcpyHostToDevice, G.stream) != hipSuccess)
-        return BACKEND_FORWARD_FAILED;
-    if (run_step(p, n_streams, p.d_slots, p.d_slots + n_streams, p.out, false, false) != hipSuccess ||
-        cdf_launch(p.out, n_streams, V, scratch, d_cdf, G.stream) != hipSuccess ||
-        cdf_find_launch(d_cdf, n_streams, V, d_cum, d_found, G.stream) != hipSuccess)
-        return BACKEND_FORWARD_FAILED;
-    if (hipMemcpyAsync(out_found, d_found, sizeof(uint32_t) * 4 * n_streams, hipMemcpyDeviceToHost, G.stream) !=
-            hipSuccess ||
-        hipStreamSynchronize(G.stream) != hipSuccess)
-        return BACKEND_FORWARD_FAILED;
-    return BACKEND_OK;
+    return forward_batch_cdf_read(n_streams, slots, tokens, targets, out_found, vocab_size, true);
 }
 
 int32_t redukt_backend_cdf_from_logits_device(const float* d_logits, uint32_t rows, uint32_t n, uint32_t* d_cdf) {

@@ -272,9 +272,11 @@ int32_t redukt_lockstep::run_lockstep(const Job& job, redukt_lockstep_stats& sta
             if (lanes[i].file >= 0) active.push_back(i);
         if (active.empty()) break;
 
-        // Phase A: one unit per active stream on the pool.
+        // Phase A: one unit per active stream on the pool; with the device's three or four
+        // values a stream a unit is a few integer operations, less than a hand-over to the
+        // pool's threads costs, so the caller codes them all.
         const auto ta = Clock::now();
-        redukt_host::parallel_for(active.size(), threads, [&](size_t k) {
+        redukt_host::parallel_for(active.size(), pick || find ? 1u : threads, [&](size_t k) {
             code_step(job, lanes[active[k]], active[k]);
         });
         stats.tokens += active.size();

@@ -154,8 +154,9 @@ struct Pool {
     float* pmax = nullptr;       // [rows16][heads] each head's largest magnitude in gatedf
     float* out = nullptr;        // [cap][vocab] logits or probabilities
     uint32_t* slots = nullptr;   // [cap] slots of the current step (validated copy)
-    uint32_t* d_slots = nullptr; // [2 cap] H2D target of the synchronous entry points: n slots, then n tokens
-    uint32_t* h_slots = nullptr; // [2 cap] pinned staging of the same
+    uint32_t* d_slots = nullptr; // [3 cap] H2D target of the synchronous entry points: n slots, n tokens,
+                                 // then n next symbols or decoder targets (the CDF readers)
+    uint32_t* h_slots = nullptr; // [3 cap] pinned staging of the same
     // Pinned staging of the outputs handed back to host memory (up to one round of
     // out_stage_bytes), with one completion event per chunk of a round (at most four).
     unsigned char* h_out = nullptr;
