@@ -182,6 +182,19 @@ int32_t redukt_backend_forward_batch_cdf_sym(uint32_t n_streams, const uint32_t*
 int32_t redukt_backend_forward_batch_cdf_find(uint32_t n_streams, const uint32_t* slots, const uint32_t* tokens,
                                               const uint32_t* targets, uint32_t* out_found, uint32_t vocab_size);
 
+/* forward_batch_cdf_sym in two halves, so that a caller that knows its next inputs
+ * (compression) can queue the next step before it has used this one's results: _submit
+ * validates and queues the step, the device CDF and the copy of the three values per
+ * stream, and returns at once with *ticket naming the call; _wait(ticket) waits for that
+ * call and writes out_bounds (3 u32 a stream, n_streams as submitted).  At most two calls
+ * are in flight: a third _submit before one of them is waited for is refused.  Calls run in
+ * submission order, after and before every other entry point's work, and each sees the
+ * recurrent state its predecessors left.  Same validation and state rules as forward_batch.
+ * No reference counterpart (an extension of the CDF entry points above). */
+int32_t redukt_backend_forward_batch_cdf_sym_submit(uint32_t n_streams, const uint32_t* slots, const uint32_t* tokens,
+                                                    const uint32_t* next_syms, uint32_t vocab_size, uint64_t* ticket);
+int32_t redukt_backend_forward_batch_cdf_sym_wait(uint64_t ticket, uint32_t* out_bounds, uint32_t n_streams);
+
 /* The device CDF on caller logits: d_logits [rows][n] f32 -> d_cdf [rows][n + 1] u32,
  * both device pointers, stream-ordered on redukt_backend_stream() (the call does not
  * wait).  1 <= n < 2^24.  For tests and for callers that hold logits on the device. */

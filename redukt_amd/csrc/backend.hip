@@ -610,6 +610,25 @@ bool out_stage_alloc(Pool& p, size_t out_bytes) {
     return true;
 }
 
+// The host side of the queued calls' buffers (the device inputs are carved with the pool).
+bool queued_alloc(Pool& p, size_t n) {
+    for (Pool::Queued& q : p.queued) {
+        if (hipHostMalloc((void**)&q.h_in, sizeof(uint32_t) * 3 * n, hipHostMallocDefault) != hipSuccess) {
+            q.h_in = nullptr;
+            return false;
+        }
+        if (hipHostMalloc((void**)&q.h_res, sizeof(uint32_t) * 3 * n, hipHostMallocDefault) != hipSuccess) {
+            q.h_res = nullptr;
+            return false;
+        }
+        if (hipEventCreateWithFlags(&q.done, hipEventDisableTiming) != hipSuccess) {
+            q.done = nullptr;
+            return false;
+        }
+    }
+    return true;
+}
+
 // Host threads that copy a round's chunks: one job per round, body(t) run once by each of
 // the threads() threads (t = 0 is the caller).  A job ends when every helper has finished
 // its part, so nothing of a job is touched after run() returns.  The helpers start on first
@@ -701,6 +720,11 @@ void pool_free(Pool& p) {
     if (p.h_out) (void)hipHostFree(p.h_out);
     for (hipEvent_t& e : p.out_ev)
         if (e) (void)hipEventDestroy(e);
+    for (Pool::Queued& q : p.queued) {
+        if (q.h_in) (void)hipHostFree(q.h_in);
+        if (q.h_res) (void)hipHostFree(q.h_res);
+        if (q.done) (void)hipEventDestroy(q.done);
+    }
     free(p.seen);
     p = Pool{};
 }
@@ -751,6 +775,7 @@ bool pool_alloc_rwkv(Pool& p, uint32_t cap) {
     bool ok = pool_carve(p, [&](Carve& c) {
         c.take(p.slots, slot_words(cap));
         c.take(p.d_slots, 3 * n);  // a step's n slots, its n tokens, then a word per stream for the CDF readers (one H2D copy)
+        for (Pool::Queued& q : p.queued) c.take(q.d_in, 3 * n);
         c.take(p.x, n * d);
         c.take(p.vfirst, n * d);
         c.take(p.rkv, n * 3 * d);
@@ -774,6 +799,7 @@ bool pool_alloc_rwkv(Pool& p, uint32_t cap) {
         c.take(p.wkv, z.wkv);
     });
     ok = ok && hipHostMalloc((void**)&p.h_slots, sizeof(uint32_t) * 3 * n, hipHostMallocDefault) == hipSuccess;
+    ok = ok && queued_alloc(p, n);
 
     ok = ok && (p.seen = (uint8_t*)calloc(n, 1)) != nullptr;
     ok = ok && out_stage_alloc(p, (size_t)n * vocab_of_model() * sizeof(float));
@@ -793,6 +819,7 @@ bool pool_alloc(Pool& p, uint32_t cap) {
     bool ok = pool_carve(p, [&](Carve& c) {
         c.take(p.slots, slot_words(cap));
         c.take(p.d_slots, 3 * n);  // a step's n slots, its n tokens, then a word per stream for the CDF readers (one H2D copy)
+        for (Pool::Queued& q : p.queued) c.take(q.d_in, 3 * n);
         c.take(p.x, n * d);
         c.take(p.xw, xw_elems(D, cap));
         c.take(p.ssp, ssp_floats(D, cap));
@@ -807,6 +834,7 @@ bool pool_alloc(Pool& p, uint32_t cap) {
         c.take(p.ssm, (size_t)D.nl * ns * di * 16);
     });
     ok = ok && hipHostMalloc((void**)&p.h_slots, sizeof(uint32_t) * 3 * n, hipHostMallocDefault) == hipSuccess;
+    ok = ok && queued_alloc(p, n);
 
     ok = ok && (p.seen = (uint8_t*)calloc(n, 1)) != nullptr;
     ok = ok && out_stage_alloc(p, (size_t)n * vocab_of_model() * sizeof(float));
@@ -1355,6 +1383,70 @@ int32_t forward_batch_cdf_read(uint32_t n_streams, const uint32_t* slots, const 
 int32_t redukt_backend_forward_batch_cdf_sym(uint32_t n_streams, const uint32_t* slots, const uint32_t* tokens,
                                              const uint32_t* next_syms, uint32_t* out_bounds, uint32_t vocab_size) {
     return forward_batch_cdf_read(n_streams, slots, tokens, next_syms, out_bounds, vocab_size, false);
+}
+
+int32_t redukt_backend_forward_batch_cdf_sym_submit(uint32_t n_streams, const uint32_t* slots, const uint32_t* tokens,
+                                                    const uint32_t* next_syms, uint32_t vocab_size, uint64_t* ticket) {
+    if (!G.ready || G.batch.cap == 0) return BACKEND_INIT_FAILED;
+    const uint32_t V = G.kind == kKindRwkv ? G.rdims.vocab : G.dims.vocab;
+    if (!ticket || vocab_size != V || n_streams > G.batch.cap || V >= (1u << 24)) return BACKEND_INVALID_ARGUMENT;
+    if (n_streams > 0 && (!slots || !tokens || !next_syms)) return BACKEND_INVALID_ARGUMENT;
+    Pool& p = G.batch;
+    Pool::Queued* q = nullptr;
+    for (Pool::Queued& c : p.queued)
+        if (c.ticket == 0) {
+            q = &c;
+            break;
+        }
+    if (!q) return BACKEND_INVALID_ARGUMENT;   // Pool::kQueued calls in flight: wait for one first
+    memset(p.seen, 0, p.cap);
+    for (uint32_t b = 0; b < n_streams; b++) {
+        if (slots[b] >= p.cap || p.seen[slots[b]] || tokens[b] >= V || next_syms[b] >= V) return BACKEND_INVALID_ARGUMENT;
+        p.seen[slots[b]] = 1;
+    }
+    if (n_streams > 0) {
+        void* scratch = nullptr;
+        uint32_t *d_cdf = nullptr, *d_pick = nullptr;
+        // (a regrown scratch synchronizes the stream first, the other call's work included)
+        if (!cdf_space(n_streams, V, true, &scratch, &d_cdf, &d_pick)) return BACKEND_FORWARD_FAILED;
+        memcpy(q->h_in, slots, sizeof(uint32_t) * n_streams);
+        memcpy(q->h_in + n_streams, tokens, sizeof(uint32_t) * n_streams);
+        memcpy(q->h_in + 2 * n_streams, next_syms, sizeof(uint32_t) * n_streams);
+        const bool ok =
+            hipMemcpyAsync(q->d_in, q->h_in, sizeof(uint32_t) * 3 * n_streams, hipMemcpyHostToDevice, G.stream) ==
+                hipSuccess &&
+            run_step(p, n_streams, q->d_in, q->d_in + n_streams, p.out, false, false) == hipSuccess &&
+            cdf_launch(p.out, n_streams, V, scratch, d_cdf, G.stream) == hipSuccess &&
+            cdf_pick_launch(d_cdf, n_streams, V, q->d_in + 2 * n_streams, d_pick, G.stream) == hipSuccess &&
+            hipMemcpyAsync(q->h_res, d_pick, sizeof(uint32_t) * 3 * n_streams, hipMemcpyDeviceToHost, G.stream) ==
+                hipSuccess;
+        if (!ok) {
+            // what was queued finishes before its buffers can be reused
+            (void)hipStreamSynchronize(G.stream);
+            return BACKEND_FORWARD_FAILED;
+        }
+    }
+    if (hipEventRecord(q->done, G.stream) != hipSuccess) {
+        (void)hipStreamSynchronize(G.stream);
+        return BACKEND_FORWARD_FAILED;
+    }
+    q->n = n_streams;
+    q->ticket = p.next_ticket++;
+    *ticket = q->ticket;
+    return BACKEND_OK;
+}
+
+int32_t redukt_backend_forward_batch_cdf_sym_wait(uint64_t ticket, uint32_t* out_bounds, uint32_t n_streams) {
+    if (!G.ready || G.batch.cap == 0) return BACKEND_INIT_FAILED;
+    Pool::Queued* q = nullptr;
+    for (Pool::Queued& c : G.batch.queued)
+        if (ticket != 0 && c.ticket == ticket) q = &c;
+    if (!q || n_streams != q->n || (n_streams > 0 && !out_bounds)) return BACKEND_INVALID_ARGUMENT;
+    const bool ok = event_wait(q->done);
+    if (ok) memcpy(out_bounds, q->h_res, sizeof(uint32_t) * 3 * n_streams);
+    q->ticket = 0;
+    q->n = 0;
+    return ok ? BACKEND_OK : BACKEND_FORWARD_FAILED;
 }
 
 int32_t redukt_backend_forward_batch_cdf_find(uint32_t n_streams, const uint32_t* slots, const uint32_t* tokens,

@@ -42,6 +42,10 @@ struct PluginApi {
     // optional: the same, handing back only the coder's three values for a known next symbol
     int32_t (*forward_batch_cdf_sym)(uint32_t, const uint32_t*, const uint32_t*, const uint32_t*, uint32_t*,
                                      uint32_t) = nullptr;
+    // optional: forward_batch_cdf_sym queued (submit) and collected (wait)
+    int32_t (*cdf_sym_submit)(uint32_t, const uint32_t*, const uint32_t*, const uint32_t*, uint32_t,
+                              uint64_t*) = nullptr;
+    int32_t (*cdf_sym_wait)(uint64_t, uint32_t*, uint32_t) = nullptr;
     // optional: the same, searching each row on the device for the decoder's target
     int32_t (*forward_batch_cdf_find)(uint32_t, const uint32_t*, const uint32_t*, const uint32_t*, uint32_t*,
                                       uint32_t) = nullptr;
@@ -68,6 +72,8 @@ struct PluginApi {
         bind(forward_batch_cdf, "redukt_backend_forward_batch_cdf");
         bind(forward_batch_cdf_sym, "redukt_backend_forward_batch_cdf_sym");
         bind(forward_batch_cdf_find, "redukt_backend_forward_batch_cdf_find");
+        bind(cdf_sym_submit, "redukt_backend_forward_batch_cdf_sym_submit");
+        bind(cdf_sym_wait, "redukt_backend_forward_batch_cdf_sym_wait");
         v2 = abi_version && batch_init && batch_reset && forward_batch && abi_version() >= 2;
         return true;
     }
@@ -87,6 +93,9 @@ struct Lane {
     uint64_t since_reset = 0;  // PluginState::tick schedule
     uint32_t row = 0;          // logits row of this lane's last forward
     int32_t target_status = REDUKT_CODEC_OK;  // the decoder target's status for that forward
+    uint64_t code_pos = 0;     // pipelined compression: the position this iteration codes
+    uint32_t code_row = 0;     // and its row in the previous forward
+    bool leaves = false;       // and whether the file ends with it
     redukt_rc_encoder enc;
     redukt_rc_decoder dec;
 };
@@ -127,6 +136,10 @@ struct redukt_lockstep {
     // (forward_batch_cdf_find, 16 bytes a stream).
     bool sym_cdf = false;
     bool find_cdf = false;
+    // Compression on that path queues each step's forward before it codes the previous
+    // step's results (forward_batch_cdf_sym_submit / _wait): the device never waits for the
+    // host between steps.
+    bool pipeline = false;
     std::vector<float> logits;
     std::vector<uint32_t> cdf;
     std::vector<uint32_t> uniform;
@@ -213,6 +226,7 @@ struct redukt_lockstep {
     }
 
     int32_t run_lockstep(const Job& job, redukt_lockstep_stats& stats);
+    int32_t run_compress_pipelined(const Job& job, redukt_lockstep_stats& stats);
     int32_t run_single(const Job& job, redukt_lockstep_stats& stats);
 };
 
@@ -338,6 +352,135 @@ int32_t redukt_lockstep::run_lockstep(const Job& job, redukt_lockstep_stats& sta
     return REDUKT_LOCKSTEP_OK;
 }
 
+int32_t redukt_lockstep::run_compress_pipelined(const Job& job, redukt_lockstep_stats& stats) {
+    // run_lockstep's compression with the same admissions, ticks, forwards and coding per
+    // iteration, reordered: a file's tokens are known in advance, so which lanes step
+    // next, and on which tokens, follows from the lengths alone.  Iteration i queues its
+    // forward before it codes with the results of iteration i - 1's forward.  A lane whose
+    // coding fails (an out-of-range token) leaves after that forward was queued with a
+    // stand-in token; its slot is reset before it takes another file, and no other
+    // stream's results depend on it.
+    std::vector<Lane> lanes(slots);
+    std::vector<uint32_t> active, fwd_slots, fwd_tokens, fwd_syms, resets;
+    active.reserve(slots);
+    uint32_t next_file = 0;
+    uint64_t pending = 0;   // ticket of the forward whose results the next coding uses
+    uint32_t pending_n = 0;
+    auto abort_run = [&]() {
+        if (pending) (void)api.cdf_sym_wait(pending, bounds.data(), pending_n);
+        for (Lane& l : lanes) {
+            if (l.file < 0) continue;
+            if (job.status) job.status[l.file] = REDUKT_CODEC_INCOMPLETE;
+            job.out_len[l.file] = 0;
+            l.file = -1;
+        }
+        for (uint32_t f = next_file; f < job.n_files; ++f) {
+            if (job.status) job.status[f] = REDUKT_CODEC_INCOMPLETE;
+            job.out_len[f] = 0;
+        }
+        return REDUKT_LOCKSTEP_FORWARD;
+    };
+    for (;;) {
+        resets.clear();
+        for (uint32_t i = 0; i < slots; ++i) {
+            if (lanes[i].file >= 0) continue;
+            while (next_file < job.n_files && job.n_tokens[next_file] == 0) {
+                if (job.status) job.status[next_file] = REDUKT_CODEC_INVALID_ARG;  // "empty input"
+                ++next_file;
+            }
+            if (next_file >= job.n_files) break;
+            start_file(job, lanes[i], next_file++);
+            resets.push_back(i);
+        }
+        if (!resets.empty() && api.batch_reset(resets.data(), uint32_t(resets.size())) != BACKEND_OK)
+            return abort_run();
+        active.clear();
+        for (uint32_t i = 0; i < slots; ++i)
+            if (lanes[i].file >= 0) active.push_back(i);
+        if (active.empty()) break;
+
+        // What Phase A will code, and how far it takes each lane.
+        const auto tb = Clock::now();
+        fwd_slots.clear();
+        fwd_tokens.clear();
+        fwd_syms.clear();
+        resets.clear();
+        for (uint32_t i : active) {
+            Lane& l = lanes[i];
+            l.code_pos = l.pos;
+            l.code_row = l.row;
+            l.leaves = l.pos + 1 >= job.n_tokens[l.file];
+        }
+        // Phase B (ticks, then the forward) for the lanes that go on, queued first.
+        for (uint32_t i : active) {
+            Lane& l = lanes[i];
+            if (l.leaves) continue;
+            if (job.reset_every > 0 && l.since_reset >= job.reset_every) {
+                resets.push_back(i);
+                l.since_reset = 0;
+            }
+            ++l.since_reset;
+            l.row = uint32_t(fwd_slots.size());
+            fwd_slots.push_back(i);
+            const uint32_t tok = job.tokens[l.file][l.code_pos], next = job.tokens[l.file][l.code_pos + 1];
+            fwd_tokens.push_back(tok < vocab ? tok : 0u);   // an out-of-range token fails its file below
+            fwd_syms.push_back(next < vocab ? next : 0u);
+        }
+        // A tick or forward that fails ends the run after this iteration's coding, as in
+        // run_lockstep, where they come after it.
+        uint64_t ticket = 0;
+        const uint32_t nf = uint32_t(fwd_slots.size());
+        bool queued = resets.empty() || api.batch_reset(resets.data(), uint32_t(resets.size())) == BACKEND_OK;
+        queued = queued && (nf == 0 || api.cdf_sym_submit(nf, fwd_slots.data(), fwd_tokens.data(), fwd_syms.data(),
+                                                          vocab, &ticket) == BACKEND_OK);
+        if (!queued) ticket = 0;
+        // Phase A with the previous forward's results.
+        if (pending) {
+            const int32_t rc = api.cdf_sym_wait(pending, bounds.data(), pending_n);
+            pending = 0;
+            if (rc != BACKEND_OK) {
+                pending = ticket;
+                pending_n = nf;
+                return abort_run();
+            }
+        }
+        pending = ticket;
+        pending_n = nf;
+        stats.forward_secs += since(tb);
+        ++stats.steps;
+        const auto ta = Clock::now();
+        for (uint32_t i : active) {
+            Lane& l = lanes[i];
+            const uint32_t tok = job.tokens[l.file][l.code_pos];
+            int32_t st;
+            if (l.code_pos == 0)
+                st = l.enc.encode_symbol(tok, uniform.data(), vocab);
+            else {
+                const uint32_t* b = bounds.data() + size_t(l.code_row) * 3;
+                st = tok < vocab ? l.enc.encode(b[0], b[1], b[2]) : REDUKT_CODEC_INVALID_ARG;  // as encode_symbol
+            }
+            if (st != REDUKT_CODEC_OK) {
+                l.status = st;
+                l.done = true;
+            } else {
+                l.next_token = tok;
+                l.pos = l.code_pos + 1;
+                l.done = l.leaves;
+            }
+        }
+        stats.tokens += active.size();
+        stats.code_secs += since(ta);
+        for (uint32_t i : active) {
+            if (lanes[i].done) {
+                end_file(job, lanes[i]);
+                ++stats.files;
+            }
+        }
+        if (!queued) return abort_run();
+    }
+    return REDUKT_LOCKSTEP_OK;
+}
+
 int32_t redukt_lockstep::run_single(const Job& job, redukt_lockstep_stats& stats) {
     // The single-file path of the plugin backbone: the v1 global state, one file after
     // the other (codec.rs:1227-1300 with the plugin's forward_into and tick).
@@ -386,7 +529,9 @@ int32_t run(redukt_lockstep* ls, const Job& job, redukt_lockstep_stats* stats_ou
     Job j = job;
     j.status = st.data();
     const auto t0 = Clock::now();
-    int32_t rc = ls->slots ? ls->run_lockstep(j, stats) : ls->run_single(j, stats);
+    int32_t rc = !ls->slots ? ls->run_single(j, stats)
+                 : job.mode == Mode::Encode && ls->device_cdf && ls->pipeline ? ls->run_compress_pipelined(j, stats)
+                                                                               : ls->run_lockstep(j, stats);
     stats.secs = since(t0);
     if (rc == REDUKT_LOCKSTEP_OK) rc = overall(j, st);
     if (job.status) std::memcpy(job.status, st.data(), st.size() * sizeof(int32_t));
@@ -447,6 +592,9 @@ extern "C" int32_t redukt_lockstep_open(const char* plugin_path, const char* wei
     const bool rows_only = e && *e && !strcmp(e, "0");
     ls->sym_cdf = ls->api.forward_batch_cdf_sym != nullptr && !rows_only;
     ls->find_cdf = ls->api.forward_batch_cdf_find != nullptr && !rows_only;
+    // REDUKT_LOCKSTEP_PIPELINE=0: compression waits for each step before queueing the next.
+    const char* pe = getenv("REDUKT_LOCKSTEP_PIPELINE");
+    ls->pipeline = ls->sym_cdf && ls->api.cdf_sym_submit && ls->api.cdf_sym_wait && !(pe && *pe && !strcmp(pe, "0"));
     ls->bounds.assign(rows * 4, 0u);
     *out = ls.release();
     return REDUKT_LOCKSTEP_OK;

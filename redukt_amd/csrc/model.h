@@ -163,6 +163,20 @@ struct Pool {
     size_t out_stage_bytes = 0;
     hipEvent_t out_ev[32] = {};
     uint8_t* seen = nullptr;     // host duplicate check, cap bytes
+    // Queued calls (forward_batch_cdf_sym_submit / _wait): at most kQueued in flight, each
+    // with its own inputs (3 cap u32: slots, tokens, next symbols; pinned and on the
+    // device), its results (3 cap u32, pinned) and its completion event.
+    static constexpr uint32_t kQueued = 2;
+    struct Queued {
+        uint32_t* h_in = nullptr;
+        uint32_t* d_in = nullptr;
+        uint32_t* h_res = nullptr;
+        hipEvent_t done = nullptr;
+        uint64_t ticket = 0;   // 0: free
+        uint32_t n = 0;
+    };
+    Queued queued[kQueued];
+    uint64_t next_ticket = 1;
 };
 
 // Kernel classes a caller can time with HIP events (see Probe).

@@ -48,7 +48,8 @@ V3_SYMBOLS = ("redukt_backend_init_ex", "redukt_backend_forward_batch_probs", "r
               "redukt_backend_eval_math", "redukt_backend_forward_batch_device_noalloc",
               "redukt_backend_forward_batch_cdf", "redukt_backend_cdf_from_logits_device",
               "redukt_backend_copy_probe", "redukt_backend_forward_batch_cdf_sym",
-              "redukt_backend_forward_batch_cdf_find")
+              "redukt_backend_forward_batch_cdf_find",
+              "redukt_backend_forward_batch_cdf_sym_submit", "redukt_backend_forward_batch_cdf_sym_wait")
 # redukt_backend_eval_math function codes: the portable element-wise functions
 MATH_FNS = {"exp": 0, "lane_exp": 1, "ln": 2, "softplus": 3, "lane_sigmoid": 4, "sigmoid": 5}
 
@@ -161,6 +162,11 @@ class PluginLibrary:
             L.redukt_backend_forward_batch_cdf_find.argtypes = [ctypes.c_uint32, _u32p, _u32p, _u32p, _u32p,
                                                                 ctypes.c_uint32]
             L.redukt_backend_forward_batch_cdf_find.restype = ctypes.c_int32
+            L.redukt_backend_forward_batch_cdf_sym_submit.argtypes = [ctypes.c_uint32, _u32p, _u32p, _u32p,
+                                                                      ctypes.c_uint32, ctypes.POINTER(ctypes.c_uint64)]
+            L.redukt_backend_forward_batch_cdf_sym_submit.restype = ctypes.c_int32
+            L.redukt_backend_forward_batch_cdf_sym_wait.argtypes = [ctypes.c_uint64, _u32p, ctypes.c_uint32]
+            L.redukt_backend_forward_batch_cdf_sym_wait.restype = ctypes.c_int32
             L.redukt_backend_cdf_from_logits_device.argtypes = [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
                                                                 ctypes.c_void_p]
             L.redukt_backend_cdf_from_logits_device.restype = ctypes.c_int32
@@ -415,6 +421,23 @@ class PluginBackend:
         return BackendResult.from_code(self.lib.lib.redukt_backend_forward_batch_cdf_find(
             len(s), _ptr(s, ctypes.c_uint32), _ptr(t, ctypes.c_uint32), _ptr(y, ctypes.c_uint32),
             _ptr(out, ctypes.c_uint32), self.vocab))
+
+    def forward_batch_cdf_sym_submit(self, slots: Sequence[int], tokens: Sequence[int], next_syms: Sequence[int]):
+        """Queues forward_batch_cdf_sym; returns (result code, ticket)."""
+        s = np.ascontiguousarray(slots, dtype=np.uint32)
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        y = np.ascontiguousarray(next_syms, dtype=np.uint32)
+        ticket = ctypes.c_uint64(0)
+        code = self.lib.lib.redukt_backend_forward_batch_cdf_sym_submit(
+            len(s), _ptr(s, ctypes.c_uint32), _ptr(t, ctypes.c_uint32), _ptr(y, ctypes.c_uint32), self.vocab,
+            ctypes.byref(ticket))
+        return BackendResult.from_code(code), int(ticket.value)
+
+    def forward_batch_cdf_sym_wait(self, ticket: int, out: np.ndarray) -> BackendResult:
+        """Waits for a queued call and writes its three values per stream into out."""
+        assert out.dtype == np.uint32 and out.flags.c_contiguous and out.size % 3 == 0
+        return BackendResult.from_code(self.lib.lib.redukt_backend_forward_batch_cdf_sym_wait(
+            ticket, _ptr(out, ctypes.c_uint32), out.size // 3))
 
     def cdf_from_logits_device(self, d_logits: int, rows: int, n: int, d_cdf: int) -> BackendResult:
         return BackendResult.from_code(self.lib.lib.redukt_backend_cdf_from_logits_device(d_logits, rows, n, d_cdf))

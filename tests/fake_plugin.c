@@ -6,7 +6,11 @@
  * The weights file holds the vocabulary size as one little-endian u32.
  * FAKE_PLUGIN_ABI=1 in the environment makes abi_version() report a v1-only plugin.
  * FAKE_PLUGIN_FAIL_AFTER=k makes every forward / forward_batch after the first k
- * (counted since init) fail with FORWARD_FAILED. */
+ * (counted since init) fail with FORWARD_FAILED.
+ * Built with -DFAKE_PLUGIN_CDF (and linked against libredukt_host.so) it also exports the
+ * device-CDF entry points of the GPU library (include/redukt_backend.h), each computing its
+ * CDF rows with the host's redukt_cdf_from_logits: forward_batch_cdf, _sym, _find and the
+ * queued _sym_submit / _sym_wait (two calls in flight, run at submit). */
 #include <stdint.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -121,3 +125,118 @@ int32_t redukt_backend_forward_batch(uint32_t n, const uint32_t* slots, const ui
     }
     return 0;
 }
+
+#ifdef FAKE_PLUGIN_CDF
+int32_t redukt_cdf_from_logits(const float* logits, uint32_t n, uint32_t* cdf);
+uint32_t redukt_cdf_lookup(const uint32_t* cdf, uint32_t n, uint32_t cum_freq);
+
+/* One step of the n streams, then each row's CDF (n x (vocab + 1) u32 into cdf). */
+static int32_t step_cdf(uint32_t n, const uint32_t* slots, const uint32_t* toks, uint32_t* cdf) {
+    if (n > g_cap || (n && (!slots || !toks))) return 5;
+    for (uint32_t i = 0; i < n; ++i) {
+        if (slots[i] >= g_cap || toks[i] >= g_vocab) return 5;
+        for (uint32_t j = 0; j < i; ++j)
+            if (slots[j] == slots[i]) return 5;
+    }
+    if (fail_now()) return 2;
+    float* lg = (float*)malloc(sizeof(float) * g_vocab);
+    if (!lg) return 2;
+    for (uint32_t i = 0; i < n; ++i) {
+        g_slot[slots[i]] = step(g_slot[slots[i]], toks[i]);
+        logits_of(g_slot[slots[i]], lg);
+        if (redukt_cdf_from_logits(lg, g_vocab, cdf + (size_t)i * (g_vocab + 1)) != 0) {
+            free(lg);
+            return 2;
+        }
+    }
+    free(lg);
+    return 0;
+}
+
+int32_t redukt_backend_forward_batch_cdf(uint32_t n, const uint32_t* slots, const uint32_t* toks, uint32_t* out,
+                                         uint32_t cdf_len) {
+    if (cdf_len != g_vocab + 1 || !out) return 5;
+    return step_cdf(n, slots, toks, out);
+}
+
+/* The three values per stream the coder reads for sym[i] (3 u32 a stream into out). */
+static int32_t step_sym(uint32_t n, const uint32_t* slots, const uint32_t* toks, const uint32_t* syms,
+                        uint32_t* out) {
+    for (uint32_t i = 0; i < n; ++i)
+        if (syms[i] >= g_vocab) return 5;
+    uint32_t* cdf = (uint32_t*)malloc(sizeof(uint32_t) * ((size_t)n * (g_vocab + 1) + 1));
+    if (!cdf) return 2;
+    const int32_t rc = step_cdf(n, slots, toks, cdf);
+    for (uint32_t i = 0; rc == 0 && i < n; ++i) {
+        const uint32_t* row = cdf + (size_t)i * (g_vocab + 1);
+        out[3 * i] = row[syms[i]];
+        out[3 * i + 1] = row[syms[i] + 1];
+        out[3 * i + 2] = row[g_vocab];
+    }
+    free(cdf);
+    return rc;
+}
+
+int32_t redukt_backend_forward_batch_cdf_sym(uint32_t n, const uint32_t* slots, const uint32_t* toks,
+                                             const uint32_t* syms, uint32_t* out, uint32_t vocab) {
+    if (vocab != g_vocab || (n && (!syms || !out))) return 5;
+    return step_sym(n, slots, toks, syms, out);
+}
+
+int32_t redukt_backend_forward_batch_cdf_find(uint32_t n, const uint32_t* slots, const uint32_t* toks,
+                                              const uint32_t* targets, uint32_t* out, uint32_t vocab) {
+    if (vocab != g_vocab || (n && (!targets || !out))) return 5;
+    uint32_t* cdf = (uint32_t*)malloc(sizeof(uint32_t) * ((size_t)n * (g_vocab + 1) + 1));
+    if (!cdf) return 2;
+    const int32_t rc = step_cdf(n, slots, toks, cdf);
+    for (uint32_t i = 0; rc == 0 && i < n; ++i) {
+        const uint32_t* row = cdf + (size_t)i * (g_vocab + 1);
+        const uint32_t s = redukt_cdf_lookup(row, g_vocab, targets[i]);
+        out[4 * i] = s;
+        out[4 * i + 1] = s < g_vocab ? row[s] : row[g_vocab];
+        out[4 * i + 2] = s < g_vocab ? row[s + 1] : row[g_vocab];
+        out[4 * i + 3] = row[g_vocab];
+    }
+    free(cdf);
+    return rc;
+}
+
+static struct {
+    uint64_t ticket;
+    uint32_t n;
+    uint32_t* res;
+} g_q[2];
+static uint64_t g_next_ticket = 1;
+
+int32_t redukt_backend_forward_batch_cdf_sym_submit(uint32_t n, const uint32_t* slots, const uint32_t* toks,
+                                                    const uint32_t* syms, uint32_t vocab, uint64_t* ticket) {
+    if (vocab != g_vocab || !ticket || (n && !syms)) return 5;
+    int k = g_q[0].ticket == 0 ? 0 : g_q[1].ticket == 0 ? 1 : -1;
+    if (k < 0) return 5;
+    uint32_t* res = (uint32_t*)malloc(sizeof(uint32_t) * (3 * (size_t)n + 1));
+    if (!res) return 2;
+    const int32_t rc = step_sym(n, slots, toks, syms, res);
+    if (rc != 0) {
+        free(res);
+        return rc;
+    }
+    g_q[k].ticket = g_next_ticket++;
+    g_q[k].n = n;
+    g_q[k].res = res;
+    *ticket = g_q[k].ticket;
+    return 0;
+}
+
+int32_t redukt_backend_forward_batch_cdf_sym_wait(uint64_t ticket, uint32_t* out, uint32_t n) {
+    for (int k = 0; k < 2; ++k) {
+        if (ticket == 0 || g_q[k].ticket != ticket) continue;
+        if (n != g_q[k].n || (n && !out)) return 5;
+        memcpy(out, g_q[k].res, sizeof(uint32_t) * 3 * (size_t)n);
+        free(g_q[k].res);
+        g_q[k].ticket = 0;
+        g_q[k].res = NULL;
+        return 0;
+    }
+    return 5;
+}
+#endif

@@ -150,6 +150,43 @@ def test_forward_batch_cdf_sym_rejects_bad_arguments(backend):
     assert code == ffi.BackendResult.INVALID_ARGUMENT   # vocab_size not the model's
 
 
+def test_forward_batch_cdf_sym_queued_equals_the_direct_call(backend):
+    # Queued calls (two in flight) give the direct call's values for the same tokens on
+    # other slots over three steps; a third call in flight, an unknown ticket and a count
+    # other than the submitted one are refused without disturbing the calls in flight.
+    backend.batch_init(64)
+    V = backend.vocab
+    rng = np.random.default_rng(14)
+    n = 23
+    toks = [[int(x) for x in rng.integers(0, V, n)] for _ in range(3)]
+    syms = [[int(x) for x in rng.integers(0, V, n)] for _ in range(3)]
+    want = []
+    for t in range(3):
+        w = np.empty(3 * n, np.uint32)
+        assert backend.forward_batch_cdf_sym(list(range(n)), toks[t], syms[t], w) == ffi.BackendResult.OK
+        want.append(w)
+    q = list(range(n, 2 * n))
+    rc0, t0 = backend.forward_batch_cdf_sym_submit(q, toks[0], syms[0])
+    rc1, t1 = backend.forward_batch_cdf_sym_submit(q, toks[1], syms[1])
+    assert rc0 == rc1 == ffi.BackendResult.OK and t0 != t1 and t0 > 0
+    assert backend.forward_batch_cdf_sym_submit(q, toks[2], syms[2])[0] == ffi.BackendResult.INVALID_ARGUMENT
+    got = np.empty(3 * n, np.uint32)
+    assert backend.forward_batch_cdf_sym_wait(t0, np.empty(3 * (n - 1), np.uint32)) == ffi.BackendResult.INVALID_ARGUMENT
+    assert backend.forward_batch_cdf_sym_wait(t0 + t1 + 7, got) == ffi.BackendResult.INVALID_ARGUMENT
+    assert backend.forward_batch_cdf_sym_wait(t0, got) == ffi.BackendResult.OK
+    assert np.array_equal(got, want[0])
+    rc2, t2 = backend.forward_batch_cdf_sym_submit(q, toks[2], syms[2])
+    assert rc2 == ffi.BackendResult.OK
+    assert backend.forward_batch_cdf_sym_wait(t1, got) == ffi.BackendResult.OK
+    assert np.array_equal(got, want[1])
+    assert backend.forward_batch_cdf_sym_wait(t2, got) == ffi.BackendResult.OK
+    assert np.array_equal(got, want[2])
+    assert backend.forward_batch_cdf_sym_wait(t0, got) == ffi.BackendResult.INVALID_ARGUMENT   # already collected
+    bad = list(q)
+    bad[3] = bad[2]
+    assert backend.forward_batch_cdf_sym_submit(bad, toks[0], syms[0])[0] == ffi.BackendResult.INVALID_ARGUMENT
+
+
 def test_forward_batch_cdf_find_equals_the_host_search(backend):
     # The symbol the device finds for a decoder target, with its two bounds and the total,
     # equals the host search (redukt_cdf_lookup) over the full device CDF row of the same
@@ -208,25 +245,27 @@ def test_forward_batch_cdf_rwkv7(tmp_path):
 def test_lockstep_device_cdf_bytes_equal_host_cdf(full_model, monkeypatch):
     # Host CDFs, device CDF rows, and the device paths that hand back only what the coder
     # reads (three values for compression's known symbol, the symbol found and its bounds
-    # for decompression's target: the defaults): the same archives, each decoding to its
-    # file.  Damaged archives (bytes flipped, a stream cut short, one empty, more tokens
+    # for decompression's target), with compression waiting for each step or queueing the
+    # next one first (the default): the same archives, each decoding to its file.  Damaged archives (bytes flipped, a stream cut short, one empty, more tokens
     # asked for than were coded) drive the decoders through arbitrary states: all three
     # decode them to the same tokens.
     rng = np.random.default_rng(77)
     files = [[int(x) for x in synth.zipf_tokens(rng, 50280, (L,))] for L in (40, 17, 64, 1, 33)]
     outs, bad = {}, {}
-    for dev, sym in ((False, "1"), (True, "0"), (True, "1")):
+    for dev, sym, pipe in ((False, "1", "1"), (True, "0", "1"), (True, "1", "0"), (True, "1", "1")):
         monkeypatch.setenv("REDUKT_LOCKSTEP_CDF_SYM", sym)
+        monkeypatch.setenv("REDUKT_LOCKSTEP_PIPELINE", pipe)
         with lockstep.Lockstep(full_model, ffi.DEFAULT_LIB, profile=Q8ROW_ALL, slots=3, device_cdf=dev) as ls:
             assert ls.device_cdf == dev
             streams, _ = ls.compress(files)
             back, _ = ls.decompress(streams, [len(f) for f in files])
             assert [b.tolist() for b in back] == files
-            outs[(dev, sym)] = streams
+            outs[(dev, sym, pipe)] = streams
             damaged = [bytes(x ^ 0x5A if i % 3 == 1 else x for i, x in enumerate(streams[0])), streams[2][:5], b"",
                        streams[3], streams[4]]
             got, _ = ls.decompress(damaged, [40, 64, 20, 30, 33])
-            bad[(dev, sym)] = [g.tolist() for g in got]
-    assert outs[(True, "1")] == outs[(False, "1")] == outs[(True, "0")]
-    assert bad[(True, "1")] == bad[(False, "1")] == bad[(True, "0")]
-    assert bad[(False, "1")][0] != files[0] and bad[(False, "1")][4] == files[4]
+            bad[(dev, sym, pipe)] = [g.tolist() for g in got]
+    ref = outs[(False, "1", "1")]
+    assert all(o == ref for o in outs.values())
+    assert all(b == bad[(False, "1", "1")] for b in bad.values())
+    assert bad[(False, "1", "1")][0] != files[0] and bad[(False, "1", "1")][4] == files[4]

@@ -227,3 +227,81 @@ def test_oracle_plugin_round_trip_on_the_cpu(oracle_plugin, tmp_path, kind):
     with Lockstep(path, plugin_path=oracle_plugin, slots=0) as single:
         one, _ = single.compress(files, reset_every=32)
     assert one == streams
+
+
+# The device-CDF paths over the stand-in plugin built with its CDF entry points
+# (-DFAKE_PLUGIN_CDF: every CDF is the host library's): host CDFs, whole device rows,
+# the coder's values per stream (compression) with the decoder's search (decompression),
+# and compression queued a step ahead (REDUKT_LOCKSTEP_PIPELINE) all code the bytes of the
+# Python restatement, with the same per-file errors and the same statuses when the
+# backbone fails.
+PATHS = {"host": (False, "1", "1"), "rows": (True, "0", "1"), "sym-find": (True, "1", "0"),
+         "pipelined": (True, "1", "1")}
+
+
+@pytest.fixture(scope="module")
+def fake_cdf(tmp_path_factory):
+    d = tmp_path_factory.mktemp("fake_plugin_cdf")
+    so = str(d / "libfake_plugin_cdf.so")
+    host = os.path.dirname(os.path.abspath(C.DEFAULT_LIB))
+    subprocess.run(["gcc", "-O2", "-shared", "-fPIC", "-ffp-contract=off", "-DFAKE_PLUGIN_CDF", "-o", so,
+                    os.path.join(HERE, "fake_plugin.c"), "-L", host, "-lredukt_host", f"-Wl,-rpath,{host}"],
+                   check=True)
+    w = str(d / "weights.bin")
+    np.array([VOCAB], np.uint32).tofile(w)
+    return so, w
+
+
+def _path(monkeypatch, name):
+    dev, sym, pipe = PATHS[name]
+    monkeypatch.setenv("REDUKT_LOCKSTEP_CDF_SYM", sym)
+    monkeypatch.setenv("REDUKT_LOCKSTEP_PIPELINE", pipe)
+    return dev
+
+
+@pytest.mark.parametrize("slots", [1, 2, 3, 7])
+@pytest.mark.parametrize("name", list(PATHS))
+def test_device_cdf_paths_equal_the_restatement(fake_cdf, monkeypatch, slots, name):
+    so, w = fake_cdf
+    fs = files(7)
+    dev = _path(monkeypatch, name)
+    with Lockstep(w, plugin_path=so, slots=slots, device_cdf=dev) as ls:
+        assert ls.device_cdf == dev
+        out, st = ls.compress(fs, reset_every=16)
+        assert out == [python_encode(f, 16) for f in fs]
+        assert st.tokens == sum(len(f) for f in fs) and st.files == len(fs)
+        back, _ = ls.decompress(out, [len(f) for f in fs], reset_every=16)
+    for f, b in zip(fs, back):
+        assert np.array_equal(f, b)
+
+
+@pytest.mark.parametrize("name", list(PATHS))
+def test_device_cdf_paths_per_file_errors(fake_cdf, monkeypatch, name):
+    so, w = fake_cdf
+    fs = files(4, (10, 10, 10))
+    bad = fs[1].copy()
+    bad[4] = VOCAB
+    dev = _path(monkeypatch, name)
+    with Lockstep(w, plugin_path=so, slots=2, device_cdf=dev) as ls:
+        with pytest.raises(LockstepError) as e:
+            ls.compress([fs[0], bad, np.zeros(0, np.uint32), fs[2]], reset_every=3)
+        assert e.value.status == LockstepStatus.CODER
+        assert e.value.file_status == [C.CodecStatus.OK, C.CodecStatus.INVALID_ARG, C.CodecStatus.INVALID_ARG,
+                                       C.CodecStatus.OK]
+        out, _ = ls.compress([fs[0], fs[2]], reset_every=3)
+        assert out[0] == python_encode(fs[0], 3) and out[1] == python_encode(fs[2], 3)
+
+
+@pytest.mark.parametrize("name", list(PATHS))
+def test_device_cdf_paths_backbone_failure(fake_cdf, monkeypatch, name):
+    # the 13th forward fails in the iteration in which file 0 codes its last token: file 0
+    # still finishes (its coding comes before that forward), the others are INCOMPLETE
+    so, w = fake_cdf
+    fs = files(6, (13, 40, 40))
+    dev = _path(monkeypatch, name)
+    monkeypatch.setenv("FAKE_PLUGIN_FAIL_AFTER", "12")
+    with Lockstep(w, plugin_path=so, slots=2, device_cdf=dev) as ls:
+        with pytest.raises(LockstepError) as e:
+            ls.compress(fs, reset_every=0)
+    assert e.value.status == LockstepStatus.FORWARD
+    assert e.value.file_status == [C.CodecStatus.OK, C.CodecStatus.INCOMPLETE, C.CodecStatus.INCOMPLETE]
