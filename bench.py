@@ -299,6 +299,43 @@ class Workload:
                 raise ffi.BackendError(ffi.BackendResult.from_code(rc), "forward_batch")
         return self.n * steps / (time.perf_counter() - t0)
 
+    def cdf_sym_rate(self, steps: int) -> float:
+        """tok/s of compression's device path through the C ABI: each step's forward, its
+        device CDFs and the coder's three values per stream (cdf[next], cdf[next + 1], the
+        total; the next symbol is the following step's token) back in host memory, each
+        step queued before the previous one's values are collected
+        (forward_batch_cdf_sym_submit / _wait), as the lockstep driver compresses."""
+        L = self.be.lib.lib
+        slots = np.arange(self.n, dtype=np.uint32)
+        toks = [np.ascontiguousarray(t, np.uint32) for t in self.tokens]
+        out = np.empty(3 * self.n, np.uint32)
+        sp, op = ffi._ptr(slots, ctypes.c_uint32), ffi._ptr(out, ctypes.c_uint32)
+        tps = [ffi._ptr(t, ctypes.c_uint32) for t in toks]
+        ticket = ctypes.c_uint64(0)
+
+        def submit(t: int) -> int:
+            rc = L.redukt_backend_forward_batch_cdf_sym_submit(self.n, sp, tps[t % len(tps)],
+                                                               tps[(t + 1) % len(tps)], self.vocab,
+                                                               ctypes.byref(ticket))
+            if rc != 0:
+                raise ffi.BackendError(ffi.BackendResult.from_code(rc), "forward_batch_cdf_sym_submit")
+            return ticket.value
+
+        def wait(tk: int) -> None:
+            rc = L.redukt_backend_forward_batch_cdf_sym_wait(tk, op, self.n)
+            if rc != 0:
+                raise ffi.BackendError(ffi.BackendResult.from_code(rc), "forward_batch_cdf_sym_wait")
+
+        wait(submit(0))   # the CDF scratch and the step's graph exist before the clock starts
+        t0 = time.perf_counter()
+        pending = submit(1)
+        for t in range(2, steps + 1):
+            nxt = submit(t)
+            wait(pending)
+            pending = nxt
+        wait(pending)
+        return self.n * steps / (time.perf_counter() - t0)
+
     def close(self) -> None:
         for b in (self.d_tokens, self.d_slots, self.d_out):
             b.close()
@@ -498,6 +535,7 @@ def main() -> int:
         dst.close()
 
     ffi_tok_s = wl.ffi_rate(min(64, K))
+    cdf_sym_tok_s = wl.cdf_sym_rate(min(64, K)) if not args.probs else None
     wl.close()
     be.close()
 
@@ -555,6 +593,7 @@ def main() -> int:
         "step_GBps": round(sb / (ms / K / 1e3) / 1e9, 1),
         "step_hbm_frac": round(sb / (ms / K / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
         "ffi_tok_s": round(ffi_tok_s, 1),
+        "cdf_sym_tok_s": round(cdf_sym_tok_s, 1) if cdf_sym_tok_s is not None else None,
         "wall_ms": round(wall * 1e3, 2),
         "kernels": per_class,
         "grid": grid,
