@@ -3185,13 +3185,18 @@ hipError_t StepRunner::run(const StepSource& src, Pool& p, const StepIO& io, hip
     hit->out = io.out;
     hit->err = io.err;
     hit->last_use = ++clock_;
+    // Every part's lead and fork first, then the graphs from the last part to the first: a
+    // graph's kernels start only once most of its launch is done (about 30 µs of host time
+    // for a part), so in a call that finds the device idle the part launched first starts
+    // first.  Launched last, part 0 on st then ends last, and st's wait for the other
+    // parts finds them done instead of taking a cross-queue wake-up after them.
     for (uint32_t k = 0; k < hit->nparts; k++) {
         const Part& pk = hit->parts[k];
         RDK_TRY(start_part(k));
         for (uint32_t i = 0; i < pk.lead; i++) RDK_TRY(launch_direct((*pk.launches)[i], stream_of(k)));
         RDK_TRY(after_lead(k));
-        RDK_TRY(hipGraphLaunch(pk.exec, stream_of(k)));
     }
+    for (uint32_t k = hit->nparts; k-- > 0;) RDK_TRY(hipGraphLaunch(hit->parts[k].exec, stream_of(k)));
     return join();
 }
 
