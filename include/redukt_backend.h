@@ -189,8 +189,9 @@ int32_t redukt_backend_forward_batch_cdf_find(uint32_t n_streams, const uint32_t
  * call and writes out_bounds (3 u32 a stream, n_streams as submitted).  At most two calls
  * are in flight: a third _submit before one of them is waited for is refused.  Calls run in
  * submission order, after and before every other entry point's work, and each sees the
- * recurrent state its predecessors left.  Same validation and state rules as forward_batch.
- * No reference counterpart (an extension of the CDF entry points above). */
+ * recurrent state its predecessors left; batch_init and free wait for the calls in flight
+ * and drop them (their tickets are refused afterwards).  Same validation and state rules
+ * as forward_batch.  No reference counterpart (an extension of the CDF entry points above). */
 int32_t redukt_backend_forward_batch_cdf_sym_submit(uint32_t n_streams, const uint32_t* slots, const uint32_t* tokens,
                                                     const uint32_t* next_syms, uint32_t vocab_size, uint64_t* ticket);
 int32_t redukt_backend_forward_batch_cdf_sym_wait(uint64_t ticket, uint32_t* out_bounds, uint32_t n_streams);
