@@ -1385,6 +1385,10 @@ int32_t redukt_backend_forward_batch_cdf_sym(uint32_t n_streams, const uint32_t*
     return forward_batch_cdf_read(n_streams, slots, tokens, next_syms, out_bounds, vocab_size, false);
 }
 
+// Tickets of queued calls, never reused in the process (a ticket from before a batch_init
+// is refused, not matched to a later call).
+static uint64_t g_next_ticket = 1;
+
 int32_t redukt_backend_forward_batch_cdf_sym_submit(uint32_t n_streams, const uint32_t* slots, const uint32_t* tokens,
                                                     const uint32_t* next_syms, uint32_t vocab_size, uint64_t* ticket) {
     if (!G.ready || G.batch.cap == 0) return BACKEND_INIT_FAILED;
@@ -1431,7 +1435,7 @@ int32_t redukt_backend_forward_batch_cdf_sym_submit(uint32_t n_streams, const ui
         return BACKEND_FORWARD_FAILED;
     }
     q->n = n_streams;
-    q->ticket = p.next_ticket++;
+    q->ticket = g_next_ticket++;
     *ticket = q->ticket;
     return BACKEND_OK;
 }

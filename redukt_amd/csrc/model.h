@@ -176,7 +176,6 @@ struct Pool {
         uint32_t n = 0;
     };
     Queued queued[kQueued];
-    uint64_t next_ticket = 1;
 };
 
 // Kernel classes a caller can time with HIP events (see Probe).

@@ -185,6 +185,15 @@ def test_forward_batch_cdf_sym_queued_equals_the_direct_call(backend):
     bad = list(q)
     bad[3] = bad[2]
     assert backend.forward_batch_cdf_sym_submit(bad, toks[0], syms[0])[0] == ffi.BackendResult.INVALID_ARGUMENT
+    # a call in flight across batch_init is dropped: its ticket is refused, and a new
+    # pool's tickets are new numbers
+    rc3, t3 = backend.forward_batch_cdf_sym_submit(q, toks[0], syms[0])
+    assert rc3 == ffi.BackendResult.OK
+    backend.batch_init(64)
+    assert backend.forward_batch_cdf_sym_wait(t3, got) == ffi.BackendResult.INVALID_ARGUMENT
+    rc4, t4 = backend.forward_batch_cdf_sym_submit(q, toks[0], syms[0])
+    assert rc4 == ffi.BackendResult.OK and t4 > t3
+    assert backend.forward_batch_cdf_sym_wait(t4, got) == ffi.BackendResult.OK
 
 
 def test_forward_batch_cdf_find_equals_the_host_search(backend):
