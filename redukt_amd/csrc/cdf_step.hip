@@ -148,14 +148,30 @@ __device__ T block_reduce(T v, F op, T* sh) {
 
 __device__ __forceinline__ double max_nan_loses(double m, double v) { return (!isnan(v) && !(v <= m)) ? v : m; }
 
+// A row whose logits start on 16 bytes: its chunks are read four elements a lane.
+__device__ __forceinline__ bool vec_row(const float* l) { return ((uintptr_t)l & 15) == 0; }
+
 // Phase 1a (chunk c of row r): the chunk's max (f64::max folding, NaN loses).
 __global__ __launch_bounds__(kCdfBlock) void k_cdf_max(CdfArgs a) {
     __shared__ double sh[kCdfBlock / 64];
     const uint32_t c = blockIdx.x, row = blockIdx.y, n = a.n;
     const float* l = a.logits + (size_t)row * n;
     double m = -__longlong_as_double(0x7ff0000000000000LL);
-    for (uint32_t i = c * kChunk + threadIdx.x; i < min(n, (c + 1) * kChunk); i += kCdfBlock)
-        m = max_nan_loses(m, (double)l[i]);
+    const uint32_t i0 = c * kChunk, i1 = min(n, (c + 1) * kChunk);
+    if (vec_row(l)) {
+        // four consecutive elements a lane (chunks start at multiples of 4)
+        for (uint32_t i = i0 + 4 * threadIdx.x; i < i1; i += 4 * kCdfBlock) {
+            if (i + 4 <= i1) {
+                const float4 v = *(const float4*)(l + i);
+                m = max_nan_loses(max_nan_loses(m, (double)v.x), (double)v.y);
+                m = max_nan_loses(max_nan_loses(m, (double)v.z), (double)v.w);
+            } else {
+                for (uint32_t k = i; k < i1; k++) m = max_nan_loses(m, (double)l[k]);
+            }
+        }
+    } else {
+        for (uint32_t i = i0 + threadIdx.x; i < i1; i += kCdfBlock) m = max_nan_loses(m, (double)l[i]);
+    }
     // every partial is -inf or a number, so the combination order does not matter
     m = block_reduce<double>(m, [](double x, double y) { return (y <= x) ? x : y; }, sh);
     if (threadIdx.x == 0) a.part[(size_t)row * a.chunks + c].max = m;
@@ -169,8 +185,21 @@ __global__ __launch_bounds__(kCdfBlock) void k_cdf_exp(CdfArgs a) {
     for (uint32_t i = 1; i < a.chunks; i++) m = (pr[i].max <= m) ? m : pr[i].max;
     const float* l = a.logits + (size_t)row * n;
     double* e = a.e + (size_t)row * n;
-    for (uint32_t i = c * kChunk + threadIdx.x; i < min(n, (c + 1) * kChunk); i += kCdfBlock)
-        e[i] = exp_f64((double)l[i] - m, c_exp.v);
+    const uint32_t i0 = c * kChunk, i1 = min(n, (c + 1) * kChunk);
+    if (vec_row(l) && ((uintptr_t)e & 15) == 0) {
+        for (uint32_t i = i0 + 4 * threadIdx.x; i < i1; i += 4 * kCdfBlock) {
+            if (i + 4 <= i1) {
+                const float4 v = *(const float4*)(l + i);
+                *(double2*)(e + i) = make_double2(exp_f64((double)v.x - m, c_exp.v), exp_f64((double)v.y - m, c_exp.v));
+                *(double2*)(e + i + 2) =
+                    make_double2(exp_f64((double)v.z - m, c_exp.v), exp_f64((double)v.w - m, c_exp.v));
+            } else {
+                for (uint32_t k = i; k < i1; k++) e[k] = exp_f64((double)l[k] - m, c_exp.v);
+            }
+        }
+    } else {
+        for (uint32_t i = i0 + threadIdx.x; i < i1; i += kCdfBlock) e[i] = exp_f64((double)l[i] - m, c_exp.v);
+    }
 }
 
 // Phase 2 (one workgroup per row): the two sequential f64 sums, in index order:
@@ -468,13 +497,28 @@ __global__ __launch_bounds__(kCdfBlock) void k_cdf_freq_parts(CdfArgs a) {
     const double* e = a.e + (size_t)row * n;
     uint64_t used = 0, best = 0;
     uint32_t total = 0;
-    for (uint32_t i = c * kChunk + threadIdx.x; i < min(n, (c + 1) * kChunk); i += kCdfBlock) {
-        const uint64_t x = extra_of(e[i], f);
+    auto take = [&](double v, uint32_t i) {
+        const uint64_t x = extra_of(v, f);
         const uint32_t fr = 1u + (uint32_t)x;
         used += x;
         total += fr;
         const uint64_t key = ((uint64_t)fr << 32) | i;
         best = key > best ? key : best;
+    };
+    const uint32_t i0 = c * kChunk, i1 = min(n, (c + 1) * kChunk);
+    if (((uintptr_t)e & 15) == 0) {
+        // two consecutive elements a lane (chunks start at even positions)
+        for (uint32_t i = i0 + 2 * threadIdx.x; i < i1; i += 2 * kCdfBlock) {
+            if (i + 2 <= i1) {
+                const double2 v = *(const double2*)(e + i);
+                take(v.x, i);
+                take(v.y, i + 1);
+            } else {
+                take(e[i], i);
+            }
+        }
+    } else {
+        for (uint32_t i = i0 + threadIdx.x; i < i1; i += kCdfBlock) take(e[i], i);
     }
     used = block_reduce<uint64_t>(used, [](uint64_t x, uint64_t y) { return x + y; }, sh64);
     best = block_reduce<uint64_t>(best, [](uint64_t x, uint64_t y) { return x > y ? x : y; }, sh64);
