@@ -77,10 +77,13 @@ int redukt_backend_forward(uint32_t tok, float* out, uint32_t vocab) {
 
 void redukt_backend_reset_state(void) { g_v1 = 0; }
 
+static void free_queued(void);
+
 void redukt_backend_free(void) {
     free(g_slot);
     g_slot = NULL;
     g_cap = 0;
+    free_queued();
 }
 
 uint32_t redukt_backend_abi_version(void) {
@@ -208,6 +211,14 @@ static struct {
 } g_q[2];
 static uint64_t g_next_ticket = 1;
 
+static void free_queued(void) {
+    for (int k = 0; k < 2; ++k) {
+        free(g_q[k].res);
+        g_q[k].res = NULL;
+        g_q[k].ticket = 0;
+    }
+}
+
 int32_t redukt_backend_forward_batch_cdf_sym_submit(uint32_t n, const uint32_t* slots, const uint32_t* toks,
                                                     const uint32_t* syms, uint32_t vocab, uint64_t* ticket) {
     if (vocab != g_vocab || !ticket || (n && !syms)) return 5;
@@ -239,4 +250,6 @@ int32_t redukt_backend_forward_batch_cdf_sym_wait(uint64_t ticket, uint32_t* out
     }
     return 5;
 }
+#else
+static void free_queued(void) {}
 #endif
